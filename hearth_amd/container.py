@@ -1,0 +1,363 @@
+"""Writer and reader of the .hearth container (the reference's docs/FORMAT.md v1), and the
+synthetic models the verify benchmarks and parity tests run on.
+
+The writer follows FORMAT.md §1-6 (the reference's writers: python/hearth/format.py:417,
+engine/tests/test_model.c:267-324): preamble, typed metadata, 128-byte tensor entries,
+32-byte expert entries, 64-byte aligned tensors, 4096-byte aligned expert slabs
+(gate [F,D], up [F,D], down [D,F] at 64-byte aligned offsets). Aliased slabs
+(flag bit 0) let synthetic benchmark containers point many experts at a few physical
+slabs; the engine still gives every (layer, expert) its own HBM copy.
+
+Random weights come from splitmix64 and Irwin-Hall sums of 12 uniforms (the recipe of
+engine/tests/test_model.c:90-102), computed exactly in float64, so a model built from a
+seed is byte-identical on every machine.
+"""
+from __future__ import annotations
+
+import math
+import struct
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+F32, F16, BF16, Q8, Q4, I32, U8 = range(7)
+QK = 64
+MAGIC = 0x48545248
+
+# FORMAT.md §3.1 key types: 1 u32, 2 f32, 3 u64, 4 str, 5 u32[], 6 f32[], 7 u8[]
+_KEY_TYPES = {
+    "arch": 4, "n_layers": 1, "d_model": 1, "vocab_size": 1, "max_seq": 1, "norm_eps": 2, "attn_kind": 1,
+    "n_heads": 1, "n_kv_heads": 1, "head_dim": 1, "qk_norm": 1, "qkv_bias": 1, "q_lora_rank": 1,
+    "kv_lora_rank": 1, "qk_nope_dim": 1, "qk_rope_dim": 1, "v_head_dim": 1, "rope_dim": 1, "rope_style": 1,
+    "rope_attn_factor": 2, "attn_scale": 2, "dense_ffn_dim": 1, "n_experts": 1, "top_k": 1, "expert_ffn_dim": 1,
+    "shared_ffn_dim": 1, "shared_gate": 1, "score_fn": 1, "score_bias": 1, "n_group": 1, "topk_group": 1,
+    "norm_topk_prob": 1, "routed_scale": 2, "emb_scale": 2, "residual_scale": 2, "logit_scale": 2,
+    "tie_embeddings": 1, "layer_kind": 7, "bos_id": 1, "eos_ids": 5, "tokenizer": 4, "chat_template": 4,
+    "source": 4, "expert_dtype": 1,
+}
+
+
+def row_bytes(dtype: int, n: int) -> int:
+    if dtype in (F32, I32):
+        return 4 * n
+    if dtype in (F16, BF16):
+        return 2 * n
+    if dtype == U8:
+        return n
+    if n % QK:
+        raise ValueError(f"{n} columns is not a multiple of {QK}")
+    return (n // QK) * (66 if dtype == Q8 else 34)
+
+
+def _al(x: int, a: int) -> int:
+    return (x + a - 1) // a * a
+
+
+def slab_layout(dtype: int, D: int, F: int) -> tuple[int, int, int, int]:
+    """(nbytes, off_gate, off_up, off_down) of one expert slab (FORMAT.md §5)."""
+    og = 0
+    ou = _al(F * row_bytes(dtype, D), 64)
+    od = _al(ou + F * row_bytes(dtype, D), 64)
+    return _al(od + D * row_bytes(dtype, F), 4096), og, ou, od
+
+
+def _meta_bytes(meta: dict) -> bytes:
+    out = bytearray()
+    for k, v in meta.items():
+        t = _KEY_TYPES.get(k)
+        if t is None:
+            raise KeyError(f"unknown metadata key {k!r}")
+        kb = k.encode("ascii")
+        out += struct.pack("<H", len(kb)) + kb + bytes([t])
+        if t == 1:
+            out += struct.pack("<I", int(v) & 0xFFFFFFFF)
+        elif t == 2:
+            out += struct.pack("<f", float(v))
+        elif t == 4:
+            b = str(v).encode("utf-8")
+            out += struct.pack("<I", len(b)) + b
+        elif t == 5:
+            out += struct.pack("<I", len(v)) + b"".join(struct.pack("<I", int(x)) for x in v)
+        elif t == 7:
+            out += struct.pack("<I", len(v)) + bytes(int(x) for x in v)
+    return bytes(out)
+
+
+@dataclass
+class _T:
+    name: str
+    dtype: int
+    shape: tuple
+    data: bytes
+
+
+@dataclass
+class ContainerWriter:
+    """Collects tensors and expert slabs, then writes one FORMAT.md v1 file."""
+    meta: dict
+    tensors: list = field(default_factory=list)
+    experts: dict = field(default_factory=dict)        # (layer, e) -> (dtype, slab bytes) or ("alias", (l, e))
+
+    def add(self, name: str, dtype: int, shape, data: bytes) -> None:
+        shape = tuple(int(s) for s in shape)
+        rows = 1
+        for s in shape[:-1]:
+            rows *= s
+        if len(data) != rows * row_bytes(dtype, shape[-1]):
+            raise ValueError(f"{name}: {len(data)} bytes for shape {shape} dtype {dtype}")
+        self.tensors.append(_T(name, dtype, shape, bytes(data)))
+
+    def add_expert(self, layer: int, e: int, dtype: int, slab: bytes) -> None:
+        self.experts[(layer, e)] = (dtype, slab)
+
+    def alias_expert(self, layer: int, e: int, src: tuple) -> None:
+        """(layer, e) shares the physical slab of expert src (flag bit 0)."""
+        self.experts[(layer, e)] = ("alias", src)
+
+    def write(self, path) -> Path:
+        path = Path(path)
+        L = int(self.meta["n_layers"])
+        E = int(self.meta.get("n_experts", 0))
+        lk = list(self.meta.get("layer_kind", [1 if E else 0] * L))
+        ne = L * E if E and any(lk) else 0
+        meta = _meta_bytes(self.meta)
+        meta_off = 64
+        tdir = _al(meta_off + len(meta), 64)
+        edir = tdir + 128 * len(self.tensors)
+        off = _al(edir + 32 * ne, 64)
+        toff = []
+        for t in self.tensors:
+            toff.append(off)
+            off = _al(off + len(t.data), 64)
+        off = _al(off, 4096)
+        phys = {}   # (layer, e) of a real slab -> offset
+        entries = [(0, 0, 0, 0)] * ne
+        for (l, e), v in sorted(self.experts.items()):
+            if v[0] == "alias":
+                continue
+            dt, slab = v
+            phys[(l, e)] = off
+            entries[l * E + e] = (off, len(slab), dt, 0)
+            off += len(slab)
+        for (l, e), v in sorted(self.experts.items()):
+            if v[0] != "alias":
+                continue
+            o, nb, dt, _ = entries[v[1][0] * E + v[1][1]]
+            entries[l * E + e] = (o, nb, dt, 1)
+        with open(path, "wb") as f:
+            f.write(struct.pack("<IIQQQQQQII", MAGIC, 1, meta_off, len(meta), tdir, len(self.tensors), edir, ne, 4096, 0))
+            f.seek(meta_off)
+            f.write(meta)
+            f.seek(tdir)
+            for t, o in zip(self.tensors, toff):
+                nm = t.name.encode("ascii")
+                if len(nm) > 79:
+                    raise ValueError(f"tensor name too long: {t.name}")
+                shape = list(t.shape) + [1] * (4 - len(t.shape))
+                f.write(nm + b"\0" * (80 - len(nm)) + struct.pack("<II4IQQQ", t.dtype, len(t.shape), *shape, o, len(t.data), 0))
+            f.seek(edir)
+            for (o, nb, dt, fl) in entries:
+                f.write(struct.pack("<QQIIQ", o, nb, dt, fl, 0))
+            for t, o in zip(self.tensors, toff):
+                f.seek(o)
+                f.write(t.data)
+            for (l, e), v in sorted(self.experts.items()):
+                if v[0] != "alias":
+                    f.seek(phys[(l, e)])
+                    f.write(v[1])
+            f.truncate(off)
+        return path
+
+
+# ---------------------------------------------------------------- seeded weights
+
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def _splitmix(state: int, n: int) -> np.ndarray:
+    """n outputs of splitmix64 starting from state (vectorised, wraps mod 2^64)."""
+    with np.errstate(over="ignore"):
+        z = np.uint64(state) + (np.arange(1, n + 1, dtype=np.uint64) * np.uint64(0x9E3779B97F4A7C15))
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def normal(seed: int, n: int, std: float) -> np.ndarray:
+    """n float32 draws of N(0, std^2) by Irwin-Hall (12 uniforms k/2^24), exact in
+    float64 up to the final scaling, so identical on every machine."""
+    s = np.zeros(n, dtype=np.float64)
+    base = (int(seed) * 0x632BE59BD9B4E019) & 0xFFFFFFFFFFFFFFFF
+    for k in range(12):
+        u = (_splitmix((base + k * 0x7F4A7C159E3779B9) & 0xFFFFFFFFFFFFFFFF, n) >> np.uint64(40)).astype(np.float64)
+        s += u * (1.0 / 16777216.0)
+    return ((s - 6.0) * std).astype(np.float32)
+
+
+def uniform_ints(seed: int, n: int, hi: int) -> np.ndarray:
+    """n integers in [0, hi) from splitmix64 (multiply-shift, bias < 2^-32)."""
+    z = _splitmix((int(seed) * 0xD1B54A32D192ED03) & 0xFFFFFFFFFFFFFFFF, n) >> np.uint64(32)
+    return ((z * np.uint64(hi)) >> np.uint64(32)).astype(np.int64)
+
+
+def uniforms(seed: int, n: int) -> np.ndarray:
+    """n float64 uniforms in [0, 1) with 53 random bits."""
+    z = _splitmix((int(seed) * 0x9FB21C651E98DF25) & 0xFFFFFFFFFFFFFFFF, n) >> np.uint64(11)
+    return z.astype(np.float64) * (1.0 / 9007199254740992.0)
+
+
+# ---------------------------------------------------------------- synthetic models
+
+@dataclass
+class Shape:
+    """Hyper-parameters of a synthetic Qwen3-MoE-style (GQA, per-head qk-norm, NEOX
+    RoPE, softmax top-k with norm_topk_prob) model."""
+    n_layers: int
+    d_model: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    n_experts: int
+    top_k: int
+    expert_ffn: int
+    vocab: int
+    max_seq: int = 4096
+    rope_theta: float = 1e6
+    arch: str = "qwen3_moe"
+
+
+TINY = Shape(n_layers=4, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, n_experts=16, top_k=4,
+             expert_ffn=256, vocab=4096, max_seq=1024)
+QWEN3_30B_A3B = Shape(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_dim=128, n_experts=128, top_k=8,
+                      expert_ffn=768, vocab=151936, max_seq=8192)
+
+
+def _meta(s: Shape, source: str) -> dict:
+    return dict(arch=s.arch, n_layers=s.n_layers, d_model=s.d_model, vocab_size=s.vocab, max_seq=s.max_seq,
+                norm_eps=1e-6, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, qk_norm=1,
+                rope_dim=s.head_dim, attn_scale=float(np.float32(1.0 / math.sqrt(s.head_dim))),
+                n_experts=s.n_experts, top_k=s.top_k, expert_ffn_dim=s.expert_ffn, norm_topk_prob=1,
+                layer_kind=[1] * s.n_layers, bos_id=1, eos_ids=[2], source=source)
+
+
+def rope_inv_freq(s: Shape) -> np.ndarray:
+    """1 / theta^(2j / rope_dim) in float32, computed with the platform libm's pow."""
+    d = s.head_dim
+    return np.array([1.0 / math.pow(s.rope_theta, (2 * j) / d) for j in range(d // 2)], dtype=np.float32)
+
+
+def make_tiny(path, quantize, seed: int = 1, shape: Shape = TINY, std: float = 0.02) -> Path:
+    """A small model with N(0, std^2) weights from `seed`: Q4 experts, Q8 attention,
+    embedding and lm_head, F32 router and norms (norms = 1.0), the quantization done by
+    the authoritative quantizer `quantize(dtype, float32 [rows, cols]) -> bytes`."""
+    s = shape
+    D, H, Hkv, hd, E, F, V, L = s.d_model, s.n_heads, s.n_kv_heads, s.head_dim, s.n_experts, s.expert_ffn, s.vocab, s.n_layers
+    w = ContainerWriter(_meta(s, f"synthetic:tiny:seed{seed}"))
+    k = [seed * 1000003]
+
+    def rnd(rows, cols):
+        k[0] += 1
+        return normal(k[0], rows * cols, std).reshape(rows, cols)
+
+    def q(name, dtype, rows, cols):
+        w.add(name, dtype, (rows, cols), quantize(dtype, rnd(rows, cols)))
+
+    ones = np.ones(D, dtype=np.float32).tobytes()
+    q("tok_embd", Q8, V, D)
+    q("lm_head", Q8, V, D)
+    w.add("out_norm", F32, (D,), ones)
+    w.add("rope_inv_freq", F32, (hd // 2,), rope_inv_freq(s).tobytes())
+    for l in range(L):
+        p = f"blk.{l}."
+        w.add(p + "attn_norm", F32, (D,), ones)
+        w.add(p + "ffn_norm", F32, (D,), ones)
+        q(p + "attn_q", Q8, H * hd, D)
+        q(p + "attn_k", Q8, Hkv * hd, D)
+        q(p + "attn_v", Q8, Hkv * hd, D)
+        q(p + "attn_o", Q8, D, H * hd)
+        w.add(p + "attn_q_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+        w.add(p + "attn_k_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+        w.add(p + "moe_router", F32, (E, D), rnd(E, D).tobytes())
+        nb, og, ou, od = slab_layout(Q4, D, F)
+        for e in range(E):
+            slab = bytearray(nb)
+            for off, (rows, cols) in ((og, (F, D)), (ou, (F, D)), (od, (D, F))):
+                b = quantize(Q4, rnd(rows, cols))
+                slab[off:off + len(b)] = b
+            w.add_expert(l, e, Q4, bytes(slab))
+    return w.write(path)
+
+
+def _random_blocks(rng: np.random.Generator, dtype: int, rows: int, cols: int) -> bytes:
+    """rows x cols of valid random Q8/Q4 blocks, std ~ 1/sqrt(cols) (the reference's
+    synthetic recipe, python/hearth/synth.py:287-305)."""
+    nb = cols // QK
+    sd = 1.0 / math.sqrt(cols)
+    if dtype == Q8:
+        blk = np.zeros((rows, nb), dtype=[("d", "<f2"), ("q", "i1", (QK,))])
+        blk["d"] = np.float16(3.0 * sd / 127.0)
+        blk["q"] = np.clip(np.rint(rng.standard_normal((rows, nb, QK), dtype=np.float32) * 42.0), -127, 127).astype(np.int8)
+    else:
+        blk = np.zeros((rows, nb), dtype=[("d", "<f2"), ("qs", "u1", (32,))])
+        blk["d"] = np.float16(3.0 * sd / 7.0)
+        qv = (np.clip(np.rint(rng.standard_normal((rows, nb, QK), dtype=np.float32) * 2.5), -8, 7) + 8).astype(np.uint8)
+        blk["qs"] = qv[..., :32] | (qv[..., 32:] << 4)
+    return blk.tobytes()
+
+
+def make_shaped(path, shape: Shape = QWEN3_30B_A3B, seed: int = 0, n_unique_slabs: int = 32,
+                n_layers: int | None = None) -> Path:
+    """A real-shaped model with random weights for throughput runs: Q4 experts, Q8
+    attention / embedding / lm_head, F32 routers (N(0, 2.5^2/D), distinct per layer) and
+    unit norms. Expert slabs cycle over n_unique_slabs physical slabs (aliased entries);
+    the engine still holds one HBM copy per (layer, expert)."""
+    s = shape if n_layers is None else Shape(**{**shape.__dict__, "n_layers": n_layers})
+    rng = np.random.default_rng(seed)
+    D, H, Hkv, hd, E, F, V, L = s.d_model, s.n_heads, s.n_kv_heads, s.head_dim, s.n_experts, s.expert_ffn, s.vocab, s.n_layers
+    w = ContainerWriter(_meta(s, f"synthetic:{s.arch}:seed{seed}"))
+    ones = np.ones(D, dtype=np.float32).tobytes()
+    w.add("tok_embd", Q8, (V, D), _random_blocks(rng, Q8, V, D))
+    w.add("lm_head", Q8, (V, D), _random_blocks(rng, Q8, V, D))
+    w.add("out_norm", F32, (D,), ones)
+    w.add("rope_inv_freq", F32, (hd // 2,), rope_inv_freq(s).tobytes())
+    nb, og, ou, od = slab_layout(Q4, D, F)
+    pool = []
+    for i in range(min(n_unique_slabs, L * E)):
+        slab = bytearray(nb)
+        for off, (rows, cols) in ((og, (F, D)), (ou, (F, D)), (od, (D, F))):
+            b = _random_blocks(rng, Q4, rows, cols)
+            slab[off:off + len(b)] = b
+        pool.append(bytes(slab))
+    for l in range(L):
+        p = f"blk.{l}."
+        w.add(p + "attn_norm", F32, (D,), ones)
+        w.add(p + "ffn_norm", F32, (D,), ones)
+        w.add(p + "attn_q", Q8, (H * hd, D), _random_blocks(rng, Q8, H * hd, D))
+        w.add(p + "attn_k", Q8, (Hkv * hd, D), _random_blocks(rng, Q8, Hkv * hd, D))
+        w.add(p + "attn_v", Q8, (Hkv * hd, D), _random_blocks(rng, Q8, Hkv * hd, D))
+        w.add(p + "attn_o", Q8, (D, H * hd), _random_blocks(rng, Q8, D, H * hd))
+        w.add(p + "attn_q_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+        w.add(p + "attn_k_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+        router = (rng.standard_normal((E, D), dtype=np.float32) * np.float32(2.5 / math.sqrt(D))).astype(np.float32)
+        w.add(p + "moe_router", F32, (E, D), router.tobytes())
+        for e in range(E):
+            i = (l * E + e) % len(pool)
+            if (l * E + e) < len(pool):
+                w.add_expert(l, e, Q4, pool[i])
+            else:
+                w.alias_expert(l, e, divmod(i, E))
+    return w.write(path)
+
+
+def sha256(path, chunk: int = 1 << 24) -> str:
+    """sha256 hex digest of a file (fingerprint of a generated container)."""
+    import hashlib
+    h = hashlib.sha256()
+    with open(path, "rb") as f:
+        while True:
+            b = f.read(chunk)
+            if not b:
+                break
+            h.update(b)
+    return h.hexdigest()

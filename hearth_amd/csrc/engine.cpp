@@ -1,0 +1,1058 @@
+/*
+ * engine.cpp — the hearth.h engine on an MI355X: open (container -> HBM), the
+ * verify/eval forward pass as a sequence of HIP kernels on one stream, rewind,
+ * telemetry, routing traces, and the tree / on-device acceptance extensions.
+ *
+ * Reference behaviour followed: engine/src/api.c (argument checks, env overrides,
+ * defaults, error codes), engine/src/model.c:1171-1331 (forward, chunking by
+ * max_batch, a failed call changes nothing), model.c:1148-1168 and 1885-1959
+ * (routing trace / replay), FORMAT.md §9 (trace file).
+ *
+ * Residency: every weight lives in HBM (288 GB per MI355X) in the GPU layouts of
+ * hx_device.h; the reference's NVMe->DRAM expert store is not needed when the routed
+ * experts fit, which is every model up to ~280 GB of Q4 experts.
+ */
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "hearth.h"
+#include "hearth_gpu.h"
+#include "hx_host.h"
+#include "hx_launch.h"
+
+using namespace hx;
+using hxd::Act;
+using hxd::ExpertW;
+using hxd::QMat;
+
+namespace {
+
+constexpr int MAX_BATCH = 4096;
+
+void fail(char *err, size_t n, const char *fmt, ...) {
+    if (!err || !n) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, n, fmt, ap);
+    va_end(ap);
+}
+
+int env_int(const char *k, int def) {
+    const char *s = getenv(k);
+    if (!s || !*s) return def;
+    char *end = nullptr;
+    const long v = strtol(s, &end, 10);
+    return end && *end == 0 ? (int)v : def;
+}
+
+double env_double(const char *k, double def) {
+    const char *s = getenv(k);
+    if (!s || !*s) return def;
+    char *end = nullptr;
+    const double v = strtod(s, &end);
+    return end && *end == 0 ? v : def;
+}
+
+int device_index() { return env_int("HEARTH_DEVICE", 0); }
+
+/* cos/sin as separate non-inlined calls, as the reference does (model.c:201-202), so
+ * no compiler fuses them into a sincos routine that can differ by an ulp. */
+__attribute__((noinline)) float host_cosf(float x) { return cosf(x); }
+__attribute__((noinline)) float host_sinf(float x) { return sinf(x); }
+
+double now_s() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+/* A matrix on the device: Q8/Q4 in the tiled layout, or F32/F16/BF16 rows as stored. */
+struct DMat {
+    bool quant = false;
+    QMat q{};
+    const void *f = nullptr;
+    int dtype = 0, rows = 0, cols = 0;
+};
+
+struct Layer {
+    bool moe = false;
+    const float *attn_norm = nullptr, *ffn_norm = nullptr;
+    DMat q, k, v, o;
+    const float *bq = nullptr, *bk = nullptr, *bv = nullptr, *qn = nullptr, *kn = nullptr;
+    DMat gate, up, down;            /* dense FFN */
+    const float *router = nullptr;  /* F32 [E][D] */
+    const float *router_bias = nullptr;
+    ExpertW *experts = nullptr;     /* device table [E] */
+    uint64_t expert_bytes_each = 0; /* algorithmic bytes of one expert (gate+up+down) */
+};
+
+struct DeviceError {
+    hipError_t e;
+};
+
+inline void ck(hipError_t e) {
+    if (e != hipSuccess) throw DeviceError{e};
+}
+
+} // namespace
+
+struct hearth_engine {
+    hearth_options opt{};
+    int verbose = 0;
+    ModelFile mf;
+    Config c;
+    int dev = 0;
+    hipStream_t st = nullptr;
+    std::vector<void *> allocs;
+
+    int L = 0, D = 0, V = 0, H = 0, Hkv = 0, hd = 0, q_dim = 0, kv_dim = 0, E = 0, K = 0, F = 0, Fd = 0;
+    int cap = 0, B = 0, rope_dim = 0;
+    std::vector<Layer> layers;
+    std::vector<int> moe_ord;
+    const uint8_t *emb = nullptr;
+    int emb_dtype = 0;
+    size_t emb_rb = 0;
+    DMat lm_head;
+    const float *out_norm = nullptr;
+    std::vector<float> inv_freq;
+
+    float *kv = nullptr;
+    size_t kv_layer = 0;   /* floats per layer: [K, V][Hkv][cap][hd] */
+
+    /* scratch for B tokens */
+    float *h = nullptr, *x = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr, *qr = nullptr, *att = nullptr,
+          *ao = nullptr, *S = nullptr, *lge = nullptr, *wts = nullptr, *Y = nullptr, *f1 = nullptr, *f2 = nullptr,
+          *logits = nullptr, *rope = nullptr, *rfull = nullptr;
+    int ldS = 0;
+    Act ax{}, aatt{}, amid{}, af{};
+    int *ids = nullptr, *route_meta = nullptr, *pair_tok = nullptr, *pair_of = nullptr, *tokens = nullptr,
+        *depth = nullptr, *anc = nullptr, *route_out = nullptr, *acc_i = nullptr;
+    unsigned long long *dstats = nullptr;
+    /* pinned host staging */
+    int *h_geom = nullptr;   /* tokens | depth | anc */
+    float *h_rope = nullptr;
+    int *h_res = nullptr;
+
+    int pos = 0;
+    /* telemetry */
+    uint64_t tokens_done = 0, forward_calls = 0;
+    double wall_s = 0.0;
+    bool profiling = false;
+    hearth_gpu_kstats ks{};
+    struct Ev { hipEvent_t a, b; double *acc; };
+    std::vector<Ev> pending_ev;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_next = 0;
+    unsigned long long stats_base[2] = {0, 0};
+    /* routing trace / replay */
+    FILE *trace = nullptr;
+    std::vector<int> h_routes;
+    int *replay_dev = nullptr;
+    int64_t replay_rows = 0;
+    /* tree verification: slots of the last uncommitted tree */
+    int tree_n = 0;
+
+    void *dalloc(size_t n) {
+        void *p = nullptr;
+        ck(hipMalloc(&p, n ? n : 256));
+        allocs.push_back(p);
+        return p;
+    }
+    template <class T> T *dnew(size_t count) { return (T *)dalloc(sizeof(T) * count); }
+    Act make_act(int rows, int n) {
+        Act a{};
+        a.nbp = ((n / 64) + 1) & ~1;
+        a.q = dnew<int8_t>((size_t)rows * a.nbp * 64);
+        a.d = dnew<float>((size_t)rows * a.nbp);
+        a.s = dnew<int32_t>((size_t)rows * a.nbp);
+        ck(hipMemset(a.q, 0, (size_t)rows * a.nbp * 64));
+        ck(hipMemset(a.d, 0, sizeof(float) * (size_t)rows * a.nbp));
+        ck(hipMemset(a.s, 0, sizeof(int32_t) * (size_t)rows * a.nbp));
+        return a;
+    }
+    ~hearth_engine() {
+        if (dev >= 0) (void)hipSetDevice(dev);
+        if (st) (void)hipStreamSynchronize(st);
+        for (auto &e : ev_pool) (void)hipEventDestroy(e);
+        for (void *p : allocs) (void)hipFree(p);
+        if (h_geom) (void)hipHostFree(h_geom);
+        if (h_rope) (void)hipHostFree(h_rope);
+        if (h_res) (void)hipHostFree(h_res);
+        if (st) (void)hipStreamDestroy(st);
+        if (trace) fclose(trace);
+    }
+
+    /* ---- profiling: events around launch groups ---- */
+    hipEvent_t next_event() {
+        if (ev_next == ev_pool.size()) {
+            hipEvent_t e;
+            ck(hipEventCreate(&e));
+            ev_pool.push_back(e);
+        }
+        return ev_pool[ev_next++];
+    }
+    template <class Fn> void timed(double *acc, Fn fn) {
+        if (!profiling) { fn(); return; }
+        hipEvent_t a = next_event(), b = next_event();
+        ck(hipEventRecord(a, st));
+        fn();
+        ck(hipEventRecord(b, st));
+        pending_ev.push_back({a, b, acc});
+    }
+    void collect_events() {
+        for (auto &p : pending_ev) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) *p.acc += ms * 1e-3;
+        }
+        pending_ev.clear();
+        ev_next = 0;
+    }
+
+    bool open_model(char *err, size_t errlen);
+    bool upload(std::string &msg);
+    void forward(int T, bool want_logits, int logit_rows_from);
+    int eval_chunked(const int32_t *tokens, int n, float *logits_out, int all_logits);
+    int run_geometry(const int32_t *tok, const int32_t *parent, int n, float *logits_out, bool keep_logits_dev);
+    void matmul(const DMat &m, const Act &a, const float *xf, int ldx, int T, float *Y, int ldy, bool scale_on, float scale);
+    void write_trace(int T);
+};
+
+/* ---------------------------------------------------------------- upload */
+
+namespace {
+
+struct Uploader {
+    hipStream_t st;
+    uint8_t *pinned[2] = {nullptr, nullptr};
+    uint8_t *dstage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool used[2] = {false, false};
+    size_t cap = (size_t)128 << 20;
+    int cur = 0;
+
+    explicit Uploader(hipStream_t s) : st(s) {
+        for (int i = 0; i < 2; i++) {
+            ck(hipHostMalloc((void **)&pinned[i], cap, hipHostMallocDefault));
+            ck(hipMalloc((void **)&dstage[i], cap));
+            ck(hipEventCreate(&done[i]));
+        }
+    }
+    ~Uploader() {
+        for (int i = 0; i < 2; i++) {
+            if (done[i]) (void)hipEventSynchronize(done[i]);
+            if (pinned[i]) (void)hipHostFree(pinned[i]);
+            if (dstage[i]) (void)hipFree(dstage[i]);
+            if (done[i]) (void)hipEventDestroy(done[i]);
+        }
+    }
+    /* next staging pair, free once its previous user has finished */
+    int take() {
+        const int i = cur;
+        cur ^= 1;
+        if (used[i]) ck(hipEventSynchronize(done[i]));
+        used[i] = true;
+        return i;
+    }
+    void raw(void *dst, const uint8_t *src, size_t n) {
+        for (size_t off = 0; off < n; off += cap) {
+            const size_t len = std::min(cap, n - off);
+            const int i = take();
+            std::memcpy(pinned[i], src + off, len);
+            ck(hipMemcpyAsync((uint8_t *)dst + off, pinned[i], len, hipMemcpyHostToDevice, st));
+            ck(hipEventRecord(done[i], st));
+        }
+    }
+    void quant(const QMat &m, const uint8_t *src) {
+        const size_t rb = row_bytes(m.dtype, (int64_t)m.nb * 64);
+        int chunk = (int)std::min<size_t>((size_t)m.rows_pad, cap / rb) & ~15;
+        if (chunk < 16) chunk = 16;
+        for (int r0 = 0; r0 < m.rows_pad; r0 += chunk) {
+            const int count = std::min(chunk, m.rows_pad - r0);
+            const int real = std::max(0, std::min(count, m.rows - r0));
+            const int i = take();
+            if (real) {
+                std::memcpy(pinned[i], src + (size_t)r0 * rb, (size_t)real * rb);
+                ck(hipMemcpyAsync(dstage[i], pinned[i], (size_t)real * rb, hipMemcpyHostToDevice, st));
+            }
+            hxl::repack(dstage[i], r0, count, m, st);
+            ck(hipEventRecord(done[i], st));
+        }
+    }
+};
+
+} // namespace
+
+bool hearth_engine::upload(std::string &msg) {
+    Uploader up(st);
+    auto vec = [&](int layer, const char *name) -> const float * {
+        const Tensor *t = layer < 0 ? mf.tensor(name) : mf.layer_tensor(layer, name);
+        if (!t) return nullptr;
+        float *d = (float *)dalloc(t->nbytes);
+        up.raw(d, mf.data(t->offset), t->nbytes);
+        return d;
+    };
+    auto qmat_alloc = [&](int dtype, int rows, int cols) -> QMat {
+        QMat m{};
+        m.dtype = dtype;
+        m.rows = rows;
+        m.rows_pad = (rows + 15) & ~15;
+        m.nb = cols / 64;
+        m.nbp = (m.nb + 1) & ~1;
+        m.w = (const uint8_t *)dalloc((size_t)(m.rows_pad / 16) * m.nbp * 1024 / (dtype == HEARTH_Q4 ? 2 : 1));
+        m.d = (const uint16_t *)dalloc(sizeof(uint16_t) * (size_t)m.nbp * m.rows_pad);
+        return m;
+    };
+    auto mat = [&](int layer, const char *name, DMat &out) -> bool {
+        const Tensor *t = layer < 0 ? mf.tensor(name) : mf.layer_tensor(layer, name);
+        if (!t) { msg = std::string("tensor '") + name + "' is missing"; return false; }
+        out.dtype = t->dtype;
+        out.rows = (int)t->shape[0];
+        out.cols = (int)t->shape[1];
+        if (dtype_is_quant(t->dtype)) {
+            out.quant = true;
+            out.q = qmat_alloc(t->dtype, out.rows, out.cols);
+            up.quant(out.q, mf.data(t->offset));
+        } else {
+            out.quant = false;
+            void *d = dalloc(t->nbytes);
+            up.raw(d, mf.data(t->offset), t->nbytes);
+            out.f = d;
+        }
+        return true;
+    };
+
+    /* embedding rows as stored (a gather of T rows per call) */
+    {
+        const Tensor *t = mf.tensor("tok_embd");
+        emb_dtype = t->dtype;
+        emb_rb = row_bytes(t->dtype, D);
+        uint8_t *d = (uint8_t *)dalloc(t->nbytes);
+        up.raw(d, mf.data(t->offset), t->nbytes);
+        emb = d;
+    }
+    if (!mat(-1, c.tie ? "tok_embd" : "lm_head", lm_head)) return false;
+    out_norm = vec(-1, "out_norm");
+    layers.resize(L);
+    for (int l = 0; l < L; l++) {
+        Layer &w = layers[l];
+        w.moe = c.layer_kind[l] != 0;
+        w.attn_norm = vec(l, "attn_norm");
+        w.ffn_norm = vec(l, "ffn_norm");
+        if (!mat(l, "attn_q", w.q) || !mat(l, "attn_k", w.k) || !mat(l, "attn_v", w.v) || !mat(l, "attn_o", w.o)) return false;
+        if (c.qkv_bias) {
+            w.bq = vec(l, "attn_q_bias");
+            w.bk = vec(l, "attn_k_bias");
+            w.bv = vec(l, "attn_v_bias");
+        }
+        if (c.qk_norm) {
+            w.qn = vec(l, "attn_q_norm");
+            w.kn = vec(l, "attn_k_norm");
+        }
+        if (!w.moe) {
+            if (!mat(l, "ffn_gate", w.gate) || !mat(l, "ffn_up", w.up) || !mat(l, "ffn_down", w.down)) return false;
+            continue;
+        }
+        w.router = vec(l, "moe_router");
+        if (c.score_bias) w.router_bias = vec(l, "moe_router_bias");
+        std::vector<ExpertW> table(E);
+        for (int e = 0; e < E; e++) {
+            const ExpertEntry *ent = mf.expert(l, e);
+            const int dt = (int)ent->dtype;
+            uint64_t og, ou, od;
+            slab_layout(dt, D, F, &og, &ou, &od);
+            const uint8_t *slab = mf.data(ent->offset);
+            table[e].gate = qmat_alloc(dt, F, D);
+            table[e].up = qmat_alloc(dt, F, D);
+            table[e].down = qmat_alloc(dt, D, F);
+            up.quant(table[e].gate, slab + og);
+            up.quant(table[e].up, slab + ou);
+            up.quant(table[e].down, slab + od);
+            w.expert_bytes_each = 2 * (uint64_t)F * row_bytes(dt, D) + (uint64_t)D * row_bytes(dt, F);
+        }
+        w.experts = (ExpertW *)dalloc(sizeof(ExpertW) * (size_t)E);
+        ck(hipMemcpyAsync(w.experts, table.data(), sizeof(ExpertW) * (size_t)E, hipMemcpyHostToDevice, st));
+        ck(hipStreamSynchronize(st));   /* the host table goes out of scope */
+    }
+    ck(hipStreamSynchronize(st));
+    return true;
+}
+
+bool hearth_engine::open_model(char *err, size_t errlen) {
+    std::string msg;
+    if (!mf.open(opt.model_path, msg)) { fail(err, errlen, "%s: %s", opt.model_path, msg.c_str()); return false; }
+    c = mf.cfg;
+    if (c.attn_kind != ATTN_GQA) {
+        fail(err, errlen, "%s: MLA attention is not supported by this build yet", opt.model_path);
+        return false;
+    }
+    if (c.shared_ffn > 0) {
+        fail(err, errlen, "%s: shared experts are not supported by this build yet", opt.model_path);
+        return false;
+    }
+    L = c.n_layers; D = c.d_model; V = c.vocab; H = c.n_heads; Hkv = c.n_kv_heads; hd = c.head_dim;
+    q_dim = H * hd; kv_dim = Hkv * hd; E = c.n_experts; K = c.top_k; F = c.expert_ffn; Fd = c.dense_ffn;
+    rope_dim = c.rope_dim;
+    if (hd > 512 || hd % 16) { fail(err, errlen, "%s: head_dim %d unsupported (needs a multiple of 16 <= 512)", opt.model_path, hd); return false; }
+    if (E > 1024) { fail(err, errlen, "%s: %d experts exceed this build's limit of 1024", opt.model_path, E); return false; }
+    if (c.n_moe && F % 64) { fail(err, errlen, "%s: expert_ffn_dim %d is not a multiple of 64", opt.model_path, F); return false; }
+    for (int l = 0; l < L && c.n_moe; l++)
+        for (int e = 0; e < E && c.layer_kind[l]; e++)
+            if (!dtype_is_quant((int)mf.expert(l, e)->dtype)) {
+                fail(err, errlen, "%s: expert (%d, %d) is %s; this build runs Q8/Q4 experts", opt.model_path, l, e,
+                     dtype_name((int)mf.expert(l, e)->dtype));
+                return false;
+            }
+    moe_ord.assign(L, -1);
+    for (int l = 0, k = 0; l < L; l++) moe_ord[l] = c.layer_kind[l] ? k++ : -1;
+    cap = opt.max_seq > 0 ? std::min(opt.max_seq, c.max_seq) : std::min(c.max_seq, 4096);
+    if (cap < 1) cap = 1;
+    B = opt.max_batch;
+    if (rope_dim) {
+        const Tensor *t = mf.tensor("rope_inv_freq");
+        inv_freq.resize(rope_dim / 2);
+        std::memcpy(inv_freq.data(), mf.data(t->offset), sizeof(float) * inv_freq.size());
+    }
+
+    dev = device_index();
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) { fail(err, errlen, "no HIP device is available"); return false; }
+    if (dev < 0 || dev >= ndev) { fail(err, errlen, "HEARTH_DEVICE=%d but %d device(s) exist", dev, ndev); return false; }
+    try {
+        ck(hipSetDevice(dev));
+        ck(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+        if (!upload(msg)) { fail(err, errlen, "%s: %s", opt.model_path, msg.c_str()); return false; }
+        /* KV cache and scratch */
+        kv_layer = (size_t)2 * Hkv * cap * hd;
+        kv = dnew<float>(kv_layer * L);
+        ck(hipMemset(kv, 0, sizeof(float) * kv_layer * L));
+        const size_t Bs = (size_t)B, P = Bs * (size_t)std::max(K, 1);
+        h = dnew<float>(Bs * D);
+        x = dnew<float>(Bs * D);
+        qb = dnew<float>(Bs * q_dim);
+        kb = dnew<float>(Bs * kv_dim);
+        vb = dnew<float>(Bs * kv_dim);
+        qr = dnew<float>(Bs * q_dim);
+        att = dnew<float>(Bs * q_dim);
+        ao = dnew<float>(Bs * D);
+        ldS = (cap + 63) & ~63;
+        S = dnew<float>(Bs * H * (size_t)ldS);
+        ax = make_act(B, D);
+        aatt = make_act(B, q_dim);
+        logits = dnew<float>(Bs * V);
+        rope = dnew<float>(Bs * (size_t)std::max(rope_dim, 2));
+        rfull = dnew<float>(Bs * 2);
+        tokens = dnew<int>(Bs);
+        depth = dnew<int>(Bs);
+        anc = dnew<int>(Bs * Bs);
+        acc_i = dnew<int>(Bs * 2 + 8);
+        dstats = dnew<unsigned long long>(4);
+        ck(hipMemset(dstats, 0, sizeof(unsigned long long) * 4));
+        if (c.n_moe) {
+            lge = dnew<float>(Bs * E);
+            ids = dnew<int>(P);
+            wts = dnew<float>(P);
+            route_meta = dnew<int>(1 + 3 * (size_t)E);
+            pair_tok = dnew<int>(P);
+            pair_of = dnew<int>(P);
+            amid = make_act((int)P, F);
+            Y = dnew<float>(P * D);
+            route_out = dnew<int>(Bs * c.n_moe * K);
+        }
+        if (Fd) {
+            f1 = dnew<float>(Bs * Fd);
+            f2 = dnew<float>(Bs * Fd);
+            af = make_act(B, Fd);
+        }
+        ck(hipHostMalloc((void **)&h_geom, sizeof(int) * (2 * Bs + Bs * Bs), hipHostMallocDefault));
+        ck(hipHostMalloc((void **)&h_rope, sizeof(float) * Bs * std::max(rope_dim, 2), hipHostMallocDefault));
+        ck(hipHostMalloc((void **)&h_res, sizeof(int) * (2 * Bs + 8), hipHostMallocDefault));
+        ck(hipDeviceSynchronize());
+    } catch (const DeviceError &e) {
+        fail(err, errlen, "%s: HIP error during open: %s", opt.model_path, hipGetErrorString(e.e));
+        return false;
+    }
+    return true;
+}
+
+/* ---------------------------------------------------------------- forward */
+
+void hearth_engine::matmul(const DMat &m, const Act &a, const float *xf, int ldx, int T, float *Yp, int ldy,
+                           bool scale_on, float scale) {
+    if (m.quant) {
+        hxd::GemmArgs g{};
+        g.nseg = 1;
+        g.seg[0].m = m.q;
+        g.seg[0].Y = Yp;
+        g.seg[0].ldy = ldy;
+        g.seg[0].scale_on = scale_on;
+        g.seg[0].scale = scale;
+        g.a = a;
+        g.T = T;
+        hxl::gemm(g, st);
+    } else {
+        hxl::fgemv(m.dtype, m.f, m.rows, m.cols, xf, ldx, T, Yp, ldy, st);
+        if (scale_on) hxl::scale_rows(Yp, ldy, T, m.rows, scale, st);
+    }
+}
+
+/* One forward of T tokens whose geometry (tokens, depth, anc, rope) is already on the
+ * device; logits of all T rows into this->logits when want_logits. */
+void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
+    const float rs = c.resid_scale;
+    timed(&ks.norm_s, [&] {
+        hxd::NormArgs n{};
+        n.mode = 0; n.h = h; n.tokens = tokens; n.emb = emb; n.emb_dtype = emb_dtype; n.emb_rb = emb_rb;
+        n.es = c.emb_scale; n.norm_w = layers[0].attn_norm; n.eps = c.eps; n.x = x; n.a = ax; n.T = T; n.D = D;
+        hxl::norm(n, st);
+    });
+    for (int l = 0; l < L; l++) {
+        const Layer &w = layers[l];
+        timed(&ks.attn_s, [&] {
+            if (w.q.quant && w.k.quant && w.v.quant) {
+                hxd::GemmArgs g{};
+                g.nseg = 3;
+                const DMat *ms[3] = {&w.q, &w.k, &w.v};
+                float *ys[3] = {qb, kb, vb};
+                const int ld[3] = {q_dim, kv_dim, kv_dim};
+                for (int s = 0; s < 3; s++) { g.seg[s].m = ms[s]->q; g.seg[s].Y = ys[s]; g.seg[s].ldy = ld[s]; }
+                g.a = ax;
+                g.T = T;
+                hxl::gemm(g, st);
+            } else {
+                matmul(w.q, ax, x, D, T, qb, q_dim, false, 1.0f);
+                matmul(w.k, ax, x, D, T, kb, kv_dim, false, 1.0f);
+                matmul(w.v, ax, x, D, T, vb, kv_dim, false, 1.0f);
+            }
+            hxd::QkvArgs qa{};
+            qa.q = qb; qa.k = kb; qa.v = vb; qa.bq = w.bq; qa.bk = w.bk; qa.bv = w.bv; qa.qn = w.qn; qa.kn = w.kn;
+            qa.qout = qr; qa.kc = kv + (size_t)l * kv_layer; qa.vc = qa.kc + (size_t)Hkv * cap * hd;
+            qa.rope = rope; qa.rfull = rfull; qa.T = T; qa.H = H; qa.Hkv = Hkv; qa.hd = hd; qa.cap = cap;
+            qa.qk_norm = c.qk_norm; qa.rope_dim = rope_dim; qa.rope_style = c.rope_style; qa.eps = c.eps; qa.pos0 = pos;
+            hxl::qkv_post(qa, st);
+            hxd::AttnArgs at{};
+            at.q = qr; at.kc = qa.kc; at.vc = qa.vc; at.S = S; at.ldS = ldS; at.out = att; at.T = T; at.H = H;
+            at.Hkv = Hkv; at.hd = hd; at.cap = cap; at.scale = c.attn_scale;
+            at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos0 = pos;
+            hxl::attention(at, st);
+            if (w.o.quant) hxl::quant_rows(att, q_dim, T, q_dim / 64, aatt, st);
+            matmul(w.o, aatt, att, q_dim, T, ao, D, false, 1.0f);
+        });
+        timed(&ks.norm_s, [&] {
+            hxd::NormArgs n{};
+            n.mode = 1; n.h = h; n.add = ao; n.rs = rs; n.norm_w = w.ffn_norm; n.eps = c.eps; n.x = x; n.a = ax;
+            n.T = T; n.D = D;
+            hxl::norm(n, st);
+        });
+        const float *next_norm = l + 1 < L ? layers[l + 1].attn_norm : out_norm;
+        if (w.moe) {
+            int *n_active = route_meta, *ulist = route_meta + 1, *u_p0 = ulist + E, *u_n = u_p0 + E;
+            timed(&ks.router_s, [&] {
+                hxl::fgemv(0, w.router, E, D, x, D, T, lge, E, st);
+                hxd::RouteArgs r{};
+                r.logits = lge; r.bias = w.router_bias; r.T = T; r.E = E; r.K = K; r.score_fn = c.score_fn;
+                r.n_group = c.n_group; r.topk_group = c.topk_group; r.norm_topk = c.norm_topk;
+                r.routed_scale = c.routed_scale; r.ids = ids; r.wts = wts; r.n_active = n_active; r.ulist = ulist;
+                r.u_p0 = u_p0; r.u_n = u_n; r.pair_tok = pair_tok; r.pair_of = pair_of;
+                r.route_out = route_out; r.moe_ord = moe_ord[l]; r.n_moe = c.n_moe; r.stats = dstats;
+                hxl::route(r, st);
+            });
+            timed(&ks.expert_s, [&] {
+                hxd::MoeArgs m{};
+                m.table = w.experts; m.n_active = n_active; m.ulist = ulist; m.u_p0 = u_p0; m.u_n = u_n;
+                m.pair_tok = pair_tok; m.x = ax; m.mid = amid; m.Y = Y; m.T = T; m.F = F; m.D = D;
+                const int slots = std::min(E, T * K);
+                hxl::expert_gateup(m, slots, st);
+                hxl::expert_down(m, slots, st);
+            });
+            if (profiling) ks.expert_launches++;
+            timed(&ks.norm_s, [&] {
+                hxd::NormArgs n{};
+                n.mode = 2; n.h = h; n.Y = Y; n.wts = wts; n.pair_of = pair_of; n.K = K; n.rs = rs;
+                n.norm_w = next_norm; n.eps = c.eps; n.x = x; n.a = ax; n.T = T; n.D = D;
+                hxl::norm(n, st);
+            });
+        } else {
+            timed(&ks.dense_s, [&] {
+                matmul(w.gate, ax, x, D, T, f1, Fd, false, 1.0f);
+                matmul(w.up, ax, x, D, T, f2, Fd, false, 1.0f);
+                hxl::swiglu_quant(f1, f2, T, Fd, af, st);
+                matmul(w.down, af, f1, Fd, T, ao, D, false, 1.0f);
+            });
+            timed(&ks.norm_s, [&] {
+                hxd::NormArgs n{};
+                n.mode = 1; n.h = h; n.add = ao; n.rs = rs; n.norm_w = next_norm; n.eps = c.eps; n.x = x; n.a = ax;
+                n.T = T; n.D = D;
+                hxl::norm(n, st);
+            });
+        }
+    }
+    if (want_logits)
+        timed(&ks.head_s, [&] { matmul(lm_head, ax, x, D, T, logits, V, true, c.logit_scale); });
+}
+
+/* Uploads tokens and geometry for n tokens at pos (parent NULL: chain) and runs the
+ * forward; returns 0 or a negative code (nothing changed on failure). */
+int hearth_engine::run_geometry(const int32_t *tok, const int32_t *parent, int n, float *logits_out, bool) {
+    int *ht = h_geom, *hdp = h_geom + B, *hanc = h_geom + 2 * B;
+    for (int i = 0; i < n; i++) {
+        ht[i] = tok[i];
+        hdp[i] = parent ? (i == 0 ? 0 : hdp[parent[i]] + 1) : i;
+        for (int v = i, j = hdp[i]; v >= 0 && j >= 0; v = parent ? parent[v] : v - 1, j--) hanc[(size_t)i * B + j] = v;
+    }
+    for (int i = 0; i < n; i++) {
+        const float p = (float)(pos + hdp[i]);
+        for (int j = 0; j < rope_dim / 2; j++) {
+            const float th = p * inv_freq[j];
+            h_rope[(size_t)i * rope_dim + 2 * j] = host_cosf(th) * c.rope_factor;
+            h_rope[(size_t)i * rope_dim + 2 * j + 1] = host_sinf(th) * c.rope_factor;
+        }
+    }
+    ck(hipMemcpyAsync(tokens, ht, sizeof(int) * n, hipMemcpyHostToDevice, st));
+    ck(hipMemcpyAsync(depth, hdp, sizeof(int) * n, hipMemcpyHostToDevice, st));
+    ck(hipMemcpyAsync(anc, hanc, sizeof(int) * (size_t)n * B, hipMemcpyHostToDevice, st));
+    if (rope_dim) ck(hipMemcpyAsync(rope, h_rope, sizeof(float) * (size_t)n * rope_dim, hipMemcpyHostToDevice, st));
+    forward(n, logits_out != nullptr, 0);
+    if (logits_out) ck(hipMemcpyAsync(logits_out, logits, sizeof(float) * (size_t)n * V, hipMemcpyDeviceToHost, st));
+    return OK;
+}
+
+void hearth_engine::write_trace(int T) {
+    if (!trace || !c.n_moe) return;
+    const size_t n = (size_t)T * c.n_moe * K;
+    h_routes.resize(n);
+    ck(hipMemcpy(h_routes.data(), route_out, sizeof(int) * n, hipMemcpyDeviceToHost));
+    std::vector<uint8_t> buf(2 * n);
+    for (size_t i = 0; i < n; i++) {
+        buf[2 * i] = (uint8_t)(h_routes[i] & 0xff);
+        buf[2 * i + 1] = (uint8_t)((h_routes[i] >> 8) & 0xff);
+    }
+    if (fwrite(buf.data(), 1, buf.size(), trace) != buf.size()) {
+        log_msg(LOG_ERROR, "routing trace: write failed; tracing stopped");
+        fclose(trace);
+        trace = nullptr;
+    }
+}
+
+int hearth_engine::eval_chunked(const int32_t *tok, int n, float *logits_out, int all_logits) {
+    const double t0 = now_s();
+    const int start = pos;
+    try {
+        for (int off = 0; off < n; off += B) {
+            const int T = std::min(B, n - off);
+            float *lg = nullptr;
+            bool copy_last = false;
+            if (logits_out && all_logits) lg = logits_out + (size_t)off * V;
+            else if (logits_out && off + T == n) copy_last = true;
+            /* all_logits 0: compute the chunk's logits only for its last row */
+            run_geometry(tok + off, nullptr, T, lg, false);
+            if (copy_last) {
+                if (!lg) {
+                    /* run_geometry skipped the head: run it for the last row only */
+                    timed(&ks.head_s, [&] {
+                        hxd::Act last = ax;
+                        last.q += (size_t)(T - 1) * ax.nbp * 64;
+                        last.d += (size_t)(T - 1) * ax.nbp;
+                        last.s += (size_t)(T - 1) * ax.nbp;
+                        matmul(lm_head, last, x + (size_t)(T - 1) * D, D, 1, logits, V, true, c.logit_scale);
+                    });
+                    ck(hipMemcpyAsync(logits_out, logits, sizeof(float) * V, hipMemcpyDeviceToHost, st));
+                }
+            }
+            write_trace(T);
+            pos += T;
+            tokens_done += T;
+            forward_calls++;
+        }
+        ck(hipStreamSynchronize(st));
+        if (profiling) collect_events();
+    } catch (const DeviceError &e) {
+        log_msg(LOG_ERROR, "HIP error in hearth_eval: %s", hipGetErrorString(e.e));
+        pos = start;
+        return E_IO;
+    }
+    wall_s += now_s() - t0;
+    return OK;
+}
+
+/* ---------------------------------------------------------------- C ABI */
+
+namespace {
+std::atomic<int> g_log_init{0};
+void init_log_level(int verbose) {
+    const char *s = getenv("HEARTH_LOG");
+    if (s && *s) set_log_level(env_int("HEARTH_LOG", LOG_WARN));
+    else if (verbose > 0 && get_log_level() < (verbose == 1 ? LOG_INFO : LOG_DEBUG))
+        set_log_level(verbose == 1 ? LOG_INFO : LOG_DEBUG);
+    g_log_init = 1;
+}
+
+bool parse_isa(const char *s, int *out) {
+    static const char *names[] = {"auto", "scalar", "avx2", "avx512"};
+    while (*s == ' ') s++;
+    for (int i = 0; i < 4; i++) {
+        const char *a = s, *b = names[i];
+        while (*a && *b && ((*a >= 'A' && *a <= 'Z') ? *a - 'A' + 'a' : *a) == *b) { a++; b++; }
+        if (!*a && !*b) { *out = i; return true; }
+    }
+    if (s[0] >= '0' && s[0] <= '3' && s[1] == 0) { *out = s[0] - '0'; return true; }
+    return false;
+}
+
+int cpu_isa() {
+#if defined(__x86_64__) && !defined(__HIP_DEVICE_COMPILE__)
+    __builtin_cpu_init();
+    if (__builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") && __builtin_cpu_supports("avx512vl") &&
+        __builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("fma") && __builtin_cpu_supports("avx2"))
+        return HEARTH_ISA_AVX512;
+    if (__builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma")) return HEARTH_ISA_AVX2;
+#endif
+    return HEARTH_ISA_SCALAR;
+}
+} // namespace
+
+extern "C" {
+
+HEARTH_API const char *hearth_version(void) { return "0.1.0"; }
+
+HEARTH_API int hearth_cpu_isa(void) { return cpu_isa(); }
+
+HEARTH_API void hearth_default_options(hearth_options *o) {
+    if (!o) return;
+    std::memset(o, 0, sizeof *o);
+    o->cache_gb = 8.0;
+    o->direct_io = 1;
+    o->policy = HEARTH_POLICY_LFU;
+    o->prefetch = HEARTH_PREFETCH_SHARED;
+    o->isa = HEARTH_ISA_AUTO;
+}
+
+/* reference api.c:108-196: env overrides, validation, defaults; then the model */
+HEARTH_API hearth_engine *hearth_open(const hearth_options *in, char *err, size_t errlen) {
+    if (err && errlen) err[0] = 0;
+    if (!in) { fail(err, errlen, "hearth_open: options are NULL"); return nullptr; }
+    hearth_options o = *in;
+    init_log_level(o.verbose);
+    const char *s = getenv("HEARTH_ISA");
+    if (s && *s && !parse_isa(s, &o.isa)) {
+        fail(err, errlen, "HEARTH_ISA=%s is not one of auto, scalar, avx2, avx512", s);
+        return nullptr;
+    }
+    o.n_threads = env_int("HEARTH_THREADS", o.n_threads);
+    o.n_io_threads = env_int("HEARTH_IO_THREADS", o.n_io_threads);
+    o.cache_gb = env_double("HEARTH_CACHE_GB", o.cache_gb);
+    if (!o.model_path || !*o.model_path) { fail(err, errlen, "hearth_open: no model path"); return nullptr; }
+    if (o.n_mirrors < 0 || o.n_mirrors > 8) { fail(err, errlen, "hearth_open: n_mirrors %d outside 0..8", o.n_mirrors); return nullptr; }
+    for (int i = 0; i < o.n_mirrors; i++)
+        if (!o.mirror_paths[i] || !*o.mirror_paths[i]) { fail(err, errlen, "hearth_open: mirror %d has no path", i); return nullptr; }
+    if (!(o.cache_gb >= 0.0) || std::isinf(o.cache_gb)) { fail(err, errlen, "hearth_open: cache_gb must be a finite number >= 0"); return nullptr; }
+    if (!(o.pin_fraction >= 0.0f) || o.pin_fraction > 1.0f) { fail(err, errlen, "hearth_open: pin_fraction must be in [0, 1]"); return nullptr; }
+    if (o.n_threads < 0 || o.n_io_threads < 0 || o.max_seq < 0 || o.max_batch < 0 || o.prefetch_extra < 0) {
+        fail(err, errlen, "hearth_open: n_threads, n_io_threads, max_seq, max_batch and prefetch_extra must be >= 0");
+        return nullptr;
+    }
+    if (o.policy != HEARTH_POLICY_LRU && o.policy != HEARTH_POLICY_LFU) { fail(err, errlen, "hearth_open: unknown cache policy %d", o.policy); return nullptr; }
+    if (o.prefetch < HEARTH_PREFETCH_OFF || o.prefetch > HEARTH_PREFETCH_SHARED) { fail(err, errlen, "hearth_open: unknown prefetch mode %d", o.prefetch); return nullptr; }
+    if (o.isa < HEARTH_ISA_AUTO || o.isa > HEARTH_ISA_AVX512) { fail(err, errlen, "hearth_open: unknown ISA %d", o.isa); return nullptr; }
+    if (o.isa == HEARTH_ISA_AUTO) o.isa = cpu_isa();
+    else if (o.isa > cpu_isa()) { fail(err, errlen, "hearth_open: ISA %d is not supported by this CPU", o.isa); return nullptr; }
+    if (o.n_threads == 0) o.n_threads = std::max(1, (int)std::thread::hardware_concurrency());
+    if (o.n_io_threads == 0) o.n_io_threads = 8;
+    if (o.max_batch == 0) o.max_batch = 512;
+    if (o.max_batch > MAX_BATCH) o.max_batch = MAX_BATCH;
+    o.direct_io = o.direct_io ? 1 : 0;
+    o.warm_start = o.warm_start ? 1 : 0;
+
+    std::unique_ptr<hearth_engine> e(new (std::nothrow) hearth_engine());
+    if (!e) { fail(err, errlen, "out of memory"); return nullptr; }
+    e->opt = o;
+    e->verbose = o.verbose;
+    if (!e->open_model(err, errlen)) return nullptr;
+    log_msg(LOG_INFO, "%s: %s, %d layers (%d MoE), d_model %d, vocab %d, KV %d positions, device %d", o.model_path,
+            e->c.arch.c_str(), e->L, e->c.n_moe, e->D, e->V, e->cap, e->dev);
+    return e.release();
+}
+
+HEARTH_API void hearth_close(hearth_engine *e) { delete e; }
+
+HEARTH_API int hearth_info(hearth_engine *e, hearth_model_info *out) {
+    if (!e || !out) return E_ARG;
+    std::memset(out, 0, sizeof *out);
+    std::snprintf(out->arch, sizeof out->arch, "%s", e->c.arch.c_str());
+    out->n_layers = e->L;
+    out->d_model = e->D;
+    out->vocab_size = e->V;
+    out->max_seq = e->c.max_seq;
+    out->n_heads = e->H;
+    out->n_kv_heads = e->Hkv;
+    out->head_dim = e->hd;
+    out->attn_kind = e->c.attn_kind;
+    out->n_experts = e->E;
+    out->top_k = e->K;
+    out->expert_ffn_dim = e->c.expert_ffn;
+    out->n_moe_layers = e->c.n_moe;
+    out->bos_id = e->c.bos_id;
+    out->n_eos = (int)std::min<size_t>(8, e->c.eos_ids.size());
+    for (int i = 0; i < out->n_eos; i++) out->eos_ids[i] = e->c.eos_ids[i];
+    out->dense_bytes = e->mf.dense_bytes;
+    out->expert_bytes = e->mf.expert_region_bytes;
+    out->slab_bytes_max = e->mf.slab_bytes_max;
+    out->params_total = e->mf.params_total;
+    out->params_active = e->mf.params_active;
+    out->cache_slots = e->c.n_moe * e->E;
+    out->isa = e->opt.isa;
+    out->n_threads = e->opt.n_threads;
+    out->n_io_threads = e->opt.n_io_threads;
+    return OK;
+}
+
+HEARTH_API int hearth_eval(hearth_engine *e, const int32_t *tokens, int n, float *logits, int all_logits) {
+    if (!e || n < 0) return E_ARG;
+    if (n == 0) return OK;
+    if (!tokens) return E_ARG;
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= e->V) return E_TOKEN;
+    if ((int64_t)e->pos + n > (int64_t)e->cap) return E_CAPACITY;
+    if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
+    e->tree_n = 0;
+    return e->eval_chunked(tokens, n, logits, all_logits ? 1 : 0);
+}
+
+HEARTH_API int hearth_pos(hearth_engine *e) { return e ? e->pos : E_ARG; }
+
+HEARTH_API int hearth_reset(hearth_engine *e) {
+    if (!e) return E_ARG;
+    e->pos = 0;
+    e->tree_n = 0;
+    return OK;
+}
+
+HEARTH_API int hearth_rewind(hearth_engine *e, int pos) {
+    if (!e || pos < 0) return E_ARG;
+    if (pos > e->pos) return E_CAPACITY;
+    e->pos = pos;
+    e->tree_n = 0;
+    return OK;
+}
+
+HEARTH_API int hearth_get_stats(hearth_engine *e, hearth_stats *out) {
+    if (!e || !out) return E_ARG;
+    std::memset(out, 0, sizeof *out);
+    unsigned long long d[2] = {0, 0};
+    if (hipSetDevice(e->dev) == hipSuccess && hipStreamSynchronize(e->st) == hipSuccess)
+        (void)hipMemcpy(d, e->dstats, sizeof d, hipMemcpyDeviceToHost);
+    out->tokens = e->tokens_done;
+    out->forward_calls = e->forward_calls;
+    out->wall_s = e->wall_s;
+    out->attn_s = e->ks.attn_s;
+    out->moe_s = e->ks.router_s + e->ks.expert_s;
+    out->dense_s = e->ks.dense_s + e->ks.head_s + e->ks.norm_s;
+    out->expert_uses = d[0] - e->stats_base[0];
+    out->expert_loads_unique = d[1] - e->stats_base[1];
+    out->cache_hits = out->expert_uses;   /* every expert is resident in HBM */
+    out->cache_slots = e->c.n_moe * e->E;
+    out->cache_resident = out->cache_slots;
+    return OK;
+}
+
+HEARTH_API void hearth_reset_stats(hearth_engine *e) {
+    if (!e) return;
+    unsigned long long d[2] = {0, 0};
+    if (hipSetDevice(e->dev) == hipSuccess && hipStreamSynchronize(e->st) == hipSuccess)
+        (void)hipMemcpy(d, e->dstats, sizeof d, hipMemcpyDeviceToHost);
+    e->stats_base[0] = d[0];
+    e->stats_base[1] = d[1];
+    e->tokens_done = e->forward_calls = 0;
+    e->wall_s = 0.0;
+    e->ks = hearth_gpu_kstats{};
+}
+
+/* FORMAT.md §9; refuses to overwrite an existing non-empty file that is not a trace
+ * (reference model.c:1148-1168 rule). */
+HEARTH_API int hearth_trace_start(hearth_engine *e, const char *path) {
+    if (!e || !path || !*path) return E_ARG;
+    FILE *f = fopen(path, "rb");
+    if (f) {
+        unsigned char m[4];
+        fseek(f, 0, SEEK_END);
+        const long size = ftell(f);
+        fseek(f, 0, SEEK_SET);
+        const bool ok = size == 0 || (size >= 4 && fread(m, 1, 4, f) == 4 && m[0] == 'H' && m[1] == 'R' && m[2] == 'T' && m[3] == 'R');
+        fclose(f);
+        if (!ok) return E_ARG;
+    }
+    f = fopen(path, "wb");
+    if (!f) return E_IO;
+    uint32_t hdr[6] = {0x52545248u, 1u, (uint32_t)e->L, (uint32_t)e->E, (uint32_t)e->K, (uint32_t)e->c.n_moe};
+    if (fwrite(hdr, 4, 6, f) != 6) { fclose(f); return E_IO; }
+    if (e->trace) fclose(e->trace);
+    e->trace = f;
+    return OK;
+}
+
+HEARTH_API int hearth_trace_stop(hearth_engine *e) {
+    if (!e) return E_ARG;
+    if (e->trace) { fclose(e->trace); e->trace = nullptr; }
+    return OK;
+}
+
+HEARTH_API int hearth_route_replay(hearth_engine *e, const char *path) {
+    if (!e) return E_ARG;
+    if (!path || !*path) return OK;
+    log_msg(LOG_ERROR, "route replay is not supported by this build yet");
+    return E_FORMAT;
+}
+
+/* ---- extensions (hearth_gpu.h) ---- */
+
+HEARTH_API int hearth_verify_tree(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n, float *logits) {
+    if (!e || n < 1 || !tokens) return E_ARG;
+    if (n > e->B) return E_ARG;
+    for (int i = 0; i < n; i++) {
+        if (tokens[i] < 0 || tokens[i] >= e->V) return E_TOKEN;
+        if (parent && ((i == 0 && parent[i] != -1) || (i > 0 && (parent[i] < 0 || parent[i] >= i)))) return E_ARG;
+    }
+    if ((int64_t)e->pos + n > (int64_t)e->cap) return E_CAPACITY;
+    if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
+    const double t0 = now_s();
+    try {
+        e->run_geometry(tokens, parent, n, logits, false);
+        e->write_trace(n);
+        ck(hipStreamSynchronize(e->st));
+        if (e->profiling) e->collect_events();
+    } catch (const DeviceError &err) {
+        log_msg(LOG_ERROR, "HIP error in hearth_verify_tree: %s", hipGetErrorString(err.e));
+        return E_IO;
+    }
+    e->tree_n = n;
+    e->tokens_done += n;
+    e->forward_calls++;
+    e->wall_s += now_s() - t0;
+    return OK;
+}
+
+HEARTH_API int hearth_commit_path(hearth_engine *e, const int32_t *path, int n) {
+    if (!e || n < 0 || (n && !path)) return E_ARG;
+    if (n > e->tree_n) return E_ARG;
+    for (int j = 0; j < n; j++)
+        if (path[j] < j || path[j] >= e->tree_n || (j && path[j] <= path[j - 1])) return E_ARG;
+    if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
+    try {
+        bool moves = false;
+        for (int j = 0; j < n; j++) moves = moves || path[j] != j;
+        if (moves) {
+            std::memcpy(e->h_res, path, sizeof(int) * n);
+            ck(hipMemcpyAsync(e->acc_i, e->h_res, sizeof(int) * n, hipMemcpyHostToDevice, e->st));
+            hxl::kv_move(e->kv, e->kv_layer, e->L, e->Hkv, e->cap, e->hd, e->pos, e->acc_i, n, e->st);
+            ck(hipStreamSynchronize(e->st));
+        }
+    } catch (const DeviceError &err) {
+        log_msg(LOG_ERROR, "HIP error in hearth_commit_path: %s", hipGetErrorString(err.e));
+        return E_IO;
+    }
+    e->pos += n;
+    e->tree_n = 0;
+    return OK;
+}
+
+HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,
+                                    int32_t *path_out, int *n_path, int32_t *final_tok, float *logits) {
+    if (!e || n < 1 || !tokens || !path_out || !n_path || !final_tok) return E_ARG;
+    if (n > e->B) return E_ARG;
+    for (int i = 0; i < n; i++) {
+        if (tokens[i] < 0 || tokens[i] >= e->V) return E_TOKEN;
+        if (parent && ((i == 0 && parent[i] != -1) || (i > 0 && (parent[i] < 0 || parent[i] >= i)))) return E_ARG;
+    }
+    if ((int64_t)e->pos + n > (int64_t)e->cap) return E_CAPACITY;
+    if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
+    const double t0 = now_s();
+    int np = 0, fin = -1, status = 0;
+    try {
+        e->run_geometry(tokens, parent, n, nullptr, false);
+        /* logits stay in HBM; the head ran only if requested -> force it here */
+        e->timed(&e->ks.head_s, [&] { e->matmul(e->lm_head, e->ax, e->x, e->D, n, e->logits, e->V, true, e->c.logit_scale); });
+        if (logits) ck(hipMemcpyAsync(logits, e->logits, sizeof(float) * (size_t)n * e->V, hipMemcpyDeviceToHost, e->st));
+        int *d_tok = e->tokens;
+        int *d_par = e->acc_i, *d_amax = e->acc_i + e->B, *d_res = e->acc_i + 2 * e->B;
+        int *h_par = e->h_res;
+        for (int i = 0; i < n; i++) h_par[i] = parent ? parent[i] : i - 1;
+        ck(hipMemcpyAsync(d_par, h_par, sizeof(int) * n, hipMemcpyHostToDevice, e->st));
+        hxd::AcceptArgs a{};
+        a.rows = e->logits; a.n = n; a.V = e->V; a.tokens = d_tok; a.parent = d_par; a.amax = d_amax;
+        a.path = e->depth; /* reuse: depth is not needed after the forward */
+        a.result = d_res;
+        hxl::accept_greedy(a, e->st);
+        ck(hipMemcpyAsync(e->h_res + e->B, e->depth, sizeof(int) * n, hipMemcpyDeviceToHost, e->st));
+        ck(hipMemcpyAsync(e->h_res + 2 * e->B, d_res, sizeof(int) * 3, hipMemcpyDeviceToHost, e->st));
+        ck(hipStreamSynchronize(e->st));
+        np = e->h_res[2 * e->B];
+        fin = e->h_res[2 * e->B + 1];
+        status = e->h_res[2 * e->B + 2];
+        if (status == 0) {
+            for (int j = 0; j < np; j++) path_out[j] = e->h_res[e->B + j];
+            bool moves = false;
+            for (int j = 0; j < np; j++) moves = moves || path_out[j] != j;
+            if (moves) {
+                ck(hipMemcpyAsync(e->acc_i, path_out, sizeof(int) * np, hipMemcpyHostToDevice, e->st));
+                hxl::kv_move(e->kv, e->kv_layer, e->L, e->Hkv, e->cap, e->hd, e->pos, e->acc_i, np, e->st);
+                ck(hipStreamSynchronize(e->st));
+            }
+        }
+        e->write_trace(n);
+        if (e->profiling) e->collect_events();
+    } catch (const DeviceError &err) {
+        log_msg(LOG_ERROR, "HIP error in hearth_verify_greedy: %s", hipGetErrorString(err.e));
+        return E_IO;
+    }
+    if (status != 0) return E_ARG;
+    *n_path = np;
+    *final_tok = fin;
+    e->pos += np;
+    e->tree_n = 0;
+    e->tokens_done += n;
+    e->forward_calls++;
+    e->wall_s += now_s() - t0;
+    return OK;
+}
+
+HEARTH_API int hearth_gpu_set_profiling(hearth_engine *e, int on) {
+    if (!e) return E_ARG;
+    e->profiling = on != 0;
+    return OK;
+}
+
+HEARTH_API int hearth_gpu_get_kstats(hearth_engine *e, hearth_gpu_kstats *out) {
+    if (!e || !out) return E_ARG;
+    *out = e->ks;
+    unsigned long long d[2] = {0, 0};
+    if (hipSetDevice(e->dev) == hipSuccess && hipStreamSynchronize(e->st) == hipSuccess)
+        (void)hipMemcpy(d, e->dstats, sizeof d, hipMemcpyDeviceToHost);
+    uint64_t per = 0;
+    for (const Layer &l : e->layers)
+        if (l.moe) { per = l.expert_bytes_each; break; }
+    out->expert_bytes = (d[1] - e->stats_base[1]) * per;
+    return OK;
+}
+
+HEARTH_API void hearth_gpu_reset_kstats(hearth_engine *e) {
+    if (e) e->ks = hearth_gpu_kstats{};
+}
+
+HEARTH_API int hearth_gpu_device(char *name, size_t n) {
+    const int d = device_index();
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, d) != hipSuccess) return E_IO;
+    if (name && n) std::snprintf(name, n, "%s (%s)", p.name, p.gcnArchName);
+    return d;
+}
+
+} // extern "C"

@@ -1,0 +1,139 @@
+/*
+ * hx_device.h — device data layouts and canonical arithmetic shared by the HIP
+ * kernels of the MI355X verify engine (gfx950).
+ *
+ * Numerics follow the reference's docs/NUMERICS.md exactly: int8 x int8 block sums
+ * are exact int32 (here from v_mfma_i32_16x16x64_i8, one 64-block per K step), the
+ * f32 fold over blocks is acc = acc + (float)isum * (dw * dx) in block order with no
+ * FMA (all sources are built with -ffp-contract=off and the fold uses explicit
+ * round-to-nearest intrinsics), dot16/sum16 use 16 lanes then the 8/4/2/1 tree, and
+ * NaN outputs are stored as 0x7fc00000. The only libm-dependent step, exp, uses
+ * hx_exp_port (Cody-Waite reduction + degree-13 Taylor polynomial in IEEE double,
+ * basic operations only), which gives the same bits as the CPU restatement's
+ * portable mode; RoPE cos/sin come from the host (libm), as in the reference
+ * (engine/src/model.c:386-397).
+ *
+ * HBM layouts
+ *   QMat (Q8/Q4 matrix, rows x cols, nb = cols/64 blocks, nbp = nb rounded up to even):
+ *     w: 1 KiB tiles. Q8: tile (rt, g) = 16 rows x block g; Q4: tile (rt, gp) = 16 rows
+ *        x blocks 2gp, 2gp+1. Lane l of a wave reads the 16 bytes at l*16 of a tile:
+ *        row rt*16 + l%16, k-group kg = l/16. Q8: bytes b of lane l = element
+ *        kperm(kg, b) of block g. Q4: bytes 0-7 = bytes 8kg..8kg+7 of block 2gp (their
+ *        low nibbles are elements 8kg.., high nibbles 32+8kg..), bytes 8-15 the same of
+ *        block 2gp+1. Rows are padded to a multiple of 16 with zero weights.
+ *     d: binary16 scales, [nbp][rows_pad] (scale of row r, block g at g*rows_pad + r).
+ *   Act (activation blocks of T vectors, NUMERICS §2): q int8 [T][nbp][64] in kperm
+ *     order, d f32 [T][nbp], s int32 [T][nbp] (sum of the 64 q).
+ *   kperm(kg, b) = b < 8 ? 8kg + b : 32 + 8kg + (b - 8): the k order of one MFMA step;
+ *     weights and activations use the same order, so the int32 sum is the block's.
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace hxd {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t CANON_NAN = 0x7fc00000u;
+
+struct QMat {
+    const uint8_t *w;
+    const uint16_t *d;
+    int dtype;        /* 3 = Q8, 4 = Q4 */
+    int rows, rows_pad, nb, nbp;
+};
+
+struct Act {
+    int8_t *q;
+    float *d;
+    int32_t *s;
+    int nbp;
+};
+
+/* ---- canonical scalar helpers (device) ---- */
+
+__device__ __forceinline__ float fadd(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float fmul(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float fdiv(float a, float b) { return __fdiv_rn(a, b); }
+__device__ __forceinline__ double dadd(double a, double b) { return __dadd_rn(a, b); }
+__device__ __forceinline__ double dmul(double a, double b) { return __dmul_rn(a, b); }
+__device__ __forceinline__ double dsub(double a, double b) { return __dsub_rn(a, b); }
+
+__device__ __forceinline__ float canon(float v) { return v != v ? __uint_as_float(CANON_NAN) : v; }
+
+/* binary16 -> binary32 (exact) */
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 x;
+    __builtin_memcpy(&x, &h, 2);
+    return (float)x;
+}
+
+/* exp in IEEE double from basic operations (Cody & Waite 1980 reduction with a
+ * 32-bit ln2 head, degree-13 Taylor series on |r| <= ln2/2, exact power-of-two
+ * scaling in two steps); the CPU restatement's ho_exp_port_d is the same function. */
+__device__ inline double exp_port_d(double x) {
+    const double inv_ln2 = 1.44269504088896338700e+00;
+    const double ln2_hi = 6.93147180369123816490e-01;
+    const double ln2_lo = 1.90821492927058770002e-10;
+    const double shifter = 6755399441055744.0;
+    if (x != x) return x;
+    if (x > 709.79) return __longlong_as_double(0x7ff0000000000000ll);
+    if (x < -745.2) return 0.0;
+    const double t = dmul(x, inv_ln2);
+    const double nd = dsub(dadd(t, shifter), shifter);
+    const long long n = (long long)nd;
+    const double r = dsub(dsub(x, dmul(nd, ln2_hi)), dmul(nd, ln2_lo));
+    double p = 1.0 / 6227020800.0;
+    p = dadd(dmul(p, r), 1.0 / 479001600.0);
+    p = dadd(dmul(p, r), 1.0 / 39916800.0);
+    p = dadd(dmul(p, r), 1.0 / 3628800.0);
+    p = dadd(dmul(p, r), 1.0 / 362880.0);
+    p = dadd(dmul(p, r), 1.0 / 40320.0);
+    p = dadd(dmul(p, r), 1.0 / 5040.0);
+    p = dadd(dmul(p, r), 1.0 / 720.0);
+    p = dadd(dmul(p, r), 1.0 / 120.0);
+    p = dadd(dmul(p, r), 1.0 / 24.0);
+    p = dadd(dmul(p, r), 1.0 / 6.0);
+    p = dadd(dmul(p, r), 0.5);
+    p = dadd(dmul(p, r), 1.0);
+    p = dadd(dmul(p, r), 1.0);
+    const long long n1 = n < -1000 ? n + 600 : (n > 1000 ? n - 600 : n), n2 = n - n1;
+    const double s1 = __longlong_as_double((n1 + 1023) << 52), s2 = __longlong_as_double((n2 + 1023) << 52);
+    return dmul(dmul(p, s1), s2);
+}
+
+__device__ __forceinline__ float exp_port_f(float x) { return __double2float_rn(exp_port_d((double)x)); }
+
+/* position of element e (0..63) of a block in kperm order */
+__device__ __forceinline__ int kperm_pos(int e) {
+    return e < 32 ? (e >> 3) * 16 + (e & 7) : ((e - 32) >> 3) * 16 + 8 + ((e - 32) & 7);
+}
+
+/* NUMERICS §2 for the 64 values held one per lane by a full wave: writes q (kperm
+ * order), d and the sum of block g of token row tok. Every lane must call it. */
+__device__ inline void quant_block_wave(float x, Act a, int tok, int g) {
+    const int lane = threadIdx.x & 63;
+    float ax = fabsf(x);
+    ax = ax == ax ? ax : 0.0f;                    /* NaN never wins the max */
+    float amax = ax;
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float d = fdiv(amax, 127.0f);
+    const float id = d != 0.0f ? fdiv(1.0f, d) : 0.0f;
+    float v = fmul(x, id);
+    if (v != v) v = 0.0f;
+    v = v > 127.0f ? 127.0f : v;
+    v = v < -127.0f ? -127.0f : v;
+    const int q = (int)__builtin_rintf(v);
+    int sum = q;
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    const size_t base = (size_t)tok * a.nbp + g;
+    a.q[base * 64 + kperm_pos(lane)] = (int8_t)q;
+    if (lane == 0) {
+        a.d[base] = d;
+        a.s[base] = sum;
+    }
+}
+
+} // namespace hxd

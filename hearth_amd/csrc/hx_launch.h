@@ -1,0 +1,143 @@
+/*
+ * hx_launch.h — kernel argument blocks and host-side launchers of the verify step.
+ * Every launcher only enqueues work on the given stream; shapes are checked by the
+ * engine before any launch (engine.cpp).
+ */
+#pragma once
+
+#include "hx_device.h"
+
+namespace hxd {
+
+struct GemmSeg {
+    QMat m;
+    float *Y;          /* Y[t * ldy + row] */
+    int ldy;
+    int scale_on;      /* 1: y = canon(scale * canon(acc)) (logit_scale) */
+    float scale;
+    int wg0;           /* first workgroup of the segment (set by the launcher) */
+};
+
+struct GemmArgs {
+    GemmSeg seg[4];
+    int nseg;
+    Act a;             /* activations of tokens [0, T) */
+    int T, t0;
+};
+
+struct ExpertW { QMat gate, up, down; };
+
+struct MoeArgs {
+    const ExpertW *table;     /* [n_experts] of this layer */
+    const int *n_active;      /* number of active experts (device scalar) */
+    const int *ulist, *u_p0, *u_n;
+    const int *pair_tok;      /* pair -> token */
+    Act x;                    /* normalized token activations [T] */
+    Act mid;                  /* SwiGLU activations per pair [P] */
+    float *Y;                 /* expert outputs [P][D] */
+    int T, F, D;
+};
+
+/* Routing (NUMERICS §5.3) of T tokens from router logits. */
+struct RouteArgs {
+    const float *logits;      /* [T][E] */
+    const float *bias;        /* [E] or null */
+    int T, E, K, score_fn, n_group, topk_group, norm_topk;
+    float routed_scale;
+    int *ids;                 /* [T][K] */
+    float *wts;               /* [T][K] */
+    int *n_active, *ulist, *u_p0, *u_n, *pair_tok, *pair_of;
+    int *route_out;           /* [T][n_moe][K] or null */
+    int moe_ord, n_moe;
+    unsigned long long *stats;   /* [0] expert uses, [1] unique expert loads */
+};
+
+/* Per-call token geometry: token t sits at KV slot pos0 + t, has RoPE position
+ * pos0 + depth[t] and attends to slots 0..pos0-1 followed by pos0 + anc[t][j] for
+ * j = 0..depth[t] (its ancestors from the root, itself last). A chain has depth[t] = t
+ * and anc[t][j] = j. */
+struct TokGeom {
+    const int *depth;         /* [T] */
+    const int *anc;           /* [T][anc_ld] */
+    int anc_ld;
+    int pos0;
+};
+
+struct AttnArgs {
+    const float *q;           /* [T][H][hd] after qk-norm and RoPE */
+    const float *kc, *vc;     /* layer caches [Hkv][cap][hd] */
+    float *S;                 /* scratch [T][H][ldS] */
+    int ldS;
+    float *out;               /* [T][H*hd] */
+    int T, H, Hkv, hd, cap;
+    float scale;
+    TokGeom g;
+};
+
+struct QkvArgs {
+    const float *q, *k, *v;   /* GEMM outputs [T][H*hd], [T][Hkv*hd] */
+    const float *bq, *bk, *bv, *qn, *kn;
+    float *qout;              /* [T][H*hd] */
+    float *kc, *vc;           /* layer caches [Hkv][cap][hd] */
+    const float *rope;        /* [T][rope_dim]: (cos, sin) pairs, host computed */
+    float *rfull;             /* [T][2] scratch for qk_norm = 2 */
+    int T, H, Hkv, hd, cap, qk_norm, rope_dim, rope_style;
+    float eps;
+    int pos0;
+};
+
+/* Residual update + RMSNorm + activation quantization, one workgroup per token:
+ *   mode 0: h = es * embed(tok[t])
+ *   mode 1: h = h + rs * add[t]
+ *   mode 2: h = h + rs * (sum_j w[t][j] * Y[pair_of[t][j]] (+ shared[t]))
+ * then x = rmsnorm(h, w) and its activation blocks. */
+struct NormArgs {
+    int mode;
+    float *h;                 /* [T][D] */
+    const float *add;         /* mode 1 / shared (mode 2, may be null) */
+    const float *Y;           /* mode 2 */
+    const float *wts;
+    const int *pair_of;
+    int K;
+    const int *tokens;        /* mode 0 */
+    const uint8_t *emb;       /* mode 0: FORMAT rows */
+    int emb_dtype;
+    size_t emb_rb;
+    float es, rs;
+    const float *norm_w;      /* [D] */
+    float eps;
+    float *x;                 /* [T][D] or null */
+    Act a;
+    int T, D;
+};
+
+struct AcceptArgs {
+    const float *rows;        /* [n][V] */
+    int n, V;
+    const int *tokens, *parent;
+    int *amax;                /* [n] argmax or -1 for bad rows */
+    int *path;                /* [n] */
+    int *result;              /* [0] n_path, [1] final token, [2] status (0 ok, -1 bad logits) */
+};
+
+} // namespace hxd
+
+namespace hxl {
+using namespace hxd;
+/* rows [r0, r0 + count) of m from FORMAT.md bytes at src_dev (count may run into the pad rows) */
+void repack(const uint8_t *src_dev, int r0, int count, const QMat &m, hipStream_t st);
+void quant_rows(const float *x, int64_t ldx, int T, int nb, const Act &a, hipStream_t st);
+void gemm(const GemmArgs &a, hipStream_t st);
+void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st);
+void expert_down(const MoeArgs &a, int n_slots, hipStream_t st);
+void fgemv(int dtype, const void *W, int rows, int cols, const float *X, int ldx, int T, float *Y, int ldy, hipStream_t st);
+void route(const RouteArgs &a, hipStream_t st);
+void norm(const NormArgs &a, hipStream_t st);
+void swiglu_quant(float *g, const float *u, int T, int F, const Act &a, hipStream_t st);
+void scale_rows(float *y, int ldy, int T, int n, float s, hipStream_t st);
+void qkv_post(const QkvArgs &a, hipStream_t st);
+void attention(const AttnArgs &a, hipStream_t st);
+void kv_move(float *cache_layer0, size_t layer_stride, int L, int Hkv, int cap, int hd, int pos0, const int *path_dev,
+             int n, hipStream_t st);
+void accept_greedy(const AcceptArgs &a, hipStream_t st);
+} // namespace hxl

@@ -1,0 +1,463 @@
+/*
+ * k_layer.hip — per-layer elementwise work, routing and greedy acceptance on gfx950.
+ *
+ * Reference semantics (engine/src/model.c): embedding 1178-1182, residual adds
+ * 1194-1198, rmsnorm quant.c:626-632, MoE combine moe_sum_range 904-923, routing
+ * route_select/route_weights 793-843 with ranks_before 220-226, union/bucketing
+ * 1020-1037, GQA post-processing gqa_post_range 484-517, SwiGLU quant.c:644-649;
+ * greedy acceptance python/hearth/generate.py:365-392 (argmax: first index wins).
+ */
+#include "hx_device.h"
+#include "hx_launch.h"
+
+using namespace hxd;
+
+namespace {
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+/* 16-lane canonical tree (NUMERICS §1) of the partials held by lanes 0..15 of a
+ * 16-lane segment: returns the total in lane 0 of the segment. */
+__device__ __forceinline__ float tree16(float L) {
+#pragma unroll
+    for (int s = 8; s >= 1; s >>= 1) L = fadd(L, __shfl_down(L, s, 16));
+    return L;
+}
+
+/* element i of a FORMAT.md row of dtype dt (embedding lookup) */
+__device__ __forceinline__ float deq_elem(const uint8_t *row, int dt, int i) {
+    switch (dt) {
+    case 0: return ((const float *)row)[i];
+    case 1: return h2f(((const uint16_t *)row)[i]);
+    case 2: return __uint_as_float((uint32_t)((const uint16_t *)row)[i] << 16);
+    case 3: {
+        const uint8_t *b = row + (size_t)(i >> 6) * 66;
+        return fmul(h2f((uint16_t)(b[0] | (b[1] << 8))), (float)(int8_t)b[2 + (i & 63)]);
+    }
+    default: {
+        const uint8_t *b = row + (size_t)(i >> 6) * 34;
+        const int w = i & 63, byte = b[2 + (w & 31)];
+        const int q = (w < 32 ? (byte & 15) : (byte >> 4)) - 8;
+        return fmul(h2f((uint16_t)(b[0] | (b[1] << 8))), (float)q);
+    }
+    }
+}
+
+/* ------------------------------------------------------------ residual + rmsnorm + quant */
+
+__global__ __launch_bounds__(256) void k_norm(NormArgs a) {
+    extern __shared__ float hs[];
+    __shared__ float r_sh;
+    const int t = blockIdx.x, D = a.D, tid = threadIdx.x;
+    float *h = a.h + (size_t)t * D;
+    for (int i = tid; i < D; i += 256) {
+        float v;
+        if (a.mode == 0) {
+            const uint8_t *row = a.emb + (size_t)a.tokens[t] * a.emb_rb;
+            v = fmul(a.es, deq_elem(row, a.emb_dtype, i));
+        } else if (a.mode == 1) {
+            v = fadd(h[i], fmul(a.rs, a.add[(size_t)t * D + i]));
+        } else {
+            float out = 0.0f;
+            for (int j = 0; j < a.K; j++) {
+                const float w = a.wts[(size_t)t * a.K + j];
+                out = fadd(out, fmul(w, a.Y[(size_t)a.pair_of[(size_t)t * a.K + j] * D + i]));
+            }
+            if (a.add) out = fadd(out, a.add[(size_t)t * D + i]);
+            v = fadd(h[i], fmul(a.rs, out));
+        }
+        h[i] = v;
+        hs[i] = v;
+    }
+    __syncthreads();
+    if (tid < 16) {
+        float L = 0.0f;
+        for (int i = tid; i < D; i += 16) L = fadd(L, fmul(hs[i], hs[i]));
+        L = tree16(L);
+        if (tid == 0) {
+            const float ms = fdiv(L, (float)D);
+            r_sh = fdiv(1.0f, __fsqrt_rn(fadd(ms, a.eps)));
+        }
+    }
+    __syncthreads();
+    const float r = r_sh;
+    const int wave = tid >> 6, lane = tid & 63;
+    for (int g = wave; g < a.a.nbp; g += 4) {
+        const int i = g * 64 + lane;
+        const float xv = i < D ? fmul(fmul(hs[i], r), a.norm_w[i]) : 0.0f;
+        if (a.x && i < D) a.x[(size_t)t * D + i] = xv;
+        quant_block_wave(xv, a.a, t, g);
+    }
+}
+
+/* mid = silu(g) * u (written back into g, as the reference does in place) then
+ * NUMERICS §2 (dense FFN / shared expert); one wave per (token, block). */
+__global__ void k_swiglu_quant(float *__restrict__ g, const float *__restrict__ u, int T, int F, Act a) {
+    const int wave = (int)((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6);
+    if (wave >= T * a.nbp) return;
+    const int t = wave / a.nbp, b = wave % a.nbp, lane = threadIdx.x & 63, i = b * 64 + lane;
+    float v = 0.0f;
+    if (i < F) {
+        const float gv = g[(size_t)t * F + i];
+        v = fmul(fdiv(gv, fadd(1.0f, exp_port_f(-gv))), u[(size_t)t * F + i]);
+        g[(size_t)t * F + i] = v;
+    }
+    quant_block_wave(v, a, t, b);
+}
+
+/* y = canon(s * y) on T rows of n values (logit_scale after a float lm_head) */
+__global__ void k_scale_rows(float *y, int ldy, int T, int n, float s) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)T * n) return;
+    float *p = y + (size_t)(i / n) * ldy + (i % n);
+    *p = canon(fmul(s, *p));
+}
+
+/* ------------------------------------------------------------ routing */
+
+/* a ranks before b: larger value first, NaN last, ties to the lower index */
+__device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib) {
+    const bool na = va != va, nb = vb != vb;
+    if (na || nb) return na == nb ? ia < ib : nb;
+    if (va != vb) return va > vb;
+    return ia < ib;
+}
+
+/* wave-wide best (value, index) over candidates; idx < 0 marks "none" */
+__device__ __forceinline__ void wave_best(float &v, int &idx) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        const bool take = oi >= 0 && (idx < 0 || ranks_before(ov, oi, v, idx));
+        v = take ? ov : v;
+        idx = take ? oi : idx;
+    }
+}
+
+constexpr int ROUTE_EMAX = 1024;
+
+/* One wave per token: scores, selection values, group limit, top-K, weights. */
+__global__ __launch_bounds__(64) void k_route_tokens(RouteArgs a) {
+    __shared__ float score[ROUTE_EMAX], sel[ROUTE_EMAX];
+    __shared__ unsigned char taken[ROUTE_EMAX], gkeep[64];
+    __shared__ float gsc[64];
+    const int t = blockIdx.x, lane = threadIdx.x, E = a.E, K = a.K;
+    const float *lg = a.logits + (size_t)t * E;
+    if (a.score_fn == 0) {
+        /* softmax (quant.c:634-642): m = running max from x[0] (a NaN x[0] makes m NaN) */
+        float m = -__builtin_huge_valf();
+        for (int e = lane; e < E; e += 64) {
+            const float x = lg[e];
+            score[e] = x;
+            if (x == x) m = fmaxf(m, x);
+        }
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        if (lg[0] != lg[0]) m = lg[0];
+        wave_sync();
+        for (int e = lane; e < E; e += 64) score[e] = exp_port_f(fadd(score[e], -m));
+        wave_sync();
+        float L = 0.0f;
+        if (lane < 16)
+            for (int e = lane; e < E; e += 16) L = fadd(L, score[e]);
+        L = tree16(L);
+        const float s = __shfl(L, 0, 64);
+        wave_sync();
+        for (int e = lane; e < E; e += 64) score[e] = fdiv(score[e], s);
+    } else {
+        for (int e = lane; e < E; e += 64) score[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
+    }
+    wave_sync();
+    for (int e = lane; e < E; e += 64) {
+        sel[e] = a.bias ? fadd(score[e], a.bias[e]) : score[e];
+        taken[e] = 0;
+    }
+    wave_sync();
+    if (a.n_group > 1) {
+        const int ng = a.n_group, gs = E / ng;
+        for (int g = 0; g < ng; g++) {
+            float v1 = 0.0f, v2 = 0.0f;
+            int i1 = -1, i2 = -1;
+            for (int i = lane; i < gs; i += 64)
+                if (i1 < 0 || ranks_before(sel[g * gs + i], i, v1, i1)) { v1 = sel[g * gs + i]; i1 = i; }
+            wave_best(v1, i1);
+            for (int i = lane; i < gs; i += 64)
+                if (i != i1 && (i2 < 0 || ranks_before(sel[g * gs + i], i, v2, i2))) { v2 = sel[g * gs + i]; i2 = i; }
+            wave_best(v2, i2);
+            if (lane == 0) { gsc[g] = i2 >= 0 ? fadd(v1, v2) : v1; gkeep[g] = 0; }
+        }
+        wave_sync();
+        for (int r = 0; r < a.topk_group; r++) {
+            float v = 0.0f;
+            int bi = -1;
+            for (int g = lane; g < ng; g += 64)
+                if (!gkeep[g] && (bi < 0 || ranks_before(gsc[g], g, v, bi))) { v = gsc[g]; bi = g; }
+            wave_best(v, bi);
+            if (lane == 0) gkeep[bi] = 1;
+            wave_sync();
+        }
+        for (int e = lane; e < E; e += 64)
+            if (!gkeep[e / gs]) sel[e] = 0.0f;
+        wave_sync();
+    }
+    int my_id = -1;
+    for (int j = 0; j < K; j++) {
+        float v = 0.0f;
+        int bi = -1;
+        for (int e = lane; e < E; e += 64)
+            if (!taken[e] && (bi < 0 || ranks_before(sel[e], e, v, bi))) { v = sel[e]; bi = e; }
+        wave_best(v, bi);
+        if (lane == 0) taken[bi] = 1;
+        if (lane == j) my_id = bi;
+        wave_sync();
+    }
+    /* weights: w_j = score[id_j]; norm_topk: w_j / (sum_j w_j + 1e-20f), sum in rank order */
+    float w = lane < K ? score[my_id] : 0.0f;
+    if (a.norm_topk) {
+        float s = 0.0f;
+        for (int j = 0; j < K; j++) {
+            const int idj = __shfl(my_id, j, 64);
+            s = fadd(s, score[idj]);
+        }
+        const float den = fadd(s, 1e-20f);
+        w = fdiv(w, den);
+    }
+    w = fmul(w, a.routed_scale);
+    if (lane < K) {
+        a.ids[(size_t)t * K + lane] = my_id;
+        a.wts[(size_t)t * K + lane] = w;
+        if (a.route_out) a.route_out[((size_t)t * a.n_moe + a.moe_ord) * K + lane] = my_id;
+    }
+}
+
+/* Union of the chosen experts in ascending id, pairs grouped by expert with tokens
+ * ascending (model.c:1020-1037); one workgroup. */
+__global__ __launch_bounds__(256) void k_route_bucket(RouteArgs a) {
+    __shared__ int cnt[ROUTE_EMAX], base[ROUTE_EMAX], slot[ROUTE_EMAX];
+    __shared__ int tot;
+    const int tid = threadIdx.x, E = a.E, P = a.T * a.K;
+    for (int e = tid; e < E; e += 256) cnt[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += 256) atomicAdd(&cnt[a.ids[p]], 1);
+    __syncthreads();
+    if (tid == 0) {
+        int pos = 0, nu = 0;
+        for (int e = 0; e < E; e++) {
+            base[e] = pos;
+            slot[e] = cnt[e] ? nu : -1;
+            if (cnt[e]) {
+                a.ulist[nu] = e;
+                a.u_p0[nu] = pos;
+                a.u_n[nu] = cnt[e];
+                nu++;
+            }
+            pos += cnt[e];
+        }
+        tot = nu;
+        *a.n_active = nu;
+        if (a.stats) {
+            a.stats[0] += (unsigned long long)P;
+            a.stats[1] += (unsigned long long)nu;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) {
+        if (!cnt[e]) continue;
+        int pos = base[e];
+        for (int p = 0; p < P; p++)
+            if (a.ids[p] == e) {
+                a.pair_tok[pos] = p / a.K;
+                a.pair_of[p] = pos;
+                pos++;
+            }
+    }
+}
+
+/* ------------------------------------------------------------ GQA post-processing */
+
+/* One wave per (token, head slot): slots [0, H) are query heads, [H, H + Hkv) key heads
+ * (which also append the value head). Bias, qk-norm (per head), RoPE from the host
+ * table, then the K/V cache at slot pos0 + t. */
+__global__ __launch_bounds__(256) void k_qkv_post(QkvArgs a, const float *__restrict__ rfull) {
+    __shared__ float buf[4][512];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nslot = a.H + a.Hkv, hd = a.hd;
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= a.T * nslot) return;
+    const int t = item / nslot, j = item % nslot;
+    const bool isq = j < a.H;
+    const int g = isq ? j : j - a.H;
+    const int qd = a.H * hd, kd = a.Hkv * hd;
+    const float *src = isq ? a.q + (size_t)t * qd + (size_t)g * hd : a.k + (size_t)t * kd + (size_t)g * hd;
+    const float *bias = isq ? (a.bq ? a.bq + (size_t)g * hd : nullptr) : (a.bk ? a.bk + (size_t)g * hd : nullptr);
+    float *x = buf[wave];
+    for (int e = lane; e < hd; e += 64) x[e] = bias ? fadd(src[e], bias[e]) : src[e];
+    wave_sync();
+    if (a.qk_norm == 1) {
+        float L = 0.0f;
+        if (lane < 16)
+            for (int e = lane; e < hd; e += 16) L = fadd(L, fmul(x[e], x[e]));
+        L = tree16(L);
+        L = __shfl(L, 0, 64);
+        const float r = fdiv(1.0f, __fsqrt_rn(fadd(fdiv(L, (float)hd), a.eps)));
+        const float *w = isq ? a.qn : a.kn;
+        wave_sync();
+        for (int e = lane; e < hd; e += 64) x[e] = fmul(fmul(x[e], r), w[e]);
+    } else if (a.qk_norm == 2) {
+        const float r = rfull[(size_t)t * 2 + (isq ? 0 : 1)];
+        const float *w = (isq ? a.qn : a.kn) + (size_t)g * hd;
+        for (int e = lane; e < hd; e += 64) x[e] = fmul(fmul(x[e], r), w[e]);
+    }
+    wave_sync();
+    const int half = a.rope_dim / 2;
+    const float *cs = a.rope + (size_t)t * a.rope_dim;
+    for (int p = lane; p < half; p += 64) {
+        const int ia = a.rope_style == 1 ? 2 * p : p, ib = a.rope_style == 1 ? 2 * p + 1 : p + half;
+        const float av = x[ia], bv = x[ib], c = cs[2 * p], s = cs[2 * p + 1];
+        x[ia] = fadd(fmul(av, c), -fmul(bv, s));
+        x[ib] = fadd(fmul(bv, c), fmul(av, s));
+    }
+    wave_sync();
+    const size_t slot = (size_t)(a.pos0 + t);
+    if (isq) {
+        for (int e = lane; e < hd; e += 64) a.qout[(size_t)t * qd + (size_t)g * hd + e] = x[e];
+    } else {
+        float *kc = a.kc + ((size_t)g * a.cap + slot) * hd, *vc = a.vc + ((size_t)g * a.cap + slot) * hd;
+        const float *vs = a.v + (size_t)t * kd + (size_t)g * hd;
+        for (int e = lane; e < hd; e += 64) {
+            kc[e] = x[e];
+            vc[e] = a.bv ? fadd(vs[e], a.bv[(size_t)g * hd + e]) : vs[e];
+        }
+    }
+}
+
+/* Full-width qk-norm (qk_norm = 2): r = 1/sqrt(dot16(x,x)/n + eps) of q (+bias) and
+ * k (+bias) per token; one wave per (token, q|k). */
+__global__ void k_fullnorm_r(QkvArgs a, float *rfull) {
+    const int wave = (int)((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6), lane = threadIdx.x & 63;
+    if (wave >= a.T * 2) return;
+    const int t = wave / 2, isk = wave % 2;
+    const int n = (isk ? a.Hkv : a.H) * a.hd;
+    const float *src = isk ? a.k + (size_t)t * n : a.q + (size_t)t * n;
+    const float *b = isk ? a.bk : a.bq;
+    float L = 0.0f;
+    if (lane < 16)
+        for (int e = lane; e < n; e += 16) {
+            const float v = b ? fadd(src[e], b[e]) : src[e];
+            L = fadd(L, fmul(v, v));
+        }
+    L = tree16(L);
+    if (lane == 0) rfull[(size_t)t * 2 + isk] = fdiv(1.0f, __fsqrt_rn(fadd(fdiv(L, (float)n), a.eps)));
+}
+
+/* ------------------------------------------------------------ KV compaction */
+
+/* Moves K/V of slot pos0 + path[j] to pos0 + j, j ascending (sources are >= their
+ * destinations and increase with j, so one thread per element in order is safe). */
+__global__ void k_kv_move(float *cache, size_t layer_stride, int L, int Hkv, int cap, int hd, int pos0,
+                          const int *__restrict__ path, int n) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t per_layer = (int64_t)2 * Hkv * hd;
+    if (idx >= per_layer * L) return;
+    const int l = (int)(idx / per_layer), r = (int)(idx % per_layer);
+    const int kvh = r / hd, e = r % hd;   /* kvh in [0, 2*Hkv): K heads then V heads */
+    float *base = cache + (size_t)l * layer_stride + (size_t)kvh * cap * hd + e;
+    for (int j = 0; j < n; j++) {
+        const int src = path[j];
+        if (src != j) base[(size_t)(pos0 + j) * hd] = base[(size_t)(pos0 + src) * hd];
+    }
+}
+
+/* ------------------------------------------------------------ greedy acceptance */
+
+__global__ __launch_bounds__(256) void k_argmax_rows(AcceptArgs a) {
+    __shared__ float bv[256];
+    __shared__ int bi[256], bad[256];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *x = a.rows + (size_t)row * a.V;
+    float v = 0.0f;
+    int idx = -1, badv = 0, fin = 0;
+    for (int i = tid; i < a.V; i += 256) {
+        const float xi = x[i];
+        if (xi != xi || xi == __builtin_huge_valf()) badv = 1;
+        if (xi != -__builtin_huge_valf()) fin = 1;
+        if (idx < 0 || xi > v) { v = xi; idx = i; }
+    }
+    bv[tid] = v; bi[tid] = idx; bad[tid] = badv | (fin << 1);
+    __syncthreads();
+    for (int s = 128; s >= 1; s >>= 1) {
+        if (tid < s) {
+            const float ov = bv[tid + s];
+            const int oi = bi[tid + s];
+            if (oi >= 0 && (bi[tid] < 0 || ov > bv[tid] || (ov == bv[tid] && oi < bi[tid]))) { bv[tid] = ov; bi[tid] = oi; }
+            bad[tid] |= bad[tid + s];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) a.amax[row] = ((bad[0] & 1) || !(bad[0] & 2)) ? -1 : bi[0];
+}
+
+__global__ void k_accept_walk(AcceptArgs a) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    int v = 0, np = 0, status = 0, fin = -1;
+    a.path[np++] = 0;
+    for (;;) {
+        const int t = a.amax[v];
+        if (t < 0) { status = -1; break; }
+        int next = -1;
+        for (int c = v + 1; c < a.n; c++)
+            if (a.parent[c] == v && a.tokens[c] == t) { next = c; break; }
+        if (next < 0) { fin = t; break; }
+        a.path[np++] = next;
+        v = next;
+    }
+    a.result[0] = np;
+    a.result[1] = fin;
+    a.result[2] = status;
+}
+
+} // namespace
+
+namespace hxl {
+
+void route(const RouteArgs &a, hipStream_t st) {
+    k_route_tokens<<<a.T, 64, 0, st>>>(a);
+    k_route_bucket<<<1, 256, 0, st>>>(a);
+}
+
+void norm(const NormArgs &a, hipStream_t st) {
+    k_norm<<<a.T, 256, (size_t)a.D * sizeof(float), st>>>(a);
+}
+
+void swiglu_quant(float *g, const float *u, int T, int F, const Act &a, hipStream_t st) {
+    const int64_t waves = (int64_t)T * a.nbp;
+    if (waves) k_swiglu_quant<<<(int)((waves + 3) / 4), 256, 0, st>>>(g, u, T, F, a);
+}
+
+void scale_rows(float *y, int ldy, int T, int n, float s, hipStream_t st) {
+    const int64_t m = (int64_t)T * n;
+    if (m) k_scale_rows<<<(int)((m + 255) / 256), 256, 0, st>>>(y, ldy, T, n, s);
+}
+
+void qkv_post(const QkvArgs &a, hipStream_t st) {
+    if (a.qk_norm == 2) k_fullnorm_r<<<(a.T * 2 + 3) / 4, 256, 0, st>>>(a, a.rfull);
+    const int items = a.T * (a.H + a.Hkv);
+    k_qkv_post<<<(items + 3) / 4, 256, 0, st>>>(a, a.rfull);
+}
+
+void kv_move(float *cache, size_t layer_stride, int L, int Hkv, int cap, int hd, int pos0, const int *path, int n,
+             hipStream_t st) {
+    const int64_t threads = (int64_t)L * 2 * Hkv * hd;
+    if (threads && n > 0) k_kv_move<<<(int)((threads + 255) / 256), 256, 0, st>>>(cache, layer_stride, L, Hkv, cap, hd, pos0, path, n);
+}
+
+void accept_greedy(const AcceptArgs &a, hipStream_t st) {
+    k_argmax_rows<<<a.n, 256, 0, st>>>(a);
+    k_accept_walk<<<1, 64, 0, st>>>(a);
+}
+
+} // namespace hxl

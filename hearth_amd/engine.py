@@ -1,0 +1,408 @@
+"""ctypes binding of the hearth.h engine (libhearth.so on an MI355X).
+
+Same surface as the reference's python/hearth/engine.py:234-461 (Engine with eval / pos
+/ rewind / reset / stats / info / kv_capacity / trace / route_replay, the struct mirrors
+of engine.py:29-86 and the error texts of engine.py:199-207), plus the verify
+extensions of include/hearth_gpu.h: verify_greedy (evaluate a chain or tree of drafts,
+accept on the GPU and commit in one call), verify_tree / commit_path, and GPU timing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from ctypes import (POINTER, Structure, byref, c_char, c_char_p, c_double, c_float, c_int, c_int32, c_size_t,
+                    c_uint64, c_void_p)
+
+import numpy as np
+
+from . import _native
+
+__all__ = ["Engine", "HearthError", "HearthOptions", "HearthModelInfo", "HearthStats", "KStats", "POLICIES",
+           "PREFETCH", "ISAS"]
+
+MAX_MIRRORS = 8
+
+
+class HearthError(RuntimeError):
+    """An engine call failed."""
+
+
+class HearthOptions(Structure):
+    _fields_ = [
+        ("model_path", c_char_p),
+        ("mirror_paths", c_char_p * MAX_MIRRORS),
+        ("n_mirrors", c_int),
+        ("cache_gb", c_double),
+        ("n_threads", c_int),
+        ("n_io_threads", c_int),
+        ("direct_io", c_int),
+        ("policy", c_int),
+        ("prefetch", c_int),
+        ("prefetch_extra", c_int),
+        ("usage_in", c_char_p),
+        ("usage_out", c_char_p),
+        ("pin_fraction", c_float),
+        ("warm_start", c_int),
+        ("max_seq", c_int),
+        ("max_batch", c_int),
+        ("isa", c_int),
+        ("verbose", c_int),
+    ]
+
+
+class HearthModelInfo(Structure):
+    _fields_ = [
+        ("arch", c_char * 32),
+        ("n_layers", c_int), ("d_model", c_int), ("vocab_size", c_int), ("max_seq", c_int),
+        ("n_heads", c_int), ("n_kv_heads", c_int), ("head_dim", c_int), ("attn_kind", c_int),
+        ("n_experts", c_int), ("top_k", c_int), ("expert_ffn_dim", c_int), ("n_moe_layers", c_int),
+        ("bos_id", c_int),
+        ("n_eos", c_int), ("eos_ids", c_int * 8),
+        ("dense_bytes", c_uint64),
+        ("expert_bytes", c_uint64),
+        ("slab_bytes_max", c_uint64),
+        ("params_total", c_double),
+        ("params_active", c_double),
+        ("cache_slots", c_int),
+        ("isa", c_int),
+        ("n_threads", c_int), ("n_io_threads", c_int),
+    ]
+
+
+class HearthStats(Structure):
+    _fields_ = [
+        ("tokens", c_uint64),
+        ("forward_calls", c_uint64),
+        ("wall_s", c_double),
+        ("attn_s", c_double), ("moe_s", c_double), ("dense_s", c_double), ("stall_s", c_double),
+        ("expert_uses", c_uint64),
+        ("expert_loads_unique", c_uint64),
+        ("cache_hits", c_uint64), ("cache_misses", c_uint64),
+        ("prefetch_issued", c_uint64), ("prefetch_used", c_uint64), ("prefetch_wasted", c_uint64),
+        ("bytes_read", c_uint64),
+        ("read_s", c_double),
+        ("evictions", c_uint64),
+        ("cache_slots", c_int), ("cache_resident", c_int), ("cache_pinned", c_int),
+        ("read_errors", c_uint64),
+    ]
+
+
+class KStats(Structure):
+    """hearth_gpu_kstats (include/hearth_gpu.h)."""
+    _fields_ = [
+        ("attn_s", c_double), ("router_s", c_double), ("expert_s", c_double), ("norm_s", c_double),
+        ("head_s", c_double), ("dense_s", c_double),
+        ("expert_launches", c_uint64), ("expert_bytes", c_uint64), ("dense_bytes", c_uint64), ("kv_bytes", c_uint64),
+    ]
+
+
+POLICIES = {"lru": 0, "lfu": 1}
+PREFETCH = {"off": 0, "none": 0, "next": 1, "shared": 2}
+ISAS = {"auto": 0, "scalar": 1, "avx2": 2, "avx512": 3}
+
+_I32P = POINTER(c_int32)
+_PROTOS = {
+    "hearth_version": (c_char_p, []),
+    "hearth_default_options": (None, [POINTER(HearthOptions)]),
+    "hearth_open": (c_void_p, [POINTER(HearthOptions), c_char_p, c_size_t]),
+    "hearth_close": (None, [c_void_p]),
+    "hearth_info": (c_int, [c_void_p, POINTER(HearthModelInfo)]),
+    "hearth_eval": (c_int, [c_void_p, _I32P, c_int, POINTER(c_float), c_int]),
+    "hearth_pos": (c_int, [c_void_p]),
+    "hearth_reset": (c_int, [c_void_p]),
+    "hearth_rewind": (c_int, [c_void_p, c_int]),
+    "hearth_get_stats": (c_int, [c_void_p, POINTER(HearthStats)]),
+    "hearth_reset_stats": (None, [c_void_p]),
+    "hearth_trace_start": (c_int, [c_void_p, c_char_p]),
+    "hearth_trace_stop": (c_int, [c_void_p]),
+    "hearth_route_replay": (c_int, [c_void_p, c_char_p]),
+    "hearth_cpu_isa": (c_int, []),
+    "hearth_verify_tree": (c_int, [c_void_p, _I32P, _I32P, c_int, POINTER(c_float)]),
+    "hearth_commit_path": (c_int, [c_void_p, _I32P, c_int]),
+    "hearth_verify_greedy": (c_int, [c_void_p, _I32P, _I32P, c_int, _I32P, POINTER(c_int), _I32P, POINTER(c_float)]),
+    "hearth_gpu_set_profiling": (c_int, [c_void_p, c_int]),
+    "hearth_gpu_get_kstats": (c_int, [c_void_p, POINTER(KStats)]),
+    "hearth_gpu_reset_kstats": (None, [c_void_p]),
+}
+
+_ERRORS = {
+    -1: "bad argument",
+    -2: "token id outside the vocabulary",
+    -3: "KV capacity exceeded",
+    -4: "device or I/O error",
+    -5: "out of memory",
+    -6: "routing trace does not fit this model",
+}
+
+
+class _Api:
+    def __init__(self, L: ctypes.CDLL):
+        for name, (res, args) in _PROTOS.items():
+            fn = getattr(L, name, None)
+            if fn is not None:
+                fn.restype, fn.argtypes = res, args
+            setattr(self, name[len("hearth_"):], fn)
+
+    def need(self, name):
+        fn = getattr(self, name)
+        if fn is None:
+            raise HearthError(f"libhearth.so does not export hearth_{name}")
+        return fn
+
+
+_api_obj: _Api | None = None
+_other_apis: dict = {}
+
+
+def _api(lib_path=None) -> _Api:
+    """The API of libhearth.so, or of another library implementing hearth.h at lib_path."""
+    global _api_obj
+    if lib_path is not None:
+        key = os.fspath(lib_path)
+        if key not in _other_apis:
+            _other_apis[key] = _Api(ctypes.CDLL(key))
+        return _other_apis[key]
+    if _api_obj is None:
+        _api_obj = _Api(_native.lib())
+    return _api_obj
+
+
+def _enum(v, table, what):
+    if isinstance(v, (int, np.integer)) and not isinstance(v, bool):
+        if int(v) not in set(table.values()):
+            raise ValueError(f"{what}: invalid value {v}")
+        return int(v)
+    if isinstance(v, str) and v.strip().lower() in table:
+        return table[v.strip().lower()]
+    raise ValueError(f"{what}: unknown {v!r}")
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a).reshape(-1), dtype=np.int32)
+
+
+class Engine:
+    """One open model on the GPU. Calls are serialised by a lock (reference engine.py:235)."""
+
+    def __init__(self, model_path, *, cache_gb=8.0, threads=0, io_threads=0, direct_io=True, policy="lfu",
+                 prefetch="shared", prefetch_extra=0, usage_in=None, usage_out=None, pin_fraction=0.0,
+                 warm_start=False, max_seq=0, max_batch=0, isa="auto", mirrors=(), verbose=0, lib=None):
+        """lib: path of another library implementing hearth.h (default: libhearth.so)."""
+        self._h = None
+        self._lock = threading.Lock()
+        if model_path is None:
+            raise TypeError("model_path is required")
+        api = self._api = _api(lib)
+        opt = HearthOptions()
+        api.need("default_options")(byref(opt))
+        keep = [os.fspath(model_path).encode("utf-8")]
+        opt.model_path = keep[0]
+        mirrors = [mirrors] if isinstance(mirrors, (str, bytes, os.PathLike)) else list(mirrors or ())
+        if len(mirrors) > MAX_MIRRORS:
+            raise ValueError(f"at most {MAX_MIRRORS} mirrors")
+        for i, m in enumerate(mirrors):
+            keep.append(os.fspath(m).encode("utf-8"))
+            opt.mirror_paths[i] = keep[-1]
+        opt.n_mirrors = len(mirrors)
+        opt.cache_gb = float(cache_gb)
+        opt.n_threads = int(threads)
+        opt.n_io_threads = int(io_threads)
+        opt.direct_io = 1 if direct_io else 0
+        opt.policy = _enum(policy, POLICIES, "policy")
+        opt.prefetch = _enum(prefetch, PREFETCH, "prefetch")
+        opt.prefetch_extra = int(prefetch_extra)
+        if usage_in is not None:
+            keep.append(os.fspath(usage_in).encode())
+            opt.usage_in = keep[-1]
+        if usage_out is not None:
+            keep.append(os.fspath(usage_out).encode())
+            opt.usage_out = keep[-1]
+        opt.pin_fraction = float(pin_fraction)
+        opt.warm_start = 1 if warm_start else 0
+        opt.max_seq = int(max_seq)
+        opt.max_batch = int(max_batch)
+        opt.isa = _enum(isa, ISAS, "isa")
+        opt.verbose = int(verbose)
+        self.model_path = os.fspath(model_path)
+        self.options = dict(max_seq=int(max_seq), max_batch=int(max_batch))
+        err = ctypes.create_string_buffer(1024)
+        h = api.need("open")(byref(opt), err, len(err))
+        if not h:
+            raise HearthError(err.value.decode("utf-8", "replace").strip() or f"hearth_open failed for {model_path!r}")
+        self._h = c_void_p(h)
+        mi = HearthModelInfo()
+        if api.need("info")(self._h, byref(mi)) < 0:
+            self.close()
+            raise HearthError("hearth_info failed")
+        self.info = {n: (bytes(getattr(mi, n)).split(b"\0", 1)[0].decode() if n == "arch" else
+                         list(getattr(mi, n)) if n == "eos_ids" else getattr(mi, n)) for n, _ in HearthModelInfo._fields_}
+        self.info["eos_ids"] = self.info["eos_ids"][:max(0, min(8, int(self.info["n_eos"])))]
+        self._vocab = int(self.info["vocab_size"])
+
+    # ---- lifecycle ----
+    def close(self) -> None:
+        with self._lock:
+            h, self._h = self._h, None
+            if h is not None:
+                self._api.need("close")(h)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+        return False
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _handle(self):
+        if self._h is None:
+            raise HearthError("engine is closed")
+        return self._h
+
+    @property
+    def vocab_size(self) -> int:
+        return self._vocab
+
+    @property
+    def kv_capacity(self) -> int:
+        model_max = int(self.info["max_seq"]) or 4096
+        req = self.options["max_seq"]
+        return min(req, model_max) if req > 0 else min(model_max, 4096)
+
+    # ---- evaluation (reference engine.py:364-420) ----
+    def eval(self, tokens, all_logits: bool = False) -> np.ndarray:
+        if isinstance(tokens, (int, np.integer)):
+            tokens = [int(tokens)]
+        arr = np.asarray(tokens).reshape(-1)
+        if arr.size and not np.issubdtype(arr.dtype, np.integer):
+            raise TypeError(f"token ids must be integers, got dtype {arr.dtype}")
+        n, V = int(arr.size), self._vocab
+        if n == 0:
+            if all_logits:
+                return np.empty((0, V), dtype=np.float32)
+            raise ValueError("eval needs at least one token")
+        if int(arr.min()) < 0 or int(arr.max()) >= V:
+            raise ValueError(f"token id out of range [0, {V})")
+        ids = _i32(arr)
+        out = np.empty((n if all_logits else 1) * V, dtype=np.float32)
+        with self._lock:
+            h = self._handle()
+            rc = self._api.eval(h, ids.ctypes.data_as(_I32P), n, out.ctypes.data_as(POINTER(c_float)),
+                                1 if all_logits else 0)
+            if rc < 0:
+                raise HearthError(f"hearth_eval failed (code {rc}) evaluating {n} tokens at position "
+                                  f"{int(self._api.pos(h))}: {_ERRORS.get(rc, 'unknown error')}")
+        return out.reshape(n, V) if all_logits else out
+
+    @property
+    def pos(self) -> int:
+        with self._lock:
+            return int(self._api.pos(self._handle()))
+
+    def reset(self) -> None:
+        with self._lock:
+            if self._api.reset(self._handle()) < 0:
+                raise HearthError("hearth_reset failed")
+
+    def rewind(self, pos: int) -> None:
+        pos = int(pos)
+        with self._lock:
+            h = self._handle()
+            cur = int(self._api.pos(h))
+            if pos < 0 or pos > cur:
+                raise ValueError(f"rewind position {pos} outside [0, {cur}]")
+            rc = self._api.rewind(h, pos)
+        if rc < 0:
+            raise HearthError(f"hearth_rewind({pos}) failed (code {rc})")
+
+    # ---- speculative verification on the device (include/hearth_gpu.h) ----
+    def verify_greedy(self, tokens, parent=None, want_logits: bool = False):
+        """Evaluates [last] + draft (chain, or tree given parent), accepts greedily on the
+        GPU and commits the accepted path. Returns (path, final_token, logits or None)."""
+        ids = _i32(tokens)
+        n = int(ids.size)
+        par = None if parent is None else _i32(parent)
+        path = np.empty(max(n, 1), dtype=np.int32)
+        npath, fin = c_int(0), np.zeros(1, dtype=np.int32)
+        lg = np.empty((n, self._vocab), dtype=np.float32) if want_logits else None
+        with self._lock:
+            rc = self._api.need("verify_greedy")(
+                self._handle(), ids.ctypes.data_as(_I32P), None if par is None else par.ctypes.data_as(_I32P), n,
+                path.ctypes.data_as(_I32P), byref(npath), fin.ctypes.data_as(_I32P),
+                None if lg is None else lg.ctypes.data_as(POINTER(c_float)))
+        if rc < 0:
+            raise HearthError(f"hearth_verify_greedy failed (code {rc}): {_ERRORS.get(rc, 'unknown error')}")
+        return path[:npath.value].tolist(), int(fin[0]), lg
+
+    def verify_tree(self, tokens, parent, want_logits: bool = True):
+        ids, par = _i32(tokens), _i32(parent)
+        n = int(ids.size)
+        lg = np.empty((n, self._vocab), dtype=np.float32) if want_logits else None
+        with self._lock:
+            rc = self._api.need("verify_tree")(self._handle(), ids.ctypes.data_as(_I32P), par.ctypes.data_as(_I32P), n,
+                                               None if lg is None else lg.ctypes.data_as(POINTER(c_float)))
+        if rc < 0:
+            raise HearthError(f"hearth_verify_tree failed (code {rc}): {_ERRORS.get(rc, 'unknown error')}")
+        return lg
+
+    def commit_path(self, path) -> None:
+        p = _i32(path)
+        with self._lock:
+            rc = self._api.need("commit_path")(self._handle(), p.ctypes.data_as(_I32P), int(p.size))
+        if rc < 0:
+            raise HearthError(f"hearth_commit_path failed (code {rc})")
+
+    # ---- telemetry ----
+    def stats(self) -> dict:
+        s = HearthStats()
+        with self._lock:
+            if self._api.get_stats(self._handle(), byref(s)) < 0:
+                raise HearthError("hearth_get_stats failed")
+        d = {name: getattr(s, name) for name, _ in HearthStats._fields_}
+        wall = d["wall_s"]
+        d.update(tok_per_s=d["tokens"] / wall if wall > 0 else 0.0,
+                 hit_rate=d["cache_hits"] / (d["cache_hits"] + d["cache_misses"]) if d["cache_hits"] + d["cache_misses"] else 0.0)
+        return d
+
+    def reset_stats(self) -> None:
+        with self._lock:
+            self._api.reset_stats(self._handle())
+
+    def set_profiling(self, on: bool) -> None:
+        with self._lock:
+            self._api.need("gpu_set_profiling")(self._handle(), 1 if on else 0)
+
+    def kstats(self) -> dict:
+        k = KStats()
+        with self._lock:
+            self._api.need("gpu_get_kstats")(self._handle(), byref(k))
+        return {name: getattr(k, name) for name, _ in KStats._fields_}
+
+    def reset_kstats(self) -> None:
+        with self._lock:
+            self._api.need("gpu_reset_kstats")(self._handle())
+
+    def trace_start(self, path) -> None:
+        with self._lock:
+            rc = self._api.need("trace_start")(self._handle(), os.fspath(path).encode())
+        if rc < 0:
+            raise HearthError(f"hearth_trace_start failed (code {rc})")
+
+    def trace_stop(self) -> None:
+        with self._lock:
+            self._api.need("trace_stop")(self._handle())
+
+    def route_replay(self, path) -> None:
+        with self._lock:
+            rc = self._api.need("route_replay")(self._handle(), os.fspath(path).encode() if path else b"")
+        if rc < 0:
+            raise HearthError(f"hearth_route_replay failed (code {rc}): {_ERRORS.get(rc, 'unknown error')}")
+
+    def __repr__(self) -> str:
+        return f"Engine({self.model_path!r}, {'closed' if self._h is None else f'pos={self.pos}'})"

@@ -1,0 +1,134 @@
+/*
+ * hx_oracle.h — CPU restatement of the reference engine's numerics, used as the
+ * checker for the MI355X build.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load liboracle.so, and only as the checker or the timed
+ * CPU baseline; the product library never links, loads or calls it.
+ *
+ * What each function restates (reference paths relative to the reference tree):
+ *   ho_f16_to_f32 / ho_f32_to_f16   engine/src/platform_common.inc:19-65 (IEEE binary16, RNE)
+ *   ho_quantize (Q8, Q4)            engine/src/quant.c:99-228, docs/NUMERICS.md §6
+ *   ho_act_quant                    engine/src/quant.c:325-348, docs/NUMERICS.md §2
+ *   ho_matmul                       engine/src/quant.c:352-427, docs/NUMERICS.md §3
+ *   ho_dot16 / ho_sum16 / rmsnorm / softmax / silu / sigmoid
+ *                                   engine/src/quant.c:604-667, docs/NUMERICS.md §1, §4
+ *   ho_open / ho_eval               engine/src/model.c:1171-1234 (forward), written as the
+ *                                   single-token loop of engine/tests/test_model.c:788-1197
+ *   ho_eval_tree / ho_commit_path   new (tree verification): node i runs at position
+ *                                   pos0 + depth(i) and attends to the context followed by
+ *                                   its ancestors in path order, i.e. exactly the chain
+ *                                   root -> i; no reference counterpart
+ *   ho_probs / ho_accept_*          python/hearth/generate.py:84-147,365-392
+ *
+ * Exponential mode (ho_set_exp_mode):
+ *   HO_EXP_LIBM      expf from the platform libm, as the reference calls it
+ *                    (docs/NUMERICS.md "expf ... come from the platform libm");
+ *                    with this mode the restatement is bit-exact to the reference
+ *                    engine (checked against the reference built from source).
+ *   HO_EXP_PORTABLE  ho_exp_port_f: Cody-Waite reduction + degree-13 Taylor in IEEE
+ *                    double using only +, -, * and exact conversions (no FMA, no libm),
+ *                    so it yields the same bits on any IEEE machine, CPU or GPU. The
+ *                    HIP kernels use the same definition; with this mode the GPU must
+ *                    match the restatement bit for bit.
+ * Parity status: every function above is pinned (pinned FNV hashes of the reference's
+ * test_quant.c, bit-exact comparison with the reference engine built from source on
+ * whole forward passes, closed forms for acceptance); see tests/ for each check.
+ */
+#ifndef HX_ORACLE_H
+#define HX_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { HO_F32 = 0, HO_F16 = 1, HO_BF16 = 2, HO_Q8 = 3, HO_Q4 = 4, HO_I32 = 5, HO_U8 = 6 };
+enum { HO_EXP_LIBM = 0, HO_EXP_PORTABLE = 1 };
+
+/* ---- formats and kernels -------------------------------------------------- */
+float    ho_f16_to_f32(uint16_t h);
+uint16_t ho_f32_to_f16(float f);
+uint16_t ho_f32_to_bf16(float f);
+size_t   ho_row_bytes(int dtype, int64_t n);
+int      ho_quantize(int dtype, const float *src, int64_t rows, int64_t cols, void *dst);
+int      ho_dequantize(int dtype, const void *src, int64_t rows, int64_t cols, float *dst);
+/* n % 64 == 0; out: n/64 blocks of { float d; int32 sum; int8 q[64] } (72 bytes) */
+void     ho_act_quant(const float *x, int64_t n, void *out);
+/* Y[t][r] = row r . X[t] per NUMERICS §3 (activation quantization inside). */
+int      ho_matmul(int dtype, const void *W, int64_t rows, int64_t cols, const float *X, int T, float *Y);
+
+/* ---- canonical helpers ---------------------------------------------------- */
+void  ho_set_exp_mode(int mode);
+int   ho_get_exp_mode(void);
+float ho_expf(float x);                 /* in the current mode */
+float ho_exp_port_f(float x);
+double ho_exp_port_d(double x);
+float ho_dot16(const float *a, const float *b, int64_t n);
+float ho_sum16(const float *a, int64_t n);
+
+/* ---- model ---------------------------------------------------------------- */
+typedef struct ho_model ho_model;
+/* cap: KV capacity (0 = min(model max_seq, 4096)). Returns NULL with a message. */
+ho_model *ho_open(const char *path, int cap, char *err, size_t errlen);
+void      ho_close(ho_model *m);
+/* out[0..]: n_layers, d_model, vocab, n_heads, n_kv_heads, head_dim, n_experts, top_k,
+ * expert_ffn, n_moe_layers, cap, attn_kind */
+void      ho_info(const ho_model *m, int *out);
+int       ho_pos(const ho_model *m);
+int       ho_rewind(ho_model *m, int pos);
+/* Chain evaluation at positions pos..pos+n-1 (pos += n). logits [n][V] or NULL;
+ * routes [n][n_moe][K] or NULL. Returns 0, or < 0 like hearth_eval. */
+int       ho_eval(ho_model *m, const int32_t *tokens, int n, float *logits, int32_t *routes);
+/* Tree evaluation: parent[0] = -1, parent[i] < i. Node i runs at pos + depth(i) and its
+ * K/V go to slot pos + i. pos is left unchanged (ho_commit_path advances it). */
+int       ho_eval_tree(ho_model *m, const int32_t *tokens, const int32_t *parent, int n,
+                       float *logits, int32_t *routes);
+/* Moves the K/V of nodes path[0..n) (path[j] at depth j) to slots pos..pos+n-1 and
+ * sets pos += n. */
+int       ho_commit_path(ho_model *m, const int32_t *path, int n);
+/* Sets the number of worker threads for the big matrix-vector products (>= 1). */
+void      ho_set_threads(ho_model *m, int n);
+
+/* ---- acceptance ----------------------------------------------------------- */
+/* Sampler.probs (generate.py:84-111) on one row of f32 logits: float64 result.
+ * temperature 0 = one-hot argmax. Returns 0, or -1 for NaN/+inf/all -inf logits. */
+int ho_probs(const float *logits, int V, double temperature, int top_k, double top_p, double min_p,
+             double *p_out);
+/* Greedy argmax, first index on ties; -1 on NaN/+inf/all -inf. */
+int ho_argmax(const float *logits, int V);
+/* Inverse-CDF draw (generate.py:113-121) with a given uniform u in [0,1). */
+int ho_draw(const double *p, int V, double u);
+/* Point-mass acceptance (generate.py:129-147): returns accepted(0/1), *tok. u0 decides,
+ * u1 draws the residual. */
+int ho_accept_point_mass(const double *p, int V, int d, double u0, double u1, int *tok);
+/* Speculative sampling with a general draft distribution q: accept d with probability
+ * min(1, p[d]/q[d]) (u0 < p[d]/q[d]); on rejection draw from max(0, p - q) normalised
+ * (u1). Reduces to ho_accept_point_mass when q is one-hot on d. */
+int ho_accept_general(const double *p, const double *q, int V, int d, double u0, double u1, int *tok);
+/* Chain verification (generate.py:365-392): rows [k+1][V], drafts[k]. mode 0 greedy,
+ * 1 point-mass sampling, 2 general q (q [k][V] float64). Uniforms: u[2i] decides draft
+ * i, u[2i+1] draws its correction, u[2k] draws the bonus token. Writes n_acc and the
+ * final token; returns 0 or -1 (bad logits). */
+int ho_accept_chain(const float *rows, int k, int V, const int32_t *drafts, int mode,
+                    double temperature, int top_k, double top_p, double min_p,
+                    const double *q, const double *u, int *n_acc, int *final_tok);
+/* Tree verification: nodes 0..n-1 (parent[0] = -1, parent[i] < i), rows [n][V] are the
+ * target logits at each node, tokens[i] the draft token of node i (node 0 = the last
+ * committed token). Children of a node are tried in index order (recursive rejection
+ * sampling, SpecInfer-style): accept child c with prob min(1, p[c.tok]/q_c[c.tok]); on
+ * rejection p := norm(max(0, p - q_c)) and the next child is tried; if none is accepted
+ * the correction is drawn from the current p. Greedy (mode 0): the child whose token is
+ * argmax(p) is taken. q: [n][V] float64 draft distribution per node (row of the node
+ * being tried; unused for greedy / point-mass). u: 2 per node + 1. path_out gets the
+ * accepted node ids from the root (path_out[0] = 0), *n_path their count, *final_tok. */
+int ho_accept_tree(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
+                   int mode, double temperature, int top_k, double top_p, double min_p,
+                   const double *q, const double *u, int32_t *path_out, int *n_path, int *final_tok);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HX_ORACLE_H */
