@@ -142,6 +142,8 @@ struct hearth_engine {
     int *h_geom = nullptr;   /* tokens | depth | anc */
     float *h_rope = nullptr;
     int *h_res = nullptr;
+    hipEvent_t geom_ev = nullptr;   /* recorded after the last upload from h_geom / h_rope */
+    bool geom_pending = false;
 
     int pos = 0;
     /* telemetry */
@@ -161,6 +163,18 @@ struct hearth_engine {
     int64_t replay_rows = 0;
     /* tree verification: slots of the last uncommitted tree */
     int tree_n = 0;
+    /* HEARTH_DEBUG_DUMP=<dir>: every forward writes named intermediate buffers there
+     * (T rows each, appended per call) for layer-by-layer comparisons */
+    std::string dump_dir;
+    void dump(const char *name, int layer, const void *dptr, int T, int width, size_t elem = 4) {
+        if (dump_dir.empty()) return;
+        std::vector<uint8_t> buf((size_t)T * width * elem);
+        ck(hipMemcpyAsync(buf.data(), dptr, buf.size(), hipMemcpyDeviceToHost, st));
+        ck(hipStreamSynchronize(st));
+        char path[1024];
+        std::snprintf(path, sizeof path, "%s/l%d_%s.bin", dump_dir.c_str(), layer, name);
+        if (FILE *f = fopen(path, "ab")) { fwrite(buf.data(), 1, buf.size(), f); fclose(f); }
+    }
 
     void *dalloc(size_t n) {
         void *p = nullptr;
@@ -184,6 +198,7 @@ struct hearth_engine {
         if (dev >= 0) (void)hipSetDevice(dev);
         if (st) (void)hipStreamSynchronize(st);
         for (auto &e : ev_pool) (void)hipEventDestroy(e);
+        if (geom_ev) (void)hipEventDestroy(geom_ev);
         for (void *p : allocs) (void)hipFree(p);
         if (h_geom) (void)hipHostFree(h_geom);
         if (h_rope) (void)hipHostFree(h_rope);
@@ -404,6 +419,7 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
     rope_dim = c.rope_dim;
     if (hd > 512 || hd % 16) { fail(err, errlen, "%s: head_dim %d unsupported (needs a multiple of 16 <= 512)", opt.model_path, hd); return false; }
     if (E > 1024) { fail(err, errlen, "%s: %d experts exceed this build's limit of 1024", opt.model_path, E); return false; }
+    if (c.n_group > 64) { fail(err, errlen, "%s: n_group %d exceeds this build's limit of 64", opt.model_path, c.n_group); return false; }
     if (c.n_moe && F % 64) { fail(err, errlen, "%s: expert_ffn_dim %d is not a multiple of 64", opt.model_path, F); return false; }
     for (int l = 0; l < L && c.n_moe; l++)
         for (int e = 0; e < E && c.layer_kind[l]; e++)
@@ -476,6 +492,7 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
         ck(hipHostMalloc((void **)&h_geom, sizeof(int) * (2 * Bs + Bs * Bs), hipHostMallocDefault));
         ck(hipHostMalloc((void **)&h_rope, sizeof(float) * Bs * std::max(rope_dim, 2), hipHostMallocDefault));
         ck(hipHostMalloc((void **)&h_res, sizeof(int) * (2 * Bs + 8), hipHostMallocDefault));
+        ck(hipEventCreateWithFlags(&geom_ev, hipEventDisableTiming));
         ck(hipDeviceSynchronize());
     } catch (const DeviceError &e) {
         fail(err, errlen, "%s: HIP error during open: %s", opt.model_path, hipGetErrorString(e.e));
@@ -539,11 +556,13 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             qa.rope = rope; qa.rfull = rfull; qa.T = T; qa.H = H; qa.Hkv = Hkv; qa.hd = hd; qa.cap = cap;
             qa.qk_norm = c.qk_norm; qa.rope_dim = rope_dim; qa.rope_style = c.rope_style; qa.eps = c.eps; qa.pos0 = pos;
             hxl::qkv_post(qa, st);
+            dump("q", l, qr, T, q_dim);
             hxd::AttnArgs at{};
             at.q = qr; at.kc = qa.kc; at.vc = qa.vc; at.S = S; at.ldS = ldS; at.out = att; at.T = T; at.H = H;
             at.Hkv = Hkv; at.hd = hd; at.cap = cap; at.scale = c.attn_scale;
             at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos0 = pos;
             hxl::attention(at, st);
+            dump("att", l, att, T, q_dim);
             if (w.o.quant) hxl::quant_rows(att, q_dim, T, q_dim / 64, aatt, st);
             matmul(w.o, aatt, att, q_dim, T, ao, D, false, 1.0f);
         });
@@ -553,6 +572,8 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             n.T = T; n.D = D;
             hxl::norm(n, st);
         });
+        dump("h_mid", l, h, T, D);
+        dump("x_ffn", l, x, T, D);
         const float *next_norm = l + 1 < L ? layers[l + 1].attn_norm : out_norm;
         if (w.moe) {
             int *n_active = route_meta, *ulist = route_meta + 1, *u_p0 = ulist + E, *u_n = u_p0 + E;
@@ -566,6 +587,8 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 r.route_out = route_out; r.moe_ord = moe_ord[l]; r.n_moe = c.n_moe; r.stats = dstats;
                 hxl::route(r, st);
             });
+            dump("router", l, lge, T, E);
+            dump("ids", l, ids, T, K);
             timed(&ks.expert_s, [&] {
                 hxd::MoeArgs m{};
                 m.table = w.experts; m.n_active = n_active; m.ulist = ulist; m.u_p0 = u_p0; m.u_n = u_n;
@@ -581,6 +604,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 n.norm_w = next_norm; n.eps = c.eps; n.x = x; n.a = ax; n.T = T; n.D = D;
                 hxl::norm(n, st);
             });
+            dump("h", l, h, T, D);
         } else {
             timed(&ks.dense_s, [&] {
                 matmul(w.gate, ax, x, D, T, f1, Fd, false, 1.0f);
@@ -603,6 +627,8 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
 /* Uploads tokens and geometry for n tokens at pos (parent NULL: chain) and runs the
  * forward; returns 0 or a negative code (nothing changed on failure). */
 int hearth_engine::run_geometry(const int32_t *tok, const int32_t *parent, int n, float *logits_out, bool) {
+    /* the staging buffers may still feed the previous call's uploads */
+    if (geom_pending) ck(hipEventSynchronize(geom_ev));
     int *ht = h_geom, *hdp = h_geom + B, *hanc = h_geom + 2 * B;
     for (int i = 0; i < n; i++) {
         ht[i] = tok[i];
@@ -621,6 +647,8 @@ int hearth_engine::run_geometry(const int32_t *tok, const int32_t *parent, int n
     ck(hipMemcpyAsync(depth, hdp, sizeof(int) * n, hipMemcpyHostToDevice, st));
     ck(hipMemcpyAsync(anc, hanc, sizeof(int) * (size_t)n * B, hipMemcpyHostToDevice, st));
     if (rope_dim) ck(hipMemcpyAsync(rope, h_rope, sizeof(float) * (size_t)n * rope_dim, hipMemcpyHostToDevice, st));
+    ck(hipEventRecord(geom_ev, st));
+    geom_pending = true;
     forward(n, logits_out != nullptr, 0);
     if (logits_out) ck(hipMemcpyAsync(logits_out, logits, sizeof(float) * (size_t)n * V, hipMemcpyDeviceToHost, st));
     return OK;
@@ -630,7 +658,8 @@ void hearth_engine::write_trace(int T) {
     if (!trace || !c.n_moe) return;
     const size_t n = (size_t)T * c.n_moe * K;
     h_routes.resize(n);
-    ck(hipMemcpy(h_routes.data(), route_out, sizeof(int) * n, hipMemcpyDeviceToHost));
+    ck(hipMemcpyAsync(h_routes.data(), route_out, sizeof(int) * n, hipMemcpyDeviceToHost, st));
+    ck(hipStreamSynchronize(st));
     std::vector<uint8_t> buf(2 * n);
     for (size_t i = 0; i < n; i++) {
         buf[2 * i] = (uint8_t)(h_routes[i] & 0xff);
@@ -776,6 +805,7 @@ HEARTH_API hearth_engine *hearth_open(const hearth_options *in, char *err, size_
     if (!e) { fail(err, errlen, "out of memory"); return nullptr; }
     e->opt = o;
     e->verbose = o.verbose;
+    if (const char *dd = getenv("HEARTH_DEBUG_DUMP")) e->dump_dir = dd;
     if (!e->open_model(err, errlen)) return nullptr;
     log_msg(LOG_INFO, "%s: %s, %d layers (%d MoE), d_model %d, vocab %d, KV %d positions, device %d", o.model_path,
             e->c.arch.c_str(), e->L, e->c.n_moe, e->D, e->V, e->cap, e->dev);

@@ -63,6 +63,25 @@ __device__ __forceinline__ double dsub(double a, double b) { return __dsub_rn(a,
 
 __device__ __forceinline__ float canon(float v) { return v != v ? __uint_as_float(CANON_NAN) : v; }
 
+/* IEEE square root (round to nearest) of a positive finite float, whatever the
+ * compiler's sqrt lowering: the hardware estimate y (within one ulp) is corrected by
+ * comparing s with the squares of the midpoints to its neighbours, computed exactly in
+ * double (a 25-bit midpoint squares to at most 50 bits; s is never exactly such a
+ * square). NUMERICS §4 needs the correctly rounded sqrtf of the reference. */
+__device__ inline float sqrt_rn(float s) {
+    if (!(s > 0.0f) || s == __builtin_huge_valf()) return __builtin_sqrtf(s);
+    float y = __builtin_amdgcn_sqrtf(s);
+    const double sd = (double)s;
+    for (int it = 0; it < 2; it++) {
+        const float yl = __uint_as_float(__float_as_uint(y) - 1u), yh = __uint_as_float(__float_as_uint(y) + 1u);
+        const double mlo = ((double)yl + (double)y) * 0.5, mhi = ((double)y + (double)yh) * 0.5;
+        if (sd < mlo * mlo) y = yl;
+        else if (sd > mhi * mhi) y = yh;
+        else break;
+    }
+    return y;
+}
+
 /* binary16 -> binary32 (exact) */
 __device__ __forceinline__ float h2f(uint16_t h) {
     _Float16 x;

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256) void k_norm(NormArgs a) {
         L = tree16(L);
         if (tid == 0) {
             const float ms = fdiv(L, (float)D);
-            r_sh = fdiv(1.0f, __fsqrt_rn(fadd(ms, a.eps)));
+            r_sh = fdiv(1.0f, sqrt_rn(fadd(ms, a.eps)));
         }
     }
     __syncthreads();
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(256) void k_qkv_post(QkvArgs a, const float *__rest
             for (int e = lane; e < hd; e += 16) L = fadd(L, fmul(x[e], x[e]));
         L = tree16(L);
         L = __shfl(L, 0, 64);
-        const float r = fdiv(1.0f, __fsqrt_rn(fadd(fdiv(L, (float)hd), a.eps)));
+        const float r = fdiv(1.0f, sqrt_rn(fadd(fdiv(L, (float)hd), a.eps)));
         const float *w = isq ? a.qn : a.kn;
         wave_sync();
         for (int e = lane; e < hd; e += 64) x[e] = fmul(fmul(x[e], r), w[e]);
@@ -351,7 +351,7 @@ __global__ void k_fullnorm_r(QkvArgs a, float *rfull) {
             L = fadd(L, fmul(v, v));
         }
     L = tree16(L);
-    if (lane == 0) rfull[(size_t)t * 2 + isk] = fdiv(1.0f, __fsqrt_rn(fadd(fdiv(L, (float)n), a.eps)));
+    if (lane == 0) rfull[(size_t)t * 2 + isk] = fdiv(1.0f, sqrt_rn(fadd(fdiv(L, (float)n), a.eps)));
 }
 
 /* ------------------------------------------------------------ KV compaction */

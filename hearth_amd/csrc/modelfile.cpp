@@ -128,8 +128,8 @@ bool build_config(const Meta &m, Config &c, std::string &err) {
     for (const char *k : {"n_layers", "d_model", "vocab_size", "n_heads"})
         if (!m.has(k)) { err = fmt("metadata is missing required key '%s'", k); return false; }
     const uint32_t BIG = 1u << 24;
-#define U(k, def, lo, hi, dst) if (!m.u32(k, def, lo, hi, dst, err)) return false
-#define F(k, def, dst) if (!m.f32(k, def, dst, err)) return false
+#define U(k, def, lo, hi, dst) do { if (!m.u32(k, def, lo, hi, dst, err)) return false; } while (0)
+#define F(k, def, dst) do { if (!m.f32(k, def, dst, err)) return false; } while (0)
     U("n_layers", 0, 1, 512, c.n_layers);
     U("d_model", 0, 1, 1u << 20, c.d_model);
     U("vocab_size", 0, 1, BIG, c.vocab);
@@ -375,7 +375,7 @@ bool ModelFile::open(const std::string &p, std::string &err) {
         if (t->dtype > HEARTH_Q4) { err = "tensor '" + name + "' has a dtype that is not a matrix dtype"; return false; }
         return true;
     };
-#define NEED(...) if (!need(__VA_ARGS__)) return false
+#define NEED(...) do { if (!need(__VA_ARGS__)) return false; } while (0)
     const int64_t D = c.d_model, H = c.n_heads;
     NEED(-1, "tok_embd", 2, c.vocab, D, false);
     if (!c.tie) NEED(-1, "lm_head", 2, c.vocab, D, false);

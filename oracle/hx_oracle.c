@@ -501,6 +501,7 @@ typedef struct cfg {
 } cfg;
 
 struct ho_model {
+    char dump_dir[512];
     uint8_t *map;
     size_t size;
     cfg c;
@@ -513,6 +514,20 @@ struct ho_model {
     size_t per_layer;
     int *moe_ord;
 };
+
+/* appends n floats to <dump_dir>/l<layer>_<name>.bin (debug comparisons) */
+static void dump(const ho_model *m, const char *name, int layer, const void *v, int n, int elem) {
+    char path[700];
+    FILE *f;
+    if (!m->dump_dir[0]) return;
+    snprintf(path, sizeof path, "%s/l%d_%s.bin", m->dump_dir, layer, name);
+    f = fopen(path, "ab");
+    if (f) { fwrite(v, (size_t)elem, (size_t)n, f); fclose(f); }
+}
+
+void ho_set_dump(ho_model *m, const char *dir) {
+    snprintf(m->dump_dir, sizeof m->dump_dir, "%s", dir ? dir : "");
+}
 
 static uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 static uint32_t rd32(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24); }
@@ -774,6 +789,7 @@ static void attn_gqa(ho_model *m, int l, const float *x, int pos, int slot, cons
     }
     memcpy(K + (size_t)slot * kd, k, sizeof(float) * kd);
     memcpy(Vc + (size_t)slot * kd, v, sizeof(float) * kd);
+    dump(m, "q", l, q, qd, 4);
     for (int h = 0; h < H; h++) {
         const int g = h / (H / Hkv);
         for (int i = 0; i < nr; i++) sc[i] = c->attn_scale * ho_dot16(q + h * hd, K + (size_t)rows[i] * kd + g * hd, hd);
@@ -784,6 +800,7 @@ static void attn_gqa(ho_model *m, int l, const float *x, int pos, int slot, cons
             o[h * hd + d] = acc;
         }
     }
+    dump(m, "att", l, o, qd, 4);
     lin(m, l, "attn_o", o, out);
     free(q); free(k); free(v); free(o); free(sc);
 }
@@ -883,6 +900,7 @@ static void route(ho_model *m, int l, const float *x, int *ids, float *w) {
     float *score = malloc(sizeof(float) * E), *sel = malloc(sizeof(float) * E);
     uint8_t *taken = calloc((size_t)E, 1);
     lin(m, l, "moe_router", x, score);
+    dump(m, "router", l, score, E, 4);
     if (c->score_fn == 0) softmax(score, E);
     else for (int e = 0; e < E; e++) score[e] = sigmoidf_(score[e]);
     const float *bias = c->score_bias ? vec(m, l, "moe_router_bias") : NULL;
@@ -937,6 +955,7 @@ static void moe(ho_model *m, int l, const float *x, float *out, int32_t *route_o
     int *ids = malloc(sizeof(int) * K);
     float *w = malloc(sizeof(float) * K), *y = malloc(sizeof(float) * D);
     route(m, l, x, ids, w);
+    dump(m, "ids", l, ids, K, 4);
     if (route_out) for (int j = 0; j < K; j++) route_out[j] = ids[j];
     for (int i = 0; i < D; i++) out[i] = 0.0f;
     for (int j = 0; j < K; j++) {
@@ -969,9 +988,12 @@ static void forward_token(ho_model *m, int tok, int pos, int slot, const int *ro
         else attn_gqa(m, l, x, pos, slot, rows, nr, a);
         for (int i = 0; i < D; i++) h[i] = h[i] + c->resid_scale * a[i];
         rmsnorm(x, h, vec(m, l, "ffn_norm"), D, c->eps);
+        dump(m, "h_mid", l, h, D, 4);
+        dump(m, "x_ffn", l, x, D, 4);
         if (c->layer_kind[l]) moe(m, l, x, a, routes ? routes + (size_t)m->moe_ord[l] * c->top_k : NULL);
         else ffn(m, l, "ffn_gate", "ffn_up", "ffn_down", x, a);
         for (int i = 0; i < D; i++) h[i] = h[i] + c->resid_scale * a[i];
+        dump(m, "h", l, h, D, 4);
     }
     if (logits) {
         rmsnorm(x, h, vec(m, -1, "out_norm"), D, c->eps);

@@ -91,6 +91,9 @@ int       ho_eval_tree(ho_model *m, const int32_t *tokens, const int32_t *parent
 int       ho_commit_path(ho_model *m, const int32_t *path, int n);
 /* Sets the number of worker threads for the big matrix-vector products (>= 1). */
 void      ho_set_threads(ho_model *m, int n);
+/* Debug: append per-token intermediates (q, att, h_mid, x_ffn, router, ids, h) to
+ * <dir>/l<layer>_<name>.bin ("" turns it off). */
+void      ho_set_dump(ho_model *m, const char *dir);
 
 /* ---- acceptance ----------------------------------------------------------- */
 /* Sampler.probs (generate.py:84-111) on one row of f32 logits: float64 result.

@@ -1,0 +1,161 @@
+"""The verify engine on the GPU against the oracle and the reference's golden outputs,
+on the tiny Qwen3-MoE-shaped model (4 layers, hidden 512, GQA 8/2, 16 experts top-4).
+
+- bit-exact with the restatement in portable-exp mode (the only libm difference from
+  the reference is exp; RoPE tables come from the host libm as in the reference);
+- within the north-star tolerance of the reference engine's own logits (max relative
+  error 1e-3 of max |logit|, top-1 and routing agreement >= 99.9%);
+- batch == sequential == chunked (INV-DET-2 on the device);
+- tree verification == chain evaluation of every root path, and committing a path
+  leaves the KV of the chain;
+- verify_greedy reproduces the reference's speculative step (generate.py:365-392).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import golden_io
+import oracle_py as O
+from hearth_amd import container
+from hearth_amd.engine import Engine, HearthError
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def eng(tiny_model):
+    e = Engine(tiny_model, max_seq=1024)
+    yield e
+    e.close()
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def test_prompt_bit_exact_with_oracle(eng, tiny_model):
+    g = golden_io.tiny_ref()
+    eng.reset()
+    lg = eng.eval(g["prompt"], all_logits=True)
+    O.set_exp_mode(O.EXP_PORTABLE)
+    lo = O.Model(tiny_model).eval(g["prompt"])
+    mism = int((_bits(lg) != _bits(lo)).sum())
+    assert mism == 0, f"{mism} of {lg.size} logits differ from the restatement"
+
+
+def test_within_tolerance_of_reference_engine(eng):
+    g = golden_io.tiny_ref()
+    eng.reset()
+    eng.trace_start("/tmp/hx_gpu_trace.hrtr") if False else None
+    lp = eng.eval(g["prompt"], all_logits=True)
+    ref = g["prompt_last8"]
+    scale = max(1.0, float(np.abs(ref).max()))
+    assert np.abs(lp[-8:] - ref).max() <= 1e-3 * scale
+    assert (lp.argmax(1) == g["prompt_argmax"]).mean() >= 0.999
+    lv = eng.eval(g["verify_tokens"], all_logits=True)
+    assert np.abs(lv - g["verify_logits"]).max() <= 1e-3 * max(1.0, float(np.abs(g["verify_logits"]).max()))
+    assert (lv.argmax(1) == g["verify_logits"].argmax(1)).all()
+
+
+def test_routing_agreement_with_reference(eng, tmp_path):
+    g = golden_io.tiny_ref()
+    eng.reset()
+    tr = tmp_path / "r.hrtr"
+    eng.trace_start(tr)
+    eng.eval(g["prompt"])
+    eng.eval(g["verify_tokens"])
+    eng.trace_stop()
+    routes = np.frombuffer(tr.read_bytes()[24:], dtype="<u2").reshape(-1, 4, 4).astype(np.int32)
+    want = np.concatenate([g["routes"][:128], g["routes"][-5:]])
+    agree = (np.sort(routes, -1) == np.sort(want, -1)).all(-1).mean()
+    assert agree >= 0.999, agree
+
+
+def test_batch_equals_sequential_and_chunked(tiny_model, eng):
+    toks = container.uniform_ints(21, 40, container.TINY.vocab)
+    eng.reset()
+    batch = eng.eval(toks, all_logits=True)
+    eng.reset()
+    seq = np.stack([eng.eval([t]) for t in toks])
+    assert np.array_equal(_bits(batch), _bits(seq))
+    with Engine(tiny_model, max_seq=256, max_batch=7) as e2:
+        chunked = e2.eval(toks, all_logits=True)
+        assert np.array_equal(_bits(batch), _bits(chunked))
+        e2.reset()
+        last = e2.eval(toks)
+        assert np.array_equal(_bits(last), _bits(batch[-1]))
+
+
+def test_failed_calls_change_nothing(eng):
+    eng.reset()
+    eng.eval([1, 2, 3])
+    with pytest.raises(ValueError):
+        eng.eval([1, container.TINY.vocab])
+    assert eng.pos == 3
+    with pytest.raises(HearthError):
+        eng.eval(list(range(2000)))
+    assert eng.pos == 3
+    eng.rewind(1)
+    assert eng.pos == 1
+    with pytest.raises(ValueError):
+        eng.rewind(5)
+
+
+def test_verify_greedy_reproduces_reference_step(eng):
+    g = golden_io.tiny_ref()
+    eng.reset()
+    eng.eval(g["prompt"])
+    path, final, lg = eng.verify_greedy(g["verify_tokens"], want_logits=True)
+    assert len(path) - 1 == int(g["n_acc"]) and final == int(g["final"])
+    assert path == list(range(len(path)))
+    assert eng.pos == 128 + len(path)
+    assert (lg.argmax(1) == g["verify_logits"].argmax(1)).all()
+    # the committed KV is the chain's: the next token's logits equal a plain eval's
+    nxt = eng.eval([final])
+    eng.reset()
+    eng.eval(g["prompt"])
+    eng.eval(g["verify_tokens"][:len(path)])
+    assert np.array_equal(_bits(nxt), _bits(eng.eval([final])))
+
+
+def test_tree_equals_chain_on_gpu(eng):
+    prompt = container.uniform_ints(5, 40, container.TINY.vocab)
+    tok = np.array([17, 5, 9, 300, 4000, 12, 8], dtype=np.int32)
+    par = np.array([-1, 0, 0, 1, 1, 2, 4], dtype=np.int32)
+    eng.reset()
+    eng.eval(prompt)
+    lt = eng.verify_tree(tok, par)
+    assert eng.pos == 40
+    for node in range(len(tok)):
+        path, v = [], node
+        while v >= 0:
+            path.append(v)
+            v = par[v]
+        path = path[::-1]
+        eng.rewind(40)
+        lc = eng.eval(tok[path], all_logits=True)
+        assert np.array_equal(_bits(lc[-1]), _bits(lt[node])), node
+    eng.rewind(40)
+    eng.verify_tree(tok, par, want_logits=False)
+    eng.commit_path([0, 1, 4, 6])
+    assert eng.pos == 44
+    after = eng.eval([77])
+    eng.rewind(40)
+    eng.eval(tok[[0, 1, 4, 6]])
+    assert np.array_equal(_bits(after), _bits(eng.eval([77])))
+
+
+def test_tree_greedy_verify_matches_oracle(eng, tiny_model):
+    prompt = container.uniform_ints(9, 30, container.TINY.vocab)
+    eng.reset()
+    eng.eval(prompt)
+    # a tree whose first branch follows the model's own argmax
+    first = int(np.argmax(eng.eval([3], all_logits=False)))
+    eng.rewind(30)
+    tok = np.array([3, 11, first, 5, first, 6], dtype=np.int32)
+    par = np.array([-1, 0, 0, 1, 2, 2], dtype=np.int32)
+    path, final, lg = eng.verify_greedy(tok, par, want_logits=True)
+    rc, opath, ofin = O.accept_tree(lg, tok, par)
+    assert rc == 0 and path == opath and final == ofin
+    assert path[:2] == [0, 2]

@@ -1,0 +1,169 @@
+"""The CPU restatement (oracle/) against the reference's own known answers.
+
+- pinned FNV-1a hashes of the reference's quantizers and kernels
+  (engine/tests/test_quant.c:55-62, 901-935), for the oracle and for the product
+  library's host quantizer;
+- whole forward passes: bit-exact with the reference engine built from its sources
+  (oracle/_ref) and with the committed golden outputs of that engine;
+- the portable exponential against the platform libm and closed forms;
+- tree evaluation against the chain evaluation of every root path.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import golden_io
+import kat
+import oracle_py as O
+from hearth_amd import _native, container
+
+
+@pytest.mark.parametrize("dtype", [3, 4])
+def test_oracle_quantizer_pins(dtype):
+    W, _ = kat.pinned_inputs()
+    assert kat.fnv1a(O.quantize(dtype, W)) == {3: kat.PIN_Q8, 4: kat.PIN_Q4}[dtype]
+
+
+def test_oracle_q4_heavy_tail_pin():
+    x = kat.det_fill_tails(64 * 1024, 3).reshape(64, 1024)
+    assert kat.fnv1a(O.quantize(4, x)) == kat.PIN_Q4_TAILS
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2, 3, 4])
+def test_oracle_matmul_pins(dtype):
+    W, X = kat.pinned_inputs()
+    Y = O.matmul(dtype, O.quantize(dtype, W), kat.R, kat.C, X)
+    assert kat.fnv1a(Y.tobytes()) == kat.PIN_Y[dtype]
+
+
+@pytest.mark.parametrize("dtype", [3, 4])
+def test_library_quantizer_pins(dtype):
+    """hearth_quantize of libhearth.so (host code) writes reference-identical bytes."""
+    W, _ = kat.pinned_inputs()
+    assert kat.fnv1a(_native.quantize(dtype, W)) == {3: kat.PIN_Q8, 4: kat.PIN_Q4}[dtype]
+    x = kat.det_fill_tails(64 * 1024, 3).reshape(64, 1024)
+    assert kat.fnv1a(_native.quantize(4, x)) == kat.PIN_Q4_TAILS
+
+
+def test_act_quant_ties_and_degenerate_blocks():
+    """NUMERICS §2 closed forms: x*id on exact .5 ties rounds half to even; zero and
+    NaN inputs give q = 0; inf saturates the scale."""
+    x = np.zeros(256, np.float32)
+    x[:64] = np.arange(64) - 31.5          # amax 32 -> id = 127/32, products on k + .5 grid
+    x[0] = 127.0
+    x[64:128] = 0.0
+    x[128:192] = np.nan
+    x[192] = np.inf
+    out = np.zeros(4 * 72, np.uint8)
+    O.lib().ho_act_quant(x.ctypes.data_as(O._FP), 256, out.ctypes.data_as(O.c_void_p))
+    blk = out.reshape(4, 72)
+    d = blk[:, :4].copy().view(np.float32)[:, 0]
+    q = blk[:, 8:].view(np.int8)
+    assert d[0] == np.float32(127.0) / np.float32(127.0)
+    ref = np.array([np.round(np.float32(v)) for v in x[:64]], dtype=np.int64)   # id = 1: ties to even
+    assert np.array_equal(q[0].astype(np.int64), np.clip(ref, -127, 127))
+    assert d[1] == 0.0 and not q[1].any()
+    assert not q[2].any()
+    assert np.isinf(d[3]) and not q[3].any()
+
+
+def test_portable_exp_matches_libm_and_closed_forms():
+    """The portable exp is within one ulp of glibc's expf and equal in > 99.9% of
+    cases; exact special values; monotone on a dense grid."""
+    L = O.lib()
+    xs = np.linspace(-103.0, 88.5, 200001, dtype=np.float32)
+    port = np.array([L.ho_exp_port_f(float(v)) for v in xs[::10]], dtype=np.float32)
+    libm = np.exp(xs[::10].astype(np.float64)).astype(np.float32)   # correctly rounded reference
+    ulp = np.abs(port.view(np.int32).astype(np.int64) - libm.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1 and (ulp == 0).mean() > 0.999
+    assert L.ho_exp_port_f(0.0) == 1.0
+    assert L.ho_exp_port_f(float("-inf")) == 0.0
+    assert math.isinf(L.ho_exp_port_f(89.0)) and math.isnan(L.ho_exp_port_f(float("nan")))
+    assert np.all(np.diff(port) >= 0)
+    for v in (-745.0, -700.0, -1.0, 1e-10, 0.5, 300.0, 709.0):
+        assert L.ho_exp_port_d(v) == pytest.approx(math.exp(v), rel=3e-16, abs=5e-324)
+
+
+def test_oracle_matches_reference_golden():
+    """The restatement (libm exp) reproduces the reference engine's committed outputs bit
+    for bit: prompt logits, every argmax, the verify logits and the routing."""
+    g = golden_io.tiny_ref()
+    if g is None:
+        pytest.skip("no golden fixture")
+    import tempfile
+    from pathlib import Path
+    path = container.make_tiny(Path(tempfile.mkdtemp()) / "t.hearth", _native.quantize, seed=1)
+    assert container.sha256(path) == str(g["sha256"])
+    O.set_exp_mode(O.EXP_LIBM)
+    m = O.Model(path)
+    lp, rp = m.eval(g["prompt"], routes=True)
+    assert np.array_equal(lp[-8:].view(np.uint32), g["prompt_last8"].view(np.uint32))
+    assert np.array_equal(lp.argmax(1), g["prompt_argmax"])
+    for t in g["continuation"][1:]:
+        pass
+    m.rewind(128)
+    lv, rv = m.eval(g["verify_tokens"], routes=True)
+    assert np.array_equal(lv.view(np.uint32), g["verify_logits"].view(np.uint32))
+    assert np.array_equal(rp, g["routes"][:128])
+    assert np.array_equal(rv, g["routes"][-5:])
+
+
+@pytest.mark.skipif(not O.REF_LIB.is_file(), reason="reference engine not built (make -C oracle)")
+def test_oracle_matches_reference_engine(tiny_model):
+    """Bit-exact with the reference engine compiled from source, batch of 64 tokens."""
+    from hearth_amd.engine import Engine
+    toks = container.uniform_ints(3, 64, container.TINY.vocab)
+    ref = Engine(tiny_model, lib=str(O.REF_LIB), threads=4, prefetch="off")
+    lr = ref.eval(toks, all_logits=True)
+    ref.close()
+    O.set_exp_mode(O.EXP_LIBM)
+    lo = O.Model(tiny_model).eval(toks)
+    assert np.array_equal(lr.view(np.uint32), lo.view(np.uint32))
+
+
+def test_tree_equals_chain(tiny_model):
+    """Every tree node's logits equal the chain evaluation of its root path (bit for bit),
+    and committing a path leaves the same KV as evaluating the chain."""
+    O.set_exp_mode(O.EXP_PORTABLE)
+    prompt = container.uniform_ints(5, 40, container.TINY.vocab)
+    tok = np.array([17, 5, 9, 300, 4000, 12, 8], dtype=np.int32)
+    par = np.array([-1, 0, 0, 1, 1, 2, 4], dtype=np.int32)
+    t = O.Model(tiny_model)
+    t.eval(prompt)
+    lt = t.eval_tree(tok, par)
+    for node in range(len(tok)):
+        path = []
+        v = node
+        while v >= 0:
+            path.append(v)
+            v = par[v]
+        path = path[::-1]
+        c = O.Model(tiny_model)
+        c.eval(prompt)
+        lc = c.eval(tok[path])
+        assert np.array_equal(lc[-1].view(np.uint32), lt[node].view(np.uint32)), node
+    t.commit_path([0, 1, 4, 6])
+    after_tree = t.eval([77])
+    c = O.Model(tiny_model)
+    c.eval(prompt)
+    c.eval(tok[[0, 1, 4, 6]])
+    assert np.array_equal(c.eval([77]).view(np.uint32), after_tree.view(np.uint32))
+
+
+def test_greedy_acceptance_closed_form():
+    """Greedy chain acceptance = longest prefix with argmax(rows[i]) == d_i, final =
+    argmax at the first mismatch (first index wins ties), generate.py:365-392."""
+    rng = np.random.default_rng(0)
+    for trial in range(200):
+        k, V = int(rng.integers(1, 9)), int(rng.integers(2, 50))
+        rows = rng.integers(-3, 4, size=(k + 1, V)).astype(np.float32)   # many ties
+        am = rows.argmax(1)
+        drafts = np.where(rng.random(k) < 0.6, am[:k], rng.integers(0, V, k)).astype(np.int32)
+        n_acc = 0
+        while n_acc < k and drafts[n_acc] == am[n_acc]:
+            n_acc += 1
+        rc, path, fin = O.accept_tree(rows, np.concatenate([[0], drafts]), np.arange(-1, k))
+        assert rc == 0 and path == list(range(n_acc + 1)) and fin == am[n_acc]
