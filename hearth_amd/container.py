@@ -306,6 +306,22 @@ def _random_blocks(rng: np.random.Generator, dtype: int, rows: int, cols: int) -
     return blk.tobytes()
 
 
+class _RowPool:
+    """Dense rows drawn from a pool of random encoded rows (the reference's synthetic
+    recipe, python/hearth/synth.py:328-338): row r of a matrix with salt s is pool row
+    (r * 31 + s) mod n. Throughput runs only need valid blocks of the right shape."""
+
+    def __init__(self, rng: np.random.Generator, n: int = 1021):
+        self.rng, self.n, self.p = rng, n, {}
+
+    def rows(self, dtype: int, rows: int, cols: int, salt: int) -> bytes:
+        key = (dtype, cols)
+        if key not in self.p:
+            self.p[key] = np.frombuffer(_random_blocks(self.rng, dtype, self.n, cols), dtype=np.uint8).reshape(self.n, -1)
+        idx = (np.arange(rows, dtype=np.int64) * 31 + salt) % self.n
+        return self.p[key][idx].tobytes()
+
+
 def make_shaped(path, shape: Shape = QWEN3_30B_A3B, seed: int = 0, n_unique_slabs: int = 32,
                 n_layers: int | None = None) -> Path:
     """A real-shaped model with random weights for throughput runs: Q4 experts, Q8
@@ -317,34 +333,35 @@ def make_shaped(path, shape: Shape = QWEN3_30B_A3B, seed: int = 0, n_unique_slab
     D, H, Hkv, hd, E, F, V, L = s.d_model, s.n_heads, s.n_kv_heads, s.head_dim, s.n_experts, s.expert_ffn, s.vocab, s.n_layers
     w = ContainerWriter(_meta(s, f"synthetic:{s.arch}:seed{seed}"))
     ones = np.ones(D, dtype=np.float32).tobytes()
-    w.add("tok_embd", Q8, (V, D), _random_blocks(rng, Q8, V, D))
-    w.add("lm_head", Q8, (V, D), _random_blocks(rng, Q8, V, D))
+    pool = _RowPool(rng)
+    w.add("tok_embd", Q8, (V, D), pool.rows(Q8, V, D, 1))
+    w.add("lm_head", Q8, (V, D), pool.rows(Q8, V, D, 2))
     w.add("out_norm", F32, (D,), ones)
     w.add("rope_inv_freq", F32, (hd // 2,), rope_inv_freq(s).tobytes())
     nb, og, ou, od = slab_layout(Q4, D, F)
-    pool = []
+    slabs = []
     for i in range(min(n_unique_slabs, L * E)):
         slab = bytearray(nb)
         for off, (rows, cols) in ((og, (F, D)), (ou, (F, D)), (od, (D, F))):
             b = _random_blocks(rng, Q4, rows, cols)
             slab[off:off + len(b)] = b
-        pool.append(bytes(slab))
+        slabs.append(bytes(slab))
     for l in range(L):
         p = f"blk.{l}."
         w.add(p + "attn_norm", F32, (D,), ones)
         w.add(p + "ffn_norm", F32, (D,), ones)
-        w.add(p + "attn_q", Q8, (H * hd, D), _random_blocks(rng, Q8, H * hd, D))
-        w.add(p + "attn_k", Q8, (Hkv * hd, D), _random_blocks(rng, Q8, Hkv * hd, D))
-        w.add(p + "attn_v", Q8, (Hkv * hd, D), _random_blocks(rng, Q8, Hkv * hd, D))
-        w.add(p + "attn_o", Q8, (D, H * hd), _random_blocks(rng, Q8, D, H * hd))
+        w.add(p + "attn_q", Q8, (H * hd, D), pool.rows(Q8, H * hd, D, 10 * l + 3))
+        w.add(p + "attn_k", Q8, (Hkv * hd, D), pool.rows(Q8, Hkv * hd, D, 10 * l + 4))
+        w.add(p + "attn_v", Q8, (Hkv * hd, D), pool.rows(Q8, Hkv * hd, D, 10 * l + 5))
+        w.add(p + "attn_o", Q8, (D, H * hd), pool.rows(Q8, D, H * hd, 10 * l + 6))
         w.add(p + "attn_q_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
         w.add(p + "attn_k_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
         router = (rng.standard_normal((E, D), dtype=np.float32) * np.float32(2.5 / math.sqrt(D))).astype(np.float32)
         w.add(p + "moe_router", F32, (E, D), router.tobytes())
         for e in range(E):
-            i = (l * E + e) % len(pool)
-            if (l * E + e) < len(pool):
-                w.add_expert(l, e, Q4, pool[i])
+            i = (l * E + e) % len(slabs)
+            if (l * E + e) < len(slabs):
+                w.add_expert(l, e, Q4, slabs[i])
             else:
                 w.alias_expert(l, e, divmod(i, E))
     return w.write(path)
