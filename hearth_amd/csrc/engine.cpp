@@ -94,6 +94,7 @@ struct Layer {
     const float *router_bias = nullptr;
     ExpertW *experts = nullptr;     /* device table [E] */
     uint64_t expert_bytes_each = 0; /* algorithmic bytes of one expert (gate+up+down) */
+    int dtype_mask = 0;             /* bit dt set when some expert has dtype dt */
 };
 
 struct DeviceError {
@@ -132,9 +133,10 @@ struct hearth_engine {
     /* scratch for B tokens */
     float *h = nullptr, *x = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr, *qr = nullptr, *att = nullptr,
           *ao = nullptr, *S = nullptr, *lge = nullptr, *wts = nullptr, *Y = nullptr, *f1 = nullptr, *f2 = nullptr,
-          *logits = nullptr, *rope = nullptr, *rfull = nullptr;
+          *logits = nullptr, *rope = nullptr, *rfull = nullptr, *midf = nullptr;
     int ldS = 0;
     Act ax{}, aatt{}, amid{}, af{};
+    hxd::SlotDesc *slot_desc = nullptr;
     int *ids = nullptr, *route_meta = nullptr, *pair_tok = nullptr, *pair_of = nullptr, *tokens = nullptr,
         *depth = nullptr, *anc = nullptr, *route_out = nullptr, *acc_i = nullptr;
     unsigned long long *dstats = nullptr;
@@ -393,6 +395,7 @@ bool hearth_engine::upload(std::string &msg) {
             up.quant(table[e].up, slab + ou);
             up.quant(table[e].down, slab + od);
             w.expert_bytes_each = 2 * (uint64_t)F * row_bytes(dt, D) + (uint64_t)D * row_bytes(dt, F);
+            w.dtype_mask |= 1 << dt;
         }
         w.experts = (ExpertW *)dalloc(sizeof(ExpertW) * (size_t)E);
         ck(hipMemcpyAsync(w.experts, table.data(), sizeof(ExpertW) * (size_t)E, hipMemcpyHostToDevice, st));
@@ -419,8 +422,13 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
     rope_dim = c.rope_dim;
     if (hd > 512 || hd % 16) { fail(err, errlen, "%s: head_dim %d unsupported (needs a multiple of 16 <= 512)", opt.model_path, hd); return false; }
     if (E > 1024) { fail(err, errlen, "%s: %d experts exceed this build's limit of 1024", opt.model_path, E); return false; }
+    if (c.n_moe && K > 64) { fail(err, errlen, "%s: top_k %d exceeds this build's limit of 64", opt.model_path, K); return false; }
     if (c.n_group > 64) { fail(err, errlen, "%s: n_group %d exceeds this build's limit of 64", opt.model_path, c.n_group); return false; }
     if (c.n_moe && F % 64) { fail(err, errlen, "%s: expert_ffn_dim %d is not a multiple of 64", opt.model_path, F); return false; }
+    if (c.n_moe && (D > 16384 || F > 16384)) {
+        fail(err, errlen, "%s: expert matrices of %d x %d exceed this build's limit of 16384", opt.model_path, F, D);
+        return false;
+    }
     for (int l = 0; l < L && c.n_moe; l++)
         for (int e = 0; e < E && c.layer_kind[l]; e++)
             if (!dtype_is_quant((int)mf.expert(l, e)->dtype)) {
@@ -478,9 +486,11 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
             ids = dnew<int>(P);
             wts = dnew<float>(P);
             route_meta = dnew<int>(1 + 3 * (size_t)E);
+            slot_desc = (hxd::SlotDesc *)dalloc(sizeof(hxd::SlotDesc) * (size_t)E);
             pair_tok = dnew<int>(P);
             pair_of = dnew<int>(P);
             amid = make_act((int)P, F);
+            midf = dnew<float>(P * F);
             Y = dnew<float>(P * D);
             route_out = dnew<int>(Bs * c.n_moe * K);
         }
@@ -561,9 +571,10 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             at.q = qr; at.kc = qa.kc; at.vc = qa.vc; at.S = S; at.ldS = ldS; at.out = att; at.T = T; at.H = H;
             at.Hkv = Hkv; at.hd = hd; at.cap = cap; at.scale = c.attn_scale;
             at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos0 = pos;
+            at.qo = aatt; at.qo_on = w.o.quant && hd % 64 == 0;
             hxl::attention(at, st);
             dump("att", l, att, T, q_dim);
-            if (w.o.quant) hxl::quant_rows(att, q_dim, T, q_dim / 64, aatt, st);
+            if (w.o.quant && !at.qo_on) hxl::quant_rows(att, q_dim, T, q_dim / 64, aatt, st);
             matmul(w.o, aatt, att, q_dim, T, ao, D, false, 1.0f);
         });
         timed(&ks.norm_s, [&] {
@@ -585,14 +596,16 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 r.routed_scale = c.routed_scale; r.ids = ids; r.wts = wts; r.n_active = n_active; r.ulist = ulist;
                 r.u_p0 = u_p0; r.u_n = u_n; r.pair_tok = pair_tok; r.pair_of = pair_of;
                 r.route_out = route_out; r.moe_ord = moe_ord[l]; r.n_moe = c.n_moe; r.stats = dstats;
+                r.table = w.experts; r.desc = slot_desc; r.n_slots = std::min(E, T * K);
                 hxl::route(r, st);
             });
             dump("router", l, lge, T, E);
             dump("ids", l, ids, T, K);
             timed(&ks.expert_s, [&] {
                 hxd::MoeArgs m{};
-                m.table = w.experts; m.n_active = n_active; m.ulist = ulist; m.u_p0 = u_p0; m.u_n = u_n;
-                m.pair_tok = pair_tok; m.x = ax; m.mid = amid; m.Y = Y; m.T = T; m.F = F; m.D = D;
+                m.table = w.experts; m.desc = slot_desc; m.n_active = n_active; m.ulist = ulist; m.u_p0 = u_p0; m.u_n = u_n;
+                m.pair_tok = pair_tok; m.x = ax; m.mid = amid; m.midf = midf; m.Y = Y; m.T = T; m.F = F; m.D = D;
+                m.P = T * K; m.dtype_mask = w.dtype_mask;
                 const int slots = std::min(E, T * K);
                 hxl::expert_gateup(m, slots, st);
                 hxl::expert_down(m, slots, st);

@@ -27,15 +27,26 @@ struct GemmArgs {
 
 struct ExpertW { QMat gate, up, down; };
 
+/* One active expert slot of a routed batch, written by the bucketing step: the expert's
+ * matrices, its first pair and its pair count (n = 0: slot unused). */
+struct SlotDesc {
+    ExpertW w;
+    int p0, n, e, pad;
+};
+
 struct MoeArgs {
     const ExpertW *table;     /* [n_experts] of this layer */
+    const SlotDesc *desc;     /* [n_slots] active expert slots */
     const int *n_active;      /* number of active experts (device scalar) */
     const int *ulist, *u_p0, *u_n;
     const int *pair_tok;      /* pair -> token */
     Act x;                    /* normalized token activations [T] */
     Act mid;                  /* SwiGLU activations per pair [P] */
+    float *midf;              /* SwiGLU activations per pair before quantization, f32 [P][F] */
     float *Y;                 /* expert outputs [P][D] */
     int T, F, D;
+    int P;                    /* pairs: T * top_k */
+    int dtype_mask;           /* bit dt set when some expert of the layer has dtype dt */
 };
 
 /* Routing (NUMERICS §5.3) of T tokens from router logits. */
@@ -50,6 +61,9 @@ struct RouteArgs {
     int *route_out;           /* [T][n_moe][K] or null */
     int moe_ord, n_moe;
     unsigned long long *stats;   /* [0] expert uses, [1] unique expert loads */
+    const ExpertW *table;     /* [E] expert matrices of the layer */
+    SlotDesc *desc;           /* [n_slots] out: active slots, then n = 0 */
+    int n_slots;
 };
 
 /* Per-call token geometry: token t sits at KV slot pos0 + t, has RoPE position
@@ -72,6 +86,8 @@ struct AttnArgs {
     int T, H, Hkv, hd, cap;
     float scale;
     TokGeom g;
+    Act qo;                   /* NUMERICS §2 blocks of out (when qo_on; head_dim % 64 == 0) */
+    int qo_on;
 };
 
 struct QkvArgs {

@@ -9,9 +9,14 @@
  * ancestors' slots from the root to itself (for a chain: slots 0..pos0+t). A tree
  * node therefore computes exactly what the chain root->node computes.
  *
+ * The value sum is one dependent f32 add chain per (token, head, d) of length
+ * pos0 + depth + 1; it is the step's latency floor, so the value kernel keeps one
+ * chain per lane, one wave per SIMD, and V tiles prefetched two tiles ahead into an
+ * LDS ring shared by the four waves (heads) of a workgroup.
+ *
  * Launch shapes are XCD-aware: workgroup IDs are dealt round-robin to the 8 XCDs,
- * so the KV-group index is the fastest-varying part of the ID and every workgroup of
- * one XCD reads the same group's K or V rows from that XCD's L2.
+ * so the KV-group index (and value d-chunk) is the fastest-varying part of the ID and
+ * the workgroups of one XCD read the same group's K or V rows from that XCD's L2.
  */
 #include "hx_device.h"
 #include "hx_launch.h"
@@ -21,133 +26,351 @@ using namespace hxd;
 namespace {
 
 constexpr int SC_ROWS = 256;   /* rows per scores workgroup (one per thread) */
-constexpr int VT = 64;         /* rows per value tile */
+constexpr int KC = 16;         /* K floats per staged chunk (head_dim % 16 == 0) */
+constexpr int MAX_ANC = 4096;  /* ancestors of one token (max_batch) */
 
 __device__ __forceinline__ int row_slot(const TokGeom &g, int t, int v) {
     return v < g.pos0 ? v : g.pos0 + g.anc[(size_t)t * g.anc_ld + (v - g.pos0)];
 }
 
-/* One thread per row v; the heads of the KV group in passes of four. */
+/* Scores of NH heads of KV group g for 256 rows v of token t: one thread per row, 16
+ * partial sums per head (element c goes to partial c % 16), then the 8/4/2/1 tree.
+ * K rows and the q chunk go through a double-buffered LDS stage, one barrier per
+ * 16-float chunk; the next chunk's loads are in flight while the current one is used. */
+template <int NH>
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
+    __shared__ float kt[2][SC_ROWS][KC + 1];
+    __shared__ float4 qs[2][NH][KC / 4];
+    __shared__ int slot_s[SC_ROWS];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
     int b = blockIdx.x;
     const int g = b % Hkv;
     b /= Hkv;
     const int t = b % a.T, c = b / a.T;
     const int nr = a.g.pos0 + a.g.depth[t] + 1;
-    const int v = c * SC_ROWS + threadIdx.x;
-    if (c * SC_ROWS >= nr || v >= nr) return;
-    const float *krow = a.kc + ((size_t)g * a.cap + row_slot(a.g, t, v)) * hd;
+    const int v0 = c * SC_ROWS;
+    if (v0 >= nr) return;   /* uniform */
+    const int tid = threadIdx.x;
+    const int nrows = nr - v0 < SC_ROWS ? nr - v0 : SC_ROWS;
+    slot_s[tid] = row_slot(a.g, t, v0 + (tid < nrows ? tid : nrows - 1));
+    __syncthreads();
+    /* staging: float4 k = tid + 256u of the chunk: row k / 4, floats 4 (k % 4) .. + 3 */
+    const float *src[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        src[u] = a.kc + ((size_t)g * a.cap + slot_s[(tid >> 2) + 64 * u]) * hd + (tid & 3) * 4;
     const float *qb = a.q + ((size_t)t * a.H + (size_t)g * grp) * hd;
-    float *Sb = a.S + ((size_t)t * a.H + (size_t)g * grp) * a.ldS + v;
-    for (int h0 = 0; h0 < grp; h0 += 4) {
-        const int nh = grp - h0 < 4 ? grp - h0 : 4;
-        float L[4][16];
+    const bool qlane = tid < NH * 4;
+    const float *qsrc = qb + (size_t)(qlane ? tid >> 2 : 0) * hd + (tid & 3) * 4;
+    const int nchunk = hd / KC, niter = (grp / NH) * nchunk;
+    float4 kr[4], qr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto gload = [&](int it) {
+        const int c0 = (it % nchunk) * KC, h0 = (it / nchunk) * NH;
 #pragma unroll
-        for (int hh = 0; hh < 4; hh++)
+        for (int u = 0; u < 4; u++) kr[u] = *(const float4 *)(src[u] + c0);
+        if (qlane) qr = *(const float4 *)(qsrc + (size_t)h0 * hd + c0);
+    };
+    auto lstore = [&](int buf) {
 #pragma unroll
-            for (int j = 0; j < 16; j++) L[hh][j] = 0.0f;
-        for (int c16 = 0; c16 < hd; c16 += 16) {
-            float kv[16];
+        for (int u = 0; u < 4; u++) {
+            float *d = &kt[buf][(tid >> 2) + 64 * u][(tid & 3) * 4];
+            d[0] = kr[u].x;
+            d[1] = kr[u].y;
+            d[2] = kr[u].z;
+            d[3] = kr[u].w;
+        }
+        if (qlane) qs[buf][tid >> 2][tid & 3] = qr;
+    };
+    float L[NH][16];
 #pragma unroll
-            for (int j = 0; j < 16; j++) kv[j] = c16 + j < hd ? krow[c16 + j] : 0.0f;
+    for (int hh = 0; hh < NH; hh++)
 #pragma unroll
-            for (int hh = 0; hh < 4; hh++) {
-                if (hh >= nh) break;
-                const float *qh = qb + (size_t)(h0 + hh) * hd + c16;
+        for (int j = 0; j < 16; j++) L[hh][j] = 0.0f;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    float *Sb = a.S + ((size_t)t * a.H + (size_t)g * grp) * a.ldS + v0 + tid;
+    for (int it = 0; it < niter; it++) {
+        const int buf = it & 1;
+        if (it + 1 < niter) gload(it + 1);
+        float kv[16];
 #pragma unroll
-                for (int j = 0; j < 16; j++)
-                    if (c16 + j < hd) L[hh][j] = fadd(L[hh][j], fmul(qh[j], kv[j]));
+        for (int j = 0; j < 16; j++) kv[j] = kt[buf][tid][j];
+#pragma unroll
+        for (int hh = 0; hh < NH; hh++) {
+            float q[16];
+#pragma unroll
+            for (int j4 = 0; j4 < 4; j4++) {
+                const float4 x = qs[buf][hh][j4];
+                q[4 * j4] = x.x;
+                q[4 * j4 + 1] = x.y;
+                q[4 * j4 + 2] = x.z;
+                q[4 * j4 + 3] = x.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++) L[hh][j] = fadd(L[hh][j], fmul(q[j], kv[j]));
+        }
+        if (it % nchunk == nchunk - 1) {
+            const int h0 = (it / nchunk) * NH;
+#pragma unroll
+            for (int hh = 0; hh < NH; hh++) {
+#pragma unroll
+                for (int s = 8; s >= 1; s >>= 1)
+#pragma unroll
+                    for (int j = 0; j < s; j++) L[hh][j] = fadd(L[hh][j], L[hh][j + s]);
+                if (tid < nrows) Sb[(size_t)(h0 + hh) * a.ldS] = fmul(a.scale, canon(L[hh][0]));
+#pragma unroll
+                for (int j = 0; j < 16; j++) L[hh][j] = 0.0f;
             }
         }
-#pragma unroll
-        for (int hh = 0; hh < 4; hh++) {
-            if (hh >= nh) break;
-#pragma unroll
-            for (int s = 8; s >= 1; s >>= 1)
-#pragma unroll
-                for (int j = 0; j < s; j++) L[hh][j] = fadd(L[hh][j], L[hh][j + s]);
-            Sb[(size_t)(h0 + hh) * a.ldS] = fmul(a.scale, canon(L[hh][0]));
-        }
+        if (it + 1 < niter) lstore(buf ^ 1);
+        __syncthreads();
     }
 }
 
-/* softmax over one (token, head) row of scores, in place (quant.c:634-642) */
+__device__ __forceinline__ float sum16_lds(const float *es, int n, int lane16, float L) {
+    /* lane lane16 of 16: continues the sequential sum L with es[lane16], es[lane16 + 16],
+     * ..., the next 8 operands read while the current 8 are added */
+    int i = lane16;
+    float cur[8], nxt[8];
+    const int full = n >= 16 * 8 ? (n - lane16) / 128 : 0;   /* groups of 8 in range */
+    if (full > 0) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) cur[u] = es[i + 16 * u];
+        for (int gi = 0; gi < full; gi++) {
+            const int inx = gi + 1 < full ? i + 128 : i;
+#pragma unroll
+            for (int u = 0; u < 8; u++) nxt[u] = es[inx + 16 * u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) L = fadd(L, cur[u]);
+#pragma unroll
+            for (int u = 0; u < 8; u++) cur[u] = nxt[u];
+            i += 128;
+        }
+    }
+    for (; i < n; i += 16) L = fadd(L, es[i]);
+    return L;
+}
+
+/* softmax over one (token, head) row of scores, in place (quant.c:634-642): running
+ * max from s[0] (a NaN s[0] stays the max, later NaNs are skipped), e = exp(s - max),
+ * sum16 of e, p = e / sum. Up to 8192 scores stay in registers; longer rows are
+ * processed in chunks of 8192 re-read from the row. */
+constexpr int SM_PER = 32;
+constexpr int SM_CH = 256 * SM_PER;
+
 __global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
-    __shared__ float red[256];
+    __shared__ float es[SM_CH];
+    __shared__ float red[4];
     __shared__ float sum_sh;
-    const int t = blockIdx.x / a.H, h = blockIdx.x % a.H, tid = threadIdx.x;
+    const int t = blockIdx.x / a.H, h = blockIdx.x % a.H, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nr = a.g.pos0 + a.g.depth[t] + 1;
     float *s = a.S + ((size_t)t * a.H + h) * a.ldS;
+    const bool inreg = nr <= SM_CH;
+    float x[SM_PER];
     float m = -__builtin_huge_valf();
-    for (int i = tid; i < nr; i += 256) {
-        const float x = s[i];
-        if (x == x) m = fmaxf(m, x);
+    if (inreg) {
+#pragma unroll
+        for (int u = 0; u < SM_PER; u++) {
+            const int i = tid + 256 * u;
+            x[u] = i < nr ? s[i] : -__builtin_huge_valf();
+        }
+#pragma unroll
+        for (int u = 0; u < SM_PER; u++)
+            if (x[u] == x[u]) m = fmaxf(m, x[u]);
+    } else {
+        for (int i = tid; i < nr; i += 256) {
+            const float v = s[i];
+            if (v == v) m = fmaxf(m, v);
+        }
     }
-    red[tid] = m;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (lane == 0) red[wave] = m;
     __syncthreads();
-    for (int k = 128; k >= 1; k >>= 1) {
-        if (tid < k) red[tid] = fmaxf(red[tid], red[tid + k]);
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s0 = s[0];
+    if (s0 != s0) m = s0;
+    float L = 0.0f;   /* lane tid < 16: partial of the elements i = tid (mod 16) */
+    for (int c0 = 0; c0 < nr; c0 += SM_CH) {
+        const int n = nr - c0 < SM_CH ? nr - c0 : SM_CH;
+        if (c0) __syncthreads();
+        if (inreg) {
+#pragma unroll
+            for (int u = 0; u < SM_PER; u++) {
+                const int i = tid + 256 * u;
+                if (i < n) {
+                    x[u] = exp_port_f(fadd(x[u], -m));
+                    es[i] = x[u];
+                }
+            }
+        } else {
+            for (int i = tid; i < n; i += 256) es[i] = exp_port_f(fadd(s[c0 + i], -m));
+        }
         __syncthreads();
+        /* SM_CH is a multiple of 16, so element c0 + i keeps lane (c0 + i) % 16 = i % 16 */
+        if (tid < 16) L = sum16_lds(es, n, tid, L);
+        if (!inreg) {
+            __syncthreads();
+            for (int i = tid; i < n; i += 256) s[c0 + i] = es[i];
+        }
     }
-    m = s[0] != s[0] ? s[0] : red[0];   /* the reference's running max starts at s[0] */
-    for (int i = tid; i < nr; i += 256) s[i] = exp_port_f(fadd(s[i], -m));
-    __syncthreads();
     if (tid < 16) {
-        float L = 0.0f;
-        for (int i = tid; i < nr; i += 16) L = fadd(L, s[i]);
 #pragma unroll
         for (int k = 8; k >= 1; k >>= 1) L = fadd(L, __shfl_down(L, k, 16));
         if (tid == 0) sum_sh = L;
     }
     __syncthreads();
     const float sum = sum_sh;
-    for (int i = tid; i < nr; i += 256) s[i] = fdiv(s[i], sum);
+    if (inreg) {
+#pragma unroll
+        for (int u = 0; u < SM_PER; u++) {
+            const int i = tid + 256 * u;
+            if (i < nr) s[i] = fdiv(x[u], sum);
+        }
+    } else {
+        for (int i = tid; i < nr; i += 256) s[i] = fdiv(s[i], sum);
+    }
 }
 
-/* o[t][h][d] = sum_v p_v * V_v[d], v in order: one wave per head (four heads of one
- * KV group per workgroup), one lane per d; V rows staged through LDS tiles shared by
- * the four waves. */
+/* o[t][h][d] = sum_v p_v * V_v[d], v in order. A workgroup holds up to four heads of
+ * one token t in one KV group g, for one 64-wide d chunk (one wave per head, lane = d).
+ * The sum is one dependent f32 add per row, so the kernel is built around that chain:
+ * products of 16 rows are formed before their 16 adds (a product never waits in front of
+ * the chain), rows come in tiles of 128 through a 3-slot LDS ring (one barrier per 128
+ * rows), and each tile is requested VPF tiles before it is written to LDS. Loads are
+ * unconditional: tile indexes are clamped to the last tile and rows/columns to valid
+ * ones; rows past the chain are never read back, columns past head_dim only feed
+ * discarded lanes. */
+constexpr int VT2 = 128;
+constexpr int VPF = 3;   /* register tile sets: the code below names three */
+
 __global__ __launch_bounds__(256) void k_attn_values(AttnArgs a) {
-    __shared__ float vt[VT][64];
-    __shared__ float pt[4][VT];
-    __shared__ int slots[VT];
+    __shared__ float vt[3][VT2][64];
+    __shared__ float pt[3][4][VT2];
+    __shared__ int anc_s[MAX_ANC];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
-    const int nq = (grp + 3) / 4, nd = (hd + 63) / 64;
+    const int nd = (hd + 63) / 64, qpt = (grp + 3) / 4;
     int b = blockIdx.x;
     const int dc = b % nd;
     b /= nd;
     const int g = b % Hkv;
     b /= Hkv;
-    const int hq = b % nq, t = b / nq;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
-    const int hin = hq * 4 + wave;                    /* head within the group */
-    const bool head_live = hin < grp;
-    const int h = g * grp + (head_live ? hin : 0);
-    const int d = dc * 64 + lane;
-    const int nr = a.g.pos0 + a.g.depth[t] + 1;
+    const int hq = b % qpt, t = b / qpt;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int hh = hq * 4 + wave;
+    const bool live = hh < grp;
+    const int h = g * grp + (live ? hh : 0);
+    const int pos0 = a.g.pos0, dep = a.g.depth[t];
+    const int nr = pos0 + dep + 1;
+    const int ntiles = (nr + VT2 - 1) / VT2, last = ntiles - 1;
+    for (int j = tid; j <= dep; j += 256) anc_s[j] = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + j];
+    __syncthreads();
     const float *p = a.S + ((size_t)t * a.H + h) * a.ldS;
-    const float *vbase = a.vc + (size_t)g * a.cap * hd;
+    /* staging: float4 u of thread tid is float4 k = 256 u + tid of the tile, i.e. row
+     * k / 16, float4 column k % 16: each wave instruction moves four whole 256-byte rows
+     * and writes 1 KiB of consecutive LDS (no bank conflicts) */
+    const int c4 = (tid & 15) * 4, rbase = tid >> 4;   /* row of float4 u: 16 u + rbase */
+    const float *vcol = a.vc + (size_t)g * a.cap * hd + (dc * 64 + c4 < hd ? dc * 64 + c4 : 0);
+    auto row_of = [&](int i, int u) -> const float * {
+        i = i < last ? i : last;
+        int v = i * VT2 + 16 * u + rbase;
+        v = v < nr ? v : nr - 1;
+        return vcol + (size_t)(v < pos0 ? v : anc_s[v - pos0]) * hd;
+    };
+    auto p_of = [&](int i, int k) -> float {
+        i = i < last ? i : last;
+        const int vp = i * VT2 + k * 64 + lane;
+        return p[vp < nr ? vp : nr - 1];
+    };
+    /* the register sets are named variables (an indexed array would go to memory) */
+#define HX_VREGS(k) float4 r##k##0, r##k##1, r##k##2, r##k##3, r##k##4, r##k##5, r##k##6, r##k##7; float rp##k##a, rp##k##b
+#define HX_VLD1(i, k, q) r##k##q = *(const float4 *)row_of(i, q)
+#define HX_VST1(slot, k, q) *(float4 *)&vt[slot][16 * q + rbase][c4] = r##k##q
+#define HX_VLOAD(i, k)                                                                   \
+    do {                                                                                 \
+        HX_VLD1(i, k, 0); HX_VLD1(i, k, 1); HX_VLD1(i, k, 2); HX_VLD1(i, k, 3);          \
+        HX_VLD1(i, k, 4); HX_VLD1(i, k, 5); HX_VLD1(i, k, 6); HX_VLD1(i, k, 7);          \
+        rp##k##a = p_of(i, 0);                                                           \
+        rp##k##b = p_of(i, 1);                                                           \
+    } while (0)
+#define HX_VSTORE(slot, k)                                                               \
+    do {                                                                                 \
+        HX_VST1(slot, k, 0); HX_VST1(slot, k, 1); HX_VST1(slot, k, 2); HX_VST1(slot, k, 3); \
+        HX_VST1(slot, k, 4); HX_VST1(slot, k, 5); HX_VST1(slot, k, 6); HX_VST1(slot, k, 7); \
+        pt[slot][wave][lane] = rp##k##a;                                                 \
+        pt[slot][wave][64 + lane] = rp##k##b;                                            \
+    } while (0)
+    HX_VREGS(0);
+    HX_VREGS(1);
+    HX_VREGS(2);
     float acc = 0.0f;
-    for (int v0 = 0; v0 < nr; v0 += VT) {
-        const int nv = nr - v0 < VT ? nr - v0 : VT;
-        if (tid < nv) slots[tid] = row_slot(a.g, t, v0 + tid);
-        if (lane < nv) pt[wave][lane] = head_live ? p[v0 + lane] : 0.0f;
-        __syncthreads();
-        for (int k = tid; k < nv * 64; k += 256) {
-            const int r = k >> 6, col = k & 63, dd = dc * 64 + col;
-            vt[r][col] = dd < hd ? vbase[(size_t)slots[r] * hd + dd] : 0.0f;
-        }
-        __syncthreads();
-        if (nv == VT) {
-#pragma unroll 16
-            for (int i = 0; i < VT; i++) acc = fadd(acc, fmul(pt[wave][i], vt[i][lane]));
+    auto compute = [&](int i) {
+        const int slot = i % 3, nv = nr - i * VT2;
+        const float *pw = pt[slot][wave], *vw = &vt[slot][0][lane];
+        if (nv >= VT2) {
+            /* 16-row groups in two alternating register sets: the operands of group
+             * k + 1 are read from LDS before the products and adds of group k */
+            float pA[16], vA[16], pB[16], vB[16];
+#define HX_GRD(P_, V_, c_)                                                               \
+            _Pragma("unroll") for (int j = 0; j < 16; j++) { P_[j] = pw[(c_) + j]; V_[j] = vw[((c_) + j) * 64]; }
+#define HX_GSUM(P_, V_)                                                                  \
+            {                                                                            \
+                float pr[16];                                                            \
+                _Pragma("unroll") for (int j = 0; j < 16; j++) pr[j] = fmul(P_[j], V_[j]); \
+                _Pragma("unroll") for (int j = 0; j < 16; j++) acc = fadd(acc, pr[j]);   \
+            }
+            HX_GRD(pA, vA, 0)
+            HX_GRD(pB, vB, 16) HX_GSUM(pA, vA)
+            HX_GRD(pA, vA, 32) HX_GSUM(pB, vB)
+            HX_GRD(pB, vB, 48) HX_GSUM(pA, vA)
+            HX_GRD(pA, vA, 64) HX_GSUM(pB, vB)
+            HX_GRD(pB, vB, 80) HX_GSUM(pA, vA)
+            HX_GRD(pA, vA, 96) HX_GSUM(pB, vB)
+            HX_GRD(pB, vB, 112) HX_GSUM(pA, vA)
+            HX_GSUM(pB, vB)
+#undef HX_GSUM
+#undef HX_GRD
         } else {
-            for (int i = 0; i < nv; i++) acc = fadd(acc, fmul(pt[wave][i], vt[i][lane]));
+            for (int r = 0; r < nv; r++) acc = fadd(acc, fmul(pw[r], vw[r * 64]));
         }
-        __syncthreads();
+    };
+    /* tiles 0 and 1 go straight to slots 0 and 1; register set k holds tile 2 + k */
+    HX_VLOAD(0, 0);
+    HX_VSTORE(0, 0);
+    HX_VLOAD(1, 0);
+    HX_VSTORE(1, 0);
+    HX_VLOAD(2, 0);
+    HX_VLOAD(3, 1);
+    HX_VLOAD(4, 2);
+    __syncthreads();
+    /* step i: sum tile i (slot i % 3), write tile i + 2 (register set (i - i0)) to slot
+     * (i + 2) % 3, which held tile i - 1 (summed before the previous barrier), then
+     * request tile i + 2 + VPF into the freed set. Steps past the last tile add nothing. */
+#define HX_VSTEP(k)                                                                      \
+    do {                                                                                 \
+        const int i_ = i0 + k;                                                           \
+        compute(i_);                                                                     \
+        HX_VSTORE((i_ + 2) % 3, k);                                                      \
+        __syncthreads();                                                                 \
+        HX_VLOAD(i_ + 2 + VPF, k);                                                       \
+    } while (0)
+    for (int i0 = 0; i0 < ntiles; i0 += VPF) {
+        HX_VSTEP(0);
+        HX_VSTEP(1);
+        HX_VSTEP(2);
     }
-    if (head_live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = acc;
+#undef HX_VSTEP
+#undef HX_VSTORE
+#undef HX_VLOAD
+#undef HX_VST1
+#undef HX_VLD1
+#undef HX_VREGS
+    const int d = dc * 64 + lane;
+    if (live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = acc;
+    /* with head_dim % 64 == 0 the wave's 64 outputs are one NUMERICS §2 block of the
+     * token's attention row */
+    if (a.qo_on && live) quant_block_wave(acc, a.qo, t, h * (hd >> 6) + dc);
 }
 
 } // namespace
@@ -157,10 +380,14 @@ namespace hxl {
 void attention(const AttnArgs &a, hipStream_t st) {
     const int max_nr = a.g.pos0 + a.T;   /* depth[t] <= t */
     const int nchunks = (max_nr + SC_ROWS - 1) / SC_ROWS;
-    k_attn_scores<<<nchunks * a.T * a.Hkv, SC_ROWS, 0, st>>>(a);
+    const int grp = a.H / a.Hkv, nsc = nchunks * a.T * a.Hkv;
+    if (grp % 8 == 0) k_attn_scores<8><<<nsc, SC_ROWS, 0, st>>>(a);
+    else if (grp % 4 == 0) k_attn_scores<4><<<nsc, SC_ROWS, 0, st>>>(a);
+    else if (grp % 2 == 0) k_attn_scores<2><<<nsc, SC_ROWS, 0, st>>>(a);
+    else k_attn_scores<1><<<nsc, SC_ROWS, 0, st>>>(a);
     k_attn_softmax<<<a.T * a.H, 256, 0, st>>>(a);
-    const int grp = a.H / a.Hkv, nq = (grp + 3) / 4, nd = (a.hd + 63) / 64;
-    k_attn_values<<<a.T * nq * a.Hkv * nd, 256, 0, st>>>(a);
+    const int nd = (a.hd + 63) / 64, qpt = (grp + 3) / 4;
+    k_attn_values<<<a.T * qpt * a.Hkv * nd, 256, 0, st>>>(a);
 }
 
 } // namespace hxl

@@ -164,69 +164,222 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs args) {
     }
 }
 
-/* ------------------------------------------------------------ grouped expert GEMMs */
+/* ------------------------------------------------------------ split-K products (few tokens) */
 
-/* gate/up of one 64-row F block of one active expert for all its tokens, then
- * mid = silu(g) * u (NUMERICS §4, quant.c:644-649) and its NUMERICS §2 block. */
-__global__ __launch_bounds__(256) void k_expert_gateup(MoeArgs a) {
-    __shared__ float mid[16][64];
-    const int nfb = a.F / 64;
-    const int u = (int)blockIdx.x / nfb, fb = (int)blockIdx.x % nfb;
-    if (u >= *a.n_active) return;
-    const int e = a.ulist[u], p0 = a.u_p0[u], n = a.u_n[u];
-    const ExpertW ew = a.table[e];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
-    const int rt = fb * 4 + wave;
-    const int *ptok = a.pair_tok + p0;
-    for (int t0 = 0; t0 < n; t0 += 16) {
-        float g[1][4], up[1][4];
-        fold_tile<1>(ew.gate, rt, a.x, t0, n, [ptok](int t) { return ptok[t]; }, g);
-        fold_tile<1>(ew.up, rt, a.x, t0, n, [ptok](int t) { return ptok[t]; }, up);
+/* With few tokens a product is bound by how many weight bytes are in flight, not by the
+ * MFMA rate. The split-K kernels give each wave of a workgroup a contiguous range of
+ * block pairs of one 16-row tile and issue all its loads at once; each wave writes the
+ * NUMERICS §3 terms (float)isum_g * (dw_g * dx_g) of its blocks to LDS, and after one
+ * barrier one thread per (row, token) folds the terms of blocks 0, 1, ... in order, so
+ * the result is the one-lane fold bit for bit. */
+constexpr int SK_MAXP = 4;      /* block pairs per wave */
+constexpr int SK_LDS = 65536;   /* bytes of terms per workgroup */
+
+/* Terms of pairs [p0, p1) of row tile rt of the NM matrices ms (same dtype DT and
+ * blocks, one shared activation) for tokens t0 .. t0 + 15 (token t's activation row
+ * is row_of(t); tokens >= n repeat row_of(n - 1)). Term (matrix mi, block g, token c,
+ * row r) goes to P[mi * pstride + (g * ntok + c) * 16 + r] for c < ntok. */
+template <int DT, int NM>
+__device__ __forceinline__ void tile_terms_chunk(const QMat *ms, int rt, const Act &a, int arow, int ntok, int p0,
+                                                 int p1, float *P, int pstride) {
+    const int lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
+    const int npair = ms[0].nbp >> 1, nb = ms[0].nb;
+    v4i raw[NM][SK_MAXP][DT == 4 ? 1 : 2];
+    uint2 sc[NM][SK_MAXP][2];
+    v4i xq[SK_MAXP][2];
+    float dx[SK_MAXP][2];
+    int sx[SK_MAXP][2];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float gv = canon(g[0][i]), uv = canon(up[0][i]);
-            const float sg = fdiv(gv, fadd(1.0f, exp_port_f(-gv)));
-            mid[lr][wave * 16 + 4 * kg + i] = fmul(sg, uv);
+    for (int k = 0; k < SK_MAXP; k++) {
+        const int gp = p0 + k < p1 ? p0 + k : p1 - 1;
+#pragma unroll
+        for (int mi = 0; mi < NM; mi++) {
+            const QMat &m = ms[mi];
+            if (DT == 4) {
+                raw[mi][k][0] = load16(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
+            } else {
+                const uint8_t *base = m.w + ((size_t)rt * m.nbp + 2 * gp) * 1024 + lane * 16;
+                raw[mi][k][0] = load16(base);
+                raw[mi][k][DT == 4 ? 0 : 1] = load16(base + 1024);
+            }
+            const uint16_t *dcol = m.d + rt * 16 + 4 * kg;
+            sc[mi][k][0] = *(const uint2 *)(dcol + (size_t)(2 * gp) * m.rows_pad);
+            sc[mi][k][1] = *(const uint2 *)(dcol + (size_t)(2 * gp + 1) * m.rows_pad);
         }
-        __syncthreads();
-        for (int tt = wave; tt < 16; tt += 4) {
-            if (t0 + tt < n) quant_block_wave(mid[tt][lane], a.mid, p0 + t0 + tt, fb);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const size_t ab = (size_t)arow * a.nbp + 2 * gp + j;
+            xq[k][j] = load16((const uint8_t *)(a.q + ab * 64 + kg * 16));
+            dx[k][j] = a.d[ab];
+            sx[k][j] = DT == 4 ? a.s[ab] : 0;
         }
-        __syncthreads();
     }
-}
-
-/* down projection of one 64-row D block of one active expert for all its tokens. */
-__global__ __launch_bounds__(256) void k_expert_down(MoeArgs a) {
-    const int ndb = (a.D + 63) / 64;
-    const int u = (int)blockIdx.x / ndb, db = (int)blockIdx.x % ndb;
-    if (u >= *a.n_active) return;
-    const int e = a.ulist[u], p0 = a.u_p0[u], n = a.u_n[u];
-    const QMat m = a.table[e].down;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
-    const int rt = db * 4 + wave;
-    if (rt * 16 >= m.rows_pad) return;
-    for (int t0 = 0; t0 < n; t0 += 16) {
-        float acc[1][4];
-        fold_tile<1>(m, rt, a.mid, t0, n, [p0](int t) { return p0 + t; }, acc);
-        const int t = t0 + lr;
-        if (t < n) {
+    const v4i zero = {0, 0, 0, 0};
+    const bool wl = lr < ntok;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int row = rt * 16 + 4 * kg + i;
-                if (row < m.rows) a.Y[(size_t)(p0 + t) * a.D + row] = canon(acc[0][i]);
+    for (int k = 0; k < SK_MAXP; k++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int g = 2 * (p0 + k) + j;
+            if (p0 + k >= p1 || g >= nb) continue;   /* uniform */
+#pragma unroll
+            for (int mi = 0; mi < NM; mi++) {
+                v4i wa;
+                if (DT == 4) {
+                    v4i w0, w1;
+                    unpack_q4(raw[mi][k][0], w0, w1);
+                    wa = j ? w1 : w0;
+                } else {
+                    wa = raw[mi][k][DT == 4 ? 0 : j];
+                }
+                v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, xq[k][j], zero, 0, 0, 0);
+                if (DT == 4) {
+                    const int off = 8 * sx[k][j];   /* sum(nib * q) - 8 sum(q) = sum((nib - 8) q) */
+                    c.x -= off; c.y -= off; c.z -= off; c.w -= off;
+                }
+                const uint2 sw = sc[mi][k][j];
+                const float d = dx[k][j];
+                float4 v;
+                v.x = fmul((float)c.x, fmul(h2f((uint16_t)(sw.x & 0xffff)), d));
+                v.y = fmul((float)c.y, fmul(h2f((uint16_t)(sw.x >> 16)), d));
+                v.z = fmul((float)c.z, fmul(h2f((uint16_t)(sw.y & 0xffff)), d));
+                v.w = fmul((float)c.w, fmul(h2f((uint16_t)(sw.y >> 16)), d));
+                if (wl) *(float4 *)(P + (size_t)mi * pstride + ((size_t)g * ntok + lr) * 16 + 4 * kg) = v;
             }
         }
     }
 }
 
+template <int DT, int NM, typename RowOf>
+__device__ __forceinline__ void tile_terms(const QMat *ms, int rt, const Act &a, int t0, int n, int ntok,
+                                           RowOf row_of, int p0, int p1, float *P, int pstride) {
+    int t = t0 + (threadIdx.x & 15);
+    t = t < n ? t : n - 1;
+    const int arow = row_of(t);
+    for (int pc = p0; pc < p1; pc += SK_MAXP)   /* uniform */
+        tile_terms_chunk<DT, NM>(ms, rt, a, arow, ntok, pc, pc + SK_MAXP < p1 ? pc + SK_MAXP : p1, P, pstride);
+}
+
+/* sum of the terms P[(g * ntok) * 16 + tid] over blocks g = 0 .. nb-1, in order */
+__device__ __forceinline__ float fold_terms(const float *P, int nb, int ntok, int tid) {
+    float acc = 0.0f;
+    const int st = ntok * 16;
+    int g = 0;
+    for (; g + 8 <= nb; g += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = P[(g + u) * st + tid];
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = fadd(acc, v[u]);
+    }
+    for (; g < nb; g++) acc = fadd(acc, P[g * st + tid]);
+    return acc;
+}
+
+/* pair range of wave w of W over npair pairs */
+__device__ __forceinline__ void wave_pairs(int npair, int W, int w, int &p0, int &p1) {
+    const int ppw = (npair + W - 1) / W;
+    p0 = w * ppw;
+    p1 = p0 + ppw < npair ? p0 + ppw : npair;
+}
+
+/* dense product of few tokens: one workgroup per 16-row tile of a segment. */
+template <int DT>
+__global__ __launch_bounds__(512) void k_gemm_sk(GemmArgs args, int ntok) {
+    extern __shared__ float P[];
+    int s = 0;
+    while (s + 1 < args.nseg && (int)blockIdx.x >= args.seg[s + 1].wg0) s++;
+    const GemmSeg &sg = args.seg[s];
+    const int rt = (int)blockIdx.x - sg.wg0;
+    const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    int p0, p1;
+    wave_pairs(sg.m.nbp >> 1, W, wave, p0, p1);
+    for (int t0 = args.t0; t0 < args.T; t0 += ntok) {
+        tile_terms<DT, 1>(&sg.m, rt, args.a, t0, args.T, ntok, [](int t) { return t; }, p0, p1, P, 0);
+        __syncthreads();
+        for (int f = tid; f < ntok * 16; f += blockDim.x) {
+            const int c = f >> 4, row = rt * 16 + (f & 15), t = t0 + c;
+            const float acc = fold_terms(P, sg.m.nb, ntok, f);
+            if (t < args.T && row < sg.m.rows) {
+                float y = canon(acc);
+                if (sg.scale_on) y = canon(fmul(sg.scale, y));
+                sg.Y[(size_t)t * sg.ldy + row] = y;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+/* gate/up of one 16-row F tile of one active expert for its n tokens, then
+ * mid = silu(g) * u (NUMERICS §4, quant.c:644-649) as f32 [pair][F]. */
+template <int DT>
+__global__ __launch_bounds__(512) void k_expert_gateup_sk(MoeArgs a, int ntok) {
+    extern __shared__ float P[];
+    const int ntile = a.F / 16;
+    const int u = (int)blockIdx.x / ntile, rt = (int)blockIdx.x % ntile;
+    const SlotDesc &sd = a.desc[u];
+    const int n = sd.n, p0 = sd.p0;
+    if (n == 0) return;
+    const ExpertW ew = sd.w;
+    if (ew.gate.dtype != DT) return;   /* the launcher runs one instantiation per dtype */
+    const QMat ms[2] = {ew.gate, ew.up};
+    const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    int q0, q1;
+    wave_pairs(ew.gate.nbp >> 1, W, wave, q0, q1);
+    const int pstride = ew.gate.nb * ntok * 16;
+    const int *ptok = a.pair_tok + p0;
+    for (int t0 = 0; t0 < n; t0 += ntok) {
+        tile_terms<DT, 2>(ms, rt, a.x, t0, n, ntok, [ptok](int t) { return ptok[t]; }, q0, q1, P, pstride);
+        __syncthreads();
+        for (int f = tid; f < ntok * 16; f += blockDim.x) {
+            const int c = f >> 4, row = rt * 16 + (f & 15);
+            const float gv = canon(fold_terms(P, ew.gate.nb, ntok, f));
+            const float uv = canon(fold_terms(P + pstride, ew.gate.nb, ntok, f));
+            if (t0 + c < n) {
+                const float sg = fdiv(gv, fadd(1.0f, exp_port_f(-gv)));
+                a.midf[(size_t)(p0 + t0 + c) * a.F + row] = fmul(sg, uv);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+/* down projection of one 16-row D tile of one active expert for its n tokens. */
+template <int DT>
+__global__ __launch_bounds__(512) void k_expert_down_sk(MoeArgs a, int ntok) {
+    extern __shared__ float P[];
+    const int ntile = (a.D + 15) / 16;
+    const int u = (int)blockIdx.x / ntile, rt = (int)blockIdx.x % ntile;
+    const SlotDesc &sd = a.desc[u];
+    const int n = sd.n, p0 = sd.p0;
+    if (n == 0) return;
+    const QMat m = sd.w.down;
+    if (m.dtype != DT) return;
+    const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    int q0, q1;
+    wave_pairs(m.nbp >> 1, W, wave, q0, q1);
+    for (int t0 = 0; t0 < n; t0 += ntok) {
+        tile_terms<DT, 1>(&m, rt, a.mid, t0, n, ntok, [p0](int t) { return p0 + t; }, q0, q1, P, 0);
+        __syncthreads();
+        for (int f = tid; f < ntok * 16; f += blockDim.x) {
+            const int c = f >> 4, row = rt * 16 + (f & 15);
+            const float acc = fold_terms(P, m.nb, ntok, f);
+            if (t0 + c < n && row < m.rows) a.Y[(size_t)(p0 + t0 + c) * a.D + row] = canon(acc);
+        }
+        __syncthreads();
+    }
+}
+
+/* ------------------------------------------------------------ grouped expert GEMMs */
+
 /* ------------------------------------------------------------ float matrices (dot16) */
 
 /* y = dot16(w_r, x_t) (NUMERICS §1/§3; quant.c:352-376): 16 lanes per (row, token),
- * lane j sums elements j, j+16, ... in order, then the 8/4/2/1 tree. */
+ * lane j sums elements j, j+16, ... in order, then the 8/4/2/1 tree. Any shape. */
 template <int WDT>
-__global__ __launch_bounds__(256) void k_fgemv(const void *__restrict__ W, int rows, int cols, const float *__restrict__ X,
-                                              int ldx, int T, float *__restrict__ Y, int ldy) {
+__global__ __launch_bounds__(256) void k_fgemv_any(const void *__restrict__ W, int rows, int cols,
+                                                  const float *__restrict__ X, int ldx, int T, float *__restrict__ Y,
+                                                  int ldy) {
     const int64_t pair = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
     const int j = threadIdx.x & 15;
     const bool live = pair < (int64_t)rows * T;
@@ -245,6 +398,78 @@ __global__ __launch_bounds__(256) void k_fgemv(const void *__restrict__ W, int r
 #pragma unroll
     for (int s = 8; s >= 1; s >>= 1) L = fadd(L, __shfl_down(L, s, 16));
     if (live && j == 0) Y[(size_t)t * ldy + r] = canon(L);
+}
+
+/* The same products for cols % 4 == 0 and ldx % 4 == 0: a workgroup computes 4 rows x 4
+ * tokens; the rows of W and X go to LDS in chunks of 2048 columns, each thread issuing
+ * all its loads of a chunk at once, and the 16 lanes of each (row, token) then run their
+ * sums from LDS (chunk boundaries are multiples of 16, so lane j keeps its elements). */
+constexpr int FG_R = 4, FG_T = 4, FG_CH = 2048;
+constexpr int FG_PER = (FG_R + FG_T) * FG_CH / 4 / 256;   /* float4 loads per thread per chunk */
+
+template <int WDT>
+__device__ __forceinline__ float4 fg_w4(const void *W, size_t idx) {
+    if (WDT == 0) return *(const float4 *)((const float *)W + idx);
+    const uint2 u = *(const uint2 *)((const uint16_t *)W + idx);
+    float4 v;
+    if (WDT == 1) {
+        v.x = h2f((uint16_t)(u.x & 0xffff)); v.y = h2f((uint16_t)(u.x >> 16));
+        v.z = h2f((uint16_t)(u.y & 0xffff)); v.w = h2f((uint16_t)(u.y >> 16));
+    } else {
+        v.x = __uint_as_float(u.x << 16); v.y = __uint_as_float(u.x & 0xffff0000u);
+        v.z = __uint_as_float(u.y << 16); v.w = __uint_as_float(u.y & 0xffff0000u);
+    }
+    return v;
+}
+
+template <int WDT>
+__global__ __launch_bounds__(256) void k_fgemv(const void *__restrict__ W, int rows, int cols,
+                                              const float *__restrict__ X, int ldx, int T, float *__restrict__ Y,
+                                              int ldy) {
+    __shared__ float buf[FG_R + FG_T][FG_CH];
+    const int nrb = (rows + FG_R - 1) / FG_R;
+    const int rb = (int)blockIdx.x % nrb, tb = (int)blockIdx.x / nrb;
+    const int tid = threadIdx.x, pr = tid >> 4, j = tid & 15;
+    const int rr = pr % FG_R, tt = pr / FG_R;
+    const int r = rb * FG_R + rr, t = tb * FG_T + tt;
+    float L = 0.0f;
+    for (int c0 = 0; c0 < cols; c0 += FG_CH) {
+        const int n = cols - c0 < FG_CH ? cols - c0 : FG_CH;
+        if (c0) __syncthreads();
+        float4 v[FG_PER];
+        /* load u: row q = u / 2 of the stage (rows of W first, then rows of X), float4
+         * column tid + 256 (u % 2); columns past the chunk read column 0 and are unused */
+#pragma unroll
+        for (int u = 0; u < FG_PER; u++) {
+            const int q = u >> 1;
+            int c4 = (tid + 256 * (u & 1)) * 4;
+            c4 = c4 < n ? c4 : 0;
+            if (q < FG_R) {
+                const int rq = rb * FG_R + q < rows ? rb * FG_R + q : rows - 1;
+                v[u] = fg_w4<WDT>(W, (size_t)rq * cols + c0 + c4);
+            } else {
+                const int tq = tb * FG_T + (q - FG_R) < T ? tb * FG_T + (q - FG_R) : T - 1;
+                v[u] = *(const float4 *)(X + (size_t)tq * ldx + c0 + c4);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < FG_PER; u++)
+            *(float4 *)&buf[u >> 1][(tid + 256 * (u & 1)) * 4] = v[u];
+        __syncthreads();
+        const float *wr = buf[rr], *xr = buf[FG_R + tt];
+        int i = j;
+        for (; i + 112 < n; i += 128) {
+            float a[8], b[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) { a[u] = wr[i + 16 * u]; b[u] = xr[i + 16 * u]; }
+#pragma unroll
+            for (int u = 0; u < 8; u++) L = fadd(L, fmul(a[u], b[u]));
+        }
+        for (; i < n; i += 16) L = fadd(L, fmul(wr[i], xr[i]));
+    }
+#pragma unroll
+    for (int s = 8; s >= 1; s >>= 1) L = fadd(L, __shfl_down(L, s, 16));
+    if (r < rows && t < T && j == 0) Y[(size_t)t * ldy + r] = canon(L);
 }
 
 } // namespace
@@ -267,7 +492,51 @@ void quant_rows(const float *x, int64_t ldx, int T, int nb, const Act &a, hipStr
     k_quant_rows<<<(int)((waves + 3) / 4), 256, 0, st>>>(x, ldx, T, nb, a);
 }
 
+/* waves per split-K workgroup for npair block pairs */
+static int sk_waves(int npair) {
+    const int w = (npair + SK_MAXP - 1) / SK_MAXP;
+    return w < 1 ? 1 : (w > 8 ? 8 : w);
+}
+
+/* tokens per split-K token tile: the terms of NM matrices of nb blocks fit SK_LDS */
+static int sk_ntok(int T, int NM, int nb) {
+    int n = T < 16 ? T : 16;
+    const int fit = SK_LDS / (NM * nb * 64);
+    n = n < fit ? n : fit;
+    return n < 1 ? 1 : n;
+}
+
+/* few-token dense product: one launch per run of consecutive segments of one dtype */
+static void gemm_sk(const GemmArgs &in, hipStream_t st) {
+    for (int s0 = 0; s0 < in.nseg;) {
+        int s1 = s0 + 1;
+        while (s1 < in.nseg && in.seg[s1].m.dtype == in.seg[s0].m.dtype && in.seg[s1].m.nb == in.seg[s0].m.nb) s1++;
+        GemmArgs g = in;
+        g.nseg = s1 - s0;
+        int wg = 0;
+        for (int s = 0; s < g.nseg; s++) {
+            g.seg[s] = in.seg[s0 + s];
+            g.seg[s].wg0 = wg;
+            wg += g.seg[s].m.rows_pad / 16;
+        }
+        const QMat &m = g.seg[0].m;
+        const int ntok = sk_ntok(in.T, 1, m.nb);
+        const int threads = 64 * sk_waves(m.nbp / 2);
+        const size_t lds = (size_t)m.nb * ntok * 64;
+        if (wg) {
+            if (m.dtype == 4) k_gemm_sk<4><<<wg, threads, lds, st>>>(g, ntok);
+            else k_gemm_sk<3><<<wg, threads, lds, st>>>(g, ntok);
+        }
+        s0 = s1;
+    }
+}
+
 void gemm(const GemmArgs &in, hipStream_t st) {
+    if (in.T <= 16 && in.t0 == 0) {
+        bool ok = true;
+        for (int s = 0; s < in.nseg; s++) ok = ok && (size_t)in.seg[s].m.nb * 64 <= (size_t)SK_LDS;
+        if (ok) { gemm_sk(in, st); return; }
+    }
     GemmArgs g = in;
     int wg = 0;
     for (int s = 0; s < g.nseg; s++) {
@@ -286,21 +555,45 @@ void gemm(const GemmArgs &in, hipStream_t st) {
     }
 }
 
+/* gate/up (split-K, one launch per expert dtype present), then NUMERICS §2 of the
+ * SwiGLU rows of all T * top_k pairs (rows of inactive pairs are never read) */
 void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st) {
-    if (n_slots > 0) k_expert_gateup<<<n_slots * (a.F / 64), 256, 0, st>>>(a);
+    if (n_slots <= 0) return;
+    const int nb = (a.D + 63) / 64, nbp = (nb + 1) & ~1;
+    const int ntok = sk_ntok(a.T, 2, nb);
+    const int threads = 64 * sk_waves(nbp / 2);
+    const size_t lds = (size_t)2 * nb * ntok * 64;
+    const int grid = n_slots * (a.F / 16);
+    if (a.dtype_mask & (1 << 4)) k_expert_gateup_sk<4><<<grid, threads, lds, st>>>(a, ntok);
+    if (a.dtype_mask & (1 << 3)) k_expert_gateup_sk<3><<<grid, threads, lds, st>>>(a, ntok);
+    quant_rows(a.midf, a.F, a.P, a.F / 64, a.mid, st);
 }
 
 void expert_down(const MoeArgs &a, int n_slots, hipStream_t st) {
-    if (n_slots > 0) k_expert_down<<<n_slots * ((a.D + 63) / 64), 256, 0, st>>>(a);
+    if (n_slots <= 0) return;
+    const int nb = (a.F + 63) / 64, nbp = (nb + 1) & ~1;
+    const int ntok = sk_ntok(a.T, 1, nb);
+    const int threads = 64 * sk_waves(nbp / 2);
+    const size_t lds = (size_t)nb * ntok * 64;
+    const int grid = n_slots * ((a.D + 15) / 16);
+    if (a.dtype_mask & (1 << 4)) k_expert_down_sk<4><<<grid, threads, lds, st>>>(a, ntok);
+    if (a.dtype_mask & (1 << 3)) k_expert_down_sk<3><<<grid, threads, lds, st>>>(a, ntok);
 }
 
 void fgemv(int dtype, const void *W, int rows, int cols, const float *X, int ldx, int T, float *Y, int ldy, hipStream_t st) {
+    if (rows <= 0 || T <= 0) return;
+    if (cols % 4 == 0 && ldx % 4 == 0) {
+        const int grid = ((rows + FG_R - 1) / FG_R) * ((T + FG_T - 1) / FG_T);
+        if (dtype == 0) k_fgemv<0><<<grid, 256, 0, st>>>(W, rows, cols, X, ldx, T, Y, ldy);
+        else if (dtype == 1) k_fgemv<1><<<grid, 256, 0, st>>>(W, rows, cols, X, ldx, T, Y, ldy);
+        else k_fgemv<2><<<grid, 256, 0, st>>>(W, rows, cols, X, ldx, T, Y, ldy);
+        return;
+    }
     const int64_t threads = (int64_t)rows * T * 16;
-    if (!threads) return;
     const int blocks = (int)((threads + 255) / 256);
-    if (dtype == 0) k_fgemv<0><<<blocks, 256, 0, st>>>(W, rows, cols, X, ldx, T, Y, ldy);
-    else if (dtype == 1) k_fgemv<1><<<blocks, 256, 0, st>>>(W, rows, cols, X, ldx, T, Y, ldy);
-    else k_fgemv<2><<<blocks, 256, 0, st>>>(W, rows, cols, X, ldx, T, Y, ldy);
+    if (dtype == 0) k_fgemv_any<0><<<blocks, 256, 0, st>>>(W, rows, cols, X, ldx, T, Y, ldy);
+    else if (dtype == 1) k_fgemv_any<1><<<blocks, 256, 0, st>>>(W, rows, cols, X, ldx, T, Y, ldy);
+    else k_fgemv_any<2><<<blocks, 256, 0, st>>>(W, rows, cols, X, ldx, T, Y, ldy);
 }
 
 } // namespace hxl

@@ -49,12 +49,27 @@ __device__ __forceinline__ float deq_elem(const uint8_t *row, int dt, int i) {
 
 /* ------------------------------------------------------------ residual + rmsnorm + quant */
 
-__global__ __launch_bounds__(256) void k_norm(NormArgs a) {
+/* Residual update of token t's hidden row h (mode 0: h = embedding * emb_scale; 1:
+ * h += rs * add; 2: h += rs * (sum_j w_j * Y[pair_j] (+ add)), j in rank order,
+ * model.c:904-923), then rmsnorm (quant.c:626-632: ms = sum16(h^2)/D, r = 1/sqrt(ms +
+ * eps), x = (h * r) * w) and NUMERICS §2 of x. One workgroup per token; every load of
+ * the residual step is issued before any of its sums. */
+__global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
     extern __shared__ float hs[];
+    __shared__ float wk[64];
+    __shared__ int pk[64];
     __shared__ float r_sh;
-    const int t = blockIdx.x, D = a.D, tid = threadIdx.x;
+    const int t = blockIdx.x, D = a.D, tid = threadIdx.x, nth = blockDim.x, K = a.K;
     float *h = a.h + (size_t)t * D;
-    for (int i = tid; i < D; i += 256) {
+    if (a.mode == 2) {
+        if (tid < K) {
+            wk[tid] = a.wts[(size_t)t * K + tid];
+            pk[tid] = a.pair_of[(size_t)t * K + tid];
+        }
+        __syncthreads();
+    }
+#pragma unroll 2
+    for (int i = tid; i < D; i += nth) {
         float v;
         if (a.mode == 0) {
             const uint8_t *row = a.emb + (size_t)a.tokens[t] * a.emb_rb;
@@ -63,9 +78,16 @@ __global__ __launch_bounds__(256) void k_norm(NormArgs a) {
             v = fadd(h[i], fmul(a.rs, a.add[(size_t)t * D + i]));
         } else {
             float out = 0.0f;
-            for (int j = 0; j < a.K; j++) {
-                const float w = a.wts[(size_t)t * a.K + j];
-                out = fadd(out, fmul(w, a.Y[(size_t)a.pair_of[(size_t)t * a.K + j] * D + i]));
+            for (int j0 = 0; j0 < K; j0 += 8) {
+                float yv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int j = j0 + u < K ? j0 + u : K - 1;
+                    yv[u] = a.Y[(size_t)pk[j] * D + i];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (j0 + u < K) out = fadd(out, fmul(wk[j0 + u], yv[u]));
             }
             if (a.add) out = fadd(out, a.add[(size_t)t * D + i]);
             v = fadd(h[i], fmul(a.rs, out));
@@ -76,7 +98,15 @@ __global__ __launch_bounds__(256) void k_norm(NormArgs a) {
     __syncthreads();
     if (tid < 16) {
         float L = 0.0f;
-        for (int i = tid; i < D; i += 16) L = fadd(L, fmul(hs[i], hs[i]));
+        int i = tid;
+        for (; i + 112 < D; i += 128) {
+            float e[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) e[u] = hs[i + 16 * u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) L = fadd(L, fmul(e[u], e[u]));
+        }
+        for (; i < D; i += 16) L = fadd(L, fmul(hs[i], hs[i]));
         L = tree16(L);
         if (tid == 0) {
             const float ms = fdiv(L, (float)D);
@@ -85,8 +115,8 @@ __global__ __launch_bounds__(256) void k_norm(NormArgs a) {
     }
     __syncthreads();
     const float r = r_sh;
-    const int wave = tid >> 6, lane = tid & 63;
-    for (int g = wave; g < a.a.nbp; g += 4) {
+    const int wave = tid >> 6, lane = tid & 63, nw = nth >> 6;
+    for (int g = wave; g < a.a.nbp; g += nw) {
         const int i = g * 64 + lane;
         const float xv = i < D ? fmul(fmul(hs[i], r), a.norm_w[i]) : 0.0f;
         if (a.x && i < D) a.x[(size_t)t * D + i] = xv;
@@ -234,47 +264,236 @@ __global__ __launch_bounds__(64) void k_route_tokens(RouteArgs a) {
     }
 }
 
-/* Union of the chosen experts in ascending id, pairs grouped by expert with tokens
- * ascending (model.c:1020-1037); one workgroup. */
-__global__ __launch_bounds__(256) void k_route_bucket(RouteArgs a) {
-    __shared__ int cnt[ROUTE_EMAX], base[ROUTE_EMAX], slot[ROUTE_EMAX];
-    __shared__ int tot;
-    const int tid = threadIdx.x, E = a.E, P = a.T * a.K;
-    for (int e = tid; e < E; e += 256) cnt[e] = 0;
-    __syncthreads();
-    for (int p = tid; p < P; p += 256) atomicAdd(&cnt[a.ids[p]], 1);
-    __syncthreads();
-    if (tid == 0) {
-        int pos = 0, nu = 0;
-        for (int e = 0; e < E; e++) {
-            base[e] = pos;
-            slot[e] = cnt[e] ? nu : -1;
-            if (cnt[e]) {
-                a.ulist[nu] = e;
-                a.u_p0[nu] = pos;
-                a.u_n[nu] = cnt[e];
-                nu++;
-            }
-            pos += cnt[e];
+/* Selection key of (value v, expert e): a larger key ranks first, and the order is
+ * ranks_before's: larger value first (-0 equals +0), NaN after every number, ties to
+ * the lower index. */
+__device__ __forceinline__ unsigned long long rank_key(float v, int e) {
+    uint32_t k;
+    if (v != v) {
+        k = 0u;
+    } else {
+        const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+        k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    }
+    return ((unsigned long long)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+/* Ungrouped routing (n_group <= 1), one workgroup per token: scores, selection values,
+ * then each expert's rank = the number of experts that rank before it; the K experts of
+ * rank < K are the reference's K rounds of best-remaining (route_select, model.c:793-843)
+ * in the same order. Weights as in k_route_tokens. */
+__global__ __launch_bounds__(256) void k_route_rank(RouteArgs a) {
+    __shared__ float score[ROUTE_EMAX];
+    __shared__ unsigned long long key[ROUTE_EMAX];
+    __shared__ int chosen[64];
+    __shared__ float red[4];
+    __shared__ float sum_sh;
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.E, K = a.K;
+    const float *lg = a.logits + (size_t)t * E;
+    if (a.score_fn == 0) {
+        /* softmax (quant.c:634-642): m = running max from x[0] (a NaN x[0] makes m NaN) */
+        float m = -__builtin_huge_valf();
+        for (int e = tid; e < E; e += 256) {
+            const float x = lg[e];
+            score[e] = x;
+            if (x == x) m = fmaxf(m, x);
         }
-        tot = nu;
-        *a.n_active = nu;
-        if (a.stats) {
-            a.stats[0] += (unsigned long long)P;
-            a.stats[1] += (unsigned long long)nu;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        if (lane == 0) red[wave] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        if (score[0] != score[0]) m = score[0];
+        for (int e = tid; e < E; e += 256) score[e] = exp_port_f(fadd(score[e], -m));
+        __syncthreads();
+        if (tid < 16) {
+            float L = 0.0f;
+            for (int e = tid; e < E; e += 16) L = fadd(L, score[e]);
+            L = tree16(L);
+            if (tid == 0) sum_sh = L;
+        }
+        __syncthreads();
+        const float sum = sum_sh;
+        for (int e = tid; e < E; e += 256) score[e] = fdiv(score[e], sum);
+    } else {
+        for (int e = tid; e < E; e += 256) score[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) key[e] = rank_key(a.bias ? fadd(score[e], a.bias[e]) : score[e], e);
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) {
+        const unsigned long long ke = key[e];
+        int rank = 0;
+        int o = 0;
+        for (; o + 4 <= E; o += 4) {
+            const unsigned long long k0 = key[o], k1 = key[o + 1], k2 = key[o + 2], k3 = key[o + 3];
+            rank += (k0 > ke) + (k1 > ke) + (k2 > ke) + (k3 > ke);
+        }
+        for (; o < E; o++) rank += key[o] > ke;
+        if (rank < K) chosen[rank] = e;
+    }
+    __syncthreads();
+    /* weights: w_j = score[id_j]; norm_topk: w_j / (sum_j w_j + 1e-20f), sum in rank order */
+    if (tid < K) {
+        const int id = chosen[tid];
+        float w = score[id];
+        if (a.norm_topk) {
+            float s = 0.0f;
+            for (int j = 0; j < K; j++) s = fadd(s, score[chosen[j]]);
+            w = fdiv(w, fadd(s, 1e-20f));
+        }
+        w = fmul(w, a.routed_scale);
+        a.ids[(size_t)t * K + tid] = id;
+        a.wts[(size_t)t * K + tid] = w;
+        if (a.route_out) a.route_out[((size_t)t * a.n_moe + a.moe_ord) * K + tid] = id;
+    }
+}
+
+/* Union of the chosen experts in ascending id, pairs grouped by expert with tokens
+ * ascending (model.c:1020-1037), by the nth threads of one workgroup. ids: the T*K
+ * chosen experts (LDS or global); cnt/base: LDS scratch of E ints. Writes the pair
+ * lists, the active-slot lists and the slot descriptors (unused slots get n = 0). */
+__device__ void bucket_pairs(const RouteArgs &a, const int *ids, int *cnt, int *base, int tid, int nth) {
+    const int E = a.E, P = a.T * a.K;
+    for (int e = tid; e < E; e += nth) cnt[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += nth) atomicAdd(&cnt[ids[p]], 1);
+    __syncthreads();
+    __shared__ int nu_sh;
+    if (tid < 64) {
+        /* exclusive scan of cnt over experts by one wave, 64 experts per round */
+        int run = 0, nu_run = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + tid;
+            const int c = e < E ? cnt[e] : 0, act = c > 0;
+            int inc = c, ninc = act;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int y = __shfl_up(inc, off, 64), ny = __shfl_up(ninc, off, 64);
+                if (tid >= off) { inc += y; ninc += ny; }
+            }
+            const int pos = run + inc - c, slot = nu_run + ninc - act;
+            if (e < E) {
+                base[e] = pos;
+                if (act) {
+                    a.ulist[slot] = e;
+                    a.u_p0[slot] = pos;
+                    a.u_n[slot] = c;
+                    SlotDesc d;
+                    d.w = a.table[e];
+                    d.p0 = pos;
+                    d.n = c;
+                    d.e = e;
+                    d.pad = 0;
+                    a.desc[slot] = d;
+                }
+            }
+            run += __shfl(inc, 63, 64);
+            nu_run += __shfl(ninc, 63, 64);
+        }
+        if (tid == 0) {
+            nu_sh = nu_run;
+            *a.n_active = nu_run;
+            if (a.stats) {
+                a.stats[0] += (unsigned long long)P;
+                a.stats[1] += (unsigned long long)nu_run;
+            }
         }
     }
     __syncthreads();
-    for (int e = tid; e < E; e += 256) {
+    for (int u = nu_sh + tid; u < a.n_slots; u += nth) a.desc[u].n = 0;
+    for (int e = tid; e < E; e += nth) {
         if (!cnt[e]) continue;
         int pos = base[e];
         for (int p = 0; p < P; p++)
-            if (a.ids[p] == e) {
+            if (ids[p] == e) {
                 a.pair_tok[pos] = p / a.K;
                 a.pair_of[p] = pos;
                 pos++;
             }
     }
+}
+
+constexpr int BUCKET_PMAX = 8192;
+
+/* bucketing of a routed batch by one workgroup (the pair list staged in LDS when it fits) */
+__global__ __launch_bounds__(1024) void k_route_bucket(RouteArgs a) {
+    __shared__ int cnt[ROUTE_EMAX], base[ROUTE_EMAX];
+    __shared__ int pid[BUCKET_PMAX];
+    const int tid = threadIdx.x, nth = blockDim.x, P = a.T * a.K;
+    const bool in_lds = P <= BUCKET_PMAX;
+    if (in_lds)
+        for (int p = tid; p < P; p += nth) pid[p] = a.ids[p];
+    __syncthreads();
+    bucket_pairs(a, in_lds ? pid : a.ids, cnt, base, tid, nth);
+}
+
+/* Ungrouped routing of up to 16 tokens (E <= 256) and their bucketing in one workgroup:
+ * wave t routes token t exactly as k_route_rank does, then all threads bucket. */
+constexpr int RS_TMAX = 16, RS_EMAX = 256;
+
+__global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
+    __shared__ float score[RS_TMAX][RS_EMAX];
+    __shared__ unsigned long long key[RS_TMAX][RS_EMAX];
+    __shared__ int chosen[RS_TMAX][64];
+    __shared__ int pid[RS_TMAX * 64];
+    __shared__ int cnt[RS_EMAX], base[RS_EMAX];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, E = a.E, K = a.K, t = wave;
+    if (t < a.T) {
+        float *sc = score[t];
+        const float *lg = a.logits + (size_t)t * E;
+        if (a.score_fn == 0) {
+            /* softmax (quant.c:634-642): m = running max from x[0] (a NaN x[0] makes m NaN) */
+            float m = -__builtin_huge_valf();
+            for (int e = lane; e < E; e += 64) {
+                const float x = lg[e];
+                sc[e] = x;
+                if (x == x) m = fmaxf(m, x);
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+            wave_sync();
+            if (sc[0] != sc[0]) m = sc[0];
+            for (int e = lane; e < E; e += 64) sc[e] = exp_port_f(fadd(sc[e], -m));
+            wave_sync();
+            float L = 0.0f;
+            if (lane < 16)
+                for (int e = lane; e < E; e += 16) L = fadd(L, sc[e]);
+            L = tree16(L);
+            const float sum = __shfl(L, 0, 64);
+            for (int e = lane; e < E; e += 64) sc[e] = fdiv(sc[e], sum);
+        } else {
+            for (int e = lane; e < E; e += 64) sc[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
+        }
+        wave_sync();
+        for (int e = lane; e < E; e += 64) key[t][e] = rank_key(a.bias ? fadd(sc[e], a.bias[e]) : sc[e], e);
+        wave_sync();
+        for (int e = lane; e < E; e += 64) {
+            const unsigned long long ke = key[t][e];
+            int rank = 0, o = 0;
+            for (; o + 4 <= E; o += 4)
+                rank += (key[t][o] > ke) + (key[t][o + 1] > ke) + (key[t][o + 2] > ke) + (key[t][o + 3] > ke);
+            for (; o < E; o++) rank += key[t][o] > ke;
+            if (rank < K) chosen[t][rank] = e;
+        }
+        wave_sync();
+        if (lane < K) {
+            const int id = chosen[t][lane];
+            float w = sc[id];
+            if (a.norm_topk) {
+                float s = 0.0f;
+                for (int j = 0; j < K; j++) s = fadd(s, sc[chosen[t][j]]);
+                w = fdiv(w, fadd(s, 1e-20f));
+            }
+            w = fmul(w, a.routed_scale);
+            a.ids[(size_t)t * K + lane] = id;
+            a.wts[(size_t)t * K + lane] = w;
+            pid[t * K + lane] = id;
+            if (a.route_out) a.route_out[((size_t)t * a.n_moe + a.moe_ord) * K + lane] = id;
+        }
+    }
+    __syncthreads();
+    bucket_pairs(a, pid, cnt, base, tid, blockDim.x);
 }
 
 /* ------------------------------------------------------------ GQA post-processing */
@@ -425,12 +644,19 @@ __global__ void k_accept_walk(AcceptArgs a) {
 namespace hxl {
 
 void route(const RouteArgs &a, hipStream_t st) {
-    k_route_tokens<<<a.T, 64, 0, st>>>(a);
-    k_route_bucket<<<1, 256, 0, st>>>(a);
+    if (a.n_group <= 1 && a.T <= RS_TMAX && a.E <= RS_EMAX && a.K <= 64) {
+        k_route_small<<<1, 1024, 0, st>>>(a);
+        return;
+    }
+    if (a.n_group > 1) k_route_tokens<<<a.T, 64, 0, st>>>(a);
+    else k_route_rank<<<a.T, 256, 0, st>>>(a);
+    k_route_bucket<<<1, 1024, 0, st>>>(a);
 }
 
 void norm(const NormArgs &a, hipStream_t st) {
-    k_norm<<<a.T, 256, (size_t)a.D * sizeof(float), st>>>(a);
+    int nth = ((a.D / 2 + 63) / 64) * 64;
+    nth = nth < 64 ? 64 : (nth > 1024 ? 1024 : nth);
+    k_norm<<<a.T, nth, (size_t)a.D * sizeof(float), st>>>(a);
 }
 
 void swiglu_quant(float *g, const float *u, int T, int F, const Act &a, hipStream_t st) {
