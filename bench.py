@@ -16,12 +16,13 @@ acceptance on the GPU, commit; generate.py:365-392 of the reference):
 value = accepted tokens / s = sum over steps of (accepted drafts + 1) / wall time of the
 steps (inputs already resident in HBM; each step returns its result to the host).
 
-The roofline fields come from a second, profiled pass over the same steps (HIP events
-around every launch group on the engine's stream): the dominant kernel class is the
-grouped Q4 expert GEMM; its algorithmic bytes are the distinct experts each step's
-routing touched times the slab bytes (2,506,752 per expert). cpu_baseline times the
-reference engine itself (compiled from its C sources into oracle/_ref) on the host
-cores on a bounded sample of the same workload.
+roofline: the grouped Q4 expert gate/up kernel (k_expert_gateup_sk), timed with HIP
+event pairs recorded on the engine's stream around each of its launches during the
+timed steps; achieved = its algorithmic bytes (distinct experts routed in the layer x
+1,671,168 B of Q4 gate+up rows each) / its summed launch durations. A second pass over
+the same steps with events around every launch group gives the per-phase GPU time
+split. cpu_baseline times the reference engine itself (compiled from its C sources into
+oracle/_ref) on up to 16 host cores on a bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -45,6 +46,21 @@ METRIC = "accepted tok/s, Qwen3-30B-A3B-shape verify k=8 (1 GPU); Q4 MoE HBM GB/
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+TRAFFIC_PROFILE = ROOT / "profiles" / "k_expert_gateup_sk_verify_k8_ctx4096_traffic.md"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel from its committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def model_path(layers: int, ctx: int, k: int) -> Path:
@@ -137,6 +153,62 @@ def cpu_baseline(path: Path, prompt, noisy, cont, k: int, steps: int, threads: i
                        f"(prefill {prefill_s:.1f}s untimed); {sum(secs) / steps * 1e3:.1f} ms/step")
 
 
+def summarize_trace(path: str, nsteps: int) -> int:
+    """Per-verify-step kernel table from a rocprofv3 --kernel-trace CSV (run_kernel_trace.csv):
+    a step is the dispatches after one k_accept_walk up to and including the next; the
+    last nsteps steps are averaged."""
+    import collections
+    import csv
+    import re
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    ends = [i for i, r in enumerate(rows) if "k_accept_walk" in r["Kernel_Name"]]
+    steps = [rows[a + 1:b + 1] for a, b in zip(ends[:-1], ends[1:])][-nsteps:]
+    if not steps:
+        print("no verify steps in the trace")
+        return 1
+    tot, cnt = collections.defaultdict(float), collections.Counter()
+    wall = busy = 0.0
+    for s in steps:
+        wall += (int(s[-1]["End_Timestamp"]) - int(s[0]["Start_Timestamp"])) / 1e3
+        for r in s:
+            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            name = re.sub(r"\(.*", "", r["Kernel_Name"].replace("(anonymous namespace)::", ""))
+            tot[name] += d
+            cnt[name] += 1
+            busy += d
+    n = len(steps)
+    print(f"{n} verify steps: first dispatch to last end {wall / n:.1f} us/step, kernel time {busy / n:.1f} us/step")
+    print(f"{'kernel':34s} {'us/step':>10s} {'calls/step':>10s} {'avg us':>9s}")
+    for k, v in sorted(tot.items(), key=lambda x: -x[1]):
+        print(f"{k:34s} {v / n:10.1f} {cnt[k] / n:10.1f} {v / cnt[k]:9.2f}")
+    return 0
+
+
+def calibrate_copy(mib: int) -> int:
+    """Device-to-device copies of a known size through the HIP runtime (the copy kernel
+    reads and writes mib MiB per dispatch), to scale FETCH_SIZE / WRITE_SIZE counters."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = mib << 20
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    for p in (src, dst):
+        if hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(n)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    try:
+        if hip.hipMemset(src, 1, ctypes.c_size_t(n)) != 0:
+            raise RuntimeError("hipMemset failed")
+        for _ in range(3):
+            if hip.hipMemcpy(dst, src, ctypes.c_size_t(n), 3) != 0:   # hipMemcpyDeviceToDevice
+                raise RuntimeError("hipMemcpy failed")
+        if hip.hipDeviceSynchronize() != 0:
+            raise RuntimeError("hipDeviceSynchronize failed")
+    finally:
+        hip.hipFree(src)
+        hip.hipFree(dst)
+    print(f"copied {mib} MiB device to device 3 times")
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="speculative-verify throughput on one MI355X")
     ap.add_argument("--gpus", type=int, default=1)
@@ -147,7 +219,15 @@ def main(argv=None) -> int:
     ap.add_argument("--k", type=int, default=8)
     ap.add_argument("--cpu-steps", type=int, default=6)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print the per-verify-step kernel table of a rocprofv3 kernel trace and exit")
+    ap.add_argument("--calibrate-copy", metavar="MIB", type=int,
+                    help="only run device-to-device copies of MIB MiB (counter calibration) and exit")
     a = ap.parse_args(argv)
+    if a.summarize_trace:
+        return summarize_trace(a.summarize_trace, 10)
+    if a.calibrate_copy:
+        return calibrate_copy(a.calibrate_copy)
     if a.gpus != 1:
         print(f"bench.py runs on exactly one GPU: this build has no multi-GPU path (asked for {a.gpus})",
               file=sys.stderr)
@@ -175,41 +255,45 @@ def main(argv=None) -> int:
     log(f"[bench] greedy continuation of {need} tokens {time.time() - t:.1f}s")
     eng.rewind(base)
     noisy = make_drafts(cont, seed=99)
-    # warmup + timed
+    # warmup, then the timed steps (no instrumentation)
     run_steps(eng, cont, noisy, base, a.k, a.warmup)
-    eng.rewind(base)
+    eng.rewind(base)      # the timed steps re-verify from the same position
     eng.reset_stats()
-    toks, secs = run_steps(eng, cont, noisy, base, a.k, a.warmup + a.steps)
-    toks, secs = toks[a.warmup:], secs[a.warmup:]
+    toks, secs = run_steps(eng, cont, noisy, base, a.k, a.steps)
     st = eng.stats()
     value = sum(toks) / sum(secs)
     ms = sorted(s * 1e3 for s in secs)
     log(f"[bench] {a.steps} steps: {value:.1f} tok/s, {sum(toks) / a.steps:.2f} tok/step, "
         f"p50 {statistics.median(ms):.3f} ms")
-    # profiled pass over the same steps
+    # the same steps again with HIP event pairs around the grouped expert launches only:
+    # the roofline kernel's launch durations
     eng.rewind(base)
-    eng.set_profiling(True)
+    eng.set_profiling(1)
     eng.reset_kstats()
-    eng.reset_stats()
-    ptoks, psecs = run_steps(eng, cont, noisy, base, a.k, a.warmup + a.steps)
+    _, secs_ev = run_steps(eng, cont, noisy, base, a.k, a.steps)
+    kx = eng.kstats()
+    eng.set_profiling(0)
+    # a second pass over the same steps with events around every launch group: the
+    # per-phase split (reported, not used for value or roofline)
+    eng.rewind(base)
+    eng.set_profiling(2)
+    eng.reset_kstats()
+    run_steps(eng, cont, noisy, base, a.k, a.steps)
     ks = eng.kstats()
-    pst = eng.stats()
-    eng.set_profiling(False)
-    n_prof = a.warmup + a.steps
-    expert_gbs = ks["expert_bytes"] / ks["expert_s"] / 1e9 if ks["expert_s"] > 0 else 0.0
-    L, D, V = a.layers, 2048, 151936
-    dense_bytes_step = L * (4096 * 2112 + 2 * 512 * 2112 + 2048 * 4224) + V * 2112
-    dense_gbs = dense_bytes_step * n_prof / (ks["attn_s"] + ks["head_s"]) / 1e9 if ks["attn_s"] > 0 else 0.0
-    per_launch_bytes = ks["expert_bytes"] / max(1, ks["expert_launches"])
-    per_launch_s = ks["expert_s"] / max(1, ks["expert_launches"])
+    eng.set_profiling(0)
+    n_launch = max(1, kx["expert_launches"])
+    gu_gbs = kx["expert_bytes"] / kx["expert_s"] / 1e9 if kx["expert_s"] > 0 else 0.0
+    dn_gbs = kx["expert_down_bytes"] / kx["expert_down_s"] / 1e9 if kx["expert_down_s"] > 0 else 0.0
     eng.close()
     cpu = None
     if not a.no_cpu:
         try:
-            cpu = cpu_baseline(path, prompt[:-1], noisy, cont, a.k, a.cpu_steps, threads=os.cpu_count() or 1)
+            cpu = cpu_baseline(path, prompt[:-1], noisy, cont, a.k, a.cpu_steps,
+                               threads=min(16, os.cpu_count() or 1))
         except Exception as ex:   # the baseline is reported, never required
             log(f"[bench] cpu baseline failed: {ex}")
-    gpu_total = sum(ks[x] for x in ("attn_s", "router_s", "expert_s", "norm_s", "head_s", "dense_s"))
+    phases = ("attn_s", "router_s", "expert_s", "expert_down_s", "norm_s", "head_s", "dense_s")
+    gpu_total = sum(ks[x] for x in phases)
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(sum(secs) / a.steps * 1e3, 4), "higher_is_better": True,
@@ -218,14 +302,17 @@ def main(argv=None) -> int:
                                f"drafts = greedy continuation with 30% random replacement", "layers": a.layers,
                    "ctx": a.ctx, "k": a.k, "tokens_per_step": round(sum(toks) / a.steps, 3),
                    "step_ms_p50": round(statistics.median(ms), 4), "step_ms_p90": round(ms[int(0.9 * (len(ms) - 1))], 4),
-                   "expert_loads_per_step": round(st["expert_loads_unique"] / a.steps, 1)},
-        "roofline": {"bound": "hbm", "achieved": round(expert_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(expert_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "grouped Q4 expert GEMM (gate/up + down)",
-                     "bytes_per_launch": int(per_launch_bytes), "s_per_launch": per_launch_s},
-        "gpu_time_split": {k: round(ks[k] / n_prof * 1e3, 4) for k in ("attn_s", "router_s", "expert_s", "norm_s", "head_s")}
-                          | {"sum_ms": round(gpu_total / n_prof * 1e3, 4),
-                             "dense_matvec_gbs": round(dense_gbs, 1)},
+                   "expert_loads_per_step": round(st["expert_loads_unique"] / a.steps, 1),
+                   "ms_per_step_with_expert_events": round(sum(secs_ev) / a.steps * 1e3, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": str(TRAFFIC_PROFILE.relative_to(ROOT)),
+                     "kernel": "k_expert_gateup_sk<4> (grouped Q4 expert gate+up)",
+                     "bytes_per_launch": int(kx["expert_bytes"] / n_launch),
+                     "us_per_launch": round(kx["expert_s"] / n_launch * 1e6, 3),
+                     "down_projection_gbs": round(dn_gbs, 1)},
+        "gpu_time_split_ms_per_step": {k: round(ks[k] / a.steps * 1e3, 4) for k in phases}
+                                      | {"sum": round(gpu_total / a.steps * 1e3, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

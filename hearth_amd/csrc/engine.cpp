@@ -94,6 +94,7 @@ struct Layer {
     const float *router_bias = nullptr;
     ExpertW *experts = nullptr;     /* device table [E] */
     uint64_t expert_bytes_each = 0; /* algorithmic bytes of one expert (gate+up+down) */
+    uint64_t expert_gateup_bytes = 0; /* of which gate + up */
     int dtype_mask = 0;             /* bit dt set when some expert has dtype dt */
 };
 
@@ -151,13 +152,14 @@ struct hearth_engine {
     /* telemetry */
     uint64_t tokens_done = 0, forward_calls = 0;
     double wall_s = 0.0;
-    bool profiling = false;
+    int profiling = 0;   /* 0 off, 1 expert launches, 2 every launch group */
     hearth_gpu_kstats ks{};
     struct Ev { hipEvent_t a, b; double *acc; };
     std::vector<Ev> pending_ev;
     std::vector<hipEvent_t> ev_pool;
     size_t ev_next = 0;
     unsigned long long stats_base[2] = {0, 0};
+    unsigned long long ks_base = 0;   /* distinct-expert loads counter at hearth_gpu_reset_kstats */
     /* routing trace / replay */
     FILE *trace = nullptr;
     std::vector<int> h_routes;
@@ -218,12 +220,20 @@ struct hearth_engine {
         }
         return ev_pool[ev_next++];
     }
-    template <class Fn> void timed(double *acc, Fn fn) {
-        if (!profiling) { fn(); return; }
+    template <class Fn> void timed(double *acc, Fn fn, int level = 2) {
+        if (profiling < level) { fn(); return; }
         hipEvent_t a = next_event(), b = next_event();
         ck(hipEventRecord(a, st));
         fn();
         ck(hipEventRecord(b, st));
+        pending_ev.push_back({a, b, acc});
+    }
+    /* the same, with the events handed to the launch so that the dispatch records them
+     * (kernel start and end, no enqueue gaps) */
+    template <class Fn> void timed_dispatch(double *acc, Fn fn, int level) {
+        if (profiling < level) { fn(nullptr, nullptr); return; }
+        hipEvent_t a = next_event(), b = next_event();
+        fn(a, b);
         pending_ev.push_back({a, b, acc});
     }
     void collect_events() {
@@ -395,6 +405,7 @@ bool hearth_engine::upload(std::string &msg) {
             up.quant(table[e].up, slab + ou);
             up.quant(table[e].down, slab + od);
             w.expert_bytes_each = 2 * (uint64_t)F * row_bytes(dt, D) + (uint64_t)D * row_bytes(dt, F);
+            w.expert_gateup_bytes = 2 * (uint64_t)F * row_bytes(dt, D);
             w.dtype_mask |= 1 << dt;
         }
         w.experts = (ExpertW *)dalloc(sizeof(ExpertW) * (size_t)E);
@@ -601,15 +612,15 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             });
             dump("router", l, lge, T, E);
             dump("ids", l, ids, T, K);
-            timed(&ks.expert_s, [&] {
+            {
                 hxd::MoeArgs m{};
                 m.table = w.experts; m.desc = slot_desc; m.n_active = n_active; m.ulist = ulist; m.u_p0 = u_p0; m.u_n = u_n;
                 m.pair_tok = pair_tok; m.x = ax; m.mid = amid; m.midf = midf; m.Y = Y; m.T = T; m.F = F; m.D = D;
                 m.P = T * K; m.dtype_mask = w.dtype_mask;
                 const int slots = std::min(E, T * K);
-                hxl::expert_gateup(m, slots, st);
-                hxl::expert_down(m, slots, st);
-            });
+                timed_dispatch(&ks.expert_s, [&](hipEvent_t e0, hipEvent_t e1) { hxl::expert_gateup(m, slots, st, e0, e1); }, 1);
+                timed(&ks.expert_down_s, [&] { hxl::expert_down(m, slots, st); }, 1);
+            }
             if (profiling) ks.expert_launches++;
             timed(&ks.norm_s, [&] {
                 hxd::NormArgs n{};
@@ -1069,7 +1080,7 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
 
 HEARTH_API int hearth_gpu_set_profiling(hearth_engine *e, int on) {
     if (!e) return E_ARG;
-    e->profiling = on != 0;
+    e->profiling = on < 0 ? 0 : (on > 2 ? 2 : on);
     return OK;
 }
 
@@ -1079,15 +1090,21 @@ HEARTH_API int hearth_gpu_get_kstats(hearth_engine *e, hearth_gpu_kstats *out) {
     unsigned long long d[2] = {0, 0};
     if (hipSetDevice(e->dev) == hipSuccess && hipStreamSynchronize(e->st) == hipSuccess)
         (void)hipMemcpy(d, e->dstats, sizeof d, hipMemcpyDeviceToHost);
-    uint64_t per = 0;
+    uint64_t per_gu = 0, per_dn = 0;
     for (const Layer &l : e->layers)
-        if (l.moe) { per = l.expert_bytes_each; break; }
-    out->expert_bytes = (d[1] - e->stats_base[1]) * per;
+        if (l.moe) { per_gu = l.expert_gateup_bytes; per_dn = l.expert_bytes_each - l.expert_gateup_bytes; break; }
+    out->expert_bytes = (d[1] - e->ks_base) * per_gu;
+    out->expert_down_bytes = (d[1] - e->ks_base) * per_dn;
     return OK;
 }
 
 HEARTH_API void hearth_gpu_reset_kstats(hearth_engine *e) {
-    if (e) e->ks = hearth_gpu_kstats{};
+    if (!e) return;
+    e->ks = hearth_gpu_kstats{};
+    unsigned long long d[2] = {0, 0};
+    if (hipSetDevice(e->dev) == hipSuccess && hipStreamSynchronize(e->st) == hipSuccess)
+        (void)hipMemcpy(d, e->dstats, sizeof d, hipMemcpyDeviceToHost);
+    e->ks_base = d[1];
 }
 
 HEARTH_API int hearth_gpu_device(char *name, size_t n) {

@@ -144,7 +144,7 @@ using namespace hxd;
 void repack(const uint8_t *src_dev, int r0, int count, const QMat &m, hipStream_t st);
 void quant_rows(const float *x, int64_t ldx, int T, int nb, const Act &a, hipStream_t st);
 void gemm(const GemmArgs &a, hipStream_t st);
-void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st);
+void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 void expert_down(const MoeArgs &a, int n_slots, hipStream_t st);
 void fgemv(int dtype, const void *W, int rows, int cols, const float *X, int ldx, int T, float *Y, int ldy, hipStream_t st);
 void route(const RouteArgs &a, hipStream_t st);

@@ -11,6 +11,7 @@
  */
 #include "hx_device.h"
 #include "hx_launch.h"
+#include <hip/hip_ext.h>
 
 using namespace hxd;
 
@@ -555,22 +556,27 @@ void gemm(const GemmArgs &in, hipStream_t st) {
     }
 }
 
-/* gate/up (split-K, one launch per expert dtype present), then NUMERICS §2 of the
- * SwiGLU rows of all T * top_k pairs (rows of inactive pairs are never read) */
-void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st) {
+/* gate/up (split-K, one launch per expert dtype present) */
+void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     if (n_slots <= 0) return;
     const int nb = (a.D + 63) / 64, nbp = (nb + 1) & ~1;
     const int ntok = sk_ntok(a.T, 2, nb);
     const int threads = 64 * sk_waves(nbp / 2);
     const size_t lds = (size_t)2 * nb * ntok * 64;
     const int grid = n_slots * (a.F / 16);
-    if (a.dtype_mask & (1 << 4)) k_expert_gateup_sk<4><<<grid, threads, lds, st>>>(a, ntok);
-    if (a.dtype_mask & (1 << 3)) k_expert_gateup_sk<3><<<grid, threads, lds, st>>>(a, ntok);
-    quant_rows(a.midf, a.F, a.P, a.F / 64, a.mid, st);
+    /* ev0/ev1 (optional) are recorded by the dispatch itself: ev0 at the start of the
+     * first launch, ev1 at the end of the last */
+    const bool q4 = a.dtype_mask & (1 << 4), q8 = a.dtype_mask & (1 << 3);
+    if (q4) hipExtLaunchKernelGGL(k_expert_gateup_sk<4>, dim3(grid), dim3(threads), (uint32_t)lds, st, ev0,
+                                  q8 ? nullptr : ev1, 0u, a, ntok);
+    if (q8) hipExtLaunchKernelGGL(k_expert_gateup_sk<3>, dim3(grid), dim3(threads), (uint32_t)lds, st,
+                                  q4 ? nullptr : ev0, ev1, 0u, a, ntok);
 }
 
+/* NUMERICS §2 of the SwiGLU rows of all T * top_k pairs, then the down projections */
 void expert_down(const MoeArgs &a, int n_slots, hipStream_t st) {
     if (n_slots <= 0) return;
+    quant_rows(a.midf, a.F, a.P, a.F / 64, a.mid, st);
     const int nb = (a.F + 63) / 64, nbp = (nb + 1) & ~1;
     const int ntok = sk_ntok(a.T, 1, nb);
     const int threads = 64 * sk_waves(nbp / 2);

@@ -94,6 +94,7 @@ class KStats(Structure):
         ("attn_s", c_double), ("router_s", c_double), ("expert_s", c_double), ("norm_s", c_double),
         ("head_s", c_double), ("dense_s", c_double),
         ("expert_launches", c_uint64), ("expert_bytes", c_uint64), ("dense_bytes", c_uint64), ("kv_bytes", c_uint64),
+        ("expert_down_s", c_double), ("expert_down_bytes", c_uint64),
     ]
 
 
@@ -374,9 +375,12 @@ class Engine:
         with self._lock:
             self._api.reset_stats(self._handle())
 
-    def set_profiling(self, on: bool) -> None:
+    def set_profiling(self, level) -> None:
+        """0/False: off; 1: events around the grouped expert launches; 2/True: around every
+        launch group (hearth_gpu_set_profiling)."""
+        lvl = 2 if level is True else (0 if level is False else int(level))
         with self._lock:
-            self._api.need("gpu_set_profiling")(self._handle(), 1 if on else 0)
+            self._api.need("gpu_set_profiling")(self._handle(), lvl)
 
     def kstats(self) -> dict:
         k = KStats()

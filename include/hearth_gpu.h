@@ -47,21 +47,26 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
 HEARTH_API int hearth_gpu_accept_greedy(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
                                         int32_t *path_out, int *n_path, int32_t *final_tok);
 
-/* GPU time per kernel class, accumulated while profiling is on (HIP events around
- * every launch group on the engine's stream). */
+/* GPU time per kernel class, accumulated while profiling is on (HIP event pairs on the
+ * engine's stream; see hearth_gpu_set_profiling for the levels). */
 typedef struct hearth_gpu_kstats {
     double attn_s;        /* QKV projection, post-processing, attention, output projection */
     double router_s;      /* router logits + routing + bucketing */
-    double expert_s;      /* grouped expert gate/up + down */
+    double expert_s;      /* grouped expert gate/up (one launch per MoE layer and expert dtype) */
     double norm_s;        /* residual, RMSNorm, activation quantization */
     double head_s;        /* lm_head */
     double dense_s;       /* dense FFN layers and shared experts */
-    uint64_t expert_launches;   /* gate/up + down launch pairs */
-    uint64_t expert_bytes;      /* algorithmic weight bytes of the active experts */
+    uint64_t expert_launches;   /* MoE layers run (gate/up launch groups) */
+    uint64_t expert_bytes;      /* algorithmic weight bytes of the active experts' gate and up matrices */
     uint64_t dense_bytes;       /* algorithmic weight bytes of attention + lm_head matrices */
     uint64_t kv_bytes;          /* KV bytes read by attention (each row once per call and head group) */
+    double expert_down_s;       /* SwiGLU activation quantization + grouped expert down projection */
+    uint64_t expert_down_bytes; /* algorithmic weight bytes of the active experts' down matrices */
 } hearth_gpu_kstats;
 
+/* level 0: off; 1: HIP events around the grouped expert launches only (expert_s,
+ * expert_down_s); 2: events around every launch group. Event pairs are recorded on the
+ * engine's stream and read when a call completes. */
 HEARTH_API int hearth_gpu_set_profiling(hearth_engine *e, int on);
 HEARTH_API int hearth_gpu_get_kstats(hearth_engine *e, hearth_gpu_kstats *out);
 HEARTH_API void hearth_gpu_reset_kstats(hearth_engine *e);
