@@ -113,6 +113,7 @@ HEARTH_API int hearth_gpu_accept_greedy(const float *rows, int n, int V, const i
     if (hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking) != hipSuccess) return E_IO;
     float *dr = (float *)s.get(sizeof(float) * (size_t)n * V);
     int *dt = (int *)s.get(sizeof(int) * (size_t)n * 4 + 16);
+    int *dpart = (int *)s.get(sizeof(int) * (size_t)n * hxd::ACCEPT_PARTS * 3);
     if (!s.ok) return E_NOMEM;
     std::vector<int> hp(n);
     for (int i = 0; i < n; i++) hp[i] = parent ? parent[i] : i - 1;
@@ -123,6 +124,8 @@ HEARTH_API int hearth_gpu_accept_greedy(const float *rows, int n, int V, const i
         return E_IO;
     hxd::AcceptArgs a{};
     a.rows = dr; a.n = n; a.V = V; a.tokens = dtok; a.parent = dpar; a.amax = damax; a.path = dpath; a.result = dres;
+    a.part_v = (float *)dpart; a.part_i = dpart + (size_t)n * hxd::ACCEPT_PARTS;
+    a.part_f = dpart + 2 * (size_t)n * hxd::ACCEPT_PARTS;
     hxl::accept_greedy(a, s.st);
     std::vector<int> res(3), path(n);
     if (hipMemcpyAsync(res.data(), dres, sizeof(int) * 3, hipMemcpyDeviceToHost, s.st) != hipSuccess ||

@@ -139,7 +139,7 @@ struct hearth_engine {
     Act ax{}, aatt{}, amid{}, af{};
     hxd::SlotDesc *slot_desc = nullptr;
     int *ids = nullptr, *route_meta = nullptr, *pair_tok = nullptr, *pair_of = nullptr, *tokens = nullptr,
-        *depth = nullptr, *anc = nullptr, *route_out = nullptr, *acc_i = nullptr;
+        *depth = nullptr, *anc = nullptr, *route_out = nullptr, *acc_i = nullptr, *acc_part = nullptr;
     unsigned long long *dstats = nullptr;
     /* pinned host staging */
     int *h_geom = nullptr;   /* tokens | depth | anc */
@@ -490,6 +490,7 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
         depth = dnew<int>(Bs);
         anc = dnew<int>(Bs * Bs);
         acc_i = dnew<int>(Bs * 2 + 8);
+        acc_part = dnew<int>(Bs * hxd::ACCEPT_PARTS * 3);
         dstats = dnew<unsigned long long>(4);
         ck(hipMemset(dstats, 0, sizeof(unsigned long long) * 4));
         if (c.n_moe) {
@@ -1042,6 +1043,8 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
         ck(hipMemcpyAsync(d_par, h_par, sizeof(int) * n, hipMemcpyHostToDevice, e->st));
         hxd::AcceptArgs a{};
         a.rows = e->logits; a.n = n; a.V = e->V; a.tokens = d_tok; a.parent = d_par; a.amax = d_amax;
+        a.part_v = (float *)e->acc_part; a.part_i = e->acc_part + (size_t)n * hxd::ACCEPT_PARTS;
+        a.part_f = e->acc_part + 2 * (size_t)n * hxd::ACCEPT_PARTS;
         a.path = e->depth; /* reuse: depth is not needed after the forward */
         a.result = d_res;
         hxl::accept_greedy(a, e->st);

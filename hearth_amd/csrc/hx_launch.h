@@ -127,11 +127,15 @@ struct NormArgs {
     int T, D;
 };
 
+constexpr int ACCEPT_PARTS = 32;   /* slices per logits row in the argmax */
+
 struct AcceptArgs {
     const float *rows;        /* [n][V] */
     int n, V;
     const int *tokens, *parent;
     int *amax;                /* [n] argmax or -1 for bad rows */
+    float *part_v;            /* [n][ACCEPT_PARTS] per-slice maxima */
+    int *part_i, *part_f;     /* [n][ACCEPT_PARTS] their indexes, flags (1 NaN/+inf, 2 not -inf) */
     int *path;                /* [n] */
     int *result;              /* [0] n_path, [1] final token, [2] status (0 ok, -1 bad logits) */
 };

@@ -233,8 +233,10 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
     }
 }
 
-/* o[t][h][d] = sum_v p_v * V_v[d], v in order. A workgroup holds up to four heads of
- * one token t in one KV group g, for one 64-wide d chunk (one wave per head, lane = d).
+/* o[t][h][d] = sum_v p_v * V_v[d], v in order. A workgroup sums up to four heads of
+ * one token t in one KV group g, for one 64-wide d chunk (one wave per head, lane = d),
+ * and has four more waves that only stage tiles, so that the summing waves issue
+ * nothing but LDS reads, multiplies and adds.
  * The sum is one dependent f32 add per row, so the kernel is built around that chain:
  * products of 16 rows are formed before their 16 adds (a product never waits in front of
  * the chain), rows come in tiles of 128 through a 3-slot LDS ring (one barrier per 128
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
 constexpr int VT2 = 128;
 constexpr int VPF = 3;   /* register tile sets: the code below names three */
 
-__global__ __launch_bounds__(256) void k_attn_values(AttnArgs a) {
+__global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
     __shared__ float vt[3][VT2][64];
     __shared__ float pt[3][4][VT2];
     __shared__ int anc_s[MAX_ANC];
@@ -257,20 +259,21 @@ __global__ __launch_bounds__(256) void k_attn_values(AttnArgs a) {
     const int g = b % Hkv;
     b /= Hkv;
     const int hq = b % qpt, t = b / qpt;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = (tid >> 6) & 3, lane = tid & 63;
+    const bool loader = tid >= 256;   /* waves 4..7 stage tiles; waves 0..3 sum */
     const int hh = hq * 4 + wave;
     const bool live = hh < grp;
     const int h = g * grp + (live ? hh : 0);
     const int pos0 = a.g.pos0, dep = a.g.depth[t];
     const int nr = pos0 + dep + 1;
     const int ntiles = (nr + VT2 - 1) / VT2, last = ntiles - 1;
-    for (int j = tid; j <= dep; j += 256) anc_s[j] = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + j];
+    for (int j = tid; j <= dep; j += 512) anc_s[j] = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + j];
     __syncthreads();
-    const float *p = a.S + ((size_t)t * a.H + h) * a.ldS;
-    /* staging: float4 u of thread tid is float4 k = 256 u + tid of the tile, i.e. row
-     * k / 16, float4 column k % 16: each wave instruction moves four whole 256-byte rows
-     * and writes 1 KiB of consecutive LDS (no bank conflicts) */
-    const int c4 = (tid & 15) * 4, rbase = tid >> 4;   /* row of float4 u: 16 u + rbase */
+    /* loader thread l = tid - 256: float4 u of the tile is float4 k = 256 u + l: row
+     * k / 16, float4 column k % 16; p rows of head (l / 64) */
+    const int l = tid & 255;
+    const float *p = a.S + ((size_t)t * a.H + h) * a.ldS;   /* head of wave (tid/64)%4 */
+    const int c4 = (l & 15) * 4, rbase = l >> 4;
     const float *vcol = a.vc + (size_t)g * a.cap * hd + (dc * 64 + c4 < hd ? dc * 64 + c4 : 0);
     auto row_of = [&](int i, int u) -> const float * {
         i = i < last ? i : last;
@@ -283,7 +286,6 @@ __global__ __launch_bounds__(256) void k_attn_values(AttnArgs a) {
         const int vp = i * VT2 + k * 64 + lane;
         return p[vp < nr ? vp : nr - 1];
     };
-    /* the register sets are named variables (an indexed array would go to memory) */
 #define HX_VREGS(k) float4 r##k##0, r##k##1, r##k##2, r##k##3, r##k##4, r##k##5, r##k##6, r##k##7; float rp##k##a, rp##k##b
 #define HX_VLD1(i, k, q) r##k##q = *(const float4 *)row_of(i, q)
 #define HX_VST1(slot, k, q) *(float4 *)&vt[slot][16 * q + rbase][c4] = r##k##q
@@ -309,8 +311,6 @@ __global__ __launch_bounds__(256) void k_attn_values(AttnArgs a) {
         const int slot = i % 3, nv = nr - i * VT2;
         const float *pw = pt[slot][wave], *vw = &vt[slot][0][lane];
         if (nv >= VT2) {
-            /* 16-row groups in two alternating register sets: the operands of group
-             * k + 1 are read from LDS before the products and adds of group k */
             float pA[16], vA[16], pB[16], vB[16];
 #define HX_GRD(P_, V_, c_)                                                               \
             _Pragma("unroll") for (int j = 0; j < 16; j++) { P_[j] = pw[(c_) + j]; V_[j] = vw[((c_) + j) * 64]; }
@@ -335,25 +335,26 @@ __global__ __launch_bounds__(256) void k_attn_values(AttnArgs a) {
             for (int r = 0; r < nv; r++) acc = fadd(acc, fmul(pw[r], vw[r * 64]));
         }
     };
-    /* tiles 0 and 1 go straight to slots 0 and 1; register set k holds tile 2 + k */
-    HX_VLOAD(0, 0);
-    HX_VSTORE(0, 0);
-    HX_VLOAD(1, 0);
-    HX_VSTORE(1, 0);
-    HX_VLOAD(2, 0);
-    HX_VLOAD(3, 1);
-    HX_VLOAD(4, 2);
+    if (loader) {
+        HX_VLOAD(0, 0);
+        HX_VSTORE(0, 0);
+        HX_VLOAD(1, 0);
+        HX_VSTORE(1, 0);
+        HX_VLOAD(2, 0);
+        HX_VLOAD(3, 1);
+        HX_VLOAD(4, 2);
+    }
     __syncthreads();
-    /* step i: sum tile i (slot i % 3), write tile i + 2 (register set (i - i0)) to slot
-     * (i + 2) % 3, which held tile i - 1 (summed before the previous barrier), then
-     * request tile i + 2 + VPF into the freed set. Steps past the last tile add nothing. */
+    /* step i: the summing waves use tile i (slot i % 3) while the loaders write tile i + 2
+     * (register set i - i0) to slot (i + 2) % 3 (it held tile i - 1, summed before the
+     * previous barrier) and then request tile i + 2 + VPF */
 #define HX_VSTEP(k)                                                                      \
     do {                                                                                 \
         const int i_ = i0 + k;                                                           \
-        compute(i_);                                                                     \
-        HX_VSTORE((i_ + 2) % 3, k);                                                      \
+        if (loader) HX_VSTORE((i_ + 2) % 3, k);                                          \
+        else compute(i_);                                                                \
         __syncthreads();                                                                 \
-        HX_VLOAD(i_ + 2 + VPF, k);                                                       \
+        if (loader) HX_VLOAD(i_ + 2 + VPF, k);                                           \
     } while (0)
     for (int i0 = 0; i0 < ntiles; i0 += VPF) {
         HX_VSTEP(0);
@@ -366,11 +367,11 @@ __global__ __launch_bounds__(256) void k_attn_values(AttnArgs a) {
 #undef HX_VST1
 #undef HX_VLD1
 #undef HX_VREGS
-    const int d = dc * 64 + lane;
-    if (live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = acc;
-    /* with head_dim % 64 == 0 the wave's 64 outputs are one NUMERICS §2 block of the
-     * token's attention row */
-    if (a.qo_on && live) quant_block_wave(acc, a.qo, t, h * (hd >> 6) + dc);
+    if (!loader) {
+        const int d = dc * 64 + lane;
+        if (live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = acc;
+        if (a.qo_on && live) quant_block_wave(acc, a.qo, t, h * (hd >> 6) + dc);
+    }
 }
 
 } // namespace
@@ -387,7 +388,7 @@ void attention(const AttnArgs &a, hipStream_t st) {
     else k_attn_scores<1><<<nsc, SC_ROWS, 0, st>>>(a);
     k_attn_softmax<<<a.T * a.H, 256, 0, st>>>(a);
     const int nd = (a.hd + 63) / 64, qpt = (grp + 3) / 4;
-    k_attn_values<<<a.T * qpt * a.Hkv * nd, 256, 0, st>>>(a);
+    k_attn_values<<<a.T * qpt * a.Hkv * nd, 512, 0, st>>>(a);
 }
 
 } // namespace hxl

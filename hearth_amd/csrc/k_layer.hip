@@ -593,31 +593,66 @@ __global__ void k_kv_move(float *cache, size_t layer_stride, int L, int Hkv, int
 
 /* ------------------------------------------------------------ greedy acceptance */
 
-__global__ __launch_bounds__(256) void k_argmax_rows(AcceptArgs a) {
+/* Greedy argmax of the verify rows, first index on ties, -1 for rows with a NaN or +inf
+ * or only -inf (generate.py:69-82). Each row is cut into ACCEPT_PARTS slices, one
+ * workgroup each, 8 loads in flight per thread; the walk merges the slices in order. */
+__global__ __launch_bounds__(256) void k_argmax_part(AcceptArgs a) {
     __shared__ float bv[256];
-    __shared__ int bi[256], bad[256];
-    const int row = blockIdx.x, tid = threadIdx.x;
+    __shared__ int bi[256], bf[256];
+    const int row = blockIdx.x / ACCEPT_PARTS, part = blockIdx.x % ACCEPT_PARTS, tid = threadIdx.x;
+    const int len = (a.V + ACCEPT_PARTS - 1) / ACCEPT_PARTS, lo = part * len;
+    const int hi = lo + len < a.V ? lo + len : a.V;
     const float *x = a.rows + (size_t)row * a.V;
     float v = 0.0f;
-    int idx = -1, badv = 0, fin = 0;
-    for (int i = tid; i < a.V; i += 256) {
-        const float xi = x[i];
-        if (xi != xi || xi == __builtin_huge_valf()) badv = 1;
-        if (xi != -__builtin_huge_valf()) fin = 1;
-        if (idx < 0 || xi > v) { v = xi; idx = i; }
+    int idx = -1, flags = 0;
+    for (int i0 = lo + tid; i0 < hi; i0 += 256 * 8) {
+        float xv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + 256 * u;
+            xv[u] = x[i < hi ? i : lo];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + 256 * u;
+            if (i < hi) {
+                const float xi = xv[u];
+                if (xi != xi || xi == __builtin_huge_valf()) flags |= 1;
+                if (xi != -__builtin_huge_valf()) flags |= 2;
+                if (idx < 0 || xi > v) { v = xi; idx = i; }
+            }
+        }
     }
-    bv[tid] = v; bi[tid] = idx; bad[tid] = badv | (fin << 1);
+    bv[tid] = v; bi[tid] = idx; bf[tid] = flags;
     __syncthreads();
     for (int s = 128; s >= 1; s >>= 1) {
         if (tid < s) {
             const float ov = bv[tid + s];
             const int oi = bi[tid + s];
             if (oi >= 0 && (bi[tid] < 0 || ov > bv[tid] || (ov == bv[tid] && oi < bi[tid]))) { bv[tid] = ov; bi[tid] = oi; }
-            bad[tid] |= bad[tid + s];
+            bf[tid] |= bf[tid + s];
         }
         __syncthreads();
     }
-    if (tid == 0) a.amax[row] = ((bad[0] & 1) || !(bad[0] & 2)) ? -1 : bi[0];
+    if (tid == 0) {
+        const size_t o = (size_t)row * ACCEPT_PARTS + part;
+        a.part_v[o] = bv[0];
+        a.part_i[o] = bi[0];
+        a.part_f[o] = bf[0];
+    }
+}
+
+/* argmax of row v from its slices (slices in index order: equal maxima keep the earlier) */
+__device__ int row_argmax(const AcceptArgs &a, int v) {
+    float best = 0.0f;
+    int bi = -1, fl = 0;
+    for (int p = 0; p < ACCEPT_PARTS; p++) {
+        const size_t o = (size_t)v * ACCEPT_PARTS + p;
+        const int pi = a.part_i[o];
+        fl |= a.part_f[o];
+        if (pi >= 0 && (bi < 0 || a.part_v[o] > best)) { best = a.part_v[o]; bi = pi; }
+    }
+    return ((fl & 1) || !(fl & 2)) ? -1 : bi;
 }
 
 __global__ void k_accept_walk(AcceptArgs a) {
@@ -625,7 +660,8 @@ __global__ void k_accept_walk(AcceptArgs a) {
     int v = 0, np = 0, status = 0, fin = -1;
     a.path[np++] = 0;
     for (;;) {
-        const int t = a.amax[v];
+        const int t = row_argmax(a, v);
+        a.amax[v] = t;
         if (t < 0) { status = -1; break; }
         int next = -1;
         for (int c = v + 1; c < a.n; c++)
@@ -682,7 +718,7 @@ void kv_move(float *cache, size_t layer_stride, int L, int Hkv, int cap, int hd,
 }
 
 void accept_greedy(const AcceptArgs &a, hipStream_t st) {
-    k_argmax_rows<<<a.n, 256, 0, st>>>(a);
+    k_argmax_part<<<a.n * ACCEPT_PARTS, 256, 0, st>>>(a);
     k_accept_walk<<<1, 64, 0, st>>>(a);
 }
 
