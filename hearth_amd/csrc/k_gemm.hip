@@ -175,6 +175,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs args) {
  * the result is the one-lane fold bit for bit. */
 constexpr int SK_MAXP = 4;      /* block pairs per wave */
 constexpr int SK_LDS = 65536;   /* bytes of terms per workgroup */
+constexpr int SK_DUMMY = 1024;  /* LDS after the terms: stores of padding token columns */
 
 /* Terms of pairs [p0, p1) of row tile rt of the NM matrices ms (same dtype DT and
  * blocks, one shared activation) for tokens t0 .. t0 + 15 (token t's activation row
@@ -215,14 +216,14 @@ __device__ __forceinline__ void tile_terms_chunk(const QMat *ms, int rt, const A
             sx[k][j] = DT == 4 ? a.s[ab] : 0;
         }
     }
+    /* all MFMAs first (each into its own registers), then the f32 terms: no term waits on
+     * the MFMA just issued. Lanes of token columns >= ntok store to the dummy area. */
     const v4i zero = {0, 0, 0, 0};
-    const bool wl = lr < ntok;
+    v4i cc[NM][SK_MAXP][2];
 #pragma unroll
-    for (int k = 0; k < SK_MAXP; k++) {
+    for (int k = 0; k < SK_MAXP; k++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int g = 2 * (p0 + k) + j;
-            if (p0 + k >= p1 || g >= nb) continue;   /* uniform */
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int mi = 0; mi < NM; mi++) {
                 v4i wa;
@@ -233,7 +234,18 @@ __device__ __forceinline__ void tile_terms_chunk(const QMat *ms, int rt, const A
                 } else {
                     wa = raw[mi][k][DT == 4 ? 0 : j];
                 }
-                v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, xq[k][j], zero, 0, 0, 0);
+                cc[mi][k][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, xq[k][j], zero, 0, 0, 0);
+            }
+    float *dmy = P + (size_t)NM * nb * ntok * 16 + lane * 4;   /* after the NM matrices' terms */
+#pragma unroll
+    for (int k = 0; k < SK_MAXP; k++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int g = 2 * (p0 + k) + j;
+            if (p0 + k >= p1 || g >= nb) continue;   /* uniform */
+#pragma unroll
+            for (int mi = 0; mi < NM; mi++) {
+                v4i c = cc[mi][k][j];
                 if (DT == 4) {
                     const int off = 8 * sx[k][j];   /* sum(nib * q) - 8 sum(q) = sum((nib - 8) q) */
                     c.x -= off; c.y -= off; c.z -= off; c.w -= off;
@@ -245,7 +257,8 @@ __device__ __forceinline__ void tile_terms_chunk(const QMat *ms, int rt, const A
                 v.y = fmul((float)c.y, fmul(h2f((uint16_t)(sw.x >> 16)), d));
                 v.z = fmul((float)c.z, fmul(h2f((uint16_t)(sw.y & 0xffff)), d));
                 v.w = fmul((float)c.w, fmul(h2f((uint16_t)(sw.y >> 16)), d));
-                if (wl) *(float4 *)(P + (size_t)mi * pstride + ((size_t)g * ntok + lr) * 16 + 4 * kg) = v;
+                float *dst = lr < ntok ? P + (size_t)mi * pstride + ((size_t)g * ntok + lr) * 16 + 4 * kg : dmy;
+                *(float4 *)dst = v;
             }
         }
     }
@@ -342,6 +355,140 @@ __global__ __launch_bounds__(512) void k_expert_gateup_sk(MoeArgs a, int ntok) {
             }
         }
         __syncthreads();
+    }
+}
+
+/* Persistent gate/up for few tokens (every expert's tokens fit one token tile and a
+ * wave's pair range fits SK_MAXP): workgroups loop over the items (active slot, 16-row
+ * F tile); as soon as an item's MFMAs have consumed its operand registers, the next
+ * item's loads are issued into them, and the barrier, the ordered fold and the SwiGLU
+ * epilogue of the current item run while those bytes are in flight. */
+template <int DT>
+__device__ __forceinline__ void gu_issue(const SlotDesc &sd, int rt, const Act &a, const int *pair_tok, int q0,
+                                         int q1, v4i (&rw)[2][SK_MAXP][DT == 4 ? 1 : 2], uint2 (&sc)[2][SK_MAXP][2],
+                                         v4i (&xq)[SK_MAXP][2], float (&dx)[SK_MAXP][2], int (&sx)[SK_MAXP][2]) {
+    const int lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
+    const int n = sd.n;
+    const int arow = pair_tok[sd.p0 + (lr < n ? lr : n - 1)];
+    const int npair = sd.w.gate.nbp >> 1;
+#pragma unroll
+    for (int k = 0; k < SK_MAXP; k++) {
+        const int gp = q0 + k < q1 ? q0 + k : q1 - 1;
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            const QMat &m = mi ? sd.w.up : sd.w.gate;
+            if (DT == 4) {
+                rw[mi][k][0] = load16(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
+            } else {
+                const uint8_t *base = m.w + ((size_t)rt * m.nbp + 2 * gp) * 1024 + lane * 16;
+                rw[mi][k][0] = load16(base);
+                rw[mi][k][DT == 4 ? 0 : 1] = load16(base + 1024);
+            }
+            const uint16_t *dcol = m.d + rt * 16 + 4 * kg;
+            sc[mi][k][0] = *(const uint2 *)(dcol + (size_t)(2 * gp) * m.rows_pad);
+            sc[mi][k][1] = *(const uint2 *)(dcol + (size_t)(2 * gp + 1) * m.rows_pad);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const size_t ab = (size_t)arow * a.nbp + 2 * gp + j;
+            xq[k][j] = load16((const uint8_t *)(a.q + ab * 64 + kg * 16));
+            dx[k][j] = a.d[ab];
+            sx[k][j] = DT == 4 ? a.s[ab] : 0;
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void gu_terms(int nb, int ntok, int q0, int q1, const v4i (&rw)[2][SK_MAXP][DT == 4 ? 1 : 2],
+                                         const uint2 (&sc)[2][SK_MAXP][2], const v4i (&xq)[SK_MAXP][2],
+                                         const float (&dx)[SK_MAXP][2], const int (&sx)[SK_MAXP][2], float *P,
+                                         int pstride) {
+    const int lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
+    const v4i zero = {0, 0, 0, 0};
+    v4i cc[2][SK_MAXP][2];
+#pragma unroll
+    for (int k = 0; k < SK_MAXP; k++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                v4i wa;
+                if (DT == 4) {
+                    v4i w0, w1;
+                    unpack_q4(rw[mi][k][0], w0, w1);
+                    wa = j ? w1 : w0;
+                } else {
+                    wa = rw[mi][k][DT == 4 ? 0 : j];
+                }
+                cc[mi][k][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, xq[k][j], zero, 0, 0, 0);
+            }
+    float *dmy = P + (size_t)2 * nb * ntok * 16 + lane * 4;   /* after both matrices' terms */
+#pragma unroll
+    for (int k = 0; k < SK_MAXP; k++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int g = 2 * (q0 + k) + j;
+            if (q0 + k >= q1 || g >= nb) continue;   /* uniform */
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                v4i c = cc[mi][k][j];
+                if (DT == 4) {
+                    const int off = 8 * sx[k][j];
+                    c.x -= off; c.y -= off; c.z -= off; c.w -= off;
+                }
+                const uint2 sw = sc[mi][k][j];
+                const float d = dx[k][j];
+                float4 v;
+                v.x = fmul((float)c.x, fmul(h2f((uint16_t)(sw.x & 0xffff)), d));
+                v.y = fmul((float)c.y, fmul(h2f((uint16_t)(sw.x >> 16)), d));
+                v.z = fmul((float)c.z, fmul(h2f((uint16_t)(sw.y & 0xffff)), d));
+                v.w = fmul((float)c.w, fmul(h2f((uint16_t)(sw.y >> 16)), d));
+                float *dst = lr < ntok ? P + (size_t)mi * pstride + ((size_t)g * ntok + lr) * 16 + 4 * kg : dmy;
+                *(float4 *)dst = v;
+            }
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_expert_gateup_pp(MoeArgs a, int ntok) {
+    extern __shared__ float P[];
+    const int ntile = a.F / 16;
+    const int n_items = *a.n_active * ntile;
+    const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    int item = blockIdx.x;
+    if (item >= n_items) return;   /* uniform */
+    v4i rw[2][SK_MAXP][DT == 4 ? 1 : 2];
+    uint2 sc[2][SK_MAXP][2];
+    v4i xq[SK_MAXP][2];
+    float dx[SK_MAXP][2];
+    int sx[SK_MAXP][2];
+    const SlotDesc *sd = &a.desc[item / ntile];
+    int q0, q1;
+    wave_pairs(sd->w.gate.nbp >> 1, W, wave, q0, q1);
+    gu_issue<DT>(*sd, item % ntile, a.x, a.pair_tok, q0, q1, rw, sc, xq, dx, sx);
+    while (item < n_items) {
+        const int rt = item % ntile, p0 = sd->p0, n = sd->n, nb = sd->w.gate.nb;
+        const int pstride = nb * ntok * 16;
+        if (sd->w.gate.dtype == DT) gu_terms<DT>(nb, ntok, q0, q1, rw, sc, xq, dx, sx, P, pstride);
+        const int next = item + (int)gridDim.x;
+        const SlotDesc *nsd = &a.desc[(next < n_items ? next : item) / ntile];
+        if (next < n_items) gu_issue<DT>(*nsd, next % ntile, a.x, a.pair_tok, q0, q1, rw, sc, xq, dx, sx);
+        __syncthreads();
+        if (sd->w.gate.dtype == DT) {
+            for (int f = tid; f < ntok * 16; f += blockDim.x) {
+                const int c = f >> 4, row = rt * 16 + (f & 15);
+                const float gv = canon(fold_terms(P, nb, ntok, f));
+                const float uv = canon(fold_terms(P + pstride, nb, ntok, f));
+                if (c < n) {
+                    const float sg = fdiv(gv, fadd(1.0f, exp_port_f(-gv)));
+                    a.midf[(size_t)(p0 + c) * a.F + row] = fmul(sg, uv);
+                }
+            }
+        }
+        __syncthreads();
+        item = next;
+        sd = nsd;
     }
 }
 
@@ -493,6 +640,18 @@ void quant_rows(const float *x, int64_t ldx, int T, int nb, const Act &a, hipStr
     k_quant_rows<<<(int)((waves + 3) / 4), 256, 0, st>>>(x, ldx, T, nb, a);
 }
 
+/* compute units of the current device (cached per device) */
+static int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cached[dev];
+}
+
 /* waves per split-K workgroup for npair block pairs */
 static int sk_waves(int npair) {
     const int w = (npair + SK_MAXP - 1) / SK_MAXP;
@@ -502,7 +661,7 @@ static int sk_waves(int npair) {
 /* tokens per split-K token tile: the terms of NM matrices of nb blocks fit SK_LDS */
 static int sk_ntok(int T, int NM, int nb) {
     int n = T < 16 ? T : 16;
-    const int fit = SK_LDS / (NM * nb * 64);
+    const int fit = (SK_LDS - SK_DUMMY) / (NM * nb * 64);
     n = n < fit ? n : fit;
     return n < 1 ? 1 : n;
 }
@@ -523,7 +682,7 @@ static void gemm_sk(const GemmArgs &in, hipStream_t st) {
         const QMat &m = g.seg[0].m;
         const int ntok = sk_ntok(in.T, 1, m.nb);
         const int threads = 64 * sk_waves(m.nbp / 2);
-        const size_t lds = (size_t)m.nb * ntok * 64;
+        const size_t lds = (size_t)m.nb * ntok * 64 + SK_DUMMY;
         if (wg) {
             if (m.dtype == 4) k_gemm_sk<4><<<wg, threads, lds, st>>>(g, ntok);
             else k_gemm_sk<3><<<wg, threads, lds, st>>>(g, ntok);
@@ -562,11 +721,21 @@ void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0
     const int nb = (a.D + 63) / 64, nbp = (nb + 1) & ~1;
     const int ntok = sk_ntok(a.T, 2, nb);
     const int threads = 64 * sk_waves(nbp / 2);
-    const size_t lds = (size_t)2 * nb * ntok * 64;
+    const size_t lds = (size_t)2 * nb * ntok * 64 + SK_DUMMY;
     const int grid = n_slots * (a.F / 16);
     /* ev0/ev1 (optional) are recorded by the dispatch itself: ev0 at the start of the
      * first launch, ev1 at the end of the last */
     const bool q4 = a.dtype_mask & (1 << 4), q8 = a.dtype_mask & (1 << 3);
+    /* few tokens, one dtype, one pair chunk per wave: the persistent kernel (two
+     * workgroups per CU on every CU) */
+    const int npair = nbp / 2, W = threads / 64;
+    if (a.T <= ntok && (q4 != q8) && (npair + W - 1) / W <= SK_MAXP && threads <= 256) {
+        const int ncu = cu_count();
+        const int pgrid = grid < 2 * ncu ? grid : 2 * ncu;
+        if (q4) hipExtLaunchKernelGGL(k_expert_gateup_pp<4>, dim3(pgrid), dim3(threads), (uint32_t)lds, st, ev0, ev1, 0u, a, ntok);
+        else hipExtLaunchKernelGGL(k_expert_gateup_pp<3>, dim3(pgrid), dim3(threads), (uint32_t)lds, st, ev0, ev1, 0u, a, ntok);
+        return;
+    }
     if (q4) hipExtLaunchKernelGGL(k_expert_gateup_sk<4>, dim3(grid), dim3(threads), (uint32_t)lds, st, ev0,
                                   q8 ? nullptr : ev1, 0u, a, ntok);
     if (q8) hipExtLaunchKernelGGL(k_expert_gateup_sk<3>, dim3(grid), dim3(threads), (uint32_t)lds, st,
@@ -580,7 +749,7 @@ void expert_down(const MoeArgs &a, int n_slots, hipStream_t st) {
     const int nb = (a.F + 63) / 64, nbp = (nb + 1) & ~1;
     const int ntok = sk_ntok(a.T, 1, nb);
     const int threads = 64 * sk_waves(nbp / 2);
-    const size_t lds = (size_t)nb * ntok * 64;
+    const size_t lds = (size_t)nb * ntok * 64 + SK_DUMMY;
     const int grid = n_slots * ((a.D + 15) / 16);
     if (a.dtype_mask & (1 << 4)) k_expert_down_sk<4><<<grid, threads, lds, st>>>(a, ntok);
     if (a.dtype_mask & (1 << 3)) k_expert_down_sk<3><<<grid, threads, lds, st>>>(a, ntok);

@@ -429,12 +429,12 @@ __global__ __launch_bounds__(1024) void k_route_bucket(RouteArgs a) {
 }
 
 /* Ungrouped routing of up to 16 tokens (E <= 256) and their bucketing in one workgroup:
- * wave t routes token t exactly as k_route_rank does, then all threads bucket. */
+ * wave t routes token t (scores and weights as k_route_rank; the K experts by K rounds
+ * of a wave maximum over the same keys), then all threads bucket. */
 constexpr int RS_TMAX = 16, RS_EMAX = 256;
 
 __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
     __shared__ float score[RS_TMAX][RS_EMAX];
-    __shared__ unsigned long long key[RS_TMAX][RS_EMAX];
     __shared__ int chosen[RS_TMAX][64];
     __shared__ int pid[RS_TMAX * 64];
     __shared__ int cnt[RS_EMAX], base[RS_EMAX];
@@ -465,16 +465,29 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
         } else {
             for (int e = lane; e < E; e += 64) sc[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
         }
-        wave_sync();
-        for (int e = lane; e < E; e += 64) key[t][e] = rank_key(a.bias ? fadd(sc[e], a.bias[e]) : sc[e], e);
-        wave_sync();
-        for (int e = lane; e < E; e += 64) {
-            const unsigned long long ke = key[t][e];
-            int rank = 0, o = 0;
-            for (; o + 4 <= E; o += 4)
-                rank += (key[t][o] > ke) + (key[t][o + 1] > ke) + (key[t][o + 2] > ke) + (key[t][o + 3] > ke);
-            for (; o < E; o++) rank += key[t][o] > ke;
-            if (rank < K) chosen[t][rank] = e;
+        /* top-K: K rounds of a wave-wide maximum of the selection keys (a larger key ranks
+         * first in ranks_before's order); the winner's key is cleared (0 is below every
+         * key) before the next round */
+        unsigned long long kk[RS_EMAX / 64];
+#pragma unroll
+        for (int u = 0; u < RS_EMAX / 64; u++) {
+            const int e = lane + 64 * u;
+            kk[u] = e < E ? rank_key(a.bias ? fadd(sc[e], a.bias[e]) : sc[e], e) : 0ull;
+        }
+        for (int j = 0; j < K; j++) {
+            unsigned long long m = 0ull;
+#pragma unroll
+            for (int u = 0; u < RS_EMAX / 64; u++) m = kk[u] > m ? kk[u] : m;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const unsigned long long o = __shfl_xor(m, off, 64);
+                m = o > m ? o : m;
+            }
+            const int e = (int)(0xFFFFFFFFu - (uint32_t)m);
+#pragma unroll
+            for (int u = 0; u < RS_EMAX / 64; u++)
+                if (lane + 64 * u == e) kk[u] = 0ull;
+            if (lane == 0) chosen[t][j] = e;
         }
         wave_sync();
         if (lane < K) {
