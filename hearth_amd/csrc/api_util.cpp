@@ -6,6 +6,7 @@
  */
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstring>
 #include <vector>
 
@@ -44,6 +45,15 @@ struct Scratch {
 };
 
 } // namespace
+
+int hx::check_sampler(const hearth_sampler *s) {
+    if (!s) return E_ARG;
+    if (!std::isfinite(s->temperature) || s->temperature < 0.0) return E_ARG;
+    if (s->top_k < 0 || !(s->top_p > 0.0 && s->top_p <= 1.0) || !(s->min_p >= 0.0 && s->min_p <= 1.0)) return E_ARG;
+    if (!std::isfinite(s->repetition_penalty) || !(s->repetition_penalty > 0.0)) return E_ARG;
+    if (s->n_context < 0 || (s->n_context > 0 && !s->context)) return E_ARG;
+    return OK;
+}
 
 extern "C" {
 
@@ -136,6 +146,77 @@ HEARTH_API int hearth_gpu_accept_greedy(const float *rows, int n, int V, const i
     *n_path = res[0];
     for (int j = 0; j < res[0]; j++) path_out[j] = path[j];
     *final_tok = res[1];
+    return OK;
+}
+
+HEARTH_API int hearth_gpu_accept_sample(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
+                                        const hearth_sampler *smp, const double *q, const double *u,
+                                        int32_t *path_out, int *n_path, int32_t *final_tok) {
+    if (!rows || n < 1 || V < 1 || !tokens || !u || !path_out || !n_path || !final_tok) return E_ARG;
+    if (check_sampler(smp) != OK || n > hxd::SAMPLE_NMAX || V > hxd::SAMPLE_VMAX) return E_ARG;
+    for (int i = 0; i < n; i++) {
+        if (tokens[i] < 0 || tokens[i] >= V) return E_TOKEN;
+        if (parent && ((i == 0 && parent[i] != -1) || (i > 0 && (parent[i] < 0 || parent[i] >= i)))) return E_ARG;
+    }
+    if (hipSetDevice(device()) != hipSuccess) return E_IO;
+    Scratch s;
+    if (hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking) != hipSuccess) return E_IO;
+    float *dr = (float *)s.get(sizeof(float) * (size_t)n * V);
+    if (!s.ok) return E_NOMEM;
+    hxl::SampleScratch m;
+    const int n_ctx = smp->repetition_penalty != 1.0 ? smp->n_context : 0;
+    if (m.ensure(n, V, q != nullptr, n_ctx) != hipSuccess) return E_NOMEM;
+    std::vector<int> hp(n);
+    for (int i = 0; i < n; i++) hp[i] = parent ? parent[i] : i - 1;
+    if (hipMemcpyAsync(dr, rows, sizeof(float) * (size_t)n * V, hipMemcpyHostToDevice, s.st) != hipSuccess ||
+        hipMemcpyAsync(m.tok, tokens, sizeof(int) * n, hipMemcpyHostToDevice, s.st) != hipSuccess ||
+        hipMemcpyAsync(m.par, hp.data(), sizeof(int) * n, hipMemcpyHostToDevice, s.st) != hipSuccess)
+        return E_IO;
+    const hxl::SamplerSpec sp{smp->temperature, smp->top_p, smp->min_p, smp->repetition_penalty, smp->top_k,
+                              smp->context, n_ctx};
+    hxl::accept_sample(m, dr, n, V, m.tok, m.par, sp, q, u, s.st);
+    std::vector<int> res(3), path(n);
+    if (hipMemcpyAsync(res.data(), m.result, sizeof(int) * 3, hipMemcpyDeviceToHost, s.st) != hipSuccess ||
+        hipMemcpyAsync(path.data(), m.path, sizeof(int) * n, hipMemcpyDeviceToHost, s.st) != hipSuccess ||
+        hipStreamSynchronize(s.st) != hipSuccess)
+        return E_IO;
+    if (res[2] != 0) return E_ARG;
+    *n_path = res[0];
+    for (int j = 0; j < res[0]; j++) path_out[j] = path[j];
+    *final_tok = res[1];
+    return OK;
+}
+
+HEARTH_API int hearth_gpu_probs(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
+                                const hearth_sampler *smp, double *p_out) {
+    if (!rows || n < 1 || V < 1 || !tokens || !p_out) return E_ARG;
+    if (check_sampler(smp) != OK || n > hxd::SAMPLE_NMAX || V > hxd::SAMPLE_VMAX) return E_ARG;
+    for (int i = 0; i < n; i++)
+        if (parent && ((i == 0 && parent[i] != -1) || (i > 0 && (parent[i] < 0 || parent[i] >= i)))) return E_ARG;
+    if (hipSetDevice(device()) != hipSuccess) return E_IO;
+    Scratch s;
+    if (hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking) != hipSuccess) return E_IO;
+    float *dr = (float *)s.get(sizeof(float) * (size_t)n * V);
+    if (!s.ok) return E_NOMEM;
+    hxl::SampleScratch m;
+    const int n_ctx = smp->repetition_penalty != 1.0 ? smp->n_context : 0;
+    if (m.ensure(n, V, false, n_ctx) != hipSuccess) return E_NOMEM;
+    std::vector<int> hp(n);
+    for (int i = 0; i < n; i++) hp[i] = parent ? parent[i] : i - 1;
+    if (hipMemcpyAsync(dr, rows, sizeof(float) * (size_t)n * V, hipMemcpyHostToDevice, s.st) != hipSuccess ||
+        hipMemcpyAsync(m.tok, tokens, sizeof(int) * n, hipMemcpyHostToDevice, s.st) != hipSuccess ||
+        hipMemcpyAsync(m.par, hp.data(), sizeof(int) * n, hipMemcpyHostToDevice, s.st) != hipSuccess)
+        return E_IO;
+    const hxl::SamplerSpec sp{smp->temperature, smp->top_p, smp->min_p, smp->repetition_penalty, smp->top_k,
+                              smp->context, n_ctx};
+    hxl::sample_probs(m, dr, n, V, m.tok, m.par, sp, s.st);
+    std::vector<int> rc(n);
+    if (hipMemcpyAsync(rc.data(), m.row_rc, sizeof(int) * n, hipMemcpyDeviceToHost, s.st) != hipSuccess ||
+        hipMemcpyAsync(p_out, m.P, sizeof(double) * (size_t)n * V, hipMemcpyDeviceToHost, s.st) != hipSuccess ||
+        hipStreamSynchronize(s.st) != hipSuccess)
+        return E_IO;
+    for (int i = 0; i < n; i++)
+        if (rc[i] != 0) return E_ARG;
     return OK;
 }
 

@@ -167,6 +167,8 @@ struct hearth_engine {
     int64_t replay_rows = 0;
     /* tree verification: slots of the last uncommitted tree */
     int tree_n = 0;
+    /* sampled acceptance scratch, grown on demand */
+    hxl::SampleScratch samp;
     /* HEARTH_DEBUG_DUMP=<dir>: every forward writes named intermediate buffers there
      * (T rows each, appended per call) for layer-by-layer comparisons */
     std::string dump_dir;
@@ -204,6 +206,7 @@ struct hearth_engine {
         for (auto &e : ev_pool) (void)hipEventDestroy(e);
         if (geom_ev) (void)hipEventDestroy(geom_ev);
         for (void *p : allocs) (void)hipFree(p);
+        samp.release();
         if (h_geom) (void)hipHostFree(h_geom);
         if (h_rope) (void)hipHostFree(h_rope);
         if (h_res) (void)hipHostFree(h_res);
@@ -1019,8 +1022,16 @@ HEARTH_API int hearth_commit_path(hearth_engine *e, const int32_t *path, int n) 
     return OK;
 }
 
-HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,
-                                    int32_t *path_out, int *n_path, int32_t *final_tok, float *logits) {
+} // extern "C"
+
+namespace {
+
+/* The verify-and-accept calls: forward + head for the tree, the acceptance enqueued by
+ * accept(d_parent) (which returns the device path and the device result triple
+ * {n_path, final token, status}), then the commit of the accepted path. */
+template <class Accept>
+int verify_and_commit(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n, float *logits,
+                      int32_t *path_out, int *n_path, int32_t *final_tok, const char *what, Accept accept) {
     if (!e || n < 1 || !tokens || !path_out || !n_path || !final_tok) return E_ARG;
     if (n > e->B) return E_ARG;
     for (int i = 0; i < n; i++) {
@@ -1036,19 +1047,13 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
         /* logits stay in HBM; the head ran only if requested -> force it here */
         e->timed(&e->ks.head_s, [&] { e->matmul(e->lm_head, e->ax, e->x, e->D, n, e->logits, e->V, true, e->c.logit_scale); });
         if (logits) ck(hipMemcpyAsync(logits, e->logits, sizeof(float) * (size_t)n * e->V, hipMemcpyDeviceToHost, e->st));
-        int *d_tok = e->tokens;
-        int *d_par = e->acc_i, *d_amax = e->acc_i + e->B, *d_res = e->acc_i + 2 * e->B;
+        int *d_par = e->acc_i;
         int *h_par = e->h_res;
         for (int i = 0; i < n; i++) h_par[i] = parent ? parent[i] : i - 1;
         ck(hipMemcpyAsync(d_par, h_par, sizeof(int) * n, hipMemcpyHostToDevice, e->st));
-        hxd::AcceptArgs a{};
-        a.rows = e->logits; a.n = n; a.V = e->V; a.tokens = d_tok; a.parent = d_par; a.amax = d_amax;
-        a.part_v = (float *)e->acc_part; a.part_i = e->acc_part + (size_t)n * hxd::ACCEPT_PARTS;
-        a.part_f = e->acc_part + 2 * (size_t)n * hxd::ACCEPT_PARTS;
-        a.path = e->depth; /* reuse: depth is not needed after the forward */
-        a.result = d_res;
-        hxl::accept_greedy(a, e->st);
-        ck(hipMemcpyAsync(e->h_res + e->B, e->depth, sizeof(int) * n, hipMemcpyDeviceToHost, e->st));
+        const int *d_path = nullptr, *d_res = nullptr;
+        e->timed(&e->ks.accept_s, [&] { accept(d_par, d_path, d_res); });
+        ck(hipMemcpyAsync(e->h_res + e->B, d_path, sizeof(int) * n, hipMemcpyDeviceToHost, e->st));
         ck(hipMemcpyAsync(e->h_res + 2 * e->B, d_res, sizeof(int) * 3, hipMemcpyDeviceToHost, e->st));
         ck(hipStreamSynchronize(e->st));
         np = e->h_res[2 * e->B];
@@ -1067,7 +1072,7 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
         e->write_trace(n);
         if (e->profiling) e->collect_events();
     } catch (const DeviceError &err) {
-        log_msg(LOG_ERROR, "HIP error in hearth_verify_greedy: %s", hipGetErrorString(err.e));
+        log_msg(LOG_ERROR, "HIP error in %s: %s", what, hipGetErrorString(err.e));
         return E_IO;
     }
     if (status != 0) return E_ARG;
@@ -1079,6 +1084,42 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
     e->forward_calls++;
     e->wall_s += now_s() - t0;
     return OK;
+}
+
+} // namespace
+
+extern "C" {
+
+HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,
+                                    int32_t *path_out, int *n_path, int32_t *final_tok, float *logits) {
+    return verify_and_commit(e, tokens, parent, n, logits, path_out, n_path, final_tok, "hearth_verify_greedy",
+                             [&](int *d_par, const int *&d_path, const int *&d_res) {
+        hxd::AcceptArgs a{};
+        a.rows = e->logits; a.n = n; a.V = e->V; a.tokens = e->tokens; a.parent = d_par; a.amax = e->acc_i + e->B;
+        a.part_v = (float *)e->acc_part; a.part_i = e->acc_part + (size_t)n * hxd::ACCEPT_PARTS;
+        a.part_f = e->acc_part + 2 * (size_t)n * hxd::ACCEPT_PARTS;
+        a.path = e->depth; /* reuse: depth is not needed after the forward */
+        a.result = e->acc_i + 2 * e->B;
+        hxl::accept_greedy(a, e->st);
+        d_path = a.path;
+        d_res = a.result;
+    });
+}
+
+HEARTH_API int hearth_verify_sample(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,
+                                    const hearth_sampler *s, const double *q, const double *u, int32_t *path_out,
+                                    int *n_path, int32_t *final_tok, float *logits) {
+    if (!e || !u || check_sampler(s) != OK) return E_ARG;
+    if (n > hxd::SAMPLE_NMAX || e->V > hxd::SAMPLE_VMAX) return E_ARG;
+    return verify_and_commit(e, tokens, parent, n, logits, path_out, n_path, final_tok, "hearth_verify_sample",
+                             [&](int *d_par, const int *&d_path, const int *&d_res) {
+        const int n_ctx = s->repetition_penalty != 1.0 ? s->n_context : 0;
+        ck(e->samp.ensure(n, e->V, q != nullptr, n_ctx));
+        hxl::SamplerSpec sp{s->temperature, s->top_p, s->min_p, s->repetition_penalty, s->top_k, s->context, n_ctx};
+        hxl::accept_sample(e->samp, e->logits, n, e->V, e->tokens, d_par, sp, q, u, e->st);
+        d_path = e->samp.path;
+        d_res = e->samp.result;
+    });
 }
 
 HEARTH_API int hearth_gpu_set_profiling(hearth_engine *e, int on) {

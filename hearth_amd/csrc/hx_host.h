@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "hearth.h"
+#include "hearth_gpu.h"
 
 namespace hx {
 
@@ -20,6 +21,10 @@ constexpr uint32_t CANON_NAN = 0x7fc00000u; /* the one NaN bit pattern outputs c
 
 /* Error codes (reference engine/src/hx_model.h:60-68). */
 enum { OK = 0, E_ARG = -1, E_TOKEN = -2, E_CAPACITY = -3, E_IO = -4, E_NOMEM = -5, E_FORMAT = -6 };
+
+/* Sampler settings check, as Sampler.__post_init__ (python/hearth/generate.py:45-56):
+ * OK or E_ARG. */
+int check_sampler(const hearth_sampler *s);
 
 enum { ATTN_GQA = 0, ATTN_MLA = 1 };
 enum { QKNORM_NONE = 0, QKNORM_HEAD = 1, QKNORM_FULL = 2 };

@@ -140,6 +140,44 @@ struct AcceptArgs {
     int *result;              /* [0] n_path, [1] final token, [2] status (0 ok, -1 bad logits) */
 };
 
+/* numpy's pairwise summation tree of the last (partial) 8192-element buffer of a row:
+ * leaves in index order, and per level the additions slot[a] = slot[a] + slot[b]
+ * (a subtree's value lives in the slot of its leftmost leaf). Built on the host. */
+constexpr int PW_MAXLEAF = 72;
+struct PwTail {
+    int len, nleaf, nlev;
+    unsigned short leaf_start[PW_MAXLEAF];
+    unsigned char leaf_len[PW_MAXLEAF];
+    unsigned char op_a[PW_MAXLEAF], op_b[PW_MAXLEAF];
+    unsigned char lev_off[12];       /* ops of level h: [lev_off[h-1], lev_off[h]) */
+};
+
+constexpr int SAMPLE_VMAX = 262144;  /* vocabulary limit of sampled acceptance */
+constexpr int SAMPLE_NMAX = 4096;    /* verify nodes per call */
+
+/* Sampled acceptance of a verify tree (chain: parent[i] = i - 1). */
+struct SampleArgs {
+    const float *rows;                /* [n][V] target logits */
+    int n, V;
+    const int *tokens, *parent;       /* [n] */
+    const double *q;                  /* [n][V] draft distributions (row v: v's children) or null */
+    const double *u;                  /* [2n] uniforms */
+    double temperature, top_p, min_p, rp;
+    int top_k;
+    const int *ctx;                   /* penalty context ids [n_ctx] */
+    int n_ctx;
+    double *P;                        /* [n][V] final distributions */
+    unsigned long long *skey;         /* [n][sort_n] sort scratch for large candidate sets */
+    int *sidx;                        /* [n][sort_n] */
+    int sort_n;                       /* power of two >= V */
+    double *wa, *wb, *cw, *cc;        /* [V] residuals and draw scratch */
+    int *ci;                          /* [V] */
+    int *row_rc;                      /* [n] 0 ok, -1 bad logits */
+    int *path;                        /* [n] accepted nodes from the root */
+    int *result;                      /* [0] path length, [1] final token, [2] status */
+    PwTail tail;                      /* pairwise tree of the row's last numpy buffer */
+};
+
 } // namespace hxd
 
 namespace hxl {
@@ -160,4 +198,35 @@ void attention(const AttnArgs &a, hipStream_t st);
 void kv_move(float *cache_layer0, size_t layer_stride, int L, int Hkv, int cap, int hd, int pos0, const int *path_dev,
              int n, hipStream_t st);
 void accept_greedy(const AcceptArgs &a, hipStream_t st);
+/* Sampler settings of one sampled acceptance (the reference's Sampler fields). */
+struct SamplerSpec {
+    double temperature, top_p, min_p, rp;
+    int top_k;
+    const int *ctx;          /* host penalty context ids */
+    int n_ctx;
+};
+
+/* Device scratch of sampled acceptance, grown on demand (every call on one stream). */
+struct SampleScratch {
+    int n_cap = 0, V = 0, ctx_cap = 0, sort_n = 0;
+    bool has_q = false;
+    double *P = nullptr, *q = nullptr, *u = nullptr, *wa = nullptr, *wb = nullptr, *cw = nullptr, *cc = nullptr;
+    unsigned long long *skey = nullptr;
+    int *sidx = nullptr, *ci = nullptr, *row_rc = nullptr, *path = nullptr, *result = nullptr, *ctx = nullptr,
+        *tok = nullptr, *par = nullptr;
+    hipError_t ensure(int n, int V, bool need_q, int n_ctx);
+    void release();
+    ~SampleScratch() { release(); }
+};
+
+/* Uploads q (host [n][V] float64, or null for point-mass drafts), u (host [2n]) and the
+ * penalty context, then runs the distribution and walk kernels on rows (device [n][V])
+ * with device tokens/parent. The accepted path is left in m.path, and n_path, final
+ * token and status (0, or -1 for bad logits) in m.result[0..2]. */
+void accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                   const SamplerSpec &s, const double *q, const double *u, hipStream_t st);
+/* The distribution kernel alone: m.P[v] = the final distribution of row v (the penalty
+ * context of row v includes the path tokens of nodes 1..v), m.row_rc[v] its status. */
+void sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                  const SamplerSpec &s, hipStream_t st);
 } // namespace hxl

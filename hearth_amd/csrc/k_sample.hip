@@ -1,0 +1,734 @@
+/*
+ * k_sample.hip — sampled speculative acceptance on the device: the reference's
+ * Sampler.probs / draw / accept_point_mass (python/hearth/generate.py:68-147) inside its
+ * verify block (generate.py:365-392), generalised to a tree of drafts (recursive
+ * rejection sampling over a node's children in index order) and to a draft
+ * distribution q per node.
+ *
+ * Everything runs in float64 in the reference's operation order, so the result is the
+ * CPU restatement's bit for bit:
+ *   - probs: penalty on the context ids, (x - max) / T, top-k by the exact k-th value,
+ *     exp (the portable double exp), division by numpy's sum, top-p over the stable
+ *     descending order with a sequential cumulative sum, min-p;
+ *   - numpy's sum: 0.0, then in order the pairwise sum of each 8192-element buffer
+ *     (8 accumulators over leaves of at most 128, halves split at multiples of 8);
+ *   - cumulative sums (top-p, the inverse-CDF draw) are one sequential float64 chain,
+ *     run by one wave over the nonzero entries only (adding +0.0 changes nothing).
+ *
+ * Top-p does not sort the whole row. A histogram of the probabilities by exponent
+ * (and one mantissa bit) picks the highest bins whose approximate mass exceeds top_p;
+ * only their entries are sorted (bitonic, in LDS up to 8192 entries, else in the row's
+ * global scratch) and summed in order. Once the running sum c has reached
+ * top_p * (1 + 2^-48), every later entry e of the descending order has
+ * before_e = fl(c_e - p_e) >= c_{e-1} (1 - 3 * 2^-53) > top_p and is dropped, so the
+ * entries below the chosen bins never need ordering. If the chosen bins run out before
+ * that (the histogram is approximate), the rest of the row is sorted and the chain
+ * continues — the result never depends on the histogram.
+ *
+ * k_sample_probs: one workgroup per verify row writes the row's final distribution.
+ * k_sample_walk:  one workgroup walks the tree from the root with the uniforms.
+ */
+#include <climits>
+#include <functional>
+#include <vector>
+
+#include "hx_launch.h"
+
+namespace hxd {
+namespace {
+
+constexpr int SP_T = 1024;
+constexpr int SP_WAVES = SP_T / 64;
+constexpr int NP_BUF = 8192;                     /* numpy's reduction buffer (elements) */
+constexpr int LV_MAX = (SAMPLE_VMAX / NP_BUF) * 64 + PW_MAXLEAF;
+constexpr int SORT_LDS = 8192;                   /* candidates sorted in LDS */
+constexpr int HBINS = 2048;                      /* p in (0, 1]: bits >> 51 < 2048 */
+constexpr int SMEM = SORT_LDS * 12;              /* LDS reused by the stages of a row */
+constexpr double INF = __builtin_huge_val();
+
+__device__ __forceinline__ double ddiv(double a, double b) { return __ddiv_rn(a, b); }
+
+/* ---------------------------------------------------------------- workgroup helpers */
+
+/* every thread gets the maximum */
+__device__ double wg_max(double v, double *red) {
+    for (int off = 32; off >= 1; off >>= 1) v = fmax(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double m = red[0];
+    for (int i = 1; i < SP_WAVES; i++) m = fmax(m, red[i]);
+    __syncthreads();
+    return m;
+}
+
+/* exclusive prefix sum over the workgroup in thread order; *total gets the sum */
+__device__ int wg_scan_excl(int v, int *red, int *total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int inc = v;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += y;
+    }
+    if (lane == 63) red[w] = inc;
+    __syncthreads();
+    int before = 0, tot = 0;
+    for (int i = 0; i < SP_WAVES; i++) {
+        if (i < w) before += red[i];
+        tot += red[i];
+    }
+    __syncthreads();
+    *total = tot;
+    return before + inc - v;
+}
+
+/* value of lane t (t uniform) of a per-lane double */
+__device__ __forceinline__ double lane_value(double x, int t) {
+    const long long b = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_readlane((int)b, t), hi = __builtin_amdgcn_readlane((int)(b >> 32), t);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+/* ---------------------------------------------------------------- numpy's sum */
+
+/* numpy's pairwise_sum on one leaf (n <= 128) */
+__device__ double pw_leaf(const double *a, int n) {
+    if (n < 8) {
+        double r = 0.0;
+        for (int i = 0; i < n; i++) r = dadd(r, a[i]);
+        return r;
+    }
+    double r0 = a[0], r1 = a[1], r2 = a[2], r3 = a[3], r4 = a[4], r5 = a[5], r6 = a[6], r7 = a[7];
+    const int lim = n - (n % 8);
+    int i = 8;
+    for (; i < lim; i += 8) {
+        r0 = dadd(r0, a[i]);
+        r1 = dadd(r1, a[i + 1]);
+        r2 = dadd(r2, a[i + 2]);
+        r3 = dadd(r3, a[i + 3]);
+        r4 = dadd(r4, a[i + 4]);
+        r5 = dadd(r5, a[i + 5]);
+        r6 = dadd(r6, a[i + 6]);
+        r7 = dadd(r7, a[i + 7]);
+    }
+    double res = dadd(dadd(dadd(r0, r1), dadd(r2, r3)), dadd(dadd(r4, r5), dadd(r6, r7)));
+    for (; i < n; i++) res = dadd(res, a[i]);
+    return res;
+}
+
+/* np.sum(a[0:V]) for float64: full 8192-element buffers are balanced trees of 64 leaves
+ * of 128; the partial last buffer follows tail. Every thread gets the sum. */
+__device__ double np_sum(const double *a, int V, const PwTail &tail, double *lv, double *bcast) {
+    const int nfull = V / NP_BUF;
+    const int tl = V - nfull * NP_BUF;
+    const int nleaf = nfull * 64 + (tl ? tail.nleaf : 0);
+    __syncthreads();                               /* a[] was written by other threads */
+    for (int L = threadIdx.x; L < nleaf; L += SP_T) {
+        int start, len;
+        if (L < nfull * 64) {
+            start = (L >> 6) * NP_BUF + (L & 63) * 128;
+            len = 128;
+        } else {
+            const int t = L - nfull * 64;
+            start = nfull * NP_BUF + tail.leaf_start[t];
+            len = tail.leaf_len[t];
+        }
+        lv[L] = pw_leaf(a + start, len);
+    }
+    __syncthreads();
+    for (int h = 1; h <= 7; h++) {
+        const int per = h <= 6 ? (64 >> h) : 0;
+        const int nf = nfull * per;
+        const int nt = (tl && h <= tail.nlev) ? tail.lev_off[h] - tail.lev_off[h - 1] : 0;
+        for (int o = threadIdx.x; o < nf + nt; o += SP_T) {
+            if (o < nf) {
+                const int s = (o / per) * 64 + (o % per) * (1 << h);
+                lv[s] = dadd(lv[s], lv[s + (1 << (h - 1))]);
+            } else {
+                const int t = tail.lev_off[h - 1] + (o - nf), base = nfull * 64;
+                lv[base + tail.op_a[t]] = dadd(lv[base + tail.op_a[t]], lv[base + tail.op_b[t]]);
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        double s = 0.0;
+        for (int b = 0; b < nfull; b++) s = dadd(s, lv[b * 64]);
+        if (tl) s = dadd(s, lv[nfull * 64]);
+        *bcast = s;
+    }
+    __syncthreads();
+    const double s = *bcast;
+    __syncthreads();
+    return s;
+}
+
+/* ---------------------------------------------------------------- top-k */
+
+/* order-preserving key of a non-NaN double (ascending keys = ascending values) */
+__device__ __forceinline__ unsigned long long okey(double x) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+    return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+__device__ __forceinline__ double okey_value(unsigned long long k) {
+    const unsigned long long b = (k >> 63) ? (k & 0x7fffffffffffffffull) : ~k;
+    return __longlong_as_double((long long)b);
+}
+
+/* value at ascending rank r (0-based) of x[0..V): radix select, 8 bits per pass */
+__device__ double select_rank(const double *x, int V, int r, uint32_t *hist, int *sh) {
+    unsigned long long prefix = 0, mask = 0;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        for (int i = threadIdx.x; i < 256; i += SP_T) hist[i] = 0;
+        __syncthreads();
+        for (int i = threadIdx.x; i < V; i += SP_T) {
+            const unsigned long long k = okey(x[i]);
+            if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255], 1u);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            const int l = threadIdx.x;
+            const uint32_t h0 = hist[4 * l], h1 = hist[4 * l + 1], h2 = hist[4 * l + 2], h3 = hist[4 * l + 3];
+            const uint32_t tot = h0 + h1 + h2 + h3;
+            uint32_t inc = tot;
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t y = __shfl_up(inc, off, 64);
+                if (l >= off) inc += y;
+            }
+            const uint32_t exc = inc - tot, rr0 = (uint32_t)r;
+            if (exc <= rr0 && rr0 < inc) {
+                uint32_t rr = rr0 - exc;
+                int d = 4 * l;
+                if (rr >= h0) {
+                    rr -= h0; d++;
+                    if (rr >= h1) {
+                        rr -= h1; d++;
+                        if (rr >= h2) { rr -= h2; d++; }
+                    }
+                }
+                sh[0] = d;
+                sh[1] = (int)rr;
+            }
+        }
+        __syncthreads();
+        prefix |= (unsigned long long)sh[0] << shift;
+        mask |= 255ull << shift;
+        r = sh[1];
+        __syncthreads();
+    }
+    return okey_value(prefix);
+}
+
+/* ---------------------------------------------------------------- sorting (top-p) */
+
+/* descending probability, ascending index on ties (np.argsort(-p, kind="stable")) */
+__device__ __forceinline__ bool before(unsigned long long ka, int ia, unsigned long long kb, int ib) {
+    return ka > kb || (ka == kb && ia < ib);
+}
+
+/* one compare-exchange stage (k, j) of a bitonic network over key/idx[0..N); base is
+ * the global index of element 0 (the direction of element i is ((base + i) & k) == 0) */
+__device__ void bitonic_stage(unsigned long long *key, int *idx, int N, int k, int j, int base) {
+    for (int t = threadIdx.x; t < N / 2; t += SP_T) {
+        const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+        const int p = i + j;
+        const bool asc = ((base + i) & k) == 0;
+        const unsigned long long ki = key[i], kp = key[p];
+        const int ii = idx[i], ip = idx[p];
+        if (asc ? before(kp, ip, ki, ii) : before(ki, ii, kp, ip)) {
+            key[i] = kp; key[p] = ki;
+            idx[i] = ip; idx[p] = ii;
+        }
+    }
+}
+
+/* stages k in [k0, k1] (j from min(k/2, jmax) down to 1) on an LDS block */
+__device__ void bitonic_block(unsigned long long *key, int *idx, int N, int k0, int k1, int jmax, int base) {
+    for (int k = k0; k <= k1; k <<= 1)
+        for (int j = (k >> 1) < jmax ? (k >> 1) : jmax; j > 0; j >>= 1) {
+            bitonic_stage(key, idx, N, k, j, base);
+            __syncthreads();
+        }
+}
+
+/* sorts gkey/gidx[0..N) (N a power of two > SORT_LDS, in global memory) with LDS blocks
+ * for the strides below SORT_LDS */
+__device__ void bitonic_global(unsigned long long *gkey, int *gidx, int N, unsigned long long *lkey, int *lidx) {
+    const int nb = N / SORT_LDS;
+    for (int k = 2; k <= N; k <<= 1) {
+        if (k > SORT_LDS)
+            for (int j = k >> 1; j >= SORT_LDS; j >>= 1) {
+                bitonic_stage(gkey, gidx, N, k, j, 0);
+                __syncthreads();
+            }
+        for (int b = 0; b < nb; b++) {
+            for (int i = threadIdx.x; i < SORT_LDS; i += SP_T) {
+                lkey[i] = gkey[b * SORT_LDS + i];
+                lidx[i] = gidx[b * SORT_LDS + i];
+            }
+            __syncthreads();
+            if (k <= SORT_LDS) bitonic_block(lkey, lidx, SORT_LDS, 2, SORT_LDS, SORT_LDS, b * SORT_LDS);
+            else bitonic_block(lkey, lidx, SORT_LDS, k, k, SORT_LDS / 2, b * SORT_LDS);
+            for (int i = threadIdx.x; i < SORT_LDS; i += SP_T) {
+                gkey[b * SORT_LDS + i] = lkey[i];
+                gidx[b * SORT_LDS + i] = lidx[i];
+            }
+            __syncthreads();
+        }
+        if (k <= SORT_LDS) k = SORT_LDS;   /* the block pass ran every stage up to SORT_LDS */
+    }
+}
+
+/* ---------------------------------------------------------------- per-row distribution */
+
+struct RowShared {
+    double red_d[SP_WAVES];
+    int red_i[SP_WAVES];
+    int red_f[SP_WAVES];
+    double bd[4];
+    int bi[8];
+};
+
+/* the Sampler.probs pipeline on row v; returns 0 or -1 (bad logits) */
+__global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
+    __shared__ __align__(16) unsigned char smem[SMEM];
+    __shared__ RowShared rs;
+    const int v = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int V = a.V;
+    const float *row = a.rows + (size_t)v * V;
+    double *P = a.P + (size_t)v * V;
+    double *lv = (double *)smem;
+
+    /* Sampler._penalised: the ids of the context and of the path nodes 1..v */
+    const bool pen = a.rp != 1.0;
+    uint32_t *bits = (uint32_t *)smem;
+    if (pen) {
+        for (int i = tid; i < (V + 31) / 32; i += SP_T) bits[i] = 0;
+        __syncthreads();
+        for (int j = tid; j < a.n_ctx; j += SP_T) {
+            const int t = a.ctx[j];
+            if (t >= 0 && t < V) atomicOr(&bits[t >> 5], 1u << (t & 31));
+        }
+        if (tid == 0)
+            for (int c = v; c > 0; c = a.parent[c]) {
+                const int t = a.tokens[c];
+                if (t >= 0 && t < V) atomicOr(&bits[t >> 5], 1u << (t & 31));
+            }
+        __syncthreads();
+    }
+    double best = -INF;
+    int bidx = -1, flags = 0;
+    for (int i = tid; i < V; i += SP_T) {
+        const float l = row[i];
+        if (l != l || l == __builtin_huge_valf()) flags |= 1;
+        if (l != -__builtin_huge_valf()) flags |= 2;
+        double x = (double)l;
+        if (pen && ((bits[i >> 5] >> (i & 31)) & 1u)) x = x > 0.0 ? ddiv(x, a.rp) : dmul(x, a.rp);
+        P[i] = x;
+        if (bidx < 0 || x > best) { best = x; bidx = i; }
+    }
+    /* max and first argmax over the workgroup, flags */
+    for (int off = 32; off >= 1; off >>= 1) {
+        const double ob = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(bidx, off, 64);
+        if (oi >= 0 && (bidx < 0 || ob > best || (ob == best && oi < bidx))) { best = ob; bidx = oi; }
+        flags |= __shfl_xor(flags, off, 64);
+    }
+    if (lane == 0) { rs.red_d[wv] = best; rs.red_i[wv] = bidx; rs.red_f[wv] = flags; }
+    __syncthreads();
+    best = rs.red_d[0]; bidx = rs.red_i[0]; flags = rs.red_f[0];
+    for (int i = 1; i < SP_WAVES; i++) {
+        const double ob = rs.red_d[i];
+        const int oi = rs.red_i[i];
+        if (oi >= 0 && (bidx < 0 || ob > best || (ob == best && oi < bidx))) { best = ob; bidx = oi; }
+        flags |= rs.red_f[i];
+    }
+    __syncthreads();
+    if ((flags & 1) || !(flags & 2)) {
+        if (tid == 0) a.row_rc[v] = -1;
+        return;
+    }
+    if (a.temperature == 0.0) {
+        for (int i = tid; i < V; i += SP_T) P[i] = i == bidx ? 1.0 : 0.0;
+        if (tid == 0) a.row_rc[v] = 0;
+        return;
+    }
+    const double mx = best, T = a.temperature;
+    for (int i = tid; i < V; i += SP_T) P[i] = ddiv(dsub(P[i], mx), T);
+    const bool use_k = a.top_k > 0 && a.top_k < V;
+    double kth = -INF;
+    if (use_k) {
+        __syncthreads();
+        kth = select_rank(P, V, V - a.top_k, (uint32_t *)smem, rs.bi);
+    }
+    for (int i = tid; i < V; i += SP_T) {
+        const double x = P[i];
+        P[i] = (use_k && x < kth) ? 0.0 : exp_port_d(x);
+    }
+    double s = np_sum(P, V, a.tail, lv, rs.bd);
+    for (int i = tid; i < V; i += SP_T) P[i] = ddiv(P[i], s);
+
+    if (a.top_p < 1.0) {
+        const double top_p = a.top_p, thr_hi = dmul(top_p, 1.0 + 0x1p-48);
+        uint32_t *hcnt = (uint32_t *)smem;
+        double *hmass = (double *)(smem + HBINS * 4);
+        for (int i = tid; i < HBINS; i += SP_T) { hcnt[i] = 0; hmass[i] = 0.0; }
+        __syncthreads();
+        for (int i = tid; i < V; i += SP_T) {
+            const double p = P[i];
+            if (p > 0.0) {
+                const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
+                atomicAdd(&hcnt[b], 1u);
+                atomicAdd(&hmass[b], p);
+            }
+        }
+        __syncthreads();
+        /* the highest bin b* whose suffix mass reaches top_p + 1e-9 (approximate sums) */
+        if (tid == 0) rs.bi[2] = -1;
+        __syncthreads();
+        {
+            const int b1 = 2 * (SP_T - 1 - tid) + 1, b0 = b1 - 1;   /* thread 0 holds the top bins */
+            const double m1 = hmass[b1], m0 = hmass[b0];
+            double inc = dadd(m1, m0);
+            for (int off = 1; off < 64; off <<= 1) {
+                const double y = __shfl_up(inc, off, 64);
+                if (lane >= off) inc = dadd(inc, y);
+            }
+            if (lane == 63) rs.red_d[wv] = inc;
+            __syncthreads();
+            double above = 0.0;
+            for (int i = 0; i < wv; i++) above = dadd(above, rs.red_d[i]);
+            const double excl = dadd(above, dsub(inc, dadd(m1, m0)));
+            const double s1 = dadd(excl, m1), s0 = dadd(s1, m0);
+            const double thr = top_p + 1e-9;
+            if (s0 >= thr) atomicMax(&rs.bi[2], s1 >= thr ? b1 : b0);
+        }
+        __syncthreads();
+        const int bstar = rs.bi[2];
+        /* tier 0: bins >= b* (all nonzero entries when b* < 0); tier 1: the rest */
+        double c = 0.0;
+        bool done = false;
+        for (int tier = 0; tier < 2 && !done; tier++) {
+            const int blo = tier == 0 ? (bstar < 0 ? 0 : bstar) : 0;
+            const int bhi = tier == 0 ? HBINS : bstar;
+            if (blo >= bhi) break;
+            /* count, then gather the tier's entries */
+            int cnt = 0;
+            for (int i = tid; i < V; i += SP_T) {
+                const double p = P[i];
+                const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
+                cnt += (p > 0.0 && b >= blo && b < bhi) ? 1 : 0;
+            }
+            int m;
+            const int off0 = wg_scan_excl(cnt, rs.red_i, &m);
+            (void)off0;
+            if (m == 0) continue;
+            int N = 1;
+            while (N < m) N <<= 1;
+            const bool in_lds = N <= SORT_LDS;
+            unsigned long long *key = in_lds ? (unsigned long long *)smem : a.skey + (size_t)v * a.sort_n;
+            int *idx = in_lds ? (int *)(smem + SORT_LDS * 8) : a.sidx + (size_t)v * a.sort_n;
+            if (tid == 0) rs.bi[3] = 0;
+            __syncthreads();
+            for (int i0 = 0; i0 < V; i0 += SP_T) {
+                const int i = i0 + tid;
+                const double p = i < V ? P[i] : 0.0;
+                const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
+                const bool cand = i < V && p > 0.0 && b >= blo && b < bhi;
+                const unsigned long long bal = __ballot(cand);
+                int base = 0;
+                if (lane == 0 && bal) base = atomicAdd(&rs.bi[3], __popcll(bal));
+                base = __shfl(base, 0, 64);
+                if (cand) {
+                    const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+                    key[pos] = (unsigned long long)__double_as_longlong(p);
+                    idx[pos] = i;
+                }
+            }
+            for (int j = m + tid; j < N; j += SP_T) { key[j] = 0ull; idx[j] = INT_MAX; }
+            __syncthreads();
+            if (in_lds) bitonic_block(key, idx, N, 2, N, N, 0);
+            else bitonic_global(key, idx, N, (unsigned long long *)smem, (int *)(smem + SORT_LDS * 8));
+            /* the sequential cumulative sum, one wave; decisions per entry */
+            if (wv == 0) {
+                int stop = m;
+                for (int base = 0; base < m; base += 64) {
+                    const int j = base + lane;
+                    const double ps = j < m ? __longlong_as_double((long long)key[j]) : 0.0;
+                    const int cnt2 = m - base < 64 ? m - base : 64;
+                    double cj = 0.0;
+                    for (int t = 0; t < cnt2; t++) {
+                        c = dadd(c, lane_value(ps, t));
+                        if (lane == t) cj = c;
+                    }
+                    if (j < m && dsub(cj, ps) >= top_p) P[idx[j]] = 0.0;
+                    if (c >= thr_hi) { stop = base + cnt2; break; }
+                }
+                if (lane == 0) { rs.bi[4] = stop; rs.bd[1] = c; }
+            }
+            __syncthreads();
+            const int stop = rs.bi[4];
+            c = rs.bd[1];
+            for (int j = stop + tid; j < m; j += SP_T) P[idx[j]] = 0.0;
+            if (stop < m || c >= thr_hi) {
+                done = true;
+                /* every entry below the tier is dropped */
+                if (blo > 0)
+                    for (int i = tid; i < V; i += SP_T) {
+                        const double p = P[i];
+                        const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
+                        if (p > 0.0 && b < blo) P[i] = 0.0;
+                    }
+            }
+            __syncthreads();
+        }
+        s = np_sum(P, V, a.tail, lv, rs.bd);
+        for (int i = tid; i < V; i += SP_T) P[i] = ddiv(P[i], s);
+    }
+    if (a.min_p > 0.0) {
+        double mp = -INF;
+        __syncthreads();
+        for (int i = tid; i < V; i += SP_T) mp = fmax(mp, P[i]);
+        mp = wg_max(mp, rs.red_d);
+        const double thr = dmul(a.min_p, mp);
+        for (int i = tid; i < V; i += SP_T)
+            if (P[i] < thr) P[i] = 0.0;
+        s = np_sum(P, V, a.tail, lv, rs.bd);
+        for (int i = tid; i < V; i += SP_T) P[i] = ddiv(P[i], s);
+    }
+    if (tid == 0) a.row_rc[v] = 0;
+}
+
+/* ---------------------------------------------------------------- the walk */
+
+/* inverse-CDF draw from w[0..V) (unnormalised, nonnegative, not all zero) with
+ * uniform u: np.cumsum order, first index whose running sum exceeds u * total */
+__device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *red, int *sh, double *shd) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int per = (V + SP_T - 1) / SP_T;
+    const int lo = tid * per < V ? tid * per : V, hi = lo + per < V ? lo + per : V;
+    int cnt = 0;
+    for (int i = lo; i < hi; i++) cnt += w[i] > 0.0 ? 1 : 0;
+    int nnz;
+    int o = wg_scan_excl(cnt, red, &nnz);
+    for (int i = lo; i < hi; i++)
+        if (w[i] > 0.0) { a.cw[o] = w[i]; a.ci[o] = i; o++; }
+    __syncthreads();
+    if ((tid >> 6) == 0) {
+        double c = 0.0;
+        for (int base = 0; base < nnz; base += 64) {
+            const int j = base + lane;
+            const double ps = j < nnz ? a.cw[j] : 0.0;
+            const int cnt2 = nnz - base < 64 ? nnz - base : 64;
+            double cj = 0.0;
+            for (int t = 0; t < cnt2; t++) {
+                c = dadd(c, lane_value(ps, t));
+                if (lane == t) cj = c;
+            }
+            if (j < nnz) a.cc[j] = cj;
+        }
+        if (lane == 0) shd[0] = c;
+    }
+    if (tid == 0) sh[0] = INT_MAX;
+    __syncthreads();
+    const double target = dmul(u, shd[0]);
+    for (int j = tid; j < nnz; j += SP_T)
+        if (a.cc[j] > target) { atomicMin(&sh[0], j); break; }
+    __syncthreads();
+    const int jb = sh[0];
+    const int r = jb < nnz ? a.ci[jb] : (nnz > 0 ? a.ci[nnz - 1] : 0);
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(SP_T) void k_sample_walk(SampleArgs a) {
+    __shared__ double lv[LV_MAX];
+    __shared__ int head[SAMPLE_NMAX], nxt[SAMPLE_NMAX];
+    __shared__ int red[SP_WAVES];
+    __shared__ int sh[4];
+    __shared__ double shd[4];
+    const int n = a.n, V = a.V, tid = threadIdx.x;
+    for (int i = tid; i < n; i += SP_T) head[i] = -1;
+    __syncthreads();
+    if (tid == 0)
+        for (int c = n - 1; c >= 1; c--) {
+            const int pa = a.parent[c];
+            nxt[c] = head[pa];
+            head[pa] = c;
+        }
+    __syncthreads();
+    int v = 0, np = 1, status = 0, fin = -1;
+    if (tid == 0) a.path[0] = 0;
+    for (;;) {
+        if (a.row_rc[v] != 0) { status = -1; break; }
+        const double *p = a.P + (size_t)v * V;
+        const double *qv = a.q ? a.q + (size_t)v * V : nullptr;
+        const double *r = nullptr;
+        double s = -1.0;                       /* < 0: p itself is the current distribution */
+        double *bufs[2] = {a.wa, a.wb};
+        int cur = 0, next = -1;
+        for (int c = head[v]; c >= 0; c = nxt[c]) {
+            const int x = a.tokens[c];
+            const double px = s < 0.0 ? p[x] : ddiv(r[x], s);
+            const double ratio = ddiv(px, qv ? qv[x] : 1.0);
+            if (a.u[2 * c] < ratio) { next = c; break; }
+            double *dst = bufs[cur];
+            for (int i = tid; i < V; i += SP_T) {
+                const double pc = s < 0.0 ? p[i] : ddiv(r[i], s);
+                const double qi = qv ? qv[i] : (i == x ? 1.0 : 0.0);
+                const double d = dsub(pc, qi);
+                dst[i] = d > 0.0 ? d : 0.0;
+            }
+            const double ns = np_sum(dst, V, a.tail, lv, shd + 2);
+            if (ns <= 0.0) { next = c; break; }
+            r = dst;
+            s = ns;
+            cur ^= 1;
+        }
+        if (next < 0) {
+            fin = draw(s < 0.0 ? p : r, V, a.u[2 * v + 1], a, red, sh, shd);
+            break;
+        }
+        if (tid == 0) a.path[np] = next;
+        np++;
+        v = next;
+    }
+    if (tid == 0) {
+        a.result[0] = np;
+        a.result[1] = fin;
+        a.result[2] = status;
+    }
+}
+
+} // namespace
+} // namespace hxd
+
+namespace hxl {
+
+namespace {
+
+int sort_len(int V) {
+    int N = SORT_LDS;
+    while (N < V) N <<= 1;
+    return N;
+}
+
+/* numpy's pairwise tree of the last partial buffer (length V % 8192) */
+void build_tail(int V, PwTail &t) {
+    t = PwTail{};
+    const int len = V % NP_BUF;
+    t.len = len;
+    if (len == 0) return;
+    std::vector<std::pair<int, int>> ops[12];
+    std::function<std::pair<int, int>(int, int)> rec = [&](int s, int n) -> std::pair<int, int> {
+        if (n <= 128) {
+            const int L = t.nleaf++;
+            t.leaf_start[L] = (unsigned short)s;
+            t.leaf_len[L] = (unsigned char)n;
+            return {L, 0};
+        }
+        int n2 = n / 2;
+        n2 -= n2 % 8;
+        const auto A = rec(s, n2), B = rec(s + n2, n - n2);
+        const int h = 1 + (A.second > B.second ? A.second : B.second);
+        ops[h].push_back({A.first, B.first});
+        return {A.first, h};
+    };
+    t.nlev = rec(0, len).second;
+    int o = 0;
+    t.lev_off[0] = 0;
+    for (int h = 1; h <= t.nlev; h++) {
+        for (const auto &op : ops[h]) {
+            t.op_a[o] = (unsigned char)op.first;
+            t.op_b[o] = (unsigned char)op.second;
+            o++;
+        }
+        t.lev_off[h] = (unsigned char)o;
+    }
+}
+
+template <class T> hipError_t grow(T *&p, size_t count) {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    return hipMalloc((void **)&p, sizeof(T) * (count ? count : 1));
+}
+
+} // namespace
+
+void SampleScratch::release() {
+    void *ps[] = {P, q, u, wa, wb, cw, cc, skey, sidx, ci, row_rc, path, result, ctx, tok, par};
+    for (void *p : ps)
+        if (p) (void)hipFree(p);
+    P = q = u = wa = wb = cw = cc = nullptr;
+    skey = nullptr;
+    sidx = ci = row_rc = path = result = ctx = tok = par = nullptr;
+    n_cap = V = ctx_cap = sort_n = 0;
+    has_q = false;
+}
+
+hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
+    hipError_t e = hipSuccess;
+    if (V_ != V) {
+        release();
+        V = V_;
+        sort_n = sort_len(V);
+        if ((e = grow(wa, V)) || (e = grow(wb, V)) || (e = grow(cw, V)) || (e = grow(cc, V)) || (e = grow(ci, V)) ||
+            (e = grow(result, 4)))
+            return e;
+    }
+    if (n > n_cap) {
+        const size_t rows = (size_t)n;
+        if ((e = grow(P, rows * V)) || (e = grow(skey, rows * sort_n)) || (e = grow(sidx, rows * sort_n)) ||
+            (e = grow(u, 2 * rows)) || (e = grow(row_rc, rows)) || (e = grow(path, rows)) || (e = grow(tok, rows)) ||
+            (e = grow(par, rows)))
+            return e;
+        if (has_q && (e = grow(q, rows * V))) return e;
+        n_cap = n;
+    }
+    if (need_q && !has_q) {
+        if ((e = grow(q, (size_t)n_cap * V))) return e;
+        has_q = true;
+    }
+    if (n_ctx > ctx_cap) {
+        if ((e = grow(ctx, (size_t)n_ctx))) return e;
+        ctx_cap = n_ctx;
+    }
+    return hipSuccess;
+}
+
+namespace {
+
+SampleArgs make_args(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                     const SamplerSpec &s, const double *q, const double *u, hipStream_t st) {
+    SampleArgs a{};
+    a.rows = rows; a.n = n; a.V = V; a.tokens = tok; a.parent = par;
+    a.temperature = s.temperature; a.top_p = s.top_p; a.min_p = s.min_p; a.rp = s.rp; a.top_k = s.top_k;
+    a.n_ctx = s.rp != 1.0 ? s.n_ctx : 0;
+    a.ctx = m.ctx;
+    a.q = q ? m.q : nullptr;
+    a.u = m.u;
+    a.P = m.P; a.skey = m.skey; a.sidx = m.sidx; a.sort_n = m.sort_n;
+    a.wa = m.wa; a.wb = m.wb; a.cw = m.cw; a.cc = m.cc; a.ci = m.ci;
+    a.row_rc = m.row_rc; a.path = m.path; a.result = m.result;
+    build_tail(V, a.tail);
+    if (q) (void)hipMemcpyAsync(m.q, q, sizeof(double) * (size_t)n * V, hipMemcpyHostToDevice, st);
+    if (u) (void)hipMemcpyAsync(m.u, u, sizeof(double) * 2 * (size_t)n, hipMemcpyHostToDevice, st);
+    if (a.n_ctx) (void)hipMemcpyAsync(m.ctx, s.ctx, sizeof(int) * (size_t)a.n_ctx, hipMemcpyHostToDevice, st);
+    return a;
+}
+
+} // namespace
+
+void accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                   const SamplerSpec &s, const double *q, const double *u, hipStream_t st) {
+    const SampleArgs a = make_args(m, rows, n, V, tok, par, s, q, u, st);
+    k_sample_probs<<<n, SP_T, 0, st>>>(a);
+    k_sample_walk<<<1, SP_T, 0, st>>>(a);
+}
+
+void sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                  const SamplerSpec &s, hipStream_t st) {
+    const SampleArgs a = make_args(m, rows, n, V, tok, par, s, nullptr, nullptr, st);
+    k_sample_probs<<<n, SP_T, 0, st>>>(a);
+}
+
+} // namespace hxl

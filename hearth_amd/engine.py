@@ -18,8 +18,8 @@ import numpy as np
 
 from . import _native
 
-__all__ = ["Engine", "HearthError", "HearthOptions", "HearthModelInfo", "HearthStats", "KStats", "POLICIES",
-           "PREFETCH", "ISAS"]
+__all__ = ["Engine", "HearthError", "HearthOptions", "HearthModelInfo", "HearthStats", "KStats", "HearthSampler",
+           "make_sampler", "chain_uniforms", "accept_greedy", "accept_sample", "gpu_probs", "POLICIES", "PREFETCH", "ISAS"]
 
 MAX_MIRRORS = 8
 
@@ -95,7 +95,40 @@ class KStats(Structure):
         ("head_s", c_double), ("dense_s", c_double),
         ("expert_launches", c_uint64), ("expert_bytes", c_uint64), ("dense_bytes", c_uint64), ("kv_bytes", c_uint64),
         ("expert_down_s", c_double), ("expert_down_bytes", c_uint64),
+        ("accept_s", c_double),
     ]
+
+
+class HearthSampler(Structure):
+    """hearth_sampler (include/hearth_gpu.h): the reference Sampler's settings."""
+    _fields_ = [
+        ("temperature", c_double), ("top_k", c_int32), ("top_p", c_double), ("min_p", c_double),
+        ("repetition_penalty", c_double), ("context", POINTER(c_int32)), ("n_context", c_int32),
+    ]
+
+
+def make_sampler(temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0, min_p: float = 0.0,
+                 repetition_penalty: float = 1.0, context=None) -> HearthSampler:
+    """A hearth_sampler; context (penalty ids) is kept alive by the returned struct."""
+    ctx = np.ascontiguousarray([] if context is None else context, dtype=np.int32)
+    s = HearthSampler(float(temperature), int(top_k), float(top_p), float(min_p), float(repetition_penalty),
+                      ctx.ctypes.data_as(POINTER(c_int32)) if ctx.size else None, int(ctx.size))
+    s._ctx = ctx
+    return s
+
+
+def chain_uniforms(stream, k: int) -> np.ndarray:
+    """Maps the reference's random stream of one verify step (generate.py:376-392 draws
+    one uniform per tried draft, then one for the final token) to hearth_verify_sample's
+    layout: u[2c] decides node c, u[2v + 1] draws at node v."""
+    r = np.asarray(stream, dtype=np.float64)
+    u = np.zeros(2 * (k + 1))
+    for c in range(1, k + 1):
+        u[2 * c] = r[c - 1]
+    for v in range(k):
+        u[2 * v + 1] = r[v + 1]
+    u[2 * k + 1] = r[k]
+    return u
 
 
 POLICIES = {"lru": 0, "lfu": 1}
@@ -122,6 +155,13 @@ _PROTOS = {
     "hearth_verify_tree": (c_int, [c_void_p, _I32P, _I32P, c_int, POINTER(c_float)]),
     "hearth_commit_path": (c_int, [c_void_p, _I32P, c_int]),
     "hearth_verify_greedy": (c_int, [c_void_p, _I32P, _I32P, c_int, _I32P, POINTER(c_int), _I32P, POINTER(c_float)]),
+    "hearth_verify_sample": (c_int, [c_void_p, _I32P, _I32P, c_int, POINTER(HearthSampler), POINTER(c_double),
+                                     POINTER(c_double), _I32P, POINTER(c_int), _I32P, POINTER(c_float)]),
+    "hearth_gpu_accept_greedy": (c_int, [POINTER(c_float), c_int, c_int, _I32P, _I32P, _I32P, POINTER(c_int), _I32P]),
+    "hearth_gpu_accept_sample": (c_int, [POINTER(c_float), c_int, c_int, _I32P, _I32P, POINTER(HearthSampler),
+                                         POINTER(c_double), POINTER(c_double), _I32P, POINTER(c_int), _I32P]),
+    "hearth_gpu_probs": (c_int, [POINTER(c_float), c_int, c_int, _I32P, _I32P, POINTER(HearthSampler),
+                                 POINTER(c_double)]),
     "hearth_gpu_set_profiling": (c_int, [c_void_p, c_int]),
     "hearth_gpu_get_kstats": (c_int, [c_void_p, POINTER(KStats)]),
     "hearth_gpu_reset_kstats": (None, [c_void_p]),
@@ -341,6 +381,49 @@ class Engine:
             raise HearthError(f"hearth_verify_greedy failed (code {rc}): {_ERRORS.get(rc, 'unknown error')}")
         return path[:npath.value].tolist(), int(fin[0]), lg
 
+    def verify_sample(self, tokens, parent=None, sampler: HearthSampler | None = None, q=None, u=None,
+                      want_logits: bool = False):
+        """Evaluates [last] + draft (chain, or tree given parent), accepts by speculative
+        sampling on the GPU (point-mass drafts when q is None, else q [n][V] float64 row v
+        = the distribution v's children were drafted from; u [2n] uniforms) and commits
+        the accepted path. Returns (path, final_token, logits or None)."""
+        ids = _i32(tokens)
+        n = int(ids.size)
+        par = None if parent is None else _i32(parent)
+        smp = sampler if sampler is not None else make_sampler()
+        uu = np.ascontiguousarray(u, dtype=np.float64)
+        if uu.size < 2 * n:
+            raise ValueError(f"need {2 * n} uniforms, got {uu.size}")
+        qq = None if q is None else np.ascontiguousarray(q, dtype=np.float64)
+        if qq is not None and qq.size != n * self._vocab:
+            raise ValueError("q must be [n][vocab]")
+        path = np.empty(max(n, 1), dtype=np.int32)
+        npath, fin = c_int(0), np.zeros(1, dtype=np.int32)
+        lg = np.empty((n, self._vocab), dtype=np.float32) if want_logits else None
+        with self._lock:
+            rc = self._api.need("verify_sample")(
+                self._handle(), ids.ctypes.data_as(_I32P), None if par is None else par.ctypes.data_as(_I32P), n,
+                byref(smp), None if qq is None else qq.ctypes.data_as(POINTER(c_double)),
+                uu.ctypes.data_as(POINTER(c_double)), path.ctypes.data_as(_I32P), byref(npath),
+                fin.ctypes.data_as(_I32P), None if lg is None else lg.ctypes.data_as(POINTER(c_float)))
+        if rc < 0:
+            raise HearthError(f"hearth_verify_sample failed (code {rc}): {_ERRORS.get(rc, 'unknown error')}")
+        return path[:npath.value].tolist(), int(fin[0]), lg
+
+    def verify_sample_chain(self, last: int, draft, sampler: HearthSampler, rng: np.random.Generator):
+        """One sampled verify step of generate() (generate.py:376-392) with the GPU doing
+        the acceptance: consumes exactly the uniforms the reference consumes from rng (one
+        per tried draft, one for the final token). Returns (n_accepted, final_token)."""
+        k = len(draft)
+        state = rng.bit_generator.state
+        stream = rng.random(k + 1)
+        path, fin, _ = self.verify_sample([int(last)] + [int(d) for d in draft], None, sampler,
+                                          u=chain_uniforms(stream, k))
+        n_acc = len(path) - 1
+        rng.bit_generator.state = state
+        rng.random(n_acc + (1 if n_acc < k else 0) + 1)
+        return n_acc, fin
+
     def verify_tree(self, tokens, parent, want_logits: bool = True):
         ids, par = _i32(tokens), _i32(parent)
         n = int(ids.size)
@@ -410,3 +493,50 @@ class Engine:
 
     def __repr__(self) -> str:
         return f"Engine({self.model_path!r}, {'closed' if self._h is None else f'pos={self.pos}'})"
+
+
+def accept_greedy(rows, tokens, parent=None, lib_path=None):
+    """hearth_gpu_accept_greedy on caller logits rows [n][V]: (rc, path, final_token)."""
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    n, V = rows.shape
+    t = _i32(tokens)
+    p = _i32(parent if parent is not None else np.arange(-1, n - 1))
+    path = np.zeros(n, dtype=np.int32)
+    npath, fin = c_int(0), np.zeros(1, dtype=np.int32)
+    rc = _api(lib_path).need("gpu_accept_greedy")(rows.ctypes.data_as(POINTER(c_float)), n, V, t.ctypes.data_as(_I32P),
+                                                  p.ctypes.data_as(_I32P), path.ctypes.data_as(_I32P), byref(npath),
+                                                  fin.ctypes.data_as(_I32P))
+    return rc, path[:npath.value].tolist(), int(fin[0])
+
+
+def accept_sample(rows, tokens, parent=None, sampler: HearthSampler | None = None, q=None, u=None, lib_path=None):
+    """hearth_gpu_accept_sample on caller logits rows [n][V]: (rc, path, final_token)."""
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    n, V = rows.shape
+    t = _i32(tokens)
+    p = _i32(parent if parent is not None else np.arange(-1, n - 1))
+    smp = sampler if sampler is not None else make_sampler()
+    uu = np.ascontiguousarray(np.zeros(2 * n) if u is None else u, dtype=np.float64)
+    qq = None if q is None else np.ascontiguousarray(q, dtype=np.float64)
+    path = np.zeros(n, dtype=np.int32)
+    npath, fin = c_int(0), np.zeros(1, dtype=np.int32)
+    rc = _api(lib_path).need("gpu_accept_sample")(
+        rows.ctypes.data_as(POINTER(c_float)), n, V, t.ctypes.data_as(_I32P), p.ctypes.data_as(_I32P), byref(smp),
+        None if qq is None else qq.ctypes.data_as(POINTER(c_double)), uu.ctypes.data_as(POINTER(c_double)),
+        path.ctypes.data_as(_I32P), byref(npath), fin.ctypes.data_as(_I32P))
+    return rc, path[:npath.value].tolist(), int(fin[0])
+
+
+def gpu_probs(rows, tokens=None, parent=None, sampler: HearthSampler | None = None, lib_path=None):
+    """hearth_gpu_probs: (rc, float64 [n][V] distributions) of caller logits rows."""
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    if rows.ndim == 1:
+        rows = rows.reshape(1, -1)
+    n, V = rows.shape
+    t = _i32(np.zeros(n) if tokens is None else tokens)
+    p = _i32(parent if parent is not None else np.arange(-1, n - 1))
+    smp = sampler if sampler is not None else make_sampler()
+    out = np.zeros((n, V), dtype=np.float64)
+    rc = _api(lib_path).need("gpu_probs")(rows.ctypes.data_as(POINTER(c_float)), n, V, t.ctypes.data_as(_I32P),
+                                          p.ctypes.data_as(_I32P), byref(smp), out.ctypes.data_as(POINTER(c_double)))
+    return rc, out

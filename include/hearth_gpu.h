@@ -47,6 +47,54 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
 HEARTH_API int hearth_gpu_accept_greedy(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
                                         int32_t *path_out, int *n_path, int32_t *final_tok);
 
+/* Sampler settings of sampled acceptance: the fields of the reference's Sampler
+ * (python/hearth/generate.py:31-56) with its validation. temperature 0 gives the one-hot
+ * argmax distribution; top_k 0, top_p 1, min_p 0 and repetition_penalty 1 are "off".
+ * The penalty applies to the distinct ids of context[0..n_context) (normally the
+ * committed sequence, ending with tokens[0]) plus, for node v, the draft tokens of the
+ * path nodes 1..v (generate.py:380: full[:len(seq) + i]). */
+typedef struct hearth_sampler {
+    double temperature;
+    int32_t top_k;
+    double top_p;
+    double min_p;
+    double repetition_penalty;
+    const int32_t *context;
+    int32_t n_context;
+} hearth_sampler;
+
+/* Sampled speculative verification in one call, acceptance on the GPU in float64 with
+ * the reference's operation order (Sampler.probs, accept_point_mass, draw;
+ * generate.py:84-147,365-392). Children of a node are tried in index order: child c
+ * (token x) is accepted when u[2c] < p_cur[x] / q_v[x], where p_cur is the node's
+ * distribution, after each rejected child replaced by max(0, p_cur - q_v) renormalised;
+ * if no child is accepted the next token is drawn from p_cur by inverse CDF with
+ * u[2v + 1]. q == NULL: every draft is a point mass (q_v = one-hot of the child's token,
+ * the reference's case); otherwise q is [n][V] float64 and row v is the distribution
+ * v's children were drafted from. u: [2n] uniforms in [0, 1). For a chain, the
+ * reference's random stream r0, r1, ... maps to u[2c] = r[c-1] (c = 1..k),
+ * u[2v+1] = r[v+1] (v < k) and u[2k+1] = r[k]. Commits the accepted path like
+ * hearth_verify_greedy. Returns -1 for bad settings or when a visited row has
+ * NaN/+inf/only -inf logits (the reference raises ValueError there). V <= 262144,
+ * n <= 4096. logits: NULL or [n][vocab]. */
+HEARTH_API int hearth_verify_sample(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,
+                                    const hearth_sampler *s, const double *q, const double *u, int32_t *path_out,
+                                    int *n_path, int32_t *final_tok, float *logits);
+
+/* The sampled acceptance alone on caller logits rows [n][V] (no engine); same result as
+ * hearth_verify_sample's walk. */
+HEARTH_API int hearth_gpu_accept_sample(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
+                                        const hearth_sampler *s, const double *q, const double *u,
+                                        int32_t *path_out, int *n_path, int32_t *final_tok);
+
+/* Sampler.probs on the GPU for every row of caller logits rows [n][V] (float64 result
+ * p_out [n][V], the distributions hearth_gpu_accept_sample works with). The penalty
+ * context of row v is s->context plus the tokens of the path nodes 1..v of the tree
+ * given by tokens/parent (parent NULL: chain). Returns -1 if a row has NaN/+inf/only
+ * -inf logits. */
+HEARTH_API int hearth_gpu_probs(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
+                                const hearth_sampler *s, double *p_out);
+
 /* GPU time per kernel class, accumulated while profiling is on (HIP event pairs on the
  * engine's stream; see hearth_gpu_set_profiling for the levels). */
 typedef struct hearth_gpu_kstats {
@@ -62,6 +110,7 @@ typedef struct hearth_gpu_kstats {
     uint64_t kv_bytes;          /* KV bytes read by attention (each row once per call and head group) */
     double expert_down_s;       /* SwiGLU activation quantization + grouped expert down projection */
     uint64_t expert_down_bytes; /* algorithmic weight bytes of the active experts' down matrices */
+    double accept_s;            /* device acceptance (greedy argmax + walk, or sampled) */
 } hearth_gpu_kstats;
 
 /* level 0: off; 1: HIP events around the grouped expert launches only (expert_s,

@@ -1075,8 +1075,8 @@ int ho_commit_path(ho_model *m, const int32_t *path, int n) {
 
 /* ------------------------------------------------------------ acceptance (generate.py) */
 
-/* numpy float64 add.reduce over a contiguous array: 0.0 + pairwise sum with 8
- * accumulators over blocks of <= 128 (numpy's pairwise summation). */
+/* numpy's pairwise summation of one contiguous run: 8 accumulators over blocks of at
+ * most 128, halves split at multiples of 8. */
 static double np_pairwise(const double *a, int64_t n) {
     if (n < 8) {
         double r = 0.0;
@@ -1097,7 +1097,16 @@ static double np_pairwise(const double *a, int64_t n) {
     n2 -= n2 % 8;
     return np_pairwise(a, n2) + np_pairwise(a + n2, n - n2);
 }
-static double np_sum(const double *a, int64_t n) { return 0.0 + np_pairwise(a, n); }
+
+/* numpy float64 add.reduce over a contiguous array: the reduction runs over buffers of
+ * 8192 elements (numpy's default buffer size), each summed pairwise and added in order
+ * to the accumulator, which starts at the identity 0.0. */
+double ho_np_sum(const double *a, int64_t n) {
+    double s = 0.0;
+    for (int64_t i = 0; i < n; i += 8192) s = s + np_pairwise(a + i, n - i < 8192 ? n - i : 8192);
+    return s;
+}
+#define np_sum ho_np_sum
 
 static int bad_logits(const float *x, int V) {
     int all_neg_inf = 1;
@@ -1130,21 +1139,44 @@ static int cmp_dbl(const void *a, const void *b) {
     return x < y ? -1 : (x > y);
 }
 
-int ho_probs(const float *logits, int V, double T, int top_k, double top_p, double min_p, double *p) {
+/* Sampler._penalised (generate.py:68-79) once the row has passed the logits check:
+ * the row as float64, and each distinct id in [0, V) of the context (s->context plus
+ * extra) divided by the penalty where positive, multiplied by it otherwise. */
+static void penalised(const float *logits, int V, const ho_sampler *s, const int32_t *extra, int n_extra, double *x) {
+    for (int i = 0; i < V; i++) x[i] = (double)logits[i];
+    const double rp = s->repetition_penalty;
+    if (rp == 1.0 || (s->n_context <= 0 && n_extra <= 0)) return;
+    uint8_t *mark = calloc((size_t)V, 1);
+    for (int j = 0; j < s->n_context; j++)
+        if (s->context[j] >= 0 && s->context[j] < V) mark[s->context[j]] = 1;
+    for (int j = 0; j < n_extra; j++)
+        if (extra[j] >= 0 && extra[j] < V) mark[extra[j]] = 1;
+    for (int i = 0; i < V; i++)
+        if (mark[i]) x[i] = x[i] > 0.0 ? x[i] / rp : x[i] * rp;
+    free(mark);
+}
+
+/* Sampler.probs (generate.py:84-111) with the penalty context s->context + extra. */
+static int probs_core(const float *logits, int V, const ho_sampler *sp, const int32_t *extra, int n_extra, double *p) {
     if (V < 1 || bad_logits(logits, V)) return -1;
+    penalised(logits, V, sp, extra, n_extra, p);
+    const double T = sp->temperature;
     if (T == 0.0) {
+        int best = 0;
+        for (int i = 1; i < V; i++)
+            if (p[i] > p[best]) best = i;
         for (int i = 0; i < V; i++) p[i] = 0.0;
-        p[ho_argmax(logits, V)] = 1.0;
+        p[best] = 1.0;
         return 0;
     }
-    double mx = (double)logits[0];
-    for (int i = 1; i < V; i++) mx = (double)logits[i] > mx ? (double)logits[i] : mx;
-    for (int i = 0; i < V; i++) p[i] = ((double)logits[i] - mx) / T;
-    if (top_k > 0 && top_k < V) {
+    double mx = p[0];
+    for (int i = 1; i < V; i++) mx = p[i] > mx ? p[i] : mx;
+    for (int i = 0; i < V; i++) p[i] = (p[i] - mx) / T;
+    if (sp->top_k > 0 && sp->top_k < V) {
         double *tmp = malloc(sizeof(double) * V);
         memcpy(tmp, p, sizeof(double) * V);
         qsort(tmp, (size_t)V, sizeof(double), cmp_dbl);
-        const double kth = tmp[V - top_k];
+        const double kth = tmp[V - sp->top_k];
         for (int i = 0; i < V; i++)
             if (p[i] < kth) p[i] = -1.0 / 0.0;
         free(tmp);
@@ -1152,7 +1184,7 @@ int ho_probs(const float *logits, int V, double T, int top_k, double top_p, doub
     for (int i = 0; i < V; i++) p[i] = ho_exp_port_d(p[i]);
     double s = np_sum(p, V);
     for (int i = 0; i < V; i++) p[i] = p[i] / s;
-    if (top_p < 1.0) {
+    if (sp->top_p < 1.0) {
         int *order = malloc(sizeof(int) * V);
         for (int i = 0; i < V; i++) order[i] = i;
         g_sort_key = p;
@@ -1163,7 +1195,7 @@ int ho_probs(const float *logits, int V, double T, int top_k, double top_p, doub
             const double ps = p[order[j]];
             c = c + ps;
             const double before = c - ps;
-            if (before >= top_p) drop[order[j]] = 1;
+            if (before >= sp->top_p) drop[order[j]] = 1;
         }
         for (int i = 0; i < V; i++)
             if (drop[i]) p[i] = 0.0;
@@ -1172,16 +1204,25 @@ int ho_probs(const float *logits, int V, double T, int top_k, double top_p, doub
         free(order);
         free(drop);
     }
-    if (min_p > 0.0) {
+    if (sp->min_p > 0.0) {
         double mp = p[0];
         for (int i = 1; i < V; i++) mp = p[i] > mp ? p[i] : mp;
-        const double thr = min_p * mp;
+        const double thr = sp->min_p * mp;
         for (int i = 0; i < V; i++)
             if (p[i] < thr) p[i] = 0.0;
         s = np_sum(p, V);
         for (int i = 0; i < V; i++) p[i] = p[i] / s;
     }
     return 0;
+}
+
+int ho_probs(const float *logits, int V, double T, int top_k, double top_p, double min_p, double *p) {
+    const ho_sampler s = {T, top_k, top_p, min_p, 1.0, NULL, 0};
+    return probs_core(logits, V, &s, NULL, 0, p);
+}
+
+int ho_probs_s(const float *logits, int V, const ho_sampler *s, const int32_t *extra, int n_extra, double *p) {
+    return probs_core(logits, V, s, extra, n_extra, p);
 }
 
 /* first i with c[i] > u (np.searchsorted side="right"), clamped, stepped back over
@@ -1229,24 +1270,30 @@ int ho_accept_point_mass(const double *p, int V, int d, double u0, double u1, in
 /* Tree acceptance; see the header. The residual after a rejected child is kept
  * unnormalised (r) with its float64 sum s, so that for one child per node every step
  * is exactly generate.py's accept_point_mass; a following sibling is accepted with
- * probability (r[x] / s) / q[x]. */
-int ho_accept_tree(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
-                   int mode, double T, int top_k, double top_p, double min_p,
-                   const double *q, const double *u, int32_t *path, int *n_path, int *final_tok) {
+ * probability (r[x] / s) / q[x]. The penalty context of node v is sp->context plus the
+ * tokens of the path nodes 1..v (generate.py:380: full[:len(seq) + i]). */
+static int accept_tree_core(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent, int mode,
+                            const ho_sampler *sp, const double *q, const double *u, int32_t *path, int *n_path,
+                            int *final_tok) {
     int v = 0, np_ = 0, rc = 0;
     double *p = malloc(sizeof(double) * V), *r = malloc(sizeof(double) * V), *qq = malloc(sizeof(double) * V);
+    int32_t *extra = malloc(sizeof(int32_t) * (n > 0 ? n : 1));
     path[np_++] = 0;
     for (;;) {
         const float *row = rows + (size_t)v * V;
         int next = -1;
+        for (int j = 1; j < np_; j++) extra[j - 1] = tokens[path[j]];
         if (mode == 0) {
-            const int t = ho_argmax(row, V);
-            if (t < 0) { rc = -1; break; }
+            if (V < 1 || bad_logits(row, V)) { rc = -1; break; }
+            penalised(row, V, sp, extra, np_ - 1, p);
+            int t = 0;
+            for (int i = 1; i < V; i++)
+                if (p[i] > p[t]) t = i;
             for (int c = v + 1; c < n; c++)
                 if (parent[c] == v && tokens[c] == t) { next = c; break; }
             if (next < 0) { *final_tok = t; break; }
         } else {
-            if (ho_probs(row, V, T, top_k, top_p, min_p, p) != 0) { rc = -1; break; }
+            if (probs_core(row, V, sp, extra, np_ - 1, p) != 0) { rc = -1; break; }
             double s = -1.0;   /* < 0: p itself is the current distribution */
             int done = 0;
             for (int c = v + 1; c < n && !done; c++) {
@@ -1283,8 +1330,21 @@ int ho_accept_tree(const float *rows, int n, int V, const int32_t *tokens, const
         v = next;
     }
     *n_path = np_;
-    free(p); free(r); free(qq);
+    free(p); free(r); free(qq); free(extra);
     return rc;
+}
+
+int ho_accept_tree(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
+                   int mode, double T, int top_k, double top_p, double min_p,
+                   const double *q, const double *u, int32_t *path, int *n_path, int *final_tok) {
+    const ho_sampler s = {T, top_k, top_p, min_p, 1.0, NULL, 0};
+    return accept_tree_core(rows, n, V, tokens, parent, mode, &s, q, u, path, n_path, final_tok);
+}
+
+int ho_accept_tree_s(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
+                     const ho_sampler *s, const double *q, const double *u, int32_t *path, int *n_path,
+                     int *final_tok) {
+    return accept_tree_core(rows, n, V, tokens, parent, q ? 2 : 1, s, q, u, path, n_path, final_tok);
 }
 
 int ho_accept_chain(const float *rows, int k, int V, const int32_t *drafts, int mode,

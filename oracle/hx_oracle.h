@@ -96,10 +96,31 @@ void      ho_set_threads(ho_model *m, int n);
 void      ho_set_dump(ho_model *m, const char *dir);
 
 /* ---- acceptance ----------------------------------------------------------- */
+/* Sampler settings (generate.py:31-56): temperature 0 = one-hot argmax; top_k 0 = off;
+ * top_p 1 = off; min_p 0 = off; repetition_penalty 1 = off. context: the tokens the
+ * penalty applies to (the committed sequence, normally ending with the verify root's
+ * token); each node of a verify tree adds its path's draft tokens (nodes 1..v). */
+typedef struct ho_sampler {
+    double temperature;
+    int top_k;
+    double top_p;
+    double min_p;
+    double repetition_penalty;
+    const int32_t *context;
+    int n_context;
+} ho_sampler;
+
+/* numpy's float64 sum of a contiguous array, as `p.sum()` computes it in generate.py:
+ * 0.0, then in order the pairwise sum (8 accumulators over blocks of at most 128) of
+ * each 8192-element buffer. */
+double ho_np_sum(const double *a, int64_t n);
 /* Sampler.probs (generate.py:84-111) on one row of f32 logits: float64 result.
  * temperature 0 = one-hot argmax. Returns 0, or -1 for NaN/+inf/all -inf logits. */
 int ho_probs(const float *logits, int V, double temperature, int top_k, double top_p, double min_p,
              double *p_out);
+/* The same with the repetition penalty (Sampler._penalised, generate.py:68-79) over
+ * s->context plus extra[0..n_extra). */
+int ho_probs_s(const float *logits, int V, const ho_sampler *s, const int32_t *extra, int n_extra, double *p_out);
 /* Greedy argmax, first index on ties; -1 on NaN/+inf/all -inf. */
 int ho_argmax(const float *logits, int V);
 /* Inverse-CDF draw (generate.py:113-121) with a given uniform u in [0,1). */
@@ -111,10 +132,10 @@ int ho_accept_point_mass(const double *p, int V, int d, double u0, double u1, in
  * min(1, p[d]/q[d]) (u0 < p[d]/q[d]); on rejection draw from max(0, p - q) normalised
  * (u1). Reduces to ho_accept_point_mass when q is one-hot on d. */
 int ho_accept_general(const double *p, const double *q, int V, int d, double u0, double u1, int *tok);
-/* Chain verification (generate.py:365-392): rows [k+1][V], drafts[k]. mode 0 greedy,
- * 1 point-mass sampling, 2 general q (q [k][V] float64). Uniforms: u[2i] decides draft
- * i, u[2i+1] draws its correction, u[2k] draws the bonus token. Writes n_acc and the
- * final token; returns 0 or -1 (bad logits). */
+/* Chain verification (generate.py:365-392): rows [k+1][V], drafts[k] (node i + 1 holds
+ * draft i). mode 0 greedy, 1 point-mass sampling, 2 general q (q [k+1][V] float64, row
+ * i = the distribution draft i was drawn from). Uniforms as for ho_accept_tree (2k + 2
+ * entries). Writes n_acc and the final token; returns 0 or -1 (bad logits). */
 int ho_accept_chain(const float *rows, int k, int V, const int32_t *drafts, int mode,
                     double temperature, int top_k, double top_p, double min_p,
                     const double *q, const double *u, int *n_acc, int *final_tok);
@@ -124,12 +145,19 @@ int ho_accept_chain(const float *rows, int k, int V, const int32_t *drafts, int 
  * sampling, SpecInfer-style): accept child c with prob min(1, p[c.tok]/q_c[c.tok]); on
  * rejection p := norm(max(0, p - q_c)) and the next child is tried; if none is accepted
  * the correction is drawn from the current p. Greedy (mode 0): the child whose token is
- * argmax(p) is taken. q: [n][V] float64 draft distribution per node (row of the node
- * being tried; unused for greedy / point-mass). u: 2 per node + 1. path_out gets the
- * accepted node ids from the root (path_out[0] = 0), *n_path their count, *final_tok. */
+ * argmax(p) is taken. q: [n][V] float64, row v = the draft distribution of v's children
+ * (unused for greedy / point-mass). u: [2n] uniforms in [0, 1): u[2c] decides child c,
+ * u[2v + 1] draws the token at node v (the correction, or the bonus at a leaf).
+ * path_out gets the accepted node ids from the root (path_out[0] = 0), *n_path their
+ * count, *final_tok the token that follows. */
 int ho_accept_tree(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
                    int mode, double temperature, int top_k, double top_p, double min_p,
                    const double *q, const double *u, int32_t *path_out, int *n_path, int *final_tok);
+/* ho_accept_tree with a sampler (penalty included): point-mass mode when q is NULL,
+ * general-q mode otherwise; temperature 0 gives the one-hot distribution. */
+int ho_accept_tree_s(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
+                     const ho_sampler *s, const double *q, const double *u, int32_t *path_out, int *n_path,
+                     int *final_tok);
 
 #ifdef __cplusplus
 }

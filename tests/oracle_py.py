@@ -20,6 +20,20 @@ _I32P, _FP, _DP = POINTER(c_int32), POINTER(c_float), POINTER(c_double)
 _lib = None
 
 
+class Sampler(ctypes.Structure):
+    """ho_sampler (oracle/hx_oracle.h)."""
+    _fields_ = [("temperature", c_double), ("top_k", c_int), ("top_p", c_double), ("min_p", c_double),
+                ("repetition_penalty", c_double), ("context", _I32P), ("n_context", c_int)]
+
+
+def sampler(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, repetition_penalty=1.0, context=()):
+    ctx = np.ascontiguousarray(context, dtype=np.int32)
+    s = Sampler(temperature, top_k, top_p, min_p, repetition_penalty,
+                ctx.ctypes.data_as(_I32P) if ctx.size else None, int(ctx.size))
+    s._keep = ctx
+    return s
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -56,6 +70,11 @@ def lib():
         L.ho_accept_general.argtypes = [_DP, _DP, c_int, c_int, c_double, c_double, POINTER(c_int)]
         L.ho_accept_tree.argtypes = [_FP, c_int, c_int, _I32P, _I32P, c_int, c_double, c_int, c_double, c_double,
                                      _DP, _DP, _I32P, POINTER(c_int), POINTER(c_int)]
+        L.ho_np_sum.restype = c_double
+        L.ho_np_sum.argtypes = [_DP, c_int64]
+        L.ho_probs_s.argtypes = [_FP, c_int, POINTER(Sampler), _I32P, c_int, _DP]
+        L.ho_accept_tree_s.argtypes = [_FP, c_int, c_int, _I32P, _I32P, POINTER(Sampler), _DP, _DP, _I32P,
+                                       POINTER(c_int), POINTER(c_int)]
         _lib = L
     return _lib
 
@@ -158,3 +177,34 @@ def probs(logits, temperature, top_k=0, top_p=1.0, min_p=0.0):
     out = np.empty(x.size, dtype=np.float64)
     rc = lib().ho_probs(x.ctypes.data_as(_FP), x.size, temperature, top_k, top_p, min_p, out.ctypes.data_as(_DP))
     return rc, out
+
+
+def np_sum(a) -> float:
+    x = np.ascontiguousarray(a, dtype=np.float64)
+    return lib().ho_np_sum(x.ctypes.data_as(_DP), x.size)
+
+
+def probs_s(logits, s: Sampler, extra=()):
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    e = np.ascontiguousarray(extra, dtype=np.int32)
+    out = np.empty(x.size, dtype=np.float64)
+    rc = lib().ho_probs_s(x.ctypes.data_as(_FP), x.size, ctypes.byref(s), e.ctypes.data_as(_I32P) if e.size else None,
+                          int(e.size), out.ctypes.data_as(_DP))
+    return rc, out
+
+
+def accept_tree_s(rows, tokens, parent, s: Sampler, q=None, u=None):
+    """Sampled tree acceptance with a sampler: point-mass when q is None, general q
+    otherwise. Returns (rc, path, final token)."""
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    n, V = rows.shape
+    t = np.ascontiguousarray(tokens, dtype=np.int32)
+    p = np.ascontiguousarray(parent, dtype=np.int32)
+    qq = None if q is None else np.ascontiguousarray(q, dtype=np.float64)
+    uu = np.zeros(2 * n) if u is None else np.ascontiguousarray(u, dtype=np.float64)
+    path = np.zeros(n, dtype=np.int32)
+    npath, fin = c_int(0), c_int(0)
+    rc = lib().ho_accept_tree_s(rows.ctypes.data_as(_FP), n, V, t.ctypes.data_as(_I32P), p.ctypes.data_as(_I32P),
+                                ctypes.byref(s), None if qq is None else qq.ctypes.data_as(_DP), uu.ctypes.data_as(_DP),
+                                path.ctypes.data_as(_I32P), ctypes.byref(npath), ctypes.byref(fin))
+    return rc, path[:npath.value].tolist(), fin.value
