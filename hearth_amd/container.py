@@ -211,8 +211,13 @@ def uniforms(seed: int, n: int) -> np.ndarray:
 
 @dataclass
 class Shape:
-    """Hyper-parameters of a synthetic Qwen3-MoE-style (GQA, per-head qk-norm, NEOX
-    RoPE, softmax top-k with norm_topk_prob) model."""
+    """Hyper-parameters of a synthetic MoE model. The defaults are Qwen3-MoE (GQA,
+    per-head qk-norm, NEOX RoPE, softmax top-k with norm_topk_prob); the other fields
+    select the FORMAT.md variants of the other supported families (q/k/v biases and a
+    gated shared expert as Qwen2-MoE, full-width qk-norm as OLMoE, sigmoid scores with a
+    selection bias, group-limited routing, routed scale, leading dense layers and a
+    shared expert as DeepSeek-V3, partial and interleaved RoPE, tied embeddings,
+    embedding/residual/logit scales)."""
     n_layers: int
     d_model: int
     n_heads: int
@@ -225,25 +230,71 @@ class Shape:
     max_seq: int = 4096
     rope_theta: float = 1e6
     arch: str = "qwen3_moe"
+    qk_norm: int = 1
+    qkv_bias: int = 0
+    rope_dim: int = 0            # 0: head_dim
+    rope_style: int = 0
+    shared_ffn: int = 0
+    shared_gate: int = 0
+    score_fn: int = 0
+    score_bias: int = 0
+    n_group: int = 1
+    topk_group: int = 1
+    norm_topk: int = 1
+    routed_scale: float = 1.0
+    n_dense: int = 0             # leading dense (layer_kind 0) layers
+    dense_ffn: int = 0
+    tie: int = 0
+    emb_scale: float = 1.0
+    resid_scale: float = 1.0
+    logit_scale: float = 1.0
 
 
 TINY = Shape(n_layers=4, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, n_experts=16, top_k=4,
              expert_ffn=256, vocab=4096, max_seq=1024)
+# Small models of the other families, for parity tests of the FORMAT.md variants.
+TINY_DSV3_GQA = Shape(n_layers=4, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, n_experts=16, top_k=4,
+                      expert_ffn=256, vocab=4096, max_seq=1024, arch="deepseek_v3", qk_norm=0, rope_style=1,
+                      shared_ffn=256, score_fn=1, score_bias=1, n_group=4, topk_group=2, norm_topk=1,
+                      routed_scale=2.5, n_dense=1, dense_ffn=512)
+TINY_QWEN2 = Shape(n_layers=3, d_model=512, n_heads=8, n_kv_heads=4, head_dim=64, n_experts=16, top_k=4,
+                   expert_ffn=192, vocab=4096, max_seq=1024, arch="qwen2_moe", qk_norm=0, qkv_bias=1,
+                   shared_ffn=384, shared_gate=1, norm_topk=0)
+TINY_OLMOE = Shape(n_layers=3, d_model=512, n_heads=8, n_kv_heads=8, head_dim=64, n_experts=16, top_k=4,
+                   expert_ffn=256, vocab=4096, max_seq=1024, arch="olmoe", qk_norm=2, norm_topk=0, rope_dim=32,
+                   tie=1, emb_scale=1.5, resid_scale=0.75, logit_scale=0.5)
+TINY_VARIANTS = {"dsv3_gqa": TINY_DSV3_GQA, "qwen2": TINY_QWEN2, "olmoe": TINY_OLMOE}
+
 QWEN3_30B_A3B = Shape(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_dim=128, n_experts=128, top_k=8,
                       expert_ffn=768, vocab=151936, max_seq=8192)
 
 
+def _rope_dim(s: Shape) -> int:
+    return s.rope_dim or s.head_dim
+
+
 def _meta(s: Shape, source: str) -> dict:
-    return dict(arch=s.arch, n_layers=s.n_layers, d_model=s.d_model, vocab_size=s.vocab, max_seq=s.max_seq,
-                norm_eps=1e-6, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, qk_norm=1,
-                rope_dim=s.head_dim, attn_scale=float(np.float32(1.0 / math.sqrt(s.head_dim))),
-                n_experts=s.n_experts, top_k=s.top_k, expert_ffn_dim=s.expert_ffn, norm_topk_prob=1,
-                layer_kind=[1] * s.n_layers, bos_id=1, eos_ids=[2], source=source)
+    m = dict(arch=s.arch, n_layers=s.n_layers, d_model=s.d_model, vocab_size=s.vocab, max_seq=s.max_seq,
+             norm_eps=1e-6, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, qk_norm=s.qk_norm,
+             rope_dim=_rope_dim(s), attn_scale=float(np.float32(1.0 / math.sqrt(s.head_dim))),
+             n_experts=s.n_experts, top_k=s.top_k, expert_ffn_dim=s.expert_ffn, norm_topk_prob=s.norm_topk,
+             layer_kind=[0] * s.n_dense + [1] * (s.n_layers - s.n_dense), bos_id=1, eos_ids=[2], source=source)
+    # keys written only where they differ from the FORMAT.md default
+    extra = dict(qkv_bias=(s.qkv_bias, 0), rope_style=(s.rope_style, 0), shared_ffn_dim=(s.shared_ffn, 0),
+                 shared_gate=(s.shared_gate, 0), score_fn=(s.score_fn, 0), score_bias=(s.score_bias, 0),
+                 n_group=(s.n_group, 1), topk_group=(s.topk_group, 1), dense_ffn_dim=(s.dense_ffn, 0),
+                 tie_embeddings=(s.tie, 0), routed_scale=(float(s.routed_scale), 1.0),
+                 emb_scale=(float(s.emb_scale), 1.0), residual_scale=(float(s.resid_scale), 1.0),
+                 logit_scale=(float(s.logit_scale), 1.0))
+    for k, (v, default) in extra.items():
+        if v != default:
+            m[k] = v
+    return m
 
 
 def rope_inv_freq(s: Shape) -> np.ndarray:
     """1 / theta^(2j / rope_dim) in float32, computed with the platform libm's pow."""
-    d = s.head_dim
+    d = _rope_dim(s)
     return np.array([1.0 / math.pow(s.rope_theta, (2 * j) / d) for j in range(d // 2)], dtype=np.float32)
 
 
@@ -263,11 +314,16 @@ def make_tiny(path, quantize, seed: int = 1, shape: Shape = TINY, std: float = 0
     def q(name, dtype, rows, cols):
         w.add(name, dtype, (rows, cols), quantize(dtype, rnd(rows, cols)))
 
+    def vec(name, n, base=0.0, sd=0.02):
+        k[0] += 1
+        w.add(name, F32, (n,), (base + normal(k[0], n, sd)).astype(np.float32).tobytes())
+
     ones = np.ones(D, dtype=np.float32).tobytes()
     q("tok_embd", Q8, V, D)
-    q("lm_head", Q8, V, D)
+    if not s.tie:
+        q("lm_head", Q8, V, D)
     w.add("out_norm", F32, (D,), ones)
-    w.add("rope_inv_freq", F32, (hd // 2,), rope_inv_freq(s).tobytes())
+    w.add("rope_inv_freq", F32, (_rope_dim(s) // 2,), rope_inv_freq(s).tobytes())
     for l in range(L):
         p = f"blk.{l}."
         w.add(p + "attn_norm", F32, (D,), ones)
@@ -276,9 +332,30 @@ def make_tiny(path, quantize, seed: int = 1, shape: Shape = TINY, std: float = 0
         q(p + "attn_k", Q8, Hkv * hd, D)
         q(p + "attn_v", Q8, Hkv * hd, D)
         q(p + "attn_o", Q8, D, H * hd)
-        w.add(p + "attn_q_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
-        w.add(p + "attn_k_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+        if s.qkv_bias:
+            vec(p + "attn_q_bias", H * hd)
+            vec(p + "attn_k_bias", Hkv * hd)
+            vec(p + "attn_v_bias", Hkv * hd)
+        if s.qk_norm == 1:
+            w.add(p + "attn_q_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+            w.add(p + "attn_k_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+        elif s.qk_norm == 2:
+            vec(p + "attn_q_norm", H * hd, 1.0, 0.1)
+            vec(p + "attn_k_norm", Hkv * hd, 1.0, 0.1)
+        if l < s.n_dense:
+            q(p + "ffn_gate", Q8, s.dense_ffn, D)
+            q(p + "ffn_up", Q8, s.dense_ffn, D)
+            q(p + "ffn_down", Q8, D, s.dense_ffn)
+            continue
         w.add(p + "moe_router", F32, (E, D), rnd(E, D).tobytes())
+        if s.score_bias:
+            vec(p + "moe_router_bias", E, 0.0, 0.05)
+        if s.shared_ffn:
+            q(p + "shexp_gate", Q8, s.shared_ffn, D)
+            q(p + "shexp_up", Q8, s.shared_ffn, D)
+            q(p + "shexp_down", Q8, D, s.shared_ffn)
+            if s.shared_gate:
+                w.add(p + "shexp_gate_inp", F32, (1, D), (rnd(1, D) * 10.0).astype(np.float32).tobytes())
         nb, og, ou, od = slab_layout(Q4, D, F)
         for e in range(E):
             slab = bytearray(nb)

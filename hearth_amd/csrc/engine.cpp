@@ -90,6 +90,8 @@ struct Layer {
     DMat q, k, v, o;
     const float *bq = nullptr, *bk = nullptr, *bv = nullptr, *qn = nullptr, *kn = nullptr;
     DMat gate, up, down;            /* dense FFN */
+    DMat sh_gate, sh_up, sh_down;   /* shared expert (MoE layers, shared_ffn_dim > 0) */
+    const float *sh_gate_inp = nullptr; /* F32 [D]: shared output scaled by sigmoid(dot16(., x)) */
     const float *router = nullptr;  /* F32 [E][D] */
     const float *router_bias = nullptr;
     ExpertW *experts = nullptr;     /* device table [E] */
@@ -118,7 +120,7 @@ struct hearth_engine {
     std::vector<void *> allocs;
 
     int L = 0, D = 0, V = 0, H = 0, Hkv = 0, hd = 0, q_dim = 0, kv_dim = 0, E = 0, K = 0, F = 0, Fd = 0;
-    int cap = 0, B = 0, rope_dim = 0;
+    int cap = 0, B = 0, rope_dim = 0, Fs = 0;
     std::vector<Layer> layers;
     std::vector<int> moe_ord;
     const uint8_t *emb = nullptr;
@@ -134,9 +136,10 @@ struct hearth_engine {
     /* scratch for B tokens */
     float *h = nullptr, *x = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr, *qr = nullptr, *att = nullptr,
           *ao = nullptr, *S = nullptr, *lge = nullptr, *wts = nullptr, *Y = nullptr, *f1 = nullptr, *f2 = nullptr,
-          *logits = nullptr, *rope = nullptr, *rfull = nullptr, *midf = nullptr;
+          *logits = nullptr, *rope = nullptr, *rfull = nullptr, *midf = nullptr, *sf1 = nullptr, *sf2 = nullptr,
+          *shb = nullptr, *shg = nullptr;
     int ldS = 0;
-    Act ax{}, aatt{}, amid{}, af{};
+    Act ax{}, aatt{}, amid{}, af{}, asf{};
     hxd::SlotDesc *slot_desc = nullptr;
     int *ids = nullptr, *route_meta = nullptr, *pair_tok = nullptr, *pair_of = nullptr, *tokens = nullptr,
         *depth = nullptr, *anc = nullptr, *route_out = nullptr, *acc_i = nullptr, *acc_part = nullptr;
@@ -394,6 +397,11 @@ bool hearth_engine::upload(std::string &msg) {
         }
         w.router = vec(l, "moe_router");
         if (c.score_bias) w.router_bias = vec(l, "moe_router_bias");
+        if (c.shared_ffn > 0) {
+            if (!mat(l, "shexp_gate", w.sh_gate) || !mat(l, "shexp_up", w.sh_up) || !mat(l, "shexp_down", w.sh_down))
+                return false;
+            if (c.shared_gate) w.sh_gate_inp = vec(l, "shexp_gate_inp");
+        }
         std::vector<ExpertW> table(E);
         for (int e = 0; e < E; e++) {
             const ExpertEntry *ent = mf.expert(l, e);
@@ -427,17 +435,20 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
         fail(err, errlen, "%s: MLA attention is not supported by this build yet", opt.model_path);
         return false;
     }
-    if (c.shared_ffn > 0) {
-        fail(err, errlen, "%s: shared experts are not supported by this build yet", opt.model_path);
-        return false;
-    }
     L = c.n_layers; D = c.d_model; V = c.vocab; H = c.n_heads; Hkv = c.n_kv_heads; hd = c.head_dim;
     q_dim = H * hd; kv_dim = Hkv * hd; E = c.n_experts; K = c.top_k; F = c.expert_ffn; Fd = c.dense_ffn;
+    Fs = c.n_moe ? c.shared_ffn : 0;
     rope_dim = c.rope_dim;
     if (hd > 512 || hd % 16) { fail(err, errlen, "%s: head_dim %d unsupported (needs a multiple of 16 <= 512)", opt.model_path, hd); return false; }
     if (E > 1024) { fail(err, errlen, "%s: %d experts exceed this build's limit of 1024", opt.model_path, E); return false; }
     if (c.n_moe && K > 64) { fail(err, errlen, "%s: top_k %d exceeds this build's limit of 64", opt.model_path, K); return false; }
     if (c.n_group > 64) { fail(err, errlen, "%s: n_group %d exceeds this build's limit of 64", opt.model_path, c.n_group); return false; }
+    if (c.n_moe && (K < 1 || K > E || c.n_group < 1 || E % c.n_group ||
+                    (c.n_group > 1 && (c.topk_group < 1 || c.topk_group > c.n_group)))) {
+        fail(err, errlen, "%s: routing shape (experts %d, top_k %d, groups %d keep %d) is inconsistent", opt.model_path,
+             E, K, c.n_group, c.topk_group);
+        return false;
+    }
     if (c.n_moe && F % 64) { fail(err, errlen, "%s: expert_ffn_dim %d is not a multiple of 64", opt.model_path, F); return false; }
     if (c.n_moe && (D > 16384 || F > 16384)) {
         fail(err, errlen, "%s: expert matrices of %d x %d exceed this build's limit of 16384", opt.model_path, F, D);
@@ -513,6 +524,13 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
             f1 = dnew<float>(Bs * Fd);
             f2 = dnew<float>(Bs * Fd);
             af = make_act(B, Fd);
+        }
+        if (Fs) {
+            sf1 = dnew<float>(Bs * Fs);
+            sf2 = dnew<float>(Bs * Fs);
+            asf = make_act(B, Fs);
+            shb = dnew<float>(Bs * D);
+            shg = dnew<float>(Bs);
         }
         ck(hipHostMalloc((void **)&h_geom, sizeof(int) * (2 * Bs + Bs * Bs), hipHostMallocDefault));
         ck(hipHostMalloc((void **)&h_rope, sizeof(float) * Bs * std::max(rope_dim, 2), hipHostMallocDefault));
@@ -626,9 +644,18 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 timed(&ks.expert_down_s, [&] { hxl::expert_down(m, slots, st); }, 1);
             }
             if (profiling) ks.expert_launches++;
+            if (Fs)   /* shared expert (reference model.c:925-934): SwiGLU FFN of x, optional sigmoid gate */
+                timed(&ks.dense_s, [&] {
+                    matmul(w.sh_gate, ax, x, D, T, sf1, Fs, false, 1.0f);
+                    matmul(w.sh_up, ax, x, D, T, sf2, Fs, false, 1.0f);
+                    hxl::swiglu_quant(sf1, sf2, T, Fs, asf, st);
+                    matmul(w.sh_down, asf, sf1, Fs, T, shb, D, false, 1.0f);
+                    if (w.sh_gate_inp) hxl::fgemv(0, w.sh_gate_inp, 1, D, x, D, T, shg, 1, st);
+                });
             timed(&ks.norm_s, [&] {
                 hxd::NormArgs n{};
                 n.mode = 2; n.h = h; n.Y = Y; n.wts = wts; n.pair_of = pair_of; n.K = K; n.rs = rs;
+                n.add = Fs ? shb : nullptr; n.add_gate = w.sh_gate_inp ? shg : nullptr;
                 n.norm_w = next_norm; n.eps = c.eps; n.x = x; n.a = ax; n.T = T; n.D = D;
                 hxl::norm(n, st);
             });

@@ -110,7 +110,8 @@ struct QkvArgs {
 struct NormArgs {
     int mode;
     float *h;                 /* [T][D] */
-    const float *add;         /* mode 1 / shared (mode 2, may be null) */
+    const float *add;         /* mode 1 / shared expert output (mode 2, may be null) */
+    const float *add_gate;    /* mode 2: per-token shared gate logit (out += add * sigmoid(gate)), or null */
     const float *Y;           /* mode 2 */
     const float *wts;
     const int *pair_of;

@@ -89,7 +89,11 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
                 for (int u = 0; u < 8; u++)
                     if (j0 + u < K) out = fadd(out, fmul(wk[j0 + u], yv[u]));
             }
-            if (a.add) out = fadd(out, a.add[(size_t)t * D + i]);
+            if (a.add) {
+                float sv = a.add[(size_t)t * D + i];
+                if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_port_f(-a.add_gate[t]))));
+                out = fadd(out, sv);
+            }
             v = fadd(h[i], fmul(a.rs, out));
         }
         h[i] = v;

@@ -32,3 +32,20 @@ def tiny_model(tmp_path_factory):
     if want is not None:
         assert container.sha256(path) == want, "tiny model bytes differ from the ones the golden fixtures were made on"
     return path
+
+
+@pytest.fixture(scope="session")
+def variant_models(tmp_path_factory):
+    """Builds (once per session) the small models of the other families (DeepSeek-V3
+    routing with a GQA attention, Qwen2-MoE, OLMoE; hearth_amd.container.TINY_VARIANTS)
+    and returns name -> path."""
+    from hearth_amd import _native, container
+    d = tmp_path_factory.mktemp("variants")
+    cache = {}
+
+    def get(name):
+        if name not in cache:
+            cache[name] = container.make_tiny(d / f"{name}.hearth", _native.quantize, seed=2,
+                                              shape=container.TINY_VARIANTS[name])
+        return cache[name]
+    return get

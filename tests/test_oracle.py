@@ -124,6 +124,29 @@ def test_oracle_matches_reference_engine(tiny_model):
     assert np.array_equal(lr.view(np.uint32), lo.view(np.uint32))
 
 
+@pytest.mark.skipif(not O.REF_LIB.is_file(), reason="reference engine not built (make -C oracle)")
+@pytest.mark.parametrize("variant", sorted(container.TINY_VARIANTS))
+def test_oracle_matches_reference_engine_variants(variant_models, variant):
+    """The restatement of the other families' features (q/k/v biases, full-width qk-norm,
+    partial and interleaved RoPE, sigmoid scores with selection bias, group-limited
+    routing, routed scale, shared experts with and without gate, dense layers, tied
+    embeddings, embedding/residual/logit scales) is bit-exact with the reference engine
+    compiled from source, with routes."""
+    from hearth_amd.engine import Engine
+    path = variant_models(variant)
+    toks = container.uniform_ints(31, 40, 4096)
+    ref = Engine(path, lib=str(O.REF_LIB), threads=4, prefetch="off")
+    lr = ref.eval(toks, all_logits=True)
+    lr2 = ref.eval(toks[:5], all_logits=True)
+    ref.close()
+    O.set_exp_mode(O.EXP_LIBM)
+    m = O.Model(path)
+    lo = m.eval(toks)
+    lo2 = m.eval(toks[:5])
+    assert np.array_equal(lr.view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(lr2.view(np.uint32), lo2.view(np.uint32))
+
+
 def test_tree_equals_chain(tiny_model):
     """Every tree node's logits equal the chain evaluation of its root path (bit for bit),
     and committing a path leaves the same KV as evaluating the chain."""
