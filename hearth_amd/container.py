@@ -248,6 +248,13 @@ class Shape:
     emb_scale: float = 1.0
     resid_scale: float = 1.0
     logit_scale: float = 1.0
+    # multi-head latent attention (attn_kind 1): q_lora 0 = uncompressed q
+    attn_kind: int = 0
+    q_lora: int = 0
+    kv_lora: int = 0
+    nope: int = 0
+    rope_qk: int = 0
+    v_head: int = 0
 
 
 TINY = Shape(n_layers=4, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, n_experts=16, top_k=4,
@@ -263,14 +270,23 @@ TINY_QWEN2 = Shape(n_layers=3, d_model=512, n_heads=8, n_kv_heads=4, head_dim=64
 TINY_OLMOE = Shape(n_layers=3, d_model=512, n_heads=8, n_kv_heads=8, head_dim=64, n_experts=16, top_k=4,
                    expert_ffn=256, vocab=4096, max_seq=1024, arch="olmoe", qk_norm=2, norm_topk=0, rope_dim=32,
                    tie=1, emb_scale=1.5, resid_scale=0.75, logit_scale=0.5)
-TINY_VARIANTS = {"dsv3_gqa": TINY_DSV3_GQA, "qwen2": TINY_QWEN2, "olmoe": TINY_OLMOE}
+TINY_DSV3 = Shape(n_layers=4, d_model=512, n_heads=4, n_kv_heads=4, head_dim=128, n_experts=16, top_k=4,
+                  expert_ffn=256, vocab=4096, max_seq=1024, arch="deepseek_v3", qk_norm=0, rope_style=1,
+                  shared_ffn=256, score_fn=1, score_bias=1, n_group=4, topk_group=2, norm_topk=1,
+                  routed_scale=2.5, n_dense=1, dense_ffn=512, attn_kind=1, q_lora=192, kv_lora=128, nope=64,
+                  rope_qk=64, v_head=64)
+TINY_MLA_NOQ = Shape(n_layers=2, d_model=512, n_heads=8, n_kv_heads=8, head_dim=96, n_experts=16, top_k=4,
+                     expert_ffn=256, vocab=4096, max_seq=1024, arch="deepseek_v2_lite", qk_norm=0,
+                     attn_kind=1, q_lora=0, kv_lora=256, nope=64, rope_qk=32, v_head=128)
+TINY_VARIANTS = {"dsv3_gqa": TINY_DSV3_GQA, "qwen2": TINY_QWEN2, "olmoe": TINY_OLMOE, "dsv3": TINY_DSV3,
+                 "mla_noq": TINY_MLA_NOQ}
 
 QWEN3_30B_A3B = Shape(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_dim=128, n_experts=128, top_k=8,
                       expert_ffn=768, vocab=151936, max_seq=8192)
 
 
 def _rope_dim(s: Shape) -> int:
-    return s.rope_dim or s.head_dim
+    return s.rope_dim or (s.rope_qk if s.attn_kind == 1 else s.head_dim)
 
 
 def _meta(s: Shape, source: str) -> dict:
@@ -289,6 +305,9 @@ def _meta(s: Shape, source: str) -> dict:
     for k, (v, default) in extra.items():
         if v != default:
             m[k] = v
+    if s.attn_kind == 1:
+        m.update(attn_kind=1, q_lora_rank=s.q_lora, kv_lora_rank=s.kv_lora, qk_nope_dim=s.nope, qk_rope_dim=s.rope_qk,
+                 v_head_dim=s.v_head, attn_scale=float(np.float32(1.0 / math.sqrt(s.nope + s.rope_qk))))
     return m
 
 
@@ -328,10 +347,23 @@ def make_tiny(path, quantize, seed: int = 1, shape: Shape = TINY, std: float = 0
         p = f"blk.{l}."
         w.add(p + "attn_norm", F32, (D,), ones)
         w.add(p + "ffn_norm", F32, (D,), ones)
-        q(p + "attn_q", Q8, H * hd, D)
-        q(p + "attn_k", Q8, Hkv * hd, D)
-        q(p + "attn_v", Q8, Hkv * hd, D)
-        q(p + "attn_o", Q8, D, H * hd)
+        if s.attn_kind == 1:
+            qh = s.nope + s.rope_qk
+            if s.q_lora:
+                q(p + "attn_q_a", Q8, s.q_lora, D)
+                vec(p + "attn_q_a_norm", s.q_lora, 1.0, 0.1)
+                q(p + "attn_q_b", Q8, H * qh, s.q_lora)
+            else:
+                q(p + "attn_q", Q8, H * qh, D)
+            q(p + "attn_kv_a", Q8, s.kv_lora + s.rope_qk, D)
+            vec(p + "attn_kv_a_norm", s.kv_lora, 1.0, 0.1)
+            q(p + "attn_kv_b", Q8, H * (s.nope + s.v_head), s.kv_lora)
+            q(p + "attn_o", Q8, D, H * s.v_head)
+        else:
+            q(p + "attn_q", Q8, H * hd, D)
+            q(p + "attn_k", Q8, Hkv * hd, D)
+            q(p + "attn_v", Q8, Hkv * hd, D)
+            q(p + "attn_o", Q8, D, H * hd)
         if s.qkv_bias:
             vec(p + "attn_q_bias", H * hd)
             vec(p + "attn_k_bias", Hkv * hd)

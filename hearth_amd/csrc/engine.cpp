@@ -91,6 +91,13 @@ struct Layer {
     const float *bq = nullptr, *bk = nullptr, *bv = nullptr, *qn = nullptr, *kn = nullptr;
     DMat gate, up, down;            /* dense FFN */
     DMat sh_gate, sh_up, sh_down;   /* shared expert (MoE layers, shared_ffn_dim > 0) */
+    /* MLA: q (q_lora 0) or q_a -> rmsnorm -> q_b; kv_a; W_UK rows as stored; W_UV per head */
+    DMat q_a, q_b, kv_a;
+    const float *q_a_norm = nullptr, *kv_a_norm = nullptr;
+    const uint8_t *kvb_raw = nullptr;
+    int kvb_dtype = 0;
+    size_t kvb_rb = 0;
+    ExpertW *uv = nullptr;          /* device [H]: .down = W_UV of head h */
     const float *sh_gate_inp = nullptr; /* F32 [D]: shared output scaled by sigmoid(dot16(., x)) */
     const float *router = nullptr;  /* F32 [E][D] */
     const float *router_bias = nullptr;
@@ -121,6 +128,8 @@ struct hearth_engine {
 
     int L = 0, D = 0, V = 0, H = 0, Hkv = 0, hd = 0, q_dim = 0, kv_dim = 0, E = 0, K = 0, F = 0, Fd = 0;
     int cap = 0, B = 0, rope_dim = 0, Fs = 0;
+    bool mla = false;
+    int C = 0, rdim = 0, nope = 0, vd = 0, qlr = 0, qh = 0;   /* MLA shape */
     std::vector<Layer> layers;
     std::vector<int> moe_ord;
     const uint8_t *emb = nullptr;
@@ -137,9 +146,9 @@ struct hearth_engine {
     float *h = nullptr, *x = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr, *qr = nullptr, *att = nullptr,
           *ao = nullptr, *S = nullptr, *lge = nullptr, *wts = nullptr, *Y = nullptr, *f1 = nullptr, *f2 = nullptr,
           *logits = nullptr, *rope = nullptr, *rfull = nullptr, *midf = nullptr, *sf1 = nullptr, *sf2 = nullptr,
-          *shb = nullptr, *shg = nullptr;
+          *shb = nullptr, *shg = nullptr, *qa = nullptr, *kva = nullptr, *olat = nullptr, *yv = nullptr;
     int ldS = 0;
-    Act ax{}, aatt{}, amid{}, af{}, asf{};
+    Act ax{}, aatt{}, amid{}, af{}, asf{}, aqa{}, alat{};
     hxd::SlotDesc *slot_desc = nullptr;
     int *ids = nullptr, *route_meta = nullptr, *pair_tok = nullptr, *pair_of = nullptr, *tokens = nullptr,
         *depth = nullptr, *anc = nullptr, *route_out = nullptr, *acc_i = nullptr, *acc_part = nullptr;
@@ -254,6 +263,16 @@ struct hearth_engine {
     bool open_model(char *err, size_t errlen);
     bool upload(std::string &msg);
     void forward(int T, bool want_logits, int logit_rows_from);
+    void attn_mla(const Layer &w, int l, int T);
+    /* KV of slots pos + path[j] -> pos + j (path on the device) */
+    void move_kv(const int *path_dev, int n) {
+        if (mla) {
+            hxl::kv_move_rows(kv, kv_layer, L, 0, C, pos, path_dev, n, st);
+            hxl::kv_move_rows(kv, kv_layer, L, (size_t)cap * C, rdim, pos, path_dev, n, st);
+        } else {
+            hxl::kv_move(kv, kv_layer, L, Hkv, cap, hd, pos, path_dev, n, st);
+        }
+    }
     int eval_chunked(const int32_t *tokens, int n, float *logits_out, int all_logits);
     int run_geometry(const int32_t *tok, const int32_t *parent, int n, float *logits_out, bool keep_logits_dev);
     void matmul(const DMat &m, const Act &a, const float *xf, int ldx, int T, float *Y, int ldy, bool scale_on, float scale);
@@ -381,7 +400,36 @@ bool hearth_engine::upload(std::string &msg) {
         w.moe = c.layer_kind[l] != 0;
         w.attn_norm = vec(l, "attn_norm");
         w.ffn_norm = vec(l, "ffn_norm");
-        if (!mat(l, "attn_q", w.q) || !mat(l, "attn_k", w.k) || !mat(l, "attn_v", w.v) || !mat(l, "attn_o", w.o)) return false;
+        if (mla) {
+            if (qlr) {
+                if (!mat(l, "attn_q_a", w.q_a) || !mat(l, "attn_q_b", w.q_b)) return false;
+                w.q_a_norm = vec(l, "attn_q_a_norm");
+            } else if (!mat(l, "attn_q", w.q)) {
+                return false;
+            }
+            if (!mat(l, "attn_kv_a", w.kv_a) || !mat(l, "attn_o", w.o)) return false;
+            w.kv_a_norm = vec(l, "attn_kv_a_norm");
+            const Tensor *t = mf.layer_tensor(l, "attn_kv_b");
+            if (!t) { msg = "tensor 'attn_kv_b' is missing"; return false; }
+            if (!dtype_is_quant(t->dtype) && t->dtype > HEARTH_BF16) { msg = "attn_kv_b has an unsupported dtype"; return false; }
+            w.kvb_dtype = t->dtype;
+            w.kvb_rb = row_bytes(t->dtype, C);
+            uint8_t *raw = (uint8_t *)dalloc(t->nbytes);
+            up.raw(raw, mf.data(t->offset), t->nbytes);
+            w.kvb_raw = raw;
+            if (!dtype_is_quant(t->dtype)) { msg = "attn_kv_b must be Q8 or Q4 for the per-head W_UV kernel"; return false; }
+            std::vector<ExpertW> uvt(H);
+            for (int h = 0; h < H; h++) {
+                uvt[h] = ExpertW{};
+                uvt[h].down = qmat_alloc(t->dtype, vd, C);
+                up.quant(uvt[h].down, mf.data(t->offset) + ((size_t)h * (nope + vd) + nope) * w.kvb_rb);
+            }
+            w.uv = (ExpertW *)dalloc(sizeof(ExpertW) * (size_t)H);
+            ck(hipMemcpyAsync(w.uv, uvt.data(), sizeof(ExpertW) * (size_t)H, hipMemcpyHostToDevice, st));
+            ck(hipStreamSynchronize(st));   /* the host table goes out of scope */
+        } else if (!mat(l, "attn_q", w.q) || !mat(l, "attn_k", w.k) || !mat(l, "attn_v", w.v) || !mat(l, "attn_o", w.o)) {
+            return false;
+        }
         if (c.qkv_bias) {
             w.bq = vec(l, "attn_q_bias");
             w.bk = vec(l, "attn_k_bias");
@@ -431,15 +479,22 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
     std::string msg;
     if (!mf.open(opt.model_path, msg)) { fail(err, errlen, "%s: %s", opt.model_path, msg.c_str()); return false; }
     c = mf.cfg;
-    if (c.attn_kind != ATTN_GQA) {
-        fail(err, errlen, "%s: MLA attention is not supported by this build yet", opt.model_path);
-        return false;
-    }
+    mla = c.attn_kind == ATTN_MLA;
     L = c.n_layers; D = c.d_model; V = c.vocab; H = c.n_heads; Hkv = c.n_kv_heads; hd = c.head_dim;
     q_dim = H * hd; kv_dim = Hkv * hd; E = c.n_experts; K = c.top_k; F = c.expert_ffn; Fd = c.dense_ffn;
     Fs = c.n_moe ? c.shared_ffn : 0;
+    if (mla) {
+        C = c.kv_lora; rdim = c.rope_qk; nope = c.nope; vd = c.v_head; qlr = c.q_lora; qh = nope + rdim;
+        if (C < 128 || C > 512 || C % 128 || rdim > hxd::MLA_RMAX || rdim % 2 || nope < 1 || nope > hxd::MLA_NOPE_MAX ||
+            vd < 64 || vd % 64 || (qlr && qlr % 64) || c.rope_dim > rdim) {
+            fail(err, errlen, "%s: MLA shape (kv_lora %d, rope %d, nope %d, v %d, q_lora %d) is outside this build's kernels",
+                 opt.model_path, C, rdim, nope, vd, qlr);
+            return false;
+        }
+        Hkv = 1; hd = C; q_dim = H * qh; kv_dim = 0;
+    }
     rope_dim = c.rope_dim;
-    if (hd > 512 || hd % 16) { fail(err, errlen, "%s: head_dim %d unsupported (needs a multiple of 16 <= 512)", opt.model_path, hd); return false; }
+    if (!mla && (hd > 512 || hd % 16)) { fail(err, errlen, "%s: head_dim %d unsupported (needs a multiple of 16 <= 512)", opt.model_path, hd); return false; }
     if (E > 1024) { fail(err, errlen, "%s: %d experts exceed this build's limit of 1024", opt.model_path, E); return false; }
     if (c.n_moe && K > 64) { fail(err, errlen, "%s: top_k %d exceeds this build's limit of 64", opt.model_path, K); return false; }
     if (c.n_group > 64) { fail(err, errlen, "%s: n_group %d exceeds this build's limit of 64", opt.model_path, c.n_group); return false; }
@@ -481,22 +536,35 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
         ck(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
         if (!upload(msg)) { fail(err, errlen, "%s: %s", opt.model_path, msg.c_str()); return false; }
         /* KV cache and scratch */
-        kv_layer = (size_t)2 * Hkv * cap * hd;
+        kv_layer = mla ? (size_t)cap * (C + rdim) : (size_t)2 * Hkv * cap * hd;
         kv = dnew<float>(kv_layer * L);
         ck(hipMemset(kv, 0, sizeof(float) * kv_layer * L));
         const size_t Bs = (size_t)B, P = Bs * (size_t)std::max(K, 1);
         h = dnew<float>(Bs * D);
         x = dnew<float>(Bs * D);
         qb = dnew<float>(Bs * q_dim);
-        kb = dnew<float>(Bs * kv_dim);
-        vb = dnew<float>(Bs * kv_dim);
-        qr = dnew<float>(Bs * q_dim);
-        att = dnew<float>(Bs * q_dim);
+        if (mla) {
+            qr = dnew<float>(Bs * H * C);                 /* absorbed queries [T][H][C] */
+            olat = dnew<float>(Bs * H * C);               /* latent attention outputs [T][H][C] */
+            alat = make_act(H * B, C);                    /* their blocks, rows (head, token) */
+            yv = dnew<float>(Bs * H * vd);                /* W_UV outputs [H][T][vd] */
+            att = dnew<float>(Bs * H * vd);
+            kva = dnew<float>(Bs * (C + rdim));
+            if (qlr) {
+                qa = dnew<float>(Bs * qlr);
+                aqa = make_act(B, qlr);
+            }
+        } else {
+            kb = dnew<float>(Bs * kv_dim);
+            vb = dnew<float>(Bs * kv_dim);
+            qr = dnew<float>(Bs * q_dim);
+            att = dnew<float>(Bs * q_dim);
+        }
         ao = dnew<float>(Bs * D);
         ldS = (cap + 63) & ~63;
         S = dnew<float>(Bs * H * (size_t)ldS);
         ax = make_act(B, D);
-        aatt = make_act(B, q_dim);
+        aatt = make_act(B, mla ? H * vd : q_dim);
         logits = dnew<float>(Bs * V);
         rope = dnew<float>(Bs * (size_t)std::max(rope_dim, 2));
         rfull = dnew<float>(Bs * 2);
@@ -565,6 +633,61 @@ void hearth_engine::matmul(const DMat &m, const Act &a, const float *xf, int ldx
     }
 }
 
+/* Multi-head latent attention of layer l for T tokens (reference attn_mla,
+ * model.c:739-787): projections, latent post step, absorbed queries, latent scores +
+ * RoPE term, softmax and latent value sum (GQA kernels, one shared group of width C),
+ * W_UV per head (grouped projection, one slot per head), output projection. */
+void hearth_engine::attn_mla(const Layer &w, int l, int T) {
+    const int kvd = C + rdim;
+    const DMat &qin = qlr ? w.q_a : w.q;
+    float *qdst = qlr ? qa : qb;
+    const int qld = qlr ? qlr : q_dim;
+    if (qin.quant && w.kv_a.quant) {
+        hxd::GemmArgs g{};
+        g.nseg = 2;
+        g.seg[0].m = qin.q; g.seg[0].Y = qdst; g.seg[0].ldy = qld;
+        g.seg[1].m = w.kv_a.q; g.seg[1].Y = kva; g.seg[1].ldy = kvd;
+        g.a = ax;
+        g.T = T;
+        hxl::gemm(g, st);
+    } else {
+        matmul(qin, ax, x, D, T, qdst, qld, false, 1.0f);
+        matmul(w.kv_a, ax, x, D, T, kva, kvd, false, 1.0f);
+    }
+    if (qlr) {
+        hxd::NormArgs n{};
+        n.mode = 3; n.h = qa; n.norm_w = w.q_a_norm; n.eps = c.eps; n.x = qa; n.a = aqa; n.T = T; n.D = qlr;
+        hxl::norm(n, st);
+        matmul(w.q_b, aqa, qa, qlr, T, qb, q_dim, false, 1.0f);
+    }
+    float *cc = kv + (size_t)l * kv_layer;
+    hxd::MlaArgs ma{};
+    ma.T = T; ma.H = H; ma.C = C; ma.rdim = rdim; ma.nope = nope; ma.vd = vd; ma.qh = qh;
+    ma.kva = kva; ma.q = qb; ma.kv_norm = w.kv_a_norm; ma.cc = cc; ma.kp = cc + (size_t)cap * C;
+    ma.rope = rope; ma.rope_dim = rope_dim; ma.rope_style = c.rope_style; ma.eps = c.eps; ma.pos0 = pos;
+    ma.wuk = w.kvb_raw; ma.wuk_dtype = w.kvb_dtype; ma.wuk_rb = w.kvb_rb; ma.qlat = qr;
+    ma.S = S; ma.ldS = ldS; ma.scale = c.attn_scale;
+    ma.g.depth = depth; ma.g.anc = anc; ma.g.anc_ld = B; ma.g.pos0 = pos;
+    ma.Yv = yv; ma.att = att; ma.aatt = aatt;
+    hxl::mla_post(ma, st);
+    hxl::mla_qlat(ma, st);
+    hxd::AttnArgs at{};
+    at.q = qr; at.kc = cc; at.vc = cc; at.S = S; at.ldS = ldS; at.out = olat; at.T = T; at.H = H; at.Hkv = 1;
+    at.hd = C; at.cap = cap; at.scale = 1.0f;
+    at.g = ma.g;
+    at.qo = alat; at.qo_on = 1; at.qo_hm = 1;
+    hxl::attention_scores(at, st);
+    hxl::mla_pe_scores(ma, st);
+    hxl::attention_finish(at, st);
+    dump("att", l, olat, T, H * C);
+    hxd::MoeArgs m{};
+    m.table = w.uv; m.head_slots = 1; m.mid = alat; m.T = T; m.D = vd; m.F = C; m.Y = yv; m.P = H * T;
+    m.dtype_mask = 1 << w.kvb_dtype;
+    hxl::expert_down_q(m, H, st);
+    hxl::mla_gather(ma, st);
+    matmul(w.o, aatt, att, H * vd, T, ao, D, false, 1.0f);
+}
+
 /* One forward of T tokens whose geometry (tokens, depth, anc, rope) is already on the
  * device; logits of all T rows into this->logits when want_logits. */
 void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
@@ -578,6 +701,10 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
     for (int l = 0; l < L; l++) {
         const Layer &w = layers[l];
         timed(&ks.attn_s, [&] {
+            if (mla) {
+                attn_mla(w, l, T);
+                return;
+            }
             if (w.q.quant && w.k.quant && w.v.quant) {
                 hxd::GemmArgs g{};
                 g.nseg = 3;
@@ -1037,7 +1164,7 @@ HEARTH_API int hearth_commit_path(hearth_engine *e, const int32_t *path, int n) 
         if (moves) {
             std::memcpy(e->h_res, path, sizeof(int) * n);
             ck(hipMemcpyAsync(e->acc_i, e->h_res, sizeof(int) * n, hipMemcpyHostToDevice, e->st));
-            hxl::kv_move(e->kv, e->kv_layer, e->L, e->Hkv, e->cap, e->hd, e->pos, e->acc_i, n, e->st);
+            e->move_kv(e->acc_i, n);
             ck(hipStreamSynchronize(e->st));
         }
     } catch (const DeviceError &err) {
@@ -1092,7 +1219,7 @@ int verify_and_commit(hearth_engine *e, const int32_t *tokens, const int32_t *pa
             for (int j = 0; j < np; j++) moves = moves || path_out[j] != j;
             if (moves) {
                 ck(hipMemcpyAsync(e->acc_i, path_out, sizeof(int) * np, hipMemcpyHostToDevice, e->st));
-                hxl::kv_move(e->kv, e->kv_layer, e->L, e->Hkv, e->cap, e->hd, e->pos, e->acc_i, np, e->st);
+                e->move_kv(e->acc_i, np);
                 ck(hipStreamSynchronize(e->st));
             }
         }

@@ -125,6 +125,39 @@ __device__ inline double exp_port_d(double x) {
 
 __device__ __forceinline__ float exp_port_f(float x) { return __double2float_rn(exp_port_d((double)x)); }
 
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+/* 16-lane canonical tree (NUMERICS §1) of the partials held by lanes 0..15 of a
+ * 16-lane segment: returns the total in lane 0 of the segment. */
+__device__ __forceinline__ float tree16(float L) {
+#pragma unroll
+    for (int s = 8; s >= 1; s >>= 1) L = fadd(L, __shfl_down(L, s, 16));
+    return L;
+}
+
+/* element i of a FORMAT.md row of dtype dt (embedding lookup) */
+__device__ __forceinline__ float deq_elem(const uint8_t *row, int dt, int i) {
+    switch (dt) {
+    case 0: return ((const float *)row)[i];
+    case 1: return h2f(((const uint16_t *)row)[i]);
+    case 2: return __uint_as_float((uint32_t)((const uint16_t *)row)[i] << 16);
+    case 3: {
+        const uint8_t *b = row + (size_t)(i >> 6) * 66;
+        return fmul(h2f((uint16_t)(b[0] | (b[1] << 8))), (float)(int8_t)b[2 + (i & 63)]);
+    }
+    default: {
+        const uint8_t *b = row + (size_t)(i >> 6) * 34;
+        const int w = i & 63, byte = b[2 + (w & 31)];
+        const int q = (w < 32 ? (byte & 15) : (byte >> 4)) - 8;
+        return fmul(h2f((uint16_t)(b[0] | (b[1] << 8))), (float)q);
+    }
+    }
+}
+
 /* position of element e (0..63) of a block in kperm order */
 __device__ __forceinline__ int kperm_pos(int e) {
     return e < 32 ? (e >> 3) * 16 + (e & 7) : ((e - 32) >> 3) * 16 + 8 + ((e - 32) & 7);

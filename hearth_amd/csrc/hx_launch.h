@@ -47,6 +47,7 @@ struct MoeArgs {
     int T, F, D;
     int P;                    /* pairs: T * top_k */
     int dtype_mask;           /* bit dt set when some expert of the layer has dtype dt */
+    int head_slots;           /* 1: slot u is table[u] for pairs [u * T, u * T + T) (MLA W_UV per head) */
 };
 
 /* Routing (NUMERICS §5.3) of T tokens from router logits. */
@@ -88,6 +89,7 @@ struct AttnArgs {
     TokGeom g;
     Act qo;                   /* NUMERICS §2 blocks of out (when qo_on; head_dim % 64 == 0) */
     int qo_on;
+    int qo_hm;                /* 1: qo rows are (head, token) = h * T + t with hd / 64 blocks each */
 };
 
 struct QkvArgs {
@@ -141,6 +143,32 @@ struct AcceptArgs {
     int *result;              /* [0] n_path, [1] final token, [2] status (0 ok, -1 bad logits) */
 };
 
+/* Multi-head latent attention of one layer (absorbed form, reference model.c:632-787). */
+constexpr int MLA_RMAX = 64;          /* qk_rope_dim limit (register tile of the RoPE scores) */
+constexpr int MLA_NOPE_MAX = 256;     /* qk_nope_dim limit */
+struct MlaArgs {
+    int T, H, C, rdim, nope, vd, qh;  /* qh = nope + rdim */
+    const float *kva;                 /* [T][C + rdim] kv_a output */
+    float *q;                         /* [T][H][qh]; q_pe is rotated in place */
+    const float *kv_norm;             /* [C] */
+    float *cc, *kp;                   /* layer caches: latent c [cap][C], rotated k_pe [cap][rdim] */
+    const float *rope;                /* [T][rope_dim] (cos, sin) pairs */
+    int rope_dim, rope_style;
+    float eps;
+    int pos0;
+    const uint8_t *wuk;               /* attn_kv_b as stored (FORMAT rows of C) */
+    int wuk_dtype;
+    size_t wuk_rb;
+    float *qlat;                      /* [T][H][C] absorbed queries */
+    float *S;                         /* scores [T][H][ldS] */
+    int ldS;
+    float scale;
+    TokGeom g;
+    const float *Yv;                  /* per-head W_UV outputs [H][T][vd] */
+    float *att;                       /* [T][H * vd] */
+    Act aatt;                         /* NUMERICS §2 blocks of att */
+};
+
 /* numpy's pairwise summation tree of the last (partial) 8192-element buffer of a row:
  * leaves in index order, and per level the additions slot[a] = slot[a] + slot[b]
  * (a subtree's value lives in the slot of its leftmost leaf). Built on the host. */
@@ -189,6 +217,13 @@ void quant_rows(const float *x, int64_t ldx, int T, int nb, const Act &a, hipStr
 void gemm(const GemmArgs &a, hipStream_t st);
 void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 void expert_down(const MoeArgs &a, int n_slots, hipStream_t st);
+/* the down kernel alone on already quantized pair activations (a.mid) */
+void expert_down_q(const MoeArgs &a, int n_slots, hipStream_t st);
+/* MLA: latent post step, absorbed queries, RoPE score term, output gather */
+void mla_post(const MlaArgs &a, hipStream_t st);
+void mla_qlat(const MlaArgs &a, hipStream_t st);
+void mla_pe_scores(const MlaArgs &a, hipStream_t st);
+void mla_gather(const MlaArgs &a, hipStream_t st);
 void fgemv(int dtype, const void *W, int rows, int cols, const float *X, int ldx, int T, float *Y, int ldy, hipStream_t st);
 void route(const RouteArgs &a, hipStream_t st);
 void norm(const NormArgs &a, hipStream_t st);
@@ -196,8 +231,14 @@ void swiglu_quant(float *g, const float *u, int T, int F, const Act &a, hipStrea
 void scale_rows(float *y, int ldy, int T, int n, float s, hipStream_t st);
 void qkv_post(const QkvArgs &a, hipStream_t st);
 void attention(const AttnArgs &a, hipStream_t st);
+/* the two halves of attention(): scores; softmax + value sum */
+void attention_scores(const AttnArgs &a, hipStream_t st);
+void attention_finish(const AttnArgs &a, hipStream_t st);
 void kv_move(float *cache_layer0, size_t layer_stride, int L, int Hkv, int cap, int hd, int pos0, const int *path_dev,
              int n, hipStream_t st);
+/* rows pos0 + path[j] -> pos0 + j of a [cap][width] array at offset off of every layer */
+void kv_move_rows(float *cache, size_t layer_stride, int L, size_t off, int width, int pos0, const int *path, int n,
+                  hipStream_t st);
 void accept_greedy(const AcceptArgs &a, hipStream_t st);
 /* Sampler settings of one sampled acceptance (the reference's Sampler fields). */
 struct SamplerSpec {

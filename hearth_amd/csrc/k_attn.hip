@@ -370,7 +370,7 @@ __global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
     if (!loader) {
         const int d = dc * 64 + lane;
         if (live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = acc;
-        if (a.qo_on && live) quant_block_wave(acc, a.qo, t, h * (hd >> 6) + dc);
+        if (a.qo_on && live) quant_block_wave(acc, a.qo, a.qo_hm ? h * a.T + t : t, a.qo_hm ? dc : h * (hd >> 6) + dc);
     }
 }
 
@@ -378,7 +378,7 @@ __global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
 
 namespace hxl {
 
-void attention(const AttnArgs &a, hipStream_t st) {
+void attention_scores(const AttnArgs &a, hipStream_t st) {
     const int max_nr = a.g.pos0 + a.T;   /* depth[t] <= t */
     const int nchunks = (max_nr + SC_ROWS - 1) / SC_ROWS;
     const int grp = a.H / a.Hkv, nsc = nchunks * a.T * a.Hkv;
@@ -386,9 +386,18 @@ void attention(const AttnArgs &a, hipStream_t st) {
     else if (grp % 4 == 0) k_attn_scores<4><<<nsc, SC_ROWS, 0, st>>>(a);
     else if (grp % 2 == 0) k_attn_scores<2><<<nsc, SC_ROWS, 0, st>>>(a);
     else k_attn_scores<1><<<nsc, SC_ROWS, 0, st>>>(a);
+}
+
+void attention_finish(const AttnArgs &a, hipStream_t st) {
+    const int grp = a.H / a.Hkv;
     k_attn_softmax<<<a.T * a.H, 256, 0, st>>>(a);
     const int nd = (a.hd + 63) / 64, qpt = (grp + 3) / 4;
     k_attn_values<<<a.T * qpt * a.Hkv * nd, 512, 0, st>>>(a);
+}
+
+void attention(const AttnArgs &a, hipStream_t st) {
+    attention_scores(a, st);
+    attention_finish(a, st);
 }
 
 } // namespace hxl

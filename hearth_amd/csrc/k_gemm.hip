@@ -498,10 +498,19 @@ __global__ __launch_bounds__(512) void k_expert_down_sk(MoeArgs a, int ntok) {
     extern __shared__ float P[];
     const int ntile = (a.D + 15) / 16;
     const int u = (int)blockIdx.x / ntile, rt = (int)blockIdx.x % ntile;
-    const SlotDesc &sd = a.desc[u];
-    const int n = sd.n, p0 = sd.p0;
+    int n, p0;
+    QMat m;
+    if (a.head_slots) {
+        n = a.T;
+        p0 = u * a.T;
+        m = a.table[u].down;
+    } else {
+        const SlotDesc &sd = a.desc[u];
+        n = sd.n;
+        p0 = sd.p0;
+        m = sd.w.down;
+    }
     if (n == 0) return;
-    const QMat m = sd.w.down;
     if (m.dtype != DT) return;
     const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
     int q0, q1;
@@ -746,6 +755,11 @@ void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0
 void expert_down(const MoeArgs &a, int n_slots, hipStream_t st) {
     if (n_slots <= 0) return;
     quant_rows(a.midf, a.F, a.P, a.F / 64, a.mid, st);
+    expert_down_q(a, n_slots, st);
+}
+
+void expert_down_q(const MoeArgs &a, int n_slots, hipStream_t st) {
+    if (n_slots <= 0) return;
     const int nb = (a.F + 63) / 64, nbp = (nb + 1) & ~1;
     const int ntok = sk_ntok(a.T, 1, nb);
     const int threads = 64 * sk_waves(nbp / 2);

@@ -14,44 +14,11 @@ using namespace hxd;
 
 namespace {
 
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-/* 16-lane canonical tree (NUMERICS §1) of the partials held by lanes 0..15 of a
- * 16-lane segment: returns the total in lane 0 of the segment. */
-__device__ __forceinline__ float tree16(float L) {
-#pragma unroll
-    for (int s = 8; s >= 1; s >>= 1) L = fadd(L, __shfl_down(L, s, 16));
-    return L;
-}
-
-/* element i of a FORMAT.md row of dtype dt (embedding lookup) */
-__device__ __forceinline__ float deq_elem(const uint8_t *row, int dt, int i) {
-    switch (dt) {
-    case 0: return ((const float *)row)[i];
-    case 1: return h2f(((const uint16_t *)row)[i]);
-    case 2: return __uint_as_float((uint32_t)((const uint16_t *)row)[i] << 16);
-    case 3: {
-        const uint8_t *b = row + (size_t)(i >> 6) * 66;
-        return fmul(h2f((uint16_t)(b[0] | (b[1] << 8))), (float)(int8_t)b[2 + (i & 63)]);
-    }
-    default: {
-        const uint8_t *b = row + (size_t)(i >> 6) * 34;
-        const int w = i & 63, byte = b[2 + (w & 31)];
-        const int q = (w < 32 ? (byte & 15) : (byte >> 4)) - 8;
-        return fmul(h2f((uint16_t)(b[0] | (b[1] << 8))), (float)q);
-    }
-    }
-}
-
 /* ------------------------------------------------------------ residual + rmsnorm + quant */
 
 /* Residual update of token t's hidden row h (mode 0: h = embedding * emb_scale; 1:
  * h += rs * add; 2: h += rs * (sum_j w_j * Y[pair_j] (+ add)), j in rank order,
- * model.c:904-923), then rmsnorm (quant.c:626-632: ms = sum16(h^2)/D, r = 1/sqrt(ms +
+ * model.c:904-923; 3: h unchanged), then rmsnorm (quant.c:626-632: ms = sum16(h^2)/D, r = 1/sqrt(ms +
  * eps), x = (h * r) * w) and NUMERICS §2 of x. One workgroup per token; every load of
  * the residual step is issued before any of its sums. */
 __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
@@ -76,6 +43,8 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
             v = fmul(a.es, deq_elem(row, a.emb_dtype, i));
         } else if (a.mode == 1) {
             v = fadd(h[i], fmul(a.rs, a.add[(size_t)t * D + i]));
+        } else if (a.mode == 3) {
+            v = h[i];
         } else {
             float out = 0.0f;
             for (int j0 = 0; j0 < K; j0 += 8) {
@@ -608,6 +577,19 @@ __global__ void k_kv_move(float *cache, size_t layer_stride, int L, int Hkv, int
     }
 }
 
+/* The same for a [cap][width] array at offset off of every layer (MLA caches). */
+__global__ void k_kv_move_rows(float *cache, size_t layer_stride, int L, size_t off, int width, int pos0,
+                               const int *__restrict__ path, int n) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)width * L) return;
+    const int l = (int)(idx / width), e = (int)(idx % width);
+    float *base = cache + (size_t)l * layer_stride + off + e;
+    for (int j = 0; j < n; j++) {
+        const int src = path[j];
+        if (src != j) base[(size_t)(pos0 + j) * width] = base[(size_t)(pos0 + src) * width];
+    }
+}
+
 /* ------------------------------------------------------------ greedy acceptance */
 
 /* Greedy argmax of the verify rows, first index on ties, -1 for rows with a NaN or +inf
@@ -732,6 +714,13 @@ void kv_move(float *cache, size_t layer_stride, int L, int Hkv, int cap, int hd,
              hipStream_t st) {
     const int64_t threads = (int64_t)L * 2 * Hkv * hd;
     if (threads && n > 0) k_kv_move<<<(int)((threads + 255) / 256), 256, 0, st>>>(cache, layer_stride, L, Hkv, cap, hd, pos0, path, n);
+}
+
+void kv_move_rows(float *cache, size_t layer_stride, int L, size_t off, int width, int pos0, const int *path, int n,
+                  hipStream_t st) {
+    const int64_t threads = (int64_t)L * width;
+    if (threads && n > 0)
+        k_kv_move_rows<<<(int)((threads + 255) / 256), 256, 0, st>>>(cache, layer_stride, L, off, width, pos0, path, n);
 }
 
 void accept_greedy(const AcceptArgs &a, hipStream_t st) {

@@ -8,10 +8,14 @@ engine compiled from source on the same containers:
 - qwen2: q/k/v biases, a shared expert scaled by its sigmoid gate, no renormalisation of
   the top-k weights;
 - olmoe: full-width qk-norm, partial RoPE (32 of 64 dims), tied embeddings, embedding /
-  residual / logit scales.
+  residual / logit scales;
+- dsv3: the DeepSeek-V3 routing above with multi-head latent attention (q_lora 192,
+  kv_lora 128, nope 64, rope 64, v 64);
+- mla_noq: latent attention without q compression (kv_lora 256, rope 32, v 128).
 
 Each model: a prompt's logits and routes bit-exact with the restatement, batch ==
-sequential, and a greedy tree verify that accepts what the restatement accepts.
+sequential, a greedy tree verify that accepts what the restatement accepts, and the
+committed KV equal to the accepted chain's.
 """
 from __future__ import annotations
 
@@ -59,3 +63,9 @@ def test_variant_bit_exact_with_oracle(variant_models, variant, tmp_path):
         rc, opath, ofin = O.accept_tree(lv, tok, par)
         assert rc == 0 and p == opath and fin == ofin
         assert p[:2] == [0, 1]
+        # the committed KV is the accepted chain's (tree slots moved into place)
+        nxt = e.eval([fin])
+        e.reset()
+        e.eval(toks[:29])
+        e.eval(tok[p])
+        assert np.array_equal(_bits(nxt), _bits(e.eval([fin])))
