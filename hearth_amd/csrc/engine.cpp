@@ -31,6 +31,7 @@
 #include "hearth_gpu.h"
 #include "hx_host.h"
 #include "hx_launch.h"
+#include "expert_store.h"
 
 using namespace hx;
 using hxd::Act;
@@ -107,13 +108,6 @@ struct Layer {
     int dtype_mask = 0;             /* bit dt set when some expert has dtype dt */
 };
 
-struct DeviceError {
-    hipError_t e;
-};
-
-inline void ck(hipError_t e) {
-    if (e != hipSuccess) throw DeviceError{e};
-}
 
 } // namespace
 
@@ -181,6 +175,10 @@ struct hearth_engine {
     int tree_n = 0;
     /* sampled acceptance scratch, grown on demand */
     hxl::SampleScratch samp;
+    /* HBM expert cache (null: every expert resident) */
+    std::unique_ptr<GpuExpertStore> store;
+    int *h_meta = nullptr;   /* pinned [1 + E]: n_active, active experts of a layer */
+    StoreStats store_base;   /* store counters at hearth_reset_stats */
     /* HEARTH_DEBUG_DUMP=<dir>: every forward writes named intermediate buffers there
      * (T rows each, appended per call) for layer-by-layer comparisons */
     std::string dump_dir;
@@ -222,6 +220,8 @@ struct hearth_engine {
         if (h_geom) (void)hipHostFree(h_geom);
         if (h_rope) (void)hipHostFree(h_rope);
         if (h_res) (void)hipHostFree(h_res);
+        if (h_meta) (void)hipHostFree(h_meta);
+        store.reset();
         if (st) (void)hipStreamDestroy(st);
         if (trace) fclose(trace);
     }
@@ -450,6 +450,17 @@ bool hearth_engine::upload(std::string &msg) {
                 return false;
             if (c.shared_gate) w.sh_gate_inp = vec(l, "shexp_gate_inp");
         }
+        if (store) {   /* experts stream through the HBM cache */
+            for (int e = 0; e < E; e++) {
+                const int dt = (int)mf.expert(l, e)->dtype;
+                w.expert_bytes_each = 2 * (uint64_t)F * row_bytes(dt, D) + (uint64_t)D * row_bytes(dt, F);
+                w.expert_gateup_bytes = 2 * (uint64_t)F * row_bytes(dt, D);
+                w.dtype_mask |= 1 << dt;
+            }
+            w.experts = (ExpertW *)dalloc(sizeof(ExpertW) * (size_t)E);
+            ck(hipMemset(w.experts, 0, sizeof(ExpertW) * (size_t)E));
+            continue;
+        }
         std::vector<ExpertW> table(E);
         for (int e = 0; e < E; e++) {
             const ExpertEntry *ent = mf.expert(l, e);
@@ -534,6 +545,31 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
     try {
         ck(hipSetDevice(dev));
         ck(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+        if (c.n_moe) {
+            /* HBM expert cache when HEARTH_GPU_EXPERT_CACHE_GB is below the expert set, or
+             * when the experts do not fit next to the dense weights, KV cache and scratch */
+            const uint64_t slot_b = GpuExpertStore::slot_bytes_for(D, F);
+            const uint64_t all = slot_b * (uint64_t)c.n_moe * E;
+            const uint64_t kvb = (uint64_t)L * cap * 4 * (mla ? (uint64_t)(C + rdim) : 2ull * Hkv * hd);
+            uint64_t budget = UINT64_MAX;
+            size_t freeb = 0, totb = 0;
+            ck(hipMemGetInfo(&freeb, &totb));
+            const uint64_t other = mf.dense_bytes + kvb + (4ull << 30);
+            budget = freeb > other ? freeb - other : 0;
+            if (const char *g = getenv("HEARTH_GPU_EXPERT_CACHE_GB"))
+                if (*g) budget = std::min<uint64_t>(budget, (uint64_t)(std::max(0.0, atof(g)) * 1073741824.0));
+            if (all > budget) {
+                const int n_slots = (int)std::max<uint64_t>((uint64_t)E, budget / slot_b);
+                store = std::make_unique<GpuExpertStore>();
+                if (!store->open(mf, L, E, D, F, n_slots, opt.policy, msg)) {
+                    fail(err, errlen, "%s: %s", opt.model_path, msg.c_str());
+                    return false;
+                }
+                ck(hipHostMalloc((void **)&h_meta, sizeof(int) * (size_t)(1 + E), hipHostMallocDefault));
+                log_msg(LOG_INFO, "expert cache: %d HBM slots of %.1f MiB for %d experts", n_slots,
+                        slot_b / 1048576.0, c.n_moe * E);
+            }
+        }
         if (!upload(msg)) { fail(err, errlen, "%s: %s", opt.model_path, msg.c_str()); return false; }
         /* KV cache and scratch */
         kv_layer = mla ? (size_t)cap * (C + rdim) : (size_t)2 * Hkv * cap * hd;
@@ -759,6 +795,12 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 r.table = w.experts; r.desc = slot_desc; r.n_slots = std::min(E, T * K);
                 hxl::route(r, st);
             });
+            if (store) {
+                ck(hipMemcpyAsync(h_meta, route_meta, sizeof(int) * (size_t)(1 + E), hipMemcpyDeviceToHost, st));
+                ck(hipStreamSynchronize(st));
+                store->ensure(l, h_meta + 1, h_meta[0], w.experts, st);
+                hxl::desc_refresh(slot_desc, w.experts, route_meta + 1, route_meta, std::min(E, T * K), st);
+            }
             dump("router", l, lge, T, E);
             dump("ids", l, ids, T, K);
             {
@@ -804,6 +846,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
     }
     if (want_logits)
         timed(&ks.head_s, [&] { matmul(lm_head, ax, x, D, T, logits, V, true, c.logit_scale); });
+    if (store) store->tick();
 }
 
 /* Uploads tokens and geometry for n tokens at pos (parent NULL: chain) and runs the
@@ -1070,9 +1113,20 @@ HEARTH_API int hearth_get_stats(hearth_engine *e, hearth_stats *out) {
     out->dense_s = e->ks.dense_s + e->ks.head_s + e->ks.norm_s;
     out->expert_uses = d[0] - e->stats_base[0];
     out->expert_loads_unique = d[1] - e->stats_base[1];
-    out->cache_hits = out->expert_uses;   /* every expert is resident in HBM */
-    out->cache_slots = e->c.n_moe * e->E;
-    out->cache_resident = out->cache_slots;
+    if (e->store) {
+        const StoreStats &ss = e->store->stats;
+        out->cache_hits = ss.hits - e->store_base.hits;
+        out->cache_misses = ss.misses - e->store_base.misses;
+        out->evictions = ss.evictions - e->store_base.evictions;
+        out->bytes_read = ss.bytes_read - e->store_base.bytes_read;
+        out->read_s = ss.load_s - e->store_base.load_s;
+        out->cache_slots = e->store->slots();
+        out->cache_resident = e->store->resident();
+    } else {
+        out->cache_hits = out->expert_uses;   /* every expert is resident in HBM */
+        out->cache_slots = e->c.n_moe * e->E;
+        out->cache_resident = out->cache_slots;
+    }
     return OK;
 }
 
@@ -1083,6 +1137,7 @@ HEARTH_API void hearth_reset_stats(hearth_engine *e) {
         (void)hipMemcpy(d, e->dstats, sizeof d, hipMemcpyDeviceToHost);
     e->stats_base[0] = d[0];
     e->stats_base[1] = d[1];
+    if (e->store) e->store_base = e->store->stats;
     e->tokens_done = e->forward_calls = 0;
     e->wall_s = 0.0;
     e->ks = hearth_gpu_kstats{};

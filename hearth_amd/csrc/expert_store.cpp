@@ -1,0 +1,194 @@
+/*
+ * expert_store.cpp — the HBM expert cache (expert_store.h).
+ */
+#include "expert_store.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+
+namespace hx {
+
+namespace {
+
+constexpr uint64_t ALIGN = 256;
+constexpr double HEAT_DECAY = 0.995;   /* per forward (reference default heat_decay, hx_store.h) */
+
+uint64_t al(uint64_t x) { return (x + ALIGN - 1) / ALIGN * ALIGN; }
+
+/* bytes of one tiled matrix (hx_device.h QMat layout) of the given dtype */
+void qmat_bytes(int dtype, int rows, int cols, uint64_t &w, uint64_t &d) {
+    const int rows_pad = (rows + 15) & ~15, nb = cols / 64, nbp = (nb + 1) & ~1;
+    w = (uint64_t)(rows_pad / 16) * nbp * 1024 / (dtype == HEARTH_Q4 ? 2 : 1);
+    d = 2ull * nbp * rows_pad;
+}
+
+double now_s() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+} // namespace
+
+GpuExpertStore::~GpuExpertStore() {
+    if (cs_) (void)hipStreamSynchronize(cs_);
+    for (int i = 0; i < 2; i++) {
+        if (pinned_[i]) (void)hipHostFree(pinned_[i]);
+        if (dstage_[i]) (void)hipFree(dstage_[i]);
+        if (staged_[i]) (void)hipEventDestroy(staged_[i]);
+    }
+    if (htable_) (void)hipHostFree(htable_);
+    if (done_) (void)hipEventDestroy(done_);
+    if (pool_) (void)hipFree(pool_);
+    if (cs_) (void)hipStreamDestroy(cs_);
+}
+
+hxd::QMat GpuExpertStore::carve(uint8_t *&p, int dtype, int rows, int cols) const {
+    hxd::QMat m{};
+    uint64_t wb, db;
+    qmat_bytes(HEARTH_Q8, rows, cols, wb, db);   /* room for the larger dtype */
+    m.dtype = dtype;
+    m.rows = rows;
+    m.rows_pad = (rows + 15) & ~15;
+    m.nb = cols / 64;
+    m.nbp = (m.nb + 1) & ~1;
+    m.w = p;
+    p += al(wb);
+    m.d = (const uint16_t *)p;
+    p += al(db);
+    return m;
+}
+
+uint64_t GpuExpertStore::slot_bytes_for(int D, int F) {
+    uint64_t wg, dg, wd, dd;
+    qmat_bytes(HEARTH_Q8, F, D, wg, dg);
+    qmat_bytes(HEARTH_Q8, D, F, wd, dd);
+    return 2 * (al(wg) + al(dg)) + al(wd) + al(dd);
+}
+
+bool GpuExpertStore::open(const ModelFile &mf, int L, int E, int D, int F, int n_slots, int policy, std::string &msg) {
+    mf_ = &mf;
+    L_ = L; E_ = E; D_ = D; F_ = F; n_slots_ = n_slots; policy_ = policy;
+    slot_bytes_ = slot_bytes_for(D, F);
+    for (int l = 0; l < L; l++)
+        for (int e = 0; e < E && mf.cfg.layer_kind[l]; e++) {
+            const ExpertEntry *x = mf.expert(l, e);
+            uint64_t og, ou, od;
+            const uint64_t need = slab_layout((int)x->dtype, D, F, &og, &ou, &od);
+            if (need > stage_bytes_) stage_bytes_ = need;
+        }
+    if (hipMalloc((void **)&pool_, slot_bytes_ * (uint64_t)n_slots) != hipSuccess) {
+        msg = "out of device memory for the expert cache slots";
+        return false;
+    }
+    if (hipStreamCreateWithFlags(&cs_, hipStreamNonBlocking) != hipSuccess || hipEventCreate(&done_) != hipSuccess ||
+        hipHostMalloc((void **)&htable_, sizeof(hxd::ExpertW) * (size_t)E, hipHostMallocDefault) != hipSuccess) {
+        msg = "HIP error creating the expert cache";
+        return false;
+    }
+    std::memset(htable_, 0, sizeof(hxd::ExpertW) * (size_t)E);
+    for (int i = 0; i < 2; i++)
+        if (hipHostMalloc((void **)&pinned_[i], stage_bytes_, hipHostMallocDefault) != hipSuccess ||
+            hipMalloc((void **)&dstage_[i], stage_bytes_) != hipSuccess || hipEventCreate(&staged_[i]) != hipSuccess) {
+            msg = "out of memory for the expert cache staging";
+            return false;
+        }
+    slot_.assign(n_slots, Slot{});
+    uint8_t *p = pool_;
+    for (int s = 0; s < n_slots; s++) {
+        slot_[s].w.gate = carve(p, HEARTH_Q8, F, D);
+        slot_[s].w.up = carve(p, HEARTH_Q8, F, D);
+        slot_[s].w.down = carve(p, HEARTH_Q8, D, F);
+    }
+    slot_of_.assign((size_t)L * E, -1);
+    heat_.assign((size_t)L * E, 0.0);
+    busy_.assign(n_slots, 0);
+    free_.clear();
+    for (int s = n_slots - 1; s >= 0; s--) free_.push_back(s);
+    return true;
+}
+
+int GpuExpertStore::resident() const { return n_slots_ - (int)free_.size(); }
+
+/* LRU: least recently used; LFU: lowest decayed heat, then least recently used
+ * (store.c:166-199). Slots serving the current layer are excluded. */
+int GpuExpertStore::victim() {
+    int best = -1;
+    for (int s = 0; s < n_slots_; s++) {
+        if (busy_[s]) continue;
+        if (best < 0) { best = s; continue; }
+        const Slot &x = slot_[s], &y = slot_[best];
+        if (policy_ == HEARTH_POLICY_LFU) {
+            const double hx_ = heat_[x.key], hy = heat_[y.key];
+            if (hx_ != hy) { if (hx_ < hy) best = s; continue; }
+        }
+        if (x.last_seq < y.last_seq) best = s;
+    }
+    return best;
+}
+
+void GpuExpertStore::load(int key, int s) {
+    const int l = key / E_, e = key % E_;
+    const ExpertEntry *x = mf_->expert(l, e);
+    const int dt = (int)x->dtype;
+    uint64_t og, ou, od;
+    const uint64_t len = std::min<uint64_t>(slab_layout(dt, D_, F_, &og, &ou, &od), x->nbytes);
+    const int i = cur_;
+    cur_ ^= 1;
+    if (staged_used_[i]) ck(hipEventSynchronize(staged_[i]));
+    std::memcpy(pinned_[i], mf_->data(x->offset), len);
+    ck(hipMemcpyAsync(dstage_[i], pinned_[i], len, hipMemcpyHostToDevice, cs_));
+    hxd::ExpertW &w = slot_[s].w;
+    w.gate.dtype = w.up.dtype = w.down.dtype = dt;
+    hxl::repack(dstage_[i] + og, 0, w.gate.rows_pad, w.gate, cs_);
+    hxl::repack(dstage_[i] + ou, 0, w.up.rows_pad, w.up, cs_);
+    hxl::repack(dstage_[i] + od, 0, w.down.rows_pad, w.down, cs_);
+    ck(hipEventRecord(staged_[i], cs_));
+    staged_used_[i] = true;
+    stats.loads++;
+    stats.bytes_read += len;
+}
+
+void GpuExpertStore::ensure(int layer, const int *experts, int n, hxd::ExpertW *table_dev, hipStream_t compute) {
+    const double t0 = now_s();
+    std::fill(busy_.begin(), busy_.end(), 0);
+    /* hits first, so that no miss of this layer evicts them */
+    for (int j = 0; j < n; j++) {
+        const int key = layer * E_ + experts[j], s = slot_of_[key];
+        if (s >= 0) busy_[s] = 1;
+    }
+    for (int j = 0; j < n; j++) {
+        const int e = experts[j], key = layer * E_ + e;
+        int s = slot_of_[key];
+        if (s >= 0) {
+            stats.hits++;
+        } else {
+            stats.misses++;
+            if (!free_.empty()) {
+                s = free_.back();
+                free_.pop_back();
+            } else {
+                s = victim();
+                slot_of_[slot_[s].key] = -1;
+                stats.evictions++;
+            }
+            slot_[s].key = key;
+            slot_of_[key] = s;
+            busy_[s] = 1;
+            load(key, s);
+        }
+        slot_[s].last_seq = ++seq_;
+        heat_[key] += 1.0;
+        htable_[e] = slot_[s].w;
+    }
+    ck(hipMemcpyAsync(table_dev, htable_, sizeof(hxd::ExpertW) * (size_t)E_, hipMemcpyHostToDevice, cs_));
+    ck(hipEventRecord(done_, cs_));
+    ck(hipStreamWaitEvent(compute, done_, 0));
+    stats.load_s += now_s() - t0;
+}
+
+void GpuExpertStore::tick() {
+    if (policy_ != HEARTH_POLICY_LFU) return;
+    for (double &h : heat_) h *= HEAT_DECAY;
+}
+
+} // namespace hx

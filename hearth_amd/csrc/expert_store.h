@@ -1,0 +1,86 @@
+/*
+ * expert_store.h — the HBM expert cache: routed experts streamed from host memory into
+ * a fixed pool of HBM slots when the experts do not fit (or HEARTH_GPU_EXPERT_CACHE_GB
+ * sets a smaller budget). The reference's tiered store (engine/src/store.c, hx_store.h)
+ * keeps slabs in a DRAM slot pool fed from NVMe; this is the same idea one tier up:
+ *   - slot_of[layer * E + e] direct index, slot -> key back-map;
+ *   - victims by LRU (least recently used) or LFU (decayed per-forward heat, ties by
+ *     recency), store.c:166-214; slots of the layer being served are never victims;
+ *   - a layer's demanded experts are made resident before its expert kernels run (the
+ *     compute stream waits for the loads), so results never depend on the cache
+ *     (weights are bytes, reference INV-DET-1);
+ *   - a load copies the slab from the mapped container into pinned staging, then to a
+ *     device staging buffer on a copy stream, and repacks its three matrices into the
+ *     slot's MFMA tile layout; the layer's device expert table gets the slot's matrices.
+ * Every call comes from the engine's thread (an engine handle is single-threaded).
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "hx_host.h"
+#include "hx_launch.h"
+
+namespace hx {
+
+/* A failed HIP call inside the engine or the store (caught at the C ABI). */
+struct DeviceError {
+    hipError_t e;
+};
+
+inline void ck(hipError_t e) {
+    if (e != hipSuccess) throw DeviceError{e};
+}
+
+struct StoreStats {
+    uint64_t hits = 0, misses = 0, evictions = 0, loads = 0, bytes_read = 0;
+    double load_s = 0.0;   /* host time spent issuing loads and waiting for staging */
+};
+
+class GpuExpertStore {
+public:
+    ~GpuExpertStore();
+    /* n_slots >= E; policy HEARTH_POLICY_LRU / _LFU. Returns false with msg on failure. */
+    bool open(const ModelFile &mf, int L, int E, int D, int F, int n_slots, int policy, std::string &msg);
+    /* Makes experts[0..n) of layer resident, writes their matrices into table_dev (device
+     * [E]) and makes `compute` wait for the loads. */
+    void ensure(int layer, const int *experts, int n, hxd::ExpertW *table_dev, hipStream_t compute);
+    /* forward boundary: LFU heat decay */
+    void tick();
+    /* HBM bytes of one slot for experts of D x F (room for Q8, the larger dtype) */
+    static uint64_t slot_bytes_for(int D, int F);
+    int slots() const { return n_slots_; }
+    int resident() const;
+    uint64_t slot_bytes() const { return slot_bytes_; }
+    StoreStats stats;
+
+private:
+    struct Slot {
+        int key = -1;
+        uint64_t last_seq = 0;
+        hxd::ExpertW w{};
+    };
+    const ModelFile *mf_ = nullptr;
+    int L_ = 0, E_ = 0, D_ = 0, F_ = 0, n_slots_ = 0, policy_ = 0;
+    uint64_t slot_bytes_ = 0, stage_bytes_ = 0, seq_ = 0;
+    uint8_t *pool_ = nullptr;
+    std::vector<Slot> slot_;
+    std::vector<int> slot_of_, free_;
+    std::vector<double> heat_;
+    std::vector<uint8_t> busy_;       /* slot holds an expert of the layer being served */
+    hipStream_t cs_ = nullptr;        /* copy stream (default priority) */
+    uint8_t *pinned_[2] = {nullptr, nullptr}, *dstage_[2] = {nullptr, nullptr};
+    hipEvent_t staged_[2] = {nullptr, nullptr};
+    bool staged_used_[2] = {false, false};
+    int cur_ = 0;
+    hxd::ExpertW *htable_ = nullptr;  /* pinned [E]: entries written this call */
+    hipEvent_t done_ = nullptr;
+    hxd::QMat carve(uint8_t *&p, int dtype, int rows, int cols) const;
+    int victim();
+    void load(int key, int slot);
+};
+
+} // namespace hx

@@ -239,6 +239,9 @@ void kv_move(float *cache_layer0, size_t layer_stride, int L, int Hkv, int cap, 
 /* rows pos0 + path[j] -> pos0 + j of a [cap][width] array at offset off of every layer */
 void kv_move_rows(float *cache, size_t layer_stride, int L, size_t off, int width, int pos0, const int *path, int n,
                   hipStream_t st);
+/* desc[u].w = table[ulist[u]] for u < *n_active (after the expert cache served a layer) */
+void desc_refresh(SlotDesc *desc, const ExpertW *table, const int *ulist, const int *n_active, int n_slots,
+                  hipStream_t st);
 void accept_greedy(const AcceptArgs &a, hipStream_t st);
 /* Sampler settings of one sampled acceptance (the reference's Sampler fields). */
 struct SamplerSpec {

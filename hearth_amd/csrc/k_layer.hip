@@ -590,6 +590,14 @@ __global__ void k_kv_move_rows(float *cache, size_t layer_stride, int L, size_t 
     }
 }
 
+/* Slot descriptors' matrices after the expert cache made the layer's experts resident
+ * (the bucketing wrote them from the table before the cache updated it). */
+__global__ void k_desc_refresh(SlotDesc *desc, const ExpertW *table, const int *ulist, const int *n_active,
+                               int n_slots) {
+    const int u = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (u < n_slots && u < *n_active) desc[u].w = table[ulist[u]];
+}
+
 /* ------------------------------------------------------------ greedy acceptance */
 
 /* Greedy argmax of the verify rows, first index on ties, -1 for rows with a NaN or +inf
@@ -721,6 +729,11 @@ void kv_move_rows(float *cache, size_t layer_stride, int L, size_t off, int widt
     const int64_t threads = (int64_t)L * width;
     if (threads && n > 0)
         k_kv_move_rows<<<(int)((threads + 255) / 256), 256, 0, st>>>(cache, layer_stride, L, off, width, pos0, path, n);
+}
+
+void desc_refresh(SlotDesc *desc, const ExpertW *table, const int *ulist, const int *n_active, int n_slots,
+                  hipStream_t st) {
+    if (n_slots > 0) k_desc_refresh<<<(n_slots + 255) / 256, 256, 0, st>>>(desc, table, ulist, n_active, n_slots);
 }
 
 void accept_greedy(const AcceptArgs &a, hipStream_t st) {

@@ -1,0 +1,138 @@
+"""The HBM expert cache (hearth_amd/csrc/expert_store.cpp) on the GPU.
+
+With HEARTH_GPU_EXPERT_CACHE_GB far below the expert set, every MoE layer streams its
+experts from host memory through a pool of E slots:
+
+- logits (prompt, chain verify, tree verify + commit) are bit-identical to the engine
+  with every expert resident: the cache moves bytes, never changes numerics
+  (reference INV-DET-1);
+- hits, misses and evictions equal a replay of the victim policy (LRU: least recently
+  used; LFU: lowest decayed heat, then least recent, store.c:166-199) over the routing
+  trace: per call and MoE layer the active experts in ascending order;
+- hearth_get_stats reports them (cache_hits / cache_misses / evictions / bytes_read).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from hearth_amd import container
+from hearth_amd.engine import Engine
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def _run(path, calls, **kw):
+    """logits of each call (lists of tokens, or ("tree", tokens, parent, path))"""
+    out = []
+    with Engine(path, max_seq=512, **kw) as e:
+        for c in calls:
+            if c[0] == "tree":
+                _, tok, par, commit = c
+                out.append(e.verify_tree(tok, par))
+                e.commit_path(commit)
+            else:
+                out.append(e.eval(c, all_logits=True))
+        stats = e.stats()
+    return out, stats
+
+
+def _replay(trace_routes, call_sizes, n_moe, E, n_slots, policy):
+    """hits, misses, evictions of the cache policy over the calls' routes"""
+    slot_key = [-1] * n_slots
+    slot_seq = [0] * n_slots
+    where = {}
+    heat = {}
+    seq = 0
+    hits = misses = evictions = 0
+    row = 0
+    for n in call_sizes:
+        rows = trace_routes[row:row + n]
+        row += n
+        for m in range(n_moe):
+            active = sorted(set(int(x) for x in rows[:, m, :].ravel()))
+            busy = {where[(m, e)] for e in active if (m, e) in where}
+            for e in active:
+                k = (m, e)
+                if k in where:
+                    hits += 1
+                    s = where[k]
+                else:
+                    misses += 1
+                    free = [s for s in range(n_slots) if slot_key[s] == -1]
+                    if free:
+                        s = free[0]
+                    else:
+                        cand = [s for s in range(n_slots) if s not in busy]
+                        if policy == "lfu":
+                            s = min(cand, key=lambda s: (heat.get(slot_key[s], 0.0), slot_seq[s], s))
+                        else:
+                            s = min(cand, key=lambda s: (slot_seq[s], s))
+                        del where[slot_key[s]]
+                        evictions += 1
+                    slot_key[s] = k
+                    where[k] = s
+                    busy.add(s)
+                seq += 1
+                slot_seq[s] = seq
+                heat[k] = heat.get(k, 0.0) + 1.0
+        if policy == "lfu":
+            for k in heat:
+                heat[k] *= 0.995
+    return hits, misses, evictions
+
+
+@pytest.mark.parametrize("policy", ["lru", "lfu"])
+def test_streamed_experts_bit_identical_and_policy(tiny_model, monkeypatch, tmp_path, policy):
+    toks = container.uniform_ints(51, 60, container.TINY.vocab)
+    calls = [list(toks[:40]), list(toks[40:45]), [int(t) for t in toks[45:46]],
+             ("tree", np.array([7, 11, 900, 5, 12], np.int32), np.array([-1, 0, 0, 1, 2], np.int32), [0, 1, 3])]
+    ref, _ = _run(tiny_model, calls)
+    monkeypatch.setenv("HEARTH_GPU_EXPERT_CACHE_GB", "0.001")
+    with Engine(tiny_model, max_seq=512, policy=policy) as e:
+        tr = tmp_path / "r.hrtr"
+        e.trace_start(tr)
+        got = []
+        for c in calls:
+            if c[0] == "tree":
+                _, tok, par, commit = c
+                got.append(e.verify_tree(tok, par))
+                e.commit_path(commit)
+            else:
+                got.append(e.eval(c, all_logits=True))
+        e.trace_stop()
+        st = e.stats()
+        after = e.eval([3])
+    for a, b in zip(ref, got):
+        assert np.array_equal(_bits(a), _bits(b))
+    assert st["cache_slots"] == 16 and st["cache_misses"] > 0 and st["evictions"] > 0
+    routes = np.frombuffer(tr.read_bytes()[24:], dtype="<u2").reshape(-1, 4, 4)
+    sizes = [40, 5, 1, 5]
+    want = _replay(routes, sizes, 4, 16, 16, policy)
+    assert (st["cache_hits"], st["cache_misses"], st["evictions"]) == want
+    assert st["cache_hits"] + st["cache_misses"] == st["expert_loads_unique"]
+    assert st["bytes_read"] == st["cache_misses"] * 208896
+    # the committed KV after streaming is the resident engine's
+    with Engine(tiny_model, max_seq=512) as e2:
+        for c in calls:
+            if c[0] == "tree":
+                e2.verify_tree(c[1], c[2], want_logits=False)
+                e2.commit_path(c[3])
+            else:
+                e2.eval(c)
+        assert np.array_equal(_bits(after), _bits(e2.eval([3])))
+
+
+def test_streamed_experts_deepseek_shape(variant_models, monkeypatch):
+    path = variant_models("dsv3")
+    toks = container.uniform_ints(52, 30, 4096)
+    ref, _ = _run(path, [list(toks[:25]), list(toks[25:])])
+    monkeypatch.setenv("HEARTH_GPU_EXPERT_CACHE_GB", "0.0001")
+    got, st = _run(path, [list(toks[:25]), list(toks[25:])])
+    for a, b in zip(ref, got):
+        assert np.array_equal(_bits(a), _bits(b))
+    assert st["cache_slots"] == 16 and st["evictions"] > 0
