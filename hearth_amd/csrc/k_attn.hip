@@ -128,6 +128,87 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     }
 }
 
+/* The same scores with the 16 dot16 partials on 16 lanes instead of 16 registers
+ * (head_dim a multiple of 64): thread (row, j) accumulates partial j of its row, the
+ * elements j, j + 16, ... in order, for 8 heads at a time; the 8/4/2/1 tree then runs
+ * across the 16 lanes of the row with DPP row shifts (lane j adds lane j + s, exactly
+ * the canonical pairing). 8 accumulators per thread instead of 128 let eight waves per
+ * SIMD hide the load latency. A row's K elements j + 16 i are loaded straight from the
+ * cache (16 lanes read 64 contiguous bytes); q of the 8 heads is staged transposed in
+ * LDS (qT[h][j][i] = q[h][16 i + j]), read four i at a time. */
+constexpr int S16_NP = 2;              /* 16-row passes per workgroup */
+constexpr int S16_RB = 16 * S16_NP;    /* rows per workgroup */
+
+template <int HI>
+__global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
+    __shared__ float4 qT[8][16][HI / 4];
+    const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
+    int b = blockIdx.x;
+    const int g = b % Hkv;
+    b /= Hkv;
+    const int t = b % a.T, c = b / a.T;
+    const int nr = a.g.pos0 + a.g.depth[t] + 1;
+    const int v0 = c * S16_RB;
+    if (v0 >= nr) return;   /* uniform */
+    const int tid = threadIdx.x, j = tid & 15, rl = tid >> 4;
+    float kv[S16_NP][HI];
+    int vrow[S16_NP];
+#pragma unroll
+    for (int pass = 0; pass < S16_NP; pass++) {
+        const int v = v0 + pass * 16 + rl;
+        vrow[pass] = v;
+        const float *kr = a.kc + ((size_t)g * a.cap + row_slot(a.g, t, v < nr ? v : nr - 1)) * hd + j;
+#pragma unroll
+        for (int i = 0; i < HI; i++) kv[pass][i] = kr[16 * i];
+    }
+    for (int h0 = 0; h0 < grp; h0 += 8) {
+        __syncthreads();
+        {
+            const float *qb = a.q + ((size_t)t * a.H + (size_t)g * grp + h0) * hd;
+            float *qf = (float *)qT;
+            for (int x = tid; x < 8 * hd; x += 256) {
+                const int hh = x / hd, e = x % hd;
+                qf[(hh * 16 + (e & 15)) * HI + (e >> 4)] = h0 + hh < grp ? qb[(size_t)hh * hd + e] : 0.0f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int pass = 0; pass < S16_NP; pass++) {
+            float acc[8];
+#pragma unroll
+            for (int hh = 0; hh < 8; hh++) acc[hh] = 0.0f;
+#pragma unroll
+            for (int i4 = 0; i4 < HI / 4; i4++) {
+#pragma unroll
+                for (int hh = 0; hh < 8; hh++) {
+                    const float4 q4 = qT[hh][j][i4];
+                    acc[hh] = fadd(acc[hh], fmul(q4.x, kv[pass][4 * i4]));
+                    acc[hh] = fadd(acc[hh], fmul(q4.y, kv[pass][4 * i4 + 1]));
+                    acc[hh] = fadd(acc[hh], fmul(q4.z, kv[pass][4 * i4 + 2]));
+                    acc[hh] = fadd(acc[hh], fmul(q4.w, kv[pass][4 * i4 + 3]));
+                }
+            }
+#pragma unroll
+            for (int hh = 0; hh < 8; hh++) {
+                /* row_shl:s (DPP control 0x100 + s): lane j reads lane j + s of its row */
+#define HX_DPP_ADD(cc) acc[hh] = fadd(acc[hh], __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc[hh]), cc, 0xF, 0xF, true)))
+                HX_DPP_ADD(0x108);
+                HX_DPP_ADD(0x104);
+                HX_DPP_ADD(0x102);
+                HX_DPP_ADD(0x101);
+#undef HX_DPP_ADD
+            }
+            const int v = vrow[pass];
+            if (j == 0 && v < nr) {
+                float *Sb = a.S + ((size_t)t * a.H + (size_t)g * grp + h0) * a.ldS + v;
+#pragma unroll
+                for (int hh = 0; hh < 8; hh++)
+                    if (h0 + hh < grp) Sb[(size_t)hh * a.ldS] = fmul(a.scale, canon(acc[hh]));
+            }
+        }
+    }
+}
+
 __device__ __forceinline__ float sum16_lds(const float *es, int n, int lane16, float L) {
     /* lane lane16 of 16: continues the sequential sum L with es[lane16], es[lane16 + 16],
      * ..., the next 8 operands read while the current 8 are added */
@@ -380,6 +461,19 @@ namespace hxl {
 
 void attention_scores(const AttnArgs &a, hipStream_t st) {
     const int max_nr = a.g.pos0 + a.T;   /* depth[t] <= t */
+    if (a.hd % 64 == 0 && a.hd <= 512) {
+        const int grid = ((max_nr + S16_RB - 1) / S16_RB) * a.T * a.Hkv;
+        switch (a.hd / 16) {
+        case 4: k_attn_scores16<4><<<grid, 256, 0, st>>>(a); return;
+        case 8: k_attn_scores16<8><<<grid, 256, 0, st>>>(a); return;
+        case 12: k_attn_scores16<12><<<grid, 256, 0, st>>>(a); return;
+        case 16: k_attn_scores16<16><<<grid, 256, 0, st>>>(a); return;
+        case 20: k_attn_scores16<20><<<grid, 256, 0, st>>>(a); return;
+        case 24: k_attn_scores16<24><<<grid, 256, 0, st>>>(a); return;
+        case 28: k_attn_scores16<28><<<grid, 256, 0, st>>>(a); return;
+        default: k_attn_scores16<32><<<grid, 256, 0, st>>>(a); return;
+        }
+    }
     const int nchunks = (max_nr + SC_ROWS - 1) / SC_ROWS;
     const int grp = a.H / a.Hkv, nsc = nchunks * a.T * a.Hkv;
     if (grp % 8 == 0) k_attn_scores<8><<<nsc, SC_ROWS, 0, st>>>(a);

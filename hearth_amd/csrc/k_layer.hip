@@ -375,15 +375,22 @@ __device__ void bucket_pairs(const RouteArgs &a, const int *ids, int *cnt, int *
     }
     __syncthreads();
     for (int u = nu_sh + tid; u < a.n_slots; u += nth) a.desc[u].n = 0;
-    for (int e = tid; e < E; e += nth) {
-        if (!cnt[e]) continue;
-        int pos = base[e];
-        for (int p = 0; p < P; p++)
-            if (ids[p] == e) {
-                a.pair_tok[pos] = p / a.K;
-                a.pair_of[p] = pos;
-                pos++;
-            }
+    /* pair p goes after the earlier pairs of its expert (tokens ascending within an
+     * expert, model.c:1030-1035): its rank = how many pairs q < p have the same id */
+    for (int p = tid; p < P; p += nth) {
+        const int e = ids[p];
+        int r = 0, q = 0;
+        for (; q + 8 <= p; q += 8) {
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = ids[q + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) r += v[u] == e ? 1 : 0;
+        }
+        for (; q < p; q++) r += ids[q] == e ? 1 : 0;
+        const int pos = base[e] + r;
+        a.pair_tok[pos] = p / a.K;
+        a.pair_of[p] = pos;
     }
 }
 
@@ -463,14 +470,15 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
             if (lane == 0) chosen[t][j] = e;
         }
         wave_sync();
+        const int id = lane < K ? chosen[t][lane] : 0;
+        float w = lane < K ? sc[id] : 0.0f;
+        if (a.norm_topk) {
+            /* sum of the K weights in rank order (route_weights, model.c:830-838) */
+            float s = 0.0f;
+            for (int j = 0; j < K; j++) s = fadd(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j)));
+            w = fdiv(w, fadd(s, 1e-20f));
+        }
         if (lane < K) {
-            const int id = chosen[t][lane];
-            float w = sc[id];
-            if (a.norm_topk) {
-                float s = 0.0f;
-                for (int j = 0; j < K; j++) s = fadd(s, sc[chosen[t][j]]);
-                w = fdiv(w, fadd(s, 1e-20f));
-            }
             w = fmul(w, a.routed_scale);
             a.ids[(size_t)t * K + lane] = id;
             a.wts[(size_t)t * K + lane] = w;
