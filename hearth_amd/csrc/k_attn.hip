@@ -11,8 +11,8 @@
  *
  * The value sum is one dependent f32 add chain per (token, head, d) of length
  * pos0 + depth + 1; it is the step's latency floor, so the value kernel keeps one
- * chain per lane, one wave per SIMD, and V tiles prefetched two tiles ahead into an
- * LDS ring shared by the four waves (heads) of a workgroup.
+ * chain per lane, one summing wave per SIMD, and V tiles streamed three tiles ahead
+ * into an LDS ring shared by the four summing waves (heads) of a workgroup.
  *
  * Launch shapes are XCD-aware: workgroup IDs are dealt round-robin to the 8 XCDs,
  * so the KV-group index (and value d-chunk) is the fastest-varying part of the ID and
@@ -316,21 +316,28 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
 
 /* o[t][h][d] = sum_v p_v * V_v[d], v in order. A workgroup sums up to four heads of
  * one token t in one KV group g, for one 64-wide d chunk (one wave per head, lane = d),
- * and has four more waves that only stage tiles, so that the summing waves issue
- * nothing but LDS reads, multiplies and adds.
- * The sum is one dependent f32 add per row, so the kernel is built around that chain:
- * products of 16 rows are formed before their 16 adds (a product never waits in front of
- * the chain), rows come in tiles of 128 through a 3-slot LDS ring (one barrier per 128
- * rows), and each tile is requested VPF tiles before it is written to LDS. Loads are
- * unconditional: tile indexes are clamped to the last tile and rows/columns to valid
- * ones; rows past the chain are never read back, columns past head_dim only feed
- * discarded lanes. */
-constexpr int VT2 = 128;
-constexpr int VPF = 3;   /* register tile sets: the code below names three */
+ * and has four more waves that only move data: they issue LDS-direct loads
+ * (global_load_lds: the bytes go from memory straight into LDS, no registers, a few
+ * address instructions per KiB), so the summing waves keep their SIMD's VALU to the
+ * product + dependent add of each row. Tiles of 128 rows and their p values cycle
+ * through a 4-slot LDS ring: while tile i is summed, tiles i+1 and i+2 are in flight
+ * and tile i+3 is issued into the slot of tile i-1. A loader wave waits (vmcnt) only
+ * for the tile it is about to publish and then joins the barrier without a release
+ * fence (a fence would wait for every load in flight). Products of 16 rows are formed
+ * before their 16 adds, so no product waits in front of the chain. Loads are
+ * unconditional: tile indexes are clamped to the last tile and rows to valid ones;
+ * rows past the chain are never read back, columns past head_dim only feed discarded
+ * lanes; every LDS write has landed before the workgroup ends. */
+constexpr int VT2 = 128;              /* rows per tile */
+constexpr int VNS = 4;                /* LDS ring slots: one summed, three in flight */
+constexpr int VLPT = 10;              /* loads per loader wave per tile: 8 x 1 KiB of V, 2 x 64 p */
+
+/* s_waitcnt with vmcnt = n and the other counters unconstrained (gfx9 encoding) */
+#define HX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 
 __global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
-    __shared__ float vt[3][VT2][64];
-    __shared__ float pt[3][4][VT2];
+    __shared__ __attribute__((aligned(16))) float vt[VNS][VT2][64];
+    __shared__ __attribute__((aligned(16))) float pt[VNS][4][VT2];
     __shared__ int anc_s[MAX_ANC];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
     const int nd = (hd + 63) / 64, qpt = (grp + 3) / 4;
@@ -341,114 +348,84 @@ __global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
     b /= Hkv;
     const int hq = b % qpt, t = b / qpt;
     const int tid = threadIdx.x, wave = (tid >> 6) & 3, lane = tid & 63;
-    const bool loader = tid >= 256;   /* waves 4..7 stage tiles; waves 0..3 sum */
+    const bool loader = tid >= 256;
     const int hh = hq * 4 + wave;
     const bool live = hh < grp;
     const int h = g * grp + (live ? hh : 0);
     const int pos0 = a.g.pos0, dep = a.g.depth[t];
     const int nr = pos0 + dep + 1;
     const int ntiles = (nr + VT2 - 1) / VT2, last = ntiles - 1;
-    for (int j = tid; j <= dep; j += 512) anc_s[j] = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + j];
+    for (int jj = tid; jj <= dep; jj += 512) anc_s[jj] = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + jj];
     __syncthreads();
-    /* loader thread l = tid - 256: float4 u of the tile is float4 k = 256 u + l: row
-     * k / 16, float4 column k % 16; p rows of head (l / 64) */
-    const int l = tid & 255;
-    const float *p = a.S + ((size_t)t * a.H + h) * a.ldS;   /* head of wave (tid/64)%4 */
-    const int c4 = (l & 15) * 4, rbase = l >> 4;
-    const float *vcol = a.vc + (size_t)g * a.cap * hd + (dc * 64 + c4 < hd ? dc * 64 + c4 : 0);
-    auto row_of = [&](int i, int u) -> const float * {
-        i = i < last ? i : last;
-        int v = i * VT2 + 16 * u + rbase;
-        v = v < nr ? v : nr - 1;
-        return vcol + (size_t)(v < pos0 ? v : anc_s[v - pos0]) * hd;
-    };
-    auto p_of = [&](int i, int k) -> float {
-        i = i < last ? i : last;
-        const int vp = i * VT2 + k * 64 + lane;
-        return p[vp < nr ? vp : nr - 1];
-    };
-#define HX_VREGS(k) float4 r##k##0, r##k##1, r##k##2, r##k##3, r##k##4, r##k##5, r##k##6, r##k##7; float rp##k##a, rp##k##b
-#define HX_VLD1(i, k, q) r##k##q = *(const float4 *)row_of(i, q)
-#define HX_VST1(slot, k, q) *(float4 *)&vt[slot][16 * q + rbase][c4] = r##k##q
-#define HX_VLOAD(i, k)                                                                   \
-    do {                                                                                 \
-        HX_VLD1(i, k, 0); HX_VLD1(i, k, 1); HX_VLD1(i, k, 2); HX_VLD1(i, k, 3);          \
-        HX_VLD1(i, k, 4); HX_VLD1(i, k, 5); HX_VLD1(i, k, 6); HX_VLD1(i, k, 7);          \
-        rp##k##a = p_of(i, 0);                                                           \
-        rp##k##b = p_of(i, 1);                                                           \
-    } while (0)
-#define HX_VSTORE(slot, k)                                                               \
-    do {                                                                                 \
-        HX_VST1(slot, k, 0); HX_VST1(slot, k, 1); HX_VST1(slot, k, 2); HX_VST1(slot, k, 3); \
-        HX_VST1(slot, k, 4); HX_VST1(slot, k, 5); HX_VST1(slot, k, 6); HX_VST1(slot, k, 7); \
-        pt[slot][wave][lane] = rp##k##a;                                                 \
-        pt[slot][wave][64 + lane] = rp##k##b;                                            \
-    } while (0)
-    HX_VREGS(0);
-    HX_VREGS(1);
-    HX_VREGS(2);
     float acc = 0.0f;
-    auto compute = [&](int i) {
-        const int slot = i % 3, nv = nr - i * VT2;
-        const float *pw = pt[slot][wave], *vw = &vt[slot][0][lane];
-        if (nv >= VT2) {
-            float pA[16], vA[16], pB[16], vB[16];
-#define HX_GRD(P_, V_, c_)                                                               \
-            _Pragma("unroll") for (int j = 0; j < 16; j++) { P_[j] = pw[(c_) + j]; V_[j] = vw[((c_) + j) * 64]; }
-#define HX_GSUM(P_, V_)                                                                  \
-            {                                                                            \
-                float pr[16];                                                            \
-                _Pragma("unroll") for (int j = 0; j < 16; j++) pr[j] = fmul(P_[j], V_[j]); \
-                _Pragma("unroll") for (int j = 0; j < 16; j++) acc = fadd(acc, pr[j]);   \
+    if (loader) {
+        /* loader wave w: rows w*32 + 4k + lane/16 of each tile (k = 0..7), float4 column
+         * lane%16; its head's p (two 64-entry dword loads per tile) */
+        const int c4 = (lane & 15) * 4, rsub = lane >> 4;
+        const float *vcol = a.vc + (size_t)g * a.cap * hd + (dc * 64 + c4 < hd ? dc * 64 + c4 : 0);
+        const float *prow = a.S + ((size_t)t * a.H + h) * a.ldS;
+        auto issue = [&](int i) {
+            const int ti = i < last ? i : last, slot = i % VNS;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                int v = ti * VT2 + wave * 32 + 4 * k + rsub;
+                v = v < nr ? v : nr - 1;
+                const float *src = vcol + (size_t)(v < pos0 ? v : anc_s[v - pos0]) * hd;
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                                 (__attribute__((address_space(3))) void *)&vt[slot][wave * 32 + 4 * k][0],
+                                                 16, 0, 0);
             }
-            HX_GRD(pA, vA, 0)
-            HX_GRD(pB, vB, 16) HX_GSUM(pA, vA)
-            HX_GRD(pA, vA, 32) HX_GSUM(pB, vB)
-            HX_GRD(pB, vB, 48) HX_GSUM(pA, vA)
-            HX_GRD(pA, vA, 64) HX_GSUM(pB, vB)
-            HX_GRD(pB, vB, 80) HX_GSUM(pA, vA)
-            HX_GRD(pA, vA, 96) HX_GSUM(pB, vB)
-            HX_GRD(pB, vB, 112) HX_GSUM(pA, vA)
-            HX_GSUM(pB, vB)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                int vp = ti * VT2 + c * 64 + lane;
+                vp = vp < nr ? vp : nr - 1;
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(prow + vp),
+                                                 (__attribute__((address_space(3))) void *)&pt[slot][wave][c * 64], 4,
+                                                 0, 0);
+            }
+        };
+        issue(0);
+        issue(1);
+        issue(2);
+        for (int i = 0; i < ntiles; i++) {
+            /* tile i landed (tiles i+1, i+2 may be in flight); a bare barrier, so that no
+             * release fence waits for the loads still in flight */
+            HX_WAIT_VMCNT(2 * VLPT);
+            __builtin_amdgcn_s_barrier();
+            issue(i + 3);              /* into the slot of tile i - 1, summed before this barrier */
+        }
+        HX_WAIT_VMCNT(0);              /* no LDS write may land after the workgroup ends */
+    } else {
+        const float *const pw0 = pt[0][wave], *const vw0 = &vt[0][0][lane];
+        for (int i = 0; i < ntiles; i++) {
+            __syncthreads();
+            const int slot = i % VNS, nv = nr - i * VT2;
+            const float *pw = pw0 + slot * (4 * VT2), *vw = vw0 + slot * (VT2 * 64);
+            if (nv >= VT2) {
+                float pA[16], vA[16], pB[16], vB[16];
+#define HX_GRD(P_, V_, c_)                                                               \
+                _Pragma("unroll") for (int j = 0; j < 16; j++) { P_[j] = pw[(c_) + j]; V_[j] = vw[((c_) + j) * 64]; }
+#define HX_GSUM(P_, V_)                                                                  \
+                {                                                                        \
+                    float pr[16];                                                        \
+                    _Pragma("unroll") for (int j = 0; j < 16; j++) pr[j] = fmul(P_[j], V_[j]); \
+                    _Pragma("unroll") for (int j = 0; j < 16; j++) acc = fadd(acc, pr[j]); \
+                }
+                HX_GRD(pA, vA, 0)
+                HX_GRD(pB, vB, 16) HX_GSUM(pA, vA)
+                HX_GRD(pA, vA, 32) HX_GSUM(pB, vB)
+                HX_GRD(pB, vB, 48) HX_GSUM(pA, vA)
+                HX_GRD(pA, vA, 64) HX_GSUM(pB, vB)
+                HX_GRD(pB, vB, 80) HX_GSUM(pA, vA)
+                HX_GRD(pA, vA, 96) HX_GSUM(pB, vB)
+                HX_GRD(pB, vB, 112) HX_GSUM(pA, vA)
+                HX_GSUM(pB, vB)
 #undef HX_GSUM
 #undef HX_GRD
-        } else {
-            for (int r = 0; r < nv; r++) acc = fadd(acc, fmul(pw[r], vw[r * 64]));
+            } else {
+                for (int r = 0; r < nv; r++) acc = fadd(acc, fmul(pw[r], vw[r * 64]));
+            }
         }
-    };
-    if (loader) {
-        HX_VLOAD(0, 0);
-        HX_VSTORE(0, 0);
-        HX_VLOAD(1, 0);
-        HX_VSTORE(1, 0);
-        HX_VLOAD(2, 0);
-        HX_VLOAD(3, 1);
-        HX_VLOAD(4, 2);
-    }
-    __syncthreads();
-    /* step i: the summing waves use tile i (slot i % 3) while the loaders write tile i + 2
-     * (register set i - i0) to slot (i + 2) % 3 (it held tile i - 1, summed before the
-     * previous barrier) and then request tile i + 2 + VPF */
-#define HX_VSTEP(k)                                                                      \
-    do {                                                                                 \
-        const int i_ = i0 + k;                                                           \
-        if (loader) HX_VSTORE((i_ + 2) % 3, k);                                          \
-        else compute(i_);                                                                \
-        __syncthreads();                                                                 \
-        if (loader) HX_VLOAD(i_ + 2 + VPF, k);                                           \
-    } while (0)
-    for (int i0 = 0; i0 < ntiles; i0 += VPF) {
-        HX_VSTEP(0);
-        HX_VSTEP(1);
-        HX_VSTEP(2);
-    }
-#undef HX_VSTEP
-#undef HX_VSTORE
-#undef HX_VLOAD
-#undef HX_VST1
-#undef HX_VLD1
-#undef HX_VREGS
-    if (!loader) {
         const int d = dc * 64 + lane;
         if (live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = acc;
         if (a.qo_on && live) quant_block_wave(acc, a.qo, a.qo_hm ? h * a.T + t : t, a.qo_hm ? dc : h * (hd >> 6) + dc);
