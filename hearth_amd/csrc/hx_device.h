@@ -89,6 +89,30 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)x;
 }
 
+/* ---- memory helpers (device) ---- */
+
+/* s_waitcnt with vmcnt = n and the other counters unconstrained (gfx9 encoding) */
+#define HX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+
+/* LDS-direct load: lane l copies SZ (4 or 16) bytes from its src to dst + l * SZ, with
+ * no register in between; counted by vmcnt like any other load */
+template <int SZ>
+__device__ __forceinline__ void lds_direct(const void *src, void *dst) {
+    static_assert(SZ == 4 || SZ == 16, "LDS-direct loads of 4 or 16 bytes");
+    if constexpr (SZ == 16)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                         (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                         (__attribute__((address_space(3))) void *)dst, 4, 0, 0);
+}
+
+/* 16-byte load from global memory (explicit address space: a global_load, never flat) */
+template <typename V>
+__device__ __forceinline__ V gload(const void *p) {
+    return *(const __attribute__((address_space(1))) V *)p;
+}
+
 /* exp in IEEE double from basic operations (Cody & Waite 1980 reduction with a
  * 32-bit ln2 head, degree-13 Taylor series on |r| <= ln2/2, exact power-of-two
  * scaling in two steps); the CPU restatement's ho_exp_port_d is the same function. */

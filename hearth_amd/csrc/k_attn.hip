@@ -332,9 +332,6 @@ constexpr int VT2 = 128;              /* rows per tile */
 constexpr int VNS = 4;                /* LDS ring slots: one summed, three in flight */
 constexpr int VLPT = 10;              /* loads per loader wave per tile: 8 x 1 KiB of V, 2 x 64 p */
 
-/* s_waitcnt with vmcnt = n and the other counters unconstrained (gfx9 encoding) */
-#define HX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
-
 __global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float vt[VNS][VT2][64];
     __shared__ __attribute__((aligned(16))) float pt[VNS][4][VT2];

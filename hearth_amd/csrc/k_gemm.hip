@@ -174,6 +174,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs args) {
  * barrier one thread per (row, token) folds the terms of blocks 0, 1, ... in order, so
  * the result is the one-lane fold bit for bit. */
 constexpr int SK_MAXP = 4;      /* block pairs per wave */
+constexpr int TK_WAVES = 4;     /* waves per workgroup of the split-K gate/up kernel */
+constexpr size_t TK_LDS_MAX = 65536;
 constexpr int SK_LDS = 65536;   /* bytes of terms per workgroup */
 constexpr int SK_DUMMY = 1024;  /* LDS after the terms: stores of padding token columns */
 
@@ -492,6 +494,183 @@ __global__ __launch_bounds__(256) void k_expert_gateup_pp(MoeArgs a, int ntok) {
     }
 }
 
+/* Gate/up for experts of at most 16 tokens, K split over S waves per row tile.
+ *
+ * Workgroup = (token group g, active slot, rpw row tiles of 16 F rows); S waves per row
+ * tile. Wave (row tile r, part p) streams block pairs [p TK_NP, (p + 1) TK_NP) of the
+ * tile's gate and up matrices into registers, every load issued at once. The slot's
+ * activations are staged once per workgroup in LDS by LDS-direct loads, in the MFMA
+ * B-operand layout with column = token.
+ *
+ * Tokens go in groups of four: for group g the B operand of column c is read from token
+ * 4 g + c % 4, so the MFMA result holds each (row, token) pair four times and lane
+ * (kg = l / 16, lr = l % 16) keeps register lr / 4: row 4 kg + lr / 4, token
+ * 4 g + lr % 4 -- one useful term per lane, matrix and block, where the 16 token
+ * columns of the plain layout would leave most lanes working on padding.
+ *
+ * Sums: part 0 folds its blocks from 0.0; part p > 0 keeps its terms in registers,
+ * takes the running sums of part p - 1 through LDS after barrier p and adds its terms
+ * in block order, so each sum is the sequential fold acc = acc + isum (dw dx) over
+ * blocks 0 .. nb-1. The last part writes SwiGLU(gate) * up. */
+template <int DT>
+struct TkCfg {
+    static constexpr int NP = DT == 4 ? 8 : 4;   /* block pairs per wave (registers) */
+    static constexpr int NV = DT == 4 ? 1 : 2;   /* 16-byte loads per pair, matrix and lane */
+};
+
+/* register q of c */
+__device__ __forceinline__ int pick4(const v4i &c, int q) {
+    const int lo = (q & 1) ? c.y : c.x, hi = (q & 1) ? c.w : c.z;
+    return (q & 2) ? hi : lo;
+}
+
+template <int DT>
+__global__ __launch_bounds__(512) void k_expert_gateup_tk(MoeArgs a, int rpw, int S, int gmax) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t tk_lds[];
+    constexpr int NP = TkCfg<DT>::NP, NV = TkCfg<DT>::NV, NBK = 2 * NP;
+    const int ntile = a.F / 16, tpw = (ntile + rpw - 1) / rpw;
+    const int g = (int)blockIdx.x % gmax, rest = (int)blockIdx.x / gmax;
+    const int u = rest / tpw;
+    if (u >= *a.n_active) return;   /* uniform */
+    const SlotDesc &sd = a.desc[u];
+    const QMat mg = sd.w.gate, mu = sd.w.up;
+    const int n = sd.n, p0 = sd.p0;
+    if (mg.dtype != DT || 4 * g >= n) return;   /* uniform */
+    const int W = rpw * S;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int rtl = wave / S, part = wave % S;
+    const int lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
+    const int rt0 = (rest % tpw) * rpw + rtl;
+    const bool live = rt0 < ntile;   /* uniform per wave */
+    const int rt = live ? rt0 : ntile - 1;   /* a dead wave loads a live tile and discards it */
+    const int nb = mg.nb, nbp = mg.nbp, npair = nbp >> 1, nbp4 = (nbp + 3) & ~3;
+    const int g0 = part * NP, kb0 = 2 * g0;   /* first pair / block of this part */
+    uint8_t *xs = tk_lds;                                   /* [nbp][64 lanes][16 B] */
+    float *dxs = (float *)(xs + (size_t)nbp * 1024);        /* [nbp4][16 tokens] */
+    int *sxs = (int *)(dxs + nbp4 * 16);                    /* [nbp4][16 tokens] */
+    uint8_t *scl = (uint8_t *)(sxs + nbp4 * 16) + wave * 2 * NBK * 32;   /* [2][NBK][16 halves] */
+    float *relay = (float *)((uint8_t *)(sxs + nbp4 * 16) + W * 2 * NBK * 32) + rtl * 2 * 64;
+    /* issue order: the token rows, the weights (straight-line loads), then the
+     * LDS-direct loads that need the token rows */
+    const int arow = a.pair_tok[p0 + (lr < n ? lr : n - 1)];   /* column lr = token lr */
+    v4i w[2][NP][NV];
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        const int gp = g0 + k < npair ? g0 + k : npair - 1;
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            const QMat &m = mi ? mu : mg;
+            if (DT == 4) {
+                w[mi][k][0] = gload<v4i>(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
+            } else {
+                const uint8_t *base = m.w + ((size_t)rt * nbp + 2 * gp) * 1024 + lane * 16;
+                w[mi][k][0] = gload<v4i>(base);
+                w[mi][k][NV - 1] = gload<v4i>(base + 1024);
+            }
+        }
+    }
+    /* one loop for every LDS-direct load: the wait for the token rows is then the only
+     * wait before them, and the weights stay in flight */
+    {
+        const Act &x = a.x;
+        const int nxq = (nbp - wave + W - 1) / W, nit = nxq > NBK / 8 ? nxq : NBK / 8;
+        int it = 0;
+        do {   /* nit >= 1 */
+            const int b = wave + it * W;
+            if (b < nbp) lds_direct<16>(x.q + ((size_t)arow * x.nbp + b) * 64 + kg * 16, xs + (size_t)b * 1024);
+            if (4 * b < nbp4) {
+                const int bb = 4 * b + kg < nbp ? 4 * b + kg : nbp - 1;
+                lds_direct<4>(x.d + (size_t)arow * x.nbp + bb, dxs + 4 * b * 16);
+                if (DT == 4) lds_direct<4>(x.s + (size_t)arow * x.nbp + bb, sxs + 4 * b * 16);
+            }
+            const int b0 = it * 8;
+            if (b0 < NBK) {
+                const int bg = kb0 + b0 + (lane >> 3), bs = bg < nbp ? bg : nbp - 1, h2 = (lane & 7) * 2;
+                lds_direct<4>(mg.d + (size_t)bs * mg.rows_pad + rt * 16 + h2, scl + b0 * 32);
+                lds_direct<4>(mu.d + (size_t)bs * mu.rows_pad + rt * 16 + h2, scl + (NBK + b0) * 32);
+            }
+        } while (++it < nit);
+    }
+    HX_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    const int q = lr >> 2;                /* register of this lane's pair: row 4 kg + q */
+    const int col = 4 * g + (lr & 3);     /* token of this lane's pair */
+    const v4i zero = {0, 0, 0, 0};
+    const bool full = kb0 + NBK <= nb;    /* uniform */
+    /* terms of local block kb (global kb0 + kb) of both matrices; the MFMA gives
+     * sum q x with q the stored nibble (Q4), so isum = sum q x - 8 sx */
+    auto terms = [&](const v4i &wa_g, const v4i &wa_u, int kb, float (&t)[2]) {
+        const int blk = kb0 + kb;
+        const v4i xq = *(const v4i *)(xs + (size_t)blk * 1024 + (kg * 16 + col) * 16);
+        const float d = dxs[blk * 16 + col];
+        const int off = DT == 4 ? 8 * sxs[blk * 16 + col] : 0;
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(mi ? wa_u : wa_g, xq, zero, 0, 0, 0);
+            const float dw = h2f(*((const uint16_t *)(scl + (size_t)(mi * NBK + kb) * 32) + 4 * kg + q));
+            t[mi] = fmul((float)(pick4(cc, q) - off), fmul(dw, d));
+        }
+    };
+    float acc[2];
+    float tm[NBK][2];
+    auto run_part = [&](bool fold) {
+#pragma unroll
+        for (int k = 0; k < NP; k++) {
+            v4i wv[2][2];
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                if (DT == 4) {
+                    unpack_q4(w[mi][k][0], wv[mi][0], wv[mi][1]);
+                } else {
+                    wv[mi][0] = w[mi][k][0];
+                    wv[mi][1] = w[mi][k][NV - 1];
+                }
+            }
+#pragma unroll
+            for (int j2 = 0; j2 < 2; j2++) {
+                const int kb = 2 * k + j2;
+                if (!full && kb0 + kb >= nb) break;   /* uniform */
+                float t[2];
+                terms(wv[0][j2], wv[1][j2], kb, t);
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++) {
+                    if (fold) acc[mi] = fadd(acc[mi], t[mi]);
+                    else tm[kb][mi] = t[mi];
+                }
+            }
+        }
+    };
+    if (part == 0) {
+        acc[0] = acc[1] = 0.0f;
+        run_part(true);
+    } else {
+        run_part(false);
+    }
+    for (int stage = 1; stage < S; stage++) {
+        if (part == stage - 1) {
+            relay[lane] = acc[0];
+            relay[64 + lane] = acc[1];
+        }
+        __syncthreads();
+        if (part == stage) {
+            acc[0] = relay[lane];
+            acc[1] = relay[64 + lane];
+#pragma unroll
+            for (int kb = 0; kb < NBK; kb++) {
+                if (!full && kb0 + kb >= nb) break;   /* uniform */
+                acc[0] = fadd(acc[0], tm[kb][0]);
+                acc[1] = fadd(acc[1], tm[kb][1]);
+            }
+        }
+        __syncthreads();   /* the relay slot is read before the next stage writes it */
+    }
+    if (part == S - 1 && live && col < n) {
+        const float gv = canon(acc[0]), uv = canon(acc[1]);
+        const float sg = fdiv(gv, fadd(1.0f, exp_port_f(-gv)));
+        a.midf[(size_t)(p0 + col) * a.F + rt * 16 + 4 * kg + q] = fmul(sg, uv);
+    }
+}
+
 /* down projection of one 16-row D tile of one active expert for its n tokens. */
 template <int DT>
 __global__ __launch_bounds__(512) void k_expert_down_sk(MoeArgs a, int ntok) {
@@ -735,6 +914,21 @@ void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0
     /* ev0/ev1 (optional) are recorded by the dispatch itself: ev0 at the start of the
      * first launch, ev1 at the end of the last */
     const bool q4 = a.dtype_mask & (1 << 4), q8 = a.dtype_mask & (1 << 3);
+    /* at most 16 tokens per expert, one dtype: the split-K kernel (one term per lane) */
+    if (a.T <= 16 && (q4 != q8)) {
+        const int NP = q4 ? TkCfg<4>::NP : TkCfg<3>::NP, NBK = 2 * NP, npair = nbp / 2, nbp4 = (nbp + 3) & ~3;
+        const int S = (npair + NP - 1) / NP;
+        const int rpw = S < TK_WAVES ? TK_WAVES / S : 1, W = rpw * S;
+        const size_t tk_lds = (size_t)nbp * 1024 + (size_t)nbp4 * 128 + (size_t)W * 2 * NBK * 32 + (size_t)rpw * 2 * 64 * 4;
+        if (W <= 8 && tk_lds <= TK_LDS_MAX) {
+            const int tpw = (a.F / 16 + rpw - 1) / rpw;
+            const int gmax = ((a.T < 16 ? a.T : 16) + 3) / 4;   /* tokens per slot <= T */
+            const dim3 tg(n_slots * tpw * gmax), tb(64 * W);
+            if (q4) hipExtLaunchKernelGGL(k_expert_gateup_tk<4>, tg, tb, (uint32_t)tk_lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
+            else hipExtLaunchKernelGGL(k_expert_gateup_tk<3>, tg, tb, (uint32_t)tk_lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
+            return;
+        }
+    }
     /* few tokens, one dtype, one pair chunk per wave: the persistent kernel (two
      * workgroups per CU on every CU) */
     const int npair = nbp / 2, W = threads / 64;
