@@ -494,13 +494,15 @@ __global__ __launch_bounds__(256) void k_expert_gateup_pp(MoeArgs a, int ntok) {
     }
 }
 
-/* Gate/up for experts of at most 16 tokens, K split over S waves per row tile.
+/* Expert products for experts of at most 16 tokens, K split over S waves per row tile:
+ * gate and up with the SwiGLU epilogue (DOWN = false), or the down projection
+ * (DOWN = true).
  *
- * Workgroup = (token group g, active slot, rpw row tiles of 16 F rows); S waves per row
+ * Workgroup = (token group g, active slot, rpw row tiles of 16 rows); S waves per row
  * tile. Wave (row tile r, part p) streams block pairs [p TK_NP, (p + 1) TK_NP) of the
- * tile's gate and up matrices into registers, every load issued at once. The slot's
- * activations are staged once per workgroup in LDS by LDS-direct loads, in the MFMA
- * B-operand layout with column = token.
+ * tile's matrices into registers, every load issued at once. The slot's activations
+ * are staged once per workgroup in LDS by LDS-direct loads, in the MFMA B-operand
+ * layout with column = token.
  *
  * Tokens go in groups of four: for group g the B operand of column c is read from token
  * 4 g + c % 4, so the MFMA result holds each (row, token) pair four times and lane
@@ -511,7 +513,7 @@ __global__ __launch_bounds__(256) void k_expert_gateup_pp(MoeArgs a, int ntok) {
  * Sums: part 0 folds its blocks from 0.0; part p > 0 keeps its terms in registers,
  * takes the running sums of part p - 1 through LDS after barrier p and adds its terms
  * in block order, so each sum is the sequential fold acc = acc + isum (dw dx) over
- * blocks 0 .. nb-1. The last part writes SwiGLU(gate) * up. */
+ * blocks 0 .. nb-1. The last part writes the result. */
 template <int DT>
 struct TkCfg {
     static constexpr int NP = DT == 4 ? 8 : 4;   /* block pairs per wave (registers) */
@@ -524,18 +526,40 @@ __device__ __forceinline__ int pick4(const v4i &c, int q) {
     return (q & 2) ? hi : lo;
 }
 
-template <int DT>
-__global__ __launch_bounds__(512) void k_expert_gateup_tk(MoeArgs a, int rpw, int S, int gmax) {
+/* LDS bytes of one workgroup */
+__host__ __device__ inline size_t tk_lds_bytes(int nbp, int nm, int np, int rpw, int S) {
+    const int nbp4 = (nbp + 3) & ~3;
+    return (size_t)nbp * 1024 + (size_t)nbp4 * 128 + (size_t)rpw * S * nm * 2 * np * 32 + (size_t)rpw * nm * 64 * 4;
+}
+
+template <int DT, bool DOWN>
+__global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, int gmax) {
     extern __shared__ __attribute__((aligned(16))) uint8_t tk_lds[];
-    constexpr int NP = TkCfg<DT>::NP, NV = TkCfg<DT>::NV, NBK = 2 * NP;
-    const int ntile = a.F / 16, tpw = (ntile + rpw - 1) / rpw;
+    constexpr int NP = TkCfg<DT>::NP, NV = TkCfg<DT>::NV, NBK = 2 * NP, NM = DOWN ? 1 : 2;
+    const int rows_out = DOWN ? a.D : a.F;
+    const int ntile = (rows_out + 15) / 16, tpw = (ntile + rpw - 1) / rpw;
     const int g = (int)blockIdx.x % gmax, rest = (int)blockIdx.x / gmax;
     const int u = rest / tpw;
-    if (u >= *a.n_active) return;   /* uniform */
-    const SlotDesc &sd = a.desc[u];
-    const QMat mg = sd.w.gate, mu = sd.w.up;
-    const int n = sd.n, p0 = sd.p0;
-    if (mg.dtype != DT || 4 * g >= n) return;   /* uniform */
+    int n, p0;
+    QMat mat[NM];
+    if (DOWN && a.head_slots) {
+        n = a.T;
+        p0 = u * a.T;
+        mat[0] = a.table[u].down;
+    } else {
+        if (u >= *a.n_active) return;   /* uniform */
+        const SlotDesc &sd = a.desc[u];
+        n = sd.n;
+        p0 = sd.p0;
+        if (DOWN) {
+            mat[0] = sd.w.down;
+        } else {
+            mat[0] = sd.w.gate;
+            mat[NM - 1] = sd.w.up;
+        }
+    }
+    if (mat[0].dtype != DT || 4 * g >= n) return;   /* uniform */
+    const Act &x = DOWN ? a.mid : a.x;
     const int W = rpw * S;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int rtl = wave / S, part = wave % S;
@@ -543,23 +567,24 @@ __global__ __launch_bounds__(512) void k_expert_gateup_tk(MoeArgs a, int rpw, in
     const int rt0 = (rest % tpw) * rpw + rtl;
     const bool live = rt0 < ntile;   /* uniform per wave */
     const int rt = live ? rt0 : ntile - 1;   /* a dead wave loads a live tile and discards it */
-    const int nb = mg.nb, nbp = mg.nbp, npair = nbp >> 1, nbp4 = (nbp + 3) & ~3;
+    const int nb = mat[0].nb, nbp = mat[0].nbp, npair = nbp >> 1, nbp4 = (nbp + 3) & ~3;
     const int g0 = part * NP, kb0 = 2 * g0;   /* first pair / block of this part */
     uint8_t *xs = tk_lds;                                   /* [nbp][64 lanes][16 B] */
     float *dxs = (float *)(xs + (size_t)nbp * 1024);        /* [nbp4][16 tokens] */
     int *sxs = (int *)(dxs + nbp4 * 16);                    /* [nbp4][16 tokens] */
-    uint8_t *scl = (uint8_t *)(sxs + nbp4 * 16) + wave * 2 * NBK * 32;   /* [2][NBK][16 halves] */
-    float *relay = (float *)((uint8_t *)(sxs + nbp4 * 16) + W * 2 * NBK * 32) + rtl * 2 * 64;
+    uint8_t *scl = (uint8_t *)(sxs + nbp4 * 16) + wave * NM * NBK * 32;   /* [NM][NBK][16 halves] */
+    float *relay = (float *)((uint8_t *)(sxs + nbp4 * 16) + W * NM * NBK * 32) + rtl * NM * 64;
     /* issue order: the token rows, the weights (straight-line loads), then the
      * LDS-direct loads that need the token rows */
-    const int arow = a.pair_tok[p0 + (lr < n ? lr : n - 1)];   /* column lr = token lr */
-    v4i w[2][NP][NV];
+    const int tcol = lr < n ? lr : n - 1;   /* column lr = token lr */
+    const int arow = DOWN ? p0 + tcol : a.pair_tok[p0 + tcol];
+    v4i w[NM][NP][NV];
 #pragma unroll
     for (int k = 0; k < NP; k++) {
         const int gp = g0 + k < npair ? g0 + k : npair - 1;
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            const QMat &m = mi ? mu : mg;
+        for (int mi = 0; mi < NM; mi++) {
+            const QMat &m = mat[mi];
             if (DT == 4) {
                 w[mi][k][0] = gload<v4i>(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
             } else {
@@ -572,7 +597,6 @@ __global__ __launch_bounds__(512) void k_expert_gateup_tk(MoeArgs a, int rpw, in
     /* one loop for every LDS-direct load: the wait for the token rows is then the only
      * wait before them, and the weights stay in flight */
     {
-        const Act &x = a.x;
         const int nxq = (nbp - wave + W - 1) / W, nit = nxq > NBK / 8 ? nxq : NBK / 8;
         int it = 0;
         do {   /* nit >= 1 */
@@ -586,8 +610,9 @@ __global__ __launch_bounds__(512) void k_expert_gateup_tk(MoeArgs a, int rpw, in
             const int b0 = it * 8;
             if (b0 < NBK) {
                 const int bg = kb0 + b0 + (lane >> 3), bs = bg < nbp ? bg : nbp - 1, h2 = (lane & 7) * 2;
-                lds_direct<4>(mg.d + (size_t)bs * mg.rows_pad + rt * 16 + h2, scl + b0 * 32);
-                lds_direct<4>(mu.d + (size_t)bs * mu.rows_pad + rt * 16 + h2, scl + (NBK + b0) * 32);
+#pragma unroll
+                for (int mi = 0; mi < NM; mi++)
+                    lds_direct<4>(mat[mi].d + (size_t)bs * mat[mi].rows_pad + rt * 16 + h2, scl + (mi * NBK + b0) * 32);
             }
         } while (++it < nit);
     }
@@ -597,43 +622,43 @@ __global__ __launch_bounds__(512) void k_expert_gateup_tk(MoeArgs a, int rpw, in
     const int col = 4 * g + (lr & 3);     /* token of this lane's pair */
     const v4i zero = {0, 0, 0, 0};
     const bool full = kb0 + NBK <= nb;    /* uniform */
-    /* terms of local block kb (global kb0 + kb) of both matrices; the MFMA gives
-     * sum q x with q the stored nibble (Q4), so isum = sum q x - 8 sx */
-    auto terms = [&](const v4i &wa_g, const v4i &wa_u, int kb, float (&t)[2]) {
+    /* terms of local block kb (global kb0 + kb); the MFMA gives sum q x with q the
+     * stored nibble (Q4), so isum = sum q x - 8 sx */
+    auto terms = [&](const v4i (&wa)[NM], int kb, float (&t)[NM]) {
         const int blk = kb0 + kb;
         const v4i xq = *(const v4i *)(xs + (size_t)blk * 1024 + (kg * 16 + col) * 16);
         const float d = dxs[blk * 16 + col];
         const int off = DT == 4 ? 8 * sxs[blk * 16 + col] : 0;
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(mi ? wa_u : wa_g, xq, zero, 0, 0, 0);
+        for (int mi = 0; mi < NM; mi++) {
+            const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[mi], xq, zero, 0, 0, 0);
             const float dw = h2f(*((const uint16_t *)(scl + (size_t)(mi * NBK + kb) * 32) + 4 * kg + q));
             t[mi] = fmul((float)(pick4(cc, q) - off), fmul(dw, d));
         }
     };
-    float acc[2];
-    float tm[NBK][2];
+    float acc[NM];
+    float tm[NBK][NM];
     auto run_part = [&](bool fold) {
 #pragma unroll
         for (int k = 0; k < NP; k++) {
-            v4i wv[2][2];
+            v4i wv[2][NM];
 #pragma unroll
-            for (int mi = 0; mi < 2; mi++) {
+            for (int mi = 0; mi < NM; mi++) {
                 if (DT == 4) {
-                    unpack_q4(w[mi][k][0], wv[mi][0], wv[mi][1]);
+                    unpack_q4(w[mi][k][0], wv[0][mi], wv[1][mi]);
                 } else {
-                    wv[mi][0] = w[mi][k][0];
-                    wv[mi][1] = w[mi][k][NV - 1];
+                    wv[0][mi] = w[mi][k][0];
+                    wv[1][mi] = w[mi][k][NV - 1];
                 }
             }
 #pragma unroll
             for (int j2 = 0; j2 < 2; j2++) {
                 const int kb = 2 * k + j2;
                 if (!full && kb0 + kb >= nb) break;   /* uniform */
-                float t[2];
-                terms(wv[0][j2], wv[1][j2], kb, t);
+                float t[NM];
+                terms(wv[j2], kb, t);
 #pragma unroll
-                for (int mi = 0; mi < 2; mi++) {
+                for (int mi = 0; mi < NM; mi++) {
                     if (fold) acc[mi] = fadd(acc[mi], t[mi]);
                     else tm[kb][mi] = t[mi];
                 }
@@ -641,34 +666,61 @@ __global__ __launch_bounds__(512) void k_expert_gateup_tk(MoeArgs a, int rpw, in
         }
     };
     if (part == 0) {
-        acc[0] = acc[1] = 0.0f;
+#pragma unroll
+        for (int mi = 0; mi < NM; mi++) acc[mi] = 0.0f;
         run_part(true);
     } else {
         run_part(false);
     }
     for (int stage = 1; stage < S; stage++) {
         if (part == stage - 1) {
-            relay[lane] = acc[0];
-            relay[64 + lane] = acc[1];
+#pragma unroll
+            for (int mi = 0; mi < NM; mi++) relay[mi * 64 + lane] = acc[mi];
         }
         __syncthreads();
         if (part == stage) {
-            acc[0] = relay[lane];
-            acc[1] = relay[64 + lane];
+#pragma unroll
+            for (int mi = 0; mi < NM; mi++) acc[mi] = relay[mi * 64 + lane];
 #pragma unroll
             for (int kb = 0; kb < NBK; kb++) {
                 if (!full && kb0 + kb >= nb) break;   /* uniform */
-                acc[0] = fadd(acc[0], tm[kb][0]);
-                acc[1] = fadd(acc[1], tm[kb][1]);
+#pragma unroll
+                for (int mi = 0; mi < NM; mi++) acc[mi] = fadd(acc[mi], tm[kb][mi]);
             }
         }
         __syncthreads();   /* the relay slot is read before the next stage writes it */
     }
-    if (part == S - 1 && live && col < n) {
-        const float gv = canon(acc[0]), uv = canon(acc[1]);
+    if (part != S - 1 || !live || col >= n) return;
+    const int row = rt * 16 + 4 * kg + q;
+    if (DOWN) {
+        if (row < mat[0].rows) a.Y[(size_t)(p0 + col) * a.D + row] = canon(acc[0]);
+    } else {
+        const float gv = canon(acc[0]), uv = canon(acc[NM - 1]);
         const float sg = fdiv(gv, fadd(1.0f, exp_port_f(-gv)));
-        a.midf[(size_t)(p0 + col) * a.F + rt * 16 + 4 * kg + q] = fmul(sg, uv);
+        a.midf[(size_t)(p0 + col) * a.F + row] = fmul(sg, uv);
     }
+}
+
+/* launches k_expert_tk for experts of at most 16 tokens and one dtype; false when the
+ * shape does not fit (the caller uses the general kernels) */
+bool launch_tk(const MoeArgs &a, bool down, int n_slots, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    const bool q4 = a.dtype_mask & (1 << 4), q8 = a.dtype_mask & (1 << 3);
+    if (a.T > 16 || q4 == q8) return false;
+    const int K = down ? a.F : a.D, rows = down ? a.D : a.F;
+    const int nb = (K + 63) / 64, nbp = (nb + 1) & ~1, npair = nbp / 2;
+    const int NP = q4 ? TkCfg<4>::NP : TkCfg<3>::NP, NM = down ? 1 : 2;
+    const int S = (npair + NP - 1) / NP;
+    const int rpw = S < TK_WAVES ? TK_WAVES / S : 1, W = rpw * S;
+    const size_t lds = tk_lds_bytes(nbp, NM, NP, rpw, S);
+    if (W > 8 || lds > TK_LDS_MAX) return false;
+    const int tpw = ((rows + 15) / 16 + rpw - 1) / rpw;
+    const int gmax = (a.T + 3) / 4;   /* tokens per slot <= T */
+    const dim3 grid(n_slots * tpw * gmax), block(64 * W);
+    if (q4 && !down) hipExtLaunchKernelGGL(k_expert_tk<4, false>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
+    if (q4 && down) hipExtLaunchKernelGGL(k_expert_tk<4, true>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
+    if (q8 && !down) hipExtLaunchKernelGGL(k_expert_tk<3, false>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
+    if (q8 && down) hipExtLaunchKernelGGL(k_expert_tk<3, true>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
+    return true;
 }
 
 /* down projection of one 16-row D tile of one active expert for its n tokens. */
@@ -915,20 +967,7 @@ void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0
      * first launch, ev1 at the end of the last */
     const bool q4 = a.dtype_mask & (1 << 4), q8 = a.dtype_mask & (1 << 3);
     /* at most 16 tokens per expert, one dtype: the split-K kernel (one term per lane) */
-    if (a.T <= 16 && (q4 != q8)) {
-        const int NP = q4 ? TkCfg<4>::NP : TkCfg<3>::NP, NBK = 2 * NP, npair = nbp / 2, nbp4 = (nbp + 3) & ~3;
-        const int S = (npair + NP - 1) / NP;
-        const int rpw = S < TK_WAVES ? TK_WAVES / S : 1, W = rpw * S;
-        const size_t tk_lds = (size_t)nbp * 1024 + (size_t)nbp4 * 128 + (size_t)W * 2 * NBK * 32 + (size_t)rpw * 2 * 64 * 4;
-        if (W <= 8 && tk_lds <= TK_LDS_MAX) {
-            const int tpw = (a.F / 16 + rpw - 1) / rpw;
-            const int gmax = ((a.T < 16 ? a.T : 16) + 3) / 4;   /* tokens per slot <= T */
-            const dim3 tg(n_slots * tpw * gmax), tb(64 * W);
-            if (q4) hipExtLaunchKernelGGL(k_expert_gateup_tk<4>, tg, tb, (uint32_t)tk_lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
-            else hipExtLaunchKernelGGL(k_expert_gateup_tk<3>, tg, tb, (uint32_t)tk_lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
-            return;
-        }
-    }
+    if (launch_tk(a, false, n_slots, st, ev0, ev1)) return;
     /* few tokens, one dtype, one pair chunk per wave: the persistent kernel (two
      * workgroups per CU on every CU) */
     const int npair = nbp / 2, W = threads / 64;
@@ -954,6 +993,7 @@ void expert_down(const MoeArgs &a, int n_slots, hipStream_t st) {
 
 void expert_down_q(const MoeArgs &a, int n_slots, hipStream_t st) {
     if (n_slots <= 0) return;
+    if (launch_tk(a, true, n_slots, st, nullptr, nullptr)) return;
     const int nb = (a.F + 63) / 64, nbp = (nb + 1) & ~1;
     const int ntok = sk_ntok(a.T, 1, nb);
     const int threads = 64 * sk_waves(nbp / 2);
