@@ -16,7 +16,7 @@ acceptance on the GPU, commit; generate.py:365-392 of the reference):
 value = accepted tokens / s = sum over steps of (accepted drafts + 1) / wall time of the
 steps (inputs already resident in HBM; each step returns its result to the host).
 
-roofline: the grouped Q4 expert gate/up kernel (k_expert_gateup_sk), timed with HIP
+roofline: the grouped Q4 expert gate/up kernel (k_expert_tk<4, false>), timed with HIP
 event pairs recorded on the engine's stream around each of its launches during the
 timed steps; achieved = its algorithmic bytes (distinct experts routed in the layer x
 1,671,168 B of Q4 gate+up rows each) / its summed launch durations. A second pass over
@@ -48,7 +48,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-TRAFFIC_PROFILE = ROOT / "profiles" / "k_expert_gateup_sk_verify_k8_ctx4096_traffic.md"
+TRAFFIC_PROFILE = ROOT / "profiles" / "k_expert_tk_gateup_verify_k8_ctx4096_traffic.md"
 
 
 def measured_traffic():
@@ -307,7 +307,7 @@ def main(argv=None) -> int:
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "traffic_source": str(TRAFFIC_PROFILE.relative_to(ROOT)),
-                     "kernel": "k_expert_gateup_sk<4> (grouped Q4 expert gate+up)",
+                     "kernel": "k_expert_tk<4, false> (grouped Q4 expert gate+up)",
                      "bytes_per_launch": int(kx["expert_bytes"] / n_launch),
                      "us_per_launch": round(kx["expert_s"] / n_launch * 1e6, 3),
                      "down_projection_gbs": round(dn_gbs, 1)},

@@ -176,6 +176,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs args) {
 constexpr int SK_MAXP = 4;      /* block pairs per wave */
 constexpr int TK_WAVES = 4;     /* waves per workgroup of the split-K gate/up kernel */
 constexpr size_t TK_LDS_MAX = 65536;
+constexpr int TK_CHUNK_ROWS = 128;   /* rows of a slot kept on one XCD (two 128-byte scale lines) */
 constexpr int SK_LDS = 65536;   /* bytes of terms per workgroup */
 constexpr int SK_DUMMY = 1024;  /* LDS after the terms: stores of padding token columns */
 
@@ -526,6 +527,13 @@ __device__ __forceinline__ int pick4(const v4i &c, int q) {
     return (q & 2) ? hi : lo;
 }
 
+/* tile sets per XCD chunk: a workgroup of fewer than 64 rows shares the 128-byte scale
+ * lines with its neighbours, so TK_CHUNK_ROWS rows stay on one XCD; from 64 rows on the
+ * workgroups go round the XCDs one by one */
+__host__ __device__ inline int tk_chunk(int rpw) {
+    return 16 * rpw >= 64 ? 1 : TK_CHUNK_ROWS / (16 * rpw);
+}
+
 /* LDS bytes of one workgroup */
 __host__ __device__ inline size_t tk_lds_bytes(int nbp, int nm, int np, int rpw, int S) {
     const int nbp4 = (nbp + 3) & ~3;
@@ -533,13 +541,21 @@ __host__ __device__ inline size_t tk_lds_bytes(int nbp, int nm, int np, int rpw,
 }
 
 template <int DT, bool DOWN>
-__global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, int gmax) {
+__global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, int gmax, int n_slots) {
     extern __shared__ __attribute__((aligned(16))) uint8_t tk_lds[];
     constexpr int NP = TkCfg<DT>::NP, NV = TkCfg<DT>::NV, NBK = 2 * NP, NM = DOWN ? 1 : 2;
     const int rows_out = DOWN ? a.D : a.F;
     const int ntile = (rows_out + 15) / 16, tpw = (ntile + rpw - 1) / rpw;
-    const int g = (int)blockIdx.x % gmax, rest = (int)blockIdx.x / gmax;
-    const int u = rest / tpw;
+    /* workgroup i runs on XCD i % 8. Chunks of TK_CHUNK_ROWS rows of one slot are dealt
+     * to the XCDs in turn and a chunk's workgroups follow each other on its XCD, so the
+     * row tiles that share 128-byte lines of the scale rows meet in one L2 while every
+     * XCD gets the same share of the bytes */
+    const int ch = tk_chunk(rpw);   /* tile sets per chunk */
+    const int cps = (tpw + ch - 1) / ch, per_chunk = ch * gmax;
+    const int xcd = (int)blockIdx.x & 7, k = (int)blockIdx.x >> 3;
+    const int c = xcd + 8 * (k / per_chunk), within = k % per_chunk;
+    const int u = c / cps, tile = (c % cps) * ch + within / gmax, g = within % gmax;
+    if (u >= n_slots || tile >= tpw) return;   /* uniform */
     int n, p0;
     QMat mat[NM];
     if (DOWN && a.head_slots) {
@@ -564,7 +580,7 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int rtl = wave / S, part = wave % S;
     const int lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
-    const int rt0 = (rest % tpw) * rpw + rtl;
+    const int rt0 = tile * rpw + rtl;
     const bool live = rt0 < ntile;   /* uniform per wave */
     const int rt = live ? rt0 : ntile - 1;   /* a dead wave loads a live tile and discards it */
     const int nb = mat[0].nb, nbp = mat[0].nbp, npair = nbp >> 1, nbp4 = (nbp + 3) & ~3;
@@ -715,11 +731,13 @@ bool launch_tk(const MoeArgs &a, bool down, int n_slots, hipStream_t st, hipEven
     if (W > 8 || lds > TK_LDS_MAX) return false;
     const int tpw = ((rows + 15) / 16 + rpw - 1) / rpw;
     const int gmax = (a.T + 3) / 4;   /* tokens per slot <= T */
-    const dim3 grid(n_slots * tpw * gmax), block(64 * W);
-    if (q4 && !down) hipExtLaunchKernelGGL(k_expert_tk<4, false>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
-    if (q4 && down) hipExtLaunchKernelGGL(k_expert_tk<4, true>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
-    if (q8 && !down) hipExtLaunchKernelGGL(k_expert_tk<3, false>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
-    if (q8 && down) hipExtLaunchKernelGGL(k_expert_tk<3, true>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax);
+    const int ch = tk_chunk(rpw);
+    const int chunks = n_slots * ((tpw + ch - 1) / ch);
+    const dim3 grid(8 * ((chunks + 7) / 8) * ch * gmax), block(64 * W);
+    if (q4 && !down) hipExtLaunchKernelGGL(k_expert_tk<4, false>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots);
+    if (q4 && down) hipExtLaunchKernelGGL(k_expert_tk<4, true>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots);
+    if (q8 && !down) hipExtLaunchKernelGGL(k_expert_tk<3, false>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots);
+    if (q8 && down) hipExtLaunchKernelGGL(k_expert_tk<3, true>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots);
     return true;
 }
 
