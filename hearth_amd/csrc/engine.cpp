@@ -102,6 +102,7 @@ struct Layer {
     const float *sh_gate_inp = nullptr; /* F32 [D]: shared output scaled by sigmoid(dot16(., x)) */
     const float *router = nullptr;  /* F32 [E][D] */
     const float *router_bias = nullptr;
+    const float *router_bias_host = nullptr;   /* the same in the mapped container (prediction) */
     ExpertW *experts = nullptr;     /* device table [E] */
     uint64_t expert_bytes_each = 0; /* algorithmic bytes of one expert (gate+up+down) */
     uint64_t expert_gateup_bytes = 0; /* of which gate + up */
@@ -179,6 +180,17 @@ struct hearth_engine {
     std::unique_ptr<GpuExpertStore> store;
     int *h_meta = nullptr;   /* pinned [1 + E]: n_active, active experts of a layer */
     StoreStats store_base;   /* store counters at hearth_reset_stats */
+    /* next-layer prediction (model.c:935-984): router of the next MoE layer on the
+     * predicted input, top_k + prefetch_extra per token, union over the batch */
+    float *pxs = nullptr, *plog = nullptr, *h_plog = nullptr;   /* [B][D], [B][E], pinned [B][E] */
+    Act apx{};
+    double pf_prec = 1.0;            /* recent precision (EWMA) */
+    int pred_layer = -1;
+    std::vector<int> pred_list;
+    std::vector<uint8_t> pf_mark;
+    void predict_select(const float *logits, const float *bias, int kk, int *out) const;
+    void prefetch_next(int nl, int T);
+    void score_prediction(int l, const int *ulist, int nu);
     /* HEARTH_DEBUG_DUMP=<dir>: every forward writes named intermediate buffers there
      * (T rows each, appended per call) for layer-by-layer comparisons */
     std::string dump_dir;
@@ -221,6 +233,7 @@ struct hearth_engine {
         if (h_rope) (void)hipHostFree(h_rope);
         if (h_res) (void)hipHostFree(h_res);
         if (h_meta) (void)hipHostFree(h_meta);
+        if (h_plog) (void)hipHostFree(h_plog);
         store.reset();
         if (st) (void)hipStreamDestroy(st);
         if (trace) fclose(trace);
@@ -444,7 +457,10 @@ bool hearth_engine::upload(std::string &msg) {
             continue;
         }
         w.router = vec(l, "moe_router");
-        if (c.score_bias) w.router_bias = vec(l, "moe_router_bias");
+        if (c.score_bias) {
+            w.router_bias = vec(l, "moe_router_bias");
+            if (const Tensor *tb = mf.layer_tensor(l, "moe_router_bias")) w.router_bias_host = (const float *)mf.data(tb->offset);
+        }
         if (c.shared_ffn > 0) {
             if (!mat(l, "shexp_gate", w.sh_gate) || !mat(l, "shexp_up", w.sh_up) || !mat(l, "shexp_down", w.sh_down))
                 return false;
@@ -636,6 +652,13 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
             shb = dnew<float>(Bs * D);
             shg = dnew<float>(Bs);
         }
+        if (store && opt.prefetch != HEARTH_PREFETCH_OFF) {
+            pxs = dnew<float>(Bs * D);
+            plog = dnew<float>(Bs * E);
+            apx = make_act(B, D);
+            ck(hipHostMalloc((void **)&h_plog, sizeof(float) * Bs * E, hipHostMallocDefault));
+            pf_mark.assign(E, 0);
+        }
         ck(hipHostMalloc((void **)&h_geom, sizeof(int) * (2 * Bs + Bs * Bs), hipHostMallocDefault));
         ck(hipHostMalloc((void **)&h_rope, sizeof(float) * Bs * std::max(rope_dim, 2), hipHostMallocDefault));
         ck(hipHostMalloc((void **)&h_res, sizeof(int) * (2 * Bs + 8), hipHostMallocDefault));
@@ -784,6 +807,29 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
         const float *next_norm = l + 1 < L ? layers[l + 1].attn_norm : out_norm;
         if (w.moe) {
             int *n_active = route_meta, *ulist = route_meta + 1, *u_p0 = ulist + E, *u_n = u_p0 + E;
+            /* next-layer prediction (model.c:989-991, 1049-1063): 1 = on h, 2 = on h plus
+             * the shared expert's output (shared mode with a shared expert) */
+            const int nl = l + 1 < L && layers[l + 1].moe ? l + 1 : -1;
+            const int pf = !pxs || nl < 0 ? 0 : opt.prefetch == HEARTH_PREFETCH_SHARED && Fs ? 2 : 1;
+            auto shared_expert = [&] {   /* reference model.c:925-934: SwiGLU FFN of x, optional sigmoid gate */
+                timed(&ks.dense_s, [&] {
+                    matmul(w.sh_gate, ax, x, D, T, sf1, Fs, false, 1.0f);
+                    matmul(w.sh_up, ax, x, D, T, sf2, Fs, false, 1.0f);
+                    hxl::swiglu_quant(sf1, sf2, T, Fs, asf, st);
+                    matmul(w.sh_down, asf, sf1, Fs, T, shb, D, false, 1.0f);
+                    if (w.sh_gate_inp) hxl::fgemv(0, w.sh_gate_inp, 1, D, x, D, T, shg, 1, st);
+                });
+            };
+            if (pf == 2) shared_expert();
+            if (pf) {   /* predicted input rmsnorm(h (+ rs * shared), ffn_norm of nl); h unchanged */
+                hxd::NormArgs n{};
+                n.mode = 4; n.h = h; n.rs = rs; n.add = pf == 2 ? shb : nullptr;
+                n.add_gate = pf == 2 && w.sh_gate_inp ? shg : nullptr;
+                n.norm_w = layers[nl].ffn_norm; n.eps = c.eps; n.x = pxs; n.a = apx; n.T = T; n.D = D;
+                hxl::norm(n, st);
+                hxl::fgemv(0, layers[nl].router, E, D, pxs, D, T, plog, E, st);
+                ck(hipMemcpyAsync(h_plog, plog, sizeof(float) * (size_t)T * E, hipMemcpyDeviceToHost, st));
+            }
             timed(&ks.router_s, [&] {
                 hxl::fgemv(0, w.router, E, D, x, D, T, lge, E, st);
                 hxd::RouteArgs r{};
@@ -798,6 +844,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             if (store) {
                 ck(hipMemcpyAsync(h_meta, route_meta, sizeof(int) * (size_t)(1 + E), hipMemcpyDeviceToHost, st));
                 ck(hipStreamSynchronize(st));
+                score_prediction(l, h_meta + 1, h_meta[0]);
                 store->ensure(l, h_meta + 1, h_meta[0], w.experts, st);
                 hxl::desc_refresh(slot_desc, w.experts, route_meta + 1, route_meta, std::min(E, T * K), st);
             }
@@ -813,14 +860,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 timed(&ks.expert_down_s, [&] { hxl::expert_down(m, slots, st); }, 1);
             }
             if (profiling) ks.expert_launches++;
-            if (Fs)   /* shared expert (reference model.c:925-934): SwiGLU FFN of x, optional sigmoid gate */
-                timed(&ks.dense_s, [&] {
-                    matmul(w.sh_gate, ax, x, D, T, sf1, Fs, false, 1.0f);
-                    matmul(w.sh_up, ax, x, D, T, sf2, Fs, false, 1.0f);
-                    hxl::swiglu_quant(sf1, sf2, T, Fs, asf, st);
-                    matmul(w.sh_down, asf, sf1, Fs, T, shb, D, false, 1.0f);
-                    if (w.sh_gate_inp) hxl::fgemv(0, w.sh_gate_inp, 1, D, x, D, T, shg, 1, st);
-                });
+            if (Fs && pf != 2) shared_expert();
             timed(&ks.norm_s, [&] {
                 hxd::NormArgs n{};
                 n.mode = 2; n.h = h; n.Y = Y; n.wts = wts; n.pair_of = pair_of; n.K = K; n.rs = rs;
@@ -828,6 +868,8 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 n.norm_w = next_norm; n.eps = c.eps; n.x = x; n.a = ax; n.T = T; n.D = D;
                 hxl::norm(n, st);
             });
+            /* the layer's work is queued: the prediction's loads overlap it */
+            if (pf) prefetch_next(nl, T);
             dump("h", l, h, T, D);
         } else {
             timed(&ks.dense_s, [&] {
@@ -847,6 +889,90 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
     if (want_logits)
         timed(&ks.head_s, [&] { matmul(lm_head, ax, x, D, T, logits, V, true, c.logit_scale); });
     if (store) store->tick();
+}
+
+/* route_select (model.c:793-830) for the prediction: score = softmax or sigmoid of the
+ * logits, sel = score (+ bias), group limit, then the kk best by sel (larger first, NaN
+ * last, ties to the lower index). Host arithmetic: it only picks experts to load. */
+void hearth_engine::predict_select(const float *lg, const float *bias, int kk, int *out) const {
+    std::vector<float> score(lg, lg + E), sel(E);
+    if (c.score_fn == 0) {
+        float m = score[0];
+        for (int e = 1; e < E; e++) m = score[e] > m ? score[e] : m;
+        float sum = 0.0f;
+        for (int e = 0; e < E; e++) sum += (score[e] = std::exp(score[e] - m));
+        for (int e = 0; e < E; e++) score[e] /= sum;
+    } else {
+        for (int e = 0; e < E; e++) score[e] = 1.0f / (1.0f + std::exp(-score[e]));
+    }
+    for (int e = 0; e < E; e++) sel[e] = bias ? score[e] + bias[e] : score[e];
+    auto before = [](float va, int ia, float vb, int ib) {
+        const bool na = va != va, nb = vb != vb;
+        if (na || nb) return na == nb ? ia < ib : nb;
+        if (va != vb) return va > vb;
+        return ia < ib;
+    };
+    if (c.n_group > 1) {
+        const int ng = c.n_group, gs = E / ng;
+        std::vector<float> gsc(ng);
+        std::vector<uint8_t> keep(ng, 0);
+        for (int g = 0; g < ng; g++) {
+            const float *v = sel.data() + (size_t)g * gs;
+            int i1 = 0, i2 = -1;
+            for (int i = 1; i < gs; i++) {
+                if (before(v[i], i, v[i1], i1)) { i2 = i1; i1 = i; }
+                else if (i2 < 0 || before(v[i], i, v[i2], i2)) i2 = i;
+            }
+            gsc[g] = i2 >= 0 ? v[i1] + v[i2] : v[i1];
+        }
+        for (int r = 0; r < c.topk_group; r++) {
+            int best = -1;
+            for (int g = 0; g < ng; g++)
+                if (!keep[g] && (best < 0 || before(gsc[g], g, gsc[best], best))) best = g;
+            keep[best] = 1;
+        }
+        for (int g = 0; g < ng; g++)
+            if (!keep[g]) std::fill(sel.begin() + (size_t)g * gs, sel.begin() + (size_t)(g + 1) * gs, 0.0f);
+    }
+    std::vector<uint8_t> taken(E, 0);
+    for (int j = 0; j < kk; j++) {
+        int best = -1;
+        for (int e = 0; e < E; e++)
+            if (!taken[e] && (best < 0 || before(sel[e], e, sel[best], best))) best = e;
+        out[j] = best;
+        taken[best] = 1;
+    }
+}
+
+/* prefetch_next (model.c:944-973): the prediction for layer nl is always made and
+ * scored when nl routes; it goes to the store only while the recent precision is at
+ * least 0.5 * top_k / (top_k + prefetch_extra). */
+void hearth_engine::prefetch_next(int nl, int T) {
+    const int kk = std::min(K + opt.prefetch_extra, E);
+    for (int e : pred_list) pf_mark[e] = 0;
+    pred_list.clear();
+    std::vector<int> sel(kk);
+    for (int t = 0; t < T; t++) {
+        predict_select(h_plog + (size_t)t * E, layers[nl].router_bias_host, kk, sel.data());
+        for (int j = 0; j < kk; j++)
+            if (!pf_mark[sel[j]]) {
+                pf_mark[sel[j]] = 1;
+                pred_list.push_back(sel[j]);
+            }
+    }
+    pred_layer = nl;
+    if (pf_prec >= 0.5 * (double)K / (double)kk) store->prefetch(nl, pred_list.data(), (int)pred_list.size());
+}
+
+/* score_prediction (model.c:976-984): precision = predicted experts used / predicted */
+void hearth_engine::score_prediction(int l, const int *ulist, int nu) {
+    if (pred_layer != l || pred_list.empty()) return;
+    int hit = 0;
+    for (int u = 0; u < nu; u++) hit += pf_mark[ulist[u]];
+    pf_prec += 0.05 * ((double)hit / (double)pred_list.size() - pf_prec);
+    for (int e : pred_list) pf_mark[e] = 0;
+    pred_list.clear();
+    pred_layer = -1;
 }
 
 /* Uploads tokens and geometry for n tokens at pos (parent NULL: chain) and runs the
@@ -1115,6 +1241,9 @@ HEARTH_API int hearth_get_stats(hearth_engine *e, hearth_stats *out) {
     out->expert_loads_unique = d[1] - e->stats_base[1];
     if (e->store) {
         const StoreStats &ss = e->store->stats;
+        out->prefetch_issued = ss.prefetch_issued - e->store_base.prefetch_issued;
+        out->prefetch_used = ss.prefetch_used - e->store_base.prefetch_used;
+        out->prefetch_wasted = ss.prefetch_wasted - e->store_base.prefetch_wasted;
         out->cache_hits = ss.hits - e->store_base.hits;
         out->cache_misses = ss.misses - e->store_base.misses;
         out->evictions = ss.evictions - e->store_base.evictions;

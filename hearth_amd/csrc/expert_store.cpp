@@ -13,6 +13,7 @@ namespace {
 
 constexpr uint64_t ALIGN = 256;
 constexpr double HEAT_DECAY = 0.995;   /* per forward (reference default heat_decay, hx_store.h) */
+constexpr double HOT_HEAT = 0.5 / (1.0 - HEAT_DECAY);   /* LFU: used in about half of all forwards */
 
 uint64_t al(uint64_t x) { return (x + ALIGN - 1) / ALIGN * ALIGN; }
 
@@ -109,21 +110,36 @@ bool GpuExpertStore::open(const ModelFile &mf, int L, int E, int D, int F, int n
 
 int GpuExpertStore::resident() const { return n_slots_ - (int)free_.size(); }
 
-/* LRU: least recently used; LFU: lowest decayed heat, then least recently used
- * (store.c:166-199). Slots serving the current layer are excluded. */
-int GpuExpertStore::victim() {
-    int best = -1;
-    for (int s = 0; s < n_slots_; s++) {
-        if (busy_[s]) continue;
-        if (best < 0) { best = s; continue; }
-        const Slot &x = slot_[s], &y = slot_[best];
-        if (policy_ == HEARTH_POLICY_LFU) {
-            const double hx_ = heat_[x.key], hy = heat_[y.key];
-            if (hx_ != hy) { if (hx_ < hy) best = s; continue; }
-        }
-        if (x.last_seq < y.last_seq) best = s;
+/* a is the better victim than b (store.c:166-177): unprotected first; LFU: lower
+ * decayed heat; then least recently used; then the lower slot */
+bool GpuExpertStore::cheaper(int a, int b) const {
+    const Slot &x = slot_[a], &y = slot_[b];
+    const bool px = protected_(x), py = protected_(y);
+    if (px != py) return !px;
+    if (policy_ == HEARTH_POLICY_LFU) {
+        const double hx_ = heat_[x.key], hy = heat_[y.key];
+        if (hx_ != hy) return hx_ < hy;
     }
+    if (x.last_seq != y.last_seq) return x.last_seq < y.last_seq;
+    return a < b;
+}
+
+/* Victim among the slots not serving the current layer (store.c:179-199): the
+ * cheapest; -1 if none, or if only protected ones remain and allow_protected is 0. */
+int GpuExpertStore::victim(bool allow_protected) {
+    int best = -1;
+    for (int s = 0; s < n_slots_; s++)
+        if (!busy_[s] && (best < 0 || cheaper(s, best))) best = s;
+    if (best >= 0 && !allow_protected && protected_(slot_[best])) return -1;
     return best;
+}
+
+void GpuExpertStore::evict(int s) {
+    Slot &x = slot_[s];
+    slot_of_[x.key] = -1;
+    stats.evictions++;
+    if (x.pf_unused) stats.prefetch_wasted++;
+    x.pf_unused = false;
 }
 
 void GpuExpertStore::load(int key, int s) {
@@ -161,21 +177,26 @@ void GpuExpertStore::ensure(int layer, const int *experts, int n, hxd::ExpertW *
         int s = slot_of_[key];
         if (s >= 0) {
             stats.hits++;
+            if (slot_[s].pf_unused) {
+                slot_[s].pf_unused = false;
+                stats.prefetch_used++;
+            }
         } else {
             stats.misses++;
             if (!free_.empty()) {
                 s = free_.back();
                 free_.pop_back();
             } else {
-                s = victim();
-                slot_of_[slot_[s].key] = -1;
-                stats.evictions++;
+                s = victim(true);
+                evict(s);
             }
             slot_[s].key = key;
             slot_of_[key] = s;
             busy_[s] = 1;
             load(key, s);
         }
+        slot_[s].prot_tick = 0;
+        slot_[s].last_tick = now_;
         slot_[s].last_seq = ++seq_;
         heat_[key] += 1.0;
         htable_[e] = slot_[s].w;
@@ -186,7 +207,44 @@ void GpuExpertStore::ensure(int layer, const int *experts, int n, hxd::ExpertW *
     stats.load_s += now_s() - t0;
 }
 
+void GpuExpertStore::prefetch(int layer, const int *experts, int n) {
+    const double t0 = now_s();
+    for (int j = 0; j < n; j++) {
+        const int key = layer * E_ + experts[j];
+        const int r = slot_of_[key];
+        if (r >= 0) {   /* resident: keep it for the coming demand */
+            slot_[r].prot_tick = now_ + 1;
+            continue;
+        }
+        int s;
+        if (!free_.empty()) {
+            s = free_.back();
+            free_.pop_back();
+        } else {
+            s = victim(false);
+            if (s >= 0) {   /* never a hot expert (store.c:207-214) */
+                const Slot &v = slot_[s];
+                if (policy_ == HEARTH_POLICY_LFU ? heat_[v.key] >= HOT_HEAT : v.last_tick == now_) s = -1;
+            }
+            if (s < 0) {
+                stats.prefetch_dropped++;
+                continue;
+            }
+            evict(s);
+        }
+        Slot &x = slot_[s];
+        x.key = key;
+        x.pf_unused = true;
+        x.prot_tick = now_ + 1;
+        slot_of_[key] = s;
+        load(key, s);
+        stats.prefetch_issued++;
+    }
+    stats.load_s += now_s() - t0;
+}
+
 void GpuExpertStore::tick() {
+    now_++;
     if (policy_ != HEARTH_POLICY_LFU) return;
     for (double &h : heat_) h *= HEAT_DECAY;
 }

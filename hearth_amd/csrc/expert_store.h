@@ -11,7 +11,12 @@
  *     (weights are bytes, reference INV-DET-1);
  *   - a load copies the slab from the mapped container into pinned staging, then to a
  *     device staging buffer on a copy stream, and repacks its three matrices into the
- *     slot's MFMA tile layout; the layer's device expert table gets the slot's matrices.
+ *     slot's MFMA tile layout; the layer's device expert table gets the slot's matrices;
+ *   - prefetch (store.c:541-561, 207-214): experts predicted for the next MoE layer are
+ *     loaded ahead into a free slot or an unprotected, not-hot victim (LRU: not used
+ *     in this forward; LFU: heat below 0.5 / (1 - decay)); resident ones are
+ *     protected for the current forward. A prefetched slot counts as used when it is
+ *     first demanded and as wasted when it is evicted before that.
  * Every call comes from the engine's thread (an engine handle is single-threaded).
  */
 #pragma once
@@ -37,6 +42,7 @@ inline void ck(hipError_t e) {
 
 struct StoreStats {
     uint64_t hits = 0, misses = 0, evictions = 0, loads = 0, bytes_read = 0;
+    uint64_t prefetch_issued = 0, prefetch_used = 0, prefetch_wasted = 0, prefetch_dropped = 0;
     double load_s = 0.0;   /* host time spent issuing loads and waiting for staging */
 };
 
@@ -48,7 +54,11 @@ public:
     /* Makes experts[0..n) of layer resident, writes their matrices into table_dev (device
      * [E]) and makes `compute` wait for the loads. */
     void ensure(int layer, const int *experts, int n, hxd::ExpertW *table_dev, hipStream_t compute);
-    /* forward boundary: LFU heat decay */
+    /* Loads experts[0..n) of layer ahead of their demand where a slot can be had
+     * without evicting a protected, in-use or hot expert; call after ensure() of the
+     * current layer (its slots stay in use). */
+    void prefetch(int layer, const int *experts, int n);
+    /* forward boundary: LFU heat decay, protection expires */
     void tick();
     /* HBM bytes of one slot for experts of D x F (room for Q8, the larger dtype) */
     static uint64_t slot_bytes_for(int D, int F);
@@ -61,11 +71,14 @@ private:
     struct Slot {
         int key = -1;
         uint64_t last_seq = 0;
+        uint64_t last_tick = 0;   /* forward of the last demand */
+        uint64_t prot_tick = 0;   /* protected while == now_ + 1 */
+        bool pf_unused = false;   /* prefetched, not demanded yet */
         hxd::ExpertW w{};
     };
     const ModelFile *mf_ = nullptr;
     int L_ = 0, E_ = 0, D_ = 0, F_ = 0, n_slots_ = 0, policy_ = 0;
-    uint64_t slot_bytes_ = 0, stage_bytes_ = 0, seq_ = 0;
+    uint64_t slot_bytes_ = 0, stage_bytes_ = 0, seq_ = 0, now_ = 0;
     uint8_t *pool_ = nullptr;
     std::vector<Slot> slot_;
     std::vector<int> slot_of_, free_;
@@ -79,7 +92,10 @@ private:
     hxd::ExpertW *htable_ = nullptr;  /* pinned [E]: entries written this call */
     hipEvent_t done_ = nullptr;
     hxd::QMat carve(uint8_t *&p, int dtype, int rows, int cols) const;
-    int victim();
+    bool protected_(const Slot &x) const { return x.prot_tick == now_ + 1; }
+    bool cheaper(int a, int b) const;
+    int victim(bool allow_protected);
+    void evict(int s);
     void load(int key, int slot);
 };
 

@@ -108,12 +108,14 @@ struct QkvArgs {
  *   mode 0: h = es * embed(tok[t])
  *   mode 1: h = h + rs * add[t]
  *   mode 2: h = h + rs * (sum_j w[t][j] * Y[pair_of[t][j]] (+ shared[t]))
- * then x = rmsnorm(h, w) and its activation blocks. */
+ *   mode 3: h unchanged
+ *   mode 4: v = h (+ rs * add[t], gated as in mode 2), h unchanged (prediction input)
+ * then x = rmsnorm(h or v, w) and its activation blocks. */
 struct NormArgs {
     int mode;
     float *h;                 /* [T][D] */
-    const float *add;         /* mode 1 / shared expert output (mode 2, may be null) */
-    const float *add_gate;    /* mode 2: per-token shared gate logit (out += add * sigmoid(gate)), or null */
+    const float *add;         /* mode 1 / shared expert output (modes 2 and 4, may be null) */
+    const float *add_gate;    /* modes 2, 4: per-token shared gate logit (add * sigmoid(gate)), or null */
     const float *Y;           /* mode 2 */
     const float *wts;
     const int *pair_of;

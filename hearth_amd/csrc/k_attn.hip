@@ -331,10 +331,11 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
 constexpr int VT2 = 128;              /* rows per tile */
 constexpr int VNS = 4;                /* LDS ring slots: one summed, three in flight */
 constexpr int VLPT = 10;              /* loads per loader wave per tile: 8 x 1 KiB of V, 2 x 64 p */
+constexpr int VPS = VT2 + 4;          /* p row stride: the four heads' rows in different banks */
 
 __global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float vt[VNS][VT2][64];
-    __shared__ __attribute__((aligned(16))) float pt[VNS][4][VT2];
+    __shared__ __attribute__((aligned(16))) float pt[VNS][4][VPS];
     __shared__ int anc_s[MAX_ANC];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
     const int nd = (hd + 63) / 64, qpt = (grp + 3) / 4;
@@ -391,13 +392,16 @@ __global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
             __builtin_amdgcn_s_barrier();
             issue(i + 3);              /* into the slot of tile i - 1, summed before this barrier */
         }
-        HX_WAIT_VMCNT(0);              /* no LDS write may land after the workgroup ends */
+        HX_WAIT_VMCNT(0);              /* no LDS write may land after the loop */
     } else {
-        const float *const pw0 = pt[0][wave], *const vw0 = &vt[0][0][lane];
+        /* summing wave w: heads hq * 4 + lane / 16, columns w * 16 + lane % 16 of the
+         * chunk -- the 16 lanes of a head read 64 bytes of each V row and the four heads
+         * share them (broadcast), a quarter of the LDS reads of one head per wave */
+        const float *const pw0 = pt[0][lane >> 4], *const vw0 = &vt[0][0][wave * 16 + (lane & 15)];
         for (int i = 0; i < ntiles; i++) {
             __syncthreads();
             const int slot = i % VNS, nv = nr - i * VT2;
-            const float *pw = pw0 + slot * (4 * VT2), *vw = vw0 + slot * (VT2 * 64);
+            const float *pw = pw0 + slot * (4 * VPS), *vw = vw0 + slot * (VT2 * 64);
             if (nv >= VT2) {
                 float pA[16], vA[16], pB[16], vB[16];
 #define HX_GRD(P_, V_, c_)                                                               \
@@ -423,9 +427,18 @@ __global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
                 for (int r = 0; r < nv; r++) acc = fadd(acc, fmul(pw[r], vw[r * 64]));
             }
         }
+    }
+    /* every LDS-direct load has landed and every tile has been read: the sums go through
+     * LDS so that wave w writes (and quantizes) the 64 columns of head hq * 4 + w */
+    __syncthreads();
+    float *ot = &vt[0][0][0];   /* [4 heads][64 columns] */
+    if (!loader) ot[(lane >> 4) * 64 + wave * 16 + (lane & 15)] = acc;
+    __syncthreads();
+    if (!loader) {
+        const float x = ot[wave * 64 + lane];
         const int d = dc * 64 + lane;
-        if (live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = acc;
-        if (a.qo_on && live) quant_block_wave(acc, a.qo, a.qo_hm ? h * a.T + t : t, a.qo_hm ? dc : h * (hd >> 6) + dc);
+        if (live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = x;
+        if (a.qo_on && live) quant_block_wave(x, a.qo, a.qo_hm ? h * a.T + t : t, a.qo_hm ? dc : h * (hd >> 6) + dc);
     }
 }
 

@@ -18,9 +18,11 @@ namespace {
 
 /* Residual update of token t's hidden row h (mode 0: h = embedding * emb_scale; 1:
  * h += rs * add; 2: h += rs * (sum_j w_j * Y[pair_j] (+ add)), j in rank order,
- * model.c:904-923; 3: h unchanged), then rmsnorm (quant.c:626-632: ms = sum16(h^2)/D, r = 1/sqrt(ms +
- * eps), x = (h * r) * w) and NUMERICS §2 of x. One workgroup per token; every load of
- * the residual step is issued before any of its sums. */
+ * model.c:904-923; 3: h unchanged; 4: v = h (+ rs * gated add) into the norm only,
+ * h unchanged -- the next-layer prediction input, model.c:1052-1058), then rmsnorm
+ * (quant.c:626-632: ms = sum16(v^2)/D, r = 1/sqrt(ms + eps), x = (v * r) * w) and
+ * NUMERICS §2 of x. One workgroup per token; every load of the residual step is issued
+ * before any of its sums. */
 __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
     extern __shared__ float hs[];
     __shared__ float wk[64];
@@ -45,6 +47,13 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
             v = fadd(h[i], fmul(a.rs, a.add[(size_t)t * D + i]));
         } else if (a.mode == 3) {
             v = h[i];
+        } else if (a.mode == 4) {
+            v = h[i];
+            if (a.add) {
+                float sv = a.add[(size_t)t * D + i];
+                if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_port_f(-a.add_gate[t]))));
+                v = fadd(v, fmul(a.rs, sv));
+            }
         } else {
             float out = 0.0f;
             for (int j0 = 0; j0 < K; j0 += 8) {
@@ -65,7 +74,7 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
             }
             v = fadd(h[i], fmul(a.rs, out));
         }
-        h[i] = v;
+        if (a.mode != 4) h[i] = v;
         hs[i] = v;
     }
     __syncthreads();

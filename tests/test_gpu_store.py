@@ -8,8 +8,12 @@ experts from host memory through a pool of E slots:
   (reference INV-DET-1);
 - hits, misses and evictions equal a replay of the victim policy (LRU: least recently
   used; LFU: lowest decayed heat, then least recent, store.c:166-199) over the routing
-  trace: per call and MoE layer the active experts in ascending order;
-- hearth_get_stats reports them (cache_hits / cache_misses / evictions / bytes_read).
+  trace: per call and MoE layer the active experts in ascending order (prefetch off);
+- hearth_get_stats reports them (cache_hits / cache_misses / evictions / bytes_read);
+- next-layer prefetch (model.c:935-984, store.c:541-561) -- the router of the next MoE
+  layer on the predicted input (h, plus the shared expert's output in shared mode) --
+  changes no logit, and its counters are consistent: every load is a miss or an issued
+  prefetch, a prefetched expert is used at most once and wasted only if never used.
 """
 from __future__ import annotations
 
@@ -93,7 +97,7 @@ def test_streamed_experts_bit_identical_and_policy(tiny_model, monkeypatch, tmp_
              ("tree", np.array([7, 11, 900, 5, 12], np.int32), np.array([-1, 0, 0, 1, 2], np.int32), [0, 1, 3])]
     ref, _ = _run(tiny_model, calls)
     monkeypatch.setenv("HEARTH_GPU_EXPERT_CACHE_GB", "0.001")
-    with Engine(tiny_model, max_seq=512, policy=policy) as e:
+    with Engine(tiny_model, max_seq=512, policy=policy, prefetch="off") as e:
         tr = tmp_path / "r.hrtr"
         e.trace_start(tr)
         got = []
@@ -132,7 +136,37 @@ def test_streamed_experts_deepseek_shape(variant_models, monkeypatch):
     toks = container.uniform_ints(52, 30, 4096)
     ref, _ = _run(path, [list(toks[:25]), list(toks[25:])])
     monkeypatch.setenv("HEARTH_GPU_EXPERT_CACHE_GB", "0.0001")
-    got, st = _run(path, [list(toks[:25]), list(toks[25:])])
+    got, st = _run(path, [list(toks[:25]), list(toks[25:])], prefetch="off")
     for a, b in zip(ref, got):
         assert np.array_equal(_bits(a), _bits(b))
     assert st["cache_slots"] == 16 and st["evictions"] > 0
+
+
+SLAB = {"tiny": 208896}
+
+
+@pytest.mark.parametrize("name", ["tiny", "dsv3"])
+@pytest.mark.parametrize("mode,extra", [("shared", 0), ("next", 2)])
+def test_prefetch_bit_identical_and_counters(tiny_model, variant_models, monkeypatch, name, mode, extra):
+    path = tiny_model if name == "tiny" else variant_models(name)
+    vocab = container.TINY.vocab if name == "tiny" else 4096
+    toks = [int(t) for t in container.uniform_ints(53, 100, vocab)]
+    calls = [toks[:40]] + [toks[i:i + 5] for i in range(40, 100, 5)]
+    ref, _ = _run(path, calls)
+    monkeypatch.setenv("HEARTH_GPU_EXPERT_CACHE_GB", "0.001")
+    off, st_off = _run(path, calls, prefetch="off")
+    got, st = _run(path, calls, prefetch=mode, prefetch_extra=extra)
+    for a, b, c in zip(ref, off, got):
+        assert np.array_equal(_bits(a), _bits(b))
+        assert np.array_equal(_bits(a), _bits(c))
+    assert st_off["prefetch_issued"] == 0
+    assert st["cache_hits"] + st["cache_misses"] == st["expert_loads_unique"] == st_off["expert_loads_unique"]
+    assert st["prefetch_issued"] > 0 and st["prefetch_used"] > 0
+    assert st["prefetch_used"] + st["prefetch_wasted"] <= st["prefetch_issued"]
+    assert st["prefetch_used"] <= st["cache_hits"]
+    slab = st_off["bytes_read"] // st_off["cache_misses"]
+    if name in SLAB:
+        assert slab == SLAB[name]
+    assert st["bytes_read"] == (st["cache_misses"] + st["prefetch_issued"]) * slab
+    # the predictions of these models are good enough to save demand loads
+    assert st["cache_misses"] < st_off["cache_misses"]
