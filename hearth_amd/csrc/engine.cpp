@@ -1189,7 +1189,7 @@ HEARTH_API int hearth_info(hearth_engine *e, hearth_model_info *out) {
     out->slab_bytes_max = e->mf.slab_bytes_max;
     out->params_total = e->mf.params_total;
     out->params_active = e->mf.params_active;
-    out->cache_slots = e->c.n_moe * e->E;
+    out->cache_slots = e->store ? e->store->slots() : e->c.n_moe * e->E;
     out->isa = e->opt.isa;
     out->n_threads = e->opt.n_threads;
     out->n_io_threads = e->opt.n_io_threads;

@@ -187,23 +187,31 @@ __device__ __forceinline__ int kperm_pos(int e) {
     return e < 32 ? (e >> 3) * 16 + (e & 7) : ((e - 32) >> 3) * 16 + 8 + ((e - 32) & 7);
 }
 
-/* NUMERICS §2 for the 64 values held one per lane by a full wave: writes q (kperm
- * order), d and the sum of block g of token row tok. Every lane must call it. */
-__device__ inline void quant_block_wave(float x, Act a, int tok, int g) {
-    const int lane = threadIdx.x & 63;
+/* NUMERICS §2 for the 64 values held one per lane by a full wave: this lane's q, the
+ * block's d and sum (the same on every lane). Every lane must call it. */
+__device__ inline void quant_block_vals(float x, int &q, float &d, int &sum) {
     float ax = fabsf(x);
     ax = ax == ax ? ax : 0.0f;                    /* NaN never wins the max */
     float amax = ax;
     for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    const float d = fdiv(amax, 127.0f);
+    d = fdiv(amax, 127.0f);
     const float id = d != 0.0f ? fdiv(1.0f, d) : 0.0f;
     float v = fmul(x, id);
     if (v != v) v = 0.0f;
     v = v > 127.0f ? 127.0f : v;
     v = v < -127.0f ? -127.0f : v;
-    const int q = (int)__builtin_rintf(v);
-    int sum = q;
+    q = (int)__builtin_rintf(v);
+    sum = q;
     for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+}
+
+/* NUMERICS §2 for the 64 values held one per lane by a full wave: writes q (kperm
+ * order), d and the sum of block g of token row tok. Every lane must call it. */
+__device__ inline void quant_block_wave(float x, Act a, int tok, int g) {
+    const int lane = threadIdx.x & 63;
+    int q, sum;
+    float d;
+    quant_block_vals(x, q, d, sum);
     const size_t base = (size_t)tok * a.nbp + g;
     a.q[base * 64 + kperm_pos(lane)] = (int8_t)q;
     if (lane == 0) {

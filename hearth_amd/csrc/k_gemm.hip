@@ -496,14 +496,14 @@ __global__ __launch_bounds__(256) void k_expert_gateup_pp(MoeArgs a, int ntok) {
 }
 
 /* Expert products for experts of at most 16 tokens, K split over S waves per row tile:
- * gate and up with the SwiGLU epilogue (DOWN = false), or the down projection
- * (DOWN = true).
+ * gate and up with the SwiGLU epilogue (MODE TK_GATEUP), or the down projection of
+ * quantized rows (TK_DOWN: the SwiGLU rows, MLA's W_UV).
  *
  * Workgroup = (token group g, active slot, rpw row tiles of 16 rows); S waves per row
  * tile. Wave (row tile r, part p) streams block pairs [p TK_NP, (p + 1) TK_NP) of the
- * tile's matrices into registers, every load issued at once. The slot's activations
- * are staged once per workgroup in LDS by LDS-direct loads, in the MFMA B-operand
- * layout with column = token.
+ * tile's matrices into registers, every load issued at once. The slot's activation
+ * blocks are staged once per workgroup in LDS by LDS-direct loads, [block][token][64 B]
+ * (the Act block of each token, k-group kg at 16 kg).
  *
  * Tokens go in groups of four: for group g the B operand of column c is read from token
  * 4 g + c % 4, so the MFMA result holds each (row, token) pair four times and lane
@@ -540,8 +540,11 @@ __host__ __device__ inline size_t tk_lds_bytes(int nbp, int nm, int np, int rpw,
     return (size_t)nbp * 1024 + (size_t)nbp4 * 128 + (size_t)rpw * S * nm * 2 * np * 32 + (size_t)rpw * nm * 64 * 4;
 }
 
-template <int DT, bool DOWN>
+enum { TK_GATEUP = 0, TK_DOWN = 1 };
+
+template <int DT, int MODE>
 __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, int gmax, int n_slots) {
+    constexpr bool DOWN = MODE != TK_GATEUP;
     extern __shared__ __attribute__((aligned(16))) uint8_t tk_lds[];
     constexpr int NP = TkCfg<DT>::NP, NV = TkCfg<DT>::NV, NBK = 2 * NP, NM = DOWN ? 1 : 2;
     const int rows_out = DOWN ? a.D : a.F;
@@ -585,15 +588,17 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
     const int rt = live ? rt0 : ntile - 1;   /* a dead wave loads a live tile and discards it */
     const int nb = mat[0].nb, nbp = mat[0].nbp, npair = nbp >> 1, nbp4 = (nbp + 3) & ~3;
     const int g0 = part * NP, kb0 = 2 * g0;   /* first pair / block of this part */
-    uint8_t *xs = tk_lds;                                   /* [nbp][64 lanes][16 B] */
+    uint8_t *xs = tk_lds;                                   /* [nbp][16 tokens][64 B] */
     float *dxs = (float *)(xs + (size_t)nbp * 1024);        /* [nbp4][16 tokens] */
     int *sxs = (int *)(dxs + nbp4 * 16);                    /* [nbp4][16 tokens] */
     uint8_t *scl = (uint8_t *)(sxs + nbp4 * 16) + wave * NM * NBK * 32;   /* [NM][NBK][16 halves] */
     float *relay = (float *)((uint8_t *)(sxs + nbp4 * 16) + W * NM * NBK * 32) + rtl * NM * 64;
     /* issue order: the token rows, the weights (straight-line loads), then the
-     * LDS-direct loads that need the token rows */
-    const int tcol = lr < n ? lr : n - 1;   /* column lr = token lr */
-    const int arow = DOWN ? p0 + tcol : a.pair_tok[p0 + tcol];
+     * LDS-direct loads that need the token rows. The q loads cover token lane / 4,
+     * k-group lane % 4 of a block; the d and s loads token lane % 16 of four blocks. */
+    const int tq = (lane >> 2) < n ? (lane >> 2) : n - 1, tds = lr < n ? lr : n - 1;
+    const int arow_q = MODE == TK_GATEUP ? a.pair_tok[p0 + tq] : p0 + tq;
+    const int arow_d = MODE == TK_GATEUP ? a.pair_tok[p0 + tds] : p0 + tds;
     v4i w[NM][NP][NV];
 #pragma unroll
     for (int k = 0; k < NP; k++) {
@@ -617,11 +622,11 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
         int it = 0;
         do {   /* nit >= 1 */
             const int b = wave + it * W;
-            if (b < nbp) lds_direct<16>(x.q + ((size_t)arow * x.nbp + b) * 64 + kg * 16, xs + (size_t)b * 1024);
+            if (b < nbp) lds_direct<16>(x.q + ((size_t)arow_q * x.nbp + b) * 64 + (lane & 3) * 16, xs + (size_t)b * 1024);
             if (4 * b < nbp4) {
                 const int bb = 4 * b + kg < nbp ? 4 * b + kg : nbp - 1;
-                lds_direct<4>(x.d + (size_t)arow * x.nbp + bb, dxs + 4 * b * 16);
-                if (DT == 4) lds_direct<4>(x.s + (size_t)arow * x.nbp + bb, sxs + 4 * b * 16);
+                lds_direct<4>(x.d + (size_t)arow_d * x.nbp + bb, dxs + 4 * b * 16);
+                if (DT == 4) lds_direct<4>(x.s + (size_t)arow_d * x.nbp + bb, sxs + 4 * b * 16);
             }
             const int b0 = it * 8;
             if (b0 < NBK) {
@@ -636,15 +641,16 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
     __builtin_amdgcn_s_barrier();
     const int q = lr >> 2;                /* register of this lane's pair: row 4 kg + q */
     const int col = 4 * g + (lr & 3);     /* token of this lane's pair */
+    const int colc = col < n ? col : n - 1;   /* its staged row (columns past n are discarded) */
     const v4i zero = {0, 0, 0, 0};
     const bool full = kb0 + NBK <= nb;    /* uniform */
     /* terms of local block kb (global kb0 + kb); the MFMA gives sum q x with q the
      * stored nibble (Q4), so isum = sum q x - 8 sx */
     auto terms = [&](const v4i (&wa)[NM], int kb, float (&t)[NM]) {
         const int blk = kb0 + kb;
-        const v4i xq = *(const v4i *)(xs + (size_t)blk * 1024 + (kg * 16 + col) * 16);
-        const float d = dxs[blk * 16 + col];
-        const int off = DT == 4 ? 8 * sxs[blk * 16 + col] : 0;
+        const v4i xq = *(const v4i *)(xs + ((size_t)blk * 16 + colc) * 64 + kg * 16);
+        const float d = dxs[blk * 16 + colc];
+        const int off = DT == 4 ? 8 * sxs[blk * 16 + colc] : 0;
 #pragma unroll
         for (int mi = 0; mi < NM; mi++) {
             const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[mi], xq, zero, 0, 0, 0);
@@ -719,7 +725,8 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
 
 /* launches k_expert_tk for experts of at most 16 tokens and one dtype; false when the
  * shape does not fit (the caller uses the general kernels) */
-bool launch_tk(const MoeArgs &a, bool down, int n_slots, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+bool launch_tk(const MoeArgs &a, int mode, int n_slots, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    const bool down = mode != TK_GATEUP;
     const bool q4 = a.dtype_mask & (1 << 4), q8 = a.dtype_mask & (1 << 3);
     if (a.T > 16 || q4 == q8) return false;
     const int K = down ? a.F : a.D, rows = down ? a.D : a.F;
@@ -734,10 +741,11 @@ bool launch_tk(const MoeArgs &a, bool down, int n_slots, hipStream_t st, hipEven
     const int ch = tk_chunk(rpw);
     const int chunks = n_slots * ((tpw + ch - 1) / ch);
     const dim3 grid(8 * ((chunks + 7) / 8) * ch * gmax), block(64 * W);
-    if (q4 && !down) hipExtLaunchKernelGGL(k_expert_tk<4, false>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots);
-    if (q4 && down) hipExtLaunchKernelGGL(k_expert_tk<4, true>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots);
-    if (q8 && !down) hipExtLaunchKernelGGL(k_expert_tk<3, false>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots);
-    if (q8 && down) hipExtLaunchKernelGGL(k_expert_tk<3, true>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots);
+#define TK_LAUNCH(DT_, MODE_) \
+    hipExtLaunchKernelGGL(k_expert_tk<DT_, MODE_>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots)
+    if (mode == TK_GATEUP) { if (q4) TK_LAUNCH(4, TK_GATEUP); else TK_LAUNCH(3, TK_GATEUP); }
+    if (mode == TK_DOWN) { if (q4) TK_LAUNCH(4, TK_DOWN); else TK_LAUNCH(3, TK_DOWN); }
+#undef TK_LAUNCH
     return true;
 }
 
@@ -985,7 +993,7 @@ void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0
      * first launch, ev1 at the end of the last */
     const bool q4 = a.dtype_mask & (1 << 4), q8 = a.dtype_mask & (1 << 3);
     /* at most 16 tokens per expert, one dtype: the split-K kernel (one term per lane) */
-    if (launch_tk(a, false, n_slots, st, ev0, ev1)) return;
+    if (launch_tk(a, TK_GATEUP, n_slots, st, ev0, ev1)) return;
     /* few tokens, one dtype, one pair chunk per wave: the persistent kernel (two
      * workgroups per CU on every CU) */
     const int npair = nbp / 2, W = threads / 64;
@@ -1011,7 +1019,7 @@ void expert_down(const MoeArgs &a, int n_slots, hipStream_t st) {
 
 void expert_down_q(const MoeArgs &a, int n_slots, hipStream_t st) {
     if (n_slots <= 0) return;
-    if (launch_tk(a, true, n_slots, st, nullptr, nullptr)) return;
+    if (launch_tk(a, TK_DOWN, n_slots, st, nullptr, nullptr)) return;
     const int nb = (a.F + 63) / 64, nbp = (nb + 1) & ~1;
     const int ntok = sk_ntok(a.T, 1, nb);
     const int threads = 64 * sk_waves(nbp / 2);

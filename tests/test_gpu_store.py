@@ -110,6 +110,7 @@ def test_streamed_experts_bit_identical_and_policy(tiny_model, monkeypatch, tmp_
                 got.append(e.eval(c, all_logits=True))
         e.trace_stop()
         st = e.stats()
+        assert e.info["cache_slots"] == 16
         after = e.eval([3])
     for a, b in zip(ref, got):
         assert np.array_equal(_bits(a), _bits(b))
