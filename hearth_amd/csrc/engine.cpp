@@ -234,6 +234,7 @@ struct hearth_engine {
         if (h_res) (void)hipHostFree(h_res);
         if (h_meta) (void)hipHostFree(h_meta);
         if (h_plog) (void)hipHostFree(h_plog);
+        if (replay_dev) (void)hipFree(replay_dev);
         store.reset();
         if (st) (void)hipStreamDestroy(st);
         if (trace) fclose(trace);
@@ -839,6 +840,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 r.u_p0 = u_p0; r.u_n = u_n; r.pair_tok = pair_tok; r.pair_of = pair_of;
                 r.route_out = route_out; r.moe_ord = moe_ord[l]; r.n_moe = c.n_moe; r.stats = dstats;
                 r.table = w.experts; r.desc = slot_desc; r.n_slots = std::min(E, T * K);
+                r.replay = replay_dev; r.replay_rows = replay_rows; r.pos0 = pos; r.depth = depth;
                 hxl::route(r, st);
             });
             if (store) {
@@ -1301,11 +1303,73 @@ HEARTH_API int hearth_trace_stop(hearth_engine *e) {
     return OK;
 }
 
+/* hx_model_route_replay (model.c:1885-1960): "" or NULL turns replay off; else the
+ * trace must match the model (E, K, n_moe; n_layers >= n_moe), hold whole rows of
+ * n_moe * K little-endian uint16 ids (at most 4 GiB), and every row must name K
+ * distinct experts below E. A failed call keeps the previous replay. */
 HEARTH_API int hearth_route_replay(hearth_engine *e, const char *path) {
     if (!e) return E_ARG;
-    if (!path || !*path) return OK;
-    log_msg(LOG_ERROR, "route replay is not supported by this build yet");
-    return E_FORMAT;
+    if (!path || !*path) {
+        if (e->replay_dev) (void)hipSetDevice(e->dev), (void)hipFree(e->replay_dev);
+        e->replay_dev = nullptr;
+        e->replay_rows = 0;
+        return OK;
+    }
+    if (!e->c.n_moe) { log_msg(LOG_ERROR, "route replay: the model has no MoE layers"); return E_FORMAT; }
+    FILE *f = fopen(path, "rb");
+    if (!f) { log_msg(LOG_ERROR, "route replay: cannot open %s", path); return E_IO; }
+    std::vector<uint8_t> buf;
+    {
+        uint8_t chunk[1 << 16];
+        size_t got;
+        while ((got = fread(chunk, 1, sizeof chunk, f)) > 0) {
+            buf.insert(buf.end(), chunk, chunk + got);
+            if (buf.size() > (4ull << 30) + 24) break;
+        }
+        const bool err = ferror(f);
+        fclose(f);
+        if (err) { log_msg(LOG_ERROR, "route replay: cannot read %s", path); return E_IO; }
+    }
+    auto rd32 = [&](size_t o) { return (uint32_t)buf[o] | ((uint32_t)buf[o + 1] << 8) | ((uint32_t)buf[o + 2] << 16) | ((uint32_t)buf[o + 3] << 24); };
+    const int E = e->E, K = e->K, nm = e->c.n_moe;
+    if (buf.size() < 24) { log_msg(LOG_ERROR, "route replay: %s is not a routing trace", path); return E_FORMAT; }
+    if (rd32(0) != 0x52545248u || rd32(4) != 1u || rd32(8) < (uint32_t)nm || rd32(12) != (uint32_t)E ||
+        rd32(16) != (uint32_t)K || rd32(20) != (uint32_t)nm) {
+        log_msg(LOG_ERROR, "route replay: %s does not match this model (needs %d experts, top-%d, %d MoE layers)", path, E,
+                K, nm);
+        return E_FORMAT;
+    }
+    const uint64_t row = (uint64_t)nm * K, body = buf.size() - 24;
+    if (body == 0 || body % (2 * row) != 0 || body > (1ull << 32)) {
+        log_msg(LOG_ERROR, "route replay: %s has a body of %llu bytes (rows of %llu bytes)", path,
+                (unsigned long long)body, (unsigned long long)(2 * row));
+        return E_FORMAT;
+    }
+    const uint64_t rows = body / (2 * row);
+    std::vector<int> ids(body / 2);
+    for (size_t i = 0; i < ids.size(); i++) ids[i] = buf[24 + 2 * i] | (buf[24 + 2 * i + 1] << 8);
+    for (uint64_t r = 0; r < rows * nm; r++) {
+        const int *v = ids.data() + r * K;
+        for (int j = 0; j < K; j++) {
+            bool bad = v[j] >= E;
+            for (int i = 0; i < j && !bad; i++) bad = v[i] == v[j];
+            if (bad) {
+                log_msg(LOG_ERROR, "route replay: %s token %llu has an invalid or repeated expert id", path,
+                        (unsigned long long)(r / nm));
+                return E_FORMAT;
+            }
+        }
+    }
+    int *d = nullptr;
+    if (hipSetDevice(e->dev) != hipSuccess || hipMalloc((void **)&d, sizeof(int) * ids.size()) != hipSuccess) return E_NOMEM;
+    if (hipMemcpy(d, ids.data(), sizeof(int) * ids.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(d);
+        return E_NOMEM;
+    }
+    if (e->replay_dev) (void)hipFree(e->replay_dev);   /* kernels that read it have finished: eval is synchronous */
+    e->replay_dev = d;
+    e->replay_rows = (int64_t)rows;
+    return OK;
 }
 
 /* ---- extensions (hearth_gpu.h) ---- */

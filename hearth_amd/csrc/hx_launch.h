@@ -65,6 +65,12 @@ struct RouteArgs {
     const ExpertW *table;     /* [E] expert matrices of the layer */
     SlotDesc *desc;           /* [n_slots] out: active slots, then n = 0 */
     int n_slots;
+    /* route replay (model.c:1004-1012): token t takes the experts of trace row
+     * (pos0 + depth[t]) % replay_rows, this MoE layer's K entries; null = routing */
+    const int *replay;        /* [replay_rows][n_moe][K] */
+    long long replay_rows;
+    int pos0;
+    const int *depth;         /* [T] */
 };
 
 /* Per-call token geometry: token t sits at KV slot pos0 + t, has RoPE position

@@ -153,6 +153,12 @@ __device__ __forceinline__ void wave_best(float &v, int &idx) {
 
 constexpr int ROUTE_EMAX = 1024;
 
+/* expert j of token t under route replay */
+__device__ __forceinline__ int replay_id(const RouteArgs &a, int t, int j) {
+    const long long pos = (long long)a.pos0 + a.depth[t];
+    return a.replay[(size_t)(pos % a.replay_rows) * (size_t)(a.n_moe * a.K) + (size_t)a.moe_ord * a.K + j];
+}
+
 /* One wave per token: scores, selection values, group limit, top-K, weights. */
 __global__ __launch_bounds__(64) void k_route_tokens(RouteArgs a) {
     __shared__ float score[ROUTE_EMAX], sel[ROUTE_EMAX];
@@ -189,6 +195,11 @@ __global__ __launch_bounds__(64) void k_route_tokens(RouteArgs a) {
         taken[e] = 0;
     }
     wave_sync();
+    int my_id = -1;
+    if (a.replay) {   /* uniform */
+        if (lane < K) my_id = replay_id(a, t, lane);
+        goto weights;
+    }
     if (a.n_group > 1) {
         const int ng = a.n_group, gs = E / ng;
         for (int g = 0; g < ng; g++) {
@@ -216,7 +227,6 @@ __global__ __launch_bounds__(64) void k_route_tokens(RouteArgs a) {
             if (!gkeep[e / gs]) sel[e] = 0.0f;
         wave_sync();
     }
-    int my_id = -1;
     for (int j = 0; j < K; j++) {
         float v = 0.0f;
         int bi = -1;
@@ -227,6 +237,7 @@ __global__ __launch_bounds__(64) void k_route_tokens(RouteArgs a) {
         if (lane == j) my_id = bi;
         wave_sync();
     }
+weights:
     /* weights: w_j = score[id_j]; norm_topk: w_j / (sum_j w_j + 1e-20f), sum in rank order */
     float w = lane < K ? score[my_id] : 0.0f;
     if (a.norm_topk) {
@@ -301,18 +312,22 @@ __global__ __launch_bounds__(256) void k_route_rank(RouteArgs a) {
         for (int e = tid; e < E; e += 256) score[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
     }
     __syncthreads();
-    for (int e = tid; e < E; e += 256) key[e] = rank_key(a.bias ? fadd(score[e], a.bias[e]) : score[e], e);
-    __syncthreads();
-    for (int e = tid; e < E; e += 256) {
-        const unsigned long long ke = key[e];
-        int rank = 0;
-        int o = 0;
-        for (; o + 4 <= E; o += 4) {
-            const unsigned long long k0 = key[o], k1 = key[o + 1], k2 = key[o + 2], k3 = key[o + 3];
-            rank += (k0 > ke) + (k1 > ke) + (k2 > ke) + (k3 > ke);
+    if (a.replay) {   /* uniform */
+        if (tid < K) chosen[tid] = replay_id(a, t, tid);
+    } else {
+        for (int e = tid; e < E; e += 256) key[e] = rank_key(a.bias ? fadd(score[e], a.bias[e]) : score[e], e);
+        __syncthreads();
+        for (int e = tid; e < E; e += 256) {
+            const unsigned long long ke = key[e];
+            int rank = 0;
+            int o = 0;
+            for (; o + 4 <= E; o += 4) {
+                const unsigned long long k0 = key[o], k1 = key[o + 1], k2 = key[o + 2], k3 = key[o + 3];
+                rank += (k0 > ke) + (k1 > ke) + (k2 > ke) + (k3 > ke);
+            }
+            for (; o < E; o++) rank += key[o] > ke;
+            if (rank < K) chosen[rank] = e;
         }
-        for (; o < E; o++) rank += key[o] > ke;
-        if (rank < K) chosen[rank] = e;
     }
     __syncthreads();
     /* weights: w_j = score[id_j]; norm_topk: w_j / (sum_j w_j + 1e-20f), sum in rank order */
@@ -454,6 +469,9 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
         } else {
             for (int e = lane; e < E; e += 64) sc[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
         }
+        if (a.replay) {   /* uniform */
+            if (lane < K) chosen[t][lane] = replay_id(a, t, lane);
+        } else {
         /* top-K: K rounds of a wave-wide maximum of the selection keys (a larger key ranks
          * first in ranks_before's order); the winner's key is cleared (0 is below every
          * key) before the next round */
@@ -477,6 +495,7 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
             for (int u = 0; u < RS_EMAX / 64; u++)
                 if (lane + 64 * u == e) kk[u] = 0ull;
             if (lane == 0) chosen[t][j] = e;
+        }
         }
         wave_sync();
         const int id = lane < K ? chosen[t][lane] : 0;

@@ -513,6 +513,9 @@ struct ho_model {
     float *kv;            /* per layer: GQA K [cap][kvd], V [cap][kvd]; MLA c [cap][C], kpe [cap][r] */
     size_t per_layer;
     int *moe_ord;
+    uint16_t *replay;     /* route replay [rows][n_moe][K], or NULL */
+    int64_t replay_rows;
+    int cur_pos;          /* position of the token being evaluated (replay row) */
 };
 
 /* appends n floats to <dump_dir>/l<layer>_<name>.bin (debug comparisons) */
@@ -713,6 +716,7 @@ void ho_close(ho_model *m) {
     free(m->ex);
     free(m->kv);
     free(m->moe_ord);
+    free(m->replay);
     free(m);
 }
 
@@ -726,6 +730,21 @@ void ho_info(const ho_model *m, int *o) {
 }
 
 int ho_pos(const ho_model *m) { return m->pos; }
+
+/* Route replay (model.c:1885-1960 loads and checks the trace): ids [rows][n_moe][K],
+ * checked by the caller; NULL or rows 0 turns it off. */
+int ho_set_replay(ho_model *m, const uint16_t *ids, int64_t rows) {
+    free(m->replay);
+    m->replay = NULL;
+    m->replay_rows = 0;
+    if (!ids || rows <= 0) return 0;
+    const size_t n = (size_t)rows * (size_t)m->c.n_moe * (size_t)m->c.top_k;
+    m->replay = (uint16_t *)malloc(n * sizeof(uint16_t));
+    if (!m->replay) return -5;
+    memcpy(m->replay, ids, n * sizeof(uint16_t));
+    m->replay_rows = rows;
+    return 0;
+}
 
 int ho_rewind(ho_model *m, int pos) {
     if (pos < 0 || pos > m->pos) return -3;
@@ -903,6 +922,14 @@ static void route(ho_model *m, int l, const float *x, int *ids, float *w) {
     dump(m, "router", l, score, E, 4);
     if (c->score_fn == 0) softmax(score, E);
     else for (int e = 0; e < E; e++) score[e] = sigmoidf_(score[e]);
+    if (m->replay) {
+        /* route replay (model.c:1004-1012): the experts of the trace row of this token's
+         * position, weights from the router's scores */
+        const uint16_t *row = m->replay + (size_t)(m->cur_pos % m->replay_rows) * (size_t)(c->n_moe * K) +
+                              (size_t)m->moe_ord[l] * K;
+        for (int j = 0; j < K; j++) ids[j] = row[j];
+        goto weights;
+    }
     const float *bias = c->score_bias ? vec(m, l, "moe_router_bias") : NULL;
     for (int e = 0; e < E; e++) sel[e] = bias ? score[e] + bias[e] : score[e];
     if (c->n_group > 1) {
@@ -936,6 +963,7 @@ static void route(ho_model *m, int l, const float *x, int *ids, float *w) {
         ids[j] = best;
         taken[best] = 1;
     }
+weights:
     for (int j = 0; j < K; j++) w[j] = score[ids[j]];
     if (c->norm_topk) {
         float s = 0.0f;
@@ -976,6 +1004,7 @@ static void moe(ho_model *m, int l, const float *x, float *out, int32_t *route_o
 }
 
 static void forward_token(ho_model *m, int tok, int pos, int slot, const int *rows, int nr, float *logits, int32_t *routes) {
+    m->cur_pos = pos;
     const cfg *c = &m->c;
     const int D = c->d_model;
     const tens *emb = find_tensor(m, -1, "tok_embd"), *head = c->tie ? emb : find_tensor(m, -1, "lm_head");

@@ -89,6 +89,10 @@ int       ho_eval_tree(ho_model *m, const int32_t *tokens, const int32_t *parent
 /* Moves the K/V of nodes path[0..n) (path[j] at depth j) to slots pos..pos+n-1 and
  * sets pos += n. */
 int       ho_commit_path(ho_model *m, const int32_t *path, int n);
+/* Route replay (model.c:1004-1012): the token at position p takes the experts of trace
+ * row p % rows for each MoE layer, weights from the router's scores. ids [rows][n_moe][K]
+ * (the caller checks them); NULL turns replay off. Returns 0 or -5. */
+int       ho_set_replay(ho_model *m, const uint16_t *ids, int64_t rows);
 /* Sets the number of worker threads for the big matrix-vector products (>= 1). */
 void      ho_set_threads(ho_model *m, int n);
 /* Debug: append per-token intermediates (q, att, h_mid, x_ffn, router, ids, h) to

@@ -63,6 +63,7 @@ def lib():
         L.ho_eval_tree.argtypes = [c_void_p, _I32P, _I32P, c_int, _FP, _I32P]
         L.ho_commit_path.argtypes = [c_void_p, _I32P, c_int]
         L.ho_set_threads.argtypes = [c_void_p, c_int]
+        L.ho_set_replay.argtypes = [c_void_p, POINTER(ctypes.c_uint16), c_int64]
         L.ho_probs.argtypes = [_FP, c_int, c_double, c_int, c_double, c_double, _DP]
         L.ho_argmax.argtypes = [_FP, c_int]
         L.ho_draw.argtypes = [_DP, c_int, c_double]
@@ -155,6 +156,35 @@ class Model:
     def commit_path(self, path) -> None:
         p = np.ascontiguousarray(path, dtype=np.int32)
         assert lib().ho_commit_path(self.h, p.ctypes.data_as(_I32P), p.size) == 0
+
+    def set_replay(self, ids) -> None:
+        """route replay: ids [rows][n_moe][K] (uint16), or None for routing"""
+        if ids is None:
+            assert lib().ho_set_replay(self.h, None, 0) == 0
+            return
+        a = np.ascontiguousarray(ids, dtype=np.uint16)
+        assert lib().ho_set_replay(self.h, a.ctypes.data_as(POINTER(ctypes.c_uint16)), a.shape[0]) == 0
+
+
+def write_trace(path, ids, n_layers: int, n_experts: int) -> None:
+    """a routing trace file (FORMAT.md §9): 'HRTR', version 1, n_layers, E, K, n_moe,
+    then rows of n_moe * K little-endian uint16 expert ids"""
+    a = np.ascontiguousarray(ids, dtype="<u2")
+    rows, n_moe, k = a.shape
+    hdr = np.array([0x52545248, 1, n_layers, n_experts, k, n_moe], dtype="<u4")
+    with open(path, "wb") as f:
+        f.write(hdr.tobytes())
+        f.write(a.tobytes())
+
+
+def synthetic_routes(seed: int, rows: int, n_moe: int, n_experts: int, k: int) -> np.ndarray:
+    """rows of K distinct experts per MoE layer"""
+    rng = np.random.default_rng(seed)
+    out = np.empty((rows, n_moe, k), dtype=np.uint16)
+    for r in range(rows):
+        for m in range(n_moe):
+            out[r, m] = rng.choice(n_experts, size=k, replace=False)
+    return out
 
 
 def accept_tree(rows, tokens, parent, mode=0, temperature=0.0, top_k=0, top_p=1.0, min_p=0.0, q=None, u=None):

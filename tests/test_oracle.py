@@ -147,6 +147,36 @@ def test_oracle_matches_reference_engine_variants(variant_models, variant):
     assert np.array_equal(lr2.view(np.uint32), lo2.view(np.uint32))
 
 
+@pytest.mark.skipif(not O.REF_LIB.is_file(), reason="reference engine not built (make -C oracle)")
+@pytest.mark.parametrize("name", ["tiny", "dsv3"])
+def test_oracle_route_replay_matches_reference_engine(tiny_model, variant_models, tmp_path, name):
+    """Route replay (model.c:1004-1012, 1885-1960): the token at position p takes the
+    experts of trace row p % rows for every MoE layer, weights from the router's scores
+    (no selection bias, no group limit). The restatement is bit-exact with the reference
+    engine replaying the same synthetic trace, rows wrapping, and reports the replayed
+    routes."""
+    from hearth_amd.engine import Engine
+    path = tiny_model if name == "tiny" else variant_models(name)
+    O.set_exp_mode(O.EXP_LIBM)
+    m = O.Model(path)
+    ids = O.synthetic_routes(7, 37, m.n_moe, m.n_experts, m.top_k)
+    tr = tmp_path / "routes.hrtr"
+    O.write_trace(tr, ids, m.n_layers, m.n_experts)
+    vocab = container.TINY.vocab if name == "tiny" else 4096
+    toks = container.uniform_ints(41, 64, vocab)
+    ref = Engine(path, lib=str(O.REF_LIB), threads=4, prefetch="off")
+    ref.route_replay(tr)
+    lr = ref.eval(toks, all_logits=True)
+    lr2 = ref.eval(toks[:5], all_logits=True)
+    ref.close()
+    m.set_replay(ids)
+    lo, ro = m.eval(toks, routes=True)
+    lo2 = m.eval(toks[:5])
+    assert np.array_equal(lr.view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(lr2.view(np.uint32), lo2.view(np.uint32))
+    assert np.array_equal(ro, ids[np.arange(64) % 37].astype(np.int32))
+
+
 def test_tree_equals_chain(tiny_model):
     """Every tree node's logits equal the chain evaluation of its root path (bit for bit),
     and committing a path leaves the same KV as evaluating the chain."""
