@@ -47,7 +47,6 @@ def test_prompt_bit_exact_with_oracle(eng, tiny_model):
 def test_within_tolerance_of_reference_engine(eng):
     g = golden_io.tiny_ref()
     eng.reset()
-    eng.trace_start("/tmp/hx_gpu_trace.hrtr") if False else None
     lp = eng.eval(g["prompt"], all_logits=True)
     ref = g["prompt_last8"]
     scale = max(1.0, float(np.abs(ref).max()))
