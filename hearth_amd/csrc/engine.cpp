@@ -154,6 +154,7 @@ struct hearth_engine {
     int *h_res = nullptr;
     hipEvent_t geom_ev = nullptr;   /* recorded after the last upload from h_geom / h_rope */
     bool geom_pending = false;
+    int geom_chain = 1;           /* the uploaded geometry is a chain (no parent table, or parent[i] = i - 1) */
 
     int pos = 0;
     /* telemetry */
@@ -727,7 +728,7 @@ void hearth_engine::attn_mla(const Layer &w, int l, int T) {
     ma.rope = rope; ma.rope_dim = rope_dim; ma.rope_style = c.rope_style; ma.eps = c.eps; ma.pos0 = pos;
     ma.wuk = w.kvb_raw; ma.wuk_dtype = w.kvb_dtype; ma.wuk_rb = w.kvb_rb; ma.qlat = qr;
     ma.S = S; ma.ldS = ldS; ma.scale = c.attn_scale;
-    ma.g.depth = depth; ma.g.anc = anc; ma.g.anc_ld = B; ma.g.pos0 = pos;
+    ma.g.depth = depth; ma.g.anc = anc; ma.g.anc_ld = B; ma.g.pos0 = pos; ma.g.chain = geom_chain;
     ma.Yv = yv; ma.att = att; ma.aatt = aatt;
     hxl::mla_post(ma, st);
     hxl::mla_qlat(ma, st);
@@ -790,7 +791,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             hxd::AttnArgs at{};
             at.q = qr; at.kc = qa.kc; at.vc = qa.vc; at.S = S; at.ldS = ldS; at.out = att; at.T = T; at.H = H;
             at.Hkv = Hkv; at.hd = hd; at.cap = cap; at.scale = c.attn_scale;
-            at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos0 = pos;
+            at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos0 = pos; at.g.chain = geom_chain;
             at.qo = aatt; at.qo_on = w.o.quant && hd % 64 == 0;
             hxl::attention(at, st);
             dump("att", l, att, T, q_dim);
@@ -983,6 +984,8 @@ int hearth_engine::run_geometry(const int32_t *tok, const int32_t *parent, int n
     /* the staging buffers may still feed the previous call's uploads */
     if (geom_pending) ck(hipEventSynchronize(geom_ev));
     int *ht = h_geom, *hdp = h_geom + B, *hanc = h_geom + 2 * B;
+    geom_chain = 1;
+    for (int i = 0; parent && i < n; i++) geom_chain &= parent[i] == i - 1;
     for (int i = 0; i < n; i++) {
         ht[i] = tok[i];
         hdp[i] = parent ? (i == 0 ? 0 : hdp[parent[i]] + 1) : i;

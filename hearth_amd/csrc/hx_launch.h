@@ -82,6 +82,7 @@ struct TokGeom {
     const int *anc;           /* [T][anc_ld] */
     int anc_ld;
     int pos0;
+    int chain;                /* 1: token t sits at slot pos0 + t with ancestors pos0..pos0 + t */
 };
 
 struct AttnArgs {

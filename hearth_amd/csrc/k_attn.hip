@@ -11,13 +11,15 @@
  *
  * The value sum is one dependent f32 add chain per (token, head, d) of length
  * pos0 + depth + 1; it is the step's latency floor, so the value kernel keeps one
- * chain per lane, one summing wave per SIMD, and V tiles streamed three tiles ahead
- * into an LDS ring shared by the four summing waves (heads) of a workgroup.
+ * chain per lane and one summing wave per SIMD, fed from transposed V tiles that
+ * eight loader waves keep three tiles ahead.
  *
  * Launch shapes are XCD-aware: workgroup IDs are dealt round-robin to the 8 XCDs,
  * so the KV-group index (and value d-chunk) is the fastest-varying part of the ID and
  * the workgroups of one XCD read the same group's K or V rows from that XCD's L2.
  */
+#include <type_traits>
+
 #include "hx_device.h"
 #include "hx_launch.h"
 
@@ -315,27 +317,58 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
 }
 
 /* o[t][h][d] = sum_v p_v * V_v[d], v in order. A workgroup sums up to four heads of
- * one token t in one KV group g, for one 64-wide d chunk (one wave per head, lane = d),
- * and has four more waves that only move data: they issue LDS-direct loads
- * (global_load_lds: the bytes go from memory straight into LDS, no registers, a few
- * address instructions per KiB), so the summing waves keep their SIMD's VALU to the
- * product + dependent add of each row. Tiles of 128 rows and their p values cycle
- * through a 4-slot LDS ring: while tile i is summed, tiles i+1 and i+2 are in flight
- * and tile i+3 is issued into the slot of tile i-1. A loader wave waits (vmcnt) only
- * for the tile it is about to publish and then joins the barrier without a release
- * fence (a fence would wait for every load in flight). Products of 16 rows are formed
- * before their 16 adds, so no product waits in front of the chain. Loads are
- * unconditional: tile indexes are clamped to the last tile and rows to valid ones;
- * rows past the chain are never read back, columns past head_dim only feed discarded
- * lanes; every LDS write has landed before the workgroup ends. */
-constexpr int VT2 = 128;              /* rows per tile */
-constexpr int VNS = 4;                /* LDS ring slots: one summed, three in flight */
-constexpr int VLPT = 10;              /* loads per loader wave per tile: 8 x 1 KiB of V, 2 x 64 p */
-constexpr int VPS = VT2 + 4;          /* p row stride: the four heads' rows in different banks */
+ * one token t in one KV group g, for one 64-wide d chunk: one summing wave per head
+ * (lane = column d, one dependent add chain per lane), and eight loader waves.
+ *
+ * The chain's floor is the add latency (about 8 cycles a row); what a summing wave
+ * issues besides the add must fit beside it. So each lane reads its column four rows
+ * at a time (one 16-byte LDS read): the loaders store V tiles transposed, as 4-row
+ * blocks of [64 columns][4 rows] (+ 4 floats of padding, which puts the 64 lanes of
+ * every transposed store in 64 different banks). The p row of the head is read one
+ * value per lane per 16 rows and each row's p reaches all lanes by a DPP row broadcast
+ * folded into the product (v_mul_f32 with row_newbcast), so p costs no instruction.
+ *
+ * Loaders: 16-byte buffer loads of V rows into registers, three tiles in flight, then
+ * transposed 4-byte stores into one of two V slots; p goes straight from memory into a
+ * 4-slot LDS ring (LDS-direct). For a chain geometry row v of every token is cache
+ * slot v, so a tile's rows need no lookup, and the buffer's range check turns rows
+ * past the cache into zeros; a tree maps each row through the token's ancestor table
+ * (clamped to the token's rows). Rows past the token's chain are loaded but never
+ * summed. Tiles are published by a barrier after each loader's own stores landed
+ * (lgkmcnt(0)); loads in flight stay in flight across it. */
+constexpr int TV_ROWS = 128;            /* rows per tile */
+constexpr int TV_BQ = 260;              /* floats per 4-row block: [64 columns][4 rows] + 4 */
+constexpr int TV_PS = 4;                /* p ring slots */
+constexpr int TV_THREADS = 768;         /* 4 summing + 8 loader waves */
 
-__global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) float vt[VNS][VT2][64];
-    __shared__ __attribute__((aligned(16))) float pt[VNS][4][VPS];
+typedef unsigned int tv_u4 __attribute__((ext_vector_type(4)));
+
+/* x of lane J of this lane's 16-lane row (DPP row_newbcast) */
+template <int J>
+__device__ __forceinline__ float tv_bc(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + J, 0xF, 0xF, false));
+}
+
+/* 16 rows of the chain: P holds p of row j in lane j of each 16-lane row, V[k] rows
+ * 4k..4k+3 of this lane's column */
+__device__ __forceinline__ void tv_sum16(float &acc, float P, const float4 (&V)[4]) {
+    const float q0 = fmul(tv_bc<0>(P), V[0].x), q1 = fmul(tv_bc<1>(P), V[0].y);
+    const float q2 = fmul(tv_bc<2>(P), V[0].z), q3 = fmul(tv_bc<3>(P), V[0].w);
+    const float q4 = fmul(tv_bc<4>(P), V[1].x), q5 = fmul(tv_bc<5>(P), V[1].y);
+    const float q6 = fmul(tv_bc<6>(P), V[1].z), q7 = fmul(tv_bc<7>(P), V[1].w);
+    const float q8 = fmul(tv_bc<8>(P), V[2].x), q9 = fmul(tv_bc<9>(P), V[2].y);
+    const float q10 = fmul(tv_bc<10>(P), V[2].z), q11 = fmul(tv_bc<11>(P), V[2].w);
+    const float q12 = fmul(tv_bc<12>(P), V[3].x), q13 = fmul(tv_bc<13>(P), V[3].y);
+    const float q14 = fmul(tv_bc<14>(P), V[3].z), q15 = fmul(tv_bc<15>(P), V[3].w);
+    acc = fadd(acc, q0); acc = fadd(acc, q1); acc = fadd(acc, q2); acc = fadd(acc, q3);
+    acc = fadd(acc, q4); acc = fadd(acc, q5); acc = fadd(acc, q6); acc = fadd(acc, q7);
+    acc = fadd(acc, q8); acc = fadd(acc, q9); acc = fadd(acc, q10); acc = fadd(acc, q11);
+    acc = fadd(acc, q12); acc = fadd(acc, q13); acc = fadd(acc, q14); acc = fadd(acc, q15);
+}
+
+__global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) float vt[2][(TV_ROWS / 4) * TV_BQ];
+    __shared__ __attribute__((aligned(16))) float pt[TV_PS][4][TV_ROWS];
     __shared__ int anc_s[MAX_ANC];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
     const int nd = (hd + 63) / 64, qpt = (grp + 3) / 4;
@@ -345,100 +378,135 @@ __global__ __launch_bounds__(512) void k_attn_values(AttnArgs a) {
     const int g = b % Hkv;
     b /= Hkv;
     const int hq = b % qpt, t = b / qpt;
-    const int tid = threadIdx.x, wave = (tid >> 6) & 3, lane = tid & 63;
-    const bool loader = tid >= 256;
-    const int hh = hq * 4 + wave;
-    const bool live = hh < grp;
-    const int h = g * grp + (live ? hh : 0);
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int pos0 = a.g.pos0, dep = a.g.depth[t];
     const int nr = pos0 + dep + 1;
-    const int ntiles = (nr + VT2 - 1) / VT2, last = ntiles - 1;
-    for (int jj = tid; jj <= dep; jj += 512) anc_s[jj] = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + jj];
-    __syncthreads();
-    float acc = 0.0f;
-    if (loader) {
-        /* loader wave w: rows w*32 + 4k + lane/16 of each tile (k = 0..7), float4 column
-         * lane%16; its head's p (two 64-entry dword loads per tile) */
-        const int c4 = (lane & 15) * 4, rsub = lane >> 4;
-        const float *vcol = a.vc + (size_t)g * a.cap * hd + (dc * 64 + c4 < hd ? dc * 64 + c4 : 0);
-        const float *prow = a.S + ((size_t)t * a.H + h) * a.ldS;
-        auto issue = [&](int i) {
-            const int ti = i < last ? i : last, slot = i % VNS;
+    const int ntiles = (nr + TV_ROWS - 1) / TV_ROWS;
+    const bool chain = a.g.chain != 0;
+    if (!chain) {
+        for (int jj = tid; jj <= dep; jj += TV_THREADS) anc_s[jj] = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + jj];
+        __syncthreads();
+    }
+    if (wave >= 4) {
+        /* loader wave lw: rows 16 lw + lane % 16 of each tile, columns 16 cb + 4 (lane / 16)
+         * .. + 3 for cb = 0..3, and half lw % 2 of head lw / 2's p row */
+        const int lw = wave - 4, r = lane & 15, cg = lane >> 4, half = lw & 1;
+        const __amdgpu_buffer_rsrc_t vrs =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(a.vc + (size_t)g * a.cap * hd), 0, a.cap * hd * 4, 0x00020000);
+        int coff[4];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                int v = ti * VT2 + wave * 32 + 4 * k + rsub;
-                v = v < nr ? v : nr - 1;
-                const float *src = vcol + (size_t)(v < pos0 ? v : anc_s[v - pos0]) * hd;
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
-                                                 (__attribute__((address_space(3))) void *)&vt[slot][wave * 32 + 4 * k][0],
-                                                 16, 0, 0);
-            }
+        for (int cb = 0; cb < 4; cb++) {
+            const int col = dc * 64 + 16 * cb + 4 * cg;
+            coff[cb] = (col < hd ? col : 0) * 4;
+        }
+        const int phh = hq * 4 + (lw >> 1);
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(a.S + ((size_t)t * a.H + (size_t)g * grp + (phh < grp ? phh : 0)) * a.ldS), 0, a.ldS * 4, 0x00020000);
+        const int hd4 = hd * 4, roff = r * hd4;
+        /* word of (row 16 lw + r, column 16 cb + 4 cg + e): bank 16 lw + r + 16 cg + 4 e mod 64 */
+        const int wbase = (4 * lw + (r >> 2)) * TV_BQ + 16 * cg + (r & 3);
+        auto store = [&](int slot, const tv_u4 (&R)[4]) {
+            float *w = &vt[slot][wbase];
 #pragma unroll
-            for (int c = 0; c < 2; c++) {
-                int vp = ti * VT2 + c * 64 + lane;
-                vp = vp < nr ? vp : nr - 1;
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(prow + vp),
-                                                 (__attribute__((address_space(3))) void *)&pt[slot][wave][c * 64], 4,
-                                                 0, 0);
+            for (int cb = 0; cb < 4; cb++) {
+                w[64 * cb + 0] = __uint_as_float(R[cb].x);
+                w[64 * cb + 4] = __uint_as_float(R[cb].y);
+                w[64 * cb + 8] = __uint_as_float(R[cb].z);
+                w[64 * cb + 12] = __uint_as_float(R[cb].w);
             }
         };
-        issue(0);
-        issue(1);
-        issue(2);
-        for (int i = 0; i < ntiles; i++) {
-            /* tile i landed (tiles i+1, i+2 may be in flight); a bare barrier, so that no
-             * release fence waits for the loads still in flight */
-            HX_WAIT_VMCNT(2 * VLPT);
-            __builtin_amdgcn_s_barrier();
-            issue(i + 3);              /* into the slot of tile i - 1, summed before this barrier */
-        }
-        HX_WAIT_VMCNT(0);              /* no LDS write may land after the loop */
+        auto run = [&](auto chain_tag) {
+            constexpr bool CHAIN = decltype(chain_tag)::value;
+            auto load = [&](int i, tv_u4 (&R)[4]) {
+                const int vb = i * TV_ROWS;
+                if constexpr (CHAIN) {
+                    const int vo = roff + (vb + 16 * lw) * hd4;
+#pragma unroll
+                    for (int cb = 0; cb < 4; cb++) R[cb] = __builtin_amdgcn_raw_buffer_load_b128(vrs, vo + coff[cb], 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (__attribute__((address_space(3))) void *)&pt[i % TV_PS][lw >> 1][64 * half],
+                                                             4, (vb + 64 * half + lane) * 4, 0, 0, 0);
+                } else {
+                    int v = vb + 16 * lw + r;
+                    v = v < nr ? v : nr - 1;
+                    const int an = anc_s[v > pos0 ? v - pos0 : 0];
+                    const int srow = v < pos0 ? v : an;
+#pragma unroll
+                    for (int cb = 0; cb < 4; cb++) R[cb] = __builtin_amdgcn_raw_buffer_load_b128(vrs, srow * hd4 + coff[cb], 0, 0);
+                    int vp = vb + 64 * half + lane;
+                    vp = vp < nr ? vp : nr - 1;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (__attribute__((address_space(3))) void *)&pt[i % TV_PS][lw >> 1][64 * half],
+                                                             4, vp * 4, 0, 0, 0);
+                }
+            };
+            tv_u4 R0[4], R1[4], R2[4];
+            load(0, R0);
+            load(1, R1);
+            load(2, R2);
+            HX_WAIT_VMCNT(10);
+            store(0, R0);
+            /* step i: tile i is published; tile i + 3 is loaded into the registers tile i came
+             * from; tile i + 1 is stored into the slot tile i - 1 was summed from. The loop
+             * has no exit inside its body, so the compiler keeps the exact load counts. */
+#define TV_STEP(i_, RL, RW)                                                                 \
+            __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) only */                       \
+            __builtin_amdgcn_s_barrier();                                                   \
+            load((i_) + 3, RL);                                                             \
+            HX_WAIT_VMCNT(10);                                                              \
+            store(((i_) + 1) & 1, RW);
+            int i = 0;
+            for (; i + 3 <= ntiles; i += 3) {
+                TV_STEP(i, R0, R1)
+                TV_STEP(i + 1, R1, R2)
+                TV_STEP(i + 2, R2, R0)
+            }
+            if (i < ntiles) {
+                TV_STEP(i, R0, R1)
+                if (i + 1 < ntiles) {
+                    TV_STEP(i + 1, R1, R2)
+                }
+            }
+#undef TV_STEP
+        };
+        if (chain) run(std::true_type{});
+        else run(std::false_type{});
+        HX_WAIT_VMCNT(0);              /* no LDS write may land after the workgroup ends */
     } else {
-        /* summing wave w: heads hq * 4 + lane / 16, columns w * 16 + lane % 16 of the
-         * chunk -- the 16 lanes of a head read 64 bytes of each V row and the four heads
-         * share them (broadcast), a quarter of the LDS reads of one head per wave */
-        const float *const pw0 = pt[0][lane >> 4], *const vw0 = &vt[0][0][wave * 16 + (lane & 15)];
+        const int hh = hq * 4 + wave;
+        const bool live = hh < grp;
+        const int h = g * grp + (live ? hh : 0);
+        float acc = 0.0f;
         for (int i = 0; i < ntiles; i++) {
             __syncthreads();
-            const int slot = i % VNS, nv = nr - i * VT2;
-            const float *pw = pw0 + slot * (4 * VPS), *vw = vw0 + slot * (VT2 * 64);
-            if (nv >= VT2) {
-                float pA[16], vA[16], pB[16], vB[16];
-#define HX_GRD(P_, V_, c_)                                                               \
-                _Pragma("unroll") for (int j = 0; j < 16; j++) { P_[j] = pw[(c_) + j]; V_[j] = vw[((c_) + j) * 64]; }
-#define HX_GSUM(P_, V_)                                                                  \
-                {                                                                        \
-                    float pr[16];                                                        \
-                    _Pragma("unroll") for (int j = 0; j < 16; j++) pr[j] = fmul(P_[j], V_[j]); \
-                    _Pragma("unroll") for (int j = 0; j < 16; j++) acc = fadd(acc, pr[j]); \
-                }
-                HX_GRD(pA, vA, 0)
-                HX_GRD(pB, vB, 16) HX_GSUM(pA, vA)
-                HX_GRD(pA, vA, 32) HX_GSUM(pB, vB)
-                HX_GRD(pB, vB, 48) HX_GSUM(pA, vA)
-                HX_GRD(pA, vA, 64) HX_GSUM(pB, vB)
-                HX_GRD(pB, vB, 80) HX_GSUM(pA, vA)
-                HX_GRD(pA, vA, 96) HX_GSUM(pB, vB)
-                HX_GRD(pB, vB, 112) HX_GSUM(pA, vA)
-                HX_GSUM(pB, vB)
-#undef HX_GSUM
-#undef HX_GRD
+            const int slot = i & 1, nv = nr - i * TV_ROWS;
+            const float4 *vw = (const float4 *)&vt[slot][lane * 4];
+            if (nv >= TV_ROWS) {
+                const float *pw1 = &pt[i % TV_PS][wave][lane & 15];
+                float4 VA[4], VB[4];
+                float PA, PB;
+                /* one group of 16 rows is read while the previous one is summed; the
+                 * scheduling barriers keep the compiler from sinking the reads */
+#define TV_RD(V_, P_, g_) \
+                _Pragma("unroll") for (int j = 0; j < 4; j++) V_[j] = vw[((g_) * 4 + j) * (TV_BQ / 4)]; P_ = pw1[(g_) * 16];
+#define TV_SB __builtin_amdgcn_sched_barrier(0);
+                TV_RD(VA, PA, 0)
+                TV_RD(VB, PB, 1) TV_SB tv_sum16(acc, PA, VA); TV_SB
+                TV_RD(VA, PA, 2) TV_SB tv_sum16(acc, PB, VB); TV_SB
+                TV_RD(VB, PB, 3) TV_SB tv_sum16(acc, PA, VA); TV_SB
+                TV_RD(VA, PA, 4) TV_SB tv_sum16(acc, PB, VB); TV_SB
+                TV_RD(VB, PB, 5) TV_SB tv_sum16(acc, PA, VA); TV_SB
+                TV_RD(VA, PA, 6) TV_SB tv_sum16(acc, PB, VB); TV_SB
+                TV_RD(VB, PB, 7) TV_SB tv_sum16(acc, PA, VA); TV_SB
+                tv_sum16(acc, PB, VB);
+#undef TV_SB
+#undef TV_RD
             } else {
-                for (int r = 0; r < nv; r++) acc = fadd(acc, fmul(pw[r], vw[r * 64]));
+                const float *pv = &pt[i % TV_PS][wave][0];
+                for (int rr = 0; rr < nv; rr++) acc = fadd(acc, fmul(pv[rr], vt[slot][(rr >> 2) * TV_BQ + lane * 4 + (rr & 3)]));
             }
         }
-    }
-    /* every LDS-direct load has landed and every tile has been read: the sums go through
-     * LDS so that wave w writes (and quantizes) the 64 columns of head hq * 4 + w */
-    __syncthreads();
-    float *ot = &vt[0][0][0];   /* [4 heads][64 columns] */
-    if (!loader) ot[(lane >> 4) * 64 + wave * 16 + (lane & 15)] = acc;
-    __syncthreads();
-    if (!loader) {
-        const float x = ot[wave * 64 + lane];
         const int d = dc * 64 + lane;
-        if (live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = x;
-        if (a.qo_on && live) quant_block_wave(x, a.qo, a.qo_hm ? h * a.T + t : t, a.qo_hm ? dc : h * (hd >> 6) + dc);
+        if (live && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h * hd + d] = acc;
+        if (a.qo_on && live) quant_block_wave(acc, a.qo, a.qo_hm ? h * a.T + t : t, a.qo_hm ? dc : h * (hd >> 6) + dc);
     }
 }
 
@@ -473,7 +541,7 @@ void attention_finish(const AttnArgs &a, hipStream_t st) {
     const int grp = a.H / a.Hkv;
     k_attn_softmax<<<a.T * a.H, 256, 0, st>>>(a);
     const int nd = (a.hd + 63) / 64, qpt = (grp + 3) / 4;
-    k_attn_values<<<a.T * qpt * a.Hkv * nd, 512, 0, st>>>(a);
+    k_attn_values<<<a.T * qpt * a.Hkv * nd, TV_THREADS, 0, st>>>(a);
 }
 
 void attention(const AttnArgs &a, hipStream_t st) {
