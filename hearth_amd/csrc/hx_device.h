@@ -115,19 +115,20 @@ __device__ __forceinline__ V gload(const void *p) {
 
 /* exp in IEEE double from basic operations (Cody & Waite 1980 reduction with a
  * 32-bit ln2 head, degree-13 Taylor series on |r| <= ln2/2, exact power-of-two
- * scaling in two steps); the CPU restatement's ho_exp_port_d is the same function. */
+ * scaling); the CPU restatement's ho_exp_port_d is the same function.
+ * Written without branches (NaN, overflow and underflow are selected at the end, the
+ * arithmetic runs on 0 for them), so that independent calls interleave. */
 __device__ inline double exp_port_d(double x) {
     const double inv_ln2 = 1.44269504088896338700e+00;
     const double ln2_hi = 6.93147180369123816490e-01;
     const double ln2_lo = 1.90821492927058770002e-10;
     const double shifter = 6755399441055744.0;
-    if (x != x) return x;
-    if (x > 709.79) return __longlong_as_double(0x7ff0000000000000ll);
-    if (x < -745.2) return 0.0;
-    const double t = dmul(x, inv_ln2);
+    const bool nan = x != x, hi = x > 709.79, lo = x < -745.2;
+    const double xs = nan || hi || lo ? 0.0 : x;
+    const double t = dmul(xs, inv_ln2);
     const double nd = dsub(dadd(t, shifter), shifter);
-    const long long n = (long long)nd;
-    const double r = dsub(dsub(x, dmul(nd, ln2_hi)), dmul(nd, ln2_lo));
+    const int n = (int)nd;   /* |n| <= 1076 for the inputs that reach here */
+    const double r = dsub(dsub(xs, dmul(nd, ln2_hi)), dmul(nd, ln2_lo));
     double p = 1.0 / 6227020800.0;
     p = dadd(dmul(p, r), 1.0 / 479001600.0);
     p = dadd(dmul(p, r), 1.0 / 39916800.0);
@@ -142,9 +143,12 @@ __device__ inline double exp_port_d(double x) {
     p = dadd(dmul(p, r), 0.5);
     p = dadd(dmul(p, r), 1.0);
     p = dadd(dmul(p, r), 1.0);
-    const long long n1 = n < -1000 ? n + 600 : (n > 1000 ? n - 600 : n), n2 = n - n1;
-    const double s1 = __longlong_as_double((n1 + 1023) << 52), s2 = __longlong_as_double((n2 + 1023) << 52);
-    return dmul(dmul(p, s1), s2);
+    /* p * 2^n with one rounding: ldexp is exact for normal results and rounds subnormal
+     * ones once, as the two-step product by 2^n1 * 2^n2 (n1, n2 normal) does */
+    double y = __builtin_amdgcn_ldexp(p, n);
+    y = lo ? 0.0 : y;
+    y = hi ? __longlong_as_double(0x7ff0000000000000ll) : y;
+    return nan ? x : y;
 }
 
 __device__ __forceinline__ float exp_port_f(float x) { return __double2float_rn(exp_port_d((double)x)); }

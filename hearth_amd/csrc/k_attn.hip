@@ -213,22 +213,22 @@ __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
 
 __device__ __forceinline__ float sum16_lds(const float *es, int n, int lane16, float L) {
     /* lane lane16 of 16: continues the sequential sum L with es[lane16], es[lane16 + 16],
-     * ..., the next 8 operands read while the current 8 are added */
+     * ..., the next 16 operands read while the current 16 are added */
     int i = lane16;
-    float cur[8], nxt[8];
-    const int full = n >= 16 * 8 ? (n - lane16) / 128 : 0;   /* groups of 8 in range */
+    float cur[16], nxt[16];
+    const int full = n >= 16 * 16 ? (n - lane16) / 256 : 0;   /* groups of 16 in range */
     if (full > 0) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) cur[u] = es[i + 16 * u];
+        for (int u = 0; u < 16; u++) cur[u] = es[i + 16 * u];
         for (int gi = 0; gi < full; gi++) {
-            const int inx = gi + 1 < full ? i + 128 : i;
+            const int inx = gi + 1 < full ? i + 256 : i;
 #pragma unroll
-            for (int u = 0; u < 8; u++) nxt[u] = es[inx + 16 * u];
+            for (int u = 0; u < 16; u++) nxt[u] = es[inx + 16 * u];
 #pragma unroll
-            for (int u = 0; u < 8; u++) L = fadd(L, cur[u]);
+            for (int u = 0; u < 16; u++) L = fadd(L, cur[u]);
 #pragma unroll
-            for (int u = 0; u < 8; u++) cur[u] = nxt[u];
-            i += 128;
+            for (int u = 0; u < 16; u++) cur[u] = nxt[u];
+            i += 256;
         }
     }
     for (; i < n; i += 16) L = fadd(L, es[i]);
@@ -237,32 +237,36 @@ __device__ __forceinline__ float sum16_lds(const float *es, int n, int lane16, f
 
 /* softmax over one (token, head) row of scores, in place (quant.c:634-642): running
  * max from s[0] (a NaN s[0] stays the max, later NaNs are skipped), e = exp(s - max),
- * sum16 of e, p = e / sum. Up to 8192 scores stay in registers; longer rows are
- * processed in chunks of 8192 re-read from the row. */
-constexpr int SM_PER = 32;
-constexpr int SM_CH = 256 * SM_PER;
+ * sum16 of e, p = e / sum. Up to 8192 scores stay in registers (16 per thread); their
+ * exps are computed four at a time (exp_port_d has no branches, so the four
+ * double-precision chains interleave). Longer rows are processed in chunks of 8192
+ * re-read from the row. */
+constexpr int SM_T = 512;
+constexpr int SM_PER = 16;
+constexpr int SM_CH = SM_T * SM_PER;
 
-__global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
+__global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
     __shared__ float es[SM_CH];
-    __shared__ float red[4];
+    __shared__ float red[SM_T / 64];
     __shared__ float sum_sh;
     const int t = blockIdx.x / a.H, h = blockIdx.x % a.H, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nr = a.g.pos0 + a.g.depth[t] + 1;
     float *s = a.S + ((size_t)t * a.H + h) * a.ldS;
     const bool inreg = nr <= SM_CH;
+    const int nu = (nr + SM_T - 1) / SM_T;   /* register entries in use (when inreg) */
     float x[SM_PER];
     float m = -__builtin_huge_valf();
     if (inreg) {
 #pragma unroll
         for (int u = 0; u < SM_PER; u++) {
-            const int i = tid + 256 * u;
+            const int i = tid + SM_T * u;
             x[u] = i < nr ? s[i] : -__builtin_huge_valf();
         }
 #pragma unroll
         for (int u = 0; u < SM_PER; u++)
             if (x[u] == x[u]) m = fmaxf(m, x[u]);
     } else {
-        for (int i = tid; i < nr; i += 256) {
+        for (int i = tid; i < nr; i += SM_T) {
             const float v = s[i];
             if (v == v) m = fmaxf(m, v);
         }
@@ -271,7 +275,8 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if (lane == 0) red[wave] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+#pragma unroll
+    for (int w = 0; w < SM_T / 64; w++) m = fmaxf(m, red[w]);
     const float s0 = s[0];
     if (s0 != s0) m = s0;
     float L = 0.0f;   /* lane tid < 16: partial of the elements i = tid (mod 16) */
@@ -279,23 +284,30 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
         const int n = nr - c0 < SM_CH ? nr - c0 : SM_CH;
         if (c0) __syncthreads();
         if (inreg) {
+            /* entries past the row hold -inf; their exps are never stored or used */
 #pragma unroll
-            for (int u = 0; u < SM_PER; u++) {
-                const int i = tid + 256 * u;
-                if (i < n) {
-                    x[u] = exp_port_f(fadd(x[u], -m));
-                    es[i] = x[u];
+            for (int u0 = 0; u0 < SM_PER; u0 += 4) {
+                if (u0 < nu) {
+                    float e[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) e[k] = exp_port_f(fadd(x[u0 + k], -m));
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        x[u0 + k] = e[k];
+                        const int i = tid + SM_T * (u0 + k);
+                        if (i < n) es[i] = e[k];
+                    }
                 }
             }
         } else {
-            for (int i = tid; i < n; i += 256) es[i] = exp_port_f(fadd(s[c0 + i], -m));
+            for (int i = tid; i < n; i += SM_T) es[i] = exp_port_f(fadd(s[c0 + i], -m));
         }
         __syncthreads();
         /* SM_CH is a multiple of 16, so element c0 + i keeps lane (c0 + i) % 16 = i % 16 */
         if (tid < 16) L = sum16_lds(es, n, tid, L);
         if (!inreg) {
             __syncthreads();
-            for (int i = tid; i < n; i += 256) s[c0 + i] = es[i];
+            for (int i = tid; i < n; i += SM_T) s[c0 + i] = es[i];
         }
     }
     if (tid < 16) {
@@ -308,11 +320,11 @@ __global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
     if (inreg) {
 #pragma unroll
         for (int u = 0; u < SM_PER; u++) {
-            const int i = tid + 256 * u;
+            const int i = tid + SM_T * u;
             if (i < nr) s[i] = fdiv(x[u], sum);
         }
     } else {
-        for (int i = tid; i < nr; i += 256) s[i] = fdiv(s[i], sum);
+        for (int i = tid; i < nr; i += SM_T) s[i] = fdiv(s[i], sum);
     }
 }
 
@@ -539,7 +551,7 @@ void attention_scores(const AttnArgs &a, hipStream_t st) {
 
 void attention_finish(const AttnArgs &a, hipStream_t st) {
     const int grp = a.H / a.Hkv;
-    k_attn_softmax<<<a.T * a.H, 256, 0, st>>>(a);
+    k_attn_softmax<<<a.T * a.H, SM_T, 0, st>>>(a);
     const int nd = (a.hd + 63) / 64, qpt = (grp + 3) / 4;
     k_attn_values<<<a.T * qpt * a.Hkv * nd, TV_THREADS, 0, st>>>(a);
 }

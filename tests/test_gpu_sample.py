@@ -5,7 +5,8 @@ pins to the reference's own Sampler / accept_point_mass outputs.
 - the device distributions equal the restatement's float64 rows bit for bit, over
   temperature, top-k, top-p (including rows flat enough that the top-p candidates
   exceed the LDS sort and go through the global sort), min-p, the repetition penalty
-  with a per-node context, ties, -inf entries and vocabularies from 7 to 151936;
+  with a per-node context, ties, -inf entries, exp arguments down to -760 (subnormal
+  and underflowing doubles) and vocabularies from 7 to 151936;
 - acceptance (path and final token) equals the restatement's on random chains and
   trees, point-mass and general draft distributions, including uniforms placed exactly
   on the acceptance boundary (a 1-ulp difference in p[x] would flip the decision);
@@ -55,6 +56,12 @@ def _rows(rng, kind, n, V):
         return np.full((n, V), 0.25, dtype=np.float32)
     if kind == "flat":
         return rng.normal(0, 0.01, (n, V)).astype(np.float32)
+    if kind == "wide":   # exp arguments down to -760: subnormal and underflowing doubles
+        x = rng.uniform(-760.0, 0.0, (n, V)).astype(np.float32)
+        x[:, 0] = 0.0
+        edge = np.float32([-700, -708.5, -709.9, -720, -730, -744.4, -745.1, -745.3])[:V - 1]
+        x[:, 1:1 + edge.size] = edge
+        return x
     x = rng.normal(0, 1, (n, V)).astype(np.float32)
     x[:, V // 3] = 20.0
     return x
@@ -76,7 +83,7 @@ def _check_probs(rows, tokens, st, ctx):
 @pytest.mark.parametrize("V", [7, 300, 4096, 8193, 20000])
 def test_gpu_probs_bit_exact(V):
     rng = np.random.default_rng(V)
-    for kind in ["normal1", "normal4", "ties", "neginf", "equal", "flat", "peaked"]:
+    for kind in ["normal1", "normal4", "ties", "neginf", "equal", "flat", "peaked", "wide"]:
         for st in SETTINGS:
             rows = _rows(rng, kind, 3, V)
             tokens = rng.integers(0, V, 3).astype(np.int32)
