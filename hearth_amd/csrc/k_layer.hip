@@ -76,19 +76,30 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
         }
         if (a.mode != 4) h[i] = v;
         hs[i] = v;
+        hs[D + i] = fmul(v, v);   /* the products of dot16(x, x), formed in parallel */
     }
     __syncthreads();
     if (tid < 16) {
+        /* lane tid: the sequential sum of the products of elements tid, tid + 16, ... */
         float L = 0.0f;
         int i = tid;
-        for (; i + 112 < D; i += 128) {
-            float e[8];
+        float cur[16], nxt[16];
+        const int full = D >= 256 ? (D - tid) / 256 : 0;
+        if (full > 0) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) e[u] = hs[i + 16 * u];
+            for (int u = 0; u < 16; u++) cur[u] = hs[D + i + 16 * u];
+            for (int gi = 0; gi < full; gi++) {
+                const int inx = gi + 1 < full ? i + 256 : i;
 #pragma unroll
-            for (int u = 0; u < 8; u++) L = fadd(L, fmul(e[u], e[u]));
+                for (int u = 0; u < 16; u++) nxt[u] = hs[D + inx + 16 * u];
+#pragma unroll
+                for (int u = 0; u < 16; u++) L = fadd(L, cur[u]);
+#pragma unroll
+                for (int u = 0; u < 16; u++) cur[u] = nxt[u];
+                i += 256;
+            }
         }
-        for (; i < D; i += 16) L = fadd(L, fmul(hs[i], hs[i]));
+        for (; i < D; i += 16) L = fadd(L, hs[D + i]);
         L = tree16(L);
         if (tid == 0) {
             const float ms = fdiv(L, (float)D);
@@ -735,7 +746,7 @@ void route(const RouteArgs &a, hipStream_t st) {
 void norm(const NormArgs &a, hipStream_t st) {
     int nth = ((a.D / 2 + 63) / 64) * 64;
     nth = nth < 64 ? 64 : (nth > 1024 ? 1024 : nth);
-    k_norm<<<a.T, nth, (size_t)a.D * sizeof(float), st>>>(a);
+    k_norm<<<a.T, nth, (size_t)a.D * 2 * sizeof(float), st>>>(a);
 }
 
 void swiglu_quant(float *g, const float *u, int T, int F, const Act &a, hipStream_t st) {
