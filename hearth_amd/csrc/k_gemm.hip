@@ -174,7 +174,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs args) {
  * barrier one thread per (row, token) folds the terms of blocks 0, 1, ... in order, so
  * the result is the one-lane fold bit for bit. */
 constexpr int SK_MAXP = 4;      /* block pairs per wave */
-constexpr int TK_WAVES = 4;     /* waves per workgroup of the split-K gate/up kernel */
+constexpr int TK_WAVES_GATEUP = 8;   /* waves per workgroup of k_expert_tk: gate/up (token blocks staged once for 8 waves) */
+constexpr int TK_WAVES_DOWN = 4;     /* and down (more, smaller workgroups over the shorter rows) */
 constexpr size_t TK_LDS_MAX = 65536;
 constexpr int TK_CHUNK_ROWS = 128;   /* rows of a slot kept on one XCD (two 128-byte scale lines) */
 constexpr int SK_LDS = 65536;   /* bytes of terms per workgroup */
@@ -733,7 +734,8 @@ bool launch_tk(const MoeArgs &a, int mode, int n_slots, hipStream_t st, hipEvent
     const int nb = (K + 63) / 64, nbp = (nb + 1) & ~1, npair = nbp / 2;
     const int NP = q4 ? TkCfg<4>::NP : TkCfg<3>::NP, NM = down ? 1 : 2;
     const int S = (npair + NP - 1) / NP;
-    const int rpw = S < TK_WAVES ? TK_WAVES / S : 1, W = rpw * S;
+    const int waves = down ? TK_WAVES_DOWN : TK_WAVES_GATEUP;
+    const int rpw = S < waves ? waves / S : 1, W = rpw * S;
     const size_t lds = tk_lds_bytes(nbp, NM, NP, rpw, S);
     if (W > 8 || lds > TK_LDS_MAX) return false;
     const int tpw = ((rows + 15) / 16 + rpw - 1) / rpw;
