@@ -859,8 +859,9 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 m.pair_tok = pair_tok; m.x = ax; m.mid = amid; m.midf = midf; m.Y = Y; m.T = T; m.F = F; m.D = D;
                 m.P = T * K; m.dtype_mask = w.dtype_mask;
                 const int slots = std::min(E, T * K);
-                timed_dispatch(&ks.expert_s, [&](hipEvent_t e0, hipEvent_t e1) { hxl::expert_gateup(m, slots, st, e0, e1); }, 1);
-                timed(&ks.expert_down_s, [&] { hxl::expert_down(m, slots, st); }, 1);
+                bool mid_done = false;
+                timed_dispatch(&ks.expert_s, [&](hipEvent_t e0, hipEvent_t e1) { mid_done = hxl::expert_gateup(m, slots, st, e0, e1); }, 1);
+                timed(&ks.expert_down_s, [&] { hxl::expert_down(m, slots, st, mid_done); }, 1);
             }
             if (profiling) ks.expert_launches++;
             if (Fs && pf != 2) shared_expert();

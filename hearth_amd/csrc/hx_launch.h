@@ -224,8 +224,8 @@ using namespace hxd;
 void repack(const uint8_t *src_dev, int r0, int count, const QMat &m, hipStream_t st);
 void quant_rows(const float *x, int64_t ldx, int T, int nb, const Act &a, hipStream_t st);
 void gemm(const GemmArgs &a, hipStream_t st);
-void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
-void expert_down(const MoeArgs &a, int n_slots, hipStream_t st);
+bool expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+void expert_down(const MoeArgs &a, int n_slots, hipStream_t st, bool mid_done = false);
 /* the down kernel alone on already quantized pair activations (a.mid) */
 void expert_down_q(const MoeArgs &a, int n_slots, hipStream_t st);
 /* MLA: latent post step, absorbed queries, RoPE score term, output gather */

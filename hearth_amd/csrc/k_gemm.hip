@@ -535,17 +535,20 @@ __host__ __device__ inline int tk_chunk(int rpw) {
     return 16 * rpw >= 64 ? 1 : TK_CHUNK_ROWS / (16 * rpw);
 }
 
-/* LDS bytes of one workgroup */
-__host__ __device__ inline size_t tk_lds_bytes(int nbp, int nm, int np, int rpw, int S) {
+/* LDS bytes of one workgroup (qf: plus the SwiGLU rows [4 tokens][16 rpw] it quantizes) */
+__host__ __device__ inline size_t tk_lds_bytes(int nbp, int nm, int np, int rpw, int S, bool qf = false) {
     const int nbp4 = (nbp + 3) & ~3;
-    return (size_t)nbp * 1024 + (size_t)nbp4 * 128 + (size_t)rpw * S * nm * 2 * np * 32 + (size_t)rpw * nm * 64 * 4;
+    return (size_t)nbp * 1024 + (size_t)nbp4 * 128 + (size_t)rpw * S * nm * 2 * np * 32 + (size_t)rpw * nm * 64 * 4 +
+           (qf ? (size_t)4 * 16 * rpw * 4 : 0);
 }
 
-enum { TK_GATEUP = 0, TK_DOWN = 1 };
+/* TK_GATEUP_Q: gate/up whose workgroups cover whole 64-row blocks of the SwiGLU rows
+ * (4 or 8 row tiles) and quantize them (NUMERICS §2) in the epilogue */
+enum { TK_GATEUP = 0, TK_DOWN = 1, TK_GATEUP_Q = 2 };
 
 template <int DT, int MODE>
 __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, int gmax, int n_slots) {
-    constexpr bool DOWN = MODE != TK_GATEUP;
+    constexpr bool DOWN = MODE == TK_DOWN, QF = MODE == TK_GATEUP_Q;
     extern __shared__ __attribute__((aligned(16))) uint8_t tk_lds[];
     constexpr int NP = TkCfg<DT>::NP, NV = TkCfg<DT>::NV, NBK = 2 * NP, NM = DOWN ? 1 : 2;
     const int rows_out = DOWN ? a.D : a.F;
@@ -593,13 +596,14 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
     float *dxs = (float *)(xs + (size_t)nbp * 1024);        /* [nbp4][16 tokens] */
     int *sxs = (int *)(dxs + nbp4 * 16);                    /* [nbp4][16 tokens] */
     uint8_t *scl = (uint8_t *)(sxs + nbp4 * 16) + wave * NM * NBK * 32;   /* [NM][NBK][16 halves] */
-    float *relay = (float *)((uint8_t *)(sxs + nbp4 * 16) + W * NM * NBK * 32) + rtl * NM * 64;
+    float *const relay0 = (float *)((uint8_t *)(sxs + nbp4 * 16) + W * NM * NBK * 32);   /* [rpw][NM][64] */
+    float *relay = relay0 + rtl * NM * 64;
     /* issue order: the token rows, the weights (straight-line loads), then the
      * LDS-direct loads that need the token rows. The q loads cover token lane / 4,
      * k-group lane % 4 of a block; the d and s loads token lane % 16 of four blocks. */
     const int tq = (lane >> 2) < n ? (lane >> 2) : n - 1, tds = lr < n ? lr : n - 1;
-    const int arow_q = MODE == TK_GATEUP ? a.pair_tok[p0 + tq] : p0 + tq;
-    const int arow_d = MODE == TK_GATEUP ? a.pair_tok[p0 + tds] : p0 + tds;
+    const int arow_q = !DOWN ? a.pair_tok[p0 + tq] : p0 + tq;
+    const int arow_d = !DOWN ? a.pair_tok[p0 + tds] : p0 + tds;
     v4i w[NM][NP][NV];
 #pragma unroll
     for (int k = 0; k < NP; k++) {
@@ -713,31 +717,51 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
         }
         __syncthreads();   /* the relay slot is read before the next stage writes it */
     }
-    if (part != S - 1 || !live || col >= n) return;
     const int row = rt * 16 + 4 * kg + q;
+    const bool out = part == S - 1 && live && col < n;
     if (DOWN) {
-        if (row < mat[0].rows) a.Y[(size_t)(p0 + col) * a.D + row] = canon(acc[0]);
-    } else {
+        if (out && row < mat[0].rows) a.Y[(size_t)(p0 + col) * a.D + row] = canon(acc[0]);
+        return;
+    }
+    float mv = 0.0f;
+    if (out) {
         const float gv = canon(acc[0]), uv = canon(acc[NM - 1]);
         const float sg = fdiv(gv, fadd(1.0f, exp_port_f(-gv)));
-        a.midf[(size_t)(p0 + col) * a.F + row] = fmul(sg, uv);
+        mv = fmul(sg, uv);
+        if (!QF) a.midf[(size_t)(p0 + col) * a.F + row] = mv;
+    }
+    if constexpr (QF) {
+        /* the workgroup's rows [16 rpw tile, +16 rpw) are whole blocks of F: the last
+         * parts put them in LDS by (token, row), then wave j quantizes block j / 4 of
+         * token 4 g + j % 4 -- the values k_quant_rows would read from midf */
+        const int nr = 16 * rpw;
+        float *qb = relay0 + rpw * NM * 64;   /* [4 tokens][16 rpw], after the relay slots */
+        if (part == S - 1) qb[(lr & 3) * nr + rtl * 16 + 4 * kg + q] = mv;
+        __syncthreads();
+        if (wave < rpw) {
+            const int tt = wave & 3, bb = wave >> 2, tcol = 4 * g + tt;
+            if (tcol < n) quant_block_wave(qb[tt * nr + bb * 64 + lane], a.mid, p0 + tcol, (tile * nr) / 64 + bb);
+        }
     }
 }
 
 /* launches k_expert_tk for experts of at most 16 tokens and one dtype; false when the
  * shape does not fit (the caller uses the general kernels) */
-bool launch_tk(const MoeArgs &a, int mode, int n_slots, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    const bool down = mode != TK_GATEUP;
+int launch_tk(const MoeArgs &a, int mode, int n_slots, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    const bool down = mode == TK_DOWN;
     const bool q4 = a.dtype_mask & (1 << 4), q8 = a.dtype_mask & (1 << 3);
-    if (a.T > 16 || q4 == q8) return false;
+    if (a.T > 16 || q4 == q8) return 0;
     const int K = down ? a.F : a.D, rows = down ? a.D : a.F;
     const int nb = (K + 63) / 64, nbp = (nb + 1) & ~1, npair = nbp / 2;
     const int NP = q4 ? TkCfg<4>::NP : TkCfg<3>::NP, NM = down ? 1 : 2;
     const int S = (npair + NP - 1) / NP;
     const int waves = down ? TK_WAVES_DOWN : TK_WAVES_GATEUP;
     const int rpw = S < waves ? waves / S : 1, W = rpw * S;
-    const size_t lds = tk_lds_bytes(nbp, NM, NP, rpw, S);
-    if (W > 8 || lds > TK_LDS_MAX) return false;
+    /* gate/up workgroups of 4 or 8 row tiles cover whole blocks of the SwiGLU rows: they
+     * quantize them too (F a multiple of 128, so the blocks need no padding block) */
+    const bool qf = mode == TK_GATEUP && a.mid.q && a.F % 128 == 0 && (rpw == 4 || rpw == 8) && a.mid.nbp == a.F / 64;
+    const size_t lds = tk_lds_bytes(nbp, NM, NP, rpw, S, qf);
+    if (W > 8 || lds > TK_LDS_MAX) return 0;
     const int tpw = ((rows + 15) / 16 + rpw - 1) / rpw;
     const int gmax = (a.T + 3) / 4;   /* tokens per slot <= T */
     const int ch = tk_chunk(rpw);
@@ -745,10 +769,13 @@ bool launch_tk(const MoeArgs &a, int mode, int n_slots, hipStream_t st, hipEvent
     const dim3 grid(8 * ((chunks + 7) / 8) * ch * gmax), block(64 * W);
 #define TK_LAUNCH(DT_, MODE_) \
     hipExtLaunchKernelGGL(k_expert_tk<DT_, MODE_>, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, a, rpw, S, gmax, n_slots)
-    if (mode == TK_GATEUP) { if (q4) TK_LAUNCH(4, TK_GATEUP); else TK_LAUNCH(3, TK_GATEUP); }
+    if (mode == TK_GATEUP) {
+        if (qf) { if (q4) TK_LAUNCH(4, TK_GATEUP_Q); else TK_LAUNCH(3, TK_GATEUP_Q); }
+        else { if (q4) TK_LAUNCH(4, TK_GATEUP); else TK_LAUNCH(3, TK_GATEUP); }
+    }
     if (mode == TK_DOWN) { if (q4) TK_LAUNCH(4, TK_DOWN); else TK_LAUNCH(3, TK_DOWN); }
 #undef TK_LAUNCH
-    return true;
+    return qf ? 2 : 1;
 }
 
 /* down projection of one 16-row D tile of one active expert for its n tokens. */
@@ -983,9 +1010,10 @@ void gemm(const GemmArgs &in, hipStream_t st) {
     }
 }
 
-/* gate/up (split-K, one launch per expert dtype present) */
-void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    if (n_slots <= 0) return;
+/* gate/up (split-K, one launch per expert dtype present); true when the launch also
+ * quantized the SwiGLU rows into a.mid */
+bool expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    if (n_slots <= 0) return false;
     const int nb = (a.D + 63) / 64, nbp = (nb + 1) & ~1;
     const int ntok = sk_ntok(a.T, 2, nb);
     const int threads = 64 * sk_waves(nbp / 2);
@@ -995,7 +1023,7 @@ void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0
      * first launch, ev1 at the end of the last */
     const bool q4 = a.dtype_mask & (1 << 4), q8 = a.dtype_mask & (1 << 3);
     /* at most 16 tokens per expert, one dtype: the split-K kernel (one term per lane) */
-    if (launch_tk(a, TK_GATEUP, n_slots, st, ev0, ev1)) return;
+    if (const int r = launch_tk(a, TK_GATEUP, n_slots, st, ev0, ev1)) return r == 2;
     /* few tokens, one dtype, one pair chunk per wave: the persistent kernel (two
      * workgroups per CU on every CU) */
     const int npair = nbp / 2, W = threads / 64;
@@ -1004,18 +1032,20 @@ void expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0
         const int pgrid = grid < 2 * ncu ? grid : 2 * ncu;
         if (q4) hipExtLaunchKernelGGL(k_expert_gateup_pp<4>, dim3(pgrid), dim3(threads), (uint32_t)lds, st, ev0, ev1, 0u, a, ntok);
         else hipExtLaunchKernelGGL(k_expert_gateup_pp<3>, dim3(pgrid), dim3(threads), (uint32_t)lds, st, ev0, ev1, 0u, a, ntok);
-        return;
+        return false;
     }
     if (q4) hipExtLaunchKernelGGL(k_expert_gateup_sk<4>, dim3(grid), dim3(threads), (uint32_t)lds, st, ev0,
                                   q8 ? nullptr : ev1, 0u, a, ntok);
     if (q8) hipExtLaunchKernelGGL(k_expert_gateup_sk<3>, dim3(grid), dim3(threads), (uint32_t)lds, st,
                                   q4 ? nullptr : ev0, ev1, 0u, a, ntok);
+    return false;
 }
 
-/* NUMERICS §2 of the SwiGLU rows of all T * top_k pairs, then the down projections */
-void expert_down(const MoeArgs &a, int n_slots, hipStream_t st) {
+/* NUMERICS §2 of the SwiGLU rows of all T * top_k pairs (unless the gate/up launch did
+ * it: mid_done), then the down projections */
+void expert_down(const MoeArgs &a, int n_slots, hipStream_t st, bool mid_done) {
     if (n_slots <= 0) return;
-    quant_rows(a.midf, a.F, a.P, a.F / 64, a.mid, st);
+    if (!mid_done) quant_rows(a.midf, a.F, a.P, a.F / 64, a.mid, st);
     expert_down_q(a, n_slots, st);
 }
 
