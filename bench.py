@@ -16,7 +16,8 @@ acceptance on the GPU, commit; generate.py:365-392 of the reference):
 value = accepted tokens / s = sum over steps of (accepted drafts + 1) / wall time of the
 steps (inputs already resident in HBM; each step returns its result to the host).
 
-roofline: the grouped Q4 expert gate/up kernel (k_expert_tk<4, false>), timed with HIP
+roofline: the grouped Q4 expert gate/up kernel (k_expert_tk<4, TK_GATEUP_Q>: gate and up,
+SwiGLU and the act-quant of its rows; k_expert_tk<4, 2> in rocprofv3 traces), timed with HIP
 event pairs recorded on the engine's stream around each of its launches during the
 timed steps; achieved = its algorithmic bytes (distinct experts routed in the layer x
 1,671,168 B of Q4 gate+up rows each) / its summed launch durations. A second pass over
@@ -307,7 +308,7 @@ def main(argv=None) -> int:
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "traffic_source": str(TRAFFIC_PROFILE.relative_to(ROOT)),
-                     "kernel": "k_expert_tk<4, false> (grouped Q4 expert gate+up)",
+                     "kernel": "k_expert_tk<4, TK_GATEUP_Q> (grouped Q4 expert gate+up, SwiGLU, act-quant)",
                      "bytes_per_launch": int(kx["expert_bytes"] / n_launch),
                      "us_per_launch": round(kx["expert_s"] / n_launch * 1e6, 3),
                      "down_projection_gbs": round(dn_gbs, 1)},
