@@ -159,6 +159,49 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+/* DPP helpers (gfx9 row_shr / row_bcast controls). A row is 16 lanes. */
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ unsigned dpp_u32(unsigned old, unsigned v) {
+    return (unsigned)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWMASK, 0xF, false);
+}
+
+/* maximum of a 64-bit key over the wave, in every lane: row_shr 1, 2, 4, 8 give lane 15 of
+ * each row its row's maximum, row_bcast 15 / 31 carry rows 0 and 2 into rows 1 and 3 and
+ * rows 0-1 into 2-3, lane 63 ends with the total, which is read back to all lanes. Lanes
+ * whose source is outside the row keep their own key. VALU steps only (no LDS). */
+__device__ inline unsigned long long wave_max_u64(unsigned long long k) {
+    unsigned lo = (unsigned)k, hi = (unsigned)(k >> 32);
+#define HX_MAX_STEP(CTRL, RM)                                                                  \
+    {                                                                                          \
+        const unsigned olo = dpp_u32<CTRL, RM>(lo, lo), ohi = dpp_u32<CTRL, RM>(hi, hi);       \
+        const unsigned long long o = ((unsigned long long)ohi << 32) | olo;                    \
+        const unsigned long long c = ((unsigned long long)hi << 32) | lo;                      \
+        if (o > c) { lo = olo; hi = ohi; }                                                     \
+    }
+    HX_MAX_STEP(0x111, 0xF)
+    HX_MAX_STEP(0x112, 0xF)
+    HX_MAX_STEP(0x114, 0xF)
+    HX_MAX_STEP(0x118, 0xF)
+    HX_MAX_STEP(0x142, 0xA)
+    HX_MAX_STEP(0x143, 0xC)
+#undef HX_MAX_STEP
+    lo = (unsigned)__builtin_amdgcn_readlane((int)lo, 63);
+    hi = (unsigned)__builtin_amdgcn_readlane((int)hi, 63);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+/* inclusive prefix sum of an int over the wave (lane order), by the same DPP steps; lanes
+ * whose source is outside the row (or whose row is not selected) add 0 */
+__device__ inline int wave_scan_incl(int v) {
+    v += (int)dpp_u32<0x111, 0xF>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x112, 0xF>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x114, 0xF>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x118, 0xF>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x142, 0xA>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x143, 0xC>(0u, (unsigned)v);
+    return v;
+}
+
 /* 16-lane canonical tree (NUMERICS §1) of the partials held by lanes 0..15 of a
  * 16-lane segment: returns the total in lane 0 of the segment. */
 __device__ __forceinline__ float tree16(float L) {

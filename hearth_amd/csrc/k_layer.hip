@@ -374,12 +374,7 @@ __device__ void bucket_pairs(const RouteArgs &a, const int *ids, int *cnt, int *
         for (int e0 = 0; e0 < E; e0 += 64) {
             const int e = e0 + tid;
             const int c = e < E ? cnt[e] : 0, act = c > 0;
-            int inc = c, ninc = act;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int y = __shfl_up(inc, off, 64), ny = __shfl_up(ninc, off, 64);
-                if (tid >= off) { inc += y; ninc += ny; }
-            }
+            const int inc = wave_scan_incl(c), ninc = wave_scan_incl(act);
             const int pos = run + inc - c, slot = nu_run + ninc - act;
             if (e < E) {
                 base[e] = pos;
@@ -496,11 +491,7 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
             unsigned long long m = 0ull;
 #pragma unroll
             for (int u = 0; u < RS_EMAX / 64; u++) m = kk[u] > m ? kk[u] : m;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const unsigned long long o = __shfl_xor(m, off, 64);
-                m = o > m ? o : m;
-            }
+            m = wave_max_u64(m);   /* keys are unique: any reduction order gives the same maximum */
             const int e = (int)(0xFFFFFFFFu - (uint32_t)m);
 #pragma unroll
             for (int u = 0; u < RS_EMAX / 64; u++)
