@@ -190,6 +190,31 @@ __device__ inline unsigned long long wave_max_u64(unsigned long long k) {
     return ((unsigned long long)hi << 32) | lo;
 }
 
+/* maximum of a non-negative float (NaN-free) and sum of an int over the wave, in every
+ * lane, by the same DPP steps (both exact whatever the order) */
+__device__ inline float wave_max_f32(float x) {
+    unsigned v = __float_as_uint(x);
+#define HX_FMAX_STEP(CTRL, RM) v = __float_as_uint(fmaxf(__uint_as_float(v), __uint_as_float(dpp_u32<CTRL, RM>(v, v))));
+    HX_FMAX_STEP(0x111, 0xF)
+    HX_FMAX_STEP(0x112, 0xF)
+    HX_FMAX_STEP(0x114, 0xF)
+    HX_FMAX_STEP(0x118, 0xF)
+    HX_FMAX_STEP(0x142, 0xA)
+    HX_FMAX_STEP(0x143, 0xC)
+#undef HX_FMAX_STEP
+    return __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)v, 63));
+}
+
+__device__ inline int wave_sum_i32(int v) {
+    v += (int)dpp_u32<0x111, 0xF>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x112, 0xF>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x114, 0xF>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x118, 0xF>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x142, 0xA>(0u, (unsigned)v);
+    v += (int)dpp_u32<0x143, 0xC>(0u, (unsigned)v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 /* inclusive prefix sum of an int over the wave (lane order), by the same DPP steps; lanes
  * whose source is outside the row (or whose row is not selected) add 0 */
 __device__ inline int wave_scan_incl(int v) {
@@ -239,8 +264,7 @@ __device__ __forceinline__ int kperm_pos(int e) {
 __device__ inline void quant_block_vals(float x, int &q, float &d, int &sum) {
     float ax = fabsf(x);
     ax = ax == ax ? ax : 0.0f;                    /* NaN never wins the max */
-    float amax = ax;
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float amax = wave_max_f32(ax);
     d = fdiv(amax, 127.0f);
     const float id = d != 0.0f ? fdiv(1.0f, d) : 0.0f;
     float v = fmul(x, id);
@@ -248,8 +272,7 @@ __device__ inline void quant_block_vals(float x, int &q, float &d, int &sum) {
     v = v > 127.0f ? 127.0f : v;
     v = v < -127.0f ? -127.0f : v;
     q = (int)__builtin_rintf(v);
-    sum = q;
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    sum = wave_sum_i32(q);
 }
 
 /* NUMERICS §2 for the 64 values held one per lane by a full wave: writes q (kperm
