@@ -253,7 +253,7 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
     const int nr = a.g.pos0 + a.g.depth[t] + 1;
     float *s = a.S + ((size_t)t * a.H + h) * a.ldS;
     const bool inreg = nr <= SM_CH;
-    const int nu = (nr + SM_T - 1) / SM_T;   /* register entries in use (when inreg) */
+    const int wlo = __builtin_amdgcn_readfirstlane(tid >> 6) * 64;   /* first thread of the wave */
     float x[SM_PER];
     float m = -__builtin_huge_valf();
     if (inreg) {
@@ -287,7 +287,9 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
             /* entries past the row hold -inf; their exps are never stored or used */
 #pragma unroll
             for (int u0 = 0; u0 < SM_PER; u0 += 4) {
-                if (u0 < nu) {
+                /* entry u of this wave holds a score iff wlo + SM_T u < n (wave-uniform):
+                 * whole groups of four where all four hold scores, then one at a time */
+                if (wlo + SM_T * (u0 + 3) < n) {
                     float e[4];
 #pragma unroll
                     for (int k = 0; k < 4; k++) e[k] = exp_port_f(fadd(x[u0 + k], -m));
@@ -296,6 +298,16 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
                         x[u0 + k] = e[k];
                         const int i = tid + SM_T * (u0 + k);
                         if (i < n) es[i] = e[k];
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        if (wlo + SM_T * (u0 + k) < n) {
+                            const float e1 = exp_port_f(fadd(x[u0 + k], -m));
+                            x[u0 + k] = e1;
+                            const int i = tid + SM_T * (u0 + k);
+                            if (i < n) es[i] = e1;
+                        }
                     }
                 }
             }
@@ -320,8 +332,10 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
     if (inreg) {
 #pragma unroll
         for (int u = 0; u < SM_PER; u++) {
-            const int i = tid + SM_T * u;
-            if (i < nr) s[i] = fdiv(x[u], sum);
+            if (wlo + SM_T * u < nr) {
+                const int i = tid + SM_T * u;
+                if (i < nr) s[i] = fdiv(x[u], sum);
+            }
         }
     } else {
         for (int i = tid; i < nr; i += SM_T) s[i] = fdiv(s[i], sum);
