@@ -230,8 +230,12 @@ __device__ inline int wave_scan_incl(int v) {
 /* 16-lane canonical tree (NUMERICS §1) of the partials held by lanes 0..15 of a
  * 16-lane segment: returns the total in lane 0 of the segment. */
 __device__ __forceinline__ float tree16(float L) {
-#pragma unroll
-    for (int s = 8; s >= 1; s >>= 1) L = fadd(L, __shfl_down(L, s, 16));
+    /* L[j] += L[j + s] for s = 8, 4, 2, 1 by DPP row shifts (lanes whose source lies past
+     * the 16-lane row read 0; none of them feeds lane 0) */
+    L = fadd(L, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(L), 0x108, 0xF, 0xF, true)));
+    L = fadd(L, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(L), 0x104, 0xF, 0xF, true)));
+    L = fadd(L, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(L), 0x102, 0xF, 0xF, true)));
+    L = fadd(L, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(L), 0x101, 0xF, 0xF, true)));
     return L;
 }
 

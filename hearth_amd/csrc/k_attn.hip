@@ -271,8 +271,7 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
             if (v == v) m = fmaxf(m, v);
         }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    m = wave_max_f32(m);   /* a maximum: any reduction order gives the same value */
     if (lane == 0) red[wave] = m;
     __syncthreads();
 #pragma unroll
@@ -323,8 +322,7 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
         }
     }
     if (tid < 16) {
-#pragma unroll
-        for (int k = 8; k >= 1; k >>= 1) L = fadd(L, __shfl_down(L, k, 16));
+        L = tree16(L);
         if (tid == 0) sum_sh = L;
     }
     __syncthreads();
