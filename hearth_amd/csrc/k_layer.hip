@@ -460,8 +460,7 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
                 sc[e] = x;
                 if (x == x) m = fmaxf(m, x);
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+            m = wave_max_f32(m);   /* a maximum: any reduction order gives the same value */
             wave_sync();
             if (sc[0] != sc[0]) m = sc[0];
             for (int e = lane; e < E; e += 64) sc[e] = exp_port_f(fadd(sc[e], -m));
@@ -470,7 +469,7 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
             if (lane < 16)
                 for (int e = lane; e < E; e += 16) L = fadd(L, sc[e]);
             L = tree16(L);
-            const float sum = __shfl(L, 0, 64);
+            const float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L), 0));
             for (int e = lane; e < E; e += 64) sc[e] = fdiv(sc[e], sum);
         } else {
             for (int e = lane; e < E; e += 64) sc[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
@@ -545,7 +544,7 @@ __global__ __launch_bounds__(256) void k_qkv_post(QkvArgs a, const float *__rest
         if (lane < 16)
             for (int e = lane; e < hd; e += 16) L = fadd(L, fmul(x[e], x[e]));
         L = tree16(L);
-        L = __shfl(L, 0, 64);
+        L = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L), 0));
         const float r = fdiv(1.0f, sqrt_rn(fadd(fdiv(L, (float)hd), a.eps)));
         const float *w = isq ? a.qn : a.kn;
         wave_sync();
