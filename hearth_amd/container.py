@@ -476,6 +476,21 @@ def make_shaped(path, shape: Shape = QWEN3_30B_A3B, seed: int = 0, n_unique_slab
     return w.write(path)
 
 
+def zipf_routes(seed: int, rows: int, n_moe: int, n_experts: int, k: int, s: float = 1.1) -> np.ndarray:
+    """Routing-trace rows [rows][n_moe][k] (uint16) with Zipf expert popularity: in each
+    MoE layer the experts are ranked by a seeded random permutation and a token takes k
+    distinct experts, drawn without replacement with p(rank r) proportional to
+    (r + 1)^-s (the reference simulator's skewed routing, docs/SIMULATOR.md:172-182).
+    Sampling without replacement is done as the top k of log p + Gumbel noise, which
+    has the same distribution as k successive renormalised draws."""
+    rng = np.random.default_rng(seed)
+    logp = -s * np.log(np.arange(1, n_experts + 1, dtype=np.float64))
+    perm = np.stack([rng.permutation(n_experts) for _ in range(n_moe)])      # rank -> expert
+    keys = logp[None, None, :] + rng.gumbel(size=(rows, n_moe, n_experts))
+    top = np.argsort(-keys, axis=-1, kind="stable")[..., :k]                   # ranks
+    return np.take_along_axis(np.broadcast_to(perm[None], (rows, n_moe, n_experts)), top, -1).astype(np.uint16)
+
+
 def sha256(path, chunk: int = 1 << 24) -> str:
     """sha256 hex digest of a file (fingerprint of a generated container)."""
     import hashlib

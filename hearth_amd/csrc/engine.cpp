@@ -292,6 +292,9 @@ struct hearth_engine {
     int run_geometry(const int32_t *tok, const int32_t *parent, int n, float *logits_out, bool keep_logits_dev);
     void matmul(const DMat &m, const Act &a, const float *xf, int ldx, int T, float *Y, int ldy, bool scale_on, float scale);
     void write_trace(int T);
+    void flush_trace();
+    std::vector<uint8_t> trace_pend;   /* trace rows of the call in progress */
+    std::vector<int> tree_parent;      /* parent table of the last uncommitted tree */
 };
 
 /* ---------------------------------------------------------------- upload */
@@ -1011,27 +1014,37 @@ int hearth_engine::run_geometry(const int32_t *tok, const int32_t *parent, int n
     return OK;
 }
 
+/* Routing-trace rows of the T tokens just evaluated: appended to trace_pend, which the
+ * call writes out only once it has succeeded (a failed call leaves the trace as it was,
+ * as the reference's tpend does, model.c:1287-1323). */
 void hearth_engine::write_trace(int T) {
     if (!trace || !c.n_moe) return;
     const size_t n = (size_t)T * c.n_moe * K;
     h_routes.resize(n);
     ck(hipMemcpyAsync(h_routes.data(), route_out, sizeof(int) * n, hipMemcpyDeviceToHost, st));
     ck(hipStreamSynchronize(st));
-    std::vector<uint8_t> buf(2 * n);
+    const size_t o = trace_pend.size();
+    trace_pend.resize(o + 2 * n);
     for (size_t i = 0; i < n; i++) {
-        buf[2 * i] = (uint8_t)(h_routes[i] & 0xff);
-        buf[2 * i + 1] = (uint8_t)((h_routes[i] >> 8) & 0xff);
+        trace_pend[o + 2 * i] = (uint8_t)(h_routes[i] & 0xff);
+        trace_pend[o + 2 * i + 1] = (uint8_t)((h_routes[i] >> 8) & 0xff);
     }
-    if (fwrite(buf.data(), 1, buf.size(), trace) != buf.size()) {
+}
+
+void hearth_engine::flush_trace() {
+    if (trace && !trace_pend.empty() && fwrite(trace_pend.data(), 1, trace_pend.size(), trace) != trace_pend.size()) {
         log_msg(LOG_ERROR, "routing trace: write failed; tracing stopped");
         fclose(trace);
         trace = nullptr;
     }
+    trace_pend.clear();
 }
 
 int hearth_engine::eval_chunked(const int32_t *tok, int n, float *logits_out, int all_logits) {
     const double t0 = now_s();
     const int start = pos;
+    const uint64_t tokens0 = tokens_done, calls0 = forward_calls;
+    trace_pend.clear();
     try {
         for (int off = 0; off < n; off += B) {
             const int T = std::min(B, n - off);
@@ -1064,8 +1077,12 @@ int hearth_engine::eval_chunked(const int32_t *tok, int n, float *logits_out, in
     } catch (const DeviceError &e) {
         log_msg(LOG_ERROR, "HIP error in hearth_eval: %s", hipGetErrorString(e.e));
         pos = start;
+        tokens_done = tokens0;
+        forward_calls = calls0;
+        trace_pend.clear();
         return E_IO;
     }
+    flush_trace();
     wall_s += now_s() - t0;
     return OK;
 }
@@ -1388,6 +1405,7 @@ HEARTH_API int hearth_verify_tree(hearth_engine *e, const int32_t *tokens, const
     if ((int64_t)e->pos + n > (int64_t)e->cap) return E_CAPACITY;
     if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
     const double t0 = now_s();
+    e->trace_pend.clear();
     try {
         e->run_geometry(tokens, parent, n, logits, false);
         e->write_trace(n);
@@ -1395,8 +1413,12 @@ HEARTH_API int hearth_verify_tree(hearth_engine *e, const int32_t *tokens, const
         if (e->profiling) e->collect_events();
     } catch (const DeviceError &err) {
         log_msg(LOG_ERROR, "HIP error in hearth_verify_tree: %s", hipGetErrorString(err.e));
+        e->trace_pend.clear();
         return E_IO;
     }
+    e->flush_trace();
+    e->tree_parent.resize(n);
+    for (int i = 0; i < n; i++) e->tree_parent[i] = parent ? parent[i] : i - 1;
     e->tree_n = n;
     e->tokens_done += n;
     e->forward_calls++;
@@ -1407,8 +1429,11 @@ HEARTH_API int hearth_verify_tree(hearth_engine *e, const int32_t *tokens, const
 HEARTH_API int hearth_commit_path(hearth_engine *e, const int32_t *path, int n) {
     if (!e || n < 0 || (n && !path)) return E_ARG;
     if (n > e->tree_n) return E_ARG;
-    for (int j = 0; j < n; j++)
+    /* a root path of the last tree: path[0] = 0 and each node the child of the previous */
+    for (int j = 0; j < n; j++) {
         if (path[j] < j || path[j] >= e->tree_n || (j && path[j] <= path[j - 1])) return E_ARG;
+        if (j == 0 ? path[0] != 0 : e->tree_parent[path[j]] != path[j - 1]) return E_ARG;
+    }
     if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
     try {
         bool moves = false;
@@ -1448,6 +1473,7 @@ int verify_and_commit(hearth_engine *e, const int32_t *tokens, const int32_t *pa
     if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
     const double t0 = now_s();
     int np = 0, fin = -1, status = 0;
+    e->trace_pend.clear();
     try {
         e->run_geometry(tokens, parent, n, nullptr, false);
         /* logits stay in HBM; the head ran only if requested -> force it here */
@@ -1479,9 +1505,14 @@ int verify_and_commit(hearth_engine *e, const int32_t *tokens, const int32_t *pa
         if (e->profiling) e->collect_events();
     } catch (const DeviceError &err) {
         log_msg(LOG_ERROR, "HIP error in %s: %s", what, hipGetErrorString(err.e));
+        e->trace_pend.clear();
         return E_IO;
     }
-    if (status != 0) return E_ARG;
+    if (status != 0) {
+        e->trace_pend.clear();
+        return E_ARG;
+    }
+    e->flush_trace();
     *n_path = np;
     *final_tok = fin;
     e->pos += np;
@@ -1489,6 +1520,36 @@ int verify_and_commit(hearth_engine *e, const int32_t *tokens, const int32_t *pa
     e->tokens_done += n;
     e->forward_calls++;
     e->wall_s += now_s() - t0;
+    return OK;
+}
+
+/* rows [0, n) of every layer's cache <-> the snapshot layout of hearth_gpu_kv_export */
+int kv_snapshot(hearth_engine *e, int n, float *host, int64_t count, bool to_host) {
+    const int64_t W = hearth_gpu_kv_row_floats(e);
+    if (count < (int64_t)e->L * n * W) return E_ARG;
+    if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
+    try {
+        const hipMemcpyKind kind = to_host ? hipMemcpyDeviceToHost : hipMemcpyHostToDevice;
+        for (int l = 0; l < e->L; l++) {
+            float *dev = e->kv + (size_t)l * e->kv_layer, *h = host + (size_t)l * n * W;
+            /* (device offset, host offset, floats) of each contiguous piece */
+            auto piece = [&](size_t doff, size_t hoff, size_t nf) {
+                if (to_host) ck(hipMemcpyAsync(h + hoff, dev + doff, sizeof(float) * nf, kind, e->st));
+                else ck(hipMemcpyAsync(dev + doff, h + hoff, sizeof(float) * nf, kind, e->st));
+            };
+            if (e->mla) {
+                piece(0, 0, (size_t)n * e->C);
+                piece((size_t)e->cap * e->C, (size_t)n * e->C, (size_t)n * e->rdim);
+            } else {
+                for (int b = 0; b < 2 * e->Hkv; b++)   /* K groups, then V groups: [cap][hd] each */
+                    piece((size_t)b * e->cap * e->hd, (size_t)b * n * e->hd, (size_t)n * e->hd);
+            }
+        }
+        ck(hipStreamSynchronize(e->st));
+    } catch (const DeviceError &err) {
+        log_msg(LOG_ERROR, "HIP error in the KV snapshot: %s", hipGetErrorString(err.e));
+        return E_IO;
+    }
     return OK;
 }
 
@@ -1555,6 +1616,28 @@ HEARTH_API void hearth_gpu_reset_kstats(hearth_engine *e) {
     if (hipSetDevice(e->dev) == hipSuccess && hipStreamSynchronize(e->st) == hipSuccess)
         (void)hipMemcpy(d, e->dstats, sizeof d, hipMemcpyDeviceToHost);
     e->ks_base = d[1];
+}
+
+HEARTH_API int64_t hearth_gpu_kv_row_floats(hearth_engine *e) {
+    if (!e) return E_ARG;
+    return e->mla ? (int64_t)e->C + e->rdim : 2 * (int64_t)e->Hkv * e->hd;
+}
+
+
+HEARTH_API int hearth_gpu_kv_export(hearth_engine *e, int n, float *dst, int64_t count) {
+    if (!e || n < 0 || n > e->pos || (n && !dst)) return E_ARG;
+    return n ? kv_snapshot(e, n, dst, count, true) : OK;
+}
+
+HEARTH_API int hearth_gpu_kv_import(hearth_engine *e, int n, const float *src, int64_t count) {
+    if (!e || n < 0 || (n && !src)) return E_ARG;
+    if (n > e->cap) return E_CAPACITY;
+    const int rc = n ? kv_snapshot(e, n, const_cast<float *>(src), count, false) : OK;
+    if (rc == OK) {
+        e->pos = n;
+        e->tree_n = 0;
+    }
+    return rc;
 }
 
 HEARTH_API int hearth_gpu_device(char *name, size_t n) {

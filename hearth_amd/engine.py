@@ -165,6 +165,9 @@ _PROTOS = {
     "hearth_gpu_set_profiling": (c_int, [c_void_p, c_int]),
     "hearth_gpu_get_kstats": (c_int, [c_void_p, POINTER(KStats)]),
     "hearth_gpu_reset_kstats": (None, [c_void_p]),
+    "hearth_gpu_kv_row_floats": (ctypes.c_int64, [c_void_p]),
+    "hearth_gpu_kv_export": (c_int, [c_void_p, c_int, POINTER(c_float), ctypes.c_int64]),
+    "hearth_gpu_kv_import": (c_int, [c_void_p, c_int, POINTER(c_float), ctypes.c_int64]),
 }
 
 _ERRORS = {
@@ -441,6 +444,28 @@ class Engine:
             rc = self._api.need("commit_path")(self._handle(), p.ctypes.data_as(_I32P), int(p.size))
         if rc < 0:
             raise HearthError(f"hearth_commit_path failed (code {rc})")
+
+    # ---- KV snapshot (hearth_gpu_kv_export / hearth_gpu_kv_import) ----
+    def kv_export(self, n: int | None = None) -> np.ndarray:
+        """The KV rows of positions [0, n) (default: pos) as float32
+        [n_layers, n * hearth_gpu_kv_row_floats] in the reference's cache layout."""
+        with self._lock:
+            h = self._handle()
+            n = int(self._api.pos(h)) if n is None else int(n)
+            w = int(self._api.need("gpu_kv_row_floats")(h))
+            out = np.empty((int(self.info["n_layers"]), n * w), dtype=np.float32)
+            rc = self._api.need("gpu_kv_export")(h, n, out.ctypes.data_as(POINTER(c_float)), out.size)
+        if rc < 0:
+            raise HearthError(f"hearth_gpu_kv_export failed (code {rc}): {_ERRORS.get(rc, 'unknown error')}")
+        return out
+
+    def kv_import(self, snap, n: int) -> None:
+        """Restores the rows of kv_export(n) and sets pos = n."""
+        a = np.ascontiguousarray(snap, dtype=np.float32)
+        with self._lock:
+            rc = self._api.need("gpu_kv_import")(self._handle(), int(n), a.ctypes.data_as(POINTER(c_float)), a.size)
+        if rc < 0:
+            raise HearthError(f"hearth_gpu_kv_import failed (code {rc}): {_ERRORS.get(rc, 'unknown error')}")
 
     # ---- telemetry ----
     def stats(self) -> dict:

@@ -120,6 +120,18 @@ HEARTH_API int hearth_gpu_set_profiling(hearth_engine *e, int on);
 HEARTH_API int hearth_gpu_get_kstats(hearth_engine *e, hearth_gpu_kstats *out);
 HEARTH_API void hearth_gpu_reset_kstats(hearth_engine *e);
 
+/* KV-cache snapshot of positions [0, n) (a conversation to resume later, or a context
+ * computed elsewhere). Layout, every layer in turn: GQA K [n_kv_heads][n][head_dim] then
+ * V [n_kv_heads][n][head_dim]; MLA latent c [n][kv_lora] then rotated k_pe [n][rope_dim]
+ * (the reference engine's per-layer cache arrays, engine/src/model.c, cut to n
+ * positions). hearth_gpu_kv_row_floats: floats per position and layer, so a snapshot
+ * holds n_layers * n * that many floats. Export needs n <= pos; import needs
+ * n <= the KV capacity, writes the rows and sets pos = n (the rows past n are left as
+ * they were). `count` is the buffer's size in floats. */
+HEARTH_API int64_t hearth_gpu_kv_row_floats(hearth_engine *e);
+HEARTH_API int hearth_gpu_kv_export(hearth_engine *e, int n, float *dst, int64_t count);
+HEARTH_API int hearth_gpu_kv_import(hearth_engine *e, int n, const float *src, int64_t count);
+
 /* Device the library runs on (HEARTH_DEVICE, default 0) and its name. */
 HEARTH_API int hearth_gpu_device(char *name, size_t n);
 

@@ -449,7 +449,10 @@ static void matvec(int dtype, const uint8_t *W, int64_t cols, const float *X, in
     }
     int64_t rows = r1 - r0;
     int nt = nthreads < 1 ? 1 : nthreads;
-    if ((double)rows * (double)cols * T < 4e5) nt = 1;
+    {   /* at least ~2M multiply-adds per thread: thread start-up costs more below that */
+        const double work = (double)rows * (double)cols * T / 2e6;
+        if (work < nt) nt = work < 1.0 ? 1 : (int)work;
+    }
     if (nt > rows) nt = (int)(rows > 0 ? rows : 1);
     mv_job jobs[64];
     pthread_t th[64];
@@ -1100,6 +1103,60 @@ int ho_commit_path(ho_model *m, const int32_t *path, int n) {
     }
     m->pos += n;
     return 0;
+}
+
+/* KV snapshot of positions [0, n), every layer in turn: GQA K [Hkv][n][hd] then
+ * V [Hkv][n][hd]; MLA latent c [n][C] then rotated k_pe [n][rope]. The same layout as
+ * the reference engine's per-layer cache arrays restricted to n positions (model.c
+ * keeps [Hkv][cap][hd] per K and V). Test infrastructure: lets a check start from a
+ * context another implementation computed. */
+int64_t ho_kv_row_floats(const ho_model *m) {
+    const cfg *c = &m->c;
+    return c->attn_kind == 1 ? (int64_t)c->kv_lora + c->rope_qk : 2 * (int64_t)c->n_kv_heads * c->head_dim;
+}
+
+static int kv_copy(ho_model *m, int n, float *ext, int to_ext) {
+    const cfg *c = &m->c;
+    if (n < 0 || n > m->cap || !ext) return -1;
+    const int64_t W = ho_kv_row_floats(m);
+    for (int l = 0; l < c->n_layers; l++) {
+        float *base = m->kv + (size_t)l * m->per_layer, *e = ext + (size_t)l * (size_t)n * (size_t)W;
+        if (c->attn_kind == 1) {
+            const int C = c->kv_lora, r = c->rope_qk;
+            float *kp = base + (size_t)m->cap * C;
+            if (to_ext) {
+                memcpy(e, base, sizeof(float) * (size_t)n * C);
+                memcpy(e + (size_t)n * C, kp, sizeof(float) * (size_t)n * r);
+            } else {
+                memcpy(base, e, sizeof(float) * (size_t)n * C);
+                memcpy(kp, e + (size_t)n * C, sizeof(float) * (size_t)n * r);
+            }
+            continue;
+        }
+        const int Hkv = c->n_kv_heads, hd = c->head_dim, kd = Hkv * hd;
+        for (int kvi = 0; kvi < 2; kvi++) {
+            float *cache = base + (size_t)kvi * m->cap * kd;
+            for (int g = 0; g < Hkv; g++)
+                for (int r = 0; r < n; r++) {
+                    float *in = cache + (size_t)r * kd + (size_t)g * hd;
+                    float *ex = e + (((size_t)kvi * Hkv + g) * n + r) * hd;
+                    if (to_ext) memcpy(ex, in, sizeof(float) * hd);
+                    else memcpy(in, ex, sizeof(float) * hd);
+                }
+        }
+    }
+    return 0;
+}
+
+int ho_kv_export(const ho_model *m, int n, float *dst) {
+    if (n > m->pos) return -1;
+    return kv_copy((ho_model *)m, n, dst, 1);
+}
+
+int ho_kv_import(ho_model *m, int n, const float *src) {
+    const int rc = kv_copy(m, n, (float *)src, 0);
+    if (rc == 0) m->pos = n;
+    return rc;
 }
 
 /* ------------------------------------------------------------ acceptance (generate.py) */

@@ -19,6 +19,8 @@
  *                                   pos0 + depth(i) and attends to the context followed by
  *                                   its ancestors in path order, i.e. exactly the chain
  *                                   root -> i; no reference counterpart
+ *   ho_kv_export / ho_kv_import     the reference engine's cache layout (model.c, [Hkv][cap][hd]
+ *                                   per K and V) cut to n positions; test plumbing, no arithmetic
  *   ho_probs / ho_accept_*          python/hearth/generate.py:84-147,365-392
  *
  * Exponential mode (ho_set_exp_mode):
@@ -98,6 +100,14 @@ void      ho_set_threads(ho_model *m, int n);
 /* Debug: append per-token intermediates (q, att, h_mid, x_ffn, router, ids, h) to
  * <dir>/l<layer>_<name>.bin ("" turns it off). */
 void      ho_set_dump(ho_model *m, const char *dir);
+
+/* KV snapshot of positions [0, n) of every layer, layer by layer: GQA K [Hkv][n][hd]
+ * then V [Hkv][n][hd]; MLA latent c [n][C] then rotated k_pe [n][rope_dim] (the reference
+ * engine's per-layer cache arrays cut to n positions). ho_kv_row_floats: floats per
+ * position and layer. Import sets pos = n. Return 0 or -1. */
+int64_t   ho_kv_row_floats(const ho_model *m);
+int       ho_kv_export(const ho_model *m, int n, float *dst);
+int       ho_kv_import(ho_model *m, int n, const float *src);
 
 /* ---- acceptance ----------------------------------------------------------- */
 /* Sampler settings (generate.py:31-56): temperature 0 = one-hot argmax; top_k 0 = off;

@@ -64,6 +64,10 @@ def lib():
         L.ho_commit_path.argtypes = [c_void_p, _I32P, c_int]
         L.ho_set_threads.argtypes = [c_void_p, c_int]
         L.ho_set_replay.argtypes = [c_void_p, POINTER(ctypes.c_uint16), c_int64]
+        L.ho_kv_row_floats.restype = c_int64
+        L.ho_kv_row_floats.argtypes = [c_void_p]
+        L.ho_kv_export.argtypes = [c_void_p, c_int, _FP]
+        L.ho_kv_import.argtypes = [c_void_p, c_int, _FP]
         L.ho_probs.argtypes = [_FP, c_int, c_double, c_int, c_double, c_double, _DP]
         L.ho_argmax.argtypes = [_FP, c_int]
         L.ho_draw.argtypes = [_DP, c_int, c_double]
@@ -132,11 +136,13 @@ class Model:
     def rewind(self, pos: int) -> None:
         assert lib().ho_rewind(self.h, pos) == 0
 
-    def eval(self, tokens, routes: bool = False):
+    def eval(self, tokens, routes: bool = False, logits: bool = True):
+        """logits [n][V] (None with logits=False: the head is skipped), and routes
+        [n][n_moe][K] with routes=True"""
         t = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
-        lg = np.empty((t.size, self.vocab), dtype=np.float32)
+        lg = np.empty((t.size, self.vocab), dtype=np.float32) if logits else None
         rt = np.empty((t.size, max(self.n_moe, 1), max(self.top_k, 1)), dtype=np.int32) if routes else None
-        rc = lib().ho_eval(self.h, t.ctypes.data_as(_I32P), t.size, lg.ctypes.data_as(_FP),
+        rc = lib().ho_eval(self.h, t.ctypes.data_as(_I32P), t.size, lg.ctypes.data_as(_FP) if logits else None,
                            rt.ctypes.data_as(_I32P) if routes else None)
         if rc != 0:
             raise RuntimeError(f"ho_eval {rc}")
@@ -156,6 +162,19 @@ class Model:
     def commit_path(self, path) -> None:
         p = np.ascontiguousarray(path, dtype=np.int32)
         assert lib().ho_commit_path(self.h, p.ctypes.data_as(_I32P), p.size) == 0
+
+    def kv_export(self, n: int | None = None) -> np.ndarray:
+        """KV rows of positions [0, n) in the layout of hearth_gpu_kv_export"""
+        n = self.pos if n is None else int(n)
+        w = lib().ho_kv_row_floats(self.h)
+        out = np.empty((self.n_layers, n * w), dtype=np.float32)
+        assert lib().ho_kv_export(self.h, n, out.ctypes.data_as(_FP)) == 0
+        return out
+
+    def kv_import(self, snap, n: int) -> None:
+        a = np.ascontiguousarray(snap, dtype=np.float32)
+        assert a.size >= self.n_layers * n * lib().ho_kv_row_floats(self.h)
+        assert lib().ho_kv_import(self.h, int(n), a.ctypes.data_as(_FP)) == 0
 
     def set_replay(self, ids) -> None:
         """route replay: ids [rows][n_moe][K] (uint16), or None for routing"""

@@ -137,6 +137,11 @@ def test_tree_equals_chain_on_gpu(eng):
         assert np.array_equal(_bits(lc[-1]), _bits(lt[node])), node
     eng.rewind(40)
     eng.verify_tree(tok, par, want_logits=False)
+    # only root paths of the tree commit: siblings, a skipped level or a missing root fail
+    for bad in ([0, 1, 2], [0, 6], [1, 4], [0, 2, 4]):
+        with pytest.raises(HearthError):
+            eng.commit_path(bad)
+        assert eng.pos == 40
     eng.commit_path([0, 1, 4, 6])
     assert eng.pos == 44
     after = eng.eval([77])

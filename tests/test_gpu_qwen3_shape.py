@@ -1,0 +1,186 @@
+"""The verify step at the Qwen3-30B-A3B shape the benchmark runs, bit for bit against
+the oracle (the CPU restatement in portable-exp mode).
+
+Model: the benchmark's recipe (container.make_shaped) at the full Qwen3-30B-A3B width:
+hidden 2048, 32 query / 4 KV heads of 128, 128 experts top-8 of FFN 768, vocab 151936,
+Q4 experts, Q8 attention / embedding / lm_head, F32 routers; every one of the 256
+(layer, expert) slabs distinct. Only the depth is cut, 48 -> 2 layers, so that the
+oracle's single-token loop finishes in seconds: every kernel configuration of a layer
+is the benchmark's.
+
+The oracle starts from the GPU's prefilled KV rows (hearth_gpu_kv_export ->
+ho_kv_import), so the contexts of 4095 and 2047 rows cost it nothing; the prefill
+kernels themselves are checked on a 160-token chunk by comparing the KV rows both
+sides write.
+
+Cases (the benchmark configurations):
+- chain verify k = 8 at a 4095-token context (T = 9; attention rows up to 4104, the
+  33-tile value pass and 4104-entry softmax rows), greedy acceptance on the GPU;
+- a 4 x 4 x 4 draft tree (85 nodes) at a 2047-token context with sampled acceptance
+  (temperature 0.8, top-p 0.95, q = softmax of N(0, 2) logits, seeded uniforms);
+- the routed-expert kernels at T = 1, 9, 33, 65 tokens with Zipf(1.1) routing (replayed
+  from a trace, as the reference's route replay does), which covers the few-token
+  split-K expert kernel (T <= 16) and the general one (T > 16);
+- a 160-token prefill chunk.
+"""
+from __future__ import annotations
+
+import dataclasses
+import os
+
+import numpy as np
+import pytest
+
+import oracle_py as O
+from hearth_amd import container
+from hearth_amd.engine import Engine, make_sampler
+
+pytestmark = pytest.mark.gpu
+
+SHAPE = dataclasses.replace(container.QWEN3_30B_A3B, n_layers=2, max_seq=8192)
+CTX = 4095
+THREADS = max(1, min(16, os.cpu_count() or 1))
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def _assert_same(gpu, ora, what):
+    bad = int((_bits(gpu) != _bits(ora)).sum())
+    assert bad == 0, f"{what}: {bad} of {gpu.size} values differ from the oracle"
+
+
+@pytest.fixture(scope="module")
+def model(tmp_path_factory):
+    path = tmp_path_factory.mktemp("qwen3w") / "qwen3_30b_a3b_2layers.hearth"
+    container.make_shaped(path, SHAPE, seed=5, n_unique_slabs=2 * SHAPE.n_experts)
+    return path
+
+
+@pytest.fixture(scope="module")
+def prefilled(model):
+    """The engine after a 4095-token prefill, and the KV rows it wrote."""
+    O.set_exp_mode(O.EXP_PORTABLE)
+    eng = Engine(model, max_seq=CTX + 256, max_batch=512)
+    prompt = container.uniform_ints(4242, CTX, SHAPE.vocab).astype(np.int32)
+    eng.eval(prompt)
+    snap = eng.kv_export(CTX)
+    yield eng, prompt, snap
+    eng.close()
+
+
+def _cut(snap, n_from, n):
+    """rows [0, n) of a snapshot of n_from rows (GQA layout [L][2 Hkv][n][hd])"""
+    L = SHAPE.n_layers
+    s = snap.reshape(L, 2 * SHAPE.n_kv_heads, n_from, SHAPE.head_dim)[:, :, :n]
+    return np.ascontiguousarray(s).reshape(L, -1)
+
+
+def test_chain_verify_k8_ctx4095(prefilled, model, tmp_path):
+    eng, prompt, snap = prefilled
+    # the model's own greedy continuation, then drafts with 3 of 8 replaced
+    eng.rewind(CTX)
+    cont = [int(prompt[-1])]
+    for _ in range(9):
+        cont.append(int(np.argmax(eng.eval([cont[-1]]))))
+    eng.rewind(CTX)
+    drafts = np.array(cont[1:9], dtype=np.int32)
+    drafts[[3, 5, 6]] = (drafts[[3, 5, 6]] + 7919) % SHAPE.vocab
+    toks = np.concatenate([[prompt[-1]], drafts]).astype(np.int32)
+    tr = tmp_path / "chain.hrtr"
+    eng.trace_start(tr)
+    path, final, lg = eng.verify_greedy(toks, want_logits=True)
+    eng.trace_stop()
+    routes = np.frombuffer(tr.read_bytes()[24:], dtype="<u2").reshape(len(toks), SHAPE.n_layers, SHAPE.top_k)
+
+    m = O.Model(model, cap=CTX + 64, threads=THREADS)
+    m.kv_import(snap, CTX)
+    lo, ro = m.eval(toks, routes=True)
+    _assert_same(lg, lo, "chain verify logits")
+    assert np.array_equal(routes.astype(np.int32), ro), "routes differ from the oracle"
+    rc, opath, ofin = O.accept_tree(lo, toks, np.arange(-1, len(toks) - 1))
+    assert rc == 0 and path == opath and final == ofin
+    assert path == [0, 1, 2, 3], path      # drafts 1..3 are the greedy continuation, draft 4 is not
+    assert eng.pos == CTX + len(path)
+
+
+def _tree_4x4x4():
+    parent = [-1]
+    level = [0]
+    for _ in range(3):
+        nxt = []
+        for p in level:
+            for _ in range(4):
+                parent.append(p)
+                nxt.append(len(parent) - 1)
+        level = nxt
+    return np.array(parent, dtype=np.int32)
+
+
+def test_tree_4x4x4_sampled_ctx2047(prefilled, model):
+    eng, prompt, snap = prefilled
+    n0 = 2047
+    s2 = _cut(snap, CTX, n0)
+    eng.kv_import(s2, n0)
+    parent = _tree_4x4x4()
+    n, V = len(parent), SHAPE.vocab
+    rng = np.random.default_rng(77)
+    z = rng.standard_normal((n, V)) * 2.0
+    q = np.exp(z - z.max(1, keepdims=True))
+    q /= q.sum(1, keepdims=True)
+    toks = np.zeros(n, dtype=np.int32)
+    toks[0] = prompt[n0]
+    for c in range(1, n):            # each child drawn from its parent's draft distribution
+        toks[c] = rng.choice(V, p=q[parent[c]])
+    u = container.uniforms(91, 2 * n)
+    smp = make_sampler(temperature=0.8, top_p=0.95)
+    path, final, lg = eng.verify_sample(toks, parent, smp, q=q, u=u, want_logits=True)
+
+    m = O.Model(model, cap=n0 + n + 8, threads=THREADS)
+    m.kv_import(s2, n0)
+    lo = m.eval_tree(toks, parent)
+    _assert_same(lg, lo, "tree verify logits")
+    rc, opath, ofin = O.accept_tree_s(lo, toks, parent, O.sampler(0.8, top_p=0.95), q=q, u=u)
+    assert rc == 0 and path == opath and final == ofin, (path, final, opath, ofin)
+    assert eng.pos == n0 + len(path)
+
+
+@pytest.mark.parametrize("T", [1, 9, 33, 65])
+def test_expert_kernels_zipf_routing(prefilled, model, tmp_path, T):
+    eng, prompt, snap = prefilled
+    n0 = 256
+    s0 = _cut(snap, CTX, n0)
+    ids = container.zipf_routes(1000 + T, 512, SHAPE.n_layers, SHAPE.n_experts, SHAPE.top_k)
+    tr = tmp_path / "zipf.hrtr"
+    O.write_trace(tr, ids, SHAPE.n_layers, SHAPE.n_experts)
+    toks = container.uniform_ints(300 + T, T, SHAPE.vocab).astype(np.int32)
+    eng.route_replay(tr)
+    try:
+        eng.kv_import(s0, n0)
+        lg = eng.eval(toks, all_logits=True)
+    finally:
+        eng.route_replay(None)
+    m = O.Model(model, cap=n0 + T + 8, threads=THREADS)
+    m.kv_import(s0, n0)
+    m.set_replay(ids)
+    lo, ro = m.eval(toks, routes=True)
+    want = ids[(n0 + np.arange(T)) % len(ids)].astype(np.int32)
+    assert np.array_equal(ro, want)
+    _assert_same(lg, lo, f"logits of {T} tokens with Zipf-routed experts")
+
+
+def test_prefill_chunk_160(model):
+    """a 160-token chunk from position 0 through the prefill kernels (two 128-token
+    passes of the dense GEMM, several 16-token tiles per expert): the KV rows both sides
+    write, and the last token's logits"""
+    n = 160
+    toks = container.uniform_ints(515, n, SHAPE.vocab).astype(np.int32)
+    with Engine(model, max_seq=1024, max_batch=512) as eng:
+        lg = eng.eval(toks)
+        kg = eng.kv_export(n)
+    m = O.Model(model, cap=1024, threads=THREADS)
+    m.eval(toks[:-1], logits=False)
+    lo = m.eval(toks[-1:])[0]
+    _assert_same(kg, m.kv_export(n), "KV rows of the prefill chunk")
+    _assert_same(lg, lo, "logits of the chunk's last token")

@@ -220,3 +220,20 @@ def test_greedy_acceptance_closed_form():
             n_acc += 1
         rc, path, fin = O.accept_tree(rows, np.concatenate([[0], drafts]), np.arange(-1, k))
         assert rc == 0 and path == list(range(n_acc + 1)) and fin == am[n_acc]
+
+
+def test_kv_snapshot_round_trip(tiny_model):
+    """ho_kv_export -> ho_kv_import into a fresh model continues exactly like the model
+    that computed the context (the layout is plumbing; the rows must arrive intact)"""
+    O.set_exp_mode(O.EXP_PORTABLE)
+    toks = container.uniform_ints(31, 24, container.TINY.vocab)
+    a = O.Model(tiny_model, cap=64)
+    a.eval(toks[:20], logits=False)
+    snap = a.kv_export()
+    assert snap.shape == (container.TINY.n_layers, 20 * 2 * container.TINY.n_kv_heads * container.TINY.head_dim)
+    b = O.Model(tiny_model, cap=64)
+    b.kv_import(snap, 20)
+    assert b.pos == 20
+    la, lb = a.eval(toks[20:]), b.eval(toks[20:])
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    assert np.array_equal(a.kv_export(), b.kv_export())
