@@ -47,6 +47,22 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
 HEARTH_API int hearth_gpu_accept_greedy(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
                                         int32_t *path_out, int *n_path, int32_t *final_tok);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops that forbid hipMalloc): the acceptance of
+ * hearth_gpu_accept_greedy on the caller's DEVICE buffers, enqueued on `stream` (a
+ * hipStream_t of the current device; NULL = the null stream) without waiting for it.
+ * rows [n][V] f32, tokens [n], parent [n] or NULL for a chain; results land in path_out
+ * [n] (accepted nodes from the root) and result [3] = {path length, final token,
+ * status: 0, or -1 for NaN/+inf/all -inf rows}. The kernels' scratch is a fixed array
+ * of HEARTH_GPU_NOALLOC_MAX_ROWS rows (392 KiB) in the library, one per GPU, held until
+ * the process ends: the call allocates nothing, and calls that overlap on one GPU race
+ * on it. Returns 0, -1 for bad arguments, -3 when n exceeds the limit, -4 for a
+ * device error; parent entries are not checked (any values give a bounded walk). */
+#define HEARTH_GPU_NOALLOC_MAX_ROWS 1024
+HEARTH_API int hearth_gpu_accept_greedy_noalloc(const float *rows, int n, int V, const int32_t *tokens,
+                                                const int32_t *parent, int32_t *path_out, int32_t *result,
+                                                void *stream);
+
 /* Sampler settings of sampled acceptance: the fields of the reference's Sampler
  * (python/hearth/generate.py:31-56) with its validation. temperature 0 gives the one-hot
  * argmax distribution; top_k 0, top_p 1, min_p 0 and repetition_penalty 1 are "off".
