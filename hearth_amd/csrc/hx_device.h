@@ -7,11 +7,11 @@
  * f32 fold over blocks is acc = acc + (float)isum * (dw * dx) in block order with no
  * FMA (all sources are built with -ffp-contract=off and the fold uses explicit
  * round-to-nearest intrinsics), dot16/sum16 use 16 lanes then the 8/4/2/1 tree, and
- * NaN outputs are stored as 0x7fc00000. The only libm-dependent step, exp, uses
- * hx_exp_port (Cody-Waite reduction + degree-13 Taylor polynomial in IEEE double,
- * basic operations only), which gives the same bits as the CPU restatement's
- * portable mode; RoPE cos/sin come from the host (libm), as in the reference
- * (engine/src/model.c:386-397).
+ * NaN outputs are stored as 0x7fc00000. The only libm-dependent step, expf, is
+ * exp_glibc_f, the platform libm's expf restated bit for bit (so results equal the
+ * reference engine's on its glibc platform); RoPE cos/sin come from the host (libm), as
+ * in the reference (engine/src/model.c:386-397). exp_port_d (double) serves the
+ * float64 sampler.
  *
  * HBM layouts
  *   QMat (Q8/Q4 matrix, rows x cols, nb = cols/64 blocks, nbp = nb rounded up to even):
@@ -151,7 +151,60 @@ __device__ inline double exp_port_d(double x) {
     return nan ? x : y;
 }
 
-__device__ __forceinline__ float exp_port_f(float x) { return __double2float_rn(exp_port_d((double)x)); }
+/* glibc's expf (sysdeps/ieee754/flt-32/e_expf.c, glibc 2.28+; the algorithm of the
+ * optimized-routines library) as its x86-64 FMA build evaluates it, the platform expf
+ * the reference engine calls: x = (k + r) ln2 / 32 with k and r from the exact product
+ * x * 32/ln2 (fma), 2^(k/32) from a 32-entry table of 2^(i/32) (correctly rounded
+ * doubles, stored minus i << 47), 2^(r/32) by a cubic in double (three fmas), one
+ * rounding to float at the end. The CPU restatement ho_exp_glibc_f is the same function
+ * and equals the libm expf on all 2^32 inputs. */
+__constant__ static const unsigned long long HX_EXP2F_TAB[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+/* the glibc expf; written without branches (the special inputs are selected at the end,
+ * the arithmetic runs on them too with a masked table index), so calls interleave.
+ * tab: the 32 table entries, from HX_EXP2F_TAB or a copy in LDS (exp_table_to_lds): a
+ * per-lane gather from LDS costs far less than one through the vector memory path. */
+__device__ inline float exp_glibc_f(float x, const unsigned long long *tab) {
+    const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32.0;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double shift = 0x1.8p+52;
+    const unsigned ux = __float_as_uint(x), abstop = (ux >> 20) & 0x7ffu;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_32, xd, shift);
+    const unsigned long long ki = (unsigned long long)__double_as_longlong(kd);
+    kd = dsub(kd, shift);
+    const double r = __builtin_fma(inv_ln2_32, xd, -kd);
+    const double s = __longlong_as_double((long long)(tab[ki & 31] + (ki << 47)));
+    const double z = __builtin_fma(c0, r, c1), r2 = dmul(r, r);
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    float res = __double2float_rn(dmul(y, s));
+    if (abstop >= 0x42bu) {                             /* |x| >= 88, inf or NaN */
+        res = x > 0x1.62e42ep6f ? __builtin_huge_valf() : res;   /* overflow */
+        res = x < -0x1.9fe368p6f ? 0.0f : res;                   /* underflow, -inf */
+        res = abstop >= 0x7f8u && ux != 0xff800000u ? x + x : res;   /* NaN, +inf */
+    }
+    return res;
+}
+
+__device__ __forceinline__ float exp_glibc_f(float x) { return exp_glibc_f(x, HX_EXP2F_TAB); }
+
+/* copies the exp table into an LDS array of 32 entries (threads 0..31 of the block; the
+ * caller synchronizes before use) */
+__device__ __forceinline__ void exp_table_to_lds(unsigned long long *lds) {
+    if (threadIdx.x < 32) lds[threadIdx.x] = HX_EXP2F_TAB[threadIdx.x];
+}
 
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -238,8 +238,8 @@ __device__ __forceinline__ float sum16_lds(const float *es, int n, int lane16, f
 /* softmax over one (token, head) row of scores, in place (quant.c:634-642): running
  * max from s[0] (a NaN s[0] stays the max, later NaNs are skipped), e = exp(s - max),
  * sum16 of e, p = e / sum. Up to 8192 scores stay in registers (16 per thread); their
- * exps are computed four at a time (exp_port_d has no branches, so the four
- * double-precision chains interleave). Longer rows are processed in chunks of 8192
+ * exps are computed four at a time (exp_glibc_f has no branches, so the four
+ * double-precision evaluations interleave). Longer rows are processed in chunks of 8192
  * re-read from the row. */
 constexpr int SM_T = 512;
 constexpr int SM_PER = 16;
@@ -249,6 +249,8 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
     __shared__ float es[SM_CH];
     __shared__ float red[SM_T / 64];
     __shared__ float sum_sh;
+    __shared__ unsigned long long etab[32];
+    exp_table_to_lds(etab);
     const int t = blockIdx.x / a.H, h = blockIdx.x % a.H, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nr = a.g.pos0 + a.g.depth[t] + 1;
     float *s = a.S + ((size_t)t * a.H + h) * a.ldS;
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
                 if (wlo + SM_T * (u0 + 3) < n) {
                     float e[4];
 #pragma unroll
-                    for (int k = 0; k < 4; k++) e[k] = exp_port_f(fadd(x[u0 + k], -m));
+                    for (int k = 0; k < 4; k++) e[k] = exp_glibc_f(fadd(x[u0 + k], -m), etab);
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
                         x[u0 + k] = e[k];
@@ -302,7 +304,7 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
                         if (wlo + SM_T * (u0 + k) < n) {
-                            const float e1 = exp_port_f(fadd(x[u0 + k], -m));
+                            const float e1 = exp_glibc_f(fadd(x[u0 + k], -m), etab);
                             x[u0 + k] = e1;
                             const int i = tid + SM_T * (u0 + k);
                             if (i < n) es[i] = e1;
@@ -311,7 +313,7 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
                 }
             }
         } else {
-            for (int i = tid; i < n; i += SM_T) es[i] = exp_port_f(fadd(s[c0 + i], -m));
+            for (int i = tid; i < n; i += SM_T) es[i] = exp_glibc_f(fadd(s[c0 + i], -m), etab);
         }
         __syncthreads();
         /* SM_CH is a multiple of 16, so element c0 + i keeps lane (c0 + i) % 16 = i % 16 */

@@ -354,7 +354,7 @@ __global__ __launch_bounds__(512) void k_expert_gateup_sk(MoeArgs a, int ntok) {
             const float gv = canon(fold_terms(P, ew.gate.nb, ntok, f));
             const float uv = canon(fold_terms(P + pstride, ew.gate.nb, ntok, f));
             if (t0 + c < n) {
-                const float sg = fdiv(gv, fadd(1.0f, exp_port_f(-gv)));
+                const float sg = fdiv(gv, fadd(1.0f, exp_glibc_f(-gv)));
                 a.midf[(size_t)(p0 + t0 + c) * a.F + row] = fmul(sg, uv);
             }
         }
@@ -485,7 +485,7 @@ __global__ __launch_bounds__(256) void k_expert_gateup_pp(MoeArgs a, int ntok) {
                 const float gv = canon(fold_terms(P, nb, ntok, f));
                 const float uv = canon(fold_terms(P + pstride, nb, ntok, f));
                 if (c < n) {
-                    const float sg = fdiv(gv, fadd(1.0f, exp_port_f(-gv)));
+                    const float sg = fdiv(gv, fadd(1.0f, exp_glibc_f(-gv)));
                     a.midf[(size_t)(p0 + c) * a.F + row] = fmul(sg, uv);
                 }
             }
@@ -726,7 +726,7 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
     float mv = 0.0f;
     if (out) {
         const float gv = canon(acc[0]), uv = canon(acc[NM - 1]);
-        const float sg = fdiv(gv, fadd(1.0f, exp_port_f(-gv)));
+        const float sg = fdiv(gv, fadd(1.0f, exp_glibc_f(-gv)));
         mv = fmul(sg, uv);
         if (!QF) a.midf[(size_t)(p0 + col) * a.F + row] = mv;
     }

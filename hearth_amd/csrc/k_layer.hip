@@ -51,7 +51,7 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
             v = h[i];
             if (a.add) {
                 float sv = a.add[(size_t)t * D + i];
-                if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_port_f(-a.add_gate[t]))));
+                if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_glibc_f(-a.add_gate[t]))));
                 v = fadd(v, fmul(a.rs, sv));
             }
         } else {
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
             }
             if (a.add) {
                 float sv = a.add[(size_t)t * D + i];
-                if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_port_f(-a.add_gate[t]))));
+                if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_glibc_f(-a.add_gate[t]))));
                 out = fadd(out, sv);
             }
             v = fadd(h[i], fmul(a.rs, out));
@@ -126,7 +126,7 @@ __global__ void k_swiglu_quant(float *__restrict__ g, const float *__restrict__ 
     float v = 0.0f;
     if (i < F) {
         const float gv = g[(size_t)t * F + i];
-        v = fmul(fdiv(gv, fadd(1.0f, exp_port_f(-gv))), u[(size_t)t * F + i]);
+        v = fmul(fdiv(gv, fadd(1.0f, exp_glibc_f(-gv))), u[(size_t)t * F + i]);
         g[(size_t)t * F + i] = v;
     }
     quant_block_wave(v, a, t, b);
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(64) void k_route_tokens(RouteArgs a) {
         for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
         if (lg[0] != lg[0]) m = lg[0];
         wave_sync();
-        for (int e = lane; e < E; e += 64) score[e] = exp_port_f(fadd(score[e], -m));
+        for (int e = lane; e < E; e += 64) score[e] = exp_glibc_f(fadd(score[e], -m));
         wave_sync();
         float L = 0.0f;
         if (lane < 16)
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(64) void k_route_tokens(RouteArgs a) {
         wave_sync();
         for (int e = lane; e < E; e += 64) score[e] = fdiv(score[e], s);
     } else {
-        for (int e = lane; e < E; e += 64) score[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
+        for (int e = lane; e < E; e += 64) score[e] = fdiv(1.0f, fadd(1.0f, exp_glibc_f(-lg[e])));
     }
     wave_sync();
     for (int e = lane; e < E; e += 64) {
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256) void k_route_rank(RouteArgs a) {
         __syncthreads();
         m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
         if (score[0] != score[0]) m = score[0];
-        for (int e = tid; e < E; e += 256) score[e] = exp_port_f(fadd(score[e], -m));
+        for (int e = tid; e < E; e += 256) score[e] = exp_glibc_f(fadd(score[e], -m));
         __syncthreads();
         if (tid < 16) {
             float L = 0.0f;
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256) void k_route_rank(RouteArgs a) {
         const float sum = sum_sh;
         for (int e = tid; e < E; e += 256) score[e] = fdiv(score[e], sum);
     } else {
-        for (int e = tid; e < E; e += 256) score[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
+        for (int e = tid; e < E; e += 256) score[e] = fdiv(1.0f, fadd(1.0f, exp_glibc_f(-lg[e])));
     }
     __syncthreads();
     if (a.replay) {   /* uniform */
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
             m = wave_max_f32(m);   /* a maximum: any reduction order gives the same value */
             wave_sync();
             if (sc[0] != sc[0]) m = sc[0];
-            for (int e = lane; e < E; e += 64) sc[e] = exp_port_f(fadd(sc[e], -m));
+            for (int e = lane; e < E; e += 64) sc[e] = exp_glibc_f(fadd(sc[e], -m));
             wave_sync();
             float L = 0.0f;
             if (lane < 16)
@@ -472,7 +472,7 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
             const float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L), 0));
             for (int e = lane; e < E; e += 64) sc[e] = fdiv(sc[e], sum);
         } else {
-            for (int e = lane; e < E; e += 64) sc[e] = fdiv(1.0f, fadd(1.0f, exp_port_f(-lg[e])));
+            for (int e = lane; e < E; e += 64) sc[e] = fdiv(1.0f, fadd(1.0f, exp_glibc_f(-lg[e])));
         }
         if (a.replay) {   /* uniform */
             if (lane < K) chosen[t][lane] = replay_id(a, t, lane);

@@ -77,7 +77,7 @@ static float bf16_to_f32(uint16_t h) { return bits_f((uint32_t)h << 16); }
 /* ------------------------------------------------------------ exponential */
 
 static int g_exp_mode = HO_EXP_LIBM;
-void ho_set_exp_mode(int mode) { g_exp_mode = mode == HO_EXP_PORTABLE ? HO_EXP_PORTABLE : HO_EXP_LIBM; }
+void ho_set_exp_mode(int mode) { g_exp_mode = mode == HO_EXP_PORTABLE || mode == HO_EXP_GLIBC ? mode : HO_EXP_LIBM; }
 int ho_get_exp_mode(void) { return g_exp_mode; }
 
 /* exp in IEEE double from basic operations only (Cody & Waite, "Software Manual for
@@ -130,7 +130,90 @@ float ho_exp_port_f(float x) { return (float)ho_exp_port_d((double)x); }
 
 static __attribute__((noinline)) float libm_expf(float x) { return expf(x); }
 
-float ho_expf(float x) { return g_exp_mode == HO_EXP_PORTABLE ? ho_exp_port_f(x) : libm_expf(x); }
+/* glibc's expf (glibc 2.28 and later, sysdeps/ieee754/flt-32/e_expf.c, the algorithm of
+ * Szabolcs Nagy's optimized-routines: exp(x) = 2^(k/32) 2^(r/32) with a 32-entry table of
+ * 2^(i/32) and a cubic in double), as its x86-64 FMA build evaluates it: the compiler
+ * fuses every multiply that feeds an add, so k and r come from the exact product
+ * x * 32/ln2 (fma) and the cubic is three fmas. The reference engine calls the platform
+ * libm's expf (docs/NUMERICS.md), which on this image is that build; the restatement is
+ * checked against it on every one of the 2^32 inputs (tests/test_oracle.py). The table
+ * entries are the correctly rounded doubles of 2^(i/32) minus i << 47 (checked against
+ * a 80-digit computation in the same test). */
+static const uint64_t EXP2F_TAB[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+float ho_exp_glibc_f(float x) {
+    const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32.0;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double shift = 0x1.8p+52;
+    const uint32_t ux = f_bits(x), abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= (f_bits(88.0f) >> 20)) {        /* |x| >= 88 or NaN */
+        if (ux == f_bits(-1.0f / 0.0f)) return 0.0f;
+        if (abstop >= (f_bits(1.0f / 0.0f) >> 20)) return x + x;
+        if (x > 0x1.62e42ep6f) return 1.0f / 0.0f;   /* overflow */
+        if (x < -0x1.9fe368p6f) return 0.0f;         /* underflow */
+    }
+    const double xd = (double)x;
+    double kd = fma(inv_ln2_32, xd, shift);
+    uint64_t ki, t;
+    memcpy(&ki, &kd, 8);
+    kd = kd - shift;
+    const double r = fma(inv_ln2_32, xd, -kd);
+    t = EXP2F_TAB[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &t, 8);
+    const double z = fma(c0, r, c1), r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(z, r2, y);
+    return (float)(y * s);
+}
+
+float ho_expf(float x) {
+    if (g_exp_mode == HO_EXP_PORTABLE) return ho_exp_port_f(x);
+    if (g_exp_mode == HO_EXP_GLIBC) return ho_exp_glibc_f(x);
+    return libm_expf(x);
+}
+
+/* Inputs u in [lo, hi) (float bit patterns) where ho_exp_glibc_f and the platform libm's
+ * expf differ (NaN results compare equal), on nthreads threads. */
+typedef struct { uint64_t lo, hi, bad; } expchk;
+static void *expchk_run(void *p) {
+    expchk *j = (expchk *)p;
+    j->bad = 0;
+    for (uint64_t u = j->lo; u < j->hi; u++) {
+        const float x = bits_f((uint32_t)u), a = libm_expf(x), b = ho_exp_glibc_f(x);
+        if (f_bits(a) != f_bits(b) && !(a != a && b != b)) j->bad++;
+    }
+    return NULL;
+}
+
+uint64_t ho_exp_glibc_mismatches(uint64_t lo, uint64_t hi, int nthreads) {
+    expchk jobs[64];
+    pthread_t th[64];
+    int nt = nthreads < 1 ? 1 : (nthreads > 64 ? 64 : nthreads);
+    for (int i = 0; i < nt; i++) {
+        jobs[i].lo = lo + (hi - lo) * (uint64_t)i / (uint64_t)nt;
+        jobs[i].hi = lo + (hi - lo) * (uint64_t)(i + 1) / (uint64_t)nt;
+    }
+    for (int i = 1; i < nt; i++) pthread_create(&th[i], NULL, expchk_run, &jobs[i]);
+    expchk_run(&jobs[0]);
+    uint64_t bad = jobs[0].bad;
+    for (int i = 1; i < nt; i++) {
+        pthread_join(th[i], NULL);
+        bad += jobs[i].bad;
+    }
+    return bad;
+}
 
 /* ------------------------------------------------------------ canonical helpers (NUMERICS §1, §4) */
 

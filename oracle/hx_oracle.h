@@ -8,6 +8,8 @@
  *
  * What each function restates (reference paths relative to the reference tree):
  *   ho_f16_to_f32 / ho_f32_to_f16   engine/src/platform_common.inc:19-65 (IEEE binary16, RNE)
+ *   ho_exp_glibc_f                  the platform libm's expf the reference calls (glibc 2.35,
+ *                                   sysdeps/ieee754/flt-32/e_expf.c; FMA build)
  *   ho_quantize (Q8, Q4)            engine/src/quant.c:99-228, docs/NUMERICS.md §6
  *   ho_act_quant                    engine/src/quant.c:325-348, docs/NUMERICS.md §2
  *   ho_matmul                       engine/src/quant.c:352-427, docs/NUMERICS.md §3
@@ -30,9 +32,12 @@
  *                    engine (checked against the reference built from source).
  *   HO_EXP_PORTABLE  ho_exp_port_f: Cody-Waite reduction + degree-13 Taylor in IEEE
  *                    double using only +, -, * and exact conversions (no FMA, no libm),
- *                    so it yields the same bits on any IEEE machine, CPU or GPU. The
- *                    HIP kernels use the same definition; with this mode the GPU must
- *                    match the restatement bit for bit.
+ *                    so it yields the same bits on any IEEE machine (within 1 ulp of libm).
+ *   HO_EXP_GLIBC     ho_exp_glibc_f: glibc's expf (sysdeps/ieee754/flt-32/e_expf.c, the
+ *                    x86-64 FMA build) restated with explicit fmas; equal to this image's
+ *                    libm expf on all 2^32 inputs. The HIP kernels use the same
+ *                    definition; with this mode the GPU must match the restatement bit
+ *                    for bit, and so the reference engine.
  * Parity status: every function above is pinned (pinned FNV hashes of the reference's
  * test_quant.c, bit-exact comparison with the reference engine built from source on
  * whole forward passes, closed forms for acceptance); see tests/ for each check.
@@ -48,7 +53,7 @@ extern "C" {
 #endif
 
 enum { HO_F32 = 0, HO_F16 = 1, HO_BF16 = 2, HO_Q8 = 3, HO_Q4 = 4, HO_I32 = 5, HO_U8 = 6 };
-enum { HO_EXP_LIBM = 0, HO_EXP_PORTABLE = 1 };
+enum { HO_EXP_LIBM = 0, HO_EXP_PORTABLE = 1, HO_EXP_GLIBC = 2 };
 
 /* ---- formats and kernels -------------------------------------------------- */
 float    ho_f16_to_f32(uint16_t h);
@@ -67,6 +72,9 @@ void  ho_set_exp_mode(int mode);
 int   ho_get_exp_mode(void);
 float ho_expf(float x);                 /* in the current mode */
 float ho_exp_port_f(float x);
+float ho_exp_glibc_f(float x);
+/* inputs u in [lo, hi) (float bit patterns) where ho_exp_glibc_f and the libm expf differ */
+uint64_t ho_exp_glibc_mismatches(uint64_t lo, uint64_t hi, int nthreads);
 double ho_exp_port_d(double x);
 float ho_dot16(const float *a, const float *b, int64_t n);
 float ho_sum16(const float *a, int64_t n);

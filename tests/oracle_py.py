@@ -15,7 +15,7 @@ ROOT = Path(__file__).resolve().parent.parent
 ORACLE = ROOT / "oracle" / "liboracle.so"
 REF_LIB = ROOT / "oracle" / "_ref" / "libhearth_ref.so"
 
-EXP_LIBM, EXP_PORTABLE = 0, 1
+EXP_LIBM, EXP_PORTABLE, EXP_GLIBC = 0, 1, 2
 _I32P, _FP, _DP = POINTER(c_int32), POINTER(c_float), POINTER(c_double)
 _lib = None
 
@@ -51,6 +51,10 @@ def lib():
         L.ho_expf.argtypes = [c_float]
         L.ho_exp_port_f.restype = c_float
         L.ho_exp_port_f.argtypes = [c_float]
+        L.ho_exp_glibc_f.restype = c_float
+        L.ho_exp_glibc_f.argtypes = [c_float]
+        L.ho_exp_glibc_mismatches.restype = ctypes.c_uint64
+        L.ho_exp_glibc_mismatches.argtypes = [ctypes.c_uint64, ctypes.c_uint64, c_int]
         L.ho_exp_port_d.restype = c_double
         L.ho_exp_port_d.argtypes = [c_double]
         L.ho_open.restype = c_void_p
@@ -86,6 +90,16 @@ def lib():
 
 def set_exp_mode(mode: int) -> None:
     lib().ho_set_exp_mode(mode)
+
+
+def gpu_numerics() -> None:
+    """the oracle mode the GPU build matches bit for bit"""
+    set_exp_mode(EXP_GLIBC)
+
+
+def reference_numerics() -> None:
+    """the oracle mode the reference engine matches bit for bit (the platform libm)"""
+    set_exp_mode(EXP_LIBM)
 
 
 def quantize(dtype: int, x) -> bytes:

@@ -1,5 +1,5 @@
 """The verify step at the Qwen3-30B-A3B shape the benchmark runs, bit for bit against
-the oracle (the CPU restatement in portable-exp mode).
+the oracle (the CPU restatement with the libm's expf restated) and the reference engine.
 
 Model: the benchmark's recipe (container.make_shaped) at the full Qwen3-30B-A3B width:
 hidden 2048, 32 query / 4 KV heads of 128, 128 experts top-8 of FFN 768, vocab 151936,
@@ -21,7 +21,8 @@ Cases (the benchmark configurations):
 - the routed-expert kernels at T = 1, 9, 33, 65 tokens with Zipf(1.1) routing (replayed
   from a trace, as the reference's route replay does), which covers the few-token
   split-K expert kernel (T <= 16) and the general one (T > 16);
-- a 160-token prefill chunk.
+- a 160-token prefill chunk;
+- and the chain verify at 4095 against the reference engine itself (no oracle between).
 """
 from __future__ import annotations
 
@@ -61,7 +62,7 @@ def model(tmp_path_factory):
 @pytest.fixture(scope="module")
 def prefilled(model):
     """The engine after a 4095-token prefill, and the KV rows it wrote."""
-    O.set_exp_mode(O.EXP_PORTABLE)
+    O.gpu_numerics()
     eng = Engine(model, max_seq=CTX + 256, max_batch=512)
     prompt = container.uniform_ints(4242, CTX, SHAPE.vocab).astype(np.int32)
     eng.eval(prompt)
@@ -103,6 +104,31 @@ def test_chain_verify_k8_ctx4095(prefilled, model, tmp_path):
     assert rc == 0 and path == opath and final == ofin
     assert path == [0, 1, 2, 3], path      # drafts 1..3 are the greedy continuation, draft 4 is not
     assert eng.pos == CTX + len(path)
+
+
+@pytest.mark.skipif(not O.REF_LIB.is_file(), reason="reference engine not built (make -C oracle)")
+def test_chain_verify_equals_reference_engine(prefilled, model):
+    """The same verify step against the reference engine itself (compiled from its C
+    sources into oracle/_ref, on the host cores): the reference prefills the 4095-token
+    prompt and evaluates [last] + 8 drafts with all_logits (generate.py:370); the GPU
+    starts from its own prefill. Every logit is equal."""
+    from hearth_amd.engine import Engine as E
+    eng, prompt, snap = prefilled
+    toks = np.concatenate([[prompt[-1]], container.uniform_ints(77, 8, SHAPE.vocab)]).astype(np.int32)
+    runs = []
+    for _ in range(2):          # the same call twice from the same imported context
+        eng.kv_import(snap, CTX)
+        runs.append(eng.eval(toks, all_logits=True))
+    _assert_same(runs[1], runs[0], "a repeated GPU evaluation")
+    ref = E(model, lib=str(O.REF_LIB), threads=THREADS, prefetch="off", max_seq=CTX + 64, cache_gb=16.0)
+    try:
+        ref.eval(prompt)
+        lr = ref.eval(toks, all_logits=True)
+    finally:
+        ref.close()
+    rows = (_bits(runs[0]) != _bits(lr)).any(1)
+    assert not rows.any(), (f"{int(rows.sum())} of 9 rows differ from the reference engine; argmax GPU "
+                            f"{runs[0].argmax(1).tolist()} reference {lr.argmax(1).tolist()}")
 
 
 def _tree_4x4x4():

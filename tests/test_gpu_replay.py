@@ -28,7 +28,7 @@ def _bits(a):
 def test_route_replay_bit_exact(tiny_model, variant_models, tmp_path, name):
     path = tiny_model if name == "tiny" else variant_models(name)
     vocab = container.TINY.vocab if name == "tiny" else 4096
-    O.set_exp_mode(O.EXP_PORTABLE)
+    O.gpu_numerics()
     m = O.Model(path)
     ids = O.synthetic_routes(11, 29, m.n_moe, m.n_experts, m.top_k)
     tr = tmp_path / "replay.hrtr"
@@ -58,7 +58,7 @@ def test_route_replay_bit_exact(tiny_model, variant_models, tmp_path, name):
 
 
 def test_route_replay_off_and_errors(tiny_model, tmp_path):
-    O.set_exp_mode(O.EXP_PORTABLE)
+    O.gpu_numerics()
     m = O.Model(tiny_model)
     ids = O.synthetic_routes(12, 10, m.n_moe, m.n_experts, m.top_k)
     good = tmp_path / "good.hrtr"

@@ -1,5 +1,5 @@
 """The verify engine on the GPU for the other model families' features, against the
-restatement (portable exp), which tests/test_oracle.py pins bit for bit to the reference
+restatement (glibc expf), which tests/test_oracle.py pins bit for bit to the reference
 engine compiled from source on the same containers:
 
 - dsv3_gqa: sigmoid scores with a selection bias, group-limited routing (4 groups, top 2
@@ -37,7 +37,7 @@ def _bits(a):
 def test_variant_bit_exact_with_oracle(variant_models, variant, tmp_path):
     path = variant_models(variant)
     toks = container.uniform_ints(41, 40, 4096)
-    O.set_exp_mode(O.EXP_PORTABLE)
+    O.gpu_numerics()
     om = O.Model(path)
     lo, ro = om.eval(toks, routes=True)
     with Engine(path, max_seq=512) as e:

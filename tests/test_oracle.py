@@ -5,12 +5,14 @@
   library's host quantizer;
 - whole forward passes: bit-exact with the reference engine built from its sources
   (oracle/_ref) and with the committed golden outputs of that engine;
-- the portable exponential against the platform libm and closed forms;
+- the portable exponential against the platform libm and closed forms, and the glibc
+  expf restatement (the device exp) against the libm on every float input;
 - tree evaluation against the chain evaluation of every root path.
 """
 from __future__ import annotations
 
 import math
+import os
 
 import numpy as np
 import pytest
@@ -97,13 +99,16 @@ def test_oracle_matches_reference_golden():
     from pathlib import Path
     path = container.make_tiny(Path(tempfile.mkdtemp()) / "t.hearth", _native.quantize, seed=1)
     assert container.sha256(path) == str(g["sha256"])
-    O.set_exp_mode(O.EXP_LIBM)
+    O.reference_numerics()
     m = O.Model(path)
     lp, rp = m.eval(g["prompt"], routes=True)
     assert np.array_equal(lp[-8:].view(np.uint32), g["prompt_last8"].view(np.uint32))
     assert np.array_equal(lp.argmax(1), g["prompt_argmax"])
-    for t in g["continuation"][1:]:
-        pass
+    # the reference's greedy continuation: one single-token eval per step
+    cont = [int(c) for c in g["continuation"]]
+    assert cont[0] == int(lp[-1].argmax())
+    for i in range(len(cont) - 1):
+        assert int(m.eval([cont[i]])[0].argmax()) == cont[i + 1], i
     m.rewind(128)
     lv, rv = m.eval(g["verify_tokens"], routes=True)
     assert np.array_equal(lv.view(np.uint32), g["verify_logits"].view(np.uint32))
@@ -119,7 +124,7 @@ def test_oracle_matches_reference_engine(tiny_model):
     ref = Engine(tiny_model, lib=str(O.REF_LIB), threads=4, prefetch="off")
     lr = ref.eval(toks, all_logits=True)
     ref.close()
-    O.set_exp_mode(O.EXP_LIBM)
+    O.reference_numerics()
     lo = O.Model(tiny_model).eval(toks)
     assert np.array_equal(lr.view(np.uint32), lo.view(np.uint32))
 
@@ -139,7 +144,7 @@ def test_oracle_matches_reference_engine_variants(variant_models, variant):
     lr = ref.eval(toks, all_logits=True)
     lr2 = ref.eval(toks[:5], all_logits=True)
     ref.close()
-    O.set_exp_mode(O.EXP_LIBM)
+    O.reference_numerics()
     m = O.Model(path)
     lo = m.eval(toks)
     lo2 = m.eval(toks[:5])
@@ -157,7 +162,7 @@ def test_oracle_route_replay_matches_reference_engine(tiny_model, variant_models
     routes."""
     from hearth_amd.engine import Engine
     path = tiny_model if name == "tiny" else variant_models(name)
-    O.set_exp_mode(O.EXP_LIBM)
+    O.reference_numerics()
     m = O.Model(path)
     ids = O.synthetic_routes(7, 37, m.n_moe, m.n_experts, m.top_k)
     tr = tmp_path / "routes.hrtr"
@@ -180,7 +185,7 @@ def test_oracle_route_replay_matches_reference_engine(tiny_model, variant_models
 def test_tree_equals_chain(tiny_model):
     """Every tree node's logits equal the chain evaluation of its root path (bit for bit),
     and committing a path leaves the same KV as evaluating the chain."""
-    O.set_exp_mode(O.EXP_PORTABLE)
+    O.gpu_numerics()
     prompt = container.uniform_ints(5, 40, container.TINY.vocab)
     tok = np.array([17, 5, 9, 300, 4000, 12, 8], dtype=np.int32)
     par = np.array([-1, 0, 0, 1, 1, 2, 4], dtype=np.int32)
@@ -225,7 +230,7 @@ def test_greedy_acceptance_closed_form():
 def test_kv_snapshot_round_trip(tiny_model):
     """ho_kv_export -> ho_kv_import into a fresh model continues exactly like the model
     that computed the context (the layout is plumbing; the rows must arrive intact)"""
-    O.set_exp_mode(O.EXP_PORTABLE)
+    O.gpu_numerics()
     toks = container.uniform_ints(31, 24, container.TINY.vocab)
     a = O.Model(tiny_model, cap=64)
     a.eval(toks[:20], logits=False)
@@ -237,3 +242,38 @@ def test_kv_snapshot_round_trip(tiny_model):
     la, lb = a.eval(toks[20:]), b.eval(toks[20:])
     assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
     assert np.array_equal(a.kv_export(), b.kv_export())
+
+
+
+def test_glibc_expf_restatement_equals_libm_on_every_float():
+    """The device exp (ho_exp_glibc_f restates it) is this image's libm expf, which the
+    reference engine calls: equal on all 2^32 inputs (NaN results compared as NaN)."""
+    bad = O.lib().ho_exp_glibc_mismatches(0, 1 << 32, min(16, os.cpu_count() or 1))
+    assert bad == 0, f"{bad} inputs differ from libm expf"
+
+
+def test_glibc_expf_table_is_2_to_the_i_over_32():
+    """The 32 table entries are the correctly rounded doubles of 2^(i/32) (80 significant
+    digits, then one rounding), stored minus i << 47 as the algorithm expects; and the
+    special values."""
+    import struct
+    from decimal import Decimal, getcontext
+    from fractions import Fraction
+    getcontext().prec = 80
+    ln2 = Decimal(2).ln()
+    want = []
+    for i in range(32):
+        f = Fraction((Decimal(i) / 32 * ln2).exp())
+        b = struct.unpack("<Q", struct.pack("<d", f.numerator / f.denominator))[0]
+        want.append((b - (i << 47)) & 0xFFFFFFFFFFFFFFFF)
+    src = (O.ROOT / "oracle" / "hx_oracle.c").read_text()
+    body = src[src.index("EXP2F_TAB[32] = {"):]
+    body = body[:body.index("};")]
+    import re
+    got = [int(h, 16) for h in re.findall(r"0x([0-9a-f]{16})ull", body)]
+    assert got == want
+    O.set_exp_mode(O.EXP_GLIBC)
+    assert O.lib().ho_expf(0.0) == 1.0 and O.lib().ho_expf(1.0) == np.float32(math.e)
+    assert O.lib().ho_expf(89.0) == float("inf") and O.lib().ho_expf(-104.0) == 0.0
+    assert O.lib().ho_expf(float("-inf")) == 0.0 and math.isnan(O.lib().ho_expf(float("nan")))
+    O.set_exp_mode(O.EXP_LIBM)
