@@ -1,21 +1,23 @@
-"""Generation with lossless prompt-lookup speculative decoding, verified on the GPU.
+"""Generation on the MI355X verify engine: prompt-lookup speculative decoding in which a
+decode step is one device call.
 
-The same interface and emitted tokens as the reference's python/hearth/generate.py:
-`generate()` (generate.py:292-400) yields `Token`s with running `GenStats`
-(generate.py:189-225), drafts come from an n-gram lookup over the context itself
-(`NgramIndex`, generate.py:150-186) and `Sampler` carries the reference's settings
-(generate.py:31-126).
+Public surface: the names, fields, argument checks and messages of the reference's
+python/hearth/generate.py (Sampler 31-126, NgramIndex 150-186, GenStats / Token 189-225,
+sync_prefix 250-266, generate 292-400), so front ends written against it run unchanged.
 
-The difference is where a verify step runs. The reference evaluates [last] + draft
-with all logits, walks the draft in numpy and rewinds the KV cache
-(generate.py:365-392). Here one engine call does all three on the device:
-`verify_greedy` (argmax compare) or `verify_sample` (exact speculative sampling with a
-point-mass proposal, fed the uniforms the reference would draw from the sampler's
-generator) evaluates the chain, accepts on the GPU and commits the accepted prefix, so
-no [k+1][V] logits block crosses PCIe. Greedy output is token-for-token the output of
-plain greedy decoding because batched evaluation is bit-identical to sequential
-evaluation; sampled output has the plain output's distribution, and with a fixed seed
-it is the sample the reference's own speculative loop draws on the same logits.
+How a generation runs here. A `_Run` owns the committed token sequence, the drafter (an
+NgramIndex over that sequence, or none) and the running GenStats. `_Run.advance()` is one
+decode forward: it asks the drafter for up to `room` tokens and hands [last] + draft to
+the engine's verify call, which evaluates the chain, accepts on the GPU (argmax
+comparison, or exact speculative sampling of a point-mass proposal fed the uniforms the
+reference would draw) and commits the accepted prefix in the KV cache. Only the accepted
+path and the next token come back to the host; no logits block crosses PCIe. `generate()`
+itself only applies the stop and length rules to the tokens each forward commits.
+
+Greedy output equals plain greedy decoding token for token (batched evaluation is
+bit-identical to sequential evaluation); sampled output has the plain output's
+distribution, and for a given seed it is the sample the reference's own speculative loop
+draws from the same logits.
 
 `engine` is anything with `pos`, `reset()`, `rewind(pos)`, `eval(tokens)`,
 `verify_greedy(tokens)` and `verify_sample(tokens, parent, sampler, u=...)`
@@ -35,17 +37,35 @@ __all__ = ["Sampler", "GenStats", "Token", "generate", "generate_ids", "NgramInd
            "kv_capacity", "check_speculative", "SPECULATIVE_MODES"]
 
 SPECULATIVE_MODES = ("none", "ngram")
+_MODE_ALIASES = {None: "none", False: "none", "none": "none", "off": "none", "": "none",
+                 True: "ngram", "ngram": "ngram", "prompt": "ngram", "prompt_lookup": "ngram"}
+
+_BAD_LOGITS = "logits contain NaN or +inf, or are all -inf"
+
+
+# ---------------------------------------------------------------- sampling settings
+
+def _finite_nonneg(v) -> bool:
+    return bool(np.isfinite(v)) and v >= 0
+
+
+# (field, predicate, message) in the order the reference checks them (generate.py:44-55)
+_SAMPLER_RULES = (
+    ("temperature", _finite_nonneg, "temperature must be >= 0, got {}"),
+    ("top_k", lambda v: v >= 0, "top_k must be >= 0, got {}"),
+    ("top_p", lambda v: 0.0 < v <= 1.0, "top_p must be in (0, 1], got {}"),
+    ("min_p", lambda v: 0.0 <= v <= 1.0, "min_p must be in [0, 1], got {}"),
+    ("repetition_penalty", lambda v: bool(np.isfinite(v)) and v > 0, "repetition_penalty must be > 0, got {}"),
+)
 
 
 @dataclass
 class Sampler:
-    """Sampling settings, applied in the reference's order (generate.py:31-36):
-    repetition penalty, temperature, top-k, top-p, min-p. temperature 0 is greedy
-    (argmax, first index wins ties). `rng` is the generator the sampled verify steps
-    draw their uniforms from (seeded by `seed`).
-
-    probs / argmax / sample evaluate one logits row on the GPU (hearth_gpu_probs,
-    hearth_gpu_accept_sample) with the reference's numerics (generate.py:69-126)."""
+    """Sampling settings, applied in the order repetition penalty, temperature, top-k,
+    top-p, min-p; temperature 0 is greedy (argmax, first index wins ties). Draws come
+    from `rng`, a generator seeded by `seed`. probs / argmax / sample evaluate one logits
+    row on the GPU (hearth_gpu_probs, hearth_gpu_accept_sample), in float64 with the
+    reference's operation order."""
     temperature: float = 1.0
     top_k: int = 0
     top_p: float = 1.0
@@ -55,17 +75,10 @@ class Sampler:
     rng: np.random.Generator = field(init=False, repr=False, compare=False)
 
     def __post_init__(self):
-        # the reference's argument checks and messages (generate.py:44-55)
-        if not np.isfinite(self.temperature) or self.temperature < 0:
-            raise ValueError(f"temperature must be >= 0, got {self.temperature}")
-        if self.top_k < 0:
-            raise ValueError(f"top_k must be >= 0, got {self.top_k}")
-        if not 0.0 < self.top_p <= 1.0:
-            raise ValueError(f"top_p must be in (0, 1], got {self.top_p}")
-        if not 0.0 <= self.min_p <= 1.0:
-            raise ValueError(f"min_p must be in [0, 1], got {self.min_p}")
-        if not np.isfinite(self.repetition_penalty) or self.repetition_penalty <= 0:
-            raise ValueError(f"repetition_penalty must be > 0, got {self.repetition_penalty}")
+        for name, ok, msg in _SAMPLER_RULES:
+            v = getattr(self, name)
+            if not ok(v):
+                raise ValueError(msg.format(v))
         self.rng = np.random.default_rng(self.seed)
 
     @classmethod
@@ -81,44 +94,50 @@ class Sampler:
         return self.repetition_penalty != 1.0
 
     def device(self, context=None, *, greedy: bool = False) -> _eng.HearthSampler:
-        """The hearth_sampler of these settings; `context` (the ids the penalty applies
-        to) is only passed when the penalty is on. greedy=True keeps the penalty and
-        sets temperature 0 (the reference's argmax of penalised logits)."""
-        ctx = context if self.uses_context and context is not None and len(context) else None
+        """These settings as a hearth_sampler. The penalty context travels only when the
+        penalty is on; greedy=True keeps the penalty and sets temperature 0 (the argmax
+        of the penalised logits)."""
+        ctx = None
+        if self.uses_context and context is not None and len(context):
+            ctx = context
         return _eng.make_sampler(0.0 if greedy else self.temperature, self.top_k, self.top_p, self.min_p,
                                  self.repetition_penalty, ctx)
 
-    @staticmethod
-    def _row(logits) -> np.ndarray:
-        return np.ascontiguousarray(logits, dtype=np.float32).reshape(1, -1)
-
     def probs(self, logits, context=None) -> np.ndarray:
-        """The final sampling distribution of one logits row (float64, one-hot when
-        greedy). NaN or +inf logits, or all -inf, raise ValueError."""
-        rc, p = _eng.gpu_probs(self._row(logits), sampler=self.device(context))
-        if rc < 0:
-            raise ValueError("logits contain NaN or +inf, or are all -inf")
+        """The final distribution of one logits row (float64; one-hot when greedy)."""
+        rc, p = _eng.gpu_probs(_one_row(logits), sampler=self.device(context))
+        _raise_on_bad(rc)
         return p[0]
 
     def argmax(self, logits, context=None) -> int:
-        rc, _, fin = _eng.accept_sample(self._row(logits), [0], None, self.device(context, greedy=True))
-        if rc < 0:
-            raise ValueError("logits contain NaN or +inf, or are all -inf")
-        return fin
+        rc, _, tok = _eng.accept_sample(_one_row(logits), [0], None, self.device(context, greedy=True))
+        _raise_on_bad(rc)
+        return tok
 
     def sample(self, logits, context=None) -> int:
-        """argmax when greedy, else one inverse-CDF draw (one uniform from rng)."""
+        """The argmax when greedy, else one inverse-CDF draw (one uniform from rng)."""
         if self.is_greedy:
             return self.argmax(logits, context)
-        rc, _, fin = _eng.accept_sample(self._row(logits), [0], None, self.device(context),
-                                        u=np.array([0.0, self.rng.random()]))
-        if rc < 0:
-            raise ValueError("logits contain NaN or +inf, or are all -inf")
-        return fin
+        u = np.array([0.0, self.rng.random()])
+        rc, _, tok = _eng.accept_sample(_one_row(logits), [0], None, self.device(context), u=u)
+        _raise_on_bad(rc)
+        return tok
 
+
+def _one_row(logits) -> np.ndarray:
+    return np.ascontiguousarray(logits, dtype=np.float32).reshape(1, -1)
+
+
+def _raise_on_bad(rc: int) -> None:
+    if rc < 0:
+        raise ValueError(_BAD_LOGITS)
+
+
+# ---------------------------------------------------------------- drafting
 
 class NgramIndex:
-    """Prompt-lookup index over a growing token sequence (generate.py:150-186).
+    """Prompt-lookup index over a growing token sequence (the reference's drafter,
+    generate.py:150-186).
 
     For each n-gram of length 1..max_n it keeps the latest start position that is
     followed by at least one token, so the current suffix never matches itself, and
@@ -153,9 +172,15 @@ class NgramIndex:
         return []
 
 
+# ---------------------------------------------------------------- statistics
+
+def _ratio(num: float, den: float) -> float:
+    return num / den if den else 0.0
+
+
 @dataclass
 class GenStats:
-    """Running totals of one generation (generate.py:189-225, same fields)."""
+    """Running totals of one generation (the reference's fields, generate.py:189-225)."""
     prompt_tokens: int = 0
     reused_tokens: int = 0         # prompt tokens whose KV the engine already held
     new_tokens: int = 0            # tokens yielded (a stop token is not)
@@ -169,28 +194,16 @@ class GenStats:
     finish_reason: str | None = None   # "stop" or "length"
     stop_id: int | None = None
 
-    @property
-    def acceptance_rate(self) -> float:
-        return self.accepted / self.drafted if self.drafted else 0.0
-
-    @property
-    def tokens_per_forward(self) -> float:
-        return self.decode_tokens / self.forwards if self.forwards else 0.0
-
-    @property
-    def prefill_tok_s(self) -> float:
-        n = self.prompt_tokens - self.reused_tokens
-        return n / self.prefill_s if self.prefill_s > 0 else 0.0
-
-    @property
-    def decode_tok_s(self) -> float:
-        return self.decode_tokens / self.decode_s if self.decode_s > 0 else 0.0
+    acceptance_rate = property(lambda self: _ratio(self.accepted, self.drafted))
+    tokens_per_forward = property(lambda self: _ratio(self.decode_tokens, self.forwards))
+    prefill_tok_s = property(lambda self: _ratio(self.prompt_tokens - self.reused_tokens, self.prefill_s))
+    decode_tok_s = property(lambda self: _ratio(self.decode_tokens, self.decode_s))
 
     def as_dict(self) -> dict:
-        d = dict(self.__dict__)
-        d.update(acceptance_rate=self.acceptance_rate, tokens_per_forward=self.tokens_per_forward,
-                 prefill_tok_s=self.prefill_tok_s, decode_tok_s=self.decode_tok_s)
-        return d
+        out = dict(self.__dict__)
+        for name in ("acceptance_rate", "tokens_per_forward", "prefill_tok_s", "decode_tok_s"):
+            out[name] = getattr(self, name)
+        return out
 
 
 class Token(NamedTuple):
@@ -201,52 +214,48 @@ class Token(NamedTuple):
     stats: GenStats    # running totals (one object for the whole generation)
 
 
+# ---------------------------------------------------------------- KV bookkeeping
+
 def kv_capacity(engine) -> int:
+    """Positions the engine's KV cache holds (kv_capacity, else the model's max_seq)."""
     cap = getattr(engine, "kv_capacity", None)
-    if cap is None:
-        info = getattr(engine, "info", None) or {}
-        cap = int(info.get("max_seq", 0)) or (1 << 30)
-    return int(cap)
+    if cap is not None:
+        return int(cap)
+    info = getattr(engine, "info", None) or {}
+    return int(info.get("max_seq", 0)) or (1 << 30)
 
 
 def common_prefix(a: Sequence[int], b: Sequence[int]) -> int:
+    """Length of the longest common prefix of two token sequences."""
     n = min(len(a), len(b))
-    if n == 0:
-        return 0
-    ne = np.flatnonzero(np.asarray(a[:n], dtype=np.int64) != np.asarray(b[:n], dtype=np.int64))
-    return int(ne[0]) if ne.size else n
+    for i, (x, y) in enumerate(zip(a[:n], b[:n])):
+        if int(x) != int(y):
+            return i
+    return n
 
 
 def sync_prefix(engine, held: Sequence[int] | None, prompt: Sequence[int]) -> int:
     """Rewinds the engine to the longest prefix of `prompt` whose KV it holds and
-    returns its length (generate.py:250-266). `held` lists the tokens behind the
-    engine's KV (None: unknown, so reset). At least one prompt token is left to
-    evaluate, since the first generated token needs its logits."""
-    if held is None:
+    returns that length. `held` lists the tokens behind the engine's KV (None: unknown,
+    so the engine is reset). The last prompt token is always left to evaluate: the first
+    generated token needs its logits."""
+    if held is None or engine.pos > len(held):
         engine.reset()
         return 0
     pos = engine.pos
-    if pos > len(held):
-        engine.reset()
-        return 0
-    k = min(common_prefix(held[:pos], prompt), len(prompt) - 1, pos)
-    if k < pos:
-        engine.rewind(k)
-    return k
-
-
-def _mode(speculative) -> str:
-    if speculative in (None, False, "none", "off", ""):
-        return "none"
-    if speculative in (True, "ngram", "prompt", "prompt_lookup"):
-        return "ngram"
-    raise ValueError(f"speculative must be one of {SPECULATIVE_MODES}, got {speculative!r}")
+    keep = min(common_prefix(held[:pos], prompt), len(prompt) - 1, pos)
+    if keep < pos:
+        engine.rewind(keep)
+    return keep
 
 
 def check_speculative(speculative, draft_len: int, ngram_n: int) -> str:
     """Validates the speculative settings (front ends reject a bad configuration at
-    start-up) and returns the normalised mode."""
-    mode = _mode(speculative)
+    start-up) and returns the normalised mode ("none" or "ngram")."""
+    try:
+        mode = _MODE_ALIASES[speculative]
+    except (KeyError, TypeError):
+        raise ValueError(f"speculative must be one of {SPECULATIVE_MODES}, got {speculative!r}") from None
     for name, v, lo in (("draft_len", draft_len, 0), ("ngram_n", ngram_n, 1)):
         if isinstance(v, bool) or not isinstance(v, (int, np.integer)):
             raise ValueError(f"{name} must be an integer, got {v!r}")
@@ -255,31 +264,99 @@ def check_speculative(speculative, draft_len: int, ngram_n: int) -> str:
     return mode
 
 
-def _chain_step(engine, seq: list[int], draft: list[int], sampler: Sampler) -> tuple[int, int]:
-    """One verify forward of [seq[-1]] + draft on the device; the engine then holds
-    seq plus the accepted drafts. Returns (accepted drafts, next token).
+# ---------------------------------------------------------------- one generation
 
-    The penalty context of row i is seq + draft[:i] (generate.py:372-375): the
-    sampler's context is seq and the device appends the path tokens. A sampled step
-    takes the reference's uniforms in the reference's order (one per tried draft, a
-    second one at a rejection, one for the final draw when every draft holds;
-    generate.py:137-147,385) and leaves rng advanced by exactly that many."""
-    toks = [seq[-1]] + draft
+def _device_verify(engine, context: list[int], draft: list[int], sampler: Sampler) -> tuple[int, int]:
+    """One verify forward of [context[-1]] + draft; afterwards the engine holds context
+    plus the accepted drafts. Returns (accepted drafts, next token).
+
+    The penalty context of draft row i is context + draft[:i] (generate.py:372-375): the
+    device sampler gets `context` and appends the path tokens itself. A sampled step uses
+    the reference's uniforms in the reference's order (one per tried draft, a second at a
+    rejection, one for the final draw when every draft holds; generate.py:137-147,385)
+    and leaves rng advanced by exactly the number it used."""
+    toks = [context[-1], *draft]
     k = len(draft)
-    if sampler.is_greedy:
-        if sampler.uses_context:
-            path, fin, _ = engine.verify_sample(toks, None, sampler.device(seq, greedy=True), u=np.zeros(2 * (k + 1)))
-        else:
-            path, fin, _ = engine.verify_greedy(toks)
-        return len(path) - 1, int(fin)
+    if sampler.is_greedy and not sampler.uses_context:
+        path, tok, _ = engine.verify_greedy(toks)
+        return len(path) - 1, int(tok)
+    if sampler.is_greedy:   # argmax of penalised logits: the sampled walk at temperature 0
+        path, tok, _ = engine.verify_sample(toks, None, sampler.device(context, greedy=True), u=np.zeros(2 * (k + 1)))
+        return len(path) - 1, int(tok)
     rng = sampler.rng
-    state = rng.bit_generator.state
-    stream = rng.random(k + 1)
-    path, fin, _ = engine.verify_sample(toks, None, sampler.device(seq), u=_eng.chain_uniforms(stream, k))
-    n_acc = len(path) - 1
-    rng.bit_generator.state = state
-    rng.random(n_acc + (1 if n_acc < k else 0) + 1)
-    return n_acc, int(fin)
+    saved = rng.bit_generator.state
+    u = _eng.chain_uniforms(rng.random(k + 1), k)
+    path, tok, _ = engine.verify_sample(toks, None, sampler.device(context), u=u)
+    accepted = len(path) - 1
+    used = accepted + 1 + (accepted < k)
+    rng.bit_generator.state = saved
+    rng.random(used)
+    return accepted, int(tok)
+
+
+class _Run:
+    """The state of one generation: the committed sequence, the drafter, the limits and
+    the statistics. After prefill() and every advance(), `pending` holds the tokens the
+    last forward committed, in order, and the engine holds all of them but the last."""
+
+    def __init__(self, engine, prompt: list[int], sampler: Sampler, drafter: NgramIndex | None, draft_len: int,
+                 max_new: int, cap: int, stats: GenStats):
+        self.engine, self.sampler, self.drafter = engine, sampler, drafter
+        self.draft_len, self.max_new, self.cap, self.stats = draft_len, max_new, cap, stats
+        self.seq = list(prompt)
+        self.pending: list[int] = []
+        self.step = 0
+        self.drafted = self.accepted = 0
+
+    def prefill(self, held) -> None:
+        st, prompt = self.stats, self.seq
+        st.reused_tokens = sync_prefix(self.engine, held, prompt)
+        t0 = time.perf_counter()
+        if len(prompt) - st.reused_tokens > 1:
+            self.engine.eval(prompt[st.reused_tokens:-1])
+        _, first = _device_verify(self.engine, self.seq, [], self.sampler)
+        st.prefill_s = time.perf_counter() - t0
+        self.pending = [first]
+
+    def commit(self, tok: int) -> None:
+        self.seq.append(tok)
+        if self.drafter is not None:
+            self.drafter.append(tok)
+
+    def base(self) -> int:
+        """The engine's position, which must hold all of seq but its last token."""
+        pos = self.engine.pos
+        if pos != len(self.seq) - 1:
+            raise RuntimeError(f"engine position {pos} out of sync with sequence length {len(self.seq)}")
+        return pos
+
+    def advance(self, base: int) -> None:
+        """One decode forward from position base. Its draft may hold up to the draft
+        length, what the token budget leaves after the forward's own token, and the KV
+        positions left."""
+        st = self.stats
+        n = min(self.draft_len, self.max_new - st.new_tokens - 1, self.cap - base - 1)
+        draft = self.drafter.propose(n) if self.drafter is not None and n > 0 else []
+        t0 = time.perf_counter()
+        self.step += 1
+        st.forwards += 1
+        self.accepted, final = _device_verify(self.engine, self.seq, draft, self.sampler)
+        self.drafted = len(draft)
+        if draft:
+            st.draft_steps += 1
+            st.drafted += self.drafted
+            st.accepted += self.accepted
+        self.pending = draft[:self.accepted] + [final]
+        st.decode_s += time.perf_counter() - t0
+
+    def release(self) -> None:
+        """Cuts the KV back to the yielded tokens (a forward commits its accepted drafts
+        before they are yielded, and the caller may stop in between)."""
+        try:
+            if self.engine.pos > len(self.seq):
+                self.engine.rewind(len(self.seq))
+        except Exception:
+            pass
 
 
 def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampler: Sampler | None = None,
@@ -292,9 +369,8 @@ def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampl
     Once a token has been yielded or the generator has returned (max_new_tokens == 0
     included), and from then on even if it is closed or interrupted, the engine holds a
     prefix of prompt + yielded tokens of length engine.pos (all but the last token
-    after a normal finish). If it raises before that, the KV content is unspecified.
-    """
-    sampler = sampler if sampler is not None else Sampler.greedy()
+    after a normal finish). If it raises before that, the KV content is unspecified."""
+    sampler = Sampler.greedy() if sampler is None else sampler
     mode = check_speculative(speculative, draft_len, ngram_n)
     if max_new_tokens < 0:
         raise ValueError("max_new_tokens must be >= 0")
@@ -304,7 +380,7 @@ def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampl
     cap = kv_capacity(engine)
     if len(prompt) > cap:
         raise ValueError(f"prompt has {len(prompt)} tokens but the KV cache holds {cap}")
-    stop = frozenset(int(s) for s in stop_ids)
+    stops = frozenset(int(s) for s in stop_ids)
     st = GenStats(prompt_tokens=len(prompt))
     if max_new_tokens == 0:
         # nothing is evaluated, but the engine still ends up holding a prefix of this
@@ -313,70 +389,38 @@ def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampl
         st.finish_reason = "length"
         return st
 
-    seq = list(prompt)
-    index = NgramIndex(ngram_n, seq) if mode == "ngram" else None
+    run = _Run(engine, prompt, sampler, NgramIndex(ngram_n, prompt) if mode == "ngram" else None, draft_len,
+               max_new_tokens, cap, st)
     try:
-        k = sync_prefix(engine, held, prompt)
-        st.reused_tokens = k
-        t0 = time.perf_counter()
-        if len(prompt) - k > 1:
-            engine.eval(prompt[k:-1])
-        _, first = _chain_step(engine, seq, [], sampler)
-        st.prefill_s = time.perf_counter() - t0
-        new, step, drafted, n_acc = [first], 0, 0, 0
-
+        run.prefill(held)
         while True:
-            for tok in new:
-                if step > 0:
-                    st.decode_tokens += 1
-                if tok in stop:
+            for tok in run.pending:
+                st.decode_tokens += run.step > 0
+                if tok in stops:
                     st.finish_reason, st.stop_id = "stop", tok
                     return st
-                seq.append(tok)
-                if index is not None:
-                    index.append(tok)
+                run.commit(tok)
                 st.new_tokens += 1
-                yield Token(tok, step, drafted, n_acc, st)
+                yield Token(tok, run.step, run.drafted, run.accepted, st)
                 if st.new_tokens >= max_new_tokens:
                     st.finish_reason = "length"
                     return st
-
-            base = engine.pos                      # holds seq[:-1]; seq[-1] is fed next
-            if base != len(seq) - 1:
-                raise RuntimeError(f"engine position {base} out of sync with sequence length {len(seq)}")
+            base = run.base()
             if base + 1 > cap:
                 st.finish_reason = "length"
                 return st
-            room = min(draft_len, max_new_tokens - st.new_tokens - 1, cap - base - 1)
-            draft = index.propose(room) if index is not None and room > 0 else []
-            t0 = time.perf_counter()
-            step += 1
-            st.forwards += 1
-            n_acc, final = _chain_step(engine, seq, draft, sampler)
-            new = draft[:n_acc] + [final]
-            drafted = len(draft)
-            if draft:
-                st.draft_steps += 1
-                st.drafted += drafted
-                st.accepted += n_acc
-            st.decode_s += time.perf_counter() - t0
+            run.advance(base)
     finally:
-        # the post-condition holds even when the generator is closed inside a burst of
-        # accepted drafts (the device committed them before they were yielded)
-        try:
-            if engine.pos > len(seq):
-                engine.rewind(len(seq))
-        except Exception:
-            pass
+        run.release()
 
 
 def generate_ids(engine, prompt_ids, max_new_tokens=256, sampler=None, stop_ids=(), speculative="none",
                  draft_len=4, ngram_n=3, *, held=None) -> tuple[list[int], GenStats]:
     """All tokens of generate() and its GenStats."""
+    ids: list[int] = []
     gen = generate(engine, prompt_ids, max_new_tokens, sampler, stop_ids, speculative, draft_len, ngram_n, held=held)
-    out = []
-    while True:
-        try:
-            out.append(next(gen).id)
-        except StopIteration as e:
-            return out, e.value
+    try:
+        while True:
+            ids.append(next(gen).id)
+    except StopIteration as done:
+        return ids, done.value
