@@ -283,6 +283,14 @@ TINY_VARIANTS = {"dsv3_gqa": TINY_DSV3_GQA, "qwen2": TINY_QWEN2, "olmoe": TINY_O
 
 QWEN3_30B_A3B = Shape(n_layers=48, d_model=2048, n_heads=32, n_kv_heads=4, head_dim=128, n_experts=128, top_k=8,
                       expert_ffn=768, vocab=151936, max_seq=8192)
+# DeepSeek-V3 widths (multi-head latent attention, 256 routed experts top-8 + a shared
+# expert, sigmoid scores with a selection bias, 8 groups top-4, routed scale 2.5),
+# depth cut to 3 dense + 20 MoE layers.
+DEEPSEEK_V3 = Shape(n_layers=23, d_model=7168, n_heads=128, n_kv_heads=128, head_dim=192, n_experts=256, top_k=8,
+                    expert_ffn=2048, vocab=129280, max_seq=8192, arch="deepseek_v3", qk_norm=0, rope_style=1,
+                    shared_ffn=2048, score_fn=1, score_bias=1, n_group=8, topk_group=4, norm_topk=1,
+                    routed_scale=2.5, n_dense=3, dense_ffn=18432, attn_kind=1, q_lora=1536, kv_lora=512, nope=128,
+                    rope_qk=64, v_head=128)
 
 
 def _rope_dim(s: Shape) -> int:
@@ -434,45 +442,84 @@ class _RowPool:
 def make_shaped(path, shape: Shape = QWEN3_30B_A3B, seed: int = 0, n_unique_slabs: int = 32,
                 n_layers: int | None = None) -> Path:
     """A real-shaped model with random weights for throughput runs: Q4 experts, Q8
-    attention / embedding / lm_head, F32 routers (N(0, 2.5^2/D), distinct per layer) and
-    unit norms. Expert slabs cycle over n_unique_slabs physical slabs (aliased entries);
-    the engine still holds one HBM copy per (layer, expert)."""
+    attention / dense FFN / shared expert / embedding / lm_head, F32 routers (N(0,
+    2.5^2/D), distinct per layer), unit norms (norms before a low-rank projection drawn
+    near 1). GQA with per-head qk-norm, or multi-head latent attention (attn_kind 1);
+    leading dense layers, a shared expert and the routing settings follow the shape.
+    Expert slabs cycle over n_unique_slabs physical slabs (aliased entries); the engine
+    still gives every (layer, expert) its own copy."""
     s = shape if n_layers is None else Shape(**{**shape.__dict__, "n_layers": n_layers})
     rng = np.random.default_rng(seed)
     D, H, Hkv, hd, E, F, V, L = s.d_model, s.n_heads, s.n_kv_heads, s.head_dim, s.n_experts, s.expert_ffn, s.vocab, s.n_layers
     w = ContainerWriter(_meta(s, f"synthetic:{s.arch}:seed{seed}"))
     ones = np.ones(D, dtype=np.float32).tobytes()
     pool = _RowPool(rng)
-    w.add("tok_embd", Q8, (V, D), pool.rows(Q8, V, D, 1))
-    w.add("lm_head", Q8, (V, D), pool.rows(Q8, V, D, 2))
+
+    def q8(name, rows, cols, salt):
+        w.add(name, Q8, (rows, cols), pool.rows(Q8, rows, cols, salt))
+
+    def near_one(name, n):
+        w.add(name, F32, (n,), (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32).tobytes())
+
+    q8("tok_embd", V, D, 1)
+    q8("lm_head", V, D, 2)
     w.add("out_norm", F32, (D,), ones)
-    w.add("rope_inv_freq", F32, (hd // 2,), rope_inv_freq(s).tobytes())
+    w.add("rope_inv_freq", F32, (_rope_dim(s) // 2,), rope_inv_freq(s).tobytes())
+    n_moe = sum(1 for l in range(L) if l >= s.n_dense)
     nb, og, ou, od = slab_layout(Q4, D, F)
     slabs = []
-    for i in range(min(n_unique_slabs, L * E)):
+    for i in range(min(n_unique_slabs, max(1, n_moe * E))):
         slab = bytearray(nb)
-        for off, (rows, cols) in ((og, (F, D)), (ou, (F, D)), (od, (D, F))):
-            b = _random_blocks(rng, Q4, rows, cols)
+        for j, (off, (rows, cols)) in enumerate(((og, (F, D)), (ou, (F, D)), (od, (D, F)))):
+            b = pool.rows(Q4, rows, cols, 7919 + 3 * i + j)
             slab[off:off + len(b)] = b
         slabs.append(bytes(slab))
+    first, n_seen = {}, 0      # unique slab -> (layer, expert) holding it; MoE entries so far
     for l in range(L):
         p = f"blk.{l}."
         w.add(p + "attn_norm", F32, (D,), ones)
         w.add(p + "ffn_norm", F32, (D,), ones)
-        w.add(p + "attn_q", Q8, (H * hd, D), pool.rows(Q8, H * hd, D, 10 * l + 3))
-        w.add(p + "attn_k", Q8, (Hkv * hd, D), pool.rows(Q8, Hkv * hd, D, 10 * l + 4))
-        w.add(p + "attn_v", Q8, (Hkv * hd, D), pool.rows(Q8, Hkv * hd, D, 10 * l + 5))
-        w.add(p + "attn_o", Q8, (D, H * hd), pool.rows(Q8, D, H * hd, 10 * l + 6))
-        w.add(p + "attn_q_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
-        w.add(p + "attn_k_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+        if s.attn_kind == 1:
+            qh = s.nope + s.rope_qk
+            if s.q_lora:
+                q8(p + "attn_q_a", s.q_lora, D, 10 * l + 3)
+                near_one(p + "attn_q_a_norm", s.q_lora)
+                q8(p + "attn_q_b", H * qh, s.q_lora, 10 * l + 4)
+            else:
+                q8(p + "attn_q", H * qh, D, 10 * l + 3)
+            q8(p + "attn_kv_a", s.kv_lora + s.rope_qk, D, 10 * l + 5)
+            near_one(p + "attn_kv_a_norm", s.kv_lora)
+            q8(p + "attn_kv_b", H * (s.nope + s.v_head), s.kv_lora, 10 * l + 6)
+            q8(p + "attn_o", D, H * s.v_head, 10 * l + 7)
+        else:
+            q8(p + "attn_q", H * hd, D, 10 * l + 3)
+            q8(p + "attn_k", Hkv * hd, D, 10 * l + 4)
+            q8(p + "attn_v", Hkv * hd, D, 10 * l + 5)
+            q8(p + "attn_o", D, H * hd, 10 * l + 6)
+            if s.qk_norm == 1:
+                w.add(p + "attn_q_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+                w.add(p + "attn_k_norm", F32, (hd,), np.ones(hd, np.float32).tobytes())
+        if l < s.n_dense:
+            q8(p + "ffn_gate", s.dense_ffn, D, 10 * l + 8)
+            q8(p + "ffn_up", s.dense_ffn, D, 10 * l + 9)
+            q8(p + "ffn_down", D, s.dense_ffn, 10 * l + 10)
+            continue
         router = (rng.standard_normal((E, D), dtype=np.float32) * np.float32(2.5 / math.sqrt(D))).astype(np.float32)
         w.add(p + "moe_router", F32, (E, D), router.tobytes())
+        if s.score_bias:
+            w.add(p + "moe_router_bias", F32, (E,), (0.05 * rng.standard_normal(E)).astype(np.float32).tobytes())
+        if s.shared_ffn:
+            q8(p + "shexp_gate", s.shared_ffn, D, 10 * l + 8)
+            q8(p + "shexp_up", s.shared_ffn, D, 10 * l + 9)
+            q8(p + "shexp_down", D, s.shared_ffn, 10 * l + 10)
         for e in range(E):
-            i = (l * E + e) % len(slabs)
-            if (l * E + e) < len(slabs):
+            i = n_seen % len(slabs)
+            if n_seen < len(slabs):
                 w.add_expert(l, e, Q4, slabs[i])
+                first[i] = (l, e)
             else:
-                w.alias_expert(l, e, divmod(i, E))
+                w.alias_expert(l, e, first[i])
+            n_seen += 1
     return w.write(path)
 
 
@@ -489,6 +536,20 @@ def zipf_routes(seed: int, rows: int, n_moe: int, n_experts: int, k: int, s: flo
     keys = logp[None, None, :] + rng.gumbel(size=(rows, n_moe, n_experts))
     top = np.argsort(-keys, axis=-1, kind="stable")[..., :k]                   # ranks
     return np.take_along_axis(np.broadcast_to(perm[None], (rows, n_moe, n_experts)), top, -1).astype(np.uint16)
+
+
+def write_route_trace(path, ids, n_layers: int, n_experts: int) -> Path:
+    """A routing-trace file (FORMAT.md §9) of ids [rows][n_moe][k]: 'HRTR', version 1,
+    n_layers, E, K, n_moe as little-endian uint32, then the rows as uint16 expert ids
+    (what hearth_trace_start writes and hearth_route_replay reads)."""
+    a = np.ascontiguousarray(ids, dtype="<u2")
+    rows, n_moe, k = a.shape
+    hdr = np.array([0x52545248, 1, n_layers, n_experts, k, n_moe], dtype="<u4")
+    path = Path(path)
+    with open(path, "wb") as f:
+        f.write(hdr.tobytes())
+        f.write(a.tobytes())
+    return path
 
 
 def sha256(path, chunk: int = 1 << 24) -> str:

@@ -25,6 +25,7 @@
 #include <memory>
 #include <string>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include "hearth.h"
@@ -382,6 +383,13 @@ bool hearth_engine::upload(std::string &msg) {
         m.d = (const uint16_t *)dalloc(sizeof(uint16_t) * (size_t)m.nbp * m.rows_pad);
         return m;
     };
+    auto qmat_copy = [&](const QMat &dst, const QMat &src) {   /* same dtype and shape */
+        const size_t wb = (size_t)(src.rows_pad / 16) * src.nbp * 1024 / (src.dtype == HEARTH_Q4 ? 2 : 1);
+        ck(hipMemcpyAsync((void *)dst.w, src.w, wb, hipMemcpyDeviceToDevice, st));
+        ck(hipMemcpyAsync((void *)dst.d, src.d, sizeof(uint16_t) * (size_t)src.nbp * src.rows_pad,
+                          hipMemcpyDeviceToDevice, st));
+    };
+    std::unordered_map<uint64_t, ExpertW> first_copy;   /* slab offset -> the matrices of its first entry */
     auto mat = [&](int layer, const char *name, DMat &out) -> bool {
         const Tensor *t = layer < 0 ? mf.tensor(name) : mf.layer_tensor(layer, name);
         if (!t) { msg = std::string("tensor '") + name + "' is missing"; return false; }
@@ -492,9 +500,17 @@ bool hearth_engine::upload(std::string &msg) {
             table[e].gate = qmat_alloc(dt, F, D);
             table[e].up = qmat_alloc(dt, F, D);
             table[e].down = qmat_alloc(dt, D, F);
-            up.quant(table[e].gate, slab + og);
-            up.quant(table[e].up, slab + ou);
-            up.quant(table[e].down, slab + od);
+            auto seen = first_copy.find(ent->offset);
+            if (seen != first_copy.end()) {   /* an aliased slab: its own copy, made on the device */
+                qmat_copy(table[e].gate, seen->second.gate);
+                qmat_copy(table[e].up, seen->second.up);
+                qmat_copy(table[e].down, seen->second.down);
+            } else {
+                up.quant(table[e].gate, slab + og);
+                up.quant(table[e].up, slab + ou);
+                up.quant(table[e].down, slab + od);
+                first_copy.emplace(ent->offset, table[e]);
+            }
             w.expert_bytes_each = 2 * (uint64_t)F * row_bytes(dt, D) + (uint64_t)D * row_bytes(dt, F);
             w.expert_gateup_bytes = 2 * (uint64_t)F * row_bytes(dt, D);
             w.dtype_mask |= 1 << dt;
@@ -569,7 +585,7 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
         if (c.n_moe) {
             /* HBM expert cache when HEARTH_GPU_EXPERT_CACHE_GB is below the expert set, or
              * when the experts do not fit next to the dense weights, KV cache and scratch */
-            const uint64_t slot_b = GpuExpertStore::slot_bytes_for(D, F);
+            const uint64_t slot_b = GpuExpertStore::slot_bytes_for(D, F, GpuExpertStore::room_dtype(mf, L, E));
             const uint64_t all = slot_b * (uint64_t)c.n_moe * E;
             const uint64_t kvb = (uint64_t)L * cap * 4 * (mla ? (uint64_t)(C + rdim) : 2ull * Hkv * hd);
             uint64_t budget = UINT64_MAX;
@@ -582,13 +598,15 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
             if (all > budget) {
                 const int n_slots = (int)std::max<uint64_t>((uint64_t)E, budget / slot_b);
                 store = std::make_unique<GpuExpertStore>();
-                if (!store->open(mf, L, E, D, F, n_slots, opt.policy, msg)) {
+                const char *ht = getenv("HEARTH_GPU_HOST_TIER");
+                if (!store->open(mf, L, E, D, F, n_slots, opt.policy, !(ht && !strcmp(ht, "0")), msg)) {
                     fail(err, errlen, "%s: %s", opt.model_path, msg.c_str());
                     return false;
                 }
                 ck(hipHostMalloc((void **)&h_meta, sizeof(int) * (size_t)(1 + E), hipHostMallocDefault));
-                log_msg(LOG_INFO, "expert cache: %d HBM slots of %.1f MiB for %d experts", n_slots,
-                        slot_b / 1048576.0, c.n_moe * E);
+                log_msg(LOG_INFO, "expert cache: %d HBM slots of %.1f MiB for %d experts; %s", n_slots,
+                        slot_b / 1048576.0, c.n_moe * E,
+                        store->host_tier() ? "loads from pinned slot images" : "staged loads from the container");
             }
         }
         if (!upload(msg)) { fail(err, errlen, "%s: %s", opt.model_path, msg.c_str()); return false; }
@@ -1616,6 +1634,25 @@ HEARTH_API void hearth_gpu_reset_kstats(hearth_engine *e) {
     if (hipSetDevice(e->dev) == hipSuccess && hipStreamSynchronize(e->st) == hipSuccess)
         (void)hipMemcpy(d, e->dstats, sizeof d, hipMemcpyDeviceToHost);
     e->ks_base = d[1];
+}
+
+HEARTH_API int hearth_gpu_get_store_info(hearth_engine *e, hearth_gpu_store_info *out) {
+    if (!e || !out) return E_ARG;
+    *out = hearth_gpu_store_info{};
+    if (!e->store) return OK;
+    try {
+        ck(hipSetDevice(e->dev));
+        e->store->harvest(true);
+    } catch (const DeviceError &) {
+        return E_IO;
+    }
+    out->streamed = 1;
+    out->host_tier = e->store->host_tier();
+    out->slots = e->store->slots();
+    out->slot_bytes = e->store->slot_bytes();
+    out->host_tier_bytes = e->store->host_tier_bytes();
+    out->copy_s = e->store->stats.copy_s;
+    return OK;
 }
 
 HEARTH_API int64_t hearth_gpu_kv_row_floats(hearth_engine *e) {

@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cstring>
+#include <unordered_map>
 
 namespace hx {
 
@@ -37,6 +38,9 @@ GpuExpertStore::~GpuExpertStore() {
         if (dstage_[i]) (void)hipFree(dstage_[i]);
         if (staged_[i]) (void)hipEventDestroy(staged_[i]);
     }
+    for (uint8_t *a : arena_) (void)hipHostFree(a);
+    for (auto &pr : ev_pend_) ev_free_.insert(ev_free_.end(), {pr.first, pr.second});
+    for (hipEvent_t ev : ev_free_) (void)hipEventDestroy(ev);
     if (htable_) (void)hipHostFree(htable_);
     if (done_) (void)hipEventDestroy(done_);
     if (pool_) (void)hipFree(pool_);
@@ -46,7 +50,7 @@ GpuExpertStore::~GpuExpertStore() {
 hxd::QMat GpuExpertStore::carve(uint8_t *&p, int dtype, int rows, int cols) const {
     hxd::QMat m{};
     uint64_t wb, db;
-    qmat_bytes(HEARTH_Q8, rows, cols, wb, db);   /* room for the larger dtype */
+    qmat_bytes(room_, rows, cols, wb, db);
     m.dtype = dtype;
     m.rows = rows;
     m.rows_pad = (rows + 15) & ~15;
@@ -59,17 +63,26 @@ hxd::QMat GpuExpertStore::carve(uint8_t *&p, int dtype, int rows, int cols) cons
     return m;
 }
 
-uint64_t GpuExpertStore::slot_bytes_for(int D, int F) {
+int GpuExpertStore::room_dtype(const ModelFile &mf, int L, int E) {
+    for (int l = 0; l < L; l++)
+        for (int e = 0; e < E && mf.cfg.layer_kind[l]; e++)
+            if (mf.expert(l, e)->dtype == HEARTH_Q8) return HEARTH_Q8;
+    return HEARTH_Q4;
+}
+
+uint64_t GpuExpertStore::slot_bytes_for(int D, int F, int room) {
     uint64_t wg, dg, wd, dd;
-    qmat_bytes(HEARTH_Q8, F, D, wg, dg);
-    qmat_bytes(HEARTH_Q8, D, F, wd, dd);
+    qmat_bytes(room, F, D, wg, dg);
+    qmat_bytes(room, D, F, wd, dd);
     return 2 * (al(wg) + al(dg)) + al(wd) + al(dd);
 }
 
-bool GpuExpertStore::open(const ModelFile &mf, int L, int E, int D, int F, int n_slots, int policy, std::string &msg) {
+bool GpuExpertStore::open(const ModelFile &mf, int L, int E, int D, int F, int n_slots, int policy, bool host_tier,
+                          std::string &msg) {
     mf_ = &mf;
     L_ = L; E_ = E; D_ = D; F_ = F; n_slots_ = n_slots; policy_ = policy;
-    slot_bytes_ = slot_bytes_for(D, F);
+    room_ = room_dtype(mf, L, E);
+    slot_bytes_ = slot_bytes_for(D, F, room_);
     for (int l = 0; l < L; l++)
         for (int e = 0; e < E && mf.cfg.layer_kind[l]; e++) {
             const ExpertEntry *x = mf.expert(l, e);
@@ -95,17 +108,76 @@ bool GpuExpertStore::open(const ModelFile &mf, int L, int E, int D, int F, int n
         }
     slot_.assign(n_slots, Slot{});
     uint8_t *p = pool_;
-    for (int s = 0; s < n_slots; s++) {
-        slot_[s].w.gate = carve(p, HEARTH_Q8, F, D);
-        slot_[s].w.up = carve(p, HEARTH_Q8, F, D);
-        slot_[s].w.down = carve(p, HEARTH_Q8, D, F);
+    for (int s = 0; s < n_slots; s++) {   /* slot s is [pool_ + s * slot_bytes_, + slot_bytes_) */
+        slot_[s].w.gate = carve(p, room_, F, D);
+        slot_[s].w.up = carve(p, room_, F, D);
+        slot_[s].w.down = carve(p, room_, D, F);
     }
     slot_of_.assign((size_t)L * E, -1);
     heat_.assign((size_t)L * E, 0.0);
     busy_.assign(n_slots, 0);
     free_.clear();
     for (int s = n_slots - 1; s >= 0; s--) free_.push_back(s);
+    if (host_tier) build_tier();
     return true;
+}
+
+/* Raw slab of expert key -> pinned staging buffer buf -> device staging -> repacked
+ * into the slot matrices w on the copy stream; the caller records staged_[buf] after
+ * its last use of the pair, which is free again once that event has passed. */
+void GpuExpertStore::stage(int key, int buf, hxd::ExpertW &w) {
+    const ExpertEntry *x = mf_->expert(key / E_, key % E_);
+    const int dt = (int)x->dtype;
+    uint64_t og, ou, od;
+    const uint64_t len = std::min<uint64_t>(slab_layout(dt, D_, F_, &og, &ou, &od), x->nbytes);
+    if (staged_used_[buf]) ck(hipEventSynchronize(staged_[buf]));
+    std::memcpy(pinned_[buf], mf_->data(x->offset), len);
+    ck(hipMemcpyAsync(dstage_[buf], pinned_[buf], len, hipMemcpyHostToDevice, cs_));
+    w.gate.dtype = w.up.dtype = w.down.dtype = dt;
+    hxl::repack(dstage_[buf] + og, 0, w.gate.rows_pad, w.gate, cs_);
+    hxl::repack(dstage_[buf] + ou, 0, w.up.rows_pad, w.up, cs_);
+    hxl::repack(dstage_[buf] + od, 0, w.down.rows_pad, w.down, cs_);
+}
+
+/* The pinned host tier: one slot image per physical slab, made by staging the slab
+ * into a slot and copying the slot back (the device repack is the one layout code). */
+void GpuExpertStore::build_tier() {
+    std::unordered_map<uint64_t, int> phys;   /* file offset -> image index */
+    std::vector<int> first;                   /* image index -> first key holding it */
+    img_.assign((size_t)L_ * E_, nullptr);
+    for (int l = 0; l < L_; l++)
+        for (int e = 0; e < E_ && mf_->cfg.layer_kind[l]; e++)
+            if (phys.emplace(mf_->expert(l, e)->offset, (int)first.size()).second) first.push_back(l * E_ + e);
+    const uint64_t n_img = first.size();
+    const uint64_t per = std::max<uint64_t>(1, (1ull << 30) / slot_bytes_);   /* images per pinned chunk */
+    std::vector<uint8_t *> base(n_img);
+    for (uint64_t i = 0; i < n_img; i += per) {
+        const uint64_t n = std::min(per, n_img - i);
+        uint8_t *a = nullptr;
+        if (hipHostMalloc((void **)&a, n * slot_bytes_, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            for (uint8_t *x : arena_) (void)hipHostFree(x);
+            arena_.clear();
+            img_.clear();
+            tier_bytes_ = 0;
+            return;   /* loads stay staged */
+        }
+        arena_.push_back(a);
+        for (uint64_t j = 0; j < n; j++) base[i + j] = a + j * slot_bytes_;
+    }
+    for (uint64_t i = 0; i < n_img; i++) {
+        const int buf = (int)(i & 1), s = (int)(i % (uint64_t)n_slots_);
+        uint8_t *sb = pool_ + (uint64_t)s * slot_bytes_;
+        stage(first[i], buf, slot_[s].w);
+        ck(hipMemcpyAsync(base[i], sb, slot_bytes_, hipMemcpyDeviceToHost, cs_));
+        ck(hipEventRecord(staged_[buf], cs_));
+        staged_used_[buf] = true;
+    }
+    ck(hipStreamSynchronize(cs_));
+    for (int l = 0; l < L_; l++)
+        for (int e = 0; e < E_ && mf_->cfg.layer_kind[l]; e++) img_[(size_t)l * E_ + e] = base[phys[mf_->expert(l, e)->offset]];
+    tier_bytes_ = n_img * slot_bytes_;
+    tier_ = true;
 }
 
 int GpuExpertStore::resident() const { return n_slots_ - (int)free_.size(); }
@@ -143,29 +215,64 @@ void GpuExpertStore::evict(int s) {
 }
 
 void GpuExpertStore::load(int key, int s) {
-    const int l = key / E_, e = key % E_;
-    const ExpertEntry *x = mf_->expert(l, e);
-    const int dt = (int)x->dtype;
-    uint64_t og, ou, od;
-    const uint64_t len = std::min<uint64_t>(slab_layout(dt, D_, F_, &og, &ou, &od), x->nbytes);
+    hxd::ExpertW &w = slot_[s].w;
+    uint8_t *sb = pool_ + (uint64_t)s * slot_bytes_;
+    if (tier_) {   /* one copy of the slot image */
+        const int dt = (int)mf_->expert(key / E_, key % E_)->dtype;
+        w.gate.dtype = w.up.dtype = w.down.dtype = dt;
+        ck(hipMemcpyAsync(sb, img_[key], slot_bytes_, hipMemcpyHostToDevice, cs_));
+        stats.loads++;
+        stats.bytes_read += slot_bytes_;
+        return;
+    }
     const int i = cur_;
     cur_ ^= 1;
-    if (staged_used_[i]) ck(hipEventSynchronize(staged_[i]));
-    std::memcpy(pinned_[i], mf_->data(x->offset), len);
-    ck(hipMemcpyAsync(dstage_[i], pinned_[i], len, hipMemcpyHostToDevice, cs_));
-    hxd::ExpertW &w = slot_[s].w;
-    w.gate.dtype = w.up.dtype = w.down.dtype = dt;
-    hxl::repack(dstage_[i] + og, 0, w.gate.rows_pad, w.gate, cs_);
-    hxl::repack(dstage_[i] + ou, 0, w.up.rows_pad, w.up, cs_);
-    hxl::repack(dstage_[i] + od, 0, w.down.rows_pad, w.down, cs_);
+    stage(key, i, w);
     ck(hipEventRecord(staged_[i], cs_));
     staged_used_[i] = true;
+    const ExpertEntry *x = mf_->expert(key / E_, key % E_);
+    uint64_t og, ou, od;
     stats.loads++;
-    stats.bytes_read += len;
+    stats.bytes_read += std::min<uint64_t>(slab_layout((int)x->dtype, D_, F_, &og, &ou, &od), x->nbytes);
+}
+
+hipEvent_t GpuExpertStore::batch_ev() {
+    if (ev_free_.empty()) {
+        hipEvent_t ev;
+        ck(hipEventCreate(&ev));
+        return ev;
+    }
+    hipEvent_t ev = ev_free_.back();
+    ev_free_.pop_back();
+    return ev;
+}
+
+void GpuExpertStore::batch_begin() {
+    harvest(false);
+    hipEvent_t a = batch_ev(), b = batch_ev();
+    ck(hipEventRecord(a, cs_));
+    ev_pend_.emplace_back(a, b);
+}
+
+void GpuExpertStore::batch_end() { ck(hipEventRecord(ev_pend_.back().second, cs_)); }
+
+void GpuExpertStore::harvest(bool wait) {
+    while (!ev_pend_.empty()) {
+        auto [a, b] = ev_pend_.front();
+        if (wait) ck(hipEventSynchronize(b));
+        else if (hipEventQuery(b) != hipSuccess) break;
+        float ms = 0.0f;
+        ck(hipEventElapsedTime(&ms, a, b));
+        stats.copy_s += ms * 1e-3;
+        ev_free_.push_back(a);
+        ev_free_.push_back(b);
+        ev_pend_.pop_front();
+    }
 }
 
 void GpuExpertStore::ensure(int layer, const int *experts, int n, hxd::ExpertW *table_dev, hipStream_t compute) {
     const double t0 = now_s();
+    bool batch = false;
     std::fill(busy_.begin(), busy_.end(), 0);
     /* hits first, so that no miss of this layer evicts them */
     for (int j = 0; j < n; j++) {
@@ -193,6 +300,8 @@ void GpuExpertStore::ensure(int layer, const int *experts, int n, hxd::ExpertW *
             slot_[s].key = key;
             slot_of_[key] = s;
             busy_[s] = 1;
+            if (!batch) batch_begin();
+            batch = true;
             load(key, s);
         }
         slot_[s].prot_tick = 0;
@@ -201,6 +310,7 @@ void GpuExpertStore::ensure(int layer, const int *experts, int n, hxd::ExpertW *
         heat_[key] += 1.0;
         htable_[e] = slot_[s].w;
     }
+    if (batch) batch_end();
     ck(hipMemcpyAsync(table_dev, htable_, sizeof(hxd::ExpertW) * (size_t)E_, hipMemcpyHostToDevice, cs_));
     ck(hipEventRecord(done_, cs_));
     ck(hipStreamWaitEvent(compute, done_, 0));
@@ -209,6 +319,7 @@ void GpuExpertStore::ensure(int layer, const int *experts, int n, hxd::ExpertW *
 
 void GpuExpertStore::prefetch(int layer, const int *experts, int n) {
     const double t0 = now_s();
+    bool batch = false;
     for (int j = 0; j < n; j++) {
         const int key = layer * E_ + experts[j];
         const int r = slot_of_[key];
@@ -237,9 +348,12 @@ void GpuExpertStore::prefetch(int layer, const int *experts, int n) {
         x.pf_unused = true;
         x.prot_tick = now_ + 1;
         slot_of_[key] = s;
+        if (!batch) batch_begin();
+        batch = true;
         load(key, s);
         stats.prefetch_issued++;
     }
+    if (batch) batch_end();
     stats.load_s += now_s() - t0;
 }
 

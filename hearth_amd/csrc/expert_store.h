@@ -9,9 +9,15 @@
  *   - a layer's demanded experts are made resident before its expert kernels run (the
  *     compute stream waits for the loads), so results never depend on the cache
  *     (weights are bytes, reference INV-DET-1);
- *   - a load copies the slab from the mapped container into pinned staging, then to a
- *     device staging buffer on a copy stream, and repacks its three matrices into the
- *     slot's MFMA tile layout; the layer's device expert table gets the slot's matrices;
+ *   - the host tier: at open, every physical slab of the container (aliased entries
+ *     share one) is repacked once into the slot layout (the MFMA tiles of its three
+ *     matrices, exactly as a slot holds them) in pinned host memory, so that a load is
+ *     a single hipMemcpyAsync of one slot image on the copy stream: no host copy, no
+ *     repack, and back-to-back loads keep the host link busy. When the pinned tier
+ *     cannot be allocated (or HEARTH_GPU_HOST_TIER=0), a load copies the slab from the
+ *     mapped container into pinned staging, then to a device staging buffer, and
+ *     repacks it there. The layer's device expert table gets the slot's matrices;
+ *   - slots are sized for the widest expert dtype present (Q4-only models get Q4 slots);
  *   - prefetch (store.c:541-561, 207-214): experts predicted for the next MoE layer are
  *     loaded ahead into a free slot or an unprotected, not-hot victim (LRU: not used
  *     in this forward; LFU: heat below 0.5 / (1 - decay)); resident ones are
@@ -24,6 +30,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <deque>
+#include <utility>
 #include <vector>
 
 #include "hx_host.h"
@@ -44,13 +52,17 @@ struct StoreStats {
     uint64_t hits = 0, misses = 0, evictions = 0, loads = 0, bytes_read = 0;
     uint64_t prefetch_issued = 0, prefetch_used = 0, prefetch_wasted = 0, prefetch_dropped = 0;
     double load_s = 0.0;   /* host time spent issuing loads and waiting for staging */
+    double copy_s = 0.0;   /* copy-stream time of the load batches (HIP events; see harvest) */
 };
 
 class GpuExpertStore {
 public:
     ~GpuExpertStore();
-    /* n_slots >= E; policy HEARTH_POLICY_LRU / _LFU. Returns false with msg on failure. */
-    bool open(const ModelFile &mf, int L, int E, int D, int F, int n_slots, int policy, std::string &msg);
+    /* n_slots >= E; policy HEARTH_POLICY_LRU / _LFU; host_tier: build the pinned slot
+     * images (falls back to staged loads when the pinned memory cannot be had). Returns
+     * false with msg on failure. */
+    bool open(const ModelFile &mf, int L, int E, int D, int F, int n_slots, int policy, bool host_tier,
+              std::string &msg);
     /* Makes experts[0..n) of layer resident, writes their matrices into table_dev (device
      * [E]) and makes `compute` wait for the loads. */
     void ensure(int layer, const int *experts, int n, hxd::ExpertW *table_dev, hipStream_t compute);
@@ -60,11 +72,17 @@ public:
     void prefetch(int layer, const int *experts, int n);
     /* forward boundary: LFU heat decay, protection expires */
     void tick();
-    /* HBM bytes of one slot for experts of D x F (room for Q8, the larger dtype) */
-    static uint64_t slot_bytes_for(int D, int F);
+    /* the widest expert dtype of the container's MoE layers (Q8 if any expert is Q8) */
+    static int room_dtype(const ModelFile &mf, int L, int E);
+    /* HBM bytes of one slot for experts of D x F stored as `room` (Q8 or Q4) */
+    static uint64_t slot_bytes_for(int D, int F, int room);
     int slots() const { return n_slots_; }
     int resident() const;
+    /* adds the durations of the finished load batches to stats.copy_s; wait: all of them */
+    void harvest(bool wait);
     uint64_t slot_bytes() const { return slot_bytes_; }
+    bool host_tier() const { return tier_; }
+    uint64_t host_tier_bytes() const { return tier_bytes_; }
     StoreStats stats;
 
 private:
@@ -77,7 +95,7 @@ private:
         hxd::ExpertW w{};
     };
     const ModelFile *mf_ = nullptr;
-    int L_ = 0, E_ = 0, D_ = 0, F_ = 0, n_slots_ = 0, policy_ = 0;
+    int L_ = 0, E_ = 0, D_ = 0, F_ = 0, n_slots_ = 0, policy_ = 0, room_ = HEARTH_Q8;
     uint64_t slot_bytes_ = 0, stage_bytes_ = 0, seq_ = 0, now_ = 0;
     uint8_t *pool_ = nullptr;
     std::vector<Slot> slot_;
@@ -91,6 +109,18 @@ private:
     int cur_ = 0;
     hxd::ExpertW *htable_ = nullptr;  /* pinned [E]: entries written this call */
     hipEvent_t done_ = nullptr;
+    bool tier_ = false;               /* loads come from the pinned slot images */
+    uint64_t tier_bytes_ = 0;
+    std::vector<uint8_t *> arena_;    /* pinned chunks holding the slot images */
+    std::vector<const uint8_t *> img_;   /* [L * E]: slot image of each expert (MoE layers) */
+    void build_tier();
+    /* event pairs bracketing the loads of one ensure() or prefetch() call on cs_ */
+    std::vector<hipEvent_t> ev_free_;
+    std::deque<std::pair<hipEvent_t, hipEvent_t>> ev_pend_;
+    hipEvent_t batch_ev();
+    void batch_begin();
+    void batch_end();
+    void stage(int key, int buf, hxd::ExpertW &w);
     hxd::QMat carve(uint8_t *&p, int dtype, int rows, int cols) const;
     bool protected_(const Slot &x) const { return x.prot_tick == now_ + 1; }
     bool cheaper(int a, int b) const;

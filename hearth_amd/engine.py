@@ -88,6 +88,14 @@ class HearthStats(Structure):
     ]
 
 
+class StoreInfo(Structure):
+    """hearth_gpu_store_info (include/hearth_gpu.h)."""
+    _fields_ = [
+        ("streamed", ctypes.c_int32), ("host_tier", ctypes.c_int32), ("slots", ctypes.c_int64),
+        ("slot_bytes", c_uint64), ("host_tier_bytes", c_uint64), ("copy_s", c_double),
+    ]
+
+
 class KStats(Structure):
     """hearth_gpu_kstats (include/hearth_gpu.h)."""
     _fields_ = [
@@ -165,6 +173,7 @@ _PROTOS = {
     "hearth_gpu_set_profiling": (c_int, [c_void_p, c_int]),
     "hearth_gpu_get_kstats": (c_int, [c_void_p, POINTER(KStats)]),
     "hearth_gpu_reset_kstats": (None, [c_void_p]),
+    "hearth_gpu_get_store_info": (c_int, [c_void_p, POINTER(StoreInfo)]),
     "hearth_gpu_kv_row_floats": (ctypes.c_int64, [c_void_p]),
     "hearth_gpu_kv_export": (c_int, [c_void_p, c_int, POINTER(c_float), ctypes.c_int64]),
     "hearth_gpu_kv_import": (c_int, [c_void_p, c_int, POINTER(c_float), ctypes.c_int64]),
@@ -499,6 +508,16 @@ class Engine:
     def reset_kstats(self) -> None:
         with self._lock:
             self._api.need("gpu_reset_kstats")(self._handle())
+
+    def store_info(self) -> dict:
+        """The HBM expert cache: streamed, host_tier, slots, slot_bytes, host_tier_bytes,
+        copy_s (hearth_gpu_get_store_info)."""
+        si = StoreInfo()
+        with self._lock:
+            rc = self._api.need("gpu_get_store_info")(self._handle(), byref(si))
+        if rc < 0:
+            raise HearthError(f"hearth_gpu_get_store_info failed (code {rc}): {_ERRORS.get(rc, 'unknown error')}")
+        return {name: getattr(si, name) for name, _ in StoreInfo._fields_}
 
     def trace_start(self, path) -> None:
         with self._lock:

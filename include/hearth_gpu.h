@@ -148,6 +148,26 @@ HEARTH_API int64_t hearth_gpu_kv_row_floats(hearth_engine *e);
 HEARTH_API int hearth_gpu_kv_export(hearth_engine *e, int n, float *dst, int64_t count);
 HEARTH_API int hearth_gpu_kv_import(hearth_engine *e, int n, const float *src, int64_t count);
 
+/* The HBM expert cache of an engine. streamed 0: every routed expert is resident in
+ * HBM (the other fields are 0). streamed 1: experts are loaded into `slots` HBM slots of
+ * `slot_bytes` each when a layer demands them (or ahead of it, prefetch); host_tier 1:
+ * a load is one copy of a slot image kept in pinned host memory (host_tier_bytes in all,
+ * one image per physical slab of the container), 0: a load stages the container's slab
+ * and repacks it on the device. copy_s: time the copy stream spent on load batches since
+ * the engine opened (HIP events around the loads of each layer's demand and of each
+ * prefetch; bytes_read of hearth_get_stats / copy_s is the host-link rate). No
+ * counterpart in the reference (its store, engine/src/store.c, has no device tier). */
+typedef struct hearth_gpu_store_info {
+    int32_t streamed;
+    int32_t host_tier;
+    int64_t slots;
+    uint64_t slot_bytes;
+    uint64_t host_tier_bytes;
+    double copy_s;
+} hearth_gpu_store_info;
+
+HEARTH_API int hearth_gpu_get_store_info(hearth_engine *e, hearth_gpu_store_info *out);
+
 /* Device the library runs on (HEARTH_DEVICE, default 0) and its name. */
 HEARTH_API int hearth_gpu_device(char *name, size_t n);
 

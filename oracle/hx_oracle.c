@@ -863,6 +863,68 @@ static void rope(float *x, const ho_model *m, int pos) {
     }
 }
 
+/* Heads [0, H) of one token's attention on up to nthreads threads: fn(ctx, h, scratch)
+ * computes head h alone and writes only its own outputs, so the thread count cannot
+ * change a result; each thread has its own scratch of `scratch_floats` floats. */
+typedef void (*head_fn)(void *ctx, int h, float *scratch);
+typedef struct {
+    head_fn fn;
+    void *ctx;
+    int h0, h1;
+    size_t scratch_floats;
+} head_job;
+
+static void *head_run(void *p) {
+    head_job *j = (head_job *)p;
+    float *scr = malloc(sizeof(float) * (j->scratch_floats ? j->scratch_floats : 1));
+    for (int h = j->h0; h < j->h1; h++) j->fn(j->ctx, h, scr);
+    free(scr);
+    return NULL;
+}
+
+static void par_heads(int H, int nthreads, head_fn fn, void *ctx, size_t scratch_floats) {
+    int nt = nthreads < 1 ? 1 : (nthreads > 64 ? 64 : nthreads);
+    if (nt > H) nt = H > 0 ? H : 1;
+    head_job jobs[64];
+    pthread_t th[64];
+    for (int i = 0; i < nt; i++) {
+        jobs[i].fn = fn; jobs[i].ctx = ctx; jobs[i].scratch_floats = scratch_floats;
+        jobs[i].h0 = H * i / nt;
+        jobs[i].h1 = H * (i + 1) / nt;
+    }
+    for (int i = 1; i < nt; i++) pthread_create(&th[i], NULL, head_run, &jobs[i]);
+    head_run(&jobs[0]);
+    for (int i = 1; i < nt; i++) pthread_join(th[i], NULL);
+}
+
+/* o_h = sum_i p_i v_{rows[i]} with each element summed over i in order from 0.0f
+ * (model.c:552-575); v row r at base + rows[i] * stride, width n */
+static void value_sum(const float *p, const int *rows, int nr, const float *base, size_t stride, int n, float *o) {
+    for (int d = 0; d < n; d++) o[d] = 0.0f;
+    for (int i = 0; i < nr; i++) {
+        const float *v = base + (size_t)rows[i] * stride;
+        for (int d = 0; d < n; d++) o[d] = o[d] + p[i] * v[d];
+    }
+}
+
+typedef struct {
+    const cfg *c;
+    const float *q, *K, *Vc;
+    float *o;
+    const int *rows;
+    int nr, kd;
+} gqa_ctx;
+
+static void gqa_head(void *p, int h, float *sc) {
+    const gqa_ctx *a = (const gqa_ctx *)p;
+    const cfg *c = a->c;
+    const int hd = c->head_dim, g = h / (c->n_heads / c->n_kv_heads);
+    for (int i = 0; i < a->nr; i++)
+        sc[i] = c->attn_scale * ho_dot16(a->q + h * hd, a->K + (size_t)a->rows[i] * a->kd + g * hd, hd);
+    softmax(sc, a->nr);
+    value_sum(sc, a->rows, a->nr, a->Vc + g * hd, (size_t)a->kd, hd, a->o + h * hd);
+}
+
 /* One token's attention. rows[0..nr) are the cache slots it attends to in order
  * (its causal prefix for a chain; context then ancestors for a tree node); the token's
  * own K/V go to slot `slot` before the scores are computed. */
@@ -870,7 +932,7 @@ static void attn_gqa(ho_model *m, int l, const float *x, int pos, int slot, cons
     const cfg *c = &m->c;
     const int H = c->n_heads, Hkv = c->n_kv_heads, hd = c->head_dim, qd = H * hd, kd = Hkv * hd;
     float *q = malloc(sizeof(float) * qd), *k = malloc(sizeof(float) * kd), *v = malloc(sizeof(float) * kd);
-    float *o = malloc(sizeof(float) * qd), *sc = malloc(sizeof(float) * (size_t)nr);
+    float *o = malloc(sizeof(float) * qd);
     float *K = m->kv + (size_t)l * m->per_layer, *Vc = K + (size_t)m->cap * kd;
     lin(m, l, "attn_q", x, q);
     lin(m, l, "attn_k", x, k);
@@ -895,19 +957,42 @@ static void attn_gqa(ho_model *m, int l, const float *x, int pos, int slot, cons
     memcpy(K + (size_t)slot * kd, k, sizeof(float) * kd);
     memcpy(Vc + (size_t)slot * kd, v, sizeof(float) * kd);
     dump(m, "q", l, q, qd, 4);
-    for (int h = 0; h < H; h++) {
-        const int g = h / (H / Hkv);
-        for (int i = 0; i < nr; i++) sc[i] = c->attn_scale * ho_dot16(q + h * hd, K + (size_t)rows[i] * kd + g * hd, hd);
-        softmax(sc, nr);
-        for (int d = 0; d < hd; d++) {
-            float acc = 0.0f;
-            for (int i = 0; i < nr; i++) acc = acc + sc[i] * Vc[(size_t)rows[i] * kd + g * hd + d];
-            o[h * hd + d] = acc;
-        }
-    }
+    gqa_ctx ctx = {c, q, K, Vc, o, rows, nr, kd};
+    par_heads(H, m->nthreads, gqa_head, &ctx, (size_t)nr);
     dump(m, "att", l, o, qd, 4);
     lin(m, l, "attn_o", o, out);
-    free(q); free(k); free(v); free(o); free(sc);
+    free(q); free(k); free(v); free(o);
+}
+
+typedef struct {
+    ho_model *m;
+    const tens *kvb;
+    size_t kvb_rb;
+    float *q, *o;
+    const float *Cc, *Kp;
+    const int *rows;
+    int nr, pos;
+} mla_ctx;
+
+/* head h of the absorbed MLA (model.c:650-737); scratch: ql, ol, wrow [C] then sc [nr] */
+static void mla_head(void *p, int h, float *scr) {
+    const mla_ctx *a = (const mla_ctx *)p;
+    const cfg *c = &a->m->c;
+    const int nope = c->nope, rd = c->rope_qk, vd = c->v_head, C = c->kv_lora, qh = nope + rd;
+    float *ql = scr, *ol = scr + C, *wrow = scr + 2 * C, *sc = scr + 3 * C;
+    float *qn = a->q + h * qh, *qpe = qn + nope;
+    if (c->rope_dim / 2) rope(qpe, a->m, a->pos);
+    for (int i = 0; i < C; i++) ql[i] = 0.0f;
+    for (int n = 0; n < nope; n++) {
+        dequant_row(a->kvb->dtype, a->kvb->data + (size_t)(h * (nope + vd) + n) * a->kvb_rb, wrow, C);
+        for (int i = 0; i < C; i++) ql[i] = ql[i] + qn[n] * wrow[i];
+    }
+    for (int i = 0; i < a->nr; i++)
+        sc[i] = c->attn_scale * (ho_dot16(ql, a->Cc + (size_t)a->rows[i] * C, C) +
+                                 ho_dot16(qpe, a->Kp + (size_t)a->rows[i] * rd, rd));
+    softmax(sc, a->nr);
+    value_sum(sc, a->rows, a->nr, a->Cc, (size_t)C, C, ol);
+    matvec(a->kvb->dtype, a->kvb->data, C, ol, 1, a->o + h * vd, vd, h * (nope + vd) + nope, h * (nope + vd) + nope + vd, 1);
 }
 
 static void attn_mla(ho_model *m, int l, const float *x, int pos, int slot, const int *rows, int nr, float *out) {
@@ -916,8 +1001,7 @@ static void attn_mla(ho_model *m, int l, const float *x, int pos, int slot, cons
     const tens *kvb = find_tensor(m, l, "attn_kv_b");
     const size_t kvb_rb = ho_row_bytes(kvb->dtype, C);
     float *q = malloc(sizeof(float) * (size_t)H * qh), *kva = malloc(sizeof(float) * (size_t)(C + rd));
-    float *ql = malloc(sizeof(float) * C), *ol = malloc(sizeof(float) * C), *wrow = malloc(sizeof(float) * C);
-    float *o = malloc(sizeof(float) * (size_t)H * vd), *sc = malloc(sizeof(float) * (size_t)nr);
+    float *o = malloc(sizeof(float) * (size_t)H * vd);
     float *Cc = m->kv + (size_t)l * m->per_layer, *Kp = Cc + (size_t)m->cap * C;
     if (c->q_lora) {
         float *qa = malloc(sizeof(float) * c->q_lora);
@@ -932,26 +1016,10 @@ static void attn_mla(ho_model *m, int l, const float *x, int pos, int slot, cons
     rmsnorm(Cc + (size_t)slot * C, kva, vec(m, l, "attn_kv_a_norm"), C, c->eps);
     memcpy(Kp + (size_t)slot * rd, kva + C, sizeof(float) * rd);
     if (c->rope_dim / 2) rope(Kp + (size_t)slot * rd, m, pos);
-    for (int h = 0; h < H; h++) {
-        float *qn = q + h * qh, *qpe = qn + nope;
-        if (c->rope_dim / 2) rope(qpe, m, pos);
-        for (int i = 0; i < C; i++) ql[i] = 0.0f;
-        for (int n = 0; n < nope; n++) {
-            dequant_row(kvb->dtype, kvb->data + (size_t)(h * (nope + vd) + n) * kvb_rb, wrow, C);
-            for (int i = 0; i < C; i++) ql[i] = ql[i] + qn[n] * wrow[i];
-        }
-        for (int i = 0; i < nr; i++)
-            sc[i] = c->attn_scale * (ho_dot16(ql, Cc + (size_t)rows[i] * C, C) + ho_dot16(qpe, Kp + (size_t)rows[i] * rd, rd));
-        softmax(sc, nr);
-        for (int i = 0; i < C; i++) {
-            float acc = 0.0f;
-            for (int r = 0; r < nr; r++) acc = acc + sc[r] * Cc[(size_t)rows[r] * C + i];
-            ol[i] = acc;
-        }
-        matvec(kvb->dtype, kvb->data, C, ol, 1, o + h * vd, vd, h * (nope + vd) + nope, h * (nope + vd) + nope + vd, 1);
-    }
+    mla_ctx ctx = {m, kvb, kvb_rb, q, o, Cc, Kp, rows, nr, pos};
+    par_heads(H, m->nthreads, mla_head, &ctx, (size_t)3 * C + (size_t)nr);
     lin(m, l, "attn_o", o, out);
-    free(q); free(kva); free(ql); free(ol); free(wrow); free(o); free(sc);
+    free(q); free(kva); free(o);
 }
 
 static void ffn(ho_model *m, int l, const char *g, const char *u, const char *d, const float *x, float *out) {

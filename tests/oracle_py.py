@@ -200,14 +200,9 @@ class Model:
 
 
 def write_trace(path, ids, n_layers: int, n_experts: int) -> None:
-    """a routing trace file (FORMAT.md §9): 'HRTR', version 1, n_layers, E, K, n_moe,
-    then rows of n_moe * K little-endian uint16 expert ids"""
-    a = np.ascontiguousarray(ids, dtype="<u2")
-    rows, n_moe, k = a.shape
-    hdr = np.array([0x52545248, 1, n_layers, n_experts, k, n_moe], dtype="<u4")
-    with open(path, "wb") as f:
-        f.write(hdr.tobytes())
-        f.write(a.tobytes())
+    """a routing trace file (FORMAT.md §9), written by the package's writer"""
+    from hearth_amd import container
+    container.write_route_trace(path, ids, n_layers, n_experts)
 
 
 def synthetic_routes(seed: int, rows: int, n_moe: int, n_experts: int, k: int) -> np.ndarray:

@@ -80,6 +80,7 @@ def test_library_exports_every_declared_function():
 def test_ctypes_mirrors_match_headers():
     structs = dict(MIRRORS)
     structs["hearth_gpu_kstats"] = E.KStats
+    structs["hearth_gpu_store_info"] = E.StoreInfo
     structs["hearth_sampler"] = E.HearthSampler
     vals = _run_layout(INC / "hearth_gpu.h", structs)
     for cname, mirror in structs.items():

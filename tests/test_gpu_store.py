@@ -171,3 +171,32 @@ def test_prefetch_bit_identical_and_counters(tiny_model, variant_models, monkeyp
     assert st["bytes_read"] == (st["cache_misses"] + st["prefetch_issued"]) * slab
     # the predictions of these models are good enough to save demand loads
     assert st["cache_misses"] < st_off["cache_misses"]
+
+
+def test_host_tier_equals_staged_loads(tiny_model, monkeypatch):
+    """A load that copies the pinned slot image (the default) and a staged load that
+    repacks the container's slab on the device fill a slot with the same bytes: equal
+    logits and counters; hearth_gpu_get_store_info reports the tier."""
+    toks = [int(t) for t in container.uniform_ints(54, 70, container.TINY.vocab)]
+    calls = [toks[:40], toks[40:45], toks[45:54], toks[54:]]
+    ref, _ = _run(tiny_model, calls)
+    with Engine(tiny_model, max_seq=512) as e:
+        assert e.store_info() == dict(streamed=0, host_tier=0, slots=0, slot_bytes=0, host_tier_bytes=0, copy_s=0.0)
+    monkeypatch.setenv("HEARTH_GPU_EXPERT_CACHE_GB", "0.0001")
+    got = {}
+    for tier in ("1", "0"):
+        monkeypatch.setenv("HEARTH_GPU_HOST_TIER", tier)
+        with Engine(tiny_model, max_seq=512, prefetch="off") as e:
+            out = [e.eval(c, all_logits=True) for c in calls]
+            got[tier] = (out, e.stats(), e.store_info())
+    n_slabs = container.TINY.n_layers * container.TINY.n_experts
+    for tier, (out, st, info) in got.items():
+        for a, b in zip(ref, out):
+            assert np.array_equal(_bits(a), _bits(b)), f"HEARTH_GPU_HOST_TIER={tier}"
+        assert info["streamed"] == 1 and info["slots"] == 16 and info["slot_bytes"] == 208896
+        assert info["host_tier"] == int(tier)
+        assert info["host_tier_bytes"] == (n_slabs * 208896 if tier == "1" else 0)
+        assert st["cache_misses"] > 0 and st["bytes_read"] == st["cache_misses"] * 208896
+        assert info["copy_s"] > 0.0
+    keys = ("cache_hits", "cache_misses", "evictions", "bytes_read")
+    assert [got["1"][1][k] for k in keys] == [got["0"][1][k] for k in keys]
