@@ -197,15 +197,16 @@ def host_cpus():
     return cpus, len(cores) or None
 
 
-def summarize_trace(path: str, nsteps: int) -> int:
+def summarize_trace(path: str, nsteps: int, last_kernel: str = "k_accept_walk") -> int:
     """Per-verify-step kernel table from a rocprofv3 --kernel-trace CSV (run_kernel_trace.csv):
-    a step is the dispatches after one k_accept_walk up to and including the next; the
+    a step is the dispatches after one `last_kernel` (the acceptance's last kernel:
+    k_accept_walk greedy, k_sample_walk sampled) up to and including the next; the
     last nsteps steps are averaged."""
     import collections
     import csv
     import re
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
-    ends = [i for i, r in enumerate(rows) if "k_accept_walk" in r["Kernel_Name"]]
+    ends = [i for i, r in enumerate(rows) if last_kernel in r["Kernel_Name"]]
     steps = [rows[a + 1:b + 1] for a, b in zip(ends[:-1], ends[1:])][-nsteps:]
     if not steps:
         print("no verify steps in the trace")
@@ -555,6 +556,13 @@ def bench_dsv3(a) -> dict:
     eng.close()
     resident = sum(r_toks) / sum(r_secs)
     log(f"[bench] dsv3 resident: {resident:.1f} tok/s, {sum(r_secs) / a.steps * 1e3:.2f} ms/step")
+    if a.resident_only:
+        return {"metric": "accepted tok/s, DeepSeek-V3-shape verify k=8, experts resident (1 GPU)",
+                "value": round(resident, 3), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+                "ms_per_step": round(sum(r_secs) / a.steps * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+                "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+                "config": {"workload": "DeepSeek-V3-shaped MLA MoE, every expert resident, chain verify k=8 at 4096",
+                           "tokens_per_step": round(sum(r_toks) / a.steps, 3)}}
     budget = os.environ.get("HEARTH_GPU_EXPERT_CACHE_GB") or "56"
     os.environ["HEARTH_GPU_EXPERT_CACHE_GB"] = budget
     t = time.time()
@@ -615,6 +623,7 @@ def main(argv=None) -> int:
                     help="chain: Qwen3-30B-A3B chain verify k=8 at 4096 (the headline); tree: 4x4x4 tree with "
                          "sampled acceptance at 2048; experts: the routed-expert kernels alone, Zipf routing; "
                          "dsv3: DeepSeek-V3 shape with streamed experts")
+    ap.add_argument("--resident-only", action="store_true", help="dsv3: skip the streamed run")
     ap.add_argument("--cpu-steps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--summarize-trace", metavar="CSV",
@@ -623,7 +632,7 @@ def main(argv=None) -> int:
                     help="only run device-to-device copies of MIB MiB (counter calibration) and exit")
     a = ap.parse_args(argv)
     if a.summarize_trace:
-        return summarize_trace(a.summarize_trace, 10)
+        return summarize_trace(a.summarize_trace, 10, "k_sample_walk" if a.workload == "tree" else "k_accept_walk")
     if a.calibrate_copy:
         return calibrate_copy(a.calibrate_copy)
     if a.gpus != 1:

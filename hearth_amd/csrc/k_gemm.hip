@@ -139,19 +139,27 @@ __device__ __forceinline__ void fold_tile(const QMat &m, int rt, const Act &a, i
 
 /* ------------------------------------------------------------ dense segmented GEMM */
 
+/* One wave per (16-row tile, group of NT 16-token tiles). Workgroup b covers row tiles
+ * of workgroup-row b % wgr and token group b / wgr; wgr is a multiple of 8, so every
+ * token group of a row tile runs on the same XCD (IDs are dealt round-robin to the 8
+ * XCDs) and re-reads its weights from that XCD's L2. */
 template <int NT>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs args) {
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs args, int wgr) {
+    const int rw = (int)blockIdx.x % wgr, tg = (int)blockIdx.x / wgr;
     int s = 0;
-    while (s + 1 < args.nseg && (int)blockIdx.x >= args.seg[s + 1].wg0) s++;
+    while (s + 1 < args.nseg && rw >= args.seg[s + 1].wg0) s++;
     const GemmSeg &sg = args.seg[s];
-    const int rt = ((int)blockIdx.x - sg.wg0) * 4 + (int)(threadIdx.x >> 6);
+    if (rw >= sg.wg0 + (sg.m.rows_pad / 16 + 3) / 4) return;   /* padding workgroup */
+    const int rt = (rw - sg.wg0) * 4 + (int)(threadIdx.x >> 6);
     if (rt * 16 >= sg.m.rows_pad) return;
+    const int t0 = args.t0 + tg * NT * 16;
+    if (t0 >= args.T) return;
     float acc[NT][4];
-    fold_tile<NT>(sg.m, rt, args.a, args.t0, args.T, [](int t) { return t; }, acc);
+    fold_tile<NT>(sg.m, rt, args.a, t0, args.T, [](int t) { return t; }, acc);
     const int lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) {
-        const int t = args.t0 + tt * 16 + lr;
+        const int t = t0 + tt * 16 + lr;
         if (t >= args.T) continue;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -993,21 +1001,26 @@ void gemm(const GemmArgs &in, hipStream_t st) {
         if (ok) { gemm_sk(in, st); return; }
     }
     GemmArgs g = in;
-    int wg = 0;
+    int wg = 0, tiles = 0;
     for (int s = 0; s < g.nseg; s++) {
         g.seg[s].wg0 = wg;
         wg += (g.seg[s].m.rows_pad / 16 + 3) / 4;
+        tiles += g.seg[s].m.rows_pad / 16;
     }
-    if (!wg) return;
-    /* token passes of up to 128 tokens; each pass re-reads the weights */
-    for (int t0 = 0; t0 < in.T; t0 += 128) {
-        g.t0 = t0;
-        const int nt = (in.T - t0 + 15) / 16;
-        if (nt <= 1) k_gemm<1><<<wg, 256, 0, st>>>(g);
-        else if (nt <= 2) k_gemm<2><<<wg, 256, 0, st>>>(g);
-        else if (nt <= 4) k_gemm<4><<<wg, 256, 0, st>>>(g);
-        else k_gemm<8><<<wg, 256, 0, st>>>(g);
-    }
+    if (!wg || in.T <= 0) return;
+    const int wgr = (wg + 7) & ~7;
+    /* tokens tiles per wave: as many as keep about 8 waves per CU busy (each wave walks
+     * all of K for its tiles, so more tiles per wave means fewer, longer waves) */
+    const int ntile = (in.T + 15) / 16, want = 8 * cu_count();
+    int nt = 8;
+    while (nt > 1 && (long long)tiles * ((ntile + nt - 1) / nt) < want) nt >>= 1;
+    if (nt > ntile) nt = ntile <= 1 ? 1 : ntile <= 2 ? 2 : ntile <= 4 ? 4 : 8;
+    g.t0 = 0;
+    const int grid = wgr * ((ntile + nt - 1) / nt);
+    if (nt == 1) k_gemm<1><<<grid, 256, 0, st>>>(g, wgr);
+    else if (nt == 2) k_gemm<2><<<grid, 256, 0, st>>>(g, wgr);
+    else if (nt == 4) k_gemm<4><<<grid, 256, 0, st>>>(g, wgr);
+    else k_gemm<8><<<grid, 256, 0, st>>>(g, wgr);
 }
 
 /* gate/up (split-K, one launch per expert dtype present); true when the launch also

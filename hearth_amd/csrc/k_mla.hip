@@ -22,8 +22,6 @@ using namespace hxd;
 
 namespace {
 
-constexpr int QL_TB = 8;    /* tokens per pass of the absorption */
-
 /* rope_apply (model.c:400-408): pairs (j, j + half) (NEOX) or (2j, 2j + 1) (GPT-J) */
 __device__ __forceinline__ void rope_wave(float *x, const float *cs, int half, int style, int lane) {
     for (int p = lane; p < half; p += 64) {
@@ -68,51 +66,74 @@ __global__ __launch_bounds__(256) void k_mla_post(MlaArgs a) {
     for (int e = lane; e < a.rdim; e += 64) dst[e] = x[e];
 }
 
-/* mla_qlat (model.c:650-671): ql[t][h][c] = sum_n q[t][h][n] * W_UK[h][n][c] with the
- * weight element dequantized as the reference does (d * q). One workgroup per (head,
- * 256 columns); each thread keeps QL_TB tokens' sums for its column. */
+/* bytes of one 64-column segment of a FORMAT.md row: a Q8 / Q4 block, or 64 floats */
+__device__ __forceinline__ int seg_bytes(int dt) { return dt == 3 ? 66 : dt == 4 ? 34 : dt == 0 ? 256 : 128; }
+
+/* mla_qlat (model.c:650-671): ql[t][h][c] = sum_n q[t][h][n] * W_UK[h][n][c], n ascending
+ * from 0.0f, with the weight element dequantized as the reference does (d * q). One
+ * workgroup per (head, 64 columns): the nope rows' segments of those columns are staged
+ * in LDS once (coalesced 2-byte loads), then tiles of QL_TT tokens' q_nope; wave w sums
+ * the tokens w, w + 4, ... of a tile, lane l column c0 + l. */
+constexpr int QL_TT = 32;
 __global__ __launch_bounds__(256) void k_mla_qlat(MlaArgs a) {
-    __shared__ float qn[QL_TB][MLA_NOPE_MAX];
-    const int nc = (a.C + 255) / 256;
-    const int h = (int)blockIdx.x / nc, c = ((int)blockIdx.x % nc) * 256 + (int)threadIdx.x;
+    extern __shared__ __attribute__((aligned(16))) uint8_t ql_lds[];
+    const int dt = a.wuk_dtype, seg = seg_bytes(dt), stride = (seg + 3) & ~3;
+    const int ncb = a.C / 64;
+    const int h = (int)blockIdx.x / ncb, cb = (int)blockIdx.x % ncb;
+    const int nope = a.nope, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    float *qn = (float *)(ql_lds + (size_t)nope * stride);   /* [QL_TT][nope] */
     const size_t row0 = (size_t)h * (a.nope + a.vd);
-    for (int t0 = 0; t0 < a.T; t0 += QL_TB) {
-        const int tn = a.T - t0 < QL_TB ? a.T - t0 : QL_TB;
+    const size_t segoff = dt >= 3 ? (size_t)cb * seg : (size_t)cb * 64 * (dt == 0 ? 4 : 2);
+    {
+        const int hw = seg >> 1;   /* 2-byte words per segment */
+        for (int i = tid; i < nope * hw; i += 256) {
+            const int n = i / hw, w = i % hw;
+            const uint16_t *src = (const uint16_t *)(a.wuk + (row0 + n) * a.wuk_rb + segoff);
+            ((uint16_t *)(ql_lds + (size_t)n * stride))[w] = src[w];
+        }
+    }
+    for (int t0 = 0; t0 < a.T; t0 += QL_TT) {
+        const int tn = a.T - t0 < QL_TT ? a.T - t0 : QL_TT;
         __syncthreads();
-        for (int i = threadIdx.x; i < tn * a.nope; i += 256) {
-            const int tt = i / a.nope, n = i % a.nope;
-            qn[tt][n] = a.q[((size_t)(t0 + tt) * a.H + h) * a.qh + n];
+        for (int i = tid; i < tn * nope; i += 256) {
+            const int tt = i / nope, n = i % nope;
+            qn[tt * nope + n] = a.q[((size_t)(t0 + tt) * a.H + h) * a.qh + n];
         }
         __syncthreads();
-        if (c < a.C) {
-            float acc[QL_TB];
+        float acc[QL_TT / 4];
 #pragma unroll
-            for (int tt = 0; tt < QL_TB; tt++) acc[tt] = 0.0f;
-            for (int n = 0; n < a.nope; n++) {
-                const float w = deq_elem(a.wuk + (row0 + n) * a.wuk_rb, a.wuk_dtype, c);
+        for (int j = 0; j < QL_TT / 4; j++) acc[j] = 0.0f;
+        for (int n = 0; n < nope; n++) {
+            const float w = deq_elem(ql_lds + (size_t)n * stride, dt, lane);
 #pragma unroll
-                for (int tt = 0; tt < QL_TB; tt++)
-                    if (tt < tn) acc[tt] = fadd(acc[tt], fmul(qn[tt][n], w));
-            }
-#pragma unroll
-            for (int tt = 0; tt < QL_TB; tt++)
-                if (tt < tn) a.qlat[((size_t)(t0 + tt) * a.H + h) * a.C + c] = acc[tt];
+            for (int j = 0; j < QL_TT / 4; j++)
+                if (wave + 4 * j < tn) acc[j] = fadd(acc[j], fmul(qn[(wave + 4 * j) * nope + n], w));
         }
+#pragma unroll
+        for (int j = 0; j < QL_TT / 4; j++)
+            if (wave + 4 * j < tn)
+                a.qlat[((size_t)(t0 + wave + 4 * j) * a.H + h) * a.C + cb * 64 + lane] = acc[j];
     }
 }
 
 /* mla_softmax's score (model.c:690-703): s = scale * (s_lat + dot16(q_pe, k_pe_v)),
- * s_lat already in S from the latent scores. One workgroup per (token, 256 rows), one
- * thread per row; the token's q_pe of every head is staged in LDS. */
+ * s_lat already in S from the latent scores. One workgroup per (token, 256 rows, 16
+ * heads), one thread per row: the 16 heads' q_pe are staged in LDS, the row's 16 s_lat
+ * are loaded up front (independent loads), then the 16 sums. */
+constexpr int PE_HG = 16;
 __global__ __launch_bounds__(256) void k_mla_pe(MlaArgs a) {
-    extern __shared__ float qpe[];   /* [H][rdim] */
-    const int t = (int)blockIdx.x % a.T, chunk = (int)blockIdx.x / a.T;
+    __shared__ float qpe[PE_HG * MLA_RMAX];
+    const int ng = (a.H + PE_HG - 1) / PE_HG;
+    int b = (int)blockIdx.x;
+    const int hg = b % ng;
+    b /= ng;
+    const int t = b % a.T, chunk = b / a.T;
     const int nr = a.g.pos0 + a.g.depth[t] + 1;
     if (chunk * 256 >= nr) return;   /* uniform */
-    const int r = a.rdim;
-    for (int i = threadIdx.x; i < a.H * r; i += 256) {
-        const int h = i / r, e = i % r;
-        qpe[i] = a.q[((size_t)t * a.H + h) * a.qh + a.nope + e];
+    const int r = a.rdim, h0 = hg * PE_HG, nh = a.H - h0 < PE_HG ? a.H - h0 : PE_HG;
+    for (int i = threadIdx.x; i < nh * r; i += 256) {
+        const int hh = i / r, e = i % r;
+        qpe[hh * MLA_RMAX + e] = a.q[((size_t)t * a.H + h0 + hh) * a.qh + a.nope + e];
     }
     __syncthreads();
     const int v = chunk * 256 + (int)threadIdx.x;
@@ -122,9 +143,13 @@ __global__ __launch_bounds__(256) void k_mla_pe(MlaArgs a) {
     float k[MLA_RMAX];
 #pragma unroll
     for (int e = 0; e < MLA_RMAX; e++) k[e] = e < r ? kr[e] : 0.0f;
-    float *s = a.S + (size_t)t * a.H * a.ldS + v;
-    for (int h = 0; h < a.H; h++) {
-        const float *qh = qpe + h * r;
+    float *s = a.S + ((size_t)t * a.H + h0) * a.ldS + v;
+    float sl[PE_HG];
+#pragma unroll
+    for (int hh = 0; hh < PE_HG; hh++) sl[hh] = hh < nh ? s[(size_t)hh * a.ldS] : 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < PE_HG; hh++) {
+        const float *qh = qpe + hh * MLA_RMAX;
         float L[16];
 #pragma unroll
         for (int j = 0; j < 16; j++) L[j] = 0.0f;
@@ -135,8 +160,7 @@ __global__ __launch_bounds__(256) void k_mla_pe(MlaArgs a) {
         for (int st = 8; st >= 1; st >>= 1)
 #pragma unroll
             for (int j = 0; j < st; j++) L[j] = fadd(L[j], L[j + st]);
-        float *sv = s + (size_t)h * a.ldS;
-        *sv = fmul(a.scale, fadd(*sv, L[0]));
+        if (hh < nh) s[(size_t)hh * a.ldS] = fmul(a.scale, fadd(sl[hh], L[0]));
     }
 }
 
@@ -166,13 +190,16 @@ void mla_post(const MlaArgs &a, hipStream_t st) {
 }
 
 void mla_qlat(const MlaArgs &a, hipStream_t st) {
-    k_mla_qlat<<<a.H * ((a.C + 255) / 256), 256, 0, st>>>(a);
+    /* C is a multiple of 128 (checked at open); LDS: nope segments + a token tile */
+    const int dt = a.wuk_dtype, seg = dt == 3 ? 66 : dt == 4 ? 34 : dt == 0 ? 256 : 128;
+    const size_t lds = (size_t)a.nope * ((seg + 3) & ~3) + sizeof(float) * (size_t)QL_TT * a.nope;
+    k_mla_qlat<<<a.H * (a.C / 64), 256, lds, st>>>(a);
 }
 
 void mla_pe_scores(const MlaArgs &a, hipStream_t st) {
     const int max_nr = a.g.pos0 + a.T;   /* depth[t] <= t */
     const int nchunks = (max_nr + 255) / 256;
-    k_mla_pe<<<a.T * nchunks, 256, sizeof(float) * (size_t)a.H * a.rdim, st>>>(a);
+    k_mla_pe<<<a.T * nchunks * ((a.H + PE_HG - 1) / PE_HG), 256, 0, st>>>(a);
 }
 
 void mla_gather(const MlaArgs &a, hipStream_t st) {
