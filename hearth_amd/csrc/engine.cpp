@@ -158,6 +158,21 @@ struct hearth_engine {
     int geom_chain = 1;           /* the uploaded geometry is a chain (no parent table, or parent[i] = i - 1) */
 
     int pos = 0;
+    int *d_pos = nullptr;    /* device [1]: pos of the forward being run (the kernels' pos0) */
+    /* Captured forwards: the launch sequence of one forward, replayed as a hipGraph, per
+     * (tokens, logits wanted, chain geometry, row bound). pos0 and the geometry live in
+     * device memory, so a graph serves every position up to its row bound. */
+    struct Captured {
+        int T, chain, rows;
+        bool logits;
+        hipGraph_t graph;
+        hipGraphExec_t exec;
+    };
+    std::vector<Captured> graphs;
+    bool graph_on = true;    /* HEARTH_GPU_GRAPH=0 turns capture off */
+    int rows_bound = 0;      /* nonzero while capturing: the graph's bound on pos + T */
+    int nr_max(int T) const { return rows_bound ? rows_bound : pos + T; }
+    void run_forward(int T, bool want_logits);
     /* telemetry */
     uint64_t tokens_done = 0, forward_calls = 0;
     double wall_s = 0.0;
@@ -227,6 +242,10 @@ struct hearth_engine {
     ~hearth_engine() {
         if (dev >= 0) (void)hipSetDevice(dev);
         if (st) (void)hipStreamSynchronize(st);
+        for (Captured &g : graphs) {
+            (void)hipGraphExecDestroy(g.exec);
+            (void)hipGraphDestroy(g.graph);
+        }
         for (auto &e : ev_pool) (void)hipEventDestroy(e);
         if (geom_ev) (void)hipEventDestroy(geom_ev);
         for (void *p : allocs) (void)hipFree(p);
@@ -682,7 +701,8 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
             ck(hipHostMalloc((void **)&h_plog, sizeof(float) * Bs * E, hipHostMallocDefault));
             pf_mark.assign(E, 0);
         }
-        ck(hipHostMalloc((void **)&h_geom, sizeof(int) * (2 * Bs + Bs * Bs), hipHostMallocDefault));
+        ck(hipHostMalloc((void **)&h_geom, sizeof(int) * (2 * Bs + Bs * Bs + 1), hipHostMallocDefault));
+        d_pos = dnew<int>(1);
         ck(hipHostMalloc((void **)&h_rope, sizeof(float) * Bs * std::max(rope_dim, 2), hipHostMallocDefault));
         ck(hipHostMalloc((void **)&h_res, sizeof(int) * (2 * Bs + 8), hipHostMallocDefault));
         ck(hipEventCreateWithFlags(&geom_ev, hipEventDisableTiming));
@@ -746,10 +766,10 @@ void hearth_engine::attn_mla(const Layer &w, int l, int T) {
     hxd::MlaArgs ma{};
     ma.T = T; ma.H = H; ma.C = C; ma.rdim = rdim; ma.nope = nope; ma.vd = vd; ma.qh = qh;
     ma.kva = kva; ma.q = qb; ma.kv_norm = w.kv_a_norm; ma.cc = cc; ma.kp = cc + (size_t)cap * C;
-    ma.rope = rope; ma.rope_dim = rope_dim; ma.rope_style = c.rope_style; ma.eps = c.eps; ma.pos0 = pos;
+    ma.rope = rope; ma.rope_dim = rope_dim; ma.rope_style = c.rope_style; ma.eps = c.eps; ma.pos = d_pos;
     ma.wuk = w.kvb_raw; ma.wuk_dtype = w.kvb_dtype; ma.wuk_rb = w.kvb_rb; ma.qlat = qr;
     ma.S = S; ma.ldS = ldS; ma.scale = c.attn_scale;
-    ma.g.depth = depth; ma.g.anc = anc; ma.g.anc_ld = B; ma.g.pos0 = pos; ma.g.chain = geom_chain;
+    ma.g.depth = depth; ma.g.anc = anc; ma.g.anc_ld = B; ma.g.pos = d_pos; ma.g.nr_max = nr_max(T); ma.g.chain = geom_chain;
     ma.Yv = yv; ma.att = att; ma.aatt = aatt;
     hxl::mla_post(ma, st);
     hxl::mla_qlat(ma, st);
@@ -806,13 +826,13 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             qa.q = qb; qa.k = kb; qa.v = vb; qa.bq = w.bq; qa.bk = w.bk; qa.bv = w.bv; qa.qn = w.qn; qa.kn = w.kn;
             qa.qout = qr; qa.kc = kv + (size_t)l * kv_layer; qa.vc = qa.kc + (size_t)Hkv * cap * hd;
             qa.rope = rope; qa.rfull = rfull; qa.T = T; qa.H = H; qa.Hkv = Hkv; qa.hd = hd; qa.cap = cap;
-            qa.qk_norm = c.qk_norm; qa.rope_dim = rope_dim; qa.rope_style = c.rope_style; qa.eps = c.eps; qa.pos0 = pos;
+            qa.qk_norm = c.qk_norm; qa.rope_dim = rope_dim; qa.rope_style = c.rope_style; qa.eps = c.eps; qa.pos = d_pos;
             hxl::qkv_post(qa, st);
             dump("q", l, qr, T, q_dim);
             hxd::AttnArgs at{};
             at.q = qr; at.kc = qa.kc; at.vc = qa.vc; at.S = S; at.ldS = ldS; at.out = att; at.T = T; at.H = H;
             at.Hkv = Hkv; at.hd = hd; at.cap = cap; at.scale = c.attn_scale;
-            at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos0 = pos; at.g.chain = geom_chain;
+            at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos = d_pos; at.g.nr_max = nr_max(T); at.g.chain = geom_chain;
             at.qo = aatt; at.qo_on = w.o.quant && hd % 64 == 0;
             hxl::attention(at, st);
             dump("att", l, att, T, q_dim);
@@ -1021,15 +1041,63 @@ int hearth_engine::run_geometry(const int32_t *tok, const int32_t *parent, int n
             h_rope[(size_t)i * rope_dim + 2 * j + 1] = host_sinf(th) * c.rope_factor;
         }
     }
+    int *hpos = h_geom + 2 * B + (size_t)B * B;
+    *hpos = pos;
     ck(hipMemcpyAsync(tokens, ht, sizeof(int) * n, hipMemcpyHostToDevice, st));
     ck(hipMemcpyAsync(depth, hdp, sizeof(int) * n, hipMemcpyHostToDevice, st));
     ck(hipMemcpyAsync(anc, hanc, sizeof(int) * (size_t)n * B, hipMemcpyHostToDevice, st));
     if (rope_dim) ck(hipMemcpyAsync(rope, h_rope, sizeof(float) * (size_t)n * rope_dim, hipMemcpyHostToDevice, st));
+    ck(hipMemcpyAsync(d_pos, hpos, sizeof(int), hipMemcpyHostToDevice, st));
     ck(hipEventRecord(geom_ev, st));
     geom_pending = true;
-    forward(n, logits_out != nullptr, 0);
+    run_forward(n, logits_out != nullptr);
     if (logits_out) ck(hipMemcpyAsync(logits_out, logits, sizeof(float) * (size_t)n * V, hipMemcpyDeviceToHost, st));
     return OK;
+}
+
+/* The forward of T tokens whose geometry is uploaded: replayed from a captured graph
+ * when the call is one a graph can serve (experts resident, no route replay, no
+ * per-launch timing or debug dumps, at most 128 tokens), else launched directly. The
+ * graph's grids cover rows up to the next multiple of 1024 (at most the capacity), and
+ * the kernels read pos0 from d_pos, so the replay computes what the direct launches
+ * would. At most 32 graphs are kept (the oldest is dropped). */
+void hearth_engine::run_forward(int T, bool want_logits) {
+    if (!graph_on || store || replay_dev || profiling || !dump_dir.empty() || T > 128) {
+        forward(T, want_logits, 0);
+        return;
+    }
+    const int rows = std::min(cap, (pos + T + 1023) / 1024 * 1024);
+    Captured *cg = nullptr;
+    for (Captured &g : graphs)
+        if (g.T == T && g.chain == geom_chain && g.rows == rows && g.logits == want_logits) cg = &g;
+    if (!cg) {
+        if (graphs.size() >= 32) {
+            (void)hipGraphExecDestroy(graphs.front().exec);
+            (void)hipGraphDestroy(graphs.front().graph);
+            graphs.erase(graphs.begin());
+        }
+        Captured g{T, geom_chain, rows, want_logits, nullptr, nullptr};
+        ck(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        rows_bound = rows;
+        try {
+            forward(T, want_logits, 0);
+        } catch (const DeviceError &) {
+            rows_bound = 0;
+            hipGraph_t dead = nullptr;
+            if (hipStreamEndCapture(st, &dead) == hipSuccess && dead) (void)hipGraphDestroy(dead);
+            throw;
+        }
+        rows_bound = 0;
+        ck(hipStreamEndCapture(st, &g.graph));
+        const hipError_t e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(g.graph);
+            throw DeviceError{e};
+        }
+        graphs.push_back(g);
+        cg = &graphs.back();
+    }
+    ck(hipGraphLaunch(cg->exec, st));
 }
 
 /* Routing-trace rows of the T tokens just evaluated: appended to trace_pend, which the
@@ -1198,6 +1266,7 @@ HEARTH_API hearth_engine *hearth_open(const hearth_options *in, char *err, size_
     e->opt = o;
     e->verbose = o.verbose;
     if (const char *dd = getenv("HEARTH_DEBUG_DUMP")) e->dump_dir = dd;
+    if (const char *gg = getenv("HEARTH_GPU_GRAPH")) e->graph_on = strcmp(gg, "0") != 0;
     if (!e->open_model(err, errlen)) return nullptr;
     log_msg(LOG_INFO, "%s: %s, %d layers (%d MoE), d_model %d, vocab %d, KV %d positions, device %d", o.model_path,
             e->c.arch.c_str(), e->L, e->c.n_moe, e->D, e->V, e->cap, e->dev);

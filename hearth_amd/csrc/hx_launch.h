@@ -76,12 +76,15 @@ struct RouteArgs {
 /* Per-call token geometry: token t sits at KV slot pos0 + t, has RoPE position
  * pos0 + depth[t] and attends to slots 0..pos0-1 followed by pos0 + anc[t][j] for
  * j = 0..depth[t] (its ancestors from the root, itself last). A chain has depth[t] = t
- * and anc[t][j] = j. */
+ * and anc[t][j] = j. pos0 is read from device memory, so that one captured launch
+ * sequence serves every position; nr_max bounds every token's row count pos0 +
+ * depth[t] + 1 and sizes the grids that cover rows. */
 struct TokGeom {
     const int *depth;         /* [T] */
     const int *anc;           /* [T][anc_ld] */
     int anc_ld;
-    int pos0;
+    const int *pos;           /* device [1]: pos0 */
+    int nr_max;
     int chain;                /* 1: token t sits at slot pos0 + t with ancestors pos0..pos0 + t */
 };
 
@@ -108,7 +111,7 @@ struct QkvArgs {
     float *rfull;             /* [T][2] scratch for qk_norm = 2 */
     int T, H, Hkv, hd, cap, qk_norm, rope_dim, rope_style;
     float eps;
-    int pos0;
+    const int *pos;           /* device [1]: pos0; token t's K/V go to slot pos0 + t */
 };
 
 /* Residual update + RMSNorm + activation quantization, one workgroup per token:
@@ -164,7 +167,7 @@ struct MlaArgs {
     const float *rope;                /* [T][rope_dim] (cos, sin) pairs */
     int rope_dim, rope_style;
     float eps;
-    int pos0;
+    const int *pos;                   /* device [1]: pos0 */
     const uint8_t *wuk;               /* attn_kv_b as stored (FORMAT rows of C) */
     int wuk_dtype;
     size_t wuk_rb;

@@ -31,8 +31,8 @@ constexpr int SC_ROWS = 256;   /* rows per scores workgroup (one per thread) */
 constexpr int KC = 16;         /* K floats per staged chunk (head_dim % 16 == 0) */
 constexpr int MAX_ANC = 4096;  /* ancestors of one token (max_batch) */
 
-__device__ __forceinline__ int row_slot(const TokGeom &g, int t, int v) {
-    return v < g.pos0 ? v : g.pos0 + g.anc[(size_t)t * g.anc_ld + (v - g.pos0)];
+__device__ __forceinline__ int row_slot(const TokGeom &g, int pos0, int t, int v) {
+    return v < pos0 ? v : pos0 + g.anc[(size_t)t * g.anc_ld + (v - pos0)];
 }
 
 /* Scores of NH heads of KV group g for 256 rows v of token t: one thread per row, 16
@@ -49,12 +49,12 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
     const int g = b % Hkv;
     b /= Hkv;
     const int t = b % a.T, c = b / a.T;
-    const int nr = a.g.pos0 + a.g.depth[t] + 1;
+    const int pos0 = *a.g.pos, nr = pos0 + a.g.depth[t] + 1;
     const int v0 = c * SC_ROWS;
     if (v0 >= nr) return;   /* uniform */
     const int tid = threadIdx.x;
     const int nrows = nr - v0 < SC_ROWS ? nr - v0 : SC_ROWS;
-    slot_s[tid] = row_slot(a.g, t, v0 + (tid < nrows ? tid : nrows - 1));
+    slot_s[tid] = row_slot(a.g, pos0, t, v0 + (tid < nrows ? tid : nrows - 1));
     __syncthreads();
     /* staging: float4 k = tid + 256u of the chunk: row k / 4, floats 4 (k % 4) .. + 3 */
     const float *src[4];
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
     const int g = b % Hkv;
     b /= Hkv;
     const int t = b % a.T, c = b / a.T;
-    const int nr = a.g.pos0 + a.g.depth[t] + 1;
+    const int pos0 = *a.g.pos, nr = pos0 + a.g.depth[t] + 1;
     const int v0 = c * S16_RB;
     if (v0 >= nr) return;   /* uniform */
     const int tid = threadIdx.x, j = tid & 15, rl = tid >> 4;
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
     for (int pass = 0; pass < S16_NP; pass++) {
         const int v = v0 + pass * 16 + rl;
         vrow[pass] = v;
-        const float *kr = a.kc + ((size_t)g * a.cap + row_slot(a.g, t, v < nr ? v : nr - 1)) * hd + j;
+        const float *kr = a.kc + ((size_t)g * a.cap + row_slot(a.g, pos0, t, v < nr ? v : nr - 1)) * hd + j;
 #pragma unroll
         for (int i = 0; i < HI; i++) kv[pass][i] = kr[16 * i];
     }
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
     __shared__ unsigned long long etab[32];
     exp_table_to_lds(etab);
     const int t = blockIdx.x / a.H, h = blockIdx.x % a.H, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nr = a.g.pos0 + a.g.depth[t] + 1;
+    const int pos0 = *a.g.pos, nr = pos0 + a.g.depth[t] + 1;
     float *s = a.S + ((size_t)t * a.H + h) * a.ldS;
     const bool inreg = nr <= SM_CH;
     const int wlo = __builtin_amdgcn_readfirstlane(tid >> 6) * 64;   /* first thread of the wave */
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
     b /= Hkv;
     const int hq = b % qpt, t = b / qpt;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int pos0 = a.g.pos0, dep = a.g.depth[t];
+    const int pos0 = *a.g.pos, dep = a.g.depth[t];
     const int nr = pos0 + dep + 1;
     const int ntiles = (nr + TV_ROWS - 1) / TV_ROWS;
     const bool chain = a.g.chain != 0;
@@ -541,7 +541,7 @@ __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
 namespace hxl {
 
 void attention_scores(const AttnArgs &a, hipStream_t st) {
-    const int max_nr = a.g.pos0 + a.T;   /* depth[t] <= t */
+    const int max_nr = a.g.nr_max;
     if (a.hd % 64 == 0 && a.hd <= 512) {
         const int grid = ((max_nr + S16_RB - 1) / S16_RB) * a.T * a.Hkv;
         switch (a.hd / 16) {

@@ -564,7 +564,7 @@ __global__ __launch_bounds__(256) void k_qkv_post(QkvArgs a, const float *__rest
         x[ib] = fadd(fmul(bv, c), fmul(av, s));
     }
     wave_sync();
-    const size_t slot = (size_t)(a.pos0 + t);
+    const size_t slot = (size_t)(*a.pos + t);
     if (isq) {
         for (int e = lane; e < hd; e += 64) a.qout[(size_t)t * qd + (size_t)g * hd + e] = x[e];
     } else {

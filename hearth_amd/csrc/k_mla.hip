@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256) void k_mla_post(MlaArgs a) {
     const int item = blockIdx.x * 4 + wave;
     if (item >= a.T * (1 + a.H)) return;
     const int t = item / (1 + a.H), j = item % (1 + a.H);
-    const size_t slot = (size_t)(a.pos0 + t);
+    const size_t slot = (size_t)(*a.pos + t);
     float *x = buf[wave];
     float *dst;
     if (j == 0) {
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256) void k_mla_pe(MlaArgs a) {
     const int hg = b % ng;
     b /= ng;
     const int t = b % a.T, chunk = b / a.T;
-    const int nr = a.g.pos0 + a.g.depth[t] + 1;
+    const int pos0 = *a.g.pos, nr = pos0 + a.g.depth[t] + 1;
     if (chunk * 256 >= nr) return;   /* uniform */
     const int r = a.rdim, h0 = hg * PE_HG, nh = a.H - h0 < PE_HG ? a.H - h0 : PE_HG;
     for (int i = threadIdx.x; i < nh * r; i += 256) {
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(256) void k_mla_pe(MlaArgs a) {
     __syncthreads();
     const int v = chunk * 256 + (int)threadIdx.x;
     if (v >= nr) return;
-    const int slot = v < a.g.pos0 ? v : a.g.pos0 + a.g.anc[(size_t)t * a.g.anc_ld + (v - a.g.pos0)];
+    const int slot = v < pos0 ? v : pos0 + a.g.anc[(size_t)t * a.g.anc_ld + (v - pos0)];
     const float *kr = a.kp + (size_t)slot * r;
     float k[MLA_RMAX];
 #pragma unroll
@@ -197,7 +197,7 @@ void mla_qlat(const MlaArgs &a, hipStream_t st) {
 }
 
 void mla_pe_scores(const MlaArgs &a, hipStream_t st) {
-    const int max_nr = a.g.pos0 + a.T;   /* depth[t] <= t */
+    const int max_nr = a.g.nr_max;
     const int nchunks = (max_nr + 255) / 256;
     k_mla_pe<<<a.T * nchunks * ((a.H + PE_HG - 1) / PE_HG), 256, 0, st>>>(a);
 }

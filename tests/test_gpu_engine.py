@@ -181,3 +181,42 @@ def test_tree_greedy_verify_matches_oracle(eng, tiny_model):
     rc, opath, ofin = O.accept_tree(lg, tok, par)
     assert rc == 0 and path == opath and final == ofin
     assert path[:2] == [0, 2]
+
+
+@pytest.mark.parametrize("which", ["tiny", "dsv3"])
+def test_captured_forward_equals_direct_launches(tiny_model, variant_models, monkeypatch, which):
+    """Calls of at most 128 tokens replay a captured graph of the forward (pos0 read from
+    device memory, grids sized for a row bound); the same call sequence with capture off
+    (HEARTH_GPU_GRAPH=0) launches every kernel directly. The graphs are replayed at
+    several positions, for chains, a tree and single tokens, with eager work (prefill
+    chunks above 128 tokens, rewinds, commits) between the replays: every logit is the
+    same."""
+    path = tiny_model if which == "tiny" else variant_models("dsv3")
+    vocab = 4096
+    toks = [int(t) for t in container.uniform_ints(61, 400, vocab)]
+    parent = [-1, 0, 0, 1, 1, 2, 3]
+
+    def run():
+        out = []
+        with Engine(path, max_seq=1024) as e:
+            out.append(e.eval(toks[:200], all_logits=True))          # 200 > 128: direct launches
+            for step in range(4):                                     # a 9-token chain, replayed at 4 positions
+                out.append(e.eval(toks[200 + 9 * step:209 + 9 * step], all_logits=True))
+                e.rewind(e.pos - 4)
+            out.append(e.eval([toks[300]], all_logits=True))          # one token
+            out.append(e.eval([toks[301]], all_logits=True))
+            for step in range(3):                                     # a 7-node tree, committed each time
+                lg = e.verify_tree(toks[310 + 7 * step:317 + 7 * step], parent)
+                out.append(lg)
+                e.commit_path([0, 1, 3])
+            out.append(e.eval(toks[340:340 + 150], all_logits=True))  # direct again
+            out.append(e.eval(toks[330:339], all_logits=True))        # the chain graph once more
+        return out
+
+    monkeypatch.setenv("HEARTH_GPU_GRAPH", "0")
+    direct = run()
+    monkeypatch.setenv("HEARTH_GPU_GRAPH", "1")
+    graphed = run()
+    assert len(direct) == len(graphed)
+    for i, (a, b) in enumerate(zip(direct, graphed)):
+        assert np.array_equal(_bits(a), _bits(b)), f"call {i}: replayed graph differs from direct launches"
