@@ -174,7 +174,7 @@ HEARTH_API int hearth_gpu_accept_sample(const float *rows, int n, int V, const i
         return E_IO;
     const hxl::SamplerSpec sp{smp->temperature, smp->top_p, smp->min_p, smp->repetition_penalty, smp->top_k,
                               smp->context, n_ctx};
-    hxl::accept_sample(m, dr, n, V, m.tok, m.par, sp, q, u, s.st);
+    if (hxl::accept_sample(m, dr, n, V, m.tok, m.par, sp, q, u, s.st) != hipSuccess) return E_IO;
     std::vector<int> res(3), path(n);
     if (hipMemcpyAsync(res.data(), m.result, sizeof(int) * 3, hipMemcpyDeviceToHost, s.st) != hipSuccess ||
         hipMemcpyAsync(path.data(), m.path, sizeof(int) * n, hipMemcpyDeviceToHost, s.st) != hipSuccess ||
@@ -209,7 +209,7 @@ HEARTH_API int hearth_gpu_probs(const float *rows, int n, int V, const int32_t *
         return E_IO;
     const hxl::SamplerSpec sp{smp->temperature, smp->top_p, smp->min_p, smp->repetition_penalty, smp->top_k,
                               smp->context, n_ctx};
-    hxl::sample_probs(m, dr, n, V, m.tok, m.par, sp, s.st);
+    if (hxl::sample_probs(m, dr, n, V, m.tok, m.par, sp, s.st) != hipSuccess) return E_IO;
     std::vector<int> rc(n);
     if (hipMemcpyAsync(rc.data(), m.row_rc, sizeof(int) * n, hipMemcpyDeviceToHost, s.st) != hipSuccess ||
         hipMemcpyAsync(p_out, m.P, sizeof(double) * (size_t)n * V, hipMemcpyDeviceToHost, s.st) != hipSuccess ||

@@ -1670,7 +1670,7 @@ HEARTH_API int hearth_verify_sample(hearth_engine *e, const int32_t *tokens, con
         const int n_ctx = s->repetition_penalty != 1.0 ? s->n_context : 0;
         ck(e->samp.ensure(n, e->V, q != nullptr, n_ctx));
         hxl::SamplerSpec sp{s->temperature, s->top_p, s->min_p, s->repetition_penalty, s->top_k, s->context, n_ctx};
-        hxl::accept_sample(e->samp, e->logits, n, e->V, e->tokens, d_par, sp, q, u, e->st);
+        ck(hxl::accept_sample(e->samp, e->logits, n, e->V, e->tokens, d_par, sp, q, u, e->st));
         d_path = e->samp.path;
         d_res = e->samp.result;
     });

@@ -208,8 +208,12 @@ struct SampleArgs {
     const int *ctx;                   /* penalty context ids [n_ctx] */
     int n_ctx;
     double *P;                        /* [n][V] final distributions */
-    unsigned long long *skey;         /* [n][sort_n] sort scratch for large candidate sets */
+    unsigned long long *skey;         /* [n][sort_n] top-p candidates (tier 0), in index order; then sort scratch */
     int *sidx;                        /* [n][sort_n] */
+    unsigned long long *skey2;        /* [n][sort_n] tier 0 sorted by descending p (stable) */
+    int *sidx2;                       /* [n][sort_n] */
+    int *seg_begin, *seg_end;         /* [n] row v's candidates: [seg_begin, seg_end) = v * sort_n + [0, m) */
+    int *bstar;                       /* [n] first histogram bin of tier 0 (-1: every nonzero entry) */
     int sort_n;                       /* power of two >= V */
     double *wa, *wb, *cw, *cc;        /* [V] residuals and draw scratch */
     int *ci;                          /* [V] */
@@ -268,9 +272,11 @@ struct SampleScratch {
     int n_cap = 0, V = 0, ctx_cap = 0, sort_n = 0;
     bool has_q = false;
     double *P = nullptr, *q = nullptr, *u = nullptr, *wa = nullptr, *wb = nullptr, *cw = nullptr, *cc = nullptr;
-    unsigned long long *skey = nullptr;
-    int *sidx = nullptr, *ci = nullptr, *row_rc = nullptr, *path = nullptr, *result = nullptr, *ctx = nullptr,
-        *tok = nullptr, *par = nullptr;
+    unsigned long long *skey = nullptr, *skey2 = nullptr;
+    int *sidx = nullptr, *sidx2 = nullptr, *seg_begin = nullptr, *seg_end = nullptr, *bstar = nullptr, *ci = nullptr,
+        *row_rc = nullptr, *path = nullptr, *result = nullptr, *ctx = nullptr, *tok = nullptr, *par = nullptr;
+    void *sort_tmp = nullptr;         /* segmented radix sort workspace for n_cap rows */
+    size_t sort_tmp_bytes = 0;
     hipError_t ensure(int n, int V, bool need_q, int n_ctx);
     void release();
     ~SampleScratch() { release(); }
@@ -280,10 +286,10 @@ struct SampleScratch {
  * penalty context, then runs the distribution and walk kernels on rows (device [n][V])
  * with device tokens/parent. The accepted path is left in m.path, and n_path, final
  * token and status (0, or -1 for bad logits) in m.result[0..2]. */
-void accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
-                   const SamplerSpec &s, const double *q, const double *u, hipStream_t st);
+hipError_t accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st);
 /* The distribution kernel alone: m.P[v] = the final distribution of row v (the penalty
  * context of row v includes the path tokens of nodes 1..v), m.row_rc[v] its status. */
-void sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
-                  const SamplerSpec &s, hipStream_t st);
+hipError_t sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                        const SamplerSpec &s, hipStream_t st);
 } // namespace hxl

@@ -17,20 +17,32 @@
  *
  * Top-p does not sort the whole row. A histogram of the probabilities by exponent
  * (and one mantissa bit) picks the highest bins whose approximate mass exceeds top_p;
- * only their entries are sorted (bitonic, in LDS up to 8192 entries, else in the row's
- * global scratch) and summed in order. Once the running sum c has reached
+ * only their entries are sorted and summed in order: the candidates of every row are
+ * gathered in index order and sorted by one segmented radix sort over all rows
+ * (rocPRIM, stable, so equal probabilities keep index order, as a stable descending
+ * argsort does). Once the running sum c has reached
  * top_p * (1 + 2^-48), every later entry e of the descending order has
  * before_e = fl(c_e - p_e) >= c_{e-1} (1 - 3 * 2^-53) > top_p and is dropped, so the
  * entries below the chosen bins never need ordering. If the chosen bins run out before
  * that (the histogram is approximate), the rest of the row is sorted and the chain
  * continues — the result never depends on the histogram.
  *
- * k_sample_probs: one workgroup per verify row writes the row's final distribution.
- * k_sample_walk:  one workgroup walks the tree from the root with the uniforms.
+ * If the chosen bins run out before the running sum reaches top_p (the histogram is
+ * approximate), the rest of the row is sorted in the workgroup (bitonic, in LDS up to
+ * 8192 entries, else in the row's global scratch) and the chain continues.
+ *
+ * k_sample_probs:  one workgroup per verify row; the distribution up to top-p, then
+ *                  the row's top-p candidates (tier 0) in index order;
+ * (segmented radix sort of the candidates, all rows at once)
+ * k_sample_top_p:  one workgroup per row; the cumulative-sum chain over the sorted
+ *                  candidates, the rest of the row if needed, renormalization, min-p;
+ * k_sample_walk:   one workgroup walks the tree from the root with the uniforms.
  */
 #include <climits>
 #include <functional>
 #include <vector>
+
+#include <rocprim/device/device_segmented_radix_sort.hpp>
 
 #include "hx_launch.h"
 
@@ -278,6 +290,96 @@ __device__ void bitonic_global(unsigned long long *gkey, int *gidx, int N, unsig
     }
 }
 
+/* ---------------------------------------------------------------- exact running sums */
+
+/* The float64 running sum c_j = fl(c_{j-1} + x_j), j = 0..m-1, from c_{-1} = 0, of
+ * finite x_j >= 0 (np.cumsum's chain), computed SP_T entries at a time by the whole
+ * workgroup. While c stays in one binade [2^e, 2^(e+1)) every partial sum is a
+ * multiple of u = 2^(e-52) and so is every rounded sum, so fl(c + x) = c + RN_u(x):
+ * the integer prefix sums of RN_u(x_j) / u give every c_j of a chunk at once. An entry
+ * whose sum would leave the binade, or whose x / u is halfway between two integers
+ * (round-half-even then depends on the parity of c / u), is added on its own and the
+ * chunk restarts after it. on_entry(j, c_j) is called once per entry by one thread.
+ * The chain stops after the chunk in which c_j >= stop_at first holds; *stop_j gets
+ * that j (m if never). Returns the last c computed. */
+struct ChainShared {
+    long long wsum[SP_WAVES];
+    double c, cnext;
+    int first_bad, stop;
+};
+
+template <class GetX, class OnEntry>
+__device__ double chain_exact(GetX get_x, int m, double stop_at, int *stop_j, OnEntry on_entry, ChainShared &cs) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    double c = 0.0;
+    int j0 = 0, stop = m;
+    while (j0 < m && stop == m) {
+        if (c == 0.0) {   /* fl(0 + x) = x */
+            c = get_x(j0);
+            if (tid == 0) on_entry(j0, c);
+            if (c >= stop_at) stop = j0;
+            j0++;
+            continue;
+        }
+        int e = ilogb(c);
+        if (e < -1022) e = -1022;
+        const double u = ldexp(1.0, e - 52);
+        const long long base = (long long)(c / u);   /* exact: c is a multiple of u below 2^53 u */
+        const int j = j0 + tid;
+        const double x = j < m ? get_x(j) : 0.0;
+        long long d = 0;
+        bool bad = false;
+        if (j < m) {
+            const double q = x / u;   /* a power-of-two scaling: exact */
+            if (!(q < 0x1p53)) {
+                bad = true;
+            } else {
+                const double f = floor(q), r = q - f;
+                d = (long long)f + (r > 0.5 ? 1 : 0);
+                bad = r == 0.5;
+            }
+        }
+        long long inc = d;
+        for (int off = 1; off < 64; off <<= 1) {
+            const long long y = __shfl_up(inc, off, 64);
+            if (lane >= off) inc += y;
+        }
+        if (lane == 63) cs.wsum[w] = inc;
+        if (tid == 0) { cs.first_bad = INT_MAX; cs.stop = INT_MAX; }
+        __syncthreads();
+        long long before = 0;
+        for (int i = 0; i < w; i++) before += cs.wsum[i];
+        const long long D = base + before + inc;   /* c_j / u if no entry before j was bad */
+        if (j < m && (bad || D >= (1ll << 53))) atomicMin(&cs.first_bad, j);
+        __syncthreads();
+        const int fb = cs.first_bad, jend = j0 + SP_T < m ? j0 + SP_T : m;
+        const int last = (fb < jend ? fb : jend) - 1;   /* last entry finished in parallel */
+        if (j <= last) {
+            const double cj = (double)D * u;   /* an integer below 2^53 times a power of two: exact */
+            on_entry(j, cj);
+            if (cj >= stop_at) atomicMin(&cs.stop, j);
+            if (j == last) cs.c = cj;
+        }
+        __syncthreads();
+        if (last >= j0) c = cs.c;
+        if (cs.stop != INT_MAX) {
+            stop = cs.stop;
+            break;
+        }
+        if (fb < jend) {   /* entry fb on its own */
+            c = dadd(c, get_x(fb));
+            if (tid == 0) on_entry(fb, c);
+            if (c >= stop_at) stop = fb;
+            j0 = fb + 1;
+        } else {
+            j0 = jend;
+        }
+        __syncthreads();
+    }
+    *stop_j = stop;
+    return c;
+}
+
 /* ---------------------------------------------------------------- per-row distribution */
 
 struct RowShared {
@@ -297,6 +399,10 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
     const float *row = a.rows + (size_t)v * V;
     double *P = a.P + (size_t)v * V;
     double *lv = (double *)smem;
+    if (tid == 0) {   /* no candidates unless top-p runs */
+        a.seg_begin[v] = v * a.sort_n;
+        a.seg_end[v] = v * a.sort_n;
+    }
 
     /* Sampler._penalised: the ids of the context and of the path nodes 1..v */
     const bool pen = a.rp != 1.0;
@@ -368,7 +474,7 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
     for (int i = tid; i < V; i += SP_T) P[i] = ddiv(P[i], s);
 
     if (a.top_p < 1.0) {
-        const double top_p = a.top_p, thr_hi = dmul(top_p, 1.0 + 0x1p-48);
+        const double top_p = a.top_p;
         uint32_t *hcnt = (uint32_t *)smem;
         double *hmass = (double *)(smem + HBINS * 4);
         for (int i = tid; i < HBINS; i += SP_T) { hcnt[i] = 0; hmass[i] = 0.0; }
@@ -404,13 +510,79 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
         }
         __syncthreads();
         const int bstar = rs.bi[2];
-        /* tier 0: bins >= b* (all nonzero entries when b* < 0); tier 1: the rest */
+        /* tier 0 (bins >= b*; all nonzero entries when b* < 0) in index order: thread tid
+         * takes the contiguous indices [tid * per, (tid + 1) * per) */
+        const int blo = bstar < 0 ? 0 : bstar, per = (V + SP_T - 1) / SP_T;
+        const int i0 = tid * per < V ? tid * per : V, i1 = i0 + per < V ? i0 + per : V;
+        int cnt = 0;
+        for (int i = i0; i < i1; i++) {
+            const double p = P[i];
+            cnt += (p > 0.0 && (int)((unsigned long long)__double_as_longlong(p) >> 51) >= blo) ? 1 : 0;
+        }
+        int m;
+        int o = wg_scan_excl(cnt, rs.red_i, &m);
+        unsigned long long *key = a.skey + (size_t)v * a.sort_n;
+        int *idx = a.sidx + (size_t)v * a.sort_n;
+        for (int i = i0; i < i1; i++) {
+            const double p = P[i];
+            if (p > 0.0 && (int)((unsigned long long)__double_as_longlong(p) >> 51) >= blo) {
+                key[o] = (unsigned long long)__double_as_longlong(p);
+                idx[o] = i;
+                o++;
+            }
+        }
+        if (tid == 0) {
+            a.seg_end[v] = v * a.sort_n + m;
+            a.bstar[v] = bstar;
+        }
+        return;   /* k_sample_top_p continues with the sorted candidates */
+    }
+    if (a.min_p > 0.0) {
+        double mp = -INF;
+        __syncthreads();
+        for (int i = tid; i < V; i += SP_T) mp = fmax(mp, P[i]);
+        mp = wg_max(mp, rs.red_d);
+        const double thr = dmul(a.min_p, mp);
+        for (int i = tid; i < V; i += SP_T)
+            if (P[i] < thr) P[i] = 0.0;
+        s = np_sum(P, V, a.tail, lv, rs.bd);
+        for (int i = tid; i < V; i += SP_T) P[i] = ddiv(P[i], s);
+    }
+    if (tid == 0) a.row_rc[v] = 0;
+}
+
+/* the top-p tail of Sampler.probs on row v (after the candidates of tier 0 were sorted),
+ * then min-p; row_rc[v] = 0 when done. Rows that finished in k_sample_probs have an
+ * empty candidate segment and are left alone. */
+__global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
+    __shared__ __align__(16) unsigned char smem[SMEM];
+    __shared__ RowShared rs;
+    __shared__ ChainShared cs;
+    const int v = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int V = a.V;
+    double *P = a.P + (size_t)v * V;
+    double *lv = (double *)smem;
+    if (a.seg_end[v] == v * a.sort_n) return;   /* uniform */
+    double s;
+    if (a.top_p < 1.0) {
+        const double top_p = a.top_p, thr_hi = dmul(top_p, 1.0 + 0x1p-48);
+        const int bstar = a.bstar[v];
+        /* tier 0: bins >= b* (all nonzero entries when b* < 0), sorted by the radix sort;
+         * tier 1: the rest, sorted here */
         double c = 0.0;
         bool done = false;
         for (int tier = 0; tier < 2 && !done; tier++) {
             const int blo = tier == 0 ? (bstar < 0 ? 0 : bstar) : 0;
             const int bhi = tier == 0 ? HBINS : bstar;
             if (blo >= bhi) break;
+            int m;
+            unsigned long long *key;
+            int *idx;
+            if (tier == 0) {
+                m = a.seg_end[v] - v * a.sort_n;
+                key = a.skey2 + (size_t)v * a.sort_n;
+                idx = a.sidx2 + (size_t)v * a.sort_n;
+            } else {
             /* count, then gather the tier's entries */
             int cnt = 0;
             for (int i = tid; i < V; i += SP_T) {
@@ -418,15 +590,14 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
                 const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
                 cnt += (p > 0.0 && b >= blo && b < bhi) ? 1 : 0;
             }
-            int m;
             const int off0 = wg_scan_excl(cnt, rs.red_i, &m);
             (void)off0;
             if (m == 0) continue;
             int N = 1;
             while (N < m) N <<= 1;
             const bool in_lds = N <= SORT_LDS;
-            unsigned long long *key = in_lds ? (unsigned long long *)smem : a.skey + (size_t)v * a.sort_n;
-            int *idx = in_lds ? (int *)(smem + SORT_LDS * 8) : a.sidx + (size_t)v * a.sort_n;
+            key = in_lds ? (unsigned long long *)smem : a.skey + (size_t)v * a.sort_n;
+            idx = in_lds ? (int *)(smem + SORT_LDS * 8) : a.sidx + (size_t)v * a.sort_n;
             if (tid == 0) rs.bi[3] = 0;
             __syncthreads();
             for (int i0 = 0; i0 < V; i0 += SP_T) {
@@ -448,27 +619,30 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
             __syncthreads();
             if (in_lds) bitonic_block(key, idx, N, 2, N, N, 0);
             else bitonic_global(key, idx, N, (unsigned long long *)smem, (int *)(smem + SORT_LDS * 8));
-            /* the sequential cumulative sum, one wave; decisions per entry */
-            if (wv == 0) {
-                int stop = m;
-                for (int base = 0; base < m; base += 64) {
-                    const int j = base + lane;
-                    const double ps = j < m ? __longlong_as_double((long long)key[j]) : 0.0;
-                    const int cnt2 = m - base < 64 ? m - base : 64;
-                    double cj = 0.0;
-                    for (int t = 0; t < cnt2; t++) {
-                        c = dadd(c, lane_value(ps, t));
-                        if (lane == t) cj = c;
-                    }
-                    if (j < m && dsub(cj, ps) >= top_p) P[idx[j]] = 0.0;
-                    if (c >= thr_hi) { stop = base + cnt2; break; }
-                }
-                if (lane == 0) { rs.bi[4] = stop; rs.bd[1] = c; }
             }
+            if (m == 0) continue;
+            /* the running sum over the entries in descending order, continuing from c;
+             * entry j is dropped when fl(c_j - p_j) >= top_p; once c_j >= top_p (1 +
+             * 2^-48), every later entry is dropped too (see above) */
+            int stop;
+            {
+                const double c_in = c;
+                auto px = [&](int j) { return __longlong_as_double((long long)key[j]); };
+                auto drop = [&](int j, double cj) {
+                    if (dsub(cj, px(j)) >= top_p) P[idx[j]] = 0.0;
+                };
+                if (c_in == 0.0) {
+                    c = chain_exact(px, m, thr_hi, &stop, drop, cs);
+                } else {
+                    /* the chain continues from tier 0's end: prepend c as entry -1 */
+                    auto px1 = [&](int j) { return j == 0 ? c_in : px(j - 1); };
+                    auto drop1 = [&](int j, double cj) { if (j > 0) drop(j - 1, cj); };
+                    c = chain_exact(px1, m + 1, thr_hi, &stop, drop1, cs);
+                    stop = stop - 1;
+                }
+            }
+            for (int j = stop + 1 + tid; j < m; j += SP_T) P[idx[j]] = 0.0;
             __syncthreads();
-            const int stop = rs.bi[4];
-            c = rs.bd[1];
-            for (int j = stop + tid; j < m; j += SP_T) P[idx[j]] = 0.0;
             if (stop < m || c >= thr_hi) {
                 done = true;
                 /* every entry below the tier is dropped */
@@ -502,8 +676,8 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
 
 /* inverse-CDF draw from w[0..V) (unnormalised, nonnegative, not all zero) with
  * uniform u: np.cumsum order, first index whose running sum exceeds u * total */
-__device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *red, int *sh, double *shd) {
-    const int tid = threadIdx.x, lane = tid & 63;
+__device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *red, int *sh, ChainShared &cs) {
+    const int tid = threadIdx.x;
     const int per = (V + SP_T - 1) / SP_T;
     const int lo = tid * per < V ? tid * per : V, hi = lo + per < V ? lo + per : V;
     int cnt = 0;
@@ -513,24 +687,12 @@ __device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *
     for (int i = lo; i < hi; i++)
         if (w[i] > 0.0) { a.cw[o] = w[i]; a.ci[o] = i; o++; }
     __syncthreads();
-    if ((tid >> 6) == 0) {
-        double c = 0.0;
-        for (int base = 0; base < nnz; base += 64) {
-            const int j = base + lane;
-            const double ps = j < nnz ? a.cw[j] : 0.0;
-            const int cnt2 = nnz - base < 64 ? nnz - base : 64;
-            double cj = 0.0;
-            for (int t = 0; t < cnt2; t++) {
-                c = dadd(c, lane_value(ps, t));
-                if (lane == t) cj = c;
-            }
-            if (j < nnz) a.cc[j] = cj;
-        }
-        if (lane == 0) shd[0] = c;
-    }
+    int stop;
+    const double total = chain_exact([&](int j) { return a.cw[j]; }, nnz, INF, &stop,
+                                     [&](int j, double cj) { a.cc[j] = cj; }, cs);
     if (tid == 0) sh[0] = INT_MAX;
     __syncthreads();
-    const double target = dmul(u, shd[0]);
+    const double target = dmul(u, total);
     for (int j = tid; j < nnz; j += SP_T)
         if (a.cc[j] > target) { atomicMin(&sh[0], j); break; }
     __syncthreads();
@@ -546,6 +708,7 @@ __global__ __launch_bounds__(SP_T) void k_sample_walk(SampleArgs a) {
     __shared__ int red[SP_WAVES];
     __shared__ int sh[4];
     __shared__ double shd[4];
+    __shared__ ChainShared cs;
     const int n = a.n, V = a.V, tid = threadIdx.x;
     for (int i = tid; i < n; i += SP_T) head[i] = -1;
     __syncthreads();
@@ -585,7 +748,7 @@ __global__ __launch_bounds__(SP_T) void k_sample_walk(SampleArgs a) {
             cur ^= 1;
         }
         if (next < 0) {
-            fin = draw(s < 0.0 ? p : r, V, a.u[2 * v + 1], a, red, sh, shd);
+            fin = draw(s < 0.0 ? p : r, V, a.u[2 * v + 1], a, red, sh, cs);
             break;
         }
         if (tid == 0) a.path[np] = next;
@@ -655,12 +818,15 @@ template <class T> hipError_t grow(T *&p, size_t count) {
 } // namespace
 
 void SampleScratch::release() {
-    void *ps[] = {P, q, u, wa, wb, cw, cc, skey, sidx, ci, row_rc, path, result, ctx, tok, par};
+    void *ps[] = {P, q, u, wa, wb, cw, cc, skey, skey2, sidx, sidx2, seg_begin, seg_end, bstar, ci, row_rc, path,
+                  result, ctx, tok, par, sort_tmp};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     P = q = u = wa = wb = cw = cc = nullptr;
-    skey = nullptr;
-    sidx = ci = row_rc = path = result = ctx = tok = par = nullptr;
+    skey = skey2 = nullptr;
+    sidx = sidx2 = seg_begin = seg_end = bstar = ci = row_rc = path = result = ctx = tok = par = nullptr;
+    sort_tmp = nullptr;
+    sort_tmp_bytes = 0;
     n_cap = V = ctx_cap = sort_n = 0;
     has_q = false;
 }
@@ -678,10 +844,21 @@ hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
     if (n > n_cap) {
         const size_t rows = (size_t)n;
         if ((e = grow(P, rows * V)) || (e = grow(skey, rows * sort_n)) || (e = grow(sidx, rows * sort_n)) ||
-            (e = grow(u, 2 * rows)) || (e = grow(row_rc, rows)) || (e = grow(path, rows)) || (e = grow(tok, rows)) ||
-            (e = grow(par, rows)))
+            (e = grow(skey2, rows * sort_n)) || (e = grow(sidx2, rows * sort_n)) || (e = grow(seg_begin, rows)) ||
+            (e = grow(seg_end, rows)) || (e = grow(bstar, rows)) || (e = grow(u, 2 * rows)) ||
+            (e = grow(row_rc, rows)) || (e = grow(path, rows)) || (e = grow(tok, rows)) || (e = grow(par, rows)))
             return e;
         if (has_q && (e = grow(q, rows * V))) return e;
+        /* the radix sort's workspace for rows segments over rows * sort_n keys */
+        size_t bytes = 0;
+        if ((e = rocprim::segmented_radix_sort_pairs_desc(nullptr, bytes, skey, skey2, sidx, sidx2,
+                                                           (unsigned int)(rows * sort_n), (unsigned int)rows,
+                                                           seg_begin, seg_end)) != hipSuccess)
+            return e;
+        if (sort_tmp) (void)hipFree(sort_tmp);
+        sort_tmp = nullptr;
+        if ((e = hipMalloc(&sort_tmp, bytes ? bytes : 1)) != hipSuccess) return e;
+        sort_tmp_bytes = bytes;
         n_cap = n;
     }
     if (need_q && !has_q) {
@@ -697,38 +874,57 @@ hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
 
 namespace {
 
-SampleArgs make_args(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
                      const SamplerSpec &s, const double *q, const double *u, hipStream_t st) {
-    SampleArgs a{};
+    a = SampleArgs{};
     a.rows = rows; a.n = n; a.V = V; a.tokens = tok; a.parent = par;
     a.temperature = s.temperature; a.top_p = s.top_p; a.min_p = s.min_p; a.rp = s.rp; a.top_k = s.top_k;
     a.n_ctx = s.rp != 1.0 ? s.n_ctx : 0;
     a.ctx = m.ctx;
     a.q = q ? m.q : nullptr;
     a.u = m.u;
-    a.P = m.P; a.skey = m.skey; a.sidx = m.sidx; a.sort_n = m.sort_n;
+    a.P = m.P; a.skey = m.skey; a.sidx = m.sidx; a.skey2 = m.skey2; a.sidx2 = m.sidx2; a.sort_n = m.sort_n;
+    a.seg_begin = m.seg_begin; a.seg_end = m.seg_end; a.bstar = m.bstar;
     a.wa = m.wa; a.wb = m.wb; a.cw = m.cw; a.cc = m.cc; a.ci = m.ci;
     a.row_rc = m.row_rc; a.path = m.path; a.result = m.result;
     build_tail(V, a.tail);
-    if (q) (void)hipMemcpyAsync(m.q, q, sizeof(double) * (size_t)n * V, hipMemcpyHostToDevice, st);
-    if (u) (void)hipMemcpyAsync(m.u, u, sizeof(double) * 2 * (size_t)n, hipMemcpyHostToDevice, st);
-    if (a.n_ctx) (void)hipMemcpyAsync(m.ctx, s.ctx, sizeof(int) * (size_t)a.n_ctx, hipMemcpyHostToDevice, st);
-    return a;
+    hipError_t e = hipSuccess;
+    if (q && (e = hipMemcpyAsync(m.q, q, sizeof(double) * (size_t)n * V, hipMemcpyHostToDevice, st)) != hipSuccess) return e;
+    if (u && (e = hipMemcpyAsync(m.u, u, sizeof(double) * 2 * (size_t)n, hipMemcpyHostToDevice, st)) != hipSuccess) return e;
+    if (a.n_ctx && (e = hipMemcpyAsync(m.ctx, s.ctx, sizeof(int) * (size_t)a.n_ctx, hipMemcpyHostToDevice, st)) != hipSuccess)
+        return e;
+    return hipSuccess;
+}
+
+/* Sampler.probs of n rows: the distribution and top-p candidates, their sort, the
+ * top-p tail */
+hipError_t probs(SampleScratch &m, const SampleArgs &a, int n, hipStream_t st) {
+    k_sample_probs<<<n, SP_T, 0, st>>>(a);
+    size_t bytes = m.sort_tmp_bytes;
+    const hipError_t e = rocprim::segmented_radix_sort_pairs_desc(
+        m.sort_tmp, bytes, a.skey, a.skey2, a.sidx, a.sidx2, (unsigned int)((size_t)n * a.sort_n), (unsigned int)n,
+        a.seg_begin, a.seg_end, 0, 64, st);
+    if (e != hipSuccess) return e;
+    k_sample_top_p<<<n, SP_T, 0, st>>>(a);
+    return hipGetLastError();
 }
 
 } // namespace
 
-void accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
-                   const SamplerSpec &s, const double *q, const double *u, hipStream_t st) {
-    const SampleArgs a = make_args(m, rows, n, V, tok, par, s, q, u, st);
-    k_sample_probs<<<n, SP_T, 0, st>>>(a);
+hipError_t accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st) {
+    SampleArgs a;
+    hipError_t e = make_args(a, m, rows, n, V, tok, par, s, q, u, st);
+    if (e != hipSuccess || (e = probs(m, a, n, st)) != hipSuccess) return e;
     k_sample_walk<<<1, SP_T, 0, st>>>(a);
+    return hipGetLastError();
 }
 
-void sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
-                  const SamplerSpec &s, hipStream_t st) {
-    const SampleArgs a = make_args(m, rows, n, V, tok, par, s, nullptr, nullptr, st);
-    k_sample_probs<<<n, SP_T, 0, st>>>(a);
+hipError_t sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                        const SamplerSpec &s, hipStream_t st) {
+    SampleArgs a;
+    const hipError_t e = make_args(a, m, rows, n, V, tok, par, s, nullptr, nullptr, st);
+    return e != hipSuccess ? e : probs(m, a, n, st);
 }
 
 } // namespace hxl
