@@ -366,6 +366,13 @@ constexpr int TV_ROWS = 128;            /* rows per tile */
 constexpr int TV_BQ = 260;              /* floats per 4-row block: [64 columns][4 rows] + 4 */
 constexpr int TV_PS = 4;                /* p ring slots */
 constexpr int TV_THREADS = 768;         /* 4 summing + 8 loader waves */
+constexpr int TV_SUM = 4, TV_LOAD = 8;  /* summing waves (one head each), loader waves */
+/* the staging map below: loader wave lw owns tile rows 16 lw .. 16 lw + 15 (lane % 16)
+ * and p half lw % 2 of head lw / 2; lane / 16 picks 4 of each 16 columns */
+static_assert(TV_THREADS == 64 * (TV_SUM + TV_LOAD), "k_attn_values: 4 summing + 8 loader waves");
+static_assert(TV_ROWS == 16 * TV_LOAD, "k_attn_values: each loader wave stages 16 rows of a tile");
+static_assert(TV_LOAD == 2 * TV_SUM && TV_ROWS == 2 * 64, "k_attn_values: two 64-row p halves per summed head");
+static_assert(TV_BQ == 4 * 64 + 4, "k_attn_values: a 4-row block holds 64 columns");
 
 typedef unsigned int tv_u4 __attribute__((ext_vector_type(4)));
 
@@ -397,7 +404,7 @@ __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float pt[TV_PS][4][TV_ROWS];
     __shared__ int anc_s[MAX_ANC];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
-    const int nd = (hd + 63) / 64, qpt = (grp + 3) / 4;
+    const int nd = (hd + 63) / 64, qpt = (grp + TV_SUM - 1) / TV_SUM;
     int b = blockIdx.x;
     const int dc = b % nd;
     b /= nd;
@@ -413,10 +420,10 @@ __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
         for (int jj = tid; jj <= dep; jj += TV_THREADS) anc_s[jj] = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + jj];
         __syncthreads();
     }
-    if (wave >= 4) {
+    if (wave >= TV_SUM) {
         /* loader wave lw: rows 16 lw + lane % 16 of each tile, columns 16 cb + 4 (lane / 16)
          * .. + 3 for cb = 0..3, and half lw % 2 of head lw / 2's p row */
-        const int lw = wave - 4, r = lane & 15, cg = lane >> 4, half = lw & 1;
+        const int lw = wave - TV_SUM, r = lane & 15, cg = lane >> 4, half = lw & 1;
         const __amdgpu_buffer_rsrc_t vrs =
             __builtin_amdgcn_make_buffer_rsrc((void *)(a.vc + (size_t)g * a.cap * hd), 0, a.cap * hd * 4, 0x00020000);
         int coff[4];
@@ -425,7 +432,7 @@ __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
             const int col = dc * 64 + 16 * cb + 4 * cg;
             coff[cb] = (col < hd ? col : 0) * 4;
         }
-        const int phh = hq * 4 + (lw >> 1);
+        const int phh = hq * TV_SUM + (lw >> 1);
         const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
             (void *)(a.S + ((size_t)t * a.H + (size_t)g * grp + (phh < grp ? phh : 0)) * a.ldS), 0, a.ldS * 4, 0x00020000);
         const int hd4 = hd * 4, roff = r * hd4;
@@ -497,7 +504,7 @@ __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
         else run(std::false_type{});
         HX_WAIT_VMCNT(0);              /* no LDS write may land after the workgroup ends */
     } else {
-        const int hh = hq * 4 + wave;
+        const int hh = hq * TV_SUM + wave;
         const bool live = hh < grp;
         const int h = g * grp + (live ? hh : 0);
         float acc = 0.0f;
@@ -566,7 +573,7 @@ void attention_scores(const AttnArgs &a, hipStream_t st) {
 void attention_finish(const AttnArgs &a, hipStream_t st) {
     const int grp = a.H / a.Hkv;
     k_attn_softmax<<<a.T * a.H, SM_T, 0, st>>>(a);
-    const int nd = (a.hd + 63) / 64, qpt = (grp + 3) / 4;
+    const int nd = (a.hd + 63) / 64, qpt = (grp + TV_SUM - 1) / TV_SUM;
     k_attn_values<<<a.T * qpt * a.Hkv * nd, TV_THREADS, 0, st>>>(a);
 }
 
