@@ -137,13 +137,16 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
  * the canonical pairing). 8 accumulators per thread instead of 128 let eight waves per
  * SIMD hide the load latency. A row's K elements j + 16 i are loaded straight from the
  * cache (16 lanes read 64 contiguous bytes); q of the 8 heads is staged transposed in
- * LDS (qT[h][j][i] = q[h][16 i + j]), read four i at a time. */
-constexpr int S16_NP = 2;              /* 16-row passes per workgroup */
-constexpr int S16_RB = 16 * S16_NP;    /* rows per workgroup */
+ * LDS (qT[h][j][i] = q[h][16 i + j]), read four i at a time. Each lane's row of qT is
+ * padded by 16 bytes, so the 16 lanes of a read hit 16 different bank groups (unpadded,
+ * a head_dim of 512 put all 16 on the same banks). NP 16-row passes per workgroup keep
+ * NP * HI = 32 K values in registers per thread. */
+template <int HI> constexpr int s16_np() { return HI <= 8 ? 4 : HI <= 16 ? 2 : 1; }
 
 template <int HI>
 __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
-    __shared__ float4 qT[8][16][HI / 4];
+    constexpr int S16_NP = s16_np<HI>(), S16_RB = 16 * S16_NP, QS = HI / 4 + 1;
+    __shared__ float4 qT[8][16][QS];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
     int b = blockIdx.x;
     const int g = b % Hkv;
@@ -170,7 +173,7 @@ __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
             float *qf = (float *)qT;
             for (int x = tid; x < 8 * hd; x += 256) {
                 const int hh = x / hd, e = x % hd;
-                qf[(hh * 16 + (e & 15)) * HI + (e >> 4)] = h0 + hh < grp ? qb[(size_t)hh * hd + e] : 0.0f;
+                qf[(hh * 16 + (e & 15)) * (4 * QS) + (e >> 4)] = h0 + hh < grp ? qb[(size_t)hh * hd + e] : 0.0f;
             }
         }
         __syncthreads();
@@ -550,17 +553,23 @@ namespace hxl {
 void attention_scores(const AttnArgs &a, hipStream_t st) {
     const int max_nr = a.g.nr_max;
     if (a.hd % 64 == 0 && a.hd <= 512) {
-        const int grid = ((max_nr + S16_RB - 1) / S16_RB) * a.T * a.Hkv;
-        switch (a.hd / 16) {
-        case 4: k_attn_scores16<4><<<grid, 256, 0, st>>>(a); return;
-        case 8: k_attn_scores16<8><<<grid, 256, 0, st>>>(a); return;
-        case 12: k_attn_scores16<12><<<grid, 256, 0, st>>>(a); return;
-        case 16: k_attn_scores16<16><<<grid, 256, 0, st>>>(a); return;
-        case 20: k_attn_scores16<20><<<grid, 256, 0, st>>>(a); return;
-        case 24: k_attn_scores16<24><<<grid, 256, 0, st>>>(a); return;
-        case 28: k_attn_scores16<28><<<grid, 256, 0, st>>>(a); return;
-        default: k_attn_scores16<32><<<grid, 256, 0, st>>>(a); return;
+#define HX_S16(HI_)                                                                         \
+        {                                                                                   \
+            constexpr int rb = 16 * s16_np<HI_>();                                          \
+            k_attn_scores16<HI_><<<((max_nr + rb - 1) / rb) * a.T * a.Hkv, 256, 0, st>>>(a); \
+            return;                                                                         \
         }
+        switch (a.hd / 16) {
+        case 4: HX_S16(4)
+        case 8: HX_S16(8)
+        case 12: HX_S16(12)
+        case 16: HX_S16(16)
+        case 20: HX_S16(20)
+        case 24: HX_S16(24)
+        case 28: HX_S16(28)
+        default: HX_S16(32)
+        }
+#undef HX_S16
     }
     const int nchunks = (max_nr + SC_ROWS - 1) / SC_ROWS;
     const int grp = a.H / a.Hkv, nsc = nchunks * a.T * a.Hkv;
