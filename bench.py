@@ -310,9 +310,9 @@ def bench_chain(a) -> dict:
     gu_gbs = kx["expert_bytes"] / kx["expert_s"] / 1e9 if kx["expert_s"] > 0 else 0.0
     dn_gbs = kx["expert_down_bytes"] / kx["expert_down_s"] / 1e9 if kx["expert_down_s"] > 0 else 0.0
     # every weight matrix a step reads once (attention projections, lm_head, the routed
-    # experts' gate/up/down) over the GPU time of the phases that read them
+    # experts' gate/up/down) over the GPU time of the launches that read them
     mat_bytes = ks["dense_bytes"] + ks["expert_bytes"] + ks["expert_down_bytes"]
-    mat_s = ks["attn_s"] + ks["expert_s"] + ks["expert_down_s"] + ks["head_s"] + ks["dense_s"]
+    mat_s = ks["proj_s"] + ks["expert_s"] + ks["expert_down_s"] + ks["head_s"] + ks["dense_s"]
     eng.close()
     cpu = None
     if not a.no_cpu:
@@ -320,7 +320,7 @@ def bench_chain(a) -> dict:
             cpu = cpu_baseline(path, prompt[:-1], noisy, cont, a.k, a.cpu_steps, threads=host_threads())
         except Exception as ex:   # the baseline is reported, never required
             log(f"[bench] cpu baseline failed: {ex}")
-    phases = ("attn_s", "router_s", "expert_s", "expert_down_s", "norm_s", "head_s", "dense_s")
+    phases = ("proj_s", "attn_s", "router_s", "expert_s", "expert_down_s", "norm_s", "head_s", "dense_s")
     gpu_total = sum(ks[x] for x in phases)
     return {
         "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
@@ -344,8 +344,8 @@ def bench_chain(a) -> dict:
                          "frac": round(mat_bytes / mat_s / 1e9 / HBM_PEAK_GBS, 4) if mat_s > 0 else 0.0,
                          "bytes_per_step": int(mat_bytes / a.steps),
                          "what": "all weight matrices of a step (attention q/k/v/o, lm_head, routed experts "
-                                 "gate/up/down) / GPU time of the attention, expert and head phases "
-                                 "(attention's time includes its KV scan)"}},
+                                 "gate/up/down, with SwiGLU and act-quant epilogues) / GPU time of the "
+                                 "launches that read them (HIP events around each launch group)"}},
         "gpu_time_split_ms_per_step": {k: round(ks[k] / a.steps * 1e3, 4) for k in phases}
                                       | {"sum": round(gpu_total / a.steps * 1e3, 4)},
         "cpu_baseline": cpu,

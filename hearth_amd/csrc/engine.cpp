@@ -105,6 +105,8 @@ struct Layer {
     const float *router_bias = nullptr;
     const float *router_bias_host = nullptr;   /* the same in the mapped container (prediction) */
     ExpertW *experts = nullptr;     /* device table [E] */
+    uint64_t proj_bytes = 0;        /* algorithmic bytes of the attention projections (MLA: with W_UV) */
+    uint64_t ffn_bytes = 0;         /* of the dense FFN or the shared expert */
     uint64_t expert_bytes_each = 0; /* algorithmic bytes of one expert (gate+up+down) */
     uint64_t expert_gateup_bytes = 0; /* of which gate + up */
     int dtype_mask = 0;             /* bit dt set when some expert has dtype dt */
@@ -132,6 +134,7 @@ struct hearth_engine {
     int emb_dtype = 0;
     size_t emb_rb = 0;
     DMat lm_head;
+    uint64_t head_bytes = 0;
     const float *out_norm = nullptr;
     std::vector<float> inv_freq;
 
@@ -539,6 +542,14 @@ bool hearth_engine::upload(std::string &msg) {
         ck(hipStreamSynchronize(st));   /* the host table goes out of scope */
     }
     ck(hipStreamSynchronize(st));
+    /* algorithmic weight bytes per forward, for the profiling counters */
+    auto mb = [](const DMat &m) -> uint64_t { return m.rows ? (uint64_t)m.rows * row_bytes(m.dtype, m.cols) : 0; };
+    for (Layer &w : layers) {
+        w.proj_bytes = mb(w.q) + mb(w.k) + mb(w.v) + mb(w.o) + mb(w.q_a) + mb(w.q_b) + mb(w.kv_a);
+        if (mla) w.proj_bytes += (uint64_t)H * vd * row_bytes(w.kvb_dtype, C);
+        w.ffn_bytes = mb(w.gate) + mb(w.up) + mb(w.down) + mb(w.sh_gate) + mb(w.sh_up) + mb(w.sh_down);
+    }
+    head_bytes = mb(lm_head);
     return true;
 }
 
@@ -744,6 +755,7 @@ void hearth_engine::attn_mla(const Layer &w, int l, int T) {
     const DMat &qin = qlr ? w.q_a : w.q;
     float *qdst = qlr ? qa : qb;
     const int qld = qlr ? qlr : q_dim;
+    timed(&ks.proj_s, [&] {
     if (qin.quant && w.kv_a.quant) {
         hxd::GemmArgs g{};
         g.nseg = 2;
@@ -762,6 +774,7 @@ void hearth_engine::attn_mla(const Layer &w, int l, int T) {
         hxl::norm(n, st);
         matmul(w.q_b, aqa, qa, qlr, T, qb, q_dim, false, 1.0f);
     }
+    });
     float *cc = kv + (size_t)l * kv_layer;
     hxd::MlaArgs ma{};
     ma.T = T; ma.H = H; ma.C = C; ma.rdim = rdim; ma.nope = nope; ma.vd = vd; ma.qh = qh;
@@ -771,9 +784,10 @@ void hearth_engine::attn_mla(const Layer &w, int l, int T) {
     ma.S = S; ma.ldS = ldS; ma.scale = c.attn_scale;
     ma.g.depth = depth; ma.g.anc = anc; ma.g.anc_ld = B; ma.g.pos = d_pos; ma.g.nr_max = nr_max(T); ma.g.chain = geom_chain;
     ma.Yv = yv; ma.att = att; ma.aatt = aatt;
+    hxd::AttnArgs at{};
+    timed(&ks.attn_s, [&] {
     hxl::mla_post(ma, st);
     hxl::mla_qlat(ma, st);
-    hxd::AttnArgs at{};
     at.q = qr; at.kc = cc; at.vc = cc; at.S = S; at.ldS = ldS; at.out = olat; at.T = T; at.H = H; at.Hkv = 1;
     at.hd = C; at.cap = cap; at.scale = 1.0f;
     at.g = ma.g;
@@ -781,13 +795,16 @@ void hearth_engine::attn_mla(const Layer &w, int l, int T) {
     hxl::attention_scores(at, st);
     hxl::mla_pe_scores(ma, st);
     hxl::attention_finish(at, st);
+    });
     dump("att", l, olat, T, H * C);
-    hxd::MoeArgs m{};
-    m.table = w.uv; m.head_slots = 1; m.mid = alat; m.T = T; m.D = vd; m.F = C; m.Y = yv; m.P = H * T;
-    m.dtype_mask = 1 << w.kvb_dtype;
-    hxl::expert_down_q(m, H, st);
-    hxl::mla_gather(ma, st);
-    matmul(w.o, aatt, att, H * vd, T, ao, D, false, 1.0f);
+    timed(&ks.proj_s, [&] {
+        hxd::MoeArgs m{};
+        m.table = w.uv; m.head_slots = 1; m.mid = alat; m.T = T; m.D = vd; m.F = C; m.Y = yv; m.P = H * T;
+        m.dtype_mask = 1 << w.kvb_dtype;
+        hxl::expert_down_q(m, H, st);
+        hxl::mla_gather(ma, st);
+        matmul(w.o, aatt, att, H * vd, T, ao, D, false, 1.0f);
+    });
 }
 
 /* One forward of T tokens whose geometry (tokens, depth, anc, rope) is already on the
@@ -802,11 +819,10 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
     });
     for (int l = 0; l < L; l++) {
         const Layer &w = layers[l];
-        timed(&ks.attn_s, [&] {
-            if (mla) {
-                attn_mla(w, l, T);
-                return;
-            }
+        if (profiling) ks.dense_bytes += w.proj_bytes + w.ffn_bytes;
+        if (mla) attn_mla(w, l, T);
+        else {
+        timed(&ks.proj_s, [&] {
             if (w.q.quant && w.k.quant && w.v.quant) {
                 hxd::GemmArgs g{};
                 g.nseg = 3;
@@ -822,6 +838,8 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 matmul(w.k, ax, x, D, T, kb, kv_dim, false, 1.0f);
                 matmul(w.v, ax, x, D, T, vb, kv_dim, false, 1.0f);
             }
+        });
+        timed(&ks.attn_s, [&] {
             hxd::QkvArgs qa{};
             qa.q = qb; qa.k = kb; qa.v = vb; qa.bq = w.bq; qa.bk = w.bk; qa.bv = w.bv; qa.qn = w.qn; qa.kn = w.kn;
             qa.qout = qr; qa.kc = kv + (size_t)l * kv_layer; qa.vc = qa.kc + (size_t)Hkv * cap * hd;
@@ -837,8 +855,9 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             hxl::attention(at, st);
             dump("att", l, att, T, q_dim);
             if (w.o.quant && !at.qo_on) hxl::quant_rows(att, q_dim, T, q_dim / 64, aatt, st);
-            matmul(w.o, aatt, att, q_dim, T, ao, D, false, 1.0f);
         });
+        timed(&ks.proj_s, [&] { matmul(w.o, aatt, att, q_dim, T, ao, D, false, 1.0f); });
+        }
         timed(&ks.norm_s, [&] {
             hxd::NormArgs n{};
             n.mode = 1; n.h = h; n.add = ao; n.rs = rs; n.norm_w = w.ffn_norm; n.eps = c.eps; n.x = x; n.a = ax;
@@ -931,8 +950,10 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             });
         }
     }
-    if (want_logits)
+    if (want_logits) {
         timed(&ks.head_s, [&] { matmul(lm_head, ax, x, D, T, logits, V, true, c.logit_scale); });
+        if (profiling) ks.dense_bytes += head_bytes;
+    }
     if (store) store->tick();
 }
 
@@ -1294,7 +1315,7 @@ HEARTH_API int hearth_info(hearth_engine *e, hearth_model_info *out) {
     out->bos_id = e->c.bos_id;
     out->n_eos = (int)std::min<size_t>(8, e->c.eos_ids.size());
     for (int i = 0; i < out->n_eos; i++) out->eos_ids[i] = e->c.eos_ids[i];
-    out->dense_bytes = e->mf.dense_bytes;
+
     out->expert_bytes = e->mf.expert_region_bytes;
     out->slab_bytes_max = e->mf.slab_bytes_max;
     out->params_total = e->mf.params_total;
@@ -1344,8 +1365,8 @@ HEARTH_API int hearth_get_stats(hearth_engine *e, hearth_stats *out) {
     out->tokens = e->tokens_done;
     out->forward_calls = e->forward_calls;
     out->wall_s = e->wall_s;
-    out->attn_s = e->ks.attn_s;
-    out->moe_s = e->ks.router_s + e->ks.expert_s;
+    out->attn_s = e->ks.attn_s + e->ks.proj_s;
+    out->moe_s = e->ks.router_s + e->ks.expert_s + e->ks.expert_down_s;
     out->dense_s = e->ks.dense_s + e->ks.head_s + e->ks.norm_s;
     out->expert_uses = d[0] - e->stats_base[0];
     out->expert_loads_unique = d[1] - e->stats_base[1];

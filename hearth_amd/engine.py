@@ -103,7 +103,7 @@ class KStats(Structure):
         ("head_s", c_double), ("dense_s", c_double),
         ("expert_launches", c_uint64), ("expert_bytes", c_uint64), ("dense_bytes", c_uint64), ("kv_bytes", c_uint64),
         ("expert_down_s", c_double), ("expert_down_bytes", c_uint64),
-        ("accept_s", c_double),
+        ("accept_s", c_double), ("proj_s", c_double),
     ]
 
 

@@ -114,7 +114,8 @@ HEARTH_API int hearth_gpu_probs(const float *rows, int n, int V, const int32_t *
 /* GPU time per kernel class, accumulated while profiling is on (HIP event pairs on the
  * engine's stream; see hearth_gpu_set_profiling for the levels). */
 typedef struct hearth_gpu_kstats {
-    double attn_s;        /* QKV projection, post-processing, attention, output projection */
+    double attn_s;        /* q/k post-processing and RoPE, scores, softmax, value sum (MLA: latent post
+                           * step, absorbed queries, RoPE scores) */
     double router_s;      /* router logits + routing + bucketing */
     double expert_s;      /* grouped expert gate/up (one launch per MoE layer and expert dtype) */
     double norm_s;        /* residual, RMSNorm, activation quantization */
@@ -122,11 +123,13 @@ typedef struct hearth_gpu_kstats {
     double dense_s;       /* dense FFN layers and shared experts */
     uint64_t expert_launches;   /* MoE layers run (gate/up launch groups) */
     uint64_t expert_bytes;      /* algorithmic weight bytes of the active experts' gate and up matrices */
-    uint64_t dense_bytes;       /* algorithmic weight bytes of attention + lm_head matrices */
+    uint64_t dense_bytes;       /* algorithmic weight bytes of the attention projections, dense FFN and
+                                 * shared-expert matrices and the lm_head read by the profiled forwards */
     uint64_t kv_bytes;          /* KV bytes read by attention (each row once per call and head group) */
     double expert_down_s;       /* SwiGLU activation quantization + grouped expert down projection */
     uint64_t expert_down_bytes; /* algorithmic weight bytes of the active experts' down matrices */
     double accept_s;            /* device acceptance (greedy argmax + walk, or sampled) */
+    double proj_s;              /* attention projections: q, k, v, o (MLA: q_a, q_b, kv_a, W_UV per head, o) */
 } hearth_gpu_kstats;
 
 /* level 0: off; 1: HIP events around the grouped expert launches only (expert_s,
