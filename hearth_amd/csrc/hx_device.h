@@ -245,6 +245,23 @@ __device__ inline unsigned long long wave_max_u64(unsigned long long k) {
 
 /* maximum of a non-negative float (NaN-free) and sum of an int over the wave, in every
  * lane, by the same DPP steps (both exact whatever the order) */
+/* maximum of an unsigned value over the wave, in every lane (the same DPP steps) */
+__device__ inline unsigned wave_max_u32(unsigned v) {
+#define HX_UMAX_STEP(CTRL, RM)                                                                 \
+    {                                                                                          \
+        const unsigned o = dpp_u32<CTRL, RM>(v, v);                                            \
+        v = o > v ? o : v;                                                                     \
+    }
+    HX_UMAX_STEP(0x111, 0xF)
+    HX_UMAX_STEP(0x112, 0xF)
+    HX_UMAX_STEP(0x114, 0xF)
+    HX_UMAX_STEP(0x118, 0xF)
+    HX_UMAX_STEP(0x142, 0xA)
+    HX_UMAX_STEP(0x143, 0xC)
+#undef HX_UMAX_STEP
+    return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 __device__ inline float wave_max_f32(float x) {
     unsigned v = __float_as_uint(x);
 #define HX_FMAX_STEP(CTRL, RM) v = __float_as_uint(fmaxf(__uint_as_float(v), __uint_as_float(dpp_u32<CTRL, RM>(v, v))));

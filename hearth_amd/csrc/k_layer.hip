@@ -21,9 +21,230 @@ namespace {
  * model.c:904-923; 3: h unchanged; 4: v = h (+ rs * gated add) into the norm only,
  * h unchanged -- the next-layer prediction input, model.c:1052-1058), then rmsnorm
  * (quant.c:626-632: ms = sum16(v^2)/D, r = 1/sqrt(ms + eps), x = (v * r) * w) and
- * NUMERICS §2 of x. One workgroup per token; every load of the residual step is issued
- * before any of its sums. */
+ * NUMERICS §2 of x. */
+__device__ __forceinline__ float norm_input(const NormArgs &a, const float *h, const float *wk, const int *pk, int t,
+                                            int i) {
+    const int D = a.D, K = a.K;
+    if (a.mode == 0) {
+        const uint8_t *row = a.emb + (size_t)a.tokens[t] * a.emb_rb;
+        return fmul(a.es, deq_elem(row, a.emb_dtype, i));
+    }
+    if (a.mode == 1) return fadd(h[i], fmul(a.rs, a.add[(size_t)t * D + i]));
+    if (a.mode == 3) return h[i];
+    if (a.mode == 4) {
+        float v = h[i];
+        if (a.add) {
+            float sv = a.add[(size_t)t * D + i];
+            if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_glibc_f(-a.add_gate[t]))));
+            v = fadd(v, fmul(a.rs, sv));
+        }
+        return v;
+    }
+    float out = 0.0f;
+    for (int j0 = 0; j0 < K; j0 += 8) {
+        float yv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u < K ? j0 + u : K - 1;
+            yv[u] = a.Y[(size_t)pk[j] * D + i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (j0 + u < K) out = fadd(out, fmul(wk[j0 + u], yv[u]));
+    }
+    if (a.add) {
+        float sv = a.add[(size_t)t * D + i];
+        if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_glibc_f(-a.add_gate[t]))));
+        out = fadd(out, sv);
+    }
+    return fadd(h[i], fmul(a.rs, out));
+}
+
+/* One workgroup per token; thread tid holds elements tid + nth u (u < EPT) in registers
+ * from the residual step to the quantization, which is also the block layout of the
+ * quantization (element g * 64 + lane is lane `lane` of wave g mod nw), so only the
+ * squares go through LDS. They are stored transposed (square of element 16 k + j at
+ * sq[j][k], rows padded by norm_sq_stride), so each of the 16 lanes of the sum16 reads
+ * its own elements four at a time; entries past D hold +0 (adding +0 to a sum of
+ * squares leaves it unchanged). Every load of the residual step (norm weights included)
+ * is issued before the first of them is used: the mode is a template argument, indices
+ * past the row are clamped to its last element (their values are replaced by 0), and
+ * the trip count nu is uniform. */
+constexpr int NM_PER = 8;   /* most elements per thread (rows up to 8192 wide) */
+
+/* elements per lane of the sum16, rounded up to whole batches of 32 (8 reads of 16 bytes) */
+__host__ __device__ __forceinline__ int norm_kp(int D) { return ((D + 15) / 16 + 31) & ~31; }
+
+/* words per transposed row: norm_kp plus 4, so that the row length in 16-byte units is
+ * odd (the 16 rows start in 16 different bank groups) */
+__host__ __device__ __forceinline__ int norm_sq_stride(int D) { return norm_kp(D) + 4; }
+
+/* the elements one row of the norm covers: the 16 lanes' padded squares and the
+ * quantized blocks (padded blocks quantize zeros) */
+__host__ __device__ __forceinline__ int norm_cover(int D, int nbp) {
+    const int n = 16 * norm_kp(D);
+    return n > nbp * 64 ? n : nbp * 64;
+}
+
+template <int MODE, int EPT>
 __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
+    extern __shared__ float sq[];
+    __shared__ float r_sh;
+    const int t = blockIdx.x, D = a.D, tid = threadIdx.x, nth = blockDim.x, K = a.K;
+    const int kp = norm_kp(D), sqs = norm_sq_stride(D), nsq = 16 * kp;
+    const int nu = (norm_cover(D, a.a.nbp) + nth - 1) / nth;   /* <= EPT, uniform */
+    float *h = a.h + (size_t)t * D;
+    const float *ad = a.add ? a.add + (size_t)t * D : nullptr;
+    float wv[EPT], vv[EPT], hv[EPT], av[EPT];
+#pragma unroll
+    for (int u = 0; u < EPT; u++) {
+        if (u < nu) {
+            const int i = tid + nth * u, ic = i < D ? i : D - 1;
+            wv[u] = a.norm_w[ic];
+            if (MODE != 0) hv[u] = h[ic];
+            if (MODE == 1 || ((MODE == 2 || MODE == 4) && ad)) av[u] = ad[ic];
+        }
+    }
+    float gs = 1.0f;   /* sigmoid of the shared expert's gate logit (modes 2, 4) */
+    if ((MODE == 2 || MODE == 4) && a.add_gate) gs = fdiv(1.0f, fadd(1.0f, exp_glibc_f(-a.add_gate[t])));
+    if (MODE == 0) {
+        const uint8_t *row = a.emb + (size_t)a.tokens[t] * a.emb_rb;
+#pragma unroll
+        for (int u = 0; u < EPT; u++) {
+            const int i = tid + nth * u, ic = i < D ? i : D - 1;
+            if (u < nu) vv[u] = fmul(a.es, deq_elem(row, a.emb_dtype, ic));
+        }
+    } else if (MODE == 1) {
+#pragma unroll
+        for (int u = 0; u < EPT; u++)
+            if (u < nu) vv[u] = fadd(hv[u], fmul(a.rs, av[u]));
+    } else if (MODE == 3) {
+#pragma unroll
+        for (int u = 0; u < EPT; u++)
+            if (u < nu) vv[u] = hv[u];
+    } else if (MODE == 4) {
+#pragma unroll
+        for (int u = 0; u < EPT; u++) {
+            if (u < nu) {
+                vv[u] = hv[u];
+                if (ad) {
+                    const float sv = a.add_gate ? fmul(av[u], gs) : av[u];
+                    vv[u] = fadd(vv[u], fmul(a.rs, sv));
+                }
+            }
+        }
+    } else {
+        /* model.c:904-923: out = sum_j w_j * Y[pair_j] in rank order (+ gated shared add);
+         * the token's pairs and weights are the same for every thread (scalar loads) */
+        constexpr int JC = EPT <= 2 ? 8 : 4;   /* pairs loaded at once */
+        const int *pt = a.pair_of + (size_t)t * K;
+        const float *wt = a.wts + (size_t)t * K;
+        float out[EPT];
+#pragma unroll
+        for (int u = 0; u < EPT; u++) out[u] = 0.0f;
+        for (int j0 = 0; j0 < K; j0 += JC) {
+            float yv[EPT][JC], wj[JC];
+            int pj[JC];
+            if (K % JC == 0) {
+                /* one scalar load each of JC pair indices and weights (the rows of pair_of
+                 * and wts start at multiples of JC words: K % JC == 0) */
+                typedef int vji __attribute__((ext_vector_type(JC)));
+                typedef float vjf __attribute__((ext_vector_type(JC)));
+                const vji pv = *(const vji *)__builtin_assume_aligned(pt + j0, 4 * JC);
+                const vjf wvv = *(const vjf *)__builtin_assume_aligned(wt + j0, 4 * JC);
+#pragma unroll
+                for (int jj = 0; jj < JC; jj++) {
+                    pj[jj] = pv[jj];
+                    wj[jj] = wvv[jj];
+                }
+            } else {
+#pragma unroll
+                for (int jj = 0; jj < JC; jj++) {
+                    const int j = j0 + jj < K ? j0 + jj : K - 1;
+                    pj[jj] = pt[j];
+                    wj[jj] = wt[j];
+                }
+            }
+#pragma unroll
+            for (int jj = 0; jj < JC; jj++) {
+                const float *yr = a.Y + (size_t)pj[jj] * D;
+#pragma unroll
+                for (int u = 0; u < EPT; u++) {
+                    const int i = tid + nth * u;
+                    if (u < nu) yv[u][jj] = yr[i < D ? i : D - 1];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < EPT; u++)
+#pragma unroll
+                for (int jj = 0; jj < JC; jj++)
+                    if (u < nu && j0 + jj < K) out[u] = fadd(out[u], fmul(wj[jj], yv[u][jj]));
+        }
+#pragma unroll
+        for (int u = 0; u < EPT; u++) {
+            if (u < nu) {
+                float o = out[u];
+                if (ad) o = fadd(o, a.add_gate ? fmul(av[u], gs) : av[u]);
+                vv[u] = fadd(hv[u], fmul(a.rs, o));
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < EPT; u++) {
+        if (u < nu) {
+            const int i = tid + nth * u;
+            if (i >= D) vv[u] = 0.0f;
+            if (i < D && MODE != 3 && MODE != 4) h[i] = vv[u];
+            if (i < nsq) sq[(i & 15) * sqs + (i >> 4)] = fmul(vv[u], vv[u]);
+        }
+    }
+    __syncthreads();
+    if (tid < 16) {
+        /* lane tid: the sequential sum of the squares of elements tid, tid + 16, ...,
+         * eight 16-byte reads in flight while the previous eight are added */
+        const float4 *row = (const float4 *)&sq[tid * sqs];
+        const int n4 = kp / 4;   /* a multiple of 8 */
+        float L = 0.0f;
+        float4 cur[8], nxt[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) cur[u] = row[u];
+        for (int c0 = 0; c0 < n4; c0 += 8) {
+            const int cn = c0 + 8 < n4 ? c0 + 8 : c0;   /* the last batch reads itself again */
+#pragma unroll
+            for (int u = 0; u < 8; u++) nxt[u] = row[cn + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                L = fadd(L, cur[u].x);
+                L = fadd(L, cur[u].y);
+                L = fadd(L, cur[u].z);
+                L = fadd(L, cur[u].w);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) cur[u] = nxt[u];
+        }
+        L = tree16(L);
+        if (tid == 0) {
+            const float ms = fdiv(L, (float)D);
+            r_sh = fdiv(1.0f, sqrt_rn(fadd(ms, a.eps)));
+        }
+    }
+    __syncthreads();
+    const float r = r_sh;
+    const int wave = tid >> 6, nw = nth >> 6;
+#pragma unroll
+    for (int u = 0; u < EPT; u++) {
+        const int g = wave + nw * u;   /* the block of element tid + nth u (wave-uniform) */
+        if (u < nu && g < a.a.nbp) {
+            const int i = tid + nth * u;
+            const float xv = i < D ? fmul(fmul(vv[u], r), wv[u]) : 0.0f;
+            if (a.x && i < D) a.x[(size_t)t * D + i] = xv;
+            quant_block_wave(xv, a.a, t, g);
+        }
+    }
+}
+
+/* The same for rows wider than NM_PER * 1024: the row goes through LDS. */
+__global__ __launch_bounds__(1024) void k_norm_wide(NormArgs a) {
     extern __shared__ float hs[];
     __shared__ float wk[64];
     __shared__ int pk[64];
@@ -37,69 +258,16 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
         }
         __syncthreads();
     }
-#pragma unroll 2
     for (int i = tid; i < D; i += nth) {
-        float v;
-        if (a.mode == 0) {
-            const uint8_t *row = a.emb + (size_t)a.tokens[t] * a.emb_rb;
-            v = fmul(a.es, deq_elem(row, a.emb_dtype, i));
-        } else if (a.mode == 1) {
-            v = fadd(h[i], fmul(a.rs, a.add[(size_t)t * D + i]));
-        } else if (a.mode == 3) {
-            v = h[i];
-        } else if (a.mode == 4) {
-            v = h[i];
-            if (a.add) {
-                float sv = a.add[(size_t)t * D + i];
-                if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_glibc_f(-a.add_gate[t]))));
-                v = fadd(v, fmul(a.rs, sv));
-            }
-        } else {
-            float out = 0.0f;
-            for (int j0 = 0; j0 < K; j0 += 8) {
-                float yv[8];
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const int j = j0 + u < K ? j0 + u : K - 1;
-                    yv[u] = a.Y[(size_t)pk[j] * D + i];
-                }
-#pragma unroll
-                for (int u = 0; u < 8; u++)
-                    if (j0 + u < K) out = fadd(out, fmul(wk[j0 + u], yv[u]));
-            }
-            if (a.add) {
-                float sv = a.add[(size_t)t * D + i];
-                if (a.add_gate) sv = fmul(sv, fdiv(1.0f, fadd(1.0f, exp_glibc_f(-a.add_gate[t]))));
-                out = fadd(out, sv);
-            }
-            v = fadd(h[i], fmul(a.rs, out));
-        }
-        if (a.mode != 4) h[i] = v;
+        const float v = norm_input(a, h, wk, pk, t, i);
+        if (a.mode != 4 && a.mode != 3) h[i] = v;
         hs[i] = v;
-        hs[D + i] = fmul(v, v);   /* the products of dot16(x, x), formed in parallel */
+        hs[D + i] = fmul(v, v);
     }
     __syncthreads();
     if (tid < 16) {
-        /* lane tid: the sequential sum of the products of elements tid, tid + 16, ... */
         float L = 0.0f;
-        int i = tid;
-        float cur[16], nxt[16];
-        const int full = D >= 256 ? (D - tid) / 256 : 0;
-        if (full > 0) {
-#pragma unroll
-            for (int u = 0; u < 16; u++) cur[u] = hs[D + i + 16 * u];
-            for (int gi = 0; gi < full; gi++) {
-                const int inx = gi + 1 < full ? i + 256 : i;
-#pragma unroll
-                for (int u = 0; u < 16; u++) nxt[u] = hs[D + inx + 16 * u];
-#pragma unroll
-                for (int u = 0; u < 16; u++) L = fadd(L, cur[u]);
-#pragma unroll
-                for (int u = 0; u < 16; u++) cur[u] = nxt[u];
-                i += 256;
-            }
-        }
-        for (; i < D; i += 16) L = fadd(L, hs[D + i]);
+        for (int i = tid; i < D; i += 16) L = fadd(L, hs[D + i]);
         L = tree16(L);
         if (tid == 0) {
             const float ms = fdiv(L, (float)D);
@@ -271,15 +439,15 @@ weights:
 /* Selection key of (value v, expert e): a larger key ranks first, and the order is
  * ranks_before's: larger value first (-0 equals +0), NaN after every number, ties to
  * the lower index. */
+__device__ __forceinline__ uint32_t order_key(float v) {
+    /* a larger value has a larger key (-0 equals +0); NaN has key 0, below every number */
+    if (v != v) return 0u;
+    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 __device__ __forceinline__ unsigned long long rank_key(float v, int e) {
-    uint32_t k;
-    if (v != v) {
-        k = 0u;
-    } else {
-        const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
-        k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    }
-    return ((unsigned long long)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+    return ((unsigned long long)order_key(v) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
 }
 
 /* Ungrouped routing (n_group <= 1), one workgroup per token: scores, selection values,
@@ -438,85 +606,219 @@ __global__ __launch_bounds__(1024) void k_route_bucket(RouteArgs a) {
     bucket_pairs(a, in_lds ? pid : a.ids, cnt, base, tid, nth);
 }
 
-/* Ungrouped routing of up to 16 tokens (E <= 256) and their bucketing in one workgroup:
- * wave t routes token t (scores and weights as k_route_rank; the K experts by K rounds
- * of a wave maximum over the same keys), then all threads bucket. */
+/* Ungrouped routing of up to 16 tokens (E <= 256, K <= 64) and their bucketing in one
+ * workgroup. Wave t routes token t: scores and weights as k_route_rank; the K experts by
+ * K rounds of a wave maximum of the 32-bit order keys of the selection values, the winner
+ * being the lowest expert index that holds the maximum (ballots in index order), which is
+ * ranks_before's order. Each choice sets the token's bit in its expert's token mask, so
+ * the bucketing needs no counting pass: an expert's pair count is the popcount of its
+ * mask, and a pair's place among its expert's pairs (tokens ascending, model.c:1030-1035)
+ * the popcount of the mask bits below its token (a token's K experts are distinct:
+ * route_select picks distinct experts, and replayed routes were recorded from it). The
+ * expert table is staged into LDS while the logits load, and all threads write the slot
+ * descriptors at the end. */
 constexpr int RS_TMAX = 16, RS_EMAX = 256;
+constexpr int RS_TW = (int)(sizeof(ExpertW) / 4), RS_DW = (int)(sizeof(SlotDesc) / 4);
+static_assert(sizeof(ExpertW) % 4 == 0 && sizeof(SlotDesc) == sizeof(ExpertW) + 16, "slot descriptor words");
+static_assert(__builtin_offsetof(SlotDesc, p0) == sizeof(ExpertW) && __builtin_offsetof(SlotDesc, n) == sizeof(ExpertW) + 4 &&
+                  __builtin_offsetof(SlotDesc, e) == sizeof(ExpertW) + 8,
+              "slot descriptor fields after the matrices: p0, n, e, pad");
+
+/* routing of token t by one wave (lane e % 64 holds expert e, NU experts per lane):
+ * scores into sc, then the K experts, their weights, and the token's bits in tmask */
+template <int NU>
+__device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, const float (&lgv)[RS_EMAX / 64], float *sc,
+                                                  int *pid, uint32_t *tmask) {
+    const int lane = threadIdx.x & 63, E = a.E, K = a.K;
+    float x[NU];
+    bool ok[NU];
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        ok[u] = lane + 64 * u < E;
+        x[u] = lgv[u];
+    }
+    if (a.score_fn == 0) {
+        /* softmax (quant.c:634-642): m = running max from x[0] (a NaN x[0] makes m NaN) */
+        float m = -__builtin_huge_valf();
+#pragma unroll
+        for (int u = 0; u < NU; u++)
+            if (ok[u] && x[u] == x[u]) m = fmaxf(m, x[u]);
+        m = wave_max_f32(m);   /* a maximum: any reduction order gives the same value */
+        const float x0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[0]), 0));
+        if (x0 != x0) m = x0;
+        float ev[NU];
+#pragma unroll
+        for (int u = 0; u < NU; u++) ev[u] = exp_glibc_f(fadd(x[u], -m));
+#pragma unroll
+        for (int u = 0; u < NU; u++)
+            if (ok[u]) sc[lane + 64 * u] = ev[u];
+        wave_sync();
+        float L = 0.0f;
+        if (lane < 16)
+            for (int e = lane; e < E; e += 16) L = fadd(L, sc[e]);
+        L = tree16(L);
+        const float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L), 0));
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            x[u] = fdiv(ev[u], sum);
+            if (ok[u]) sc[lane + 64 * u] = x[u];
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            x[u] = fdiv(1.0f, fadd(1.0f, exp_glibc_f(-x[u])));
+            if (ok[u]) sc[lane + 64 * u] = x[u];
+        }
+    }
+    wave_sync();
+    int my_id = 0;
+    if (a.replay) {   /* uniform */
+        if (lane < K) my_id = replay_id(a, t, lane);
+    } else {
+        /* top-K: K rounds of the wave maximum of the order keys of the still unchosen
+         * experts; the lowest expert index holding it wins */
+        uint32_t kk[NU];
+        bool live[NU];
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            const int e = lane + 64 * u;
+            kk[u] = order_key(a.bias && ok[u] ? fadd(x[u], a.bias[e]) : x[u]);
+            live[u] = ok[u];
+        }
+        for (int j = 0; j < K; j++) {
+            uint32_t m = 0u;
+#pragma unroll
+            for (int u = 0; u < NU; u++) m = live[u] && kk[u] > m ? kk[u] : m;
+            m = wave_max_u32(m);
+            int e = 0;
+#pragma unroll
+            for (int u = NU - 1; u >= 0; u--) {
+                const unsigned long long b = __ballot(live[u] && kk[u] == m);
+                e = b ? 64 * u + __builtin_ctzll(b) : e;   /* the lowest u with a hit is taken last */
+            }
+#pragma unroll
+            for (int u = 0; u < NU; u++)
+                if (lane + 64 * u == e) live[u] = false;
+            my_id = lane == j ? e : my_id;
+        }
+    }
+    float w = lane < K ? sc[my_id] : 0.0f;
+    if (a.norm_topk) {
+        /* sum of the K weights in rank order (route_weights, model.c:830-838) */
+        float s = 0.0f;
+        for (int j = 0; j < K; j++) s = fadd(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j)));
+        w = fdiv(w, fadd(s, 1e-20f));
+    }
+    if (lane < K) {
+        w = fmul(w, a.routed_scale);
+        a.ids[(size_t)t * K + lane] = my_id;
+        a.wts[(size_t)t * K + lane] = w;
+        pid[t * K + lane] = my_id;
+        atomicOr(&tmask[my_id], 1u << t);
+        if (a.route_out) a.route_out[((size_t)t * a.n_moe + a.moe_ord) * K + lane] = my_id;
+    }
+}
 
 __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
     __shared__ float score[RS_TMAX][RS_EMAX];
-    __shared__ int chosen[RS_TMAX][64];
     __shared__ int pid[RS_TMAX * 64];
-    __shared__ int cnt[RS_EMAX], base[RS_EMAX];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, E = a.E, K = a.K, t = wave;
-    if (t < a.T) {
-        float *sc = score[t];
+    __shared__ uint32_t tmask[RS_EMAX];
+    __shared__ int base[RS_EMAX], slot_e[RS_EMAX];
+    __shared__ uint32_t tab[RS_EMAX * RS_TW];
+    __shared__ int nu_sh;
+    const int tid = threadIdx.x, nth = blockDim.x, wave = tid >> 6, lane = tid & 63, E = a.E, K = a.K, t = wave;
+    const int T = a.T, P = T * K;
+    float lgv[RS_EMAX / 64];
+    if (t < T) {
         const float *lg = a.logits + (size_t)t * E;
-        if (a.score_fn == 0) {
-            /* softmax (quant.c:634-642): m = running max from x[0] (a NaN x[0] makes m NaN) */
-            float m = -__builtin_huge_valf();
-            for (int e = lane; e < E; e += 64) {
-                const float x = lg[e];
-                sc[e] = x;
-                if (x == x) m = fmaxf(m, x);
-            }
-            m = wave_max_f32(m);   /* a maximum: any reduction order gives the same value */
-            wave_sync();
-            if (sc[0] != sc[0]) m = sc[0];
-            for (int e = lane; e < E; e += 64) sc[e] = exp_glibc_f(fadd(sc[e], -m));
-            wave_sync();
-            float L = 0.0f;
-            if (lane < 16)
-                for (int e = lane; e < E; e += 16) L = fadd(L, sc[e]);
-            L = tree16(L);
-            const float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L), 0));
-            for (int e = lane; e < E; e += 64) sc[e] = fdiv(sc[e], sum);
-        } else {
-            for (int e = lane; e < E; e += 64) sc[e] = fdiv(1.0f, fadd(1.0f, exp_glibc_f(-lg[e])));
-        }
-        if (a.replay) {   /* uniform */
-            if (lane < K) chosen[t][lane] = replay_id(a, t, lane);
-        } else {
-        /* top-K: K rounds of a wave-wide maximum of the selection keys (a larger key ranks
-         * first in ranks_before's order); the winner's key is cleared (0 is below every
-         * key) before the next round */
-        unsigned long long kk[RS_EMAX / 64];
 #pragma unroll
         for (int u = 0; u < RS_EMAX / 64; u++) {
             const int e = lane + 64 * u;
-            kk[u] = e < E ? rank_key(a.bias ? fadd(sc[e], a.bias[e]) : sc[e], e) : 0ull;
+            lgv[u] = e < E ? lg[e] : 0.0f;
         }
-        for (int j = 0; j < K; j++) {
-            unsigned long long m = 0ull;
+    }
+    {
+        /* the expert table into LDS: all loads of a round issued before its stores */
+        const uint32_t *tw = (const uint32_t *)a.table;
+        const int nw = E * RS_TW;
+        for (int w0 = 0; w0 < nw; w0 += 4 * nth) {
+            uint32_t v[4];
 #pragma unroll
-            for (int u = 0; u < RS_EMAX / 64; u++) m = kk[u] > m ? kk[u] : m;
-            m = wave_max_u64(m);   /* keys are unique: any reduction order gives the same maximum */
-            const int e = (int)(0xFFFFFFFFu - (uint32_t)m);
+            for (int k = 0; k < 4; k++) {
+                const int w = w0 + tid + k * nth;
+                v[k] = w < nw ? tw[w] : 0u;
+            }
 #pragma unroll
-            for (int u = 0; u < RS_EMAX / 64; u++)
-                if (lane + 64 * u == e) kk[u] = 0ull;
-            if (lane == 0) chosen[t][j] = e;
+            for (int k = 0; k < 4; k++) {
+                const int w = w0 + tid + k * nth;
+                if (w < nw) tab[w] = v[k];
+            }
         }
-        }
-        wave_sync();
-        const int id = lane < K ? chosen[t][lane] : 0;
-        float w = lane < K ? sc[id] : 0.0f;
-        if (a.norm_topk) {
-            /* sum of the K weights in rank order (route_weights, model.c:830-838) */
-            float s = 0.0f;
-            for (int j = 0; j < K; j++) s = fadd(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j)));
-            w = fdiv(w, fadd(s, 1e-20f));
-        }
-        if (lane < K) {
-            w = fmul(w, a.routed_scale);
-            a.ids[(size_t)t * K + lane] = id;
-            a.wts[(size_t)t * K + lane] = w;
-            pid[t * K + lane] = id;
-            if (a.route_out) a.route_out[((size_t)t * a.n_moe + a.moe_ord) * K + lane] = id;
+    }
+    for (int e = tid; e < E; e += nth) tmask[e] = 0u;
+    __syncthreads();
+    if (t < T) {
+        switch ((E + 63) / 64) {
+        case 1: route_token_small<1>(a, t, lgv, score[t], pid, tmask); break;
+        case 2: route_token_small<2>(a, t, lgv, score[t], pid, tmask); break;
+        case 3: route_token_small<3>(a, t, lgv, score[t], pid, tmask); break;
+        default: route_token_small<4>(a, t, lgv, score[t], pid, tmask); break;
         }
     }
     __syncthreads();
-    bucket_pairs(a, pid, cnt, base, tid, blockDim.x);
+    if (wave == 0) {
+        /* exclusive scan of the pair counts over experts, 64 experts per round */
+        int run = 0, nu_run = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + lane;
+            const int c = e < E ? __popc(tmask[e]) : 0, act = c > 0;
+            const int inc = wave_scan_incl(c), ninc = wave_scan_incl(act);
+            const int pos = run + inc - c, slot = nu_run + ninc - act;
+            if (e < E) {
+                base[e] = pos;
+                if (act) {
+                    a.ulist[slot] = e;
+                    a.u_p0[slot] = pos;
+                    a.u_n[slot] = c;
+                    slot_e[slot] = e;
+                }
+            }
+            run += __builtin_amdgcn_readlane(inc, 63);
+            nu_run += __builtin_amdgcn_readlane(ninc, 63);
+        }
+        if (lane == 0) {
+            nu_sh = nu_run;
+            *a.n_active = nu_run;
+            if (a.stats) {
+                a.stats[0] += (unsigned long long)P;
+                a.stats[1] += (unsigned long long)nu_run;
+            }
+        }
+    }
+    __syncthreads();
+    const int nu = nu_sh;
+    for (int p = tid; p < P; p += nth) {
+        const int e = pid[p], tt = p / K;
+        const int pos = base[e] + __popc(tmask[e] & ((1u << tt) - 1u));
+        a.pair_tok[pos] = tt;
+        a.pair_of[p] = pos;
+    }
+    /* slot descriptors, one word per thread: the active slots in full, n = 0 in the rest */
+    uint32_t *dw = (uint32_t *)a.desc;
+    for (int w = tid; w < a.n_slots * RS_DW; w += nth) {
+        const int slot = w / RS_DW, k = w % RS_DW;
+        if (slot < nu) {
+            const int e = slot_e[slot];
+            uint32_t v = 0u;
+            if (k < RS_TW) v = tab[e * RS_TW + k];
+            else if (k == RS_TW) v = (uint32_t)base[e];
+            else if (k == RS_TW + 1) v = (uint32_t)__popc(tmask[e]);
+            else if (k == RS_TW + 2) v = (uint32_t)e;
+            dw[w] = v;
+        } else if (k == RS_TW + 1) {
+            dw[w] = 0u;
+        }
+    }
 }
 
 /* ------------------------------------------------------------ GQA post-processing */
@@ -734,9 +1036,26 @@ void route(const RouteArgs &a, hipStream_t st) {
 }
 
 void norm(const NormArgs &a, hipStream_t st) {
-    int nth = ((a.D / 2 + 63) / 64) * 64;
-    nth = nth < 64 ? 64 : (nth > 1024 ? 1024 : nth);
-    k_norm<<<a.T, nth, (size_t)a.D * 2 * sizeof(float), st>>>(a);
+    const int n = norm_cover(a.D, a.a.nbp);
+    if (n <= NM_PER * 1024) {
+        const int nth = n < 1024 ? n : 1024;   /* a multiple of 64 */
+        const int ept = (n + nth - 1) / nth;
+        const size_t lds = (size_t)16 * norm_sq_stride(a.D) * sizeof(float);
+#define HX_NORM(M_)                                                              \
+        if (ept <= 2) k_norm<M_, 2><<<a.T, nth, lds, st>>>(a);                   \
+        else if (ept <= 4) k_norm<M_, 4><<<a.T, nth, lds, st>>>(a);              \
+        else k_norm<M_, 8><<<a.T, nth, lds, st>>>(a);                            \
+        return;
+        switch (a.mode) {
+        case 0: HX_NORM(0)
+        case 1: HX_NORM(1)
+        case 2: HX_NORM(2)
+        case 3: HX_NORM(3)
+        default: HX_NORM(4)
+        }
+#undef HX_NORM
+    }
+    k_norm_wide<<<a.T, 1024, (size_t)a.D * 2 * sizeof(float), st>>>(a);
 }
 
 void swiglu_quant(float *g, const float *u, int T, int F, const Act &a, hipStream_t st) {
