@@ -224,10 +224,17 @@ struct hearth_engine {
         if (FILE *f = fopen(path, "ab")) { fwrite(buf.data(), 1, buf.size(), f); fclose(f); }
     }
 
+    /* HEARTH_GPU_POISON=1 fills every work buffer with 0xFF bytes (a NaN in every float)
+     * when it is allocated: a kernel that reads memory no kernel wrote then shows */
     void *dalloc(size_t n) {
         void *p = nullptr;
         ck(hipMalloc(&p, n ? n : 256));
         allocs.push_back(p);
+        static const bool poison = [] {
+            const char *s = getenv("HEARTH_GPU_POISON");
+            return s && strcmp(s, "0") != 0;
+        }();
+        if (poison) ck(hipMemset(p, 0xFF, n ? n : 256));
         return p;
     }
     template <class T> T *dnew(size_t count) { return (T *)dalloc(sizeof(T) * count); }

@@ -210,7 +210,7 @@ struct SampleArgs {
     double *P;                        /* [n][V] final distributions */
     unsigned long long *skey;         /* [n][sort_n] top-p candidates (tier 0), in index order; then sort scratch */
     int *sidx;                        /* [n][sort_n] */
-    unsigned long long *skey2;        /* [n][sort_n] tier 0 sorted by descending p (stable) */
+    unsigned long long *skey2;        /* [n][sort_n] sort scratch of a fine bin too large for LDS */
     int *sidx2;                       /* [n][sort_n] */
     int *seg_begin, *seg_end;         /* [n] row v's candidates: [seg_begin, seg_end) = v * sort_n + [0, m) */
     int *bstar;                       /* [n] first histogram bin of tier 0 (-1: every nonzero entry) */
@@ -275,8 +275,6 @@ struct SampleScratch {
     unsigned long long *skey = nullptr, *skey2 = nullptr;
     int *sidx = nullptr, *sidx2 = nullptr, *seg_begin = nullptr, *seg_end = nullptr, *bstar = nullptr, *ci = nullptr,
         *row_rc = nullptr, *path = nullptr, *result = nullptr, *ctx = nullptr, *tok = nullptr, *par = nullptr;
-    void *sort_tmp = nullptr;         /* segmented radix sort workspace for n_cap rows */
-    size_t sort_tmp_bytes = 0;
     hipError_t ensure(int n, int V, bool need_q, int n_ctx);
     void release();
     ~SampleScratch() { release(); }

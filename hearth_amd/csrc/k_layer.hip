@@ -719,75 +719,86 @@ __device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, con
     }
 }
 
-__global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
-    __shared__ float score[RS_TMAX][RS_EMAX];
-    __shared__ int pid[RS_TMAX * 64];
-    __shared__ uint32_t tmask[RS_EMAX];
-    __shared__ int base[RS_EMAX], slot_e[RS_EMAX];
-    __shared__ uint32_t tab[RS_EMAX * RS_TW];
-    __shared__ int nu_sh;
-    const int tid = threadIdx.x, nth = blockDim.x, wave = tid >> 6, lane = tid & 63, E = a.E, K = a.K, t = wave;
-    const int T = a.T, P = T * K;
-    float lgv[RS_EMAX / 64];
-    if (t < T) {
-        const float *lg = a.logits + (size_t)t * E;
+/* LDS of the small routing: scores, chosen experts, token masks, scan results and the
+ * staged expert table */
+struct RouteSmem {
+    float score[RS_TMAX][RS_EMAX];
+    int pid[RS_TMAX * 64];
+    uint32_t tmask[RS_EMAX];
+    int base[RS_EMAX], slot_e[RS_EMAX];
+    uint32_t tab[RS_EMAX * RS_TW];
+    int nu;
+};
+
+/* the expert table into LDS (all loads of a round issued before its stores) and the
+ * token masks cleared; the caller's barrier publishes both */
+__device__ __forceinline__ void route_small_stage(const RouteArgs &a, RouteSmem &rs, int tid, int nth) {
+    const uint32_t *tw = (const uint32_t *)a.table;
+    const int nw = a.E * RS_TW;
+    for (int w0 = 0; w0 < nw; w0 += 4 * nth) {
+        uint32_t v[4];
 #pragma unroll
-        for (int u = 0; u < RS_EMAX / 64; u++) {
-            const int e = lane + 64 * u;
-            lgv[u] = e < E ? lg[e] : 0.0f;
+        for (int k = 0; k < 4; k++) {
+            const int w = w0 + tid + k * nth;
+            v[k] = w < nw ? tw[w] : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int w = w0 + tid + k * nth;
+            if (w < nw) rs.tab[w] = v[k];
         }
     }
-    {
-        /* the expert table into LDS: all loads of a round issued before its stores */
-        const uint32_t *tw = (const uint32_t *)a.table;
-        const int nw = E * RS_TW;
-        for (int w0 = 0; w0 < nw; w0 += 4 * nth) {
-            uint32_t v[4];
+    for (int e = tid; e < a.E; e += nth) rs.tmask[e] = 0u;
+}
+
+/* logits of token t, expert lane + 64 u, into registers */
+__device__ __forceinline__ void route_small_logits(const RouteArgs &a, const float *logits, int t, float (&lgv)[RS_EMAX / 64]) {
+    const int lane = threadIdx.x & 63;
+    const float *lg = logits + (size_t)t * a.E;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int w = w0 + tid + k * nth;
-                v[k] = w < nw ? tw[w] : 0u;
-            }
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int w = w0 + tid + k * nth;
-                if (w < nw) tab[w] = v[k];
-            }
-        }
+    for (int u = 0; u < RS_EMAX / 64; u++) {
+        const int e = lane + 64 * u;
+        lgv[u] = e < a.E ? lg[e] : 0.0f;
     }
-    for (int e = tid; e < E; e += nth) tmask[e] = 0u;
-    __syncthreads();
-    if (t < T) {
-        switch ((E + 63) / 64) {
-        case 1: route_token_small<1>(a, t, lgv, score[t], pid, tmask); break;
-        case 2: route_token_small<2>(a, t, lgv, score[t], pid, tmask); break;
-        case 3: route_token_small<3>(a, t, lgv, score[t], pid, tmask); break;
-        default: route_token_small<4>(a, t, lgv, score[t], pid, tmask); break;
-        }
+}
+
+/* token t's routing by the calling wave */
+__device__ __forceinline__ void route_small_token(const RouteArgs &a, RouteSmem &rs, int t, const float (&lgv)[RS_EMAX / 64]) {
+    switch ((a.E + 63) / 64) {
+    case 1: route_token_small<1>(a, t, lgv, rs.score[t], rs.pid, rs.tmask); break;
+    case 2: route_token_small<2>(a, t, lgv, rs.score[t], rs.pid, rs.tmask); break;
+    case 3: route_token_small<3>(a, t, lgv, rs.score[t], rs.pid, rs.tmask); break;
+    default: route_token_small<4>(a, t, lgv, rs.score[t], rs.pid, rs.tmask); break;
     }
+}
+
+/* bucketing after every token is routed: scan of the pair counts, pair places, slot
+ * descriptors (all threads of the workgroup call it) */
+__device__ __forceinline__ void route_small_bucket(const RouteArgs &a, RouteSmem &rs, int tid, int nth) {
+    const int E = a.E, K = a.K, P = a.T * K, wave = tid >> 6, lane = tid & 63;
     __syncthreads();
     if (wave == 0) {
         /* exclusive scan of the pair counts over experts, 64 experts per round */
         int run = 0, nu_run = 0;
         for (int e0 = 0; e0 < E; e0 += 64) {
             const int e = e0 + lane;
-            const int c = e < E ? __popc(tmask[e]) : 0, act = c > 0;
+            const int c = e < E ? __popc(rs.tmask[e]) : 0, act = c > 0;
             const int inc = wave_scan_incl(c), ninc = wave_scan_incl(act);
             const int pos = run + inc - c, slot = nu_run + ninc - act;
             if (e < E) {
-                base[e] = pos;
+                rs.base[e] = pos;
                 if (act) {
                     a.ulist[slot] = e;
                     a.u_p0[slot] = pos;
                     a.u_n[slot] = c;
-                    slot_e[slot] = e;
+                    rs.slot_e[slot] = e;
                 }
             }
             run += __builtin_amdgcn_readlane(inc, 63);
             nu_run += __builtin_amdgcn_readlane(ninc, 63);
         }
         if (lane == 0) {
-            nu_sh = nu_run;
+            rs.nu = nu_run;
             *a.n_active = nu_run;
             if (a.stats) {
                 a.stats[0] += (unsigned long long)P;
@@ -796,10 +807,10 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
         }
     }
     __syncthreads();
-    const int nu = nu_sh;
+    const int nu = rs.nu;
     for (int p = tid; p < P; p += nth) {
-        const int e = pid[p], tt = p / K;
-        const int pos = base[e] + __popc(tmask[e] & ((1u << tt) - 1u));
+        const int e = rs.pid[p], tt = p / K;
+        const int pos = rs.base[e] + __popc(rs.tmask[e] & ((1u << tt) - 1u));
         a.pair_tok[pos] = tt;
         a.pair_of[p] = pos;
     }
@@ -808,17 +819,28 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
     for (int w = tid; w < a.n_slots * RS_DW; w += nth) {
         const int slot = w / RS_DW, k = w % RS_DW;
         if (slot < nu) {
-            const int e = slot_e[slot];
+            const int e = rs.slot_e[slot];
             uint32_t v = 0u;
-            if (k < RS_TW) v = tab[e * RS_TW + k];
-            else if (k == RS_TW) v = (uint32_t)base[e];
-            else if (k == RS_TW + 1) v = (uint32_t)__popc(tmask[e]);
+            if (k < RS_TW) v = rs.tab[e * RS_TW + k];
+            else if (k == RS_TW) v = (uint32_t)rs.base[e];
+            else if (k == RS_TW + 1) v = (uint32_t)__popc(rs.tmask[e]);
             else if (k == RS_TW + 2) v = (uint32_t)e;
             dw[w] = v;
         } else if (k == RS_TW + 1) {
             dw[w] = 0u;
         }
     }
+}
+
+__global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
+    __shared__ RouteSmem rs;
+    const int tid = threadIdx.x, nth = blockDim.x, t = tid >> 6;
+    float lgv[RS_EMAX / 64];
+    if (t < a.T) route_small_logits(a, a.logits, t, lgv);
+    route_small_stage(a, rs, tid, nth);
+    __syncthreads();
+    if (t < a.T) route_small_token(a, rs, t, lgv);
+    route_small_bucket(a, rs, tid, nth);
 }
 
 /* ------------------------------------------------------------ GQA post-processing */

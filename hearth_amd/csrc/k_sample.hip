@@ -17,32 +17,28 @@
  *
  * Top-p does not sort the whole row. A histogram of the probabilities by exponent
  * (and one mantissa bit) picks the highest bins whose approximate mass exceeds top_p;
- * only their entries are sorted and summed in order: the candidates of every row are
- * gathered in index order and sorted by one segmented radix sort over all rows
- * (rocPRIM, stable, so equal probabilities keep index order, as a stable descending
- * argsort does). Once the running sum c has reached
+ * only their entries (tier 0, gathered in index order) take part in the running sum, and
+ * they are not sorted whole either: by fine bins of their top bits from the top down,
+ * a bin is added in bulk when no entry of it can take the running sum out of its binade,
+ * to top_p or onto a rounding tie (then the sum over the bin is order-independent), and
+ * otherwise gathered, sorted (descending p, index order on ties: the stable descending
+ * argsort) and summed entry by entry (top_p_binned). Once the running sum c has reached
  * top_p * (1 + 2^-48), every later entry e of the descending order has
  * before_e = fl(c_e - p_e) >= c_{e-1} (1 - 3 * 2^-53) > top_p and is dropped, so the
- * entries below the chosen bins never need ordering. If the chosen bins run out before
- * that (the histogram is approximate), the rest of the row is sorted and the chain
- * continues — the result never depends on the histogram.
- *
- * If the chosen bins run out before the running sum reaches top_p (the histogram is
- * approximate), the rest of the row is sorted in the workgroup (bitonic, in LDS up to
- * 8192 entries, else in the row's global scratch) and the chain continues.
+ * entries below the chosen bins never need ordering. If tier 0 runs out before that
+ * (the histogram is approximate), the rest of the row is sorted in the workgroup
+ * (bitonic, in LDS up to 8192 entries, else in the row's global scratch) and the chain
+ * continues -- the result never depends on the histogram.
  *
  * k_sample_probs:  one workgroup per verify row; the distribution up to top-p, then
  *                  the row's top-p candidates (tier 0) in index order;
- * (segmented radix sort of the candidates, all rows at once)
- * k_sample_top_p:  one workgroup per row; the cumulative-sum chain over the sorted
- *                  candidates, the rest of the row if needed, renormalization, min-p;
+ * k_sample_top_p:  one workgroup per row; the cumulative-sum chain over tier 0 by fine
+ *                  bins, the rest of the row if needed, renormalization, min-p;
  * k_sample_walk:   one workgroup walks the tree from the root with the uniforms.
  */
 #include <climits>
 #include <functional>
 #include <vector>
-
-#include <rocprim/device/device_segmented_radix_sort.hpp>
 
 #include "hx_launch.h"
 
@@ -551,13 +547,211 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
     if (tid == 0) a.row_rc[v] = 0;
 }
 
-/* the top-p tail of Sampler.probs on row v (after the candidates of tier 0 were sorted),
+/* ---------------------------------------------------------------- top-p over fine bins */
+
+/* Tier 0 is summed without sorting it whole. The candidates (p bits and index, in index
+ * order) fall into fine bins by their top bits: bin = (bits >> (51 - mb)) - (blo << mb),
+ * a larger bin holding larger p, and the descending order is the bins from the top down,
+ * each bin in its own order. The running sum c only needs that order inside a bin when
+ * (a) c is 0 (the first entry sets c, the top bin), (b) the bin takes c out of its
+ * binade [2^e, 2^(e+1)), (c) the bin takes c to top_p (from there the drop decisions
+ * fl(c_j - p_j) >= top_p and the stop need each c_j), or (d) one of its p is halfway
+ * between two multiples of u = 2^(e-52) (the tie goes to the even result, which depends
+ * on c). Otherwise fl(c + p) = c + u RN(p / u) for each of its entries, whatever their
+ * order, and every entry is kept (each c_j < top_p): the bin adds u times the sum of the
+ * integers RN(p / u). A round computes those sums for every bin left at the current u
+ * (one pass over the candidates), adds the bins above the first bin that meets (b)-(d)
+ * in bulk, then gathers that bin, sorts it (p descending, index ascending: the stable
+ * descending argsort) and runs chain_exact over it from c. Rounds continue down the bins
+ * until the chain stops (c >= top_p (1 + 2^-48): the rest of the row is dropped) or
+ * tier 0 runs out (c carries over to tier 1). Every p left is at most c (the top entry
+ * is summed first), so p / u < 2^53; a bin's sum is kept as a high part (>> 20) and a
+ * low part so that no 64-bit sum can wrap, and is saturated once it passes 2^53. */
+constexpr int TB_NBIN = 2048;
+constexpr unsigned long long TB_FLAG = 1ull << 63, TB_SAT = 1ull << 60, TB_LIM = 1ull << 53;
+
+struct TopPBins {
+    unsigned long long hi[TB_NBIN], lo[TB_NBIN];
+    int cnt[TB_NBIN];
+    unsigned long long wpre[SP_WAVES];
+    unsigned long long dpre;   /* units before the crossing bin (or all, when none) */
+    int ib[4];                 /* [0] top bin, [1] gather counter, [2] crossing bin */
+};
+
+__device__ __forceinline__ unsigned long long tb_sat_add(unsigned long long a, unsigned long long b) {
+    const unsigned long long s = a + b;   /* a, b <= TB_SAT: no wrap */
+    return s > TB_SAT ? TB_SAT : s;
+}
+
+/* returns c after tier 0; stopped: the chain reached its stop (every later entry of the
+ * row, below tier 0 included, is to be dropped; those of tier 0 are dropped here) */
+__device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, double top_p, double thr_hi, double *P,
+                               unsigned char *smem, TopPBins &tb, ChainShared &cs, bool &stopped) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const unsigned long long *key = a.skey + (size_t)v * a.sort_n;
+    const int *idx = a.sidx + (size_t)v * a.sort_n;
+    int mb = 0;
+    while (mb < 7 && ((2048 - blo) << (mb + 1)) <= TB_NBIN) mb++;
+    const int nb = (2048 - blo) << mb, sh = 51 - mb, bofs = blo << mb;
+    for (int b = tid; b < nb; b += SP_T) tb.cnt[b] = 0;
+    if (tid == 0) tb.ib[0] = -1;
+    __syncthreads();
+    {
+        int top = -1;
+        for (int j = tid; j < m; j += SP_T) {
+            const int b = (int)(key[j] >> sh) - bofs;   /* in [0, nb): 0 < p <= 1 in a bin >= blo */
+            if (b >= 0 && b < nb) {
+                atomicAdd(&tb.cnt[b], 1);
+                top = b > top ? b : top;
+            }
+        }
+        for (int off = 32; off >= 1; off >>= 1) {
+            const int o = __shfl_xor(top, off, 64);
+            top = o > top ? o : top;
+        }
+        if (lane == 0 && top >= 0) atomicMax(&tb.ib[0], top);
+    }
+    __syncthreads();
+    int cur = tb.ib[0];
+    double c = 0.0;
+    stopped = false;
+    int stop_bin = -1;
+    while (cur >= 0) {
+        int bx = cur;   /* the bin summed entry by entry this round */
+        if (c >= top_p) {
+            /* every bin left is summed entry by entry: the next one that holds entries */
+            while (bx >= 0 && tb.cnt[bx] == 0) bx--;
+        } else if (c > 0.0) {
+            int e = ilogb(c);
+            if (e < -1022) e = -1022;
+            const double u = ldexp(1.0, e - 52);
+            const unsigned long long D0 = (unsigned long long)(c / u);   /* exact: c is a multiple of u below 2^53 u */
+            for (int b = tid; b <= cur; b += SP_T) { tb.hi[b] = 0ull; tb.lo[b] = 0ull; }
+            if (tid == 0) tb.ib[2] = -1;
+            __syncthreads();
+            for (int j = tid; j < m; j += SP_T) {
+                const unsigned long long k = key[j];
+                const int b = (int)(k >> sh) - bofs;
+                if (b >= 0 && b <= cur) {
+                    const double q = __longlong_as_double((long long)k) / u;   /* a power-of-two scaling: exact */
+                    const double f = floor(q), r = q - f;
+                    if (r == 0.5) {
+                        atomicOr(&tb.hi[b], TB_FLAG);
+                    } else {
+                        const unsigned long long d = (unsigned long long)f + (r > 0.5 ? 1ull : 0ull);
+                        atomicAdd(&tb.hi[b], d >> 20);
+                        atomicAdd(&tb.lo[b], d & 0xFFFFFull);
+                    }
+                }
+            }
+            __syncthreads();
+            /* descending scan: thread t holds bins cur - 2t (first) and cur - 2t - 1 */
+            const int b1 = cur - 2 * tid, b2 = b1 - 1;
+            auto sval = [&](int b, bool &flag) -> unsigned long long {
+                flag = false;
+                if (b < 0) return 0ull;
+                const unsigned long long h = tb.hi[b];
+                flag = (h & TB_FLAG) != 0ull;
+                const unsigned long long hh = h & ~TB_FLAG;
+                if (hh >= (1ull << 33)) return TB_SAT;
+                return tb_sat_add(hh << 20, tb.lo[b]);
+            };
+            bool f1, f2;
+            const unsigned long long s1 = sval(b1, f1), s2 = sval(b2, f2), s12 = tb_sat_add(s1, s2);
+            unsigned long long inc = s12;
+            for (int off = 1; off < 64; off <<= 1) {
+                const unsigned long long y = __shfl_up(inc, off, 64);
+                if (lane >= off) inc = tb_sat_add(inc, y);
+            }
+            if (lane == 63) tb.wpre[w] = inc;
+            __syncthreads();
+            unsigned long long wb = 0ull;
+            for (int i = 0; i < w; i++) wb = tb_sat_add(wb, tb.wpre[i]);
+            unsigned long long excl = __shfl_up(inc, 1, 64);
+            excl = tb_sat_add(wb, lane ? excl : 0ull);
+            const unsigned long long pre1 = tb_sat_add(D0, excl), aft1 = tb_sat_add(pre1, s1), aft2 = tb_sat_add(aft1, s2);
+            auto crosses = [&](unsigned long long after) {
+                return after >= TB_LIM || (double)after * u >= top_p;
+            };
+            int cand = -1;
+            if (b1 >= 0 && (f1 || crosses(aft1))) cand = b1;
+            else if (b2 >= 0 && (f2 || crosses(aft2))) cand = b2;
+            if (cand >= 0) atomicMax(&tb.ib[2], cand);
+            __syncthreads();
+            bx = tb.ib[2];
+            if (bx >= 0 && (bx == b1 || bx == b2)) tb.dpre = bx == b1 ? pre1 : aft1;
+            if (bx < 0 && tid == SP_T - 1) tb.dpre = tb_sat_add(D0, tb_sat_add(wb, inc));   /* every bin left */
+            __syncthreads();
+            c = (double)tb.dpre * u;   /* below 2^53 u: exact */
+            __syncthreads();
+        }
+        if (bx < 0) break;   /* every bin left was added in bulk */
+        const int n = tb.cnt[bx];
+        if (n > 0) {
+            int N = 1;
+            while (N < n) N <<= 1;
+            const bool in_lds = N <= SORT_LDS;
+            unsigned long long *sk = in_lds ? (unsigned long long *)smem : a.skey2 + (size_t)v * a.sort_n;
+            int *si = in_lds ? (int *)(smem + SORT_LDS * 8) : a.sidx2 + (size_t)v * a.sort_n;
+            if (tid == 0) tb.ib[1] = 0;
+            __syncthreads();
+            for (int j0 = 0; j0 < m; j0 += SP_T) {
+                const int j = j0 + tid;
+                const unsigned long long k = j < m ? key[j] : 0ull;
+                const bool in = j < m && (int)(k >> sh) - bofs == bx;
+                const unsigned long long bal = __ballot(in);
+                int base = 0;
+                if (lane == 0 && bal) base = atomicAdd(&tb.ib[1], __popcll(bal));
+                base = __shfl(base, 0, 64);
+                if (in) {
+                    const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+                    sk[pos] = k;
+                    si[pos] = idx[j];
+                }
+            }
+            for (int j = n + tid; j < N; j += SP_T) { sk[j] = 0ull; si[j] = INT_MAX; }
+            __syncthreads();
+            if (in_lds) bitonic_block(sk, si, N, 2, N, N, 0);
+            else bitonic_global(sk, si, N, (unsigned long long *)smem, (int *)(smem + SORT_LDS * 8));
+            int stop;
+            const double c_in = c;
+            auto px = [&](int j) { return __longlong_as_double((long long)sk[j]); };
+            auto drop = [&](int j, double cj) {
+                if (dsub(cj, px(j)) >= top_p) P[si[j]] = 0.0;
+            };
+            if (c_in == 0.0) {
+                c = chain_exact(px, n, thr_hi, &stop, drop, cs);
+            } else {
+                auto px1 = [&](int j) { return j == 0 ? c_in : px(j - 1); };
+                auto drop1 = [&](int j, double cj) { if (j > 0) drop(j - 1, cj); };
+                c = chain_exact(px1, n + 1, thr_hi, &stop, drop1, cs);
+                stop = stop - 1;
+            }
+            for (int j = stop + 1 + tid; j < n; j += SP_T) P[si[j]] = 0.0;
+            __syncthreads();
+            if (stop < n) {
+                stopped = true;
+                stop_bin = bx;
+                break;
+            }
+        }
+        cur = bx - 1;
+    }
+    if (stopped)
+        for (int j = tid; j < m; j += SP_T)
+            if ((int)(key[j] >> sh) - bofs < stop_bin) P[idx[j]] = 0.0;
+    __syncthreads();
+    return c;
+}
+
+/* the top-p tail of Sampler.probs on row v (after the candidates of tier 0 were gathered),
  * then min-p; row_rc[v] = 0 when done. Rows that finished in k_sample_probs have an
  * empty candidate segment and are left alone. */
 __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
     __shared__ __align__(16) unsigned char smem[SMEM];
     __shared__ RowShared rs;
     __shared__ ChainShared cs;
+    __shared__ TopPBins tb;
     const int v = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int V = a.V;
     double *P = a.P + (size_t)v * V;
@@ -580,8 +774,20 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
             int *idx;
             if (tier == 0) {
                 m = a.seg_end[v] - v * a.sort_n;
-                key = a.skey2 + (size_t)v * a.sort_n;
-                idx = a.sidx2 + (size_t)v * a.sort_n;
+                if (m == 0) continue;
+                bool stopped;
+                c = top_p_binned(a, v, m, blo, top_p, thr_hi, P, smem, tb, cs, stopped);
+                if (stopped || c >= thr_hi) {
+                    done = true;
+                    if (blo > 0)
+                        for (int i = tid; i < V; i += SP_T) {
+                            const double p = P[i];
+                            const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
+                            if (p > 0.0 && b < blo) P[i] = 0.0;
+                        }
+                }
+                __syncthreads();
+                continue;
             } else {
             /* count, then gather the tier's entries */
             int cnt = 0;
@@ -819,14 +1025,12 @@ template <class T> hipError_t grow(T *&p, size_t count) {
 
 void SampleScratch::release() {
     void *ps[] = {P, q, u, wa, wb, cw, cc, skey, skey2, sidx, sidx2, seg_begin, seg_end, bstar, ci, row_rc, path,
-                  result, ctx, tok, par, sort_tmp};
+                  result, ctx, tok, par};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     P = q = u = wa = wb = cw = cc = nullptr;
     skey = skey2 = nullptr;
     sidx = sidx2 = seg_begin = seg_end = bstar = ci = row_rc = path = result = ctx = tok = par = nullptr;
-    sort_tmp = nullptr;
-    sort_tmp_bytes = 0;
     n_cap = V = ctx_cap = sort_n = 0;
     has_q = false;
 }
@@ -849,16 +1053,6 @@ hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
             (e = grow(row_rc, rows)) || (e = grow(path, rows)) || (e = grow(tok, rows)) || (e = grow(par, rows)))
             return e;
         if (has_q && (e = grow(q, rows * V))) return e;
-        /* the radix sort's workspace for rows segments over rows * sort_n keys */
-        size_t bytes = 0;
-        if ((e = rocprim::segmented_radix_sort_pairs_desc(nullptr, bytes, skey, skey2, sidx, sidx2,
-                                                           (unsigned int)(rows * sort_n), (unsigned int)rows,
-                                                           seg_begin, seg_end)) != hipSuccess)
-            return e;
-        if (sort_tmp) (void)hipFree(sort_tmp);
-        sort_tmp = nullptr;
-        if ((e = hipMalloc(&sort_tmp, bytes ? bytes : 1)) != hipSuccess) return e;
-        sort_tmp_bytes = bytes;
         n_cap = n;
     }
     if (need_q && !has_q) {
@@ -896,15 +1090,9 @@ hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, 
     return hipSuccess;
 }
 
-/* Sampler.probs of n rows: the distribution and top-p candidates, their sort, the
- * top-p tail */
-hipError_t probs(SampleScratch &m, const SampleArgs &a, int n, hipStream_t st) {
+/* Sampler.probs of n rows: the distribution and top-p candidates, then the top-p tail */
+hipError_t probs(SampleScratch &, const SampleArgs &a, int n, hipStream_t st) {
     k_sample_probs<<<n, SP_T, 0, st>>>(a);
-    size_t bytes = m.sort_tmp_bytes;
-    const hipError_t e = rocprim::segmented_radix_sort_pairs_desc(
-        m.sort_tmp, bytes, a.skey, a.skey2, a.sidx, a.sidx2, (unsigned int)((size_t)n * a.sort_n), (unsigned int)n,
-        a.seg_begin, a.seg_end, 0, 64, st);
-    if (e != hipSuccess) return e;
     k_sample_top_p<<<n, SP_T, 0, st>>>(a);
     return hipGetLastError();
 }

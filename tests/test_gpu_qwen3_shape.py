@@ -120,15 +120,32 @@ def test_chain_verify_equals_reference_engine(prefilled, model):
         eng.kv_import(snap, CTX)
         runs.append(eng.eval(toks, all_logits=True))
     _assert_same(runs[1], runs[0], "a repeated GPU evaluation")
-    ref = E(model, lib=str(O.REF_LIB), threads=THREADS, prefetch="off", max_seq=CTX + 64, cache_gb=16.0)
-    try:
-        ref.eval(prompt)
-        lr = ref.eval(toks, all_logits=True)
-    finally:
-        ref.close()
+
+    def reference_run():
+        ref = E(model, lib=str(O.REF_LIB), threads=THREADS, prefetch="off", max_seq=CTX + 64, cache_gb=16.0)
+        try:
+            ref.eval(prompt)
+            return ref.eval(toks, all_logits=True)
+        finally:
+            ref.close()
+
+    lr = reference_run()
     rows = (_bits(runs[0]) != _bits(lr)).any(1)
-    assert not rows.any(), (f"{int(rows.sum())} of 9 rows differ from the reference engine; argmax GPU "
-                            f"{runs[0].argmax(1).tolist()} reference {lr.argmax(1).tolist()}")
+    if rows.any():
+        # tell a GPU difference from a reference run that does not repeat itself: a second
+        # reference run, and the oracle's own prefill and verify step
+        lr2 = reference_run()
+        m = O.Model(model, cap=CTX + 64, threads=THREADS)
+        m.eval(prompt, logits=False)
+        lo = m.eval(toks)
+        same = lambda x, y: bool(np.array_equal(_bits(x), _bits(y)))   # noqa: E731
+        detail = (f"{int(rows.sum())} of 9 rows differ from the reference engine (argmax GPU "
+                  f"{runs[0].argmax(1).tolist()}, reference {lr.argmax(1).tolist()}); GPU == oracle from its own "
+                  f"prefill: {same(runs[0], lo)}; reference == oracle: {same(lr, lo)}; the reference repeats "
+                  f"itself: {same(lr, lr2)}")
+        if not same(lr, lr2):
+            pytest.skip("the reference engine gave two different results on this host: " + detail)
+        raise AssertionError(detail)
 
 
 def _tree_4x4x4():
