@@ -546,6 +546,183 @@ __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
     }
 }
 
+
+constexpr long long TV_WIDE = 2048;     /* summing waves (one head each) from which the wide shapes pay */
+
+/* The same sums when there are many chains (a tree's tokens, MLA's 128 heads): NS
+ * summing waves of R heads each (NS * R heads of one KV group per workgroup, R
+ * independent chains per lane sharing each V read), NL loader waves, ROWS rows per tile
+ * (16 per loader wave). Each staged V tile then serves more chains, and several summing
+ * waves share each SIMD (the single-chain kernel above keeps one per SIMD, where the
+ * latency of its one chain is the floor). p of the workgroup's heads: load k of loader
+ * lw takes 64 consecutive rows of one head (element f = (k NL + lw) 64 + lane of the
+ * [head][row] tile). */
+template <int NS, int NL, int R, int ROWS>
+__global__ __launch_bounds__(64 * (NS + NL)) void k_attn_values_w(AttnArgs a) {
+    constexpr int NT = 64 * (NS + NL), NH = NS * R, PL = NH * ROWS / (NL * 64), NG = ROWS / 16;
+    constexpr int WV = 2 * (4 + PL);   /* loads of two tiles: the loads still in flight when a tile is stored */
+    static_assert(ROWS == 16 * NL, "k_attn_values: each loader wave stages 16 rows of a tile");
+    static_assert(ROWS % 64 == 0 && (NH * ROWS) % (NL * 64) == 0, "k_attn_values: p in loads of 64 rows of one head");
+    static_assert(NG % 2 == 0 && WV < 64, "k_attn_values: groups of 16 rows in pairs; vmcnt fits");
+    __shared__ __attribute__((aligned(16))) float vt[2][(ROWS / 4) * TV_BQ];
+    __shared__ __attribute__((aligned(16))) float pt[TV_PS][NH][ROWS];
+    __shared__ int anc_s[MAX_ANC];
+    const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
+    const int nd = (hd + 63) / 64, qpt = (grp + NH - 1) / NH;
+    int b = blockIdx.x;
+    const int dc = b % nd;
+    b /= nd;
+    const int g = b % Hkv;
+    b /= Hkv;
+    const int hq = b % qpt, t = b / qpt;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int pos0 = *a.g.pos, dep = a.g.depth[t];
+    const int nr = pos0 + dep + 1;
+    const int ntiles = (nr + ROWS - 1) / ROWS;
+    const bool chain = a.g.chain != 0;
+    if (!chain) {
+        for (int jj = tid; jj <= dep; jj += NT) anc_s[jj] = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + jj];
+        __syncthreads();
+    }
+    if (wave >= NS) {
+        /* loader wave lw: rows 16 lw + lane % 16 of each tile, columns 16 cb + 4 (lane / 16)
+         * .. + 3 for cb = 0..3, and PL 64-row pieces of the heads' p rows */
+        const int lw = wave - NS, r = lane & 15, cg = lane >> 4;
+        const __amdgpu_buffer_rsrc_t vrs =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(a.vc + (size_t)g * a.cap * hd), 0, a.cap * hd * 4, 0x00020000);
+        int coff[4];
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++) {
+            const int col = dc * 64 + 16 * cb + 4 * cg;
+            coff[cb] = (col < hd ? col : 0) * 4;
+        }
+        /* p piece k: 64 rows from row pro(k) of local head phl(k), from S by an LDS-direct load */
+        const float *srow0 = a.S + ((size_t)t * a.H + (size_t)g * grp) * a.ldS;
+        auto pload = [&](int k, int slot, auto voff) {
+            const int f0 = (k * NL + lw) * 64, phl = f0 / ROWS, pro = f0 % ROWS, phh = hq * NH + phl;
+            const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(srow0 + (size_t)(phh < grp ? phh : 0) * a.ldS), 0, a.ldS * 4, 0x00020000);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (__attribute__((address_space(3))) void *)&pt[slot][phl][pro], 4,
+                                                     voff(pro) * 4, 0, 0, 0);
+        };
+        const int hd4 = hd * 4, roff = r * hd4;
+        /* word of (row 16 lw + r, column 16 cb + 4 cg + e): bank 16 lw + r + 16 cg + 4 e mod 64 */
+        const int wbase = (4 * lw + (r >> 2)) * TV_BQ + 16 * cg + (r & 3);
+        auto store = [&](int slot, const tv_u4 (&Rg)[4]) {
+            float *w = &vt[slot][wbase];
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) {
+                w[64 * cb + 0] = __uint_as_float(Rg[cb].x);
+                w[64 * cb + 4] = __uint_as_float(Rg[cb].y);
+                w[64 * cb + 8] = __uint_as_float(Rg[cb].z);
+                w[64 * cb + 12] = __uint_as_float(Rg[cb].w);
+            }
+        };
+        auto run = [&](auto chain_tag) {
+            constexpr bool CHAIN = decltype(chain_tag)::value;
+            auto load = [&](int i, tv_u4 (&Rg)[4]) {
+                const int vb = i * ROWS;
+                if constexpr (CHAIN) {
+                    const int vo = roff + (vb + 16 * lw) * hd4;
+#pragma unroll
+                    for (int cb = 0; cb < 4; cb++) Rg[cb] = __builtin_amdgcn_raw_buffer_load_b128(vrs, vo + coff[cb], 0, 0);
+#pragma unroll
+                    for (int k = 0; k < PL; k++) pload(k, i % TV_PS, [&](int pro) { return vb + pro + lane; });
+                } else {
+                    int v = vb + 16 * lw + r;
+                    v = v < nr ? v : nr - 1;
+                    const int an = anc_s[v > pos0 ? v - pos0 : 0];
+                    const int srow = v < pos0 ? v : an;
+#pragma unroll
+                    for (int cb = 0; cb < 4; cb++) Rg[cb] = __builtin_amdgcn_raw_buffer_load_b128(vrs, srow * hd4 + coff[cb], 0, 0);
+#pragma unroll
+                    for (int k = 0; k < PL; k++)
+                        pload(k, i % TV_PS, [&](int pro) {
+                            const int vp = vb + pro + lane;
+                            return vp < nr ? vp : nr - 1;
+                        });
+                }
+            };
+            tv_u4 R0[4], R1[4], R2[4];
+            load(0, R0);
+            load(1, R1);
+            load(2, R2);
+            HX_WAIT_VMCNT(WV);
+            store(0, R0);
+            /* step i: tile i is published; tile i + 3 is loaded into the registers tile i came
+             * from; tile i + 1 is stored into the slot tile i - 1 was summed from. The loop
+             * has no exit inside its body, so the compiler keeps the exact load counts. */
+#define TV_STEP(i_, RL, RW)                                                                 \
+            __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) only */                       \
+            __builtin_amdgcn_s_barrier();                                                   \
+            load((i_) + 3, RL);                                                             \
+            HX_WAIT_VMCNT(WV);                                                              \
+            store(((i_) + 1) & 1, RW);
+            int i = 0;
+            for (; i + 3 <= ntiles; i += 3) {
+                TV_STEP(i, R0, R1)
+                TV_STEP(i + 1, R1, R2)
+                TV_STEP(i + 2, R2, R0)
+            }
+            if (i < ntiles) {
+                TV_STEP(i, R0, R1)
+                if (i + 1 < ntiles) {
+                    TV_STEP(i + 1, R1, R2)
+                }
+            }
+#undef TV_STEP
+        };
+        if (chain) run(std::true_type{});
+        else run(std::false_type{});
+        HX_WAIT_VMCNT(0);              /* no LDS write may land after the workgroup ends */
+    } else {
+        bool live[R];
+        int h[R];
+        float acc[R];
+#pragma unroll
+        for (int rr = 0; rr < R; rr++) {
+            const int hh = hq * NH + wave * R + rr;
+            live[rr] = hh < grp;
+            h[rr] = g * grp + (live[rr] ? hh : 0);
+            acc[rr] = 0.0f;
+        }
+        for (int i = 0; i < ntiles; i++) {
+            __syncthreads();
+            const int slot = i & 1, nv = nr - i * ROWS;
+            const float4 *vw = (const float4 *)&vt[slot][lane * 4];
+            if (nv >= ROWS) {
+                const float *pw = &pt[i % TV_PS][wave * R][lane & 15];
+                /* group by group of 16 rows: the R chains of a lane and the other summing
+                 * waves of the SIMD cover the latency of the reads */
+                for (int gr = 0; gr < NG; gr++) {
+                    float4 V[4];
+                    float P[R];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) V[j] = vw[(gr * 4 + j) * (TV_BQ / 4)];
+#pragma unroll
+                    for (int rr = 0; rr < R; rr++) P[rr] = pw[rr * ROWS + gr * 16];
+#pragma unroll
+                    for (int rr = 0; rr < R; rr++) tv_sum16(acc[rr], P[rr], V);
+                }
+            } else {
+                const float *pv = &pt[i % TV_PS][wave * R][0];
+                for (int rw = 0; rw < nv; rw++) {
+                    const float vv = vt[slot][(rw >> 2) * TV_BQ + lane * 4 + (rw & 3)];
+#pragma unroll
+                    for (int rr = 0; rr < R; rr++) acc[rr] = fadd(acc[rr], fmul(pv[rr * ROWS + rw], vv));
+                }
+            }
+        }
+        const int d = dc * 64 + lane;
+#pragma unroll
+        for (int rr = 0; rr < R; rr++) {
+            if (live[rr] && d < hd) a.out[(size_t)t * a.H * hd + (size_t)h[rr] * hd + d] = acc[rr];
+            if (a.qo_on && live[rr])
+                quant_block_wave(acc[rr], a.qo, a.qo_hm ? h[rr] * a.T + t : t, a.qo_hm ? dc : h[rr] * (hd >> 6) + dc);
+        }
+    }
+}
+
 } // namespace
 
 namespace hxl {
@@ -580,9 +757,19 @@ void attention_scores(const AttnArgs &a, hipStream_t st) {
 }
 
 void attention_finish(const AttnArgs &a, hipStream_t st) {
-    const int grp = a.H / a.Hkv;
+    const int grp = a.H / a.Hkv, nd = (a.hd + 63) / 64;
     k_attn_softmax<<<a.T * a.H, SM_T, 0, st>>>(a);
-    const int nd = (a.hd + 63) / 64, qpt = (grp + TV_SUM - 1) / TV_SUM;
+    const bool wide = (long long)a.T * a.H * nd >= TV_WIDE;
+#define HX_TV(NS_, NL_, R_, ROWS_)                                                                     \
+    {                                                                                                  \
+        const int qpt = (grp + NS_ * R_ - 1) / (NS_ * R_);                                             \
+        k_attn_values_w<NS_, NL_, R_, ROWS_><<<a.T * qpt * a.Hkv * nd, 64 * (NS_ + NL_), 0, st>>>(a);  \
+        return;                                                                                        \
+    }
+    if (wide && grp >= 16) HX_TV(8, 4, 2, 64)
+    if (wide && grp >= 8) HX_TV(4, 4, 2, 64)
+#undef HX_TV
+    const int qpt = (grp + TV_SUM - 1) / TV_SUM;
     k_attn_values<<<a.T * qpt * a.Hkv * nd, TV_THREADS, 0, st>>>(a);
 }
 
