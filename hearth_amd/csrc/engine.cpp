@@ -173,6 +173,13 @@ struct hearth_engine {
     };
     std::vector<Captured> graphs;
     bool graph_on = true;    /* HEARTH_GPU_GRAPH=0 turns capture off */
+    /* attention order of the GQA layers: 0 the reference's canonical order (default), 1
+     * chunked (where the shape allows it, attn_chunk_ok); MLA layers are canonical */
+    int attn_mode = 0;
+    bool attn_chunk_ok = false;
+    float *apo = nullptr, *apm = nullptr, *apl = nullptr;   /* chunked partials (alias S) */
+    int anc_ld = 0;                                         /* chunks per partial row */
+    void drop_graphs();
     int rows_bound = 0;      /* nonzero while capturing: the graph's bound on pos + T */
     int nr_max(int T) const { return rows_bound ? rows_bound : pos + T; }
     void run_forward(int T, bool want_logits);
@@ -674,7 +681,19 @@ bool hearth_engine::open_model(char *err, size_t errlen) {
         }
         ao = dnew<float>(Bs * D);
         ldS = (cap + 63) & ~63;
-        S = dnew<float>(Bs * H * (size_t)ldS);
+        attn_chunk_ok = !mla && hxl::attention_chunked_ok(hd, H / Hkv);
+        if (attn_chunk_ok) {
+            /* one buffer serves either order: the canonical scores S or the chunked
+             * partials (a call uses one of them) */
+            anc_ld = (cap + 63) / 64;
+            const size_t part = Bs * H * (size_t)anc_ld;
+            S = dnew<float>(std::max(Bs * H * (size_t)ldS, part * (size_t)(hd + 2)));
+            apo = S;
+            apm = apo + part * (size_t)hd;
+            apl = apm + part;
+        } else {
+            S = dnew<float>(Bs * H * (size_t)ldS);
+        }
         ax = make_act(B, D);
         aatt = make_act(B, mla ? H * vd : q_dim);
         logits = dnew<float>(Bs * V);
@@ -859,7 +878,12 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             at.Hkv = Hkv; at.hd = hd; at.cap = cap; at.scale = c.attn_scale;
             at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos = d_pos; at.g.nr_max = nr_max(T); at.g.chain = geom_chain;
             at.qo = aatt; at.qo_on = w.o.quant && hd % 64 == 0;
-            hxl::attention(at, st);
+            if (attn_mode == 1) {
+                at.po = apo; at.pm = apm; at.pl = apl; at.nc_ld = anc_ld;
+                hxl::attention_chunked(at, st);
+            } else {
+                hxl::attention(at, st);
+            }
             dump("att", l, att, T, q_dim);
             if (w.o.quant && !at.qo_on) hxl::quant_rows(att, q_dim, T, q_dim / 64, aatt, st);
         });
@@ -1089,6 +1113,19 @@ int hearth_engine::run_geometry(const int32_t *tok, const int32_t *parent, int n
  * graph's grids cover rows up to the next multiple of 1024 (at most the capacity), and
  * the kernels read pos0 from d_pos, so the replay computes what the direct launches
  * would. At most 32 graphs are kept (the oldest is dropped). */
+/* Captured forwards hold the launches of the attention order they were captured with;
+ * a change of order drops them (after the stream has finished with them). */
+void hearth_engine::drop_graphs() {
+    if (graphs.empty()) return;
+    (void)hipSetDevice(dev);
+    (void)hipStreamSynchronize(st);
+    for (Captured &g : graphs) {
+        (void)hipGraphExecDestroy(g.exec);
+        (void)hipGraphDestroy(g.graph);
+    }
+    graphs.clear();
+}
+
 void hearth_engine::run_forward(int T, bool want_logits) {
     if (!graph_on || store || replay_dev || profiling || !dump_dir.empty() || T > 128) {
         forward(T, want_logits, 0);
@@ -1296,6 +1333,8 @@ HEARTH_API hearth_engine *hearth_open(const hearth_options *in, char *err, size_
     if (const char *dd = getenv("HEARTH_DEBUG_DUMP")) e->dump_dir = dd;
     if (const char *gg = getenv("HEARTH_GPU_GRAPH")) e->graph_on = strcmp(gg, "0") != 0;
     if (!e->open_model(err, errlen)) return nullptr;
+    const char *am = getenv("HEARTH_GPU_ATTN");
+    e->attn_mode = e->attn_chunk_ok && am && strcmp(am, "chunked") == 0 ? 1 : 0;
     log_msg(LOG_INFO, "%s: %s, %d layers (%d MoE), d_model %d, vocab %d, KV %d positions, device %d", o.model_path,
             e->c.arch.c_str(), e->L, e->c.n_moe, e->D, e->V, e->cap, e->dev);
     return e.release();
@@ -1703,6 +1742,18 @@ HEARTH_API int hearth_verify_sample(hearth_engine *e, const int32_t *tokens, con
         d_res = e->samp.result;
     });
 }
+
+HEARTH_API int hearth_gpu_set_attn_mode(hearth_engine *e, int mode) {
+    if (!e || (mode != HEARTH_GPU_ATTN_CANONICAL && mode != HEARTH_GPU_ATTN_CHUNKED)) return E_ARG;
+    if (mode == HEARTH_GPU_ATTN_CHUNKED && !e->attn_chunk_ok) return E_ARG;
+    if (mode != e->attn_mode) {
+        e->drop_graphs();
+        e->attn_mode = mode;
+    }
+    return OK;
+}
+
+HEARTH_API int hearth_gpu_get_attn_mode(hearth_engine *e) { return e ? e->attn_mode : E_ARG; }
 
 HEARTH_API int hearth_gpu_set_profiling(hearth_engine *e, int on) {
     if (!e) return E_ARG;

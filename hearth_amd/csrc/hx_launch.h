@@ -100,6 +100,8 @@ struct AttnArgs {
     Act qo;                   /* NUMERICS §2 blocks of out (when qo_on; head_dim % 64 == 0) */
     int qo_on;
     int qo_hm;                /* 1: qo rows are (head, token) = h * T + t with hd / 64 blocks each */
+    float *po, *pm, *pl;      /* chunked attention partials: [T * H][nc_ld][hd], [T * H][nc_ld] twice */
+    int nc_ld;                /* chunks per partial row: at least ceil(nr_max / 64) */
 };
 
 struct QkvArgs {
@@ -250,6 +252,10 @@ void attention(const AttnArgs &a, hipStream_t st);
 /* the two halves of attention(): scores; softmax + value sum */
 void attention_scores(const AttnArgs &a, hipStream_t st);
 void attention_finish(const AttnArgs &a, hipStream_t st);
+/* attention in the chunked order (64-row chunks folded in order; see k_attn.hip), for
+ * head_dim 64 or 128 and grp * head_dim <= 12288 (attention_chunked_ok) */
+bool attention_chunked_ok(int hd, int grp);
+void attention_chunked(const AttnArgs &a, hipStream_t st);
 void kv_move(float *cache_layer0, size_t layer_stride, int L, int Hkv, int cap, int hd, int pos0, const int *path_dev,
              int n, hipStream_t st);
 /* rows pos0 + path[j] -> pos0 + j of a [cap][width] array at offset off of every layer */

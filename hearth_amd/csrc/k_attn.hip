@@ -18,6 +18,7 @@
  * so the KV-group index (and value d-chunk) is the fastest-varying part of the ID and
  * the workgroups of one XCD read the same group's K or V rows from that XCD's L2.
  */
+#include <algorithm>
 #include <type_traits>
 
 #include "hx_device.h"
@@ -723,6 +724,277 @@ __global__ __launch_bounds__(64 * (NS + NL)) void k_attn_values_w(AttnArgs a) {
     }
 }
 
+/* ---- chunked attention ------------------------------------------------------------
+ * The engine's default order for GQA layers (a documented tolerance against the
+ * reference's order above, not bit-exact to it): the token's row list in chunks of 64
+ * rows (chunk c = logical rows 64c .. 64c+63), per chunk and head
+ *   s_i = scale * dotf(q, k_i)        dotf: fmaf over d = 0 .. hd-1 in order from 0.0f
+ *   m_c = max s_i (NaN if one is NaN), e_i = exp(s_i - m_c)
+ *   l_c = pairwise sum of the 64 positions (e_i, 0 past the token's rows), over the lanes
+ *         (ac_pairwise64)
+ *   o_c[d] = fmaf(e_i, v_i[d], o) over the chunk's rows in order from 0.0f
+ * and then, over the chunks in order, M = max m_c, w_c = exp(m_c - M),
+ * L = fmaf(l_c, w_c, L), O[d] = fmaf(o_c[d], w_c, O), out = O / L. Each step depends on
+ * the token's row list only (batch == sequential, tree node == chain root -> node).
+ *
+ * k_attn_chunk: one workgroup per (chunk, KV group, block of tokens), 8 waves. The
+ * chunk's 64 K rows, its V rows (transposed in 4-row blocks) and the block's queries go
+ * to LDS by LDS-direct loads, V last, so that the scores run while V lands. An item is
+ * RW heads of one token: scores with one key per lane (queries read as LDS broadcasts),
+ * the item's e kept in LDS, then the value sums with one column per lane. A tree node's
+ * own rows (logical rows past pos0, at its ancestors' slots) are read from the cache
+ * directly. k_attn_combine: one wave per (token, head, 64 columns) folds the chunks. */
+constexpr int AC_CH = 64;          /* rows per chunk */
+constexpr int AC_WAVES = 8;
+constexpr int AC_IPW = 4;          /* items per wave */
+constexpr int AC_QMAX = 12288;     /* floats of staged queries */
+
+__device__ __forceinline__ float ac_nanmax(float a, float b) { return a != a || b != b ? a + b : fmaxf(a, b); }
+
+/* the pairwise tree over the 64 lanes ((x0 + x1) + (x2 + x3)) + ..., in every lane: pairs
+ * and quads by quad_perm, 8 and 16 lanes by the half-row and row mirrors (every lane of a
+ * quad, then of a half-row, already holds the same partial), then the four row sums */
+__device__ __forceinline__ float ac_pairwise64(float x) {
+#define HX_PW_STEP(CTRL) x = fadd(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false)));
+    HX_PW_STEP(0xB1)    /* quad_perm [1, 0, 3, 2] */
+    HX_PW_STEP(0x4E)    /* quad_perm [2, 3, 0, 1] */
+    HX_PW_STEP(0x141)   /* row_half_mirror */
+    HX_PW_STEP(0x140)   /* row_mirror */
+#undef HX_PW_STEP
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+    return fadd(fadd(r0, r1), fadd(r2, r3));
+}
+
+template <int HD, int RW>
+__global__ __launch_bounds__(64 * AC_WAVES) void k_attn_chunk(AttnArgs a, int ntb, int nblk, int ncg) {
+    constexpr int ND = HD / 64, KLD = HD + 4, VQ = 4 * HD + 4;
+    constexpr int NKW = AC_CH * ND / AC_WAVES;   /* K loads per wave (64 dwords each) */
+    constexpr int NVW = AC_CH * ND / AC_WAVES;   /* V loads per wave */
+    static_assert(HD % 64 == 0 && (AC_CH * ND) % AC_WAVES == 0 && NKW + NVW < 48, "k_attn_chunk: staging map");
+    __shared__ __attribute__((aligned(16))) float ks[AC_CH * KLD];
+    __shared__ __attribute__((aligned(16))) float vq[(AC_CH / 4) * VQ];
+    __shared__ __attribute__((aligned(16))) float qs[AC_QMAX];
+    __shared__ __attribute__((aligned(16))) float es[AC_WAVES][AC_IPW][RW][AC_CH];
+    __shared__ unsigned long long etab[32];
+    const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
+    int b = blockIdx.x;
+    const int tb = b % nblk;
+    b /= nblk;
+    const int g = b % Hkv;
+    const int c = ncg - 1 - b / Hkv;             /* the last (partial) chunk first */
+    const int r0 = c * AC_CH;
+    const int t0 = tb * ntb, nt = min(ntb, a.T - t0);
+    if (nt <= 0) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    /* lane i holds the depth of token t0 + i (ntb <= 64), read once */
+    const int pos0 = *a.g.pos;
+    const int dep_l = lane < nt ? a.g.depth[t0 + lane] : 0;
+    const int dmax = (int)wave_max_u32((unsigned)dep_l);
+    if (pos0 + dmax + 1 <= r0) return;           /* no token of the block reaches the chunk */
+    /* rows of the chunk that every token reads from the slot of the same index */
+    const int kshared = min(max((a.g.chain ? pos0 + a.T : pos0) - r0, 0), AC_CH);
+    const float *kbase = a.kc + (size_t)g * a.cap * hd, *vbase = a.vc + (size_t)g * a.cap * hd;
+    exp_table_to_lds(etab);
+    {
+        const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void *)kbase, 0, a.cap * hd * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vbase, 0, a.cap * hd * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc((void *)a.q, 0, a.T * a.H * hd * 4, 0x00020000);
+        /* K: load f = k * 8 + wave is row f / ND, columns 64 (f % ND) .. + 63 */
+#pragma unroll
+        for (int k = 0; k < NKW; k++) {
+            const int f = k * AC_WAVES + wave, j = f / ND, cb = f % ND;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void *)&ks[j * KLD + 64 * cb], 4,
+                                                     ((r0 + j) * hd + 64 * cb + lane) * 4, 0, 0, 0);
+        }
+        /* queries of the block: load f is (token, head, 64 columns) */
+        const int nq = nt * grp * ND;
+        for (int f = wave; f < nq; f += AC_WAVES) {
+            const int cb = f % ND, th = f / ND, tl = th / grp, hl = th % grp;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                qrs, (__attribute__((address_space(3))) void *)&qs[th * HD + 64 * cb], 4,
+                (((t0 + tl) * a.H + g * grp + hl) * hd + 64 * cb + lane) * 4, 0, 0, 0);
+        }
+        /* V, transposed: load f is rows 4 qb .. 4 qb + 3 of columns 16 u .. 16 u + 15;
+         * lane l takes row 4 qb + l % 4 of column 16 u + l / 4, so the 64 dwords land in
+         * order in block qb: [column][4 rows] */
+#pragma unroll
+        for (int k = 0; k < NVW; k++) {
+            const int f = k * AC_WAVES + wave, qb = f / (HD / 16), u = f % (HD / 16);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                vrs, (__attribute__((address_space(3))) void *)&vq[qb * VQ + 64 * u], 4,
+                ((r0 + 4 * qb + (lane & 3)) * hd + 16 * u + (lane >> 2)) * 4, 0, 0, 0);
+        }
+        HX_WAIT_VMCNT(NVW);                      /* this wave's K and query loads landed */
+        __builtin_amdgcn_s_waitcnt(0xC07F);      /* and its exp table stores */
+        __builtin_amdgcn_s_barrier();            /* ... and every other wave's */
+    }
+    static_assert(AC_WAVES * AC_IPW <= 64, "k_attn_chunk: a block's tokens fit one wave's lanes");
+    const int ipt = grp / RW, nitems = nt * ipt;
+    const float scale = a.scale;
+    /* scores, e, m, l of this wave's items */
+#pragma unroll 1
+    for (int k = 0; k < AC_IPW; k++) {
+        const int it = wave + k * AC_WAVES;
+        if (it >= nitems) break;
+        const int tl = it / ipt, hb = it % ipt, t = t0 + tl;
+        const int nk = min(pos0 + __builtin_amdgcn_readlane(dep_l, tl) + 1 - r0, AC_CH);
+        if (nk <= 0) continue;
+        const bool valid = lane < nk;
+        float acc[RW];
+#pragma unroll
+        for (int r = 0; r < RW; r++) acc[r] = 0.0f;
+        const float4 *qv4 = (const float4 *)&qs[(tl * grp + hb * RW) * HD];
+        if (valid && lane < kshared) {
+            const float4 *kv4 = (const float4 *)&ks[lane * KLD];
+#pragma unroll 4
+            for (int d4 = 0; d4 < HD / 4; d4++) {
+                const float4 kv = kv4[d4];
+#pragma unroll
+                for (int r = 0; r < RW; r++) {
+                    const float4 qv = qv4[r * (HD / 4) + d4];
+                    acc[r] = __builtin_fmaf(qv.x, kv.x, acc[r]);
+                    acc[r] = __builtin_fmaf(qv.y, kv.y, acc[r]);
+                    acc[r] = __builtin_fmaf(qv.z, kv.z, acc[r]);
+                    acc[r] = __builtin_fmaf(qv.w, kv.w, acc[r]);
+                }
+            }
+        } else if (valid) {
+            /* a tree node's own rows: logical row r0 + lane >= pos0 at its ancestor's slot */
+            const int slot = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + (r0 + lane - pos0)];
+            const float4 *kv4 = (const float4 *)(kbase + (size_t)slot * hd);
+#pragma unroll 2
+            for (int d4 = 0; d4 < HD / 4; d4++) {
+                const float4 kv = kv4[d4];
+#pragma unroll
+                for (int r = 0; r < RW; r++) {
+                    const float4 qv = qv4[r * (HD / 4) + d4];
+                    acc[r] = __builtin_fmaf(qv.x, kv.x, acc[r]);
+                    acc[r] = __builtin_fmaf(qv.y, kv.y, acc[r]);
+                    acc[r] = __builtin_fmaf(qv.z, kv.z, acc[r]);
+                    acc[r] = __builtin_fmaf(qv.w, kv.w, acc[r]);
+                }
+            }
+        }
+        const size_t row0 = (size_t)t * a.H + g * grp + hb * RW;
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const float sv = valid ? fmul(scale, acc[r]) : -__builtin_huge_valf();
+            const bool anynan = __builtin_amdgcn_ballot_w64(sv != sv) != 0;
+            const float m = anynan ? __builtin_nanf("") : wave_max_f32(sv);
+            const float e = valid ? exp_glibc_f(fsub(sv, m), etab) : 0.0f;
+            const float l = ac_pairwise64(e);
+            es[wave][k][r][lane] = e;
+            if (lane == 0) {
+                a.pm[(row0 + r) * a.nc_ld + c] = m;
+                a.pl[(row0 + r) * a.nc_ld + c] = l;
+            }
+        }
+    }
+    HX_WAIT_VMCNT(0);                            /* this wave's V loads landed */
+    __builtin_amdgcn_s_waitcnt(0xC07F);          /* and its e stores */
+    __builtin_amdgcn_s_barrier();
+    /* value sums of this wave's items: lane = column */
+#pragma unroll 1
+    for (int k = 0; k < AC_IPW; k++) {
+        const int it = wave + k * AC_WAVES;
+        if (it >= nitems) break;
+        const int tl = it / ipt, hb = it % ipt, t = t0 + tl;
+        const int nk = min(pos0 + __builtin_amdgcn_readlane(dep_l, tl) + 1 - r0, AC_CH);
+        if (nk <= 0) continue;
+        const int jl = min(nk, kshared);
+        const size_t row0 = (size_t)t * a.H + g * grp + hb * RW;
+#pragma unroll 1
+        for (int cb = 0; cb < ND; cb++) {
+            const int d = 64 * cb + lane;
+            float acc[RW];
+#pragma unroll
+            for (int r = 0; r < RW; r++) acc[r] = 0.0f;
+            int j = 0;
+#pragma unroll 4
+            for (; j + 4 <= jl; j += 4) {
+                const float4 vv = *(const float4 *)&vq[(j >> 2) * VQ + 4 * d];
+#pragma unroll
+                for (int r = 0; r < RW; r++) {
+                    const float4 ev = *(const float4 *)&es[wave][k][r][j];
+                    acc[r] = __builtin_fmaf(ev.x, vv.x, acc[r]);
+                    acc[r] = __builtin_fmaf(ev.y, vv.y, acc[r]);
+                    acc[r] = __builtin_fmaf(ev.z, vv.z, acc[r]);
+                    acc[r] = __builtin_fmaf(ev.w, vv.w, acc[r]);
+                }
+            }
+            for (; j < jl; j++) {
+                const float vv = vq[(j >> 2) * VQ + 4 * d + (j & 3)];
+#pragma unroll
+                for (int r = 0; r < RW; r++) acc[r] = __builtin_fmaf(es[wave][k][r][j], vv, acc[r]);
+            }
+            for (; j < nk; j++) {
+                const int slot = pos0 + a.g.anc[(size_t)t * a.g.anc_ld + (r0 + j - pos0)];
+                const float vv = vbase[(size_t)slot * hd + d];
+#pragma unroll
+                for (int r = 0; r < RW; r++) acc[r] = __builtin_fmaf(es[wave][k][r][j], vv, acc[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < RW; r++) a.po[((row0 + r) * a.nc_ld + c) * HD + d] = acc[r];
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
+    constexpr int ND = HD / 64;
+    __shared__ unsigned long long etab[32];
+    exp_table_to_lds(etab);
+    __syncthreads();
+    const int idx = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (idx >= a.T * a.H * ND) return;
+    const int cb = idx % ND, row = idx / ND, t = row / a.H, h = row % a.H;
+    const int nr = *a.g.pos + a.g.depth[t] + 1, nc = (nr + AC_CH - 1) / AC_CH;
+    const float *pm = a.pm + (size_t)row * a.nc_ld, *pl = a.pl + (size_t)row * a.nc_ld;
+    const float *po = a.po + (size_t)row * a.nc_ld * HD + 64 * cb + lane;
+    /* M over the chunks, lane c % 64 holding chunk c (a maximum: any order) */
+    float mx = -__builtin_huge_valf();
+    bool nan = false;
+    for (int c = lane; c < nc; c += 64) {
+        const float v = pm[c];
+        nan |= v != v;
+        mx = fmaxf(mx, v);
+    }
+    const bool anynan = __builtin_amdgcn_ballot_w64(nan) != 0;
+    const float M = anynan ? __builtin_nanf("") : wave_max_f32(mx);
+    /* 64 chunks at a time: lane j computes w and holds l of chunk c0 + j; the folds over
+     * the chunks in order take them by readlane */
+    float L = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < nc; c0 += 64) {
+        const int c = c0 + lane, n = min(64, nc - c0);
+        const float w = c < nc ? exp_glibc_f(fsub(pm[c], M), etab) : 0.0f;
+        const float l = c < nc ? pl[c] : 0.0f;
+        const float *pc = po + (size_t)c0 * HD;
+        int j = 0;
+        for (; j + 4 <= n; j += 4) {
+            float ov[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) ov[u] = pc[(size_t)(j + u) * HD];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j + u));
+                L = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), j + u)), wj, L);
+                O = __builtin_fmaf(ov[u], wj, O);
+            }
+        }
+        for (; j < n; j++) {
+            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+            L = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), j)), wj, L);
+            O = __builtin_fmaf(pc[(size_t)j * HD], wj, O);
+        }
+    }
+    const float out = fdiv(O, L);
+    a.out[(size_t)t * a.H * HD + (size_t)h * HD + 64 * cb + lane] = out;
+    if (a.qo_on) quant_block_wave(out, a.qo, a.qo_hm ? h * a.T + t : t, a.qo_hm ? cb : h * ND + cb);
+}
+
 } // namespace
 
 namespace hxl {
@@ -771,6 +1043,25 @@ void attention_finish(const AttnArgs &a, hipStream_t st) {
 #undef HX_TV
     const int qpt = (grp + TV_SUM - 1) / TV_SUM;
     k_attn_values<<<a.T * qpt * a.Hkv * nd, TV_THREADS, 0, st>>>(a);
+}
+
+bool attention_chunked_ok(int hd, int grp) { return (hd == 64 || hd == 128) && grp >= 1 && grp * hd <= AC_QMAX && grp <= 32 * 4; }
+
+void attention_chunked(const AttnArgs &a, hipStream_t st) {
+    const int grp = a.H / a.Hkv, rw = grp % 4 == 0 ? 4 : grp % 2 == 0 ? 2 : 1, ipt = grp / rw;
+    const int ntb_max = std::max(1, std::min(AC_WAVES * AC_IPW / ipt, AC_QMAX / (grp * a.hd)));
+    const int nblk = (a.T + ntb_max - 1) / ntb_max, ntb = (a.T + nblk - 1) / nblk;
+    const int ncg = (a.g.nr_max + AC_CH - 1) / AC_CH;
+    const int grid = ncg * a.Hkv * nblk, nc_rows = a.T * a.H * (a.hd / 64);
+#define HX_AC(HD_, RW_) k_attn_chunk<HD_, RW_><<<grid, 64 * AC_WAVES, 0, st>>>(a, ntb, nblk, ncg)
+    if (a.hd == 128) {
+        if (rw == 4) HX_AC(128, 4); else if (rw == 2) HX_AC(128, 2); else HX_AC(128, 1);
+        k_attn_combine<128><<<(nc_rows + 3) / 4, 256, 0, st>>>(a);
+    } else {
+        if (rw == 4) HX_AC(64, 4); else if (rw == 2) HX_AC(64, 2); else HX_AC(64, 1);
+        k_attn_combine<64><<<(nc_rows + 3) / 4, 256, 0, st>>>(a);
+    }
+#undef HX_AC
 }
 
 void attention(const AttnArgs &a, hipStream_t st) {

@@ -140,6 +140,7 @@ def chain_uniforms(stream, k: int) -> np.ndarray:
 
 
 POLICIES = {"lru": 0, "lfu": 1}
+ATTN_MODES = {"canonical": 0, "chunked": 1}
 PREFETCH = {"off": 0, "none": 0, "next": 1, "shared": 2}
 ISAS = {"auto": 0, "scalar": 1, "avx2": 2, "avx512": 3}
 
@@ -170,6 +171,8 @@ _PROTOS = {
                                          POINTER(c_double), POINTER(c_double), _I32P, POINTER(c_int), _I32P]),
     "hearth_gpu_probs": (c_int, [POINTER(c_float), c_int, c_int, _I32P, _I32P, POINTER(HearthSampler),
                                  POINTER(c_double)]),
+    "hearth_gpu_set_attn_mode": (c_int, [c_void_p, c_int]),
+    "hearth_gpu_get_attn_mode": (c_int, [c_void_p]),
     "hearth_gpu_set_profiling": (c_int, [c_void_p, c_int]),
     "hearth_gpu_get_kstats": (c_int, [c_void_p, POINTER(KStats)]),
     "hearth_gpu_reset_kstats": (None, [c_void_p]),
@@ -240,8 +243,10 @@ class Engine:
 
     def __init__(self, model_path, *, cache_gb=8.0, threads=0, io_threads=0, direct_io=True, policy="lfu",
                  prefetch="shared", prefetch_extra=0, usage_in=None, usage_out=None, pin_fraction=0.0,
-                 warm_start=False, max_seq=0, max_batch=0, isa="auto", mirrors=(), verbose=0, lib=None):
-        """lib: path of another library implementing hearth.h (default: libhearth.so)."""
+                 warm_start=False, max_seq=0, max_batch=0, isa="auto", mirrors=(), verbose=0, lib=None, attn=None):
+        """lib: path of another library implementing hearth.h (default: libhearth.so).
+        attn: None (the library's default), "canonical" or "chunked": the attention order of
+        the GQA layers (hearth_gpu_set_attn_mode)."""
         self._h = None
         self._lock = threading.Lock()
         if model_path is None:
@@ -292,6 +297,12 @@ class Engine:
                          list(getattr(mi, n)) if n == "eos_ids" else getattr(mi, n)) for n, _ in HearthModelInfo._fields_}
         self.info["eos_ids"] = self.info["eos_ids"][:max(0, min(8, int(self.info["n_eos"])))]
         self._vocab = int(self.info["vocab_size"])
+        if attn is not None:
+            try:
+                self.attn_mode = attn
+            except Exception:
+                self.close()
+                raise
 
     # ---- lifecycle ----
     def close(self) -> None:
@@ -491,6 +502,22 @@ class Engine:
     def reset_stats(self) -> None:
         with self._lock:
             self._api.reset_stats(self._handle())
+
+    @property
+    def attn_mode(self) -> str:
+        """The attention order of the GQA layers: "canonical" (the reference's, bit-exact to
+        it; the default) or "chunked" (64-row chunks, opt-in); see include/hearth_gpu.h."""
+        with self._lock:
+            m = self._api.need("gpu_get_attn_mode")(self._handle())
+        return {v: k for k, v in ATTN_MODES.items()}[m]
+
+    @attn_mode.setter
+    def attn_mode(self, mode) -> None:
+        m = _enum(mode, ATTN_MODES, "attn")
+        with self._lock:
+            rc = self._api.need("gpu_set_attn_mode")(self._handle(), m)
+        if rc < 0:
+            raise ValueError(f"attention order {mode!r} is not available for this model")
 
     def set_profiling(self, level) -> None:
         """0/False: off; 1: events around the grouped expert launches; 2/True: around every

@@ -111,6 +111,29 @@ HEARTH_API int hearth_gpu_accept_sample(const float *rows, int n, int V, const i
 HEARTH_API int hearth_gpu_probs(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
                                 const hearth_sampler *s, double *p_out);
 
+/* Attention order of the engine's GQA layers. No counterpart in the reference, whose
+ * ADR-0003-canonical-numerics.md:44-45 lets a GPU backend document its tolerance:
+ *   HEARTH_GPU_ATTN_CANONICAL  the reference's order (engine/src/model.c:519-589): dot16
+ *                              scores, one softmax over the row list, sequential value
+ *                              sums; logits bit-exact to the reference engine.
+ *   HEARTH_GPU_ATTN_CHUNKED    the row list in chunks of 64 rows, scores and value sums by
+ *                              fused multiply-adds, one partial softmax per chunk, chunks
+ *                              folded in order (oracle/hx_oracle.h lists the exact steps).
+ *                              Each head's output is within about 1e-6 of the canonical one,
+ *                              but models that quantize activations to int8 amplify that:
+ *                              it is an opt-in order with a measured, not a guaranteed,
+ *                              agreement with the reference.
+ * Either order depends on a token's row list only, so batch == sequential and tree ==
+ * chain hold bit for bit in both. Default: canonical; HEARTH_GPU_ATTN=chunked at open
+ * selects the chunked order where the shape allows it (GQA with head_dim 64 or 128).
+ * MLA attention is canonical in both modes. set returns -1 for an unknown mode or a
+ * model the chunked order does not cover; call it between calls that use the engine.
+ * get returns the order in use. */
+#define HEARTH_GPU_ATTN_CANONICAL 0
+#define HEARTH_GPU_ATTN_CHUNKED 1
+HEARTH_API int hearth_gpu_set_attn_mode(hearth_engine *e, int mode);
+HEARTH_API int hearth_gpu_get_attn_mode(hearth_engine *e);
+
 /* GPU time per kernel class, accumulated while profiling is on (HIP event pairs on the
  * engine's stream; see hearth_gpu_set_profiling for the levels). */
 typedef struct hearth_gpu_kstats {

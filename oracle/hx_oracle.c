@@ -233,6 +233,10 @@ float ho_dot16(const float *a, const float *b, int64_t n) {
     return L[0];
 }
 
+static int g_attn_mode = HO_ATTN_CANONICAL;
+void ho_set_attn_mode(int mode) { g_attn_mode = mode == HO_ATTN_CHUNKED ? mode : HO_ATTN_CANONICAL; }
+int ho_get_attn_mode(void) { return g_attn_mode; }
+
 static void rmsnorm(float *y, const float *x, const float *w, int64_t n, float eps) {
     const float ms = ho_dot16(x, x, n) / (float)n;
     const float r = 1.0f / sqrtf(ms + eps);
@@ -602,6 +606,8 @@ struct ho_model {
     uint16_t *replay;     /* route replay [rows][n_moe][K], or NULL */
     int64_t replay_rows;
     int cur_pos;          /* position of the token being evaluated (replay row) */
+    float *margins;       /* ho_set_margins: routing margins [tokens][n_moe] of the next eval */
+    float *cur_margin;    /* where route() writes the margin of the current token and layer */
 };
 
 /* appends n floats to <dump_dir>/l<layer>_<name>.bin (debug comparisons) */
@@ -915,10 +921,74 @@ typedef struct {
     int nr, kd;
 } gqa_ctx;
 
+/* the larger of a and b, NaN if either is NaN */
+static float nanmax(float a, float b) { return a != a || b != b ? a + b : (b > a ? b : a); }
+
+/* HO_ATTN_CHUNKED for one head (the steps ho_set_attn_mode lists); scratch: sc [nr],
+ * oc [n], mc [nc] */
+static void chunked_head(const float *q, const int *rows, int nr, const float *K, const float *Vc, size_t stride,
+                         int n, float scale, float *sc, float *oc, float *mc, float *out) {
+    const int CH = HO_ATTN_CHUNK, nc = (nr + CH - 1) / CH;
+    for (int i = 0; i < nr; i++) {
+        const float *k = K + (size_t)rows[i] * stride;
+        float acc = 0.0f;
+        for (int d = 0; d < n; d++) acc = fmaf(q[d], k[d], acc);
+        sc[i] = scale * acc;
+    }
+    float M = 0.0f;
+    for (int c = 0; c < nc; c++) {
+        const int i0 = c * CH, i1 = i0 + CH < nr ? i0 + CH : nr;
+        float m = sc[i0];
+        for (int i = i0 + 1; i < i1; i++) m = nanmax(m, sc[i]);
+        mc[c] = m;
+        M = c ? nanmax(M, m) : m;
+    }
+    float L = 0.0f;
+    for (int d = 0; d < n; d++) out[d] = 0.0f;
+    for (int c = 0; c < nc; c++) {
+        const int i0 = c * CH, i1 = i0 + CH < nr ? i0 + CH : nr;
+        float a[HO_ATTN_CHUNK];
+        for (int j = 0; j < CH; j++) a[j] = i0 + j < i1 ? ho_expf(sc[i0 + j] - mc[c]) : 0.0f;
+        for (int d = 0; d < n; d++) oc[d] = 0.0f;
+        for (int i = i0; i < i1; i++) {
+            const float *v = Vc + (size_t)rows[i] * stride;
+            for (int d = 0; d < n; d++) oc[d] = fmaf(a[i - i0], v[d], oc[d]);
+        }
+        for (int w = 1; w < CH; w *= 2)
+            for (int k = 0; k < CH; k += 2 * w) a[k] = a[k] + a[k + w];
+        const float wc = ho_expf(mc[c] - M);
+        L = fmaf(a[0], wc, L);
+        for (int d = 0; d < n; d++) out[d] = fmaf(oc[d], wc, out[d]);
+    }
+    for (int d = 0; d < n; d++) out[d] = out[d] / L;
+}
+
+int ho_attn_head(const float *q, const float *K, const float *V, size_t stride, const int32_t *rows, int nr, int n,
+                 float scale, float *out) {
+    if (!q || !K || !V || !rows || !out || nr < 1 || n < 1) return -1;
+    float *sc = malloc(sizeof(float) * ((size_t)nr + (size_t)n + (size_t)nr));
+    if (!sc) return -5;
+    if (g_attn_mode == HO_ATTN_CHUNKED) {
+        chunked_head(q, (const int *)rows, nr, K, V, stride, n, scale, sc, sc + nr, sc + nr + n, out);
+    } else {
+        for (int i = 0; i < nr; i++) sc[i] = scale * ho_dot16(q, K + (size_t)rows[i] * stride, n);
+        softmax(sc, nr);
+        value_sum(sc, (const int *)rows, nr, V, stride, n, out);
+    }
+    free(sc);
+    return 0;
+}
+
 static void gqa_head(void *p, int h, float *sc) {
     const gqa_ctx *a = (const gqa_ctx *)p;
     const cfg *c = a->c;
     const int hd = c->head_dim, g = h / (c->n_heads / c->n_kv_heads);
+    if (g_attn_mode == HO_ATTN_CHUNKED) {
+        float *oc = sc + a->nr, *mc = oc + hd;
+        chunked_head(a->q + h * hd, a->rows, a->nr, a->K + g * hd, a->Vc + g * hd, (size_t)a->kd, hd, c->attn_scale,
+                     sc, oc, mc, a->o + h * hd);
+        return;
+    }
     for (int i = 0; i < a->nr; i++)
         sc[i] = c->attn_scale * ho_dot16(a->q + h * hd, a->K + (size_t)a->rows[i] * a->kd + g * hd, hd);
     softmax(sc, a->nr);
@@ -958,7 +1028,7 @@ static void attn_gqa(ho_model *m, int l, const float *x, int pos, int slot, cons
     memcpy(Vc + (size_t)slot * kd, v, sizeof(float) * kd);
     dump(m, "q", l, q, qd, 4);
     gqa_ctx ctx = {c, q, K, Vc, o, rows, nr, kd};
-    par_heads(H, m->nthreads, gqa_head, &ctx, (size_t)nr);
+    par_heads(H, m->nthreads, gqa_head, &ctx, (size_t)nr + hd + (size_t)(nr + HO_ATTN_CHUNK - 1) / HO_ATTN_CHUNK);
     dump(m, "att", l, o, qd, 4);
     lin(m, l, "attn_o", o, out);
     free(q); free(k); free(v); free(o);
@@ -1117,6 +1187,28 @@ static void route(ho_model *m, int l, const float *x, int *ids, float *w) {
         ids[j] = best;
         taken[best] = 1;
     }
+    if (m->cur_margin) {
+        /* the smallest gap between consecutive selection scores among the top K + 1, relative
+         * to the larger one for softmax scoring, absolute for sigmoid scoring */
+        const int n = K + 1 < E ? K + 1 : E;
+        float prev = sel[ids[0]], g = 1e30f;
+        for (int j = 1; j < n; j++) {
+            float v;
+            if (j < K) {
+                v = sel[ids[j]];
+            } else {
+                int best = -1;
+                for (int e = 0; e < E; e++)
+                    if (!taken[e] && (best < 0 || ranks_before(sel[e], e, sel[best], best))) best = e;
+                v = sel[best];
+            }
+            const double gap = (double)prev - (double)v;
+            const double r = c->score_fn == 0 ? gap / (prev > 1e-30f ? prev : 1e-30f) : gap;
+            if (r < g) g = (float)r;
+            prev = v;
+        }
+        *m->cur_margin = g;
+    }
 weights:
     for (int j = 0; j < K; j++) w[j] = score[ids[j]];
     if (c->norm_topk) {
@@ -1157,7 +1249,8 @@ static void moe(ho_model *m, int l, const float *x, float *out, int32_t *route_o
     free(y);
 }
 
-static void forward_token(ho_model *m, int tok, int pos, int slot, const int *rows, int nr, float *logits, int32_t *routes) {
+static void forward_token(ho_model *m, int tok, int pos, int slot, const int *rows, int nr, float *logits, int32_t *routes,
+                          float *margins) {
     m->cur_pos = pos;
     const cfg *c = &m->c;
     const int D = c->d_model;
@@ -1173,8 +1266,10 @@ static void forward_token(ho_model *m, int tok, int pos, int slot, const int *ro
         rmsnorm(x, h, vec(m, l, "ffn_norm"), D, c->eps);
         dump(m, "h_mid", l, h, D, 4);
         dump(m, "x_ffn", l, x, D, 4);
+        m->cur_margin = margins && c->layer_kind[l] ? margins + m->moe_ord[l] : NULL;
         if (c->layer_kind[l]) moe(m, l, x, a, routes ? routes + (size_t)m->moe_ord[l] * c->top_k : NULL);
         else ffn(m, l, "ffn_gate", "ffn_up", "ffn_down", x, a);
+        m->cur_margin = NULL;
         for (int i = 0; i < D; i++) h[i] = h[i] + c->resid_scale * a[i];
         dump(m, "h", l, h, D, 4);
     }
@@ -1188,6 +1283,8 @@ static void forward_token(ho_model *m, int tok, int pos, int slot, const int *ro
     free(a);
 }
 
+void ho_set_margins(ho_model *m, float *buf) { m->margins = buf; }
+
 int ho_eval(ho_model *m, const int32_t *tokens, int n, float *logits, int32_t *routes) {
     const cfg *c = &m->c;
     if (n < 0 || !tokens) return -1;
@@ -1199,8 +1296,10 @@ int ho_eval(ho_model *m, const int32_t *tokens, int n, float *logits, int32_t *r
     for (int i = 0; i < n; i++) {
         const int p = m->pos + i;
         forward_token(m, tokens[i], p, p, rows, p + 1, logits ? logits + (size_t)i * c->vocab : NULL,
-                      routes ? routes + (size_t)i * c->n_moe * c->top_k : NULL);
+                      routes ? routes + (size_t)i * c->n_moe * c->top_k : NULL,
+                      m->margins ? m->margins + (size_t)i * c->n_moe : NULL);
     }
+    m->margins = NULL;
     m->pos += n;
     free(rows);
     return 0;
@@ -1224,8 +1323,10 @@ int ho_eval_tree(ho_model *m, const int32_t *tokens, const int32_t *parent, int 
         for (int v = i, j = d; v >= 0; v = parent[v], j--) rows[pos0 + j] = pos0 + v;
         forward_token(m, tokens[i], pos0 + d, pos0 + i, rows, pos0 + d + 1,
                       logits ? logits + (size_t)i * c->vocab : NULL,
-                      routes ? routes + (size_t)i * c->n_moe * c->top_k : NULL);
+                      routes ? routes + (size_t)i * c->n_moe * c->top_k : NULL,
+                      m->margins ? m->margins + (size_t)i * c->n_moe : NULL);
     }
+    m->margins = NULL;
     free(depth);
     free(rows);
     return 0;

@@ -38,6 +38,16 @@
  *                    libm expf on all 2^32 inputs. The HIP kernels use the same
  *                    definition; with this mode the GPU must match the restatement bit
  *                    for bit, and so the reference engine.
+ * Attention mode (ho_set_attn_mode):
+ *   HO_ATTN_CANONICAL  the reference's order (engine/src/model.c:519-589): dot16 scores,
+ *                      one softmax over the whole row list, sequential value sums.
+ *   HO_ATTN_CHUNKED    the GPU engine's default order for GQA attention: the row list in
+ *                      chunks of HO_ATTN_CHUNK rows, one partial softmax and value sum per
+ *                      chunk, combined in chunk order (ho_set_attn_mode documents the exact
+ *                      steps). Within the north star's tolerance of the reference, not
+ *                      bit-exact to it; no reference counterpart (the reference allows a GPU
+ *                      backend to document its tolerance, ADR-0003-canonical-numerics.md:44-45).
+ *                      MLA attention keeps the canonical order in both modes.
  * Parity status: every function above is pinned (pinned FNV hashes of the reference's
  * test_quant.c, bit-exact comparison with the reference engine built from source on
  * whole forward passes, closed forms for acceptance); see tests/ for each check.
@@ -54,6 +64,7 @@ extern "C" {
 
 enum { HO_F32 = 0, HO_F16 = 1, HO_BF16 = 2, HO_Q8 = 3, HO_Q4 = 4, HO_I32 = 5, HO_U8 = 6 };
 enum { HO_EXP_LIBM = 0, HO_EXP_PORTABLE = 1, HO_EXP_GLIBC = 2 };
+enum { HO_ATTN_CANONICAL = 0, HO_ATTN_CHUNKED = 1, HO_ATTN_CHUNK = 64 };
 
 /* ---- formats and kernels -------------------------------------------------- */
 float    ho_f16_to_f32(uint16_t h);
@@ -77,6 +88,28 @@ float ho_exp_glibc_f(float x);
 uint64_t ho_exp_glibc_mismatches(uint64_t lo, uint64_t hi, int nthreads);
 double ho_exp_port_d(double x);
 float ho_dot16(const float *a, const float *b, int64_t n);
+/* Attention order of GQA layers (default HO_ATTN_CANONICAL). HO_ATTN_CHUNKED, for one
+ * head with query q and the token's row list rows[0..nr) (logical row i reads K/V cache
+ * slot rows[i]); chunk c holds logical rows 64c .. min(64c + 64, nr) - 1:
+ *   s_i = scale * dotf(q, k_rows[i]), dotf = fmaf(a[d], b[d], acc) for d = 0 .. hd-1
+ *         from acc = 0.0f
+ *   m_c = max of s_i over the chunk (NaN if one of them is NaN)
+ *   e_i = expf(s_i - m_c)                                  (ho_expf, the exp mode)
+ *   l_c = pairwise sum of the chunk's 64 positions (e_i, 0.0f past row nr - 1): for
+ *         w = 1, 2, 4, 8, 16, 32: a[k] = a[k] + a[k + w] for k = 0, 2w, 4w ..; l_c = a[0]
+ *   o_c[d] = fmaf(e_i, v_rows[i][d], o) over the chunk's rows in order, from 0.0f
+ *   M = max of m_c over the chunks; w_c = expf(m_c - M)
+ *   L = fmaf(l_c, w_c, L) over c in order from 0.0f; O[d] the same with o_c[d]
+ *   out[d] = O[d] / L
+ * Every step depends on the row list only: batch == sequential and tree == chain hold
+ * bit for bit in either mode. */
+void  ho_set_attn_mode(int mode);
+int   ho_get_attn_mode(void);
+/* One head's attention in the current mode: query q [n], K and V rows at K + rows[i] *
+ * stride and V + rows[i] * stride (n floats each) for i < nr; out [n]. The GQA layers'
+ * per-head step, exposed for tests. Returns 0, -1 for bad arguments. */
+int   ho_attn_head(const float *q, const float *K, const float *V, size_t stride, const int32_t *rows, int nr, int n,
+                   float scale, float *out);
 float ho_sum16(const float *a, int64_t n);
 
 /* ---- model ---------------------------------------------------------------- */
@@ -92,6 +125,12 @@ int       ho_rewind(ho_model *m, int pos);
 /* Chain evaluation at positions pos..pos+n-1 (pos += n). logits [n][V] or NULL;
  * routes [n][n_moe][K] or NULL. Returns 0, or < 0 like hearth_eval. */
 int       ho_eval(ho_model *m, const int32_t *tokens, int n, float *logits, int32_t *routes);
+/* The next ho_eval / ho_eval_tree writes, for token i and MoE layer j, the routing margin
+ * to buf[i * n_moe + j]: the smallest gap between consecutive selection scores among the
+ * top K + 1, relative to the larger score for softmax scoring and absolute for sigmoid
+ * scoring (the quantities the reference's synthetic models keep clear, python/hearth/
+ * synth.py:171-186). Test instrumentation; buf must hold n * n_moe floats. */
+void      ho_set_margins(ho_model *m, float *buf);
 /* Tree evaluation: parent[0] = -1, parent[i] < i. Node i runs at pos + depth(i) and its
  * K/V go to slot pos + i. pos is left unchanged (ho_commit_path advances it). */
 int       ho_eval_tree(ho_model *m, const int32_t *tokens, const int32_t *parent, int n,

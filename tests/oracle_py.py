@@ -16,6 +16,7 @@ ORACLE = ROOT / "oracle" / "liboracle.so"
 REF_LIB = ROOT / "oracle" / "_ref" / "libhearth_ref.so"
 
 EXP_LIBM, EXP_PORTABLE, EXP_GLIBC = 0, 1, 2
+ATTN_CANONICAL, ATTN_CHUNKED = 0, 1
 _I32P, _FP, _DP = POINTER(c_int32), POINTER(c_float), POINTER(c_double)
 _lib = None
 
@@ -47,6 +48,9 @@ def lib():
         L.ho_act_quant.argtypes = [_FP, c_int64, c_void_p]
         L.ho_matmul.argtypes = [c_int, c_void_p, c_int64, c_int64, _FP, c_int, _FP]
         L.ho_set_exp_mode.argtypes = [c_int]
+        L.ho_set_attn_mode.argtypes = [c_int]
+        L.ho_set_margins.argtypes = [c_void_p, _FP]
+        L.ho_attn_head.argtypes = [_FP, _FP, _FP, c_size_t, _I32P, c_int, c_int, c_float, _FP]
         L.ho_expf.restype = c_float
         L.ho_expf.argtypes = [c_float]
         L.ho_exp_port_f.restype = c_float
@@ -92,14 +96,35 @@ def set_exp_mode(mode: int) -> None:
     lib().ho_set_exp_mode(mode)
 
 
-def gpu_numerics() -> None:
-    """the oracle mode the GPU build matches bit for bit"""
+def set_attn_mode(mode: int) -> None:
+    lib().ho_set_attn_mode(mode)
+
+
+def attn_head(q, K, V, rows, scale: float) -> np.ndarray:
+    """ho_attn_head in the current modes: q [n], K and V [R][n] float32, rows [nr]"""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    K = np.ascontiguousarray(K, dtype=np.float32)
+    V = np.ascontiguousarray(V, dtype=np.float32)
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    out = np.zeros(q.size, dtype=np.float32)
+    rc = lib().ho_attn_head(q.ctypes.data_as(_FP), K.ctypes.data_as(_FP), V.ctypes.data_as(_FP), K.shape[1],
+                            rows.ctypes.data_as(_I32P), rows.size, q.size, scale, out.ctypes.data_as(_FP))
+    assert rc == 0, rc
+    return out
+
+
+def gpu_numerics(attn: int = ATTN_CANONICAL) -> None:
+    """the oracle mode the GPU build matches bit for bit: its exp, and the attention order
+    (the engine's default, canonical, unless given)"""
     set_exp_mode(EXP_GLIBC)
+    set_attn_mode(attn)
 
 
 def reference_numerics() -> None:
-    """the oracle mode the reference engine matches bit for bit (the platform libm)"""
+    """the oracle mode the reference engine matches bit for bit (the platform libm, the
+    canonical attention order)"""
     set_exp_mode(EXP_LIBM)
+    set_attn_mode(ATTN_CANONICAL)
 
 
 def quantize(dtype: int, x) -> bytes:
@@ -149,6 +174,14 @@ class Model:
 
     def rewind(self, pos: int) -> None:
         assert lib().ho_rewind(self.h, pos) == 0
+
+    def eval_margins(self, tokens):
+        """logits, routes and the routing margins [n][n_moe] (ho_set_margins) of a chain eval"""
+        t = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+        mg = np.empty((t.size, max(self.n_moe, 1)), dtype=np.float32)
+        lib().ho_set_margins(self.h, mg.ctypes.data_as(_FP))
+        lg, rt = self.eval(t, routes=True)
+        return lg, rt, mg
 
     def eval(self, tokens, routes: bool = False, logits: bool = True):
         """logits [n][V] (None with logits=False: the head is skipped), and routes

@@ -227,3 +227,29 @@ def test_prefill_chunk_160(model):
     lo = m.eval(toks[-1:])[0]
     _assert_same(kg, m.kv_export(n), "KV rows of the prefill chunk")
     _assert_same(lg, lo, "logits of the chunk's last token")
+
+
+@pytest.mark.parametrize("what", ["chain", "tree"])
+def test_chunked_order_equals_oracle(prefilled, model, what):
+    """The chunked attention order (opt-in) from the same contexts: the k=8 chain at 4095
+    and the 4x4x4 tree at 2047, bit for bit against the oracle's chunked restatement."""
+    eng, prompt, snap = prefilled
+    O.gpu_numerics(O.ATTN_CHUNKED)
+    eng.attn_mode = "chunked"
+    try:
+        if what == "chain":
+            n0, parent = CTX, None
+            toks = np.concatenate([[prompt[-1]], container.uniform_ints(77, 8, SHAPE.vocab)]).astype(np.int32)
+        else:
+            n0, parent = 2047, _tree_4x4x4()
+            toks = container.uniform_ints(99, len(parent), SHAPE.vocab).astype(np.int32)
+        s0 = snap if n0 == CTX else _cut(snap, CTX, n0)
+        eng.kv_import(s0, n0)
+        lg = eng.eval(toks, all_logits=True) if parent is None else eng.verify_tree(toks, parent)
+        m = O.Model(model, cap=n0 + len(toks) + 8, threads=THREADS)
+        m.kv_import(s0, n0)
+        lo = m.eval(toks) if parent is None else m.eval_tree(toks, parent)
+        _assert_same(lg, lo, f"chunked {what} logits")
+    finally:
+        eng.attn_mode = "canonical"
+        O.gpu_numerics()
