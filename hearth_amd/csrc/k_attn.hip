@@ -215,6 +215,85 @@ __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
     }
 }
 
+/* The same scores for a chain of at most ST_TMAX tokens at a large head_dim (the MLA
+ * latent, 512), where every token reads row v from slot v: one workgroup per 64 rows and
+ * block of up to ST_HB heads, for every token. Thread (row, j) loads its row's K elements
+ * j + 16 i once and runs through all (token, 8-head) blocks of q, staged transposed in
+ * LDS two at a time (one barrier per block), so the K rows are read once per layer
+ * instead of once per token. Each score is the same sequence of operations as in
+ * k_attn_scores16. (At head_dim 128 the per-token kernel is faster: it has nine times
+ * the workgroups to hide its latencies with; measured 16.8 against 24.6 µs.) */
+constexpr int ST_HB = 32;
+constexpr int ST_TMAX = 64;
+
+template <int HI>
+__global__ __launch_bounds__(1024) void k_attn_scores16t(AttnArgs a, int nhb) {
+    constexpr int QS = HI / 4 + 1;
+    __shared__ float4 qT[2][8][16][QS];
+    __shared__ int nr_s[ST_TMAX];
+    const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd, T = a.T;
+    int b = blockIdx.x;
+    const int hb = b % nhb;
+    b /= nhb;
+    const int g = b % Hkv, c = b / Hkv;
+    const int pos0 = *a.g.pos, nrmax = pos0 + T;
+    const int v0 = c * 64;
+    if (v0 >= nrmax) return;   /* uniform: past every token's rows */
+    const int tid = threadIdx.x, j = tid & 15, v = v0 + (tid >> 4);
+    if (tid < T) nr_s[tid] = pos0 + a.g.depth[tid] + 1;
+    float kv[HI];
+    {
+        const float *kr = a.kc + ((size_t)g * a.cap + (v < nrmax ? v : nrmax - 1)) * hd + j;
+#pragma unroll
+        for (int i = 0; i < HI; i++) kv[i] = kr[16 * i];
+    }
+    const int h_lo = hb * ST_HB, h_hi = min(grp, h_lo + ST_HB), nh8 = (h_hi - h_lo + 7) / 8, nblk = T * nh8;
+    auto stage = [&](int blk, int buf) {
+        const int t = blk / nh8, h0 = h_lo + (blk % nh8) * 8;
+        const float *qb = a.q + ((size_t)t * a.H + (size_t)g * grp + h0) * hd;
+        float *qf = (float *)qT[buf];
+        for (int x = tid; x < 8 * hd; x += 1024) {
+            const int hh = x / hd, e = x % hd;
+            qf[(hh * 16 + (e & 15)) * (4 * QS) + (e >> 4)] = h0 + hh < h_hi ? qb[(size_t)hh * hd + e] : 0.0f;
+        }
+    };
+    stage(0, 0);
+    for (int blk = 0; blk < nblk; blk++) {
+        __syncthreads();   /* block blk staged; block blk - 1's buffer free */
+        if (blk + 1 < nblk) stage(blk + 1, (blk + 1) & 1);
+        const int t = blk / nh8, h0 = h_lo + (blk % nh8) * 8, buf = blk & 1;
+        float acc[8];
+#pragma unroll
+        for (int hh = 0; hh < 8; hh++) acc[hh] = 0.0f;
+#pragma unroll
+        for (int i4 = 0; i4 < HI / 4; i4++) {
+#pragma unroll
+            for (int hh = 0; hh < 8; hh++) {
+                const float4 q4 = qT[buf][hh][j][i4];
+                acc[hh] = fadd(acc[hh], fmul(q4.x, kv[4 * i4]));
+                acc[hh] = fadd(acc[hh], fmul(q4.y, kv[4 * i4 + 1]));
+                acc[hh] = fadd(acc[hh], fmul(q4.z, kv[4 * i4 + 2]));
+                acc[hh] = fadd(acc[hh], fmul(q4.w, kv[4 * i4 + 3]));
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < 8; hh++) {
+#define HX_DPP_ADD(cc) acc[hh] = fadd(acc[hh], __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc[hh]), cc, 0xF, 0xF, true)))
+            HX_DPP_ADD(0x108);
+            HX_DPP_ADD(0x104);
+            HX_DPP_ADD(0x102);
+            HX_DPP_ADD(0x101);
+#undef HX_DPP_ADD
+        }
+        if (j == 0 && v < nr_s[t]) {
+            float *Sb = a.S + ((size_t)t * a.H + (size_t)g * grp + h0) * a.ldS + v;
+#pragma unroll
+            for (int hh = 0; hh < 8; hh++)
+                if (h0 + hh < h_hi) Sb[(size_t)hh * a.ldS] = fmul(a.scale, canon(acc[hh]));
+        }
+    }
+}
+
 __device__ __forceinline__ float sum16_lds(const float *es, int n, int lane16, float L) {
     /* lane lane16 of 16: continues the sequential sum L with es[lane16], es[lane16 + 16],
      * ..., the next 16 operands read while the current 16 are added */
@@ -1001,6 +1080,13 @@ namespace hxl {
 
 void attention_scores(const AttnArgs &a, hipStream_t st) {
     const int max_nr = a.g.nr_max;
+    if (a.g.chain && a.T <= ST_TMAX && a.hd == 512) {
+        const int nhb = (a.H / a.Hkv + ST_HB - 1) / ST_HB, grid = ((max_nr + 63) / 64) * a.Hkv * nhb;
+        if (grid >= 128) {
+            k_attn_scores16t<32><<<grid, 1024, 0, st>>>(a, nhb);
+            return;
+        }
+    }
     if (a.hd % 64 == 0 && a.hd <= 512) {
 #define HX_S16(HI_)                                                                         \
         {                                                                                   \
