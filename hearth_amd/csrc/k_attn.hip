@@ -878,9 +878,9 @@ __global__ __launch_bounds__(64 * AC_WAVES) void k_attn_chunk(AttnArgs a, int nt
     const float *kbase = a.kc + (size_t)g * a.cap * hd, *vbase = a.vc + (size_t)g * a.cap * hd;
     exp_table_to_lds(etab);
     {
+        const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc((void *)a.q, 0, a.T * a.H * hd * 4, 0x00020000);
         const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void *)kbase, 0, a.cap * hd * 4, 0x00020000);
         const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vbase, 0, a.cap * hd * 4, 0x00020000);
-        const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc((void *)a.q, 0, a.T * a.H * hd * 4, 0x00020000);
         /* K: load f = k * 8 + wave is row f / ND, columns 64 (f % ND) .. + 63 */
 #pragma unroll
         for (int k = 0; k < NKW; k++) {
@@ -888,14 +888,14 @@ __global__ __launch_bounds__(64 * AC_WAVES) void k_attn_chunk(AttnArgs a, int nt
             __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void *)&ks[j * KLD + 64 * cb], 4,
                                                      ((r0 + j) * hd + 64 * cb + lane) * 4, 0, 0, 0);
         }
-        /* queries of the block: load f is (token, head, 64 columns) */
-        const int nq = nt * grp * ND;
-        for (int f = wave; f < nq; f += AC_WAVES) {
-            const int cb = f % ND, th = f / ND, tl = th / grp, hl = th % grp;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                qrs, (__attribute__((address_space(3))) void *)&qs[th * HD + 64 * cb], 4,
-                (((t0 + tl) * a.H + g * grp + hl) * hd + 64 * cb + lane) * 4, 0, 0, 0);
-        }
+        /* queries of the block: a token's grp heads are grp * hd contiguous floats; load u
+         * of token tl is its floats 64 u .. 64 u + 63 */
+        const int qrow = grp * ND;
+        for (int tl = 0; tl < nt; tl++)
+            for (int u = wave; u < qrow; u += AC_WAVES)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    qrs, (__attribute__((address_space(3))) void *)&qs[tl * grp * HD + 64 * u], 4,
+                    (((t0 + tl) * a.H + g * grp) * hd + 64 * u + lane) * 4, 0, 0, 0);
         /* V, transposed: load f is rows 4 qb .. 4 qb + 3 of columns 16 u .. 16 u + 15;
          * lane l takes row 4 qb + l % 4 of column 16 u + l / 4, so the 64 dwords land in
          * order in block qb: [column][4 rows] */
@@ -928,7 +928,7 @@ __global__ __launch_bounds__(64 * AC_WAVES) void k_attn_chunk(AttnArgs a, int nt
         const float4 *qv4 = (const float4 *)&qs[(tl * grp + hb * RW) * HD];
         if (valid && lane < kshared) {
             const float4 *kv4 = (const float4 *)&ks[lane * KLD];
-#pragma unroll 4
+#pragma unroll
             for (int d4 = 0; d4 < HD / 4; d4++) {
                 const float4 kv = kv4[d4];
 #pragma unroll
@@ -992,6 +992,22 @@ __global__ __launch_bounds__(64 * AC_WAVES) void k_attn_chunk(AttnArgs a, int nt
 #pragma unroll
             for (int r = 0; r < RW; r++) acc[r] = 0.0f;
             int j = 0;
+            if (jl == AC_CH) {
+                /* a whole chunk in LDS (all but the last one or two): straight-line code */
+#pragma unroll
+                for (int q = 0; q < AC_CH / 4; q++) {
+                    const float4 vv = *(const float4 *)&vq[q * VQ + 4 * d];
+#pragma unroll
+                    for (int r = 0; r < RW; r++) {
+                        const float4 ev = *(const float4 *)&es[wave][k][r][4 * q];
+                        acc[r] = __builtin_fmaf(ev.x, vv.x, acc[r]);
+                        acc[r] = __builtin_fmaf(ev.y, vv.y, acc[r]);
+                        acc[r] = __builtin_fmaf(ev.z, vv.z, acc[r]);
+                        acc[r] = __builtin_fmaf(ev.w, vv.w, acc[r]);
+                    }
+                }
+                j = AC_CH;
+            }
 #pragma unroll 4
             for (; j + 4 <= jl; j += 4) {
                 const float4 vv = *(const float4 *)&vq[(j >> 2) * VQ + 4 * d];
