@@ -554,6 +554,18 @@ __host__ __device__ inline size_t tk_lds_bytes(int nbp, int nm, int np, int rpw,
  * (4 or 8 row tiles) and quantize them (NUMERICS §2) in the epilogue */
 enum { TK_GATEUP = 0, TK_DOWN = 1, TK_GATEUP_Q = 2 };
 
+/* s_waitcnt vmcnt(n) for an n known once loops are unrolled (0 <= n <= 31) */
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+    switch (n) {
+#define HX_W(k) case k: HX_WAIT_VMCNT(k); break;
+    HX_W(0) HX_W(1) HX_W(2) HX_W(3) HX_W(4) HX_W(5) HX_W(6) HX_W(7) HX_W(8) HX_W(9) HX_W(10) HX_W(11)
+    HX_W(12) HX_W(13) HX_W(14) HX_W(15) HX_W(16) HX_W(17) HX_W(18) HX_W(19) HX_W(20) HX_W(21) HX_W(22)
+    HX_W(23) HX_W(24) HX_W(25) HX_W(26) HX_W(27) HX_W(28) HX_W(29) HX_W(30) HX_W(31)
+#undef HX_W
+    default: HX_WAIT_VMCNT(0);
+    }
+}
+
 template <int DT, int MODE>
 __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, int gmax, int n_slots) {
     constexpr bool DOWN = MODE == TK_DOWN, QF = MODE == TK_GATEUP_Q;
@@ -613,23 +625,27 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
     const int arow_q = !DOWN ? a.pair_tok[p0 + tq] : p0 + tq;
     const int arow_d = !DOWN ? a.pair_tok[p0 + tds] : p0 + tds;
     v4i w[NM][NP][NV];
-#pragma unroll
-    for (int k = 0; k < NP; k++) {
+    /* pairs [0, NA) go before the token rows, pairs [NA, NP) after them: the wait for the
+     * token rows then leaves the later weights in flight, and each pair's MFMAs start as
+     * soon as its own bytes are in (the compiler waits for each register as it is used) */
+    constexpr int NA = NP / 4 > 0 ? NP / 4 : 1;
+    auto load_pair = [&](int k, int dep) {
         const int gp = g0 + k < npair ? g0 + k : npair - 1;
 #pragma unroll
         for (int mi = 0; mi < NM; mi++) {
             const QMat &m = mat[mi];
             if (DT == 4) {
-                w[mi][k][0] = gload<v4i>(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
+                w[mi][k][0] = gload<v4i>(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16 + dep);
             } else {
-                const uint8_t *base = m.w + ((size_t)rt * nbp + 2 * gp) * 1024 + lane * 16;
+                const uint8_t *base = m.w + ((size_t)rt * nbp + 2 * gp) * 1024 + lane * 16 + dep;
                 w[mi][k][0] = gload<v4i>(base);
                 w[mi][k][NV - 1] = gload<v4i>(base + 1024);
             }
         }
-    }
-    /* one loop for every LDS-direct load: the wait for the token rows is then the only
-     * wait before them, and the weights stay in flight */
+    };
+#pragma unroll
+    for (int k = 0; k < NA; k++) load_pair(k, 0);
+    /* one loop for every LDS-direct load */
     {
         const int nxq = (nbp - wave + W - 1) / W, nit = nxq > NBK / 8 ? nxq : NBK / 8;
         int it = 0;
@@ -650,8 +666,15 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
             }
         } while (++it < nit);
     }
-    HX_WAIT_VMCNT(0);
+    /* the later weights: their addresses depend on an empty volatile asm after the
+     * LDS-direct loads, so no load of them can be issued before those */
+    int dep = 0;
+    asm volatile("" : "+v"(dep));
+#pragma unroll
+    for (int k = NA; k < NP; k++) load_pair(k, dep);
+    HX_WAIT_VMCNT(NM * (NP - NA) * NV);   /* the token rows, scales and pairs [0, NA) */
     __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);    /* no weight use moves above the barrier */
     const int q = lr >> 2;                /* register of this lane's pair: row 4 kg + q */
     const int col = 4 * g + (lr & 3);     /* token of this lane's pair */
     const int colc = col < n ? col : n - 1;   /* its staged row (columns past n are discarded) */
@@ -676,6 +699,8 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
     auto run_part = [&](bool fold) {
 #pragma unroll
         for (int k = 0; k < NP; k++) {
+            /* pair k's loads are in when at most the later pairs' are outstanding */
+            if (k >= NA) wait_vmcnt_le(NM * NV * (NP - 1 - k));
             v4i wv[2][NM];
 #pragma unroll
             for (int mi = 0; mi < NM; mi++) {
