@@ -168,6 +168,7 @@ struct hearth_engine {
     struct Captured {
         int T, chain, rows;
         bool logits;
+        bool loop;           /* a whole step of the greedy loop (loop_step), not a forward alone */
         hipGraph_t graph;
         hipGraphExec_t exec;
     };
@@ -201,6 +202,23 @@ struct hearth_engine {
     int64_t replay_rows = 0;
     /* tree verification: slots of the last uncommitted tree */
     int tree_n = 0;
+    /* the greedy speculative loop on the device (hearth_gpu_spec_greedy), allocated on
+     * first use: state block, committed sequence, stop ids, handled tokens, per-step
+     * records, the acceptance's draft ids and chain parents, its path, and the RoPE
+     * table of every position (rows [0, lp_rtab_rows) filled so far) */
+    int *lp_state = nullptr, *lp_hist = nullptr, *lp_stops = nullptr, *lp_out = nullptr, *lp_rec = nullptr,
+        *lp_cmp = nullptr, *lp_par = nullptr, *lp_path = nullptr;
+    float *lp_rtab = nullptr;
+    int lp_rtab_rows = 0;
+    int *h_lp = nullptr;                 /* pinned: the done flags of the steps in flight, then the state */
+    hipEvent_t lp_ev[2] = {nullptr, nullptr};
+    const int *route_live = nullptr;     /* RouteArgs.live of the forwards being launched */
+    void loop_prepare();
+    void loop_rope_table(int rows);
+    hxd::LoopArgs loop_args(int T);
+    void loop_step(int T);
+    void launch_loop_step(int T, int rows);
+    bool loop_ok() const { return !store && !replay_dev && !trace && !profiling && dump_dir.empty(); }
     /* sampled acceptance scratch, grown on demand */
     hxl::SampleScratch samp;
     /* HBM expert cache (null: every expert resident) */
@@ -272,6 +290,9 @@ struct hearth_engine {
         if (h_res) (void)hipHostFree(h_res);
         if (h_meta) (void)hipHostFree(h_meta);
         if (h_plog) (void)hipHostFree(h_plog);
+        if (h_lp) (void)hipHostFree(h_lp);
+        for (hipEvent_t &ev : lp_ev)
+            if (ev) (void)hipEventDestroy(ev);
         if (replay_dev) (void)hipFree(replay_dev);
         store.reset();
         if (st) (void)hipStreamDestroy(st);
@@ -933,6 +954,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 r.route_out = route_out; r.moe_ord = moe_ord[l]; r.n_moe = c.n_moe; r.stats = dstats;
                 r.table = w.experts; r.desc = slot_desc; r.n_slots = std::min(E, T * K);
                 r.replay = replay_dev; r.replay_rows = replay_rows; r.pos0 = pos; r.depth = depth;
+                r.live = route_live;
                 hxl::route(r, st);
             });
             if (store) {
@@ -1134,14 +1156,14 @@ void hearth_engine::run_forward(int T, bool want_logits) {
     const int rows = std::min(cap, (pos + T + 1023) / 1024 * 1024);
     Captured *cg = nullptr;
     for (Captured &g : graphs)
-        if (g.T == T && g.chain == geom_chain && g.rows == rows && g.logits == want_logits) cg = &g;
+        if (!g.loop && g.T == T && g.chain == geom_chain && g.rows == rows && g.logits == want_logits) cg = &g;
     if (!cg) {
         if (graphs.size() >= 32) {
             (void)hipGraphExecDestroy(graphs.front().exec);
             (void)hipGraphDestroy(graphs.front().graph);
             graphs.erase(graphs.begin());
         }
-        Captured g{T, geom_chain, rows, want_logits, nullptr, nullptr};
+        Captured g{T, geom_chain, rows, want_logits, false, nullptr, nullptr};
         ck(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         rows_bound = rows;
         try {
@@ -1153,6 +1175,111 @@ void hearth_engine::run_forward(int T, bool want_logits) {
             throw;
         }
         rows_bound = 0;
+        ck(hipStreamEndCapture(st, &g.graph));
+        const hipError_t e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(g.graph);
+            throw DeviceError{e};
+        }
+        graphs.push_back(g);
+        cg = &graphs.back();
+    }
+    ck(hipGraphLaunch(cg->exec, st));
+}
+
+/* ---------------------------------------------------------------- greedy loop on the device */
+
+void hearth_engine::loop_prepare() {
+    if (lp_state) return;
+    lp_hist = dnew<int>((size_t)cap + B + 2);
+    lp_stops = dnew<int>(hxd::LOOP_STOPS_MAX);
+    lp_out = dnew<int>((size_t)HEARTH_GPU_SPEC_MAX_STEPS * B);
+    lp_rec = dnew<int>((size_t)HEARTH_GPU_SPEC_MAX_STEPS * 3);
+    lp_cmp = dnew<int>(B);
+    lp_par = dnew<int>(B);
+    lp_path = dnew<int>(B);
+    if (rope_dim) lp_rtab = dnew<float>((size_t)cap * rope_dim);
+    if (!h_lp) ck(hipHostMalloc((void **)&h_lp, sizeof(int) * hxd::LS_FIELDS, hipHostMallocDefault));
+    for (hipEvent_t &ev : lp_ev)
+        if (!ev) ck(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    lp_state = dnew<int>(hxd::LS_FIELDS);   /* last: a failure above retries everything */
+}
+
+/* RoPE rows of positions [lp_rtab_rows, rows): the same host cosf/sinf values that
+ * run_geometry uploads per call (rope_tables, model.c:386-397) */
+void hearth_engine::loop_rope_table(int rows) {
+    if (!rope_dim || rows <= lp_rtab_rows) return;
+    const int half = rope_dim / 2;
+    std::vector<float> tab((size_t)(rows - lp_rtab_rows) * rope_dim);
+    for (int p = lp_rtab_rows; p < rows; p++) {
+        float *r = tab.data() + (size_t)(p - lp_rtab_rows) * rope_dim;
+        for (int j = 0; j < half; j++) {
+            const float th = (float)p * inv_freq[j];
+            r[2 * j] = host_cosf(th) * c.rope_factor;
+            r[2 * j + 1] = host_sinf(th) * c.rope_factor;
+        }
+    }
+    ck(hipMemcpy(lp_rtab + (size_t)lp_rtab_rows * rope_dim, tab.data(), sizeof(float) * tab.size(),
+                 hipMemcpyHostToDevice));
+    lp_rtab_rows = rows;
+}
+
+hxd::LoopArgs hearth_engine::loop_args(int T) {
+    hxd::LoopArgs a{};
+    a.state = lp_state; a.hist = lp_hist; a.hist_cap = cap + B + 2; a.stops = lp_stops;
+    a.out = lp_out; a.out_cap = HEARTH_GPU_SPEC_MAX_STEPS * B; a.rec = lp_rec; a.rec_cap = HEARTH_GPU_SPEC_MAX_STEPS;
+    a.tokens = tokens; a.cmp = lp_cmp; a.rope = rope; a.rtab = lp_rtab; a.rope_dim = rope_dim; a.cap = cap;
+    a.pos = d_pos; a.result = acc_i + 2 * B; a.T = T;
+    return a;
+}
+
+/* One step: drafts and geometry rows, the forward of T rows with the head, the greedy
+ * acceptance of the live rows, the commit. */
+void hearth_engine::loop_step(int T) {
+    const hxd::LoopArgs la = loop_args(T);
+    hxl::loop_draft(la, st);
+    forward(T, true, 0);
+    hxd::AcceptArgs a{};
+    a.rows = logits; a.n = T; a.V = V; a.tokens = lp_cmp; a.parent = lp_par; a.amax = acc_i + B;
+    a.part_v = (float *)acc_part; a.part_i = acc_part + (size_t)T * hxd::ACCEPT_PARTS;
+    a.part_f = acc_part + 2 * (size_t)T * hxd::ACCEPT_PARTS;
+    a.path = lp_path; a.result = acc_i + 2 * B;
+    hxl::accept_greedy(a, st);
+    hxl::loop_commit(la, st);
+}
+
+/* A step of T rows whose positions stay below rows: replayed from a captured graph
+ * (graphs on), else launched directly with the same row bound. */
+void hearth_engine::launch_loop_step(int T, int rows) {
+    struct Bound {   /* the launch bounds of a loop step, reset on every exit */
+        hearth_engine *e;
+        Bound(hearth_engine *x, int rows) : e(x) { e->rows_bound = rows; e->route_live = e->lp_state + hxd::LS_LIVE; }
+        ~Bound() { e->rows_bound = 0; e->route_live = nullptr; }
+    };
+    if (!graph_on) {
+        Bound b(this, rows);
+        loop_step(T);
+        return;
+    }
+    Captured *cg = nullptr;
+    for (Captured &g : graphs)
+        if (g.loop && g.T == T && g.rows == rows) cg = &g;
+    if (!cg) {
+        if (graphs.size() >= 32) {
+            (void)hipGraphExecDestroy(graphs.front().exec);
+            (void)hipGraphDestroy(graphs.front().graph);
+            graphs.erase(graphs.begin());
+        }
+        Captured g{T, 1, rows, true, true, nullptr, nullptr};
+        ck(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        try {
+            Bound b(this, rows);
+            loop_step(T);
+        } catch (const DeviceError &) {
+            hipGraph_t dead = nullptr;
+            if (hipStreamEndCapture(st, &dead) == hipSuccess && dead) (void)hipGraphDestroy(dead);
+            throw;
+        }
         ck(hipStreamEndCapture(st, &g.graph));
         const hipError_t e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
         if (e != hipSuccess) {
@@ -1725,6 +1852,94 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
         d_path = a.path;
         d_res = a.result;
     });
+}
+
+HEARTH_API int hearth_gpu_spec_loop_ok(hearth_engine *e) { return e && e->loop_ok() ? 1 : 0; }
+
+HEARTH_API int hearth_gpu_spec_greedy(hearth_engine *e, const int32_t *seq, int n_seq, int new_tokens, int max_new,
+                                      int draft_len, int ngram_n, const int32_t *stop_ids, int n_stop, int max_steps,
+                                      int32_t *out, int32_t *records, hearth_gpu_spec_result *res) {
+    if (!e || !seq || n_seq < 1 || !out || !records || !res) return E_ARG;
+    if (new_tokens < 0 || max_new <= new_tokens || draft_len < 0 || ngram_n < 0) return E_ARG;
+    if (n_stop < 0 || n_stop > hxd::LOOP_STOPS_MAX || (n_stop && !stop_ids)) return E_ARG;
+    if (max_steps < 1 || max_steps > HEARTH_GPU_SPEC_MAX_STEPS) return E_ARG;
+    const int T = draft_len + 1;
+    if (T > e->B || T > 128) return E_ARG;
+    if (!e->loop_ok()) {
+        log_msg(LOG_ERROR, "hearth_gpu_spec_greedy: not available with expert streaming, route replay, a routing "
+                           "trace or profiling");
+        return E_ARG;
+    }
+    if (e->pos != n_seq - 1) return E_ARG;
+    for (int i = 0; i < n_seq; i++)
+        if (seq[i] < 0 || seq[i] >= e->V) return E_TOKEN;
+    /* step s runs at a position <= pos + s T and writes rows below pos + (s + 1) T */
+    const int S = std::min(max_steps, (e->cap - e->pos) / T);
+    if (S < 1) return E_CAPACITY;
+    if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
+    const double t0 = now_s();
+    const int pos0 = e->pos, rows = std::min(e->cap, (pos0 + S * T + 1023) / 1024 * 1024);
+    int launched = 0;
+    int state[hxd::LS_FIELDS] = {};
+    try {
+        ck(hipStreamSynchronize(e->st));
+        e->loop_prepare();
+        e->loop_rope_table(std::min(e->cap, pos0 + S * T));
+        state[hxd::LS_LEN] = n_seq;
+        state[hxd::LS_NEW] = new_tokens;
+        state[hxd::LS_MAXNEW] = max_new;
+        state[hxd::LS_NGRAM] = draft_len ? ngram_n : 0;
+        state[hxd::LS_NSTOP] = n_stop;
+        state[hxd::LS_KVPOS] = pos0;
+        state[hxd::LS_LIVE] = 1;
+        /* chain geometry of T rows: depth i, ancestors 0..i; parents i - 1 */
+        std::vector<int> depth_h(T), anc_h((size_t)T * e->B, 0), par_h(T);
+        for (int i = 0; i < T; i++) {
+            depth_h[i] = i;
+            par_h[i] = i - 1;
+            for (int j = 0; j <= i; j++) anc_h[(size_t)i * e->B + j] = j;
+        }
+        ck(hipMemcpy(e->lp_state, state, sizeof state, hipMemcpyHostToDevice));
+        ck(hipMemcpy(e->lp_hist, seq, sizeof(int) * n_seq, hipMemcpyHostToDevice));
+        if (n_stop) ck(hipMemcpy(e->lp_stops, stop_ids, sizeof(int) * n_stop, hipMemcpyHostToDevice));
+        ck(hipMemcpy(e->depth, depth_h.data(), sizeof(int) * T, hipMemcpyHostToDevice));
+        ck(hipMemcpy(e->anc, anc_h.data(), sizeof(int) * anc_h.size(), hipMemcpyHostToDevice));
+        ck(hipMemcpy(e->lp_par, par_h.data(), sizeof(int) * T, hipMemcpyHostToDevice));
+        ck(hipMemcpy(e->d_pos, &pos0, sizeof(int), hipMemcpyHostToDevice));
+        e->geom_chain = 1;
+        e->tree_n = 0;
+        /* two steps in flight: before step i is queued, the done flag of step i - 2 is
+         * read, so at most two steps run after the one that ended the run */
+        for (int i = 0; i < S; i++) {
+            if (i >= 2) {
+                ck(hipEventSynchronize(e->lp_ev[i & 1]));
+                if (e->h_lp[i & 1] != hxd::LOOP_RUNNING) break;
+            }
+            e->launch_loop_step(T, rows);
+            launched++;
+            ck(hipMemcpyAsync(e->h_lp + (i & 1), e->lp_state + hxd::LS_DONE, sizeof(int), hipMemcpyDeviceToHost, e->st));
+            ck(hipEventRecord(e->lp_ev[i & 1], e->st));
+        }
+        ck(hipMemcpyAsync(e->h_lp, e->lp_state, sizeof(int) * hxd::LS_FIELDS, hipMemcpyDeviceToHost, e->st));
+        ck(hipStreamSynchronize(e->st));
+        std::memcpy(state, e->h_lp, sizeof state);
+        const int nout = std::min(state[hxd::LS_NOUT], S * T), nst = std::min(state[hxd::LS_STEP], S);
+        if (nout) ck(hipMemcpy(out, e->lp_out, sizeof(int) * nout, hipMemcpyDeviceToHost));
+        if (nst) ck(hipMemcpy(records, e->lp_rec, sizeof(int) * 3 * nst, hipMemcpyDeviceToHost));
+        res->n_out = nout;
+        res->n_steps = nst;
+    } catch (const DeviceError &err) {
+        log_msg(LOG_ERROR, "HIP error in hearth_gpu_spec_greedy: %s", hipGetErrorString(err.e));
+        return E_IO;
+    }
+    res->finish = state[hxd::LS_DONE];
+    res->stop_id = state[hxd::LS_STOP];
+    res->pos = state[hxd::LS_KVPOS];
+    e->pos = state[hxd::LS_KVPOS];
+    e->tokens_done += (uint64_t)launched * T;
+    e->forward_calls += launched;
+    e->wall_s += now_s() - t0;
+    return OK;
 }
 
 HEARTH_API int hearth_verify_sample(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,

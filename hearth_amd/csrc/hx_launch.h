@@ -71,6 +71,9 @@ struct RouteArgs {
     long long replay_rows;
     int pos0;
     const int *depth;         /* [T] */
+    /* device [1] or null: tokens t >= *live are padding and take the experts and weights
+     * of token 0 (their rows are computed from token 0's router logits) */
+    const int *live;
 };
 
 /* Per-call token geometry: token t sits at KV slot pos0 + t, has RoPE position
@@ -225,6 +228,44 @@ struct SampleArgs {
     PwTail tail;                      /* pairwise tree of the row's last numpy buffer */
 };
 
+/* Greedy speculative decoding loop on the device (k_loop.hip): fields of the state block. */
+enum LoopField {
+    LS_LEN,       /* length of the committed sequence in hist */
+    LS_NEW,       /* tokens yielded by the generation so far */
+    LS_DONE,      /* LOOP_* */
+    LS_STOP,      /* the stop token that ended the run */
+    LS_STEP,      /* verify steps committed */
+    LS_NOUT,      /* tokens written to out */
+    LS_ND,        /* draft length of the current step */
+    LS_LIVE,      /* rows of the current step that are not padding (ND + 1) */
+    LS_MAXNEW,    /* the generation's token budget */
+    LS_NGRAM,     /* longest n-gram the prompt lookup matches (0: no drafts) */
+    LS_NSTOP,     /* stop ids */
+    LS_KVPOS,     /* the engine position after the last committed step */
+    LS_FIELDS = 16
+};
+enum LoopDone { LOOP_RUNNING = 0, LOOP_STOP = 1, LOOP_LENGTH = 2, LOOP_BAD = 3 };
+constexpr int LOOP_STOPS_MAX = 64;
+
+struct LoopArgs {
+    int *state;                       /* [LS_FIELDS] */
+    int *hist;                        /* [hist_cap] committed sequence */
+    int hist_cap;
+    const int *stops;                 /* [LOOP_STOPS_MAX] */
+    int *out;                         /* [out_cap] tokens each step handled, in order */
+    int out_cap;
+    int *rec;                         /* [rec_cap][3] per step: drafted, accepted, tokens handled */
+    int rec_cap;
+    int *tokens;                      /* [T] the forward's token ids */
+    int *cmp;                         /* [T] the acceptance's draft ids (-1 for padding) */
+    float *rope;                      /* [T][rope_dim] the forward's (cos, sin) rows */
+    const float *rtab;                /* [cap][rope_dim] (cos, sin) of every position */
+    int rope_dim, cap;
+    int *pos;                         /* device [1]: the forward's pos0, advanced by the commit */
+    const int *result;                /* the acceptance's n_path, final token, status */
+    int T;                            /* rows per step: draft length + 1 */
+};
+
 } // namespace hxd
 
 namespace hxl {
@@ -296,4 +337,8 @@ hipError_t accept_sample(SampleScratch &m, const float *rows, int n, int V, cons
  * context of row v includes the path tokens of nodes 1..v), m.row_rc[v] its status. */
 hipError_t sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
                         const SamplerSpec &s, hipStream_t st);
+/* One step of the greedy loop: the drafts, token ids and RoPE rows of the next forward
+ * (loop_draft), and the commit of the acceptance that followed it (loop_commit). */
+void loop_draft(const LoopArgs &a, hipStream_t st);
+void loop_commit(const LoopArgs &a, hipStream_t st);
 } // namespace hxl

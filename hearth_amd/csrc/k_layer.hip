@@ -332,6 +332,10 @@ __device__ __forceinline__ void wave_best(float &v, int &idx) {
 
 constexpr int ROUTE_EMAX = 1024;
 
+/* the router-logits row token t is routed from: padding tokens (t >= *live) take
+ * token 0's, so they add no expert to the batch */
+__device__ __forceinline__ int route_row(const RouteArgs &a, int t) { return a.live && t >= *a.live ? 0 : t; }
+
 /* expert j of token t under route replay */
 __device__ __forceinline__ int replay_id(const RouteArgs &a, int t, int j) {
     const long long pos = (long long)a.pos0 + a.depth[t];
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(64) void k_route_tokens(RouteArgs a) {
     __shared__ unsigned char taken[ROUTE_EMAX], gkeep[64];
     __shared__ float gsc[64];
     const int t = blockIdx.x, lane = threadIdx.x, E = a.E, K = a.K;
-    const float *lg = a.logits + (size_t)t * E;
+    const float *lg = a.logits + (size_t)route_row(a, t) * E;
     if (a.score_fn == 0) {
         /* softmax (quant.c:634-642): m = running max from x[0] (a NaN x[0] makes m NaN) */
         float m = -__builtin_huge_valf();
@@ -461,7 +465,7 @@ __global__ __launch_bounds__(256) void k_route_rank(RouteArgs a) {
     __shared__ float red[4];
     __shared__ float sum_sh;
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.E, K = a.K;
-    const float *lg = a.logits + (size_t)t * E;
+    const float *lg = a.logits + (size_t)route_row(a, t) * E;
     if (a.score_fn == 0) {
         /* softmax (quant.c:634-642): m = running max from x[0] (a NaN x[0] makes m NaN) */
         float m = -__builtin_huge_valf();
@@ -836,7 +840,7 @@ __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
     __shared__ RouteSmem rs;
     const int tid = threadIdx.x, nth = blockDim.x, t = tid >> 6;
     float lgv[RS_EMAX / 64];
-    if (t < a.T) route_small_logits(a, a.logits, t, lgv);
+    if (t < a.T) route_small_logits(a, a.logits, route_row(a, t), lgv);
     route_small_stage(a, rs, tid, nth);
     __syncthreads();
     if (t < a.T) route_small_token(a, rs, t, lgv);

@@ -107,6 +107,17 @@ class KStats(Structure):
     ]
 
 
+class SpecResult(Structure):
+    """hearth_gpu_spec_result (include/hearth_gpu.h)."""
+    _fields_ = [("n_out", ctypes.c_int32), ("n_steps", ctypes.c_int32), ("finish", ctypes.c_int32),
+                ("stop_id", ctypes.c_int32), ("pos", ctypes.c_int32)]
+
+
+SPEC_FINISH = {0: None, 1: "stop", 2: "length", 3: "bad_logits"}
+SPEC_MAX_STEPS = 1024
+SPEC_STOPS_MAX = 64
+
+
 class HearthSampler(Structure):
     """hearth_sampler (include/hearth_gpu.h): the reference Sampler's settings."""
     _fields_ = [
@@ -171,6 +182,9 @@ _PROTOS = {
                                          POINTER(c_double), POINTER(c_double), _I32P, POINTER(c_int), _I32P]),
     "hearth_gpu_probs": (c_int, [POINTER(c_float), c_int, c_int, _I32P, _I32P, POINTER(HearthSampler),
                                  POINTER(c_double)]),
+    "hearth_gpu_spec_greedy": (c_int, [c_void_p, _I32P, c_int, c_int, c_int, c_int, c_int, _I32P, c_int, c_int,
+                                       _I32P, _I32P, POINTER(SpecResult)]),
+    "hearth_gpu_spec_loop_ok": (c_int, [c_void_p]),
     "hearth_gpu_set_attn_mode": (c_int, [c_void_p, c_int]),
     "hearth_gpu_get_attn_mode": (c_int, [c_void_p]),
     "hearth_gpu_set_profiling": (c_int, [c_void_p, c_int]),
@@ -446,6 +460,47 @@ class Engine:
         rng.bit_generator.state = state
         rng.random(n_acc + (1 if n_acc < k else 0) + 1)
         return n_acc, fin
+
+    @property
+    def spec_loop_ok(self) -> bool:
+        """Whether spec_greedy can run (no expert streaming, route replay, routing trace
+        or profiling)."""
+        fn = self._api.gpu_spec_loop_ok
+        with self._lock:
+            return fn is not None and bool(fn(self._handle()))
+
+    def spec_greedy(self, seq, new_tokens: int, max_new: int, draft_len: int, ngram_n: int, stop_ids=(),
+                    max_steps: int = 64):
+        """Greedy speculative decoding steps with prompt-lookup drafts, run on the device
+        (hearth_gpu_spec_greedy). The engine must hold seq[:-1]. Returns None when not
+        one step of draft_len + 1 rows fits in the KV cache, else a dict: "steps", a list
+        of (drafted, accepted, tokens handled) per step, in order; "finish" (None, "stop",
+        "length" or "bad_logits", the last meaning the step after the reported ones met a
+        row the greedy sampler rejects); "stop_id"; "pos" (the engine position)."""
+        ids = _i32(seq)
+        stops = _i32(list(stop_ids))
+        if stops.size > SPEC_STOPS_MAX:
+            raise ValueError(f"at most {SPEC_STOPS_MAX} stop ids")
+        max_steps = max(1, min(int(max_steps), SPEC_MAX_STEPS))
+        out = np.empty(max_steps * (int(draft_len) + 1), dtype=np.int32)
+        rec = np.empty(3 * max_steps, dtype=np.int32)
+        res = SpecResult()
+        with self._lock:
+            rc = self._api.need("gpu_spec_greedy")(
+                self._handle(), ids.ctypes.data_as(_I32P), int(ids.size), int(new_tokens), int(max_new),
+                int(draft_len), int(ngram_n), stops.ctypes.data_as(_I32P) if stops.size else None, int(stops.size),
+                max_steps, out.ctypes.data_as(_I32P), rec.ctypes.data_as(_I32P), byref(res))
+        if rc == -3:
+            return None
+        if rc < 0:
+            raise HearthError(f"hearth_gpu_spec_greedy failed (code {rc}): {_ERRORS.get(rc, 'unknown error')}")
+        steps, o = [], 0
+        for s in range(res.n_steps):
+            d, a, h = (int(v) for v in rec[3 * s:3 * s + 3])
+            steps.append((d, a, out[o:o + h].tolist()))
+            o += h
+        return {"steps": steps, "finish": SPEC_FINISH[int(res.finish)], "stop_id": int(res.stop_id),
+                "pos": int(res.pos)}
 
     def verify_tree(self, tokens, parent, want_logits: bool = True):
         ids, par = _i32(tokens), _i32(parent)

@@ -6,13 +6,18 @@ python/hearth/generate.py (Sampler 31-126, NgramIndex 150-186, GenStats / Token 
 sync_prefix 250-266, generate 292-400), so front ends written against it run unchanged.
 
 How a generation runs here. A `_Run` owns the committed token sequence, the drafter (an
-NgramIndex over that sequence, or none) and the running GenStats. `_Run.advance()` is one
-decode forward: it asks the drafter for up to `room` tokens and hands [last] + draft to
-the engine's verify call, which evaluates the chain, accepts on the GPU (argmax
-comparison, or exact speculative sampling of a point-mass proposal fed the uniforms the
-reference would draw) and commits the accepted prefix in the KV cache. Only the accepted
-path and the next token come back to the host; no logits block crosses PCIe. `generate()`
-itself only applies the stop and length rules to the tokens each forward commits.
+NgramIndex over that sequence, or none) and the running GenStats. A host step
+(`_Run.advance()` without the device loop) is one decode forward: it asks the drafter for
+up to `room` tokens and hands [last] + draft to the engine's verify call, which evaluates
+the chain, accepts on the GPU (argmax comparison, or exact speculative sampling of a
+point-mass proposal fed the uniforms the reference would draw) and commits the accepted
+prefix in the KV cache. Only the accepted path and the next token come back to the host;
+no logits block crosses PCIe. Greedy runs without a repetition penalty go further: the
+engine's device loop (Engine.spec_greedy) drafts from the sequence it keeps in HBM and
+applies the stop and length rules itself, so a batch of steps runs with no host round
+trip between them, and only the committed tokens and per-step counts come back.
+`generate()` applies the stop and length rules to the tokens each forward commits (for a
+device batch, the same cut the device made).
 
 Greedy output equals plain greedy decoding token for token (batched evaluation is
 bit-identical to sequential evaluation); sampled output has the plain output's
@@ -20,8 +25,9 @@ distribution, and for a given seed it is the sample the reference's own speculat
 draws from the same logits.
 
 `engine` is anything with `pos`, `reset()`, `rewind(pos)`, `eval(tokens)`,
-`verify_greedy(tokens)` and `verify_sample(tokens, parent, sampler, u=...)`
-(hearth_amd.engine.Engine, or a test double).
+`verify_greedy(tokens)` and `verify_sample(tokens, parent, sampler, u=...)`, and
+optionally `spec_loop_ok` and `spec_greedy(...)` (hearth_amd.engine.Engine, or a test
+double).
 """
 from __future__ import annotations
 
@@ -296,17 +302,29 @@ def _device_verify(engine, context: list[int], draft: list[int], sampler: Sample
 
 class _Run:
     """The state of one generation: the committed sequence, the drafter, the limits and
-    the statistics. After prefill() and every advance(), `pending` holds the tokens the
-    last forward committed, in order, and the engine holds all of them but the last."""
+    the statistics. After prefill() and every advance(), `steps` holds the forwards that
+    call ran, in order, as (drafted, accepted, tokens committed by the forward), and the
+    engine holds all of the committed tokens but the last.
+
+    A greedy run without a repetition penalty, on an engine that offers it
+    (`spec_loop_ok`), advances by batches of steps run on the device
+    (Engine.spec_greedy: drafting, verify, acceptance and the stop and length rules
+    without a host round trip per step); the host steps take over near the end of the KV
+    cache, where a step's draft must be shorter than the draft length."""
 
     def __init__(self, engine, prompt: list[int], sampler: Sampler, drafter: NgramIndex | None, draft_len: int,
-                 max_new: int, cap: int, stats: GenStats):
+                 max_new: int, cap: int, stats: GenStats, stops: frozenset, device_loop: bool):
         self.engine, self.sampler, self.drafter = engine, sampler, drafter
         self.draft_len, self.max_new, self.cap, self.stats = draft_len, max_new, cap, stats
         self.seq = list(prompt)
-        self.pending: list[int] = []
+        self.steps: list[tuple[int, int, list[int]]] = []
+        self.decoding = False     # steps come from decode forwards (not the prefill)
         self.step = 0
         self.drafted = self.accepted = 0
+        self.stops = sorted(stops)
+        self.loop = device_loop
+        self.batch = 4            # device steps per call, doubling up to 64
+        self.bad = False          # the device batch ended at a step with a rejected logits row
 
     def prefill(self, held) -> None:
         st, prompt = self.stats, self.seq
@@ -316,7 +334,18 @@ class _Run:
             self.engine.eval(prompt[st.reused_tokens:-1])
         _, first = _device_verify(self.engine, self.seq, [], self.sampler)
         st.prefill_s = time.perf_counter() - t0
-        self.pending = [first]
+        self.steps = [(0, 0, [first])]
+
+    def begin(self, drafted: int, accepted: int) -> None:
+        """Counts one decode forward before its tokens are handled."""
+        st = self.stats
+        self.step += 1
+        st.forwards += 1
+        self.drafted, self.accepted = drafted, accepted
+        if drafted:
+            st.draft_steps += 1
+            st.drafted += drafted
+            st.accepted += accepted
 
     def commit(self, tok: int) -> None:
         self.seq.append(tok)
@@ -331,22 +360,31 @@ class _Run:
         return pos
 
     def advance(self, base: int) -> None:
-        """One decode forward from position base. Its draft may hold up to the draft
-        length, what the token budget leaves after the forward's own token, and the KV
-        positions left."""
+        """The next decode forwards from position base: a batch on the device, or one
+        host step. A host step's draft may hold up to the draft length, what the token
+        budget leaves after the forward's own token, and the KV positions left."""
         st = self.stats
+        if self.bad:
+            raise ValueError(_BAD_LOGITS)
+        self.decoding = True
+        t0 = time.perf_counter()
+        if self.loop:
+            k = self.draft_len if self.drafter is not None else 0
+            res = self.engine.spec_greedy(self.seq, st.new_tokens, self.max_new, k,
+                                          self.drafter.max_n if self.drafter is not None else 0, self.stops,
+                                          max_steps=min(self.batch, self.max_new - st.new_tokens))
+            if res is not None:
+                self.batch = min(2 * self.batch, 64)
+                self.steps = res["steps"]
+                self.bad = res["finish"] == "bad_logits"
+                st.decode_s += time.perf_counter() - t0
+                if self.bad and not self.steps:
+                    raise ValueError(_BAD_LOGITS)
+                return
         n = min(self.draft_len, self.max_new - st.new_tokens - 1, self.cap - base - 1)
         draft = self.drafter.propose(n) if self.drafter is not None and n > 0 else []
-        t0 = time.perf_counter()
-        self.step += 1
-        st.forwards += 1
-        self.accepted, final = _device_verify(self.engine, self.seq, draft, self.sampler)
-        self.drafted = len(draft)
-        if draft:
-            st.draft_steps += 1
-            st.drafted += self.drafted
-            st.accepted += self.accepted
-        self.pending = draft[:self.accepted] + [final]
+        accepted, final = _device_verify(self.engine, self.seq, draft, self.sampler)
+        self.steps = [(len(draft), accepted, draft[:accepted] + [final])]
         st.decode_s += time.perf_counter() - t0
 
     def release(self) -> None:
@@ -359,13 +397,30 @@ class _Run:
             pass
 
 
+def _use_device_loop(engine, sampler: Sampler, stops: frozenset, device_loop: bool | None) -> bool:
+    able = sampler.is_greedy and not sampler.uses_context and len(stops) <= _eng.SPEC_STOPS_MAX
+    if device_loop is False or not able:
+        if device_loop:
+            raise ValueError("the device loop runs greedy decoding without a repetition penalty and at most "
+                             f"{_eng.SPEC_STOPS_MAX} stop ids")
+        return False
+    ok = bool(getattr(engine, "spec_loop_ok", False))
+    if device_loop and not ok:
+        raise ValueError("this engine cannot run the device loop (expert streaming, route replay, a routing trace "
+                         "or profiling is on)")
+    return ok
+
+
 def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampler: Sampler | None = None,
              stop_ids: Sequence[int] = (), speculative: str = "none", draft_len: int = 4, ngram_n: int = 3,
-             *, held: Sequence[int] | None = None) -> Iterator[Token]:
+             *, held: Sequence[int] | None = None, device_loop: bool | None = None) -> Iterator[Token]:
     """Yields the generated tokens one at a time (a stop token is not yielded) and
     returns the GenStats (StopIteration.value).
 
     held: the tokens whose KV the engine holds (prefix reuse); None resets the engine.
+    device_loop: None runs greedy decoding (no repetition penalty) in batches of steps on
+    the device when the engine offers it, False always steps from the host, True requires
+    the device loop. The tokens and statistics are the same either way.
     Once a token has been yielded or the generator has returned (max_new_tokens == 0
     included), and from then on even if it is closed or interrupted, the engine holds a
     prefix of prompt + yielded tokens of length engine.pos (all but the last token
@@ -390,21 +445,24 @@ def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampl
         return st
 
     run = _Run(engine, prompt, sampler, NgramIndex(ngram_n, prompt) if mode == "ngram" else None, draft_len,
-               max_new_tokens, cap, st)
+               max_new_tokens, cap, st, stops, _use_device_loop(engine, sampler, stops, device_loop))
     try:
         run.prefill(held)
         while True:
-            for tok in run.pending:
-                st.decode_tokens += run.step > 0
-                if tok in stops:
-                    st.finish_reason, st.stop_id = "stop", tok
-                    return st
-                run.commit(tok)
-                st.new_tokens += 1
-                yield Token(tok, run.step, run.drafted, run.accepted, st)
-                if st.new_tokens >= max_new_tokens:
-                    st.finish_reason = "length"
-                    return st
+            for drafted, accepted, toks in run.steps:
+                if run.decoding:
+                    run.begin(drafted, accepted)
+                for tok in toks:
+                    st.decode_tokens += run.step > 0
+                    if tok in stops:
+                        st.finish_reason, st.stop_id = "stop", tok
+                        return st
+                    run.commit(tok)
+                    st.new_tokens += 1
+                    yield Token(tok, run.step, run.drafted, run.accepted, st)
+                    if st.new_tokens >= max_new_tokens:
+                        st.finish_reason = "length"
+                        return st
             base = run.base()
             if base + 1 > cap:
                 st.finish_reason = "length"
@@ -415,10 +473,11 @@ def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampl
 
 
 def generate_ids(engine, prompt_ids, max_new_tokens=256, sampler=None, stop_ids=(), speculative="none",
-                 draft_len=4, ngram_n=3, *, held=None) -> tuple[list[int], GenStats]:
+                 draft_len=4, ngram_n=3, *, held=None, device_loop=None) -> tuple[list[int], GenStats]:
     """All tokens of generate() and its GenStats."""
     ids: list[int] = []
-    gen = generate(engine, prompt_ids, max_new_tokens, sampler, stop_ids, speculative, draft_len, ngram_n, held=held)
+    gen = generate(engine, prompt_ids, max_new_tokens, sampler, stop_ids, speculative, draft_len, ngram_n, held=held,
+                   device_loop=device_loop)
     try:
         while True:
             ids.append(next(gen).id)

@@ -41,6 +41,49 @@ HEARTH_API int hearth_commit_path(hearth_engine *e, const int32_t *path, int n);
 HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,
                                     int32_t *path_out, int *n_path, int32_t *final_tok, float *logits);
 
+/* Greedy speculative decoding with the drafting on the device: replaces the loop of
+ * the reference's generate() (python/hearth/generate.py:292-400) around its verify
+ * block (365-392) with prompt-lookup drafts (NgramIndex, generate.py:150-186), for a
+ * greedy sampler without a repetition penalty. Runs up to max_steps verify steps
+ * without a host round trip per step: each proposes up to draft_len tokens that follow
+ * the latest earlier occurrence of the longest suffix of at most ngram_n tokens
+ * (ngram_n or draft_len 0: no drafts; the draft also leaves room in the token budget
+ * for the step's own token), verifies [last] + draft, accepts greedily (as
+ * hearth_verify_greedy) and handles the step's tokens as generate() does: each, in
+ * order, ends the run if it is one of stop_ids (it is not committed), else is
+ * committed, and the run ends once new_tokens reaches max_new.
+ *
+ * The engine must hold seq[0 .. n_seq - 2] (pos == n_seq - 1); new_tokens counts the
+ * tokens already yielded (0 <= new_tokens < max_new). Every step evaluates
+ * draft_len + 1 rows (rows past a shorter draft are padding), so only
+ * (capacity - pos) / (draft_len + 1) steps fit: 0 of them returns -3 and the caller
+ * finishes with hearth_verify_greedy and shorter drafts. out receives the tokens each
+ * step handled (the accepted drafts, then the final token; a stop token that ended the
+ * run included), at least max_steps * (draft_len + 1) entries; records[3 s ..] the
+ * draft length, the drafts accepted and the tokens handled of step s (3 * max_steps
+ * entries). Afterwards pos is the position generate() leaves: n_seq - 1 plus the
+ * committed tokens, or at most the committed sequence's length once the run has ended.
+ * Returns -1 when the engine cannot run the loop (expert streaming, route replay or a
+ * routing trace, profiling; see hearth_gpu_spec_loop_ok). No counterpart in the
+ * reference's C API. */
+#define HEARTH_GPU_SPEC_MAX_STEPS 1024
+#define HEARTH_GPU_SPEC_RUNNING 0   /* max_steps ran (or the capacity ended them) */
+#define HEARTH_GPU_SPEC_STOP 1      /* a stop token ended the run */
+#define HEARTH_GPU_SPEC_LENGTH 2    /* the token budget ended the run */
+#define HEARTH_GPU_SPEC_BAD 3       /* the step after the reported ones met a NaN/+inf/all -inf row */
+typedef struct hearth_gpu_spec_result {
+    int32_t n_out;      /* entries written to out */
+    int32_t n_steps;    /* steps reported in records */
+    int32_t finish;     /* HEARTH_GPU_SPEC_* */
+    int32_t stop_id;    /* the stop token (finish STOP) */
+    int32_t pos;        /* the engine position afterwards */
+} hearth_gpu_spec_result;
+HEARTH_API int hearth_gpu_spec_greedy(hearth_engine *e, const int32_t *seq, int n_seq, int new_tokens, int max_new,
+                                      int draft_len, int ngram_n, const int32_t *stop_ids, int n_stop, int max_steps,
+                                      int32_t *out, int32_t *records, hearth_gpu_spec_result *res);
+/* 1 if the engine can run hearth_gpu_spec_greedy, else 0. */
+HEARTH_API int hearth_gpu_spec_loop_ok(hearth_engine *e);
+
 /* The acceptance kernel alone on caller logits (no engine): rows [n][V] f32. Same
  * result as hearth_verify_greedy's walk. Returns -1 for NaN/+inf/all -inf rows
  * (the reference Sampler raises for those, generate.py:69-79). */

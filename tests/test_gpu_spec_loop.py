@@ -1,0 +1,110 @@
+"""The greedy speculative loop on the device (hearth_gpu_spec_greedy) against the host
+steps (one hearth_verify_greedy per step, drafts from NgramIndex on the host).
+
+generate() with the device loop must yield what the host steps yield: the same tokens,
+Token fields (step, drafted, accepted), GenStats counts and finish, the same engine
+position and the same KV bits, on the tiny Qwen3-MoE model and the other families
+(Qwen2-MoE, OLMoE, DeepSeek-V3 with latent attention), with drafts and without, with a
+stop token or a token budget that ends a batch in its middle, near the end of the KV
+cache (where the host steps take over), with graph capture off, and in the chunked
+attention order. The host steps are themselves pinned to the oracle and to plain greedy
+decoding by the other GPU tests, and the drafting formulation to NgramIndex on the CPU.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from hearth_amd import container
+from hearth_amd.engine import Engine
+from hearth_amd.generate import Sampler, generate
+
+pytestmark = pytest.mark.gpu
+
+
+def _prompt(vocab):
+    base = [int(t) for t in container.uniform_ints(31, 12, vocab)]
+    return base * 3 + base[:5]
+
+
+def _gen(e, prompt, n, stops, spec, k, ng, loop):
+    print(f"generate n={n} stops={list(stops)} {spec} k={k} ng={ng} device_loop={loop}", flush=True)
+    gen = generate(e, prompt, n, Sampler.greedy(), stops, spec, k, ng, device_loop=loop)
+    toks = []
+    try:
+        while True:
+            toks.append(next(gen))
+    except StopIteration as done:
+        st = done.value
+    kv = e.kv_export(e.pos)
+    counts = (st.new_tokens, st.decode_tokens, st.forwards, st.draft_steps, st.drafted, st.accepted,
+              st.finish_reason, st.stop_id)
+    return [(t.id, t.step, t.drafted, t.accepted) for t in toks], counts, e.pos, np.ascontiguousarray(kv).view(np.uint32)
+
+
+def _same(e, prompt, n, stops, spec, k, ng):
+    ref = _gen(e, prompt, n, stops, spec, k, ng, False)
+    got = _gen(e, prompt, n, stops, spec, k, ng, True)
+    assert got[0] == ref[0], "tokens or Token fields differ"
+    assert got[1] == ref[1], "GenStats counts differ"
+    assert got[2] == ref[2], "engine position differs"
+    assert np.array_equal(got[3], ref[3]), "KV differs"
+    return got
+
+
+@pytest.mark.parametrize("name", ["tiny", "qwen2", "olmoe", "dsv3"])
+def test_device_loop_equals_host_steps(name, tiny_model, variant_models):
+    path = tiny_model if name == "tiny" else variant_models(name)
+    with Engine(path, max_seq=512) as e:
+        assert e.spec_loop_ok
+        prompt = _prompt(e.vocab_size)
+        drafted = accepted = 0
+        for spec, k, ng in (("ngram", 4, 3), ("ngram", 8, 2), ("none", 4, 3)):
+            toks, counts, _, _ = _same(e, prompt, 48, (), spec, k, ng)
+            assert counts[6] == "length" and len(toks) == 48
+            drafted += counts[4]
+            accepted += counts[5]
+        assert drafted > 0 and accepted > 0, (drafted, accepted)
+        # a stop token and a budget that end a batch in its middle
+        plain = [t[0] for t in _gen(e, prompt, 40, (), "none", 4, 3, False)[0]]
+        for stop_at in (0, 9, 25):
+            toks, counts, _, _ = _same(e, prompt, 40, (plain[stop_at],), "ngram", 6, 3)
+            assert counts[6] == "stop" and counts[7] == plain[stop_at]
+        for n in (1, 2, 7, 19):
+            _same(e, prompt, n, (), "ngram", 6, 3)
+    print(f"{name}: drafted {drafted} accepted {accepted}", file=sys.stderr)
+
+
+def test_end_of_cache_and_direct_call(tiny_model):
+    with Engine(tiny_model, max_seq=96) as e:
+        prompt = _prompt(e.vocab_size)
+        toks, counts, pos, _ = _same(e, prompt, 200, (), "ngram", 6, 3)
+        assert counts[6] == "length" and pos <= 96
+        # the direct call: None when not one step of draft_len + 1 rows fits
+        e.reset()
+        e.eval(prompt[:-1])
+        res = e.spec_greedy(prompt, 0, 100, 4, 3, (), max_steps=3)
+        assert res is not None and len(res["steps"]) <= 3 and res["pos"] == e.pos
+        handled = [t for s in res["steps"] for t in s[2]]
+        assert e.pos == len(prompt) - 1 + len(handled)
+        e.reset()
+        e.eval(prompt * 2)
+        seq = (prompt * 3)[:e.pos + 1]
+        room = 96 - e.pos
+        assert e.spec_greedy(seq, 0, 10, room, 3) is None
+        assert e.spec_greedy(seq, 0, 10, room - 1, 3) is not None
+
+
+def test_graphs_off_and_chunked_order(tiny_model, monkeypatch):
+    with Engine(tiny_model, max_seq=512) as e:
+        prompt = _prompt(e.vocab_size)
+        want = _same(e, prompt, 40, (), "ngram", 5, 3)
+    monkeypatch.setenv("HEARTH_GPU_GRAPH", "0")
+    with Engine(tiny_model, max_seq=512) as e:
+        got = _same(e, prompt, 40, (), "ngram", 5, 3)
+    assert got[0] == want[0] and np.array_equal(got[3], want[3])
+    monkeypatch.delenv("HEARTH_GPU_GRAPH")
+    with Engine(tiny_model, max_seq=512, attn="chunked") as e:
+        _same(e, prompt, 40, (), "ngram", 5, 3)
