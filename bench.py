@@ -2,7 +2,7 @@
 greedy linear-chain verification with k = 8 drafts at a 4096-token context.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--layers 48] [--ctx 4096] [--k 8]
-    python bench.py --workload {chain,tree,experts,dsv3}
+    python bench.py --workload {chain,tree,experts,dsv3,generate}
 
 The default workload (chain) is described below; the others print their own JSON line:
   tree     the same model, one 4x4x4 draft tree (85 nodes) per step at a 2048-token
@@ -13,7 +13,12 @@ The default workload (chain) is described below; the others print their own JSON
   dsv3     the DeepSeek-V3 shape (MLA, 256 experts top-8 + shared, 3 dense + 20 MoE
            layers), chain verify k = 8 at 4096, with the experts streamed from pinned
            host memory through an HBM cache below the expert set (and resident, for
-           comparison).
+           comparison);
+  generate the same model, greedy generation of --gen tokens after a 4096-token prompt
+           with prompt-lookup drafts (k = 8, n-grams up to 3): generate() with the
+           device loop (drafting, verify, acceptance and stop/length rules on the GPU,
+           no host round trip per step) against the host steps (one verify call per
+           step); both must yield the same tokens.
 
 Workload (one step = one verify of [last] + k drafts: eval on the GPU, greedy
 acceptance on the GPU, commit; generate.py:365-392 of the reference):
@@ -611,6 +616,44 @@ def bench_dsv3(a) -> dict:
     }
 
 
+def bench_generate(a) -> dict:
+    """End-to-end greedy generation with n-gram drafts on the Qwen3-30B-A3B shape: the
+    device loop against the host steps, same tokens required."""
+    from hearth_amd import container
+    from hearth_amd.engine import Engine
+    from hearth_amd.generate import Sampler, generate_ids
+
+    path = model_path(a.layers, a.ctx, a.k)
+    # a prompt that repeats itself (a document quoted back), so the lookup finds drafts
+    rnd = container.uniform_ints(4321, a.ctx // 2, container.QWEN3_30B_A3B.vocab)
+    prompt = [int(t) for t in np.concatenate([rnd, rnd])[:a.ctx]]
+    eng = Engine(path, max_seq=a.ctx + a.gen + 64, max_batch=512)
+    runs = {}
+    for loop in (False, True, False, True):   # warm both, then time the second of each
+        t = time.perf_counter()
+        ids, st = generate_ids(eng, prompt, a.gen, Sampler.greedy(), (), "ngram", a.k, 3, device_loop=loop)
+        wall = time.perf_counter() - t
+        runs[loop] = (ids, st, wall)
+        log(f"[bench] device_loop={loop}: {st.new_tokens} tokens, {st.forwards} forwards, accepted "
+            f"{st.accepted}/{st.drafted}, decode {st.decode_tok_s:.1f} tok/s (prefill {st.prefill_s:.2f}s)")
+    eng.close()
+    (h_ids, h_st, _), (d_ids, d_st, _) = runs[False], runs[True]
+    if h_ids != d_ids:
+        raise RuntimeError("the device loop and the host steps generated different tokens")
+    return {
+        "metric": "greedy_generate_decode_tok_s", "value": round(d_st.decode_tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": d_st.forwards, "warmup": 1, "ms_per_step": round(d_st.decode_s / max(1, d_st.forwards) * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": f"Qwen3-30B-A3B-shaped greedy generation of {a.gen} tokens after a {a.ctx}-token "
+                               f"self-repeating prompt, prompt-lookup drafts k={a.k} n<=3, device loop",
+                   "layers": a.layers, "ctx": a.ctx, "k": a.k, "gen": a.gen,
+                   "tokens_per_forward": round(d_st.tokens_per_forward, 3),
+                   "acceptance_rate": round(d_st.acceptance_rate, 4),
+                   "host_steps_decode_tok_s": round(h_st.decode_tok_s, 2),
+                   "host_steps_ms_per_forward": round(h_st.decode_s / max(1, h_st.forwards) * 1e3, 4)},
+    }
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="speculative-verify throughput on one MI355X")
     ap.add_argument("--gpus", type=int, default=1)
@@ -619,10 +662,12 @@ def main(argv=None) -> int:
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--k", type=int, default=8)
-    ap.add_argument("--workload", choices=("chain", "tree", "experts", "dsv3"), default="chain",
+    ap.add_argument("--workload", choices=("chain", "tree", "experts", "dsv3", "generate"), default="chain",
                     help="chain: Qwen3-30B-A3B chain verify k=8 at 4096 (the headline); tree: 4x4x4 tree with "
                          "sampled acceptance at 2048; experts: the routed-expert kernels alone, Zipf routing; "
-                         "dsv3: DeepSeek-V3 shape with streamed experts")
+                         "dsv3: DeepSeek-V3 shape with streamed experts; generate: greedy generation with "
+                         "n-gram drafts, device loop against host steps")
+    ap.add_argument("--gen", type=int, default=256, help="generate: tokens to generate")
     ap.add_argument("--resident-only", action="store_true", help="dsv3: skip the streamed run")
     ap.add_argument("--cpu-steps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
@@ -639,7 +684,8 @@ def main(argv=None) -> int:
         print(f"bench.py runs on exactly one GPU: this build has no multi-GPU path (asked for {a.gpus})",
               file=sys.stderr)
         return 2
-    out = {"chain": bench_chain, "tree": bench_tree, "experts": bench_experts, "dsv3": bench_dsv3}[a.workload](a)
+    out = {"chain": bench_chain, "tree": bench_tree, "experts": bench_experts, "dsv3": bench_dsv3,
+           "generate": bench_generate}[a.workload](a)
     print(json.dumps(out))
     return 0
 

@@ -898,6 +898,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             at.q = qr; at.kc = qa.kc; at.vc = qa.vc; at.S = S; at.ldS = ldS; at.out = att; at.T = T; at.H = H;
             at.Hkv = Hkv; at.hd = hd; at.cap = cap; at.scale = c.attn_scale;
             at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos = d_pos; at.g.nr_max = nr_max(T); at.g.chain = geom_chain;
+            at.g.live = route_live;
             at.qo = aatt; at.qo_on = w.o.quant && hd % 64 == 0;
             if (attn_mode == 1) {
                 at.po = apo; at.pm = apm; at.pl = apl; at.nc_ld = anc_ld;

@@ -89,6 +89,9 @@ struct TokGeom {
     const int *pos;           /* device [1]: pos0 */
     int nr_max;
     int chain;                /* 1: token t sits at slot pos0 + t with ancestors pos0..pos0 + t */
+    /* device [1] or null: tokens t >= *live are padding; the GQA score, softmax and value
+     * kernels skip them (their attention output rows are not written) */
+    const int *live;
 };
 
 struct AttnArgs {

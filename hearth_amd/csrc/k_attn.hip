@@ -153,6 +153,7 @@ __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
     const int g = b % Hkv;
     b /= Hkv;
     const int t = b % a.T, c = b / a.T;
+    if (a.g.live && t >= *a.g.live) return;   /* padding token (uniform) */
     const int pos0 = *a.g.pos, nr = pos0 + a.g.depth[t] + 1;
     const int v0 = c * S16_RB;
     if (v0 >= nr) return;   /* uniform */
@@ -335,6 +336,7 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
     __shared__ unsigned long long etab[32];
     exp_table_to_lds(etab);
     const int t = blockIdx.x / a.H, h = blockIdx.x % a.H, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (a.g.live && t >= *a.g.live) return;   /* padding token (uniform) */
     const int pos0 = *a.g.pos, nr = pos0 + a.g.depth[t] + 1;
     float *s = a.S + ((size_t)t * a.H + h) * a.ldS;
     const bool inreg = nr <= SM_CH;
@@ -494,6 +496,7 @@ __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
     const int g = b % Hkv;
     b /= Hkv;
     const int hq = b % qpt, t = b / qpt;
+    if (a.g.live && t >= *a.g.live) return;   /* padding token (uniform) */
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int pos0 = *a.g.pos, dep = a.g.depth[t];
     const int nr = pos0 + dep + 1;
@@ -575,12 +578,23 @@ __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
                 TV_STEP(i + 1, R1, R2)
                 TV_STEP(i + 2, R2, R0)
             }
+            /* the last one or two steps load nothing (their tiles would lie past the
+             * rows): the loads of the tiles still to publish are waited for in full. A
+             * step's load count is not a bound here, because the compiler drops register
+             * loads whose values are never used, so a count-based wait could let the
+             * LDS-direct p rows of the tile being published still be in flight */
+#define TV_LAST(i_, RW)                                                                     \
+            __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) only */                       \
+            __builtin_amdgcn_s_barrier();                                                   \
+            HX_WAIT_VMCNT(0);                                                               \
+            store(((i_) + 1) & 1, RW);
             if (i < ntiles) {
-                TV_STEP(i, R0, R1)
+                TV_LAST(i, R1)
                 if (i + 1 < ntiles) {
-                    TV_STEP(i + 1, R1, R2)
+                    TV_LAST(i + 1, R2)
                 }
             }
+#undef TV_LAST
 #undef TV_STEP
         };
         if (chain) run(std::true_type{});
@@ -655,6 +669,7 @@ __global__ __launch_bounds__(64 * (NS + NL)) void k_attn_values_w(AttnArgs a) {
     const int g = b % Hkv;
     b /= Hkv;
     const int hq = b % qpt, t = b / qpt;
+    if (a.g.live && t >= *a.g.live) return;   /* padding token (uniform) */
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int pos0 = *a.g.pos, dep = a.g.depth[t];
     const int nr = pos0 + dep + 1;
@@ -744,12 +759,23 @@ __global__ __launch_bounds__(64 * (NS + NL)) void k_attn_values_w(AttnArgs a) {
                 TV_STEP(i + 1, R1, R2)
                 TV_STEP(i + 2, R2, R0)
             }
+            /* the last one or two steps load nothing (their tiles would lie past the
+             * rows): the loads of the tiles still to publish are waited for in full. A
+             * step's load count is not a bound here, because the compiler drops register
+             * loads whose values are never used, so a count-based wait could let the
+             * LDS-direct p rows of the tile being published still be in flight */
+#define TV_LAST(i_, RW)                                                                     \
+            __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) only */                       \
+            __builtin_amdgcn_s_barrier();                                                   \
+            HX_WAIT_VMCNT(0);                                                               \
+            store(((i_) + 1) & 1, RW);
             if (i < ntiles) {
-                TV_STEP(i, R0, R1)
+                TV_LAST(i, R1)
                 if (i + 1 < ntiles) {
-                    TV_STEP(i + 1, R1, R2)
+                    TV_LAST(i + 1, R2)
                 }
             }
+#undef TV_LAST
 #undef TV_STEP
         };
         if (chain) run(std::true_type{});

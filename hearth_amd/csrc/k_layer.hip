@@ -718,7 +718,7 @@ __device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, con
         a.ids[(size_t)t * K + lane] = my_id;
         a.wts[(size_t)t * K + lane] = w;
         pid[t * K + lane] = my_id;
-        atomicOr(&tmask[my_id], 1u << t);
+        if (!a.live || t < *a.live) atomicOr(&tmask[my_id], 1u << t);   /* padding tokens add no pair */
         if (a.route_out) a.route_out[((size_t)t * a.n_moe + a.moe_ord) * K + lane] = my_id;
     }
 }
@@ -805,15 +805,19 @@ __device__ __forceinline__ void route_small_bucket(const RouteArgs &a, RouteSmem
             rs.nu = nu_run;
             *a.n_active = nu_run;
             if (a.stats) {
-                a.stats[0] += (unsigned long long)P;
+                a.stats[0] += (unsigned long long)run;
                 a.stats[1] += (unsigned long long)nu_run;
             }
         }
     }
     __syncthreads();
-    const int nu = rs.nu;
+    const int nu = rs.nu, live = a.live ? *a.live : a.T;
     for (int p = tid; p < P; p += nth) {
         const int e = rs.pid[p], tt = p / K;
+        if (tt >= live) {   /* a padding token reads token 0's pair of the same rank (same expert) */
+            a.pair_of[p] = rs.base[e];
+            continue;
+        }
         const int pos = rs.base[e] + __popc(rs.tmask[e] & ((1u << tt) - 1u));
         a.pair_tok[pos] = tt;
         a.pair_of[p] = pos;

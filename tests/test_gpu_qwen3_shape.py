@@ -229,6 +229,28 @@ def test_prefill_chunk_160(model):
     _assert_same(lg, lo, "logits of the chunk's last token")
 
 
+def test_prefill_and_verify_are_deterministic(model):
+    """the same 609 tokens (a 512-token chunk, an 88-token chunk, a 9-token step)
+    evaluated 32 times give the same logits and KV bits every time. The 512- and
+    88-token chunks sum their values with the wide kernel (64-row tiles), the 9-token step
+    with the narrow one (128-row tiles); many of their token rows leave one or two tiles
+    after the loaders' groups of three, whose loads must be waited for in full before a
+    tile is published (the compiler drops the unused register loads of those steps)."""
+    toks = container.uniform_ints(616, 609, SHAPE.vocab).astype(np.int32)
+    first = None
+    with Engine(model, max_seq=1024, max_batch=512) as eng:
+        for r in range(32):
+            eng.reset()
+            eng.eval(toks[:512])
+            eng.eval(toks[512:600])
+            lg = eng.eval(toks[600:], all_logits=True)
+            got = (_bits(lg), _bits(eng.kv_export(609)))
+            if first is None:
+                first = got
+            else:
+                assert np.array_equal(got[0], first[0]) and np.array_equal(got[1], first[1]), f"run {r} differs"
+
+
 @pytest.mark.parametrize("what", ["chain", "tree"])
 def test_chunked_order_equals_oracle(prefilled, model, what):
     """The chunked attention order (opt-in) from the same contexts: the k=8 chain at 4095
