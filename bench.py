@@ -628,18 +628,20 @@ def bench_generate(a) -> dict:
     rnd = container.uniform_ints(4321, a.ctx // 2, container.QWEN3_30B_A3B.vocab)
     prompt = [int(t) for t in np.concatenate([rnd, rnd])[:a.ctx]]
     eng = Engine(path, max_seq=a.ctx + a.gen + 64, max_batch=512)
-    runs = {}
-    for loop in (False, True, False, True):   # warm both, then time the second of each
-        t = time.perf_counter()
-        ids, st = generate_ids(eng, prompt, a.gen, Sampler.greedy(), (), "ngram", a.k, 3, device_loop=loop)
-        wall = time.perf_counter() - t
-        runs[loop] = (ids, st, wall)
-        log(f"[bench] device_loop={loop}: {st.new_tokens} tokens, {st.forwards} forwards, accepted "
-            f"{st.accepted}/{st.drafted}, decode {st.decode_tok_s:.1f} tok/s (prefill {st.prefill_s:.2f}s)")
+    res = {}
+    for spec, k in (("ngram", a.k), ("none", 0)):
+        for loop in (False, True, False, True):   # warm both, then keep the second of each
+            ids, st = generate_ids(eng, prompt, a.gen, Sampler.greedy(), (), spec, k, 3, device_loop=loop)
+            res[spec, loop] = (ids, st)
+            log(f"[bench] {spec} k={k} device_loop={loop}: {st.new_tokens} tokens, {st.forwards} forwards, "
+                f"accepted {st.accepted}/{st.drafted}, decode {st.decode_tok_s:.1f} tok/s")
+        if res[spec, False][0] != res[spec, True][0]:
+            raise RuntimeError(f"{spec}: the device loop and the host steps generated different tokens")
     eng.close()
-    (h_ids, h_st, _), (d_ids, d_st, _) = runs[False], runs[True]
-    if h_ids != d_ids:
-        raise RuntimeError("the device loop and the host steps generated different tokens")
+    if res["ngram", True][0] != res["none", True][0]:
+        raise RuntimeError("speculative and plain greedy generation differ")
+    d_st, h_st = res["ngram", True][1], res["ngram", False][1]
+    p_dev, p_host = res["none", True][1], res["none", False][1]
     return {
         "metric": "greedy_generate_decode_tok_s", "value": round(d_st.decode_tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": d_st.forwards, "warmup": 1, "ms_per_step": round(d_st.decode_s / max(1, d_st.forwards) * 1e3, 4),
@@ -650,7 +652,9 @@ def bench_generate(a) -> dict:
                    "tokens_per_forward": round(d_st.tokens_per_forward, 3),
                    "acceptance_rate": round(d_st.acceptance_rate, 4),
                    "host_steps_decode_tok_s": round(h_st.decode_tok_s, 2),
-                   "host_steps_ms_per_forward": round(h_st.decode_s / max(1, h_st.forwards) * 1e3, 4)},
+                   "host_steps_ms_per_forward": round(h_st.decode_s / max(1, h_st.forwards) * 1e3, 4),
+                   "plain_device_loop_decode_tok_s": round(p_dev.decode_tok_s, 2),
+                   "plain_host_steps_decode_tok_s": round(p_host.decode_tok_s, 2)},
     }
 
 

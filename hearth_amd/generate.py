@@ -12,10 +12,11 @@ up to `room` tokens and hands [last] + draft to the engine's verify call, which 
 the chain, accepts on the GPU (argmax comparison, or exact speculative sampling of a
 point-mass proposal fed the uniforms the reference would draw) and commits the accepted
 prefix in the KV cache. Only the accepted path and the next token come back to the host;
-no logits block crosses PCIe. Greedy runs without a repetition penalty go further: the
-engine's device loop (Engine.spec_greedy) drafts from the sequence it keeps in HBM and
-applies the stop and length rules itself, so a batch of steps runs with no host round
-trip between them, and only the committed tokens and per-step counts come back.
+no logits block crosses PCIe. Greedy runs without a repetition penalty can go further:
+the engine's device loop (Engine.spec_greedy) drafts from the sequence it keeps in HBM
+and applies the stop and length rules itself, so a batch of steps runs with no host
+round trip between them, and only the committed tokens and per-step counts come back
+(`device_loop`: by default for runs without drafts).
 `generate()` applies the stop and length rules to the tokens each forward commits (for a
 device batch, the same cut the device made).
 
@@ -306,8 +307,8 @@ class _Run:
     call ran, in order, as (drafted, accepted, tokens committed by the forward), and the
     engine holds all of the committed tokens but the last.
 
-    A greedy run without a repetition penalty, on an engine that offers it
-    (`spec_loop_ok`), advances by batches of steps run on the device
+    With `loop` set (a greedy run without a repetition penalty, on an engine that offers
+    it: `spec_loop_ok`), the run advances by batches of steps run on the device
     (Engine.spec_greedy: drafting, verify, acceptance and the stop and length rules
     without a host round trip per step); the host steps take over near the end of the KV
     cache, where a step's draft must be shorter than the draft length."""
@@ -397,8 +398,13 @@ class _Run:
             pass
 
 
-def _use_device_loop(engine, sampler: Sampler, stops: frozenset, device_loop: bool | None) -> bool:
+def _use_device_loop(engine, sampler: Sampler, stops: frozenset, device_loop: bool | None, drafts: bool) -> bool:
+    """None picks the device loop for greedy runs without drafts only: with drafts, every
+    device step evaluates draft_len + 1 rows however short its draft, which at low
+    acceptance costs about what the saved host round trip gains."""
     able = sampler.is_greedy and not sampler.uses_context and len(stops) <= _eng.SPEC_STOPS_MAX
+    if device_loop is None and drafts:
+        return False
     if device_loop is False or not able:
         if device_loop:
             raise ValueError("the device loop runs greedy decoding without a repetition penalty and at most "
@@ -418,9 +424,10 @@ def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampl
     returns the GenStats (StopIteration.value).
 
     held: the tokens whose KV the engine holds (prefix reuse); None resets the engine.
-    device_loop: None runs greedy decoding (no repetition penalty) in batches of steps on
-    the device when the engine offers it, False always steps from the host, True requires
-    the device loop. The tokens and statistics are the same either way.
+    device_loop: True runs greedy decoding (no repetition penalty) in batches of steps on
+    the device (drafting included), False always steps from the host, None picks the
+    device loop for greedy runs without drafts when the engine offers it. The tokens and
+    statistics are the same either way.
     Once a token has been yielded or the generator has returned (max_new_tokens == 0
     included), and from then on even if it is closed or interrupted, the engine holds a
     prefix of prompt + yielded tokens of length engine.pos (all but the last token
@@ -445,7 +452,8 @@ def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampl
         return st
 
     run = _Run(engine, prompt, sampler, NgramIndex(ngram_n, prompt) if mode == "ngram" else None, draft_len,
-               max_new_tokens, cap, st, stops, _use_device_loop(engine, sampler, stops, device_loop))
+               max_new_tokens, cap, st, stops,
+               _use_device_loop(engine, sampler, stops, device_loop, mode == "ngram" and draft_len > 0))
     try:
         run.prefill(held)
         while True:

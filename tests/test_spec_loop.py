@@ -140,7 +140,7 @@ def test_device_batches_equal_host_steps(kw):
         for prompt in PROMPTS + [REPEAT]:
             for spec, k, ng in (("ngram", 4, 3), ("ngram", 1, 1), ("ngram", 8, 2), ("none", 4, 3), ("ngram", 0, 3)):
                 ref_e, ref, ref_st = _run(lambda: ToyEngine(seed=seed, **kw), prompt, 40, (), spec, k, ng, False)
-                e, got, st = _run(lambda: LoopToy(seed=seed, **kw), prompt, 40, (), spec, k, ng, None)
+                e, got, st = _run(lambda: LoopToy(seed=seed, **kw), prompt, 40, (), spec, k, ng, True)
                 assert got == ref, (seed, prompt, spec, k, ng)
                 assert _counts(st) == _counts(ref_st)
                 assert e.kv == ref_e.kv
@@ -160,7 +160,7 @@ def test_stops_budgets_and_capacity_inside_a_batch():
             for n in (1, 2, 5, 13, 60):
                 for cap in (512, 40, 23):
                     a_e, a, a_st = _run(lambda: ToyEngine(max_seq=cap, **mk), REPEAT, n, stops, "ngram", 6, 3, False)
-                    b_e, b, b_st = _run(lambda: LoopToy(max_seq=cap, **mk), REPEAT, n, stops, "ngram", 6, 3, None)
+                    b_e, b, b_st = _run(lambda: LoopToy(max_seq=cap, **mk), REPEAT, n, stops, "ngram", 6, 3, True)
                     assert a == b, (seed, stop_at, n, cap)
                     assert _counts(a_st) == _counts(b_st) and a_e.kv == b_e.kv
                     cut += b_st.finish_reason == "stop" and b_e.batches > 0
@@ -171,7 +171,7 @@ def test_closing_inside_a_batch_leaves_a_prefix():
     inside = 0
     for k in range(1, 40):
         e = LoopToy(seed=3, follow=4.0)
-        gen = generate(e, REPEAT, 60, Sampler.greedy(), speculative="ngram", draft_len=6)
+        gen = generate(e, REPEAT, 60, Sampler.greedy(), speculative="ngram", draft_len=6, device_loop=True)
         got = [next(gen).id for _ in range(k)]
         inside += e.pos > len(REPEAT) + k
         gen.close()
@@ -193,5 +193,10 @@ def test_loop_selection():
         generate_ids(ToyEngine(), REPEAT, 8, Sampler.greedy(), (), "ngram", 4, 3, device_loop=True)
     generate_ids(e, REPEAT, 8, Sampler.greedy(), (), "ngram", 4, 3, device_loop=False)
     assert e.batches == 0
+    # None: the device loop for greedy runs without drafts, host steps with drafts
     generate_ids(e, REPEAT, 8, Sampler.greedy(), (), "ngram", 4, 3)
+    assert e.batches == 0
+    generate_ids(e, REPEAT, 8, Sampler.greedy(), (), "none", 4, 3)
     assert e.batches > 0
+    generate_ids(e, REPEAT, 8, Sampler.greedy(), (), "ngram", 4, 3, device_loop=True)
+    assert e.batches > 1
