@@ -533,11 +533,25 @@ __global__ __launch_bounds__(256) void k_route_rank(RouteArgs a) {
  * ascending (model.c:1020-1037), by the nth threads of one workgroup. ids: the T*K
  * chosen experts (LDS or global); cnt/base: LDS scratch of E ints. Writes the pair
  * lists, the active-slot lists and the slot descriptors (unused slots get n = 0). */
-__device__ void bucket_pairs(const RouteArgs &a, const int *ids, int *cnt, int *base, int tid, int nth) {
-    const int E = a.E, P = a.T * a.K;
+/* u64 words of the per-expert token masks (ceil(T / 64) words per expert) */
+constexpr int BK_MASKW = 2048;
+
+__device__ void bucket_pairs(const RouteArgs &a, const int *ids, int *cnt, int *base, unsigned long long *tm, int tid,
+                             int nth) {
+    const int E = a.E, P = a.T * a.K, nw = (a.T + 63) >> 6;
+    const bool masks = nw * E <= BK_MASKW;
     for (int e = tid; e < E; e += nth) cnt[e] = 0;
+    if (masks)
+        for (int i = tid; i < nw * E; i += nth) tm[i] = 0ull;
     __syncthreads();
-    for (int p = tid; p < P; p += nth) atomicAdd(&cnt[ids[p]], 1);
+    for (int p = tid; p < P; p += nth) {
+        const int e = ids[p];
+        atomicAdd(&cnt[e], 1);
+        if (masks) {
+            const int t = p / a.K;
+            atomicOr(&tm[e * nw + (t >> 6)], 1ull << (t & 63));
+        }
+    }
     __syncthreads();
     __shared__ int nu_sh;
     if (tid < 64) {
@@ -578,9 +592,23 @@ __device__ void bucket_pairs(const RouteArgs &a, const int *ids, int *cnt, int *
     __syncthreads();
     for (int u = nu_sh + tid; u < a.n_slots; u += nth) a.desc[u].n = 0;
     /* pair p goes after the earlier pairs of its expert (tokens ascending within an
-     * expert, model.c:1030-1035): its rank = how many pairs q < p have the same id */
+     * expert, model.c:1030-1035): its rank = how many pairs q < p have the same id.
+     * A token's K experts are distinct (route_select picks distinct experts; replayed
+     * rows are checked), so with the token masks that is the number of tokens below
+     * p's token that chose the expert */
     for (int p = tid; p < P; p += nth) {
         const int e = ids[p];
+        if (masks) {
+            const int t = p / a.K, w0 = t >> 6;
+            const unsigned long long *m = tm + (size_t)e * nw;
+            int r = 0;
+            for (int w = 0; w < w0; w++) r += __popcll(m[w]);
+            r += __popcll(m[w0] & ((1ull << (t & 63)) - 1ull));
+            const int pos = base[e] + r;
+            a.pair_tok[pos] = t;
+            a.pair_of[p] = pos;
+            continue;
+        }
         int r = 0, q = 0;
         for (; q + 8 <= p; q += 8) {
             int v[8];
@@ -602,12 +630,13 @@ constexpr int BUCKET_PMAX = 8192;
 __global__ __launch_bounds__(1024) void k_route_bucket(RouteArgs a) {
     __shared__ int cnt[ROUTE_EMAX], base[ROUTE_EMAX];
     __shared__ int pid[BUCKET_PMAX];
+    __shared__ unsigned long long tmk[BK_MASKW];
     const int tid = threadIdx.x, nth = blockDim.x, P = a.T * a.K;
     const bool in_lds = P <= BUCKET_PMAX;
     if (in_lds)
         for (int p = tid; p < P; p += nth) pid[p] = a.ids[p];
     __syncthreads();
-    bucket_pairs(a, in_lds ? pid : a.ids, cnt, base, tid, nth);
+    bucket_pairs(a, in_lds ? pid : a.ids, cnt, base, tmk, tid, nth);
 }
 
 /* Ungrouped routing of up to 16 tokens (E <= 256, K <= 64) and their bucketing in one
