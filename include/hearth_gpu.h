@@ -63,9 +63,10 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
  * draft length, the drafts accepted and the tokens handled of step s (3 * max_steps
  * entries). Afterwards pos is the position generate() leaves: n_seq - 1 plus the
  * committed tokens, or at most the committed sequence's length once the run has ended.
- * Returns -1 when the engine cannot run the loop (expert streaming, route replay or a
- * routing trace, profiling; see hearth_gpu_spec_loop_ok). No counterpart in the
- * reference's C API. */
+ * Limits: draft_len + 1 <= min(max_batch, 128), n_stop <= 64, max_steps <= 1024.
+ * Returns -1 for arguments outside them, and when the engine cannot run the loop
+ * (expert streaming, route replay or a routing trace, profiling; see
+ * hearth_gpu_spec_loop_ok). No counterpart in the reference's C API. */
 #define HEARTH_GPU_SPEC_MAX_STEPS 1024
 #define HEARTH_GPU_SPEC_RUNNING 0   /* max_steps ran (or the capacity ended them) */
 #define HEARTH_GPU_SPEC_STOP 1      /* a stop token ended the run */
