@@ -225,6 +225,20 @@ struct hearth_engine {
     std::unique_ptr<GpuExpertStore> store;
     int *h_meta = nullptr;   /* pinned [1 + E]: n_active, active experts of a layer */
     StoreStats store_base;   /* store counters at hearth_reset_stats */
+    /* With the expert cache, a call that fails (a load that could not be enqueued) must
+     * leave the statistics as they were: the store's counters and the routing counters
+     * dstats[0..1] (copied to dstats[2..3] at the start of the call, in stream order) are
+     * put back. Without the cache a failure is a device error and nothing is kept. */
+    void call_mark() {
+        if (!store) return;
+        store->mark();
+        (void)hipMemcpyAsync(dstats + 2, dstats, 2 * sizeof(unsigned long long), hipMemcpyDeviceToDevice, st);
+    }
+    void call_rollback() {
+        if (!store) return;
+        store->rollback();
+        (void)hipMemcpyAsync(dstats, dstats + 2, 2 * sizeof(unsigned long long), hipMemcpyDeviceToDevice, st);
+    }
     /* next-layer prediction (model.c:935-984): router of the next MoE layer on the
      * predicted input, top_k + prefetch_extra per token, union over the batch */
     float *pxs = nullptr, *plog = nullptr, *h_plog = nullptr;   /* [B][D], [B][E], pinned [B][E] */
@@ -1324,6 +1338,7 @@ int hearth_engine::eval_chunked(const int32_t *tok, int n, float *logits_out, in
     const int start = pos;
     const uint64_t tokens0 = tokens_done, calls0 = forward_calls;
     trace_pend.clear();
+    call_mark();
     try {
         for (int off = 0; off < n; off += B) {
             const int T = std::min(B, n - off);
@@ -1355,6 +1370,7 @@ int hearth_engine::eval_chunked(const int32_t *tok, int n, float *logits_out, in
         if (profiling) collect_events();
     } catch (const DeviceError &e) {
         log_msg(LOG_ERROR, "HIP error in hearth_eval: %s", hipGetErrorString(e.e));
+        call_rollback();
         pos = start;
         tokens_done = tokens0;
         forward_calls = calls0;
@@ -1688,6 +1704,7 @@ HEARTH_API int hearth_verify_tree(hearth_engine *e, const int32_t *tokens, const
     if (hipSetDevice(e->dev) != hipSuccess) return E_IO;
     const double t0 = now_s();
     e->trace_pend.clear();
+    e->call_mark();
     try {
         e->run_geometry(tokens, parent, n, logits, false);
         e->write_trace(n);
@@ -1695,6 +1712,7 @@ HEARTH_API int hearth_verify_tree(hearth_engine *e, const int32_t *tokens, const
         if (e->profiling) e->collect_events();
     } catch (const DeviceError &err) {
         log_msg(LOG_ERROR, "HIP error in hearth_verify_tree: %s", hipGetErrorString(err.e));
+        e->call_rollback();
         e->trace_pend.clear();
         return E_IO;
     }
@@ -1756,6 +1774,7 @@ int verify_and_commit(hearth_engine *e, const int32_t *tokens, const int32_t *pa
     const double t0 = now_s();
     int np = 0, fin = -1, status = 0;
     e->trace_pend.clear();
+    e->call_mark();
     try {
         e->run_geometry(tokens, parent, n, nullptr, false);
         /* logits stay in HBM; the head ran only if requested -> force it here */
@@ -1787,6 +1806,7 @@ int verify_and_commit(hearth_engine *e, const int32_t *tokens, const int32_t *pa
         if (e->profiling) e->collect_events();
     } catch (const DeviceError &err) {
         log_msg(LOG_ERROR, "HIP error in %s: %s", what, hipGetErrorString(err.e));
+        e->call_rollback();
         e->trace_pend.clear();
         return E_IO;
     }

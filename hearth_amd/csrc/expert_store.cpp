@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdlib>
 #include <cstring>
 #include <unordered_map>
 
@@ -81,6 +82,7 @@ bool GpuExpertStore::open(const ModelFile &mf, int L, int E, int D, int F, int n
                           std::string &msg) {
     mf_ = &mf;
     L_ = L; E_ = E; D_ = D; F_ = F; n_slots_ = n_slots; policy_ = policy;
+    if (const char *fl = std::getenv("HEARTH_GPU_STORE_FAIL_LOAD")) fail_load_ = std::atoll(fl);
     room_ = room_dtype(mf, L, E);
     slot_bytes_ = slot_bytes_for(D, F, room_);
     for (int l = 0; l < L; l++)
@@ -215,6 +217,7 @@ void GpuExpertStore::evict(int s) {
 }
 
 void GpuExpertStore::load(int key, int s) {
+    if (fail_load_ > 0 && ++n_load_calls_ == fail_load_) throw DeviceError{hipErrorInvalidValue};
     hxd::ExpertW &w = slot_[s].w;
     uint8_t *sb = pool_ + (uint64_t)s * slot_bytes_;
     if (tier_) {   /* one copy of the slot image */
@@ -272,89 +275,126 @@ void GpuExpertStore::harvest(bool wait) {
 
 void GpuExpertStore::ensure(int layer, const int *experts, int n, hxd::ExpertW *table_dev, hipStream_t compute) {
     const double t0 = now_s();
+    const StoreStats st0 = stats;
     bool batch = false;
+    int pend_key = -1, pend_slot = -1;   /* the miss whose load is being enqueued */
     std::fill(busy_.begin(), busy_.end(), 0);
-    /* hits first, so that no miss of this layer evicts them */
-    for (int j = 0; j < n; j++) {
-        const int key = layer * E_ + experts[j], s = slot_of_[key];
-        if (s >= 0) busy_[s] = 1;
-    }
-    for (int j = 0; j < n; j++) {
-        const int e = experts[j], key = layer * E_ + e;
-        int s = slot_of_[key];
-        if (s >= 0) {
-            stats.hits++;
-            if (slot_[s].pf_unused) {
-                slot_[s].pf_unused = false;
-                stats.prefetch_used++;
-            }
-        } else {
-            stats.misses++;
-            if (!free_.empty()) {
-                s = free_.back();
-                free_.pop_back();
-            } else {
-                s = victim(true);
-                evict(s);
-            }
-            slot_[s].key = key;
-            slot_of_[key] = s;
-            busy_[s] = 1;
-            if (!batch) batch_begin();
-            batch = true;
-            load(key, s);
+    try {
+        /* hits first, so that no miss of this layer evicts them */
+        for (int j = 0; j < n; j++) {
+            const int key = layer * E_ + experts[j], s = slot_of_[key];
+            if (s >= 0) busy_[s] = 1;
         }
-        slot_[s].prot_tick = 0;
-        slot_[s].last_tick = now_;
-        slot_[s].last_seq = ++seq_;
-        heat_[key] += 1.0;
-        htable_[e] = slot_[s].w;
+        for (int j = 0; j < n; j++) {
+            const int e = experts[j], key = layer * E_ + e;
+            int s = slot_of_[key];
+            if (s >= 0) {
+                stats.hits++;
+                if (slot_[s].pf_unused) {
+                    slot_[s].pf_unused = false;
+                    stats.prefetch_used++;
+                }
+            } else {
+                stats.misses++;
+                if (!free_.empty()) {
+                    s = free_.back();
+                    free_.pop_back();
+                } else {
+                    s = victim(true);
+                    evict(s);
+                }
+                slot_[s].key = key;
+                slot_of_[key] = s;
+                busy_[s] = 1;
+                pend_key = key;
+                pend_slot = s;
+                if (!batch) batch_begin();
+                batch = true;
+                load(key, s);
+                pend_key = pend_slot = -1;
+            }
+            slot_[s].prot_tick = 0;
+            slot_[s].last_tick = now_;
+            slot_[s].last_seq = ++seq_;
+            heat_[key] += 1.0;
+            htable_[e] = slot_[s].w;
+        }
+        if (batch) batch_end();
+        ck(hipMemcpyAsync(table_dev, htable_, sizeof(hxd::ExpertW) * (size_t)E_, hipMemcpyHostToDevice, cs_));
+        ck(hipEventRecord(done_, cs_));
+        ck(hipStreamWaitEvent(compute, done_, 0));
+    } catch (const DeviceError &) {
+        /* the slot whose load did not enqueue holds no expert: unmap it, so that no later
+         * call counts it as a hit */
+        if (pend_key >= 0) unmap(pend_key, pend_slot);
+        if (batch) (void)hipEventRecord(ev_pend_.back().second, cs_);   /* close the batch's event pair */
+        stats = st0;
+        throw;
     }
-    if (batch) batch_end();
-    ck(hipMemcpyAsync(table_dev, htable_, sizeof(hxd::ExpertW) * (size_t)E_, hipMemcpyHostToDevice, cs_));
-    ck(hipEventRecord(done_, cs_));
-    ck(hipStreamWaitEvent(compute, done_, 0));
     stats.load_s += now_s() - t0;
 }
 
 void GpuExpertStore::prefetch(int layer, const int *experts, int n) {
     const double t0 = now_s();
+    const StoreStats st0 = stats;
     bool batch = false;
-    for (int j = 0; j < n; j++) {
-        const int key = layer * E_ + experts[j];
-        const int r = slot_of_[key];
-        if (r >= 0) {   /* resident: keep it for the coming demand */
-            slot_[r].prot_tick = now_ + 1;
-            continue;
-        }
-        int s;
-        if (!free_.empty()) {
-            s = free_.back();
-            free_.pop_back();
-        } else {
-            s = victim(false);
-            if (s >= 0) {   /* never a hot expert (store.c:207-214) */
-                const Slot &v = slot_[s];
-                if (policy_ == HEARTH_POLICY_LFU ? heat_[v.key] >= HOT_HEAT : v.last_tick == now_) s = -1;
-            }
-            if (s < 0) {
-                stats.prefetch_dropped++;
+    int pend_key = -1, pend_slot = -1;
+    try {
+        for (int j = 0; j < n; j++) {
+            const int key = layer * E_ + experts[j];
+            const int r = slot_of_[key];
+            if (r >= 0) {   /* resident: keep it for the coming demand */
+                slot_[r].prot_tick = now_ + 1;
                 continue;
             }
-            evict(s);
+            int s;
+            if (!free_.empty()) {
+                s = free_.back();
+                free_.pop_back();
+            } else {
+                s = victim(false);
+                if (s >= 0) {   /* never a hot expert (store.c:207-214) */
+                    const Slot &v = slot_[s];
+                    if (policy_ == HEARTH_POLICY_LFU ? heat_[v.key] >= HOT_HEAT : v.last_tick == now_) s = -1;
+                }
+                if (s < 0) {
+                    stats.prefetch_dropped++;
+                    continue;
+                }
+                evict(s);
+            }
+            Slot &x = slot_[s];
+            x.key = key;
+            x.pf_unused = true;
+            x.prot_tick = now_ + 1;
+            slot_of_[key] = s;
+            pend_key = key;
+            pend_slot = s;
+            if (!batch) batch_begin();
+            batch = true;
+            load(key, s);
+            pend_key = pend_slot = -1;
+            stats.prefetch_issued++;
         }
-        Slot &x = slot_[s];
-        x.key = key;
-        x.pf_unused = true;
-        x.prot_tick = now_ + 1;
-        slot_of_[key] = s;
-        if (!batch) batch_begin();
-        batch = true;
-        load(key, s);
-        stats.prefetch_issued++;
+        if (batch) batch_end();
+    } catch (const DeviceError &) {
+        if (pend_key >= 0) unmap(pend_key, pend_slot);
+        if (batch) (void)hipEventRecord(ev_pend_.back().second, cs_);   /* close the batch's event pair */
+        stats = st0;
+        throw;
     }
-    if (batch) batch_end();
     stats.load_s += now_s() - t0;
+}
+
+/* slot s, mapped to key but without its bytes: back to the free list */
+void GpuExpertStore::unmap(int key, int s) {
+    slot_of_[key] = -1;
+    Slot &x = slot_[s];
+    x.key = -1;
+    x.pf_unused = false;
+    x.prot_tick = 0;
+    busy_[s] = 0;
+    free_.push_back(s);
 }
 
 void GpuExpertStore::tick() {

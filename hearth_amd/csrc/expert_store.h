@@ -72,6 +72,12 @@ public:
     void prefetch(int layer, const int *experts, int n);
     /* forward boundary: LFU heat decay, protection expires */
     void tick();
+    /* start of an API call that may run forwards: remembers the counters; rollback()
+     * (after that call failed) puts them back, so a failed call leaves the statistics
+     * as they were. Residency is not rolled back: every slot still mapped holds a load
+     * that was enqueued in full. */
+    void mark() { mark_ = stats; }
+    void rollback() { stats = mark_; }
     /* the widest expert dtype of the container's MoE layers (Q8 if any expert is Q8) */
     static int room_dtype(const ModelFile &mf, int L, int E);
     /* HBM bytes of one slot for experts of D x F stored as `room` (Q8 or Q4) */
@@ -86,6 +92,10 @@ public:
     StoreStats stats;
 
 private:
+    StoreStats mark_;
+    /* HEARTH_GPU_STORE_FAIL_LOAD=n at open: the n-th load since open fails once with a
+     * HIP error before anything is enqueued (host-side test of the failure path) */
+    long long fail_load_ = 0, n_load_calls_ = 0;
     struct Slot {
         int key = -1;
         uint64_t last_seq = 0;
@@ -126,6 +136,7 @@ private:
     bool cheaper(int a, int b) const;
     int victim(bool allow_protected);
     void evict(int s);
+    void unmap(int key, int s);
     void load(int key, int slot);
 };
 

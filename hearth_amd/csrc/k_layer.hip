@@ -539,12 +539,15 @@ constexpr int BK_MASKW = 2048;
 __device__ void bucket_pairs(const RouteArgs &a, const int *ids, int *cnt, int *base, unsigned long long *tm, int tid,
                              int nth) {
     const int E = a.E, P = a.T * a.K, nw = (a.T + 63) >> 6;
+    /* pairs of padding tokens (t >= *live, which routed from token 0's logits) are not
+     * bucketed: each reads token 0's pair of the same rank, which is its expert's first */
+    const int PL = (a.live ? *a.live : a.T) * a.K;
     const bool masks = nw * E <= BK_MASKW;
     for (int e = tid; e < E; e += nth) cnt[e] = 0;
     if (masks)
         for (int i = tid; i < nw * E; i += nth) tm[i] = 0ull;
     __syncthreads();
-    for (int p = tid; p < P; p += nth) {
+    for (int p = tid; p < PL; p += nth) {
         const int e = ids[p];
         atomicAdd(&cnt[e], 1);
         if (masks) {
@@ -584,7 +587,7 @@ __device__ void bucket_pairs(const RouteArgs &a, const int *ids, int *cnt, int *
             nu_sh = nu_run;
             *a.n_active = nu_run;
             if (a.stats) {
-                a.stats[0] += (unsigned long long)P;
+                a.stats[0] += (unsigned long long)PL;
                 a.stats[1] += (unsigned long long)nu_run;
             }
         }
@@ -598,6 +601,10 @@ __device__ void bucket_pairs(const RouteArgs &a, const int *ids, int *cnt, int *
      * p's token that chose the expert */
     for (int p = tid; p < P; p += nth) {
         const int e = ids[p];
+        if (p >= PL) {
+            a.pair_of[p] = base[e];
+            continue;
+        }
         if (masks) {
             const int t = p / a.K, w0 = t >> 6;
             const unsigned long long *m = tm + (size_t)e * nw;

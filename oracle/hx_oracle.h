@@ -41,8 +41,8 @@
  * Attention mode (ho_set_attn_mode):
  *   HO_ATTN_CANONICAL  the reference's order (engine/src/model.c:519-589): dot16 scores,
  *                      one softmax over the whole row list, sequential value sums.
- *   HO_ATTN_CHUNKED    the GPU engine's default order for GQA attention: the row list in
- *                      chunks of HO_ATTN_CHUNK rows, one partial softmax and value sum per
+ *   HO_ATTN_CHUNKED    the GPU engine's opt-in order for GQA attention (its default is the
+ *                      canonical order): the row list in chunks of HO_ATTN_CHUNK rows, one partial softmax and value sum per
  *                      chunk, combined in chunk order (ho_set_attn_mode documents the exact
  *                      steps). Within the north star's tolerance of the reference, not
  *                      bit-exact to it; no reference counterpart (the reference allows a GPU

@@ -200,3 +200,39 @@ def test_host_tier_equals_staged_loads(tiny_model, monkeypatch):
         assert info["copy_s"] > 0.0
     keys = ("cache_hits", "cache_misses", "evictions", "bytes_read")
     assert [got["1"][1][k] for k in keys] == [got["0"][1][k] for k in keys]
+
+
+@pytest.mark.parametrize("tier", ["1", "0"])
+@pytest.mark.parametrize("fail_at", [1, 7, 23])
+def test_failed_load_changes_nothing(tiny_model, monkeypatch, tier, fail_at):
+    """HEARTH_GPU_STORE_FAIL_LOAD=n makes the n-th expert load since open fail once on the
+    host, before anything is enqueued (hearth.h:131-132: a failed call changes nothing).
+    The call returns an error with the position and every counter as before it; the slot
+    whose load failed is not left mapped, so the same call run again is a miss there,
+    loads the expert and gives the resident engine's logits bit for bit."""
+    toks = [int(t) for t in container.uniform_ints(55, 60, container.TINY.vocab)]
+    calls = [toks[:30], toks[30:39], toks[39:48]]
+    ref, _ = _run(tiny_model, calls)
+    monkeypatch.setenv("HEARTH_GPU_EXPERT_CACHE_GB", "0.0001")
+    monkeypatch.setenv("HEARTH_GPU_HOST_TIER", tier)
+    monkeypatch.setenv("HEARTH_GPU_STORE_FAIL_LOAD", str(fail_at))
+    failed = 0
+    with Engine(tiny_model, max_seq=512, prefetch="off") as e:
+        got = []
+        for c in calls:
+            before_pos, before = e.pos, e.stats()
+            try:
+                got.append(e.eval(c, all_logits=True))
+            except Exception:
+                failed += 1
+                assert e.pos == before_pos
+                after = e.stats()
+                for k in ("cache_hits", "cache_misses", "evictions", "bytes_read", "expert_loads_unique"):
+                    assert after[k] == before[k], k
+                got.append(e.eval(c, all_logits=True))   # the injected failure fires once
+        st = e.stats()
+    assert failed == 1
+    for a, b in zip(ref, got):
+        assert np.array_equal(_bits(a), _bits(b))
+    assert st["cache_hits"] + st["cache_misses"] == st["expert_loads_unique"]
+    assert st["bytes_read"] == st["cache_misses"] * 208896
