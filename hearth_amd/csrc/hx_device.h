@@ -172,9 +172,11 @@ __constant__ static const unsigned long long HX_EXP2F_TAB[32] = {
 
 /* the glibc expf; written without branches (the special inputs are selected at the end,
  * the arithmetic runs on them too with a masked table index), so calls interleave.
- * tab: the 32 table entries, from HX_EXP2F_TAB or a copy in LDS (exp_table_to_lds): a
- * per-lane gather from LDS costs far less than one through the vector memory path. */
-__device__ inline float exp_glibc_f(float x, const unsigned long long *tab) {
+ * tab(i) returns table entry i: from HX_EXP2F_TAB, from a copy in LDS (exp_table_to_lds:
+ * a per-lane gather from LDS costs far less than one through the vector memory path) or
+ * from the wave's registers (exp_glibc_f_wave). */
+template <typename Fetch>
+__device__ __forceinline__ float exp_glibc_core(float x, Fetch tab) {
     const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32.0;
     const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
@@ -186,7 +188,7 @@ __device__ inline float exp_glibc_f(float x, const unsigned long long *tab) {
     const unsigned long long ki = (unsigned long long)__double_as_longlong(kd);
     kd = dsub(kd, shift);
     const double r = __builtin_fma(inv_ln2_32, xd, -kd);
-    const double s = __longlong_as_double((long long)(tab[ki & 31] + (ki << 47)));
+    const double s = __longlong_as_double((long long)(tab((int)(ki & 31)) + (ki << 47)));
     const double z = __builtin_fma(c0, r, c1), r2 = dmul(r, r);
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
@@ -199,7 +201,25 @@ __device__ inline float exp_glibc_f(float x, const unsigned long long *tab) {
     return res;
 }
 
+__device__ inline float exp_glibc_f(float x, const unsigned long long *tab) {
+    return exp_glibc_core(x, [&](int i) { return tab[i]; });
+}
+
 __device__ __forceinline__ float exp_glibc_f(float x) { return exp_glibc_f(x, HX_EXP2F_TAB); }
+
+/* the table entry a lane holds for exp_glibc_f_wave: entry lane % 32, loaded once (early:
+ * nothing waits for it until the first exp) */
+__device__ __forceinline__ unsigned long long exp_table_lane() { return HX_EXP2F_TAB[threadIdx.x & 31]; }
+
+/* exp_glibc_f with the table in the registers of the wave (ev = exp_table_lane()), read by
+ * ds_bpermute (no LDS memory, no barrier). Every lane of the wave must be active. */
+__device__ inline float exp_glibc_f_wave(float x, unsigned long long ev) {
+    return exp_glibc_core(x, [&](int i) {
+        const unsigned lo = (unsigned)__builtin_amdgcn_ds_bpermute(i << 2, (int)(unsigned)ev);
+        const unsigned hi = (unsigned)__builtin_amdgcn_ds_bpermute(i << 2, (int)(unsigned)(ev >> 32));
+        return ((unsigned long long)hi << 32) | lo;
+    });
+}
 
 /* copies the exp table into an LDS array of 32 entries (threads 0..31 of the block; the
  * caller synchronizes before use) */

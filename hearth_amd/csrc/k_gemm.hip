@@ -570,6 +570,8 @@ template <int DT, int MODE>
 __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, int gmax, int n_slots) {
     constexpr bool DOWN = MODE == TK_DOWN, QF = MODE == TK_GATEUP_Q;
     extern __shared__ __attribute__((aligned(16))) uint8_t tk_lds[];
+    /* the exp table of the SwiGLU epilogue, one entry per lane, loaded with the weights */
+    const unsigned long long ev = DOWN ? 0ull : exp_table_lane();
     constexpr int NP = TkCfg<DT>::NP, NV = TkCfg<DT>::NV, NBK = 2 * NP, NM = DOWN ? 1 : 2;
     const int rows_out = DOWN ? a.D : a.F;
     const int ntile = (rows_out + 15) / 16, tpw = (ntile + rpw - 1) / rpw;
@@ -757,11 +759,14 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
         return;
     }
     float mv = 0.0f;
-    if (out) {
+    {
+        /* every lane takes the exp (the table is read across the wave); the outputs keep it */
         const float gv = canon(acc[0]), uv = canon(acc[NM - 1]);
-        const float sg = fdiv(gv, fadd(1.0f, exp_glibc_f(-gv)));
-        mv = fmul(sg, uv);
-        if (!QF) a.midf[(size_t)(p0 + col) * a.F + row] = mv;
+        const float sg = fdiv(gv, fadd(1.0f, exp_glibc_f_wave(-gv, ev)));
+        if (out) {
+            mv = fmul(sg, uv);
+            if (!QF) a.midf[(size_t)(p0 + col) * a.F + row] = mv;
+        }
     }
     if constexpr (QF) {
         /* the workgroup's rows [16 rpw tile, +16 rpw) are whole blocks of F: the last

@@ -667,8 +667,9 @@ static_assert(__builtin_offsetof(SlotDesc, p0) == sizeof(ExpertW) && __builtin_o
 /* routing of token t by one wave (lane e % 64 holds expert e, NU experts per lane):
  * scores into sc, then the K experts, their weights, and the token's bits in tmask */
 template <int NU>
-__device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, const float (&lgv)[RS_EMAX / 64], float *sc,
-                                                  int *pid, uint32_t *tmask) {
+__device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, const float (&lgv)[RS_EMAX / 64],
+                                                  const float (&bv)[RS_EMAX / 64], int live, float *sc, int *pid,
+                                                  uint32_t *tmask) {
     const int lane = threadIdx.x & 63, E = a.E, K = a.K;
     float x[NU];
     bool ok[NU];
@@ -722,7 +723,7 @@ __device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, con
 #pragma unroll
         for (int u = 0; u < NU; u++) {
             const int e = lane + 64 * u;
-            kk[u] = order_key(a.bias && ok[u] ? fadd(x[u], a.bias[e]) : x[u]);
+            kk[u] = order_key(a.bias && ok[u] ? fadd(x[u], bv[u]) : x[u]);
             live[u] = ok[u];
         }
         for (int j = 0; j < K; j++) {
@@ -754,7 +755,7 @@ __device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, con
         a.ids[(size_t)t * K + lane] = my_id;
         a.wts[(size_t)t * K + lane] = w;
         pid[t * K + lane] = my_id;
-        if (!a.live || t < *a.live) atomicOr(&tmask[my_id], 1u << t);   /* padding tokens add no pair */
+        if (t < live) atomicOr(&tmask[my_id], 1u << t);   /* padding tokens add no pair */
         if (a.route_out) a.route_out[((size_t)t * a.n_moe + a.moe_ord) * K + lane] = my_id;
     }
 }
@@ -791,30 +792,35 @@ __device__ __forceinline__ void route_small_stage(const RouteArgs &a, RouteSmem 
     for (int e = tid; e < a.E; e += nth) rs.tmask[e] = 0u;
 }
 
-/* logits of token t, expert lane + 64 u, into registers */
-__device__ __forceinline__ void route_small_logits(const RouteArgs &a, const float *logits, int t, float (&lgv)[RS_EMAX / 64]) {
+/* logits of token t and of token 0 (the row of padding tokens), and the selection bias,
+ * expert lane + 64 u, into registers: every load issued at once */
+__device__ __forceinline__ void route_small_logits(const RouteArgs &a, const float *logits, int t, float (&lgv)[RS_EMAX / 64],
+                                                   float (&lg0)[RS_EMAX / 64], float (&bv)[RS_EMAX / 64]) {
     const int lane = threadIdx.x & 63;
     const float *lg = logits + (size_t)t * a.E;
 #pragma unroll
     for (int u = 0; u < RS_EMAX / 64; u++) {
         const int e = lane + 64 * u;
         lgv[u] = e < a.E ? lg[e] : 0.0f;
+        lg0[u] = e < a.E && a.live ? logits[e] : 0.0f;
+        bv[u] = e < a.E && a.bias ? a.bias[e] : 0.0f;
     }
 }
 
 /* token t's routing by the calling wave */
-__device__ __forceinline__ void route_small_token(const RouteArgs &a, RouteSmem &rs, int t, const float (&lgv)[RS_EMAX / 64]) {
+__device__ __forceinline__ void route_small_token(const RouteArgs &a, RouteSmem &rs, int t, const float (&lgv)[RS_EMAX / 64],
+                                                  const float (&bv)[RS_EMAX / 64], int live) {
     switch ((a.E + 63) / 64) {
-    case 1: route_token_small<1>(a, t, lgv, rs.score[t], rs.pid, rs.tmask); break;
-    case 2: route_token_small<2>(a, t, lgv, rs.score[t], rs.pid, rs.tmask); break;
-    case 3: route_token_small<3>(a, t, lgv, rs.score[t], rs.pid, rs.tmask); break;
-    default: route_token_small<4>(a, t, lgv, rs.score[t], rs.pid, rs.tmask); break;
+    case 1: route_token_small<1>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask); break;
+    case 2: route_token_small<2>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask); break;
+    case 3: route_token_small<3>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask); break;
+    default: route_token_small<4>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask); break;
     }
 }
 
 /* bucketing after every token is routed: scan of the pair counts, pair places, slot
  * descriptors (all threads of the workgroup call it) */
-__device__ __forceinline__ void route_small_bucket(const RouteArgs &a, RouteSmem &rs, int tid, int nth) {
+__device__ __forceinline__ void route_small_bucket(const RouteArgs &a, RouteSmem &rs, int tid, int nth, int live) {
     const int E = a.E, K = a.K, P = a.T * K, wave = tid >> 6, lane = tid & 63;
     __syncthreads();
     if (wave == 0) {
@@ -840,14 +846,14 @@ __device__ __forceinline__ void route_small_bucket(const RouteArgs &a, RouteSmem
         if (lane == 0) {
             rs.nu = nu_run;
             *a.n_active = nu_run;
-            if (a.stats) {
-                a.stats[0] += (unsigned long long)run;
-                a.stats[1] += (unsigned long long)nu_run;
+            if (a.stats) {   /* counters only: no return value, nothing waits for them */
+                atomicAdd(&a.stats[0], (unsigned long long)run);
+                atomicAdd(&a.stats[1], (unsigned long long)nu_run);
             }
         }
     }
     __syncthreads();
-    const int nu = rs.nu, live = a.live ? *a.live : a.T;
+    const int nu = rs.nu;
     for (int p = tid; p < P; p += nth) {
         const int e = rs.pid[p], tt = p / K;
         if (tt >= live) {   /* a padding token reads token 0's pair of the same rank (same expert) */
@@ -879,12 +885,21 @@ __device__ __forceinline__ void route_small_bucket(const RouteArgs &a, RouteSmem
 __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
     __shared__ RouteSmem rs;
     const int tid = threadIdx.x, nth = blockDim.x, t = tid >> 6;
-    float lgv[RS_EMAX / 64];
-    if (t < a.T) route_small_logits(a, a.logits, route_row(a, t), lgv);
+    /* the padding bound is read with the logits (route_row would make the logit loads
+     * wait for it): padding tokens take token 0's logits */
+    const int live = a.live ? *a.live : a.T;
+    float lgv[RS_EMAX / 64], lg0[RS_EMAX / 64], bv[RS_EMAX / 64];
+    if (t < a.T) route_small_logits(a, a.logits, t, lgv, lg0, bv);
     route_small_stage(a, rs, tid, nth);
     __syncthreads();
-    if (t < a.T) route_small_token(a, rs, t, lgv);
-    route_small_bucket(a, rs, tid, nth);
+    if (t < a.T) {
+        if (t >= live) {
+#pragma unroll
+            for (int u = 0; u < RS_EMAX / 64; u++) lgv[u] = lg0[u];
+        }
+        route_small_token(a, rs, t, lgv, bv, live);
+    }
+    route_small_bucket(a, rs, tid, nth, live);
 }
 
 /* ------------------------------------------------------------ GQA post-processing */
