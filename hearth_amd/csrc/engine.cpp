@@ -168,7 +168,8 @@ struct hearth_engine {
     struct Captured {
         int T, chain, rows;
         bool logits;
-        bool loop;           /* a whole step of the greedy loop (loop_step), not a forward alone */
+        bool loop;           /* a whole step of the device loop (loop_step), not a forward alone */
+        uint64_t skey;       /* loop steps: the sampler they accept with (0: greedy) */
         hipGraph_t graph;
         hipGraphExec_t exec;
     };
@@ -212,6 +213,14 @@ struct hearth_engine {
     int lp_rtab_rows = 0;
     int *h_lp = nullptr;                 /* pinned: the done flags of the steps in flight, then the state */
     hipEvent_t lp_ev[2] = {nullptr, nullptr};
+    /* sampled runs (hearth_gpu_spec_sample): the acceptance scratch of the loop (its own,
+     * so that growing the call-by-call scratch never moves what a captured step reads),
+     * the run's uniform stream, the sampler, and its key among the captured steps (0:
+     * greedy acceptance) */
+    hxl::SampleScratch lp_samp;
+    double *lp_ustream = nullptr;
+    hxl::SamplerSpec lp_spec{};
+    uint64_t lp_skey = 0;
     const int *route_live = nullptr;     /* RouteArgs.live of the forwards being launched */
     void loop_prepare();
     void loop_rope_table(int rows);
@@ -299,6 +308,7 @@ struct hearth_engine {
         if (geom_ev) (void)hipEventDestroy(geom_ev);
         for (void *p : allocs) (void)hipFree(p);
         samp.release();
+        lp_samp.release();
         if (h_geom) (void)hipHostFree(h_geom);
         if (h_rope) (void)hipHostFree(h_rope);
         if (h_res) (void)hipHostFree(h_res);
@@ -1178,7 +1188,7 @@ void hearth_engine::run_forward(int T, bool want_logits) {
             (void)hipGraphDestroy(graphs.front().graph);
             graphs.erase(graphs.begin());
         }
-        Captured g{T, geom_chain, rows, want_logits, false, nullptr, nullptr};
+        Captured g{T, geom_chain, rows, want_logits, false, 0, nullptr, nullptr};
         ck(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         rows_bound = rows;
         try {
@@ -1214,6 +1224,7 @@ void hearth_engine::loop_prepare() {
     lp_par = dnew<int>(B);
     lp_path = dnew<int>(B);
     if (rope_dim) lp_rtab = dnew<float>((size_t)cap * rope_dim);
+    lp_ustream = dnew<double>((size_t)HEARTH_GPU_SPEC_MAX_STEPS * 128);
     if (!h_lp) ck(hipHostMalloc((void **)&h_lp, sizeof(int) * hxd::LS_FIELDS, hipHostMallocDefault));
     for (hipEvent_t &ev : lp_ev)
         if (!ev) ck(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
@@ -1244,7 +1255,15 @@ hxd::LoopArgs hearth_engine::loop_args(int T) {
     a.state = lp_state; a.hist = lp_hist; a.hist_cap = cap + B + 2; a.stops = lp_stops;
     a.out = lp_out; a.out_cap = HEARTH_GPU_SPEC_MAX_STEPS * B; a.rec = lp_rec; a.rec_cap = HEARTH_GPU_SPEC_MAX_STEPS;
     a.tokens = tokens; a.cmp = lp_cmp; a.rope = rope; a.rtab = lp_rtab; a.rope_dim = rope_dim; a.cap = cap;
-    a.pos = d_pos; a.result = acc_i + 2 * B; a.T = T;
+    a.pos = d_pos; a.result = lp_skey ? lp_samp.result : acc_i + 2 * B; a.T = T;
+    if (lp_skey) {
+        /* temperature 0 (a penalised argmax) draws nothing: zero uniforms, as the host
+         * steps pass */
+        a.sampled = lp_spec.temperature > 0.0;
+        a.ustream = a.sampled ? lp_ustream : nullptr;
+        a.ustream_n = HEARTH_GPU_SPEC_MAX_STEPS * 128;
+        a.u = lp_samp.u;
+    }
     return a;
 }
 
@@ -1254,6 +1273,14 @@ void hearth_engine::loop_step(int T) {
     const hxd::LoopArgs la = loop_args(T);
     hxl::loop_draft(la, st);
     forward(T, true, 0);
+    if (lp_skey) {
+        /* the sampled walk over the live rows (the chain parents of lp_par), penalty context
+         * = the committed sequence (it ends with the step's first token) */
+        ck(hxl::accept_sample_dev(lp_samp, logits, T, V, tokens, lp_par, lp_spec, lp_hist, lp_state + hxd::LS_LEN,
+                                  lp_state + hxd::LS_LIVE, st));
+        hxl::loop_commit(la, st);
+        return;
+    }
     hxd::AcceptArgs a{};
     a.rows = logits; a.n = T; a.V = V; a.tokens = lp_cmp; a.parent = lp_par; a.amax = acc_i + B;
     a.part_v = (float *)acc_part; a.part_i = acc_part + (size_t)T * hxd::ACCEPT_PARTS;
@@ -1278,14 +1305,14 @@ void hearth_engine::launch_loop_step(int T, int rows) {
     }
     Captured *cg = nullptr;
     for (Captured &g : graphs)
-        if (g.loop && g.T == T && g.rows == rows) cg = &g;
+        if (g.loop && g.T == T && g.rows == rows && g.skey == lp_skey) cg = &g;
     if (!cg) {
         if (graphs.size() >= 32) {
             (void)hipGraphExecDestroy(graphs.front().exec);
             (void)hipGraphDestroy(graphs.front().graph);
             graphs.erase(graphs.begin());
         }
-        Captured g{T, 1, rows, true, true, nullptr, nullptr};
+        Captured g{T, 1, rows, true, true, lp_skey, nullptr, nullptr};
         ck(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         try {
             Bound b(this, rows);
@@ -1877,18 +1904,26 @@ HEARTH_API int hearth_verify_greedy(hearth_engine *e, const int32_t *tokens, con
 
 HEARTH_API int hearth_gpu_spec_loop_ok(hearth_engine *e) { return e && e->loop_ok() ? 1 : 0; }
 
-HEARTH_API int hearth_gpu_spec_greedy(hearth_engine *e, const int32_t *seq, int n_seq, int new_tokens, int max_new,
-                                      int draft_len, int ngram_n, const int32_t *stop_ids, int n_stop, int max_steps,
-                                      int32_t *out, int32_t *records, hearth_gpu_spec_result *res) {
+/* The speculative loop on the device (greedy: smp null; sampled: smp and, at a positive
+ * temperature, uni[0 .. n_uni) the run's uniform stream, of which *n_used were consumed). */
+static int spec_run(hearth_engine *e, const int32_t *seq, int n_seq, int new_tokens, int max_new, int draft_len,
+                    int ngram_n, const int32_t *stop_ids, int n_stop, int max_steps, const hearth_sampler *smp,
+                    const double *uni, int n_uni, int32_t *out, int32_t *records, hearth_gpu_spec_result *res,
+                    int *n_used) {
+    const char *what = smp ? "hearth_gpu_spec_sample" : "hearth_gpu_spec_greedy";
     if (!e || !seq || n_seq < 1 || !out || !records || !res) return E_ARG;
     if (new_tokens < 0 || max_new <= new_tokens || draft_len < 0 || ngram_n < 0) return E_ARG;
     if (n_stop < 0 || n_stop > hxd::LOOP_STOPS_MAX || (n_stop && !stop_ids)) return E_ARG;
     if (max_steps < 1 || max_steps > HEARTH_GPU_SPEC_MAX_STEPS) return E_ARG;
     const int T = draft_len + 1;
     if (T > e->B || T > 128) return E_ARG;
+    if (smp) {
+        if (!n_used || check_sampler(smp) != OK || T > hxd::SAMPLE_NMAX || e->V > hxd::SAMPLE_VMAX) return E_ARG;
+        /* a step uses at most T uniforms */
+        if (smp->temperature > 0.0 && (!uni || n_uni < max_steps * T)) return E_ARG;
+    }
     if (!e->loop_ok()) {
-        log_msg(LOG_ERROR, "hearth_gpu_spec_greedy: not available with expert streaming, route replay, a routing "
-                           "trace or profiling");
+        log_msg(LOG_ERROR, "%s: not available with expert streaming, route replay, a routing trace or profiling", what);
         return E_ARG;
     }
     if (e->pos != n_seq - 1) return E_ARG;
@@ -1906,6 +1941,26 @@ HEARTH_API int hearth_gpu_spec_greedy(hearth_engine *e, const int32_t *seq, int 
         ck(hipStreamSynchronize(e->st));
         e->loop_prepare();
         e->loop_rope_table(std::min(e->cap, pos0 + S * T));
+        e->lp_skey = 0;
+        if (smp) {
+            /* a captured step bakes the sampler settings into its kernel arguments: they
+             * key the step (never 0); a larger scratch drops the captured steps */
+            const double f[5] = {smp->temperature, (double)smp->top_k, smp->top_p, smp->min_p, smp->repetition_penalty};
+            uint64_t k = 1469598103934665603ull;
+            for (double x : f) {
+                uint64_t bits;
+                std::memcpy(&bits, &x, 8);
+                k = (k ^ bits) * 1099511628211ull;
+            }
+            e->lp_skey = k ? k : 1;
+            e->lp_spec = hxl::SamplerSpec{smp->temperature, smp->top_p, smp->min_p, smp->repetition_penalty, smp->top_k,
+                                          nullptr, 0};
+            const int cap0 = e->lp_samp.n_cap;
+            ck(e->lp_samp.ensure(T, e->V, false, 0));
+            if (e->lp_samp.n_cap != cap0) e->drop_graphs();
+            if (smp->temperature > 0.0)
+                ck(hipMemcpy(e->lp_ustream, uni, sizeof(double) * (size_t)S * T, hipMemcpyHostToDevice));
+        }
         state[hxd::LS_LEN] = n_seq;
         state[hxd::LS_NEW] = new_tokens;
         state[hxd::LS_MAXNEW] = max_new;
@@ -1950,17 +2005,36 @@ HEARTH_API int hearth_gpu_spec_greedy(hearth_engine *e, const int32_t *seq, int 
         res->n_out = nout;
         res->n_steps = nst;
     } catch (const DeviceError &err) {
-        log_msg(LOG_ERROR, "HIP error in hearth_gpu_spec_greedy: %s", hipGetErrorString(err.e));
+        log_msg(LOG_ERROR, "HIP error in %s: %s", what, hipGetErrorString(err.e));
+        e->lp_skey = 0;
         return E_IO;
     }
+    e->lp_skey = 0;
     res->finish = state[hxd::LS_DONE];
     res->stop_id = state[hxd::LS_STOP];
     res->pos = state[hxd::LS_KVPOS];
+    if (n_used) *n_used = state[hxd::LS_UOFF];
     e->pos = state[hxd::LS_KVPOS];
     e->tokens_done += (uint64_t)launched * T;
     e->forward_calls += launched;
     e->wall_s += now_s() - t0;
     return OK;
+}
+
+HEARTH_API int hearth_gpu_spec_greedy(hearth_engine *e, const int32_t *seq, int n_seq, int new_tokens, int max_new,
+                                      int draft_len, int ngram_n, const int32_t *stop_ids, int n_stop, int max_steps,
+                                      int32_t *out, int32_t *records, hearth_gpu_spec_result *res) {
+    return spec_run(e, seq, n_seq, new_tokens, max_new, draft_len, ngram_n, stop_ids, n_stop, max_steps, nullptr,
+                    nullptr, 0, out, records, res, nullptr);
+}
+
+HEARTH_API int hearth_gpu_spec_sample(hearth_engine *e, const int32_t *seq, int n_seq, int new_tokens, int max_new,
+                                      int draft_len, int ngram_n, const int32_t *stop_ids, int n_stop, int max_steps,
+                                      const hearth_sampler *smp, const double *uniforms, int n_uniforms, int32_t *out,
+                                      int32_t *records, hearth_gpu_spec_result *res, int *n_used) {
+    if (!smp) return E_ARG;
+    return spec_run(e, seq, n_seq, new_tokens, max_new, draft_len, ngram_n, stop_ids, n_stop, max_steps, smp,
+                    uniforms, n_uniforms, out, records, res, n_used);
 }
 
 HEARTH_API int hearth_verify_sample(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,

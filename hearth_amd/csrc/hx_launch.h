@@ -229,6 +229,8 @@ struct SampleArgs {
     int *path;                        /* [n] accepted nodes from the root */
     int *result;                      /* [0] path length, [1] final token, [2] status */
     PwTail tail;                      /* pairwise tree of the row's last numpy buffer */
+    const int *live;                  /* device [1] or null: rows >= *live are padding (no distribution, never walked) */
+    const int *n_ctx_dev;             /* device [1] or null: the penalty context length (else n_ctx) */
 };
 
 /* Greedy speculative decoding loop on the device (k_loop.hip): fields of the state block. */
@@ -245,6 +247,7 @@ enum LoopField {
     LS_NGRAM,     /* longest n-gram the prompt lookup matches (0: no drafts) */
     LS_NSTOP,     /* stop ids */
     LS_KVPOS,     /* the engine position after the last committed step */
+    LS_UOFF,      /* sampled runs: uniforms of the run's stream consumed so far */
     LS_FIELDS = 16
 };
 enum LoopDone { LOOP_RUNNING = 0, LOOP_STOP = 1, LOOP_LENGTH = 2, LOOP_BAD = 3 };
@@ -267,6 +270,13 @@ struct LoopArgs {
     int *pos;                         /* device [1]: the forward's pos0, advanced by the commit */
     const int *result;                /* the acceptance's n_path, final token, status */
     int T;                            /* rows per step: draft length + 1 */
+    /* sampled runs (null ustream: no uniforms are used): the run's random stream, the
+     * sampled acceptance's uniforms [2T] that the drafter fills from it in the
+     * reference's order, and whether the commit advances LS_UOFF */
+    const double *ustream;
+    int ustream_n;
+    double *u;
+    int sampled;
 };
 
 } // namespace hxd
@@ -340,6 +350,12 @@ hipError_t accept_sample(SampleScratch &m, const float *rows, int n, int V, cons
  * context of row v includes the path tokens of nodes 1..v), m.row_rc[v] its status. */
 hipError_t sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
                         const SamplerSpec &s, hipStream_t st);
+/* accept_sample with every input already on the device and nothing copied (so it can be
+ * captured): the uniforms in m.u, the penalty context ctx_dev[0 .. *n_ctx_dev), rows
+ * >= *live treated as padding */
+hipError_t accept_sample_dev(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                             const SamplerSpec &s, const int *ctx_dev, const int *n_ctx_dev, const int *live,
+                             hipStream_t st);
 /* One step of the greedy loop: the drafts, token ids and RoPE rows of the next forward
  * (loop_draft), and the commit of the acceptance that followed it (loop_commit). */
 void loop_draft(const LoopArgs &a, hipStream_t st);

@@ -1,16 +1,18 @@
 /*
- * k_loop.hip — the greedy speculative decoding loop on the device: the prompt-lookup
+ * k_loop.hip — the speculative decoding loop on the device: the prompt-lookup
  * drafter (the reference's NgramIndex, python/hearth/generate.py:150-186) and the
  * commit of one verify step's tokens (the verify block, generate.py:365-392, and the
  * token loop of generate(), generate.py:292-400), so that a run of verify steps needs no
  * host round trip.
  *
- * One step is: k_loop_draft (the drafts, the forward's token ids and RoPE rows), the
- * forward of T = k + 1 rows, the greedy acceptance (accept_greedy), k_loop_commit. T is
+ * One step is: k_loop_draft (the drafts, the forward's token ids and RoPE rows, and for a
+ * sampled run the step's uniforms), the forward of T = k + 1 rows, the greedy or sampled
+ * acceptance (accept_greedy, accept_sample_dev), k_loop_commit. T is
  * the same for every step of a run, so one captured graph serves them all. A step whose
  * draft is shorter than k fills the rows after it with the last token (a valid id for
  * the embedding) and gives those rows the comparison id -1, which no argmax equals, so
- * the acceptance never walks into them; the routing gives padding rows the experts of
+ * the greedy acceptance never walks into them (the sampled walk takes rows past the
+ * draft as padding: LS_LIVE); the routing gives padding rows the experts of
  * row 0 (they load no expert of their own). Rows are causal, and every row's result is
  * independent of the batch it is computed in, so padding changes nothing in the rows
  * before it.
@@ -69,6 +71,25 @@ __global__ __launch_bounds__(1024) void k_loop_draft(LoopArgs a) {
         s[LS_ND] = nd;
         s[LS_LIVE] = nd + 1;
     }
+    /* sampled runs: the step's uniforms from the run's stream r (from LS_UOFF on) in the
+     * reference's order (generate.py:376-392: one per tried draft, then one for the draw
+     * at the node where the walk ends), laid out for the sampled walk: u[2c] decides node
+     * c, u[2v + 1] draws at node v -- so u[2c] = r[c - 1] (c = 1..nd), u[2v + 1] = r[v + 1]
+     * (v < nd) and u[2 nd + 1] = r[nd]; a step uses at most nd + 1 of them */
+    if (a.u) {
+        const int o = s[LS_UOFF];
+        auto r = [&](int i) { return a.ustream && o + i < a.ustream_n ? a.ustream[o + i] : 0.0; };
+        for (int i = tid; i < 2 * a.T; i += blockDim.x) {
+            const int c = i >> 1;
+            double v = 0.0;
+            if (!(i & 1)) {
+                if (c >= 1 && c <= nd) v = r(c - 1);
+            } else if (c <= nd) {
+                v = r(c < nd ? c + 1 : nd);
+            }
+            a.u[i] = v;
+        }
+    }
     /* RoPE rows of positions pos0 + i from the table (the engine checks that every step
      * of a run stays below the capacity; the clamp only keeps the read in the table) */
     const int p = *a.pos;
@@ -117,6 +138,9 @@ __global__ void k_loop_commit(LoopArgs a) {
             break;
         }
     }
+    /* uniforms the sampled walk used: one per tried draft (accepted ones and the first
+     * rejected one), one for the final draw */
+    if (a.sampled) s[LS_UOFF] += nacc + 1 + (nacc < s[LS_ND] ? 1 : 0);
     const int step = s[LS_STEP];
     if (step < a.rec_cap) {
         a.rec[3 * step] = s[LS_ND];

@@ -391,6 +391,7 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
     __shared__ __align__(16) unsigned char smem[SMEM];
     __shared__ RowShared rs;
     const int v = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (a.live && v >= *a.live) return;   /* padding row (uniform) */
     const int V = a.V;
     const float *row = a.rows + (size_t)v * V;
     double *P = a.P + (size_t)v * V;
@@ -406,7 +407,8 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
     if (pen) {
         for (int i = tid; i < (V + 31) / 32; i += SP_T) bits[i] = 0;
         __syncthreads();
-        for (int j = tid; j < a.n_ctx; j += SP_T) {
+        const int n_ctx = a.n_ctx_dev ? *a.n_ctx_dev : a.n_ctx;
+        for (int j = tid; j < n_ctx; j += SP_T) {
             const int t = a.ctx[j];
             if (t >= 0 && t < V) atomicOr(&bits[t >> 5], 1u << (t & 31));
         }
@@ -753,6 +755,7 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
     __shared__ ChainShared cs;
     __shared__ TopPBins tb;
     const int v = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (a.live && v >= *a.live) return;   /* padding row (uniform) */
     const int V = a.V;
     double *P = a.P + (size_t)v * V;
     double *lv = (double *)smem;
@@ -915,7 +918,8 @@ __global__ __launch_bounds__(SP_T) void k_sample_walk(SampleArgs a) {
     __shared__ int sh[4];
     __shared__ double shd[4];
     __shared__ ChainShared cs;
-    const int n = a.n, V = a.V, tid = threadIdx.x;
+    const int V = a.V, tid = threadIdx.x;
+    const int n = a.live ? *a.live : a.n;   /* padding rows are not in the tree */
     for (int i = tid; i < n; i += SP_T) head[i] = -1;
     __syncthreads();
     if (tid == 0)
@@ -1104,6 +1108,24 @@ hipError_t accept_sample(SampleScratch &m, const float *rows, int n, int V, cons
     SampleArgs a;
     hipError_t e = make_args(a, m, rows, n, V, tok, par, s, q, u, st);
     if (e != hipSuccess || (e = probs(m, a, n, st)) != hipSuccess) return e;
+    k_sample_walk<<<1, SP_T, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t accept_sample_dev(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
+                             const SamplerSpec &s, const int *ctx_dev, const int *n_ctx_dev, const int *live,
+                             hipStream_t st) {
+    SampleArgs a;
+    SamplerSpec sp = s;
+    sp.n_ctx = 0;   /* nothing to copy: the context is on the device */
+    hipError_t e = make_args(a, m, rows, n, V, tok, par, sp, nullptr, nullptr, st);
+    if (e != hipSuccess) return e;
+    if (s.rp != 1.0) {
+        a.ctx = ctx_dev;
+        a.n_ctx_dev = n_ctx_dev;
+    }
+    a.live = live;
+    if ((e = probs(m, a, n, st)) != hipSuccess) return e;
     k_sample_walk<<<1, SP_T, 0, st>>>(a);
     return hipGetLastError();
 }

@@ -223,6 +223,12 @@ class Token(NamedTuple):
 
 # ---------------------------------------------------------------- KV bookkeeping
 
+def _max_batch(engine) -> int:
+    """Rows one forward may evaluate (the engine's max_batch option; 0 means 512, api.c:178-179)."""
+    opts = getattr(engine, "options", None) or {}
+    return int(opts.get("max_batch", 0) or 512)
+
+
 def kv_capacity(engine) -> int:
     """Positions the engine's KV cache holds (kv_capacity, else the model's max_seq)."""
     cap = getattr(engine, "kv_capacity", None)
@@ -371,9 +377,17 @@ class _Run:
         t0 = time.perf_counter()
         if self.loop:
             k = self.draft_len if self.drafter is not None else 0
-            res = self.engine.spec_greedy(self.seq, st.new_tokens, self.max_new, k,
-                                          self.drafter.max_n if self.drafter is not None else 0, self.stops,
-                                          max_steps=min(self.batch, self.max_new - st.new_tokens))
+            ng = self.drafter.max_n if self.drafter is not None else 0
+            steps = min(self.batch, self.max_new - st.new_tokens)
+            smp = self.sampler
+            if smp.is_greedy and not smp.uses_context:
+                res = self.engine.spec_greedy(self.seq, st.new_tokens, self.max_new, k, ng, self.stops, max_steps=steps)
+            else:
+                # sampled acceptance on the device; the penalty context is the committed
+                # sequence there, so the sampler travels without one
+                res = self.engine.spec_sample(self.seq, st.new_tokens, self.max_new, k, ng,
+                                              smp.device(None, greedy=smp.is_greedy),
+                                              None if smp.is_greedy else smp.rng, self.stops, max_steps=steps)
             if res is not None:
                 self.batch = min(2 * self.batch, 64)
                 self.steps = res["steps"]
@@ -398,17 +412,23 @@ class _Run:
             pass
 
 
-def _use_device_loop(engine, sampler: Sampler, stops: frozenset, device_loop: bool | None, drafts: bool) -> bool:
-    """None picks the device loop for greedy runs without drafts only: with drafts, every
-    device step evaluates draft_len + 1 rows however short its draft, which at low
-    acceptance costs about what the saved host round trip gains."""
-    able = sampler.is_greedy and not sampler.uses_context and len(stops) <= _eng.SPEC_STOPS_MAX
+def _use_device_loop(engine, sampler: Sampler, stops: frozenset, device_loop: bool | None, drafts: bool,
+                     draft_len: int = 0) -> bool:
+    """None picks the device loop for runs without drafts only: with drafts, every device
+    step evaluates draft_len + 1 rows however short its draft, which at low acceptance
+    costs about what the saved host round trip gains."""
+    able = len(stops) <= _eng.SPEC_STOPS_MAX and draft_len + 1 <= _eng.SPEC_ROWS_MAX
     if device_loop is None and drafts:
         return False
     if device_loop is False or not able:
         if device_loop:
-            raise ValueError("the device loop runs greedy decoding without a repetition penalty and at most "
-                             f"{_eng.SPEC_STOPS_MAX} stop ids")
+            raise ValueError(f"the device loop runs at most {_eng.SPEC_STOPS_MAX} stop ids and drafts of at most "
+                             f"{_eng.SPEC_ROWS_MAX - 1} tokens")
+        return False
+    if drafts and draft_len + 1 > _max_batch(engine):
+        if device_loop:
+            raise ValueError(f"the device loop evaluates draft_len + 1 = {draft_len + 1} rows per step, more than "
+                             f"the engine's max_batch {_max_batch(engine)}")
         return False
     ok = bool(getattr(engine, "spec_loop_ok", False))
     if device_loop and not ok:
@@ -424,10 +444,11 @@ def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampl
     returns the GenStats (StopIteration.value).
 
     held: the tokens whose KV the engine holds (prefix reuse); None resets the engine.
-    device_loop: True runs greedy decoding (no repetition penalty) in batches of steps on
-    the device (drafting included), False always steps from the host, None picks the
-    device loop for greedy runs without drafts when the engine offers it. The tokens and
-    statistics are the same either way.
+    device_loop: True runs the generation in batches of steps on the device (drafting and
+    acceptance included, greedy or sampled: the sampler's generator is advanced by exactly
+    the uniforms the host steps would draw), False always steps from the host, None picks
+    the device loop for runs without drafts when the engine offers it. The tokens, the
+    statistics and the generator's state afterwards are the same either way.
     Once a token has been yielded or the generator has returned (max_new_tokens == 0
     included), and from then on even if it is closed or interrupted, the engine holds a
     prefix of prompt + yielded tokens of length engine.pos (all but the last token
@@ -453,7 +474,8 @@ def generate(engine, prompt_ids: Sequence[int], max_new_tokens: int = 256, sampl
 
     run = _Run(engine, prompt, sampler, NgramIndex(ngram_n, prompt) if mode == "ngram" else None, draft_len,
                max_new_tokens, cap, st, stops,
-               _use_device_loop(engine, sampler, stops, device_loop, mode == "ngram" and draft_len > 0))
+               _use_device_loop(engine, sampler, stops, device_loop, mode == "ngram" and draft_len > 0,
+                                draft_len if mode == "ngram" else 0))
     try:
         run.prefill(held)
         while True:

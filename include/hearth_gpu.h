@@ -155,6 +155,23 @@ HEARTH_API int hearth_gpu_accept_sample(const float *rows, int n, int V, const i
 HEARTH_API int hearth_gpu_probs(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,
                                 const hearth_sampler *s, double *p_out);
 
+/* The loop of hearth_gpu_spec_greedy with sampled acceptance (hearth_verify_sample's
+ * walk over each step's chain, the Sampler smp; its penalty context is the committed
+ * sequence, so smp->context is not read). A positive temperature draws from the run's
+ * random stream uniforms[0 .. n_uniforms), at least max_steps * (draft_len + 1) values,
+ * in the reference's order (generate.py:376-392: one per tried draft, then one for the
+ * draw where the walk ends; step after step); *n_used reports how many the run consumed,
+ * so the caller's generator can be advanced by exactly that many. Temperature 0 (a
+ * penalised argmax) reads no uniforms (uniforms may be NULL) and reports 0. Same
+ * arguments, results and limits as hearth_gpu_spec_greedy otherwise, plus the sampled
+ * acceptance's (draft_len + 1 <= 128, vocabulary within its limit); -1 also for a
+ * sampler that hearth_verify_sample would reject. No counterpart in the reference's C
+ * API (the reference draws its uniforms on the host, step by step). */
+HEARTH_API int hearth_gpu_spec_sample(hearth_engine *e, const int32_t *seq, int n_seq, int new_tokens, int max_new,
+                                      int draft_len, int ngram_n, const int32_t *stop_ids, int n_stop, int max_steps,
+                                      const hearth_sampler *smp, const double *uniforms, int n_uniforms, int32_t *out,
+                                      int32_t *records, hearth_gpu_spec_result *res, int *n_used);
+
 /* Attention order of the engine's GQA layers. No counterpart in the reference, whose
  * ADR-0003-canonical-numerics.md:44-45 lets a GPU backend document its tolerance:
  *   HEARTH_GPU_ATTN_CANONICAL  the reference's order (engine/src/model.c:519-589): dot16

@@ -1,5 +1,6 @@
-"""The greedy speculative loop on the device (hearth_gpu_spec_greedy) against the host
-steps (one hearth_verify_greedy per step, drafts from NgramIndex on the host).
+"""The speculative loop on the device (hearth_gpu_spec_greedy, hearth_gpu_spec_sample)
+against the host steps (one hearth_verify_greedy / hearth_verify_sample per step, drafts
+from NgramIndex on the host).
 
 generate() with the device loop must yield what the host steps yield: the same tokens,
 Token fields (step, drafted, accepted), GenStats counts and finish, the same engine
@@ -29,9 +30,9 @@ def _prompt(vocab):
     return base * 3 + base[:5]
 
 
-def _gen(e, prompt, n, stops, spec, k, ng, loop):
-    print(f"generate n={n} stops={list(stops)} {spec} k={k} ng={ng} device_loop={loop}", flush=True)
-    gen = generate(e, prompt, n, Sampler.greedy(), stops, spec, k, ng, device_loop=loop)
+def _gen(e, prompt, n, stops, spec, k, ng, loop, sampler=None):
+    print(f"generate n={n} stops={list(stops)} {spec} k={k} ng={ng} device_loop={loop} sampler={sampler}", flush=True)
+    gen = generate(e, prompt, n, sampler or Sampler.greedy(), stops, spec, k, ng, device_loop=loop)
     toks = []
     try:
         while True:
@@ -44,13 +45,17 @@ def _gen(e, prompt, n, stops, spec, k, ng, loop):
     return [(t.id, t.step, t.drafted, t.accepted) for t in toks], counts, e.pos, np.ascontiguousarray(kv).view(np.uint32)
 
 
-def _same(e, prompt, n, stops, spec, k, ng):
-    ref = _gen(e, prompt, n, stops, spec, k, ng, False)
-    got = _gen(e, prompt, n, stops, spec, k, ng, True)
+def _same(e, prompt, n, stops, spec, k, ng, sampler_kw=None):
+    s_ref = Sampler(seed=7, **sampler_kw) if sampler_kw else None
+    s_dev = Sampler(seed=7, **sampler_kw) if sampler_kw else None
+    ref = _gen(e, prompt, n, stops, spec, k, ng, False, s_ref)
+    got = _gen(e, prompt, n, stops, spec, k, ng, True, s_dev)
     assert got[0] == ref[0], "tokens or Token fields differ"
     assert got[1] == ref[1], "GenStats counts differ"
     assert got[2] == ref[2], "engine position differs"
     assert np.array_equal(got[3], ref[3]), "KV differs"
+    if sampler_kw:
+        assert s_dev.rng.random() == s_ref.rng.random(), "the sampler's generator advanced differently"
     return got
 
 
@@ -108,3 +113,31 @@ def test_graphs_off_and_chunked_order(tiny_model, monkeypatch):
     monkeypatch.delenv("HEARTH_GPU_GRAPH")
     with Engine(tiny_model, max_seq=512, attn="chunked") as e:
         _same(e, prompt, 40, (), "ngram", 5, 3)
+
+
+@pytest.mark.parametrize("name", ["tiny", "dsv3"])
+def test_sampled_device_loop_equals_host_steps(name, tiny_model, variant_models):
+    """Sampled acceptance in the device loop (hearth_gpu_spec_sample): top-p, top-k, min-p,
+    a repetition penalty and a penalised argmax, with drafts and without, a stop token
+    and a budget inside a batch: the same tokens, counts, position, KV bits and generator
+    state as the host steps (each a hearth_verify_sample with the reference's uniforms)."""
+    path = tiny_model if name == "tiny" else variant_models(name)
+    settings = (dict(temperature=0.8, top_p=0.95), dict(temperature=1.2, top_k=8, min_p=0.02),
+                dict(temperature=0.7, repetition_penalty=1.3), dict(temperature=0.0, repetition_penalty=1.2))
+    with Engine(path, max_seq=512) as e:
+        prompt = _prompt(e.vocab_size)
+        drafted = accepted = 0
+        for kw in settings:
+            for spec, k, ng in (("ngram", 4, 3), ("ngram", 8, 2), ("none", 4, 3)):
+                toks, counts, _, _ = _same(e, prompt, 40, (), spec, k, ng, kw)
+                assert len(toks) == 40 and counts[6] == "length"
+                drafted += counts[4]
+                accepted += counts[5]
+        # the tiny model accepts some drafts at these settings; the DeepSeek-V3-style
+        # variant's sampled distributions are too flat to accept any
+        assert drafted > 0 and (accepted > 0 or name != "tiny"), (drafted, accepted)
+        first = [t[0] for t in _gen(e, prompt, 30, (), "ngram", 6, 3, False, Sampler(seed=7, temperature=0.9))[0]]
+        toks, counts, _, _ = _same(e, prompt, 30, (first[11],), "ngram", 6, 3, dict(temperature=0.9))
+        assert counts[6] == "stop" and counts[7] == first[11]
+        for n in (1, 5, 17):
+            _same(e, prompt, n, (), "ngram", 6, 3, dict(temperature=1.1, top_p=0.9))

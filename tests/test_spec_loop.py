@@ -1,4 +1,4 @@
-"""The greedy speculative loop on the device (hearth_gpu_spec_greedy), on the CPU.
+"""The speculative loop on the device (hearth_gpu_spec_greedy, hearth_gpu_spec_sample), on the CPU.
 
 - The device drafter's formulation (k_loop_draft: the largest end e among those with the
   most trailing tokens equal to the sequence's suffix, capped at ngram_n) proposes what
@@ -18,6 +18,7 @@ import numpy as np
 import pytest
 
 import oracle_py as O
+from hearth_amd.engine import chain_uniforms
 from hearth_amd.generate import NgramIndex, Sampler, generate, generate_ids
 from test_generate import PROMPTS, REPEAT, ToyEngine
 
@@ -72,6 +73,13 @@ class LoopToy(ToyEngine):
         self.padded_rows = 0
 
     def spec_greedy(self, seq, new_tokens, max_new, draft_len, ngram_n, stop_ids=(), max_steps=64):
+        def accept(rows, cmp, nd, hist):
+            T = len(cmp)
+            return O.accept_tree(rows, np.asarray(cmp, np.int32), np.arange(-1, T - 1), mode=0)
+
+        return self._steps(seq, new_tokens, max_new, draft_len, ngram_n, stop_ids, max_steps, accept)
+
+    def _steps(self, seq, new_tokens, max_new, draft_len, ngram_n, stop_ids, max_steps, accept):
         seq = [int(t) for t in seq]
         assert self.pos == len(seq) - 1 and 0 <= new_tokens < max_new
         T = draft_len + 1
@@ -90,7 +98,7 @@ class LoopToy(ToyEngine):
             cmp = [last] + draft + [-1] * (T - 1 - nd)                 # padding: no argmax equals -1
             pos0 = self.pos
             rows = self.eval(rows_tokens, all_logits=True)
-            rc, path, fin = O.accept_tree(rows, np.asarray(cmp, np.int32), np.arange(-1, T - 1), mode=0)
+            rc, path, fin = accept(rows, cmp, nd, hist)
             if rc != 0:
                 del self.kv[pos0:]
                 finish = "bad_logits"
@@ -116,9 +124,41 @@ class LoopToy(ToyEngine):
         return {"steps": steps, "finish": finish, "stop_id": stop_id, "pos": self.pos}
 
 
-def _run(make, prompt, n, stops, spec, k, ng, loop):
+    def spec_sample(self, seq, new_tokens, max_new, draft_len, ngram_n, sampler, rng, stop_ids=(), max_steps=64):
+        """hearth_gpu_spec_sample restated: the same steps with the sampled walk over each
+        step's live rows (penalty context = the committed sequence), the step's uniforms
+        taken in order from a window of the run's stream, rng advanced by those used."""
+        draws = sampler.temperature > 0.0
+        saved = rng.bit_generator.state if draws else None
+        stream = rng.random(max_steps * (draft_len + 1)) if draws else None
+        used = 0
+
+        def accept(rows, cmp, nd, hist):
+            nonlocal used
+            s = O.sampler(sampler.temperature, sampler.top_k, sampler.top_p, sampler.min_p,
+                          sampler.repetition_penalty, context=hist)
+            u = chain_uniforms(stream[used:used + nd + 1], nd) if draws else np.zeros(2 * (nd + 1))
+            rc, path, fin = O.accept_tree_s(rows[:nd + 1], np.asarray(cmp[:nd + 1], np.int32), np.arange(-1, nd), s, u=u)
+            if rc == 0 and draws:
+                nacc = len(path) - 1
+                used += nacc + 1 + (nacc < nd)
+            return rc, path, fin
+
+        try:
+            res = self._steps(seq, new_tokens, max_new, draft_len, ngram_n, stop_ids, max_steps, accept)
+        finally:
+            if draws:
+                rng.bit_generator.state = saved
+        if draws and used:
+            rng.random(used)
+        if res is not None:
+            res["used"] = used
+        return res
+
+
+def _run(make, prompt, n, stops, spec, k, ng, loop, sampler=None):
     e = make()
-    gen = generate(e, prompt, n, Sampler.greedy(), stops, spec, k, ng, device_loop=loop)
+    gen = generate(e, prompt, n, sampler or Sampler.greedy(), stops, spec, k, ng, device_loop=loop)
     toks = []
     try:
         while True:
@@ -180,23 +220,61 @@ def test_closing_inside_a_batch_leaves_a_prefix():
     assert inside > 0
 
 
+@pytest.mark.parametrize("kw", [dict(follow=2.5), dict(follow=1.0, history_amp=1.0)])
+def test_sampled_device_batches_equal_host_steps(kw):
+    """Sampled and penalised runs: the device batches yield the host steps' tokens, Token
+    fields and counts, keep the same KV, and leave the sampler's generator in the same
+    state (the window of uniforms is rewound to what the steps used)."""
+    drafted = batches = draws = 0
+    settings = (dict(temperature=0.8, top_p=0.95), dict(temperature=1.3, top_k=5),
+                dict(temperature=0.7, repetition_penalty=1.3), dict(temperature=0.0, repetition_penalty=1.2),
+                dict(temperature=1.0, min_p=0.1))
+    for seed in range(3):
+        for prompt in (PROMPTS[0], PROMPTS[3], REPEAT):
+            for st_kw in settings:
+                for spec, k, ng in (("ngram", 4, 3), ("ngram", 8, 2), ("none", 4, 3)):
+                    s_ref = Sampler(seed=100 + seed, **st_kw)
+                    s_dev = Sampler(seed=100 + seed, **st_kw)
+                    ref_e, ref, ref_st = _run(lambda: ToyEngine(seed=seed, **kw), prompt, 30, (), spec, k, ng, False,
+                                              s_ref)
+                    e, got, st = _run(lambda: LoopToy(seed=seed, **kw), prompt, 30, (), spec, k, ng, True, s_dev)
+                    assert got == ref, (seed, prompt, st_kw, spec, k, ng)
+                    assert _counts(st) == _counts(ref_st)
+                    assert e.kv == ref_e.kv
+                    assert s_dev.rng.random() == s_ref.rng.random(), "generator states differ"
+                    drafted += st.drafted
+                    batches += e.batches
+                    draws += st_kw["temperature"] > 0
+    assert drafted > 0 and batches > 0 and draws > 0
+
+
 def test_loop_selection():
     e = LoopToy(seed=1, follow=2.0)
     pen = Sampler(temperature=0.0, repetition_penalty=1.2)
-    # a penalised or sampled run, or too many stop ids, stays on the host steps
-    for s, stops in ((pen, ()), (Sampler(temperature=0.7, seed=1), ()), (Sampler.greedy(), list(range(100, 165)))):
-        generate_ids(e, REPEAT, 8, s, stops, "ngram", 4, 3)
+    # with drafts, any sampler stays on the host steps by default and takes the device
+    # loop on request; too many stop ids, or drafts wider than the loop's rows, never do
+    for s in (pen, Sampler(temperature=0.7, seed=1), Sampler.greedy()):
+        generate_ids(e, REPEAT, 8, s, (), "ngram", 4, 3)
+        assert e.batches == 0
+        generate_ids(e, REPEAT, 8, s, (), "ngram", 4, 3, device_loop=True)
+        assert e.batches > 0
+        e.batches = 0
+    for stops, k in ((list(range(100, 165)), 4), ((), 128)):
+        generate_ids(e, REPEAT, 8, Sampler.greedy(), stops, "ngram", k, 3)
         assert e.batches == 0
         with pytest.raises(ValueError):
-            generate_ids(e, REPEAT, 8, s, stops, "ngram", 4, 3, device_loop=True)
+            generate_ids(e, REPEAT, 8, Sampler.greedy(), stops, "ngram", k, 3, device_loop=True)
     with pytest.raises(ValueError):
         generate_ids(ToyEngine(), REPEAT, 8, Sampler.greedy(), (), "ngram", 4, 3, device_loop=True)
     generate_ids(e, REPEAT, 8, Sampler.greedy(), (), "ngram", 4, 3, device_loop=False)
     assert e.batches == 0
-    # None: the device loop for greedy runs without drafts, host steps with drafts
+    # None: the device loop for runs without drafts (greedy, penalised or sampled), host
+    # steps with drafts
     generate_ids(e, REPEAT, 8, Sampler.greedy(), (), "ngram", 4, 3)
     assert e.batches == 0
-    generate_ids(e, REPEAT, 8, Sampler.greedy(), (), "none", 4, 3)
-    assert e.batches > 0
+    for s in (Sampler.greedy(), pen, Sampler(temperature=0.9, seed=2)):
+        e.batches = 0
+        generate_ids(e, REPEAT, 8, s, (), "none", 4, 3)
+        assert e.batches > 0
     generate_ids(e, REPEAT, 8, Sampler.greedy(), (), "ngram", 4, 3, device_loop=True)
     assert e.batches > 1
