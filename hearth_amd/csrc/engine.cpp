@@ -211,7 +211,7 @@ struct hearth_engine {
         *lp_cmp = nullptr, *lp_par = nullptr, *lp_path = nullptr;
     float *lp_rtab = nullptr;
     int lp_rtab_rows = 0;
-    int *h_lp = nullptr;                 /* pinned: the done flags of the steps in flight, then the state */
+    int *h_lp = nullptr;                 /* pinned: (LS_NEW, LS_DONE) of the steps in flight, then the state */
     hipEvent_t lp_ev[2] = {nullptr, nullptr};
     /* sampled runs (hearth_gpu_spec_sample): the acceptance scratch of the loop (its own,
      * so that growing the call-by-call scratch never moves what a captured step reads),
@@ -1984,16 +1984,25 @@ static int spec_run(hearth_engine *e, const int32_t *seq, int n_seq, int new_tok
         ck(hipMemcpy(e->d_pos, &pos0, sizeof(int), hipMemcpyHostToDevice));
         e->geom_chain = 1;
         e->tree_n = 0;
-        /* two steps in flight: before step i is queued, the done flag of step i - 2 is
-         * read, so at most two steps run after the one that ended the run */
+        /* two steps in flight: before step i is queued, step i - 2 has finished, and step
+         * i - 1 too when it could spend the token budget (a step yields at most T tokens),
+         * so a run that ends on its budget queues no step after the last; a stop token or
+         * bad logits can leave two more, which commit nothing. Each step copies its
+         * (LS_NEW, LS_DONE) pair to h_lp + 2 (i & 1). */
+        static_assert(hxd::LS_DONE == hxd::LS_NEW + 1, "the step copy reads LS_NEW and LS_DONE together");
+        int seen = new_tokens;   /* tokens yielded as of the last step read */
+        auto finished = [&](int j) {
+            ck(hipEventSynchronize(e->lp_ev[j & 1]));
+            seen = e->h_lp[2 * (j & 1)];
+            return e->h_lp[2 * (j & 1) + 1] != hxd::LOOP_RUNNING;
+        };
         for (int i = 0; i < S; i++) {
-            if (i >= 2) {
-                ck(hipEventSynchronize(e->lp_ev[i & 1]));
-                if (e->h_lp[i & 1] != hxd::LOOP_RUNNING) break;
-            }
+            if (i >= 2 && finished(i - 2)) break;
+            if (i >= 1 && seen + T >= max_new && finished(i - 1)) break;
             e->launch_loop_step(T, rows);
             launched++;
-            ck(hipMemcpyAsync(e->h_lp + (i & 1), e->lp_state + hxd::LS_DONE, sizeof(int), hipMemcpyDeviceToHost, e->st));
+            ck(hipMemcpyAsync(e->h_lp + 2 * (i & 1), e->lp_state + hxd::LS_NEW, 2 * sizeof(int),
+                              hipMemcpyDeviceToHost, e->st));
             ck(hipEventRecord(e->lp_ev[i & 1], e->st));
         }
         ck(hipMemcpyAsync(e->h_lp, e->lp_state, sizeof(int) * hxd::LS_FIELDS, hipMemcpyDeviceToHost, e->st));

@@ -678,108 +678,119 @@ __global__ __launch_bounds__(512) void k_expert_tk(MoeArgs a, int rpw, int S, in
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);    /* no weight use moves above the barrier */
     const int q = lr >> 2;                /* register of this lane's pair: row 4 kg + q */
-    const int col = 4 * g + (lr & 3);     /* token of this lane's pair */
-    const int colc = col < n ? col : n - 1;   /* its staged row (columns past n are discarded) */
-    const v4i zero = {0, 0, 0, 0};
-    const bool full = kb0 + NBK <= nb;    /* uniform */
-    /* terms of local block kb (global kb0 + kb); the MFMA gives sum q x with q the
-     * stored nibble (Q4), so isum = sum q x - 8 sx */
-    auto terms = [&](const v4i (&wa)[NM], int kb, float (&t)[NM]) {
-        const int blk = kb0 + kb;
-        const v4i xq = *(const v4i *)(xs + ((size_t)blk * 16 + colc) * 64 + kg * 16);
-        const float d = dxs[blk * 16 + colc];
-        const int off = DT == 4 ? 8 * sxs[blk * 16 + colc] : 0;
-#pragma unroll
-        for (int mi = 0; mi < NM; mi++) {
-            const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[mi], xq, zero, 0, 0, 0);
-            const float dw = h2f(*((const uint16_t *)(scl + (size_t)(mi * NBK + kb) * 32) + 4 * kg + q));
-            t[mi] = fmul((float)(pick4(cc, q) - off), fmul(dw, d));
-        }
-    };
-    float acc[NM];
-    float tm[NBK][NM];
-    auto run_part = [&](bool fold) {
-#pragma unroll
-        for (int k = 0; k < NP; k++) {
-            /* pair k's loads are in when at most the later pairs' are outstanding */
-            if (k >= NA) wait_vmcnt_le(NM * NV * (NP - 1 - k));
-            v4i wv[2][NM];
+    /* one group of 4 tokens: the MFMAs, the fold over the parts and the epilogue */
+    auto group = [&](int g) {
+        const int col = 4 * g + (lr & 3);     /* token of this lane's pair */
+        const int colc = col < n ? col : n - 1;   /* its staged row (columns past n are discarded) */
+        const v4i zero = {0, 0, 0, 0};
+        const bool full = kb0 + NBK <= nb;    /* uniform */
+        /* terms of local block kb (global kb0 + kb); the MFMA gives sum q x with q the
+         * stored nibble (Q4), so isum = sum q x - 8 sx */
+        auto terms = [&](const v4i (&wa)[NM], int kb, float (&t)[NM]) {
+            const int blk = kb0 + kb;
+            const v4i xq = *(const v4i *)(xs + ((size_t)blk * 16 + colc) * 64 + kg * 16);
+            const float d = dxs[blk * 16 + colc];
+            const int off = DT == 4 ? 8 * sxs[blk * 16 + colc] : 0;
 #pragma unroll
             for (int mi = 0; mi < NM; mi++) {
-                if (DT == 4) {
-                    unpack_q4(w[mi][k][0], wv[0][mi], wv[1][mi]);
-                } else {
-                    wv[0][mi] = w[mi][k][0];
-                    wv[1][mi] = w[mi][k][NV - 1];
-                }
+                const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[mi], xq, zero, 0, 0, 0);
+                const float dw = h2f(*((const uint16_t *)(scl + (size_t)(mi * NBK + kb) * 32) + 4 * kg + q));
+                t[mi] = fmul((float)(pick4(cc, q) - off), fmul(dw, d));
             }
+        };
+        float acc[NM];
+        float tm[NBK][NM];
+        auto run_part = [&](bool fold) {
 #pragma unroll
-            for (int j2 = 0; j2 < 2; j2++) {
-                const int kb = 2 * k + j2;
-                if (!full && kb0 + kb >= nb) break;   /* uniform */
-                float t[NM];
-                terms(wv[j2], kb, t);
+            for (int k = 0; k < NP; k++) {
+                /* pair k's loads are in when at most the later pairs' are outstanding */
+                if (k >= NA) wait_vmcnt_le(NM * NV * (NP - 1 - k));
+                v4i wv[2][NM];
 #pragma unroll
                 for (int mi = 0; mi < NM; mi++) {
-                    if (fold) acc[mi] = fadd(acc[mi], t[mi]);
-                    else tm[kb][mi] = t[mi];
+                    if (DT == 4) {
+                        unpack_q4(w[mi][k][0], wv[0][mi], wv[1][mi]);
+                    } else {
+                        wv[0][mi] = w[mi][k][0];
+                        wv[1][mi] = w[mi][k][NV - 1];
+                    }
                 }
+#pragma unroll
+                for (int j2 = 0; j2 < 2; j2++) {
+                    const int kb = 2 * k + j2;
+                    if (!full && kb0 + kb >= nb) break;   /* uniform */
+                    float t[NM];
+                    terms(wv[j2], kb, t);
+#pragma unroll
+                    for (int mi = 0; mi < NM; mi++) {
+                        if (fold) acc[mi] = fadd(acc[mi], t[mi]);
+                        else tm[kb][mi] = t[mi];
+                    }
+                }
+            }
+        };
+        if (part == 0) {
+#pragma unroll
+            for (int mi = 0; mi < NM; mi++) acc[mi] = 0.0f;
+            run_part(true);
+        } else {
+            run_part(false);
+        }
+        for (int stage = 1; stage < S; stage++) {
+            if (part == stage - 1) {
+#pragma unroll
+                for (int mi = 0; mi < NM; mi++) relay[mi * 64 + lane] = acc[mi];
+            }
+            __syncthreads();
+            if (part == stage) {
+#pragma unroll
+                for (int mi = 0; mi < NM; mi++) acc[mi] = relay[mi * 64 + lane];
+#pragma unroll
+                for (int kb = 0; kb < NBK; kb++) {
+                    if (!full && kb0 + kb >= nb) break;   /* uniform */
+#pragma unroll
+                    for (int mi = 0; mi < NM; mi++) acc[mi] = fadd(acc[mi], tm[kb][mi]);
+                }
+            }
+            __syncthreads();   /* the relay slot is read before the next stage writes it */
+        }
+        const int row = rt * 16 + 4 * kg + q;
+        const bool out = part == S - 1 && live && col < n;
+        if (DOWN) {
+            if (out && row < mat[0].rows) a.Y[(size_t)(p0 + col) * a.D + row] = canon(acc[0]);
+            return;
+        }
+        float mv = 0.0f;
+        {
+            /* every lane takes the exp (the table is read across the wave); the outputs keep it */
+            const float gv = canon(acc[0]), uv = canon(acc[NM - 1]);
+            const float sg = fdiv(gv, fadd(1.0f, exp_glibc_f_wave(-gv, ev)));
+            if (out) {
+                mv = fmul(sg, uv);
+                if (!QF) a.midf[(size_t)(p0 + col) * a.F + row] = mv;
+            }
+        }
+        if constexpr (QF) {
+            /* the workgroup's rows [16 rpw tile, +16 rpw) are whole blocks of F: the last
+             * parts put them in LDS by (token, row), then wave j quantizes block j / 4 of
+             * token 4 g + j % 4 -- the values k_quant_rows would read from midf */
+            const int nr = 16 * rpw;
+            float *qb = relay0 + rpw * NM * 64;   /* [4 tokens][16 rpw], after the relay slots */
+            if (part == S - 1) qb[(lr & 3) * nr + rtl * 16 + 4 * kg + q] = mv;
+            __syncthreads();
+            if (wave < rpw) {
+                const int tt = wave & 3, bb = wave >> 2, tcol = 4 * g + tt;
+                if (tcol < n) quant_block_wave(qb[tt * nr + bb * 64 + lane], a.mid, p0 + tcol, (tile * nr) / 64 + bb);
             }
         }
     };
-    if (part == 0) {
-#pragma unroll
-        for (int mi = 0; mi < NM; mi++) acc[mi] = 0.0f;
-        run_part(true);
-    } else {
-        run_part(false);
-    }
-    for (int stage = 1; stage < S; stage++) {
-        if (part == stage - 1) {
-#pragma unroll
-            for (int mi = 0; mi < NM; mi++) relay[mi * 64 + lane] = acc[mi];
-        }
-        __syncthreads();
-        if (part == stage) {
-#pragma unroll
-            for (int mi = 0; mi < NM; mi++) acc[mi] = relay[mi * 64 + lane];
-#pragma unroll
-            for (int kb = 0; kb < NBK; kb++) {
-                if (!full && kb0 + kb >= nb) break;   /* uniform */
-#pragma unroll
-                for (int mi = 0; mi < NM; mi++) acc[mi] = fadd(acc[mi], tm[kb][mi]);
-            }
-        }
-        __syncthreads();   /* the relay slot is read before the next stage writes it */
-    }
-    const int row = rt * 16 + 4 * kg + q;
-    const bool out = part == S - 1 && live && col < n;
     if (DOWN) {
-        if (out && row < mat[0].rows) a.Y[(size_t)(p0 + col) * a.D + row] = canon(acc[0]);
-        return;
-    }
-    float mv = 0.0f;
-    {
-        /* every lane takes the exp (the table is read across the wave); the outputs keep it */
-        const float gv = canon(acc[0]), uv = canon(acc[NM - 1]);
-        const float sg = fdiv(gv, fadd(1.0f, exp_glibc_f_wave(-gv, ev)));
-        if (out) {
-            mv = fmul(sg, uv);
-            if (!QF) a.midf[(size_t)(p0 + col) * a.F + row] = mv;
-        }
-    }
-    if constexpr (QF) {
-        /* the workgroup's rows [16 rpw tile, +16 rpw) are whole blocks of F: the last
-         * parts put them in LDS by (token, row), then wave j quantizes block j / 4 of
-         * token 4 g + j % 4 -- the values k_quant_rows would read from midf */
-        const int nr = 16 * rpw;
-        float *qb = relay0 + rpw * NM * 64;   /* [4 tokens][16 rpw], after the relay slots */
-        if (part == S - 1) qb[(lr & 3) * nr + rtl * 16 + 4 * kg + q] = mv;
-        __syncthreads();
-        if (wave < rpw) {
-            const int tt = wave & 3, bb = wave >> 2, tcol = 4 * g + tt;
-            if (tcol < n) quant_block_wave(qb[tt * nr + bb * 64 + lane], a.mid, p0 + tcol, (tile * nr) / 64 + bb);
-        }
+        /* down runs every group of the slot from the same weight registers (the
+         * stage loop's last barrier orders the relay slots between groups) */
+        const int ng = (n + 3) >> 2;
+        for (int gi = 0; gi < ng; gi++) group(gi);
+    } else {
+        group(g);
     }
 }
 
@@ -801,7 +812,8 @@ int launch_tk(const MoeArgs &a, int mode, int n_slots, hipStream_t st, hipEvent_
     const size_t lds = tk_lds_bytes(nbp, NM, NP, rpw, S, qf);
     if (W > 8 || lds > TK_LDS_MAX) return 0;
     const int tpw = ((rows + 15) / 16 + rpw - 1) / rpw;
-    const int gmax = (a.T + 3) / 4;   /* tokens per slot <= T */
+    /* gate/up: a workgroup per group of 4 tokens; down: one runs all of its slot's groups */
+    const int gmax = down ? 1 : (a.T + 3) / 4;   /* tokens per slot <= T */
     const int ch = tk_chunk(rpw);
     const int chunks = n_slots * ((tpw + ch - 1) / ch);
     const dim3 grid(8 * ((chunks + 7) / 8) * ch * gmax), block(64 * W);
