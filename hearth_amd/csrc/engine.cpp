@@ -2062,6 +2062,58 @@ HEARTH_API int hearth_verify_sample(hearth_engine *e, const int32_t *tokens, con
     });
 }
 
+HEARTH_API int hearth_gpu_verify_sample_dq(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,
+                                           const hearth_sampler *s, const double *q_dev, const double *u,
+                                           int32_t *path_out, int *n_path, int32_t *final_tok, float *logits) {
+    if (!e || !u || !q_dev || check_sampler(s) != OK) return E_ARG;
+    if (n > hxd::SAMPLE_NMAX || e->V > hxd::SAMPLE_VMAX) return E_ARG;
+    hipPointerAttribute_t pa{};
+    if (hipPointerGetAttributes(&pa, q_dev) != hipSuccess || pa.type != hipMemoryTypeDevice || pa.device != e->dev) {
+        (void)hipGetLastError();
+        log_msg(LOG_ERROR, "hearth_gpu_verify_sample_dq: q is not device memory of the engine's GPU");
+        return E_ARG;
+    }
+    return verify_and_commit(e, tokens, parent, n, logits, path_out, n_path, final_tok, "hearth_gpu_verify_sample_dq",
+                             [&](int *d_par, const int *&d_path, const int *&d_res) {
+        const int n_ctx = s->repetition_penalty != 1.0 ? s->n_context : 0;
+        ck(e->samp.ensure(n, e->V, false, n_ctx));
+        hxl::SamplerSpec sp{s->temperature, s->top_p, s->min_p, s->repetition_penalty, s->top_k, s->context, n_ctx};
+        ck(hxl::accept_sample(e->samp, e->logits, n, e->V, e->tokens, d_par, sp, q_dev, u, e->st, true));
+        d_path = e->samp.path;
+        d_res = e->samp.result;
+    });
+}
+
+HEARTH_API void *hearth_gpu_malloc(hearth_engine *e, size_t bytes) {
+    if (!e || !bytes || hipSetDevice(e->dev) != hipSuccess) return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
+
+HEARTH_API int hearth_gpu_upload(hearth_engine *e, void *dst, const void *src, size_t bytes) {
+    if (!e || !dst || (!src && bytes)) return E_ARG;
+    if (hipSetDevice(e->dev) != hipSuccess || hipStreamSynchronize(e->st) != hipSuccess ||
+        hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        return E_IO;
+    }
+    return OK;
+}
+
+HEARTH_API int hearth_gpu_free(hearth_engine *e, void *p) {
+    if (!e) return E_ARG;
+    if (!p) return OK;
+    if (hipSetDevice(e->dev) != hipSuccess || hipStreamSynchronize(e->st) != hipSuccess || hipFree(p) != hipSuccess) {
+        (void)hipGetLastError();
+        return E_IO;
+    }
+    return OK;
+}
+
 HEARTH_API int hearth_gpu_set_attn_mode(hearth_engine *e, int mode) {
     if (!e || (mode != HEARTH_GPU_ATTN_CANONICAL && mode != HEARTH_GPU_ATTN_CHUNKED)) return E_ARG;
     if (mode == HEARTH_GPU_ATTN_CHUNKED && !e->attn_chunk_ok) return E_ARG;

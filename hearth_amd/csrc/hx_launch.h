@@ -345,7 +345,7 @@ struct SampleScratch {
  * with device tokens/parent. The accepted path is left in m.path, and n_path, final
  * token and status (0, or -1 for bad logits) in m.result[0..2]. */
 hipError_t accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
-                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st);
+                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st, bool q_dev = false);
 /* The distribution kernel alone: m.P[v] = the final distribution of row v (the penalty
  * context of row v includes the path tokens of nodes 1..v), m.row_rc[v] its status. */
 hipError_t sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,

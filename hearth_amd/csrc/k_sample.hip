@@ -1073,13 +1073,13 @@ hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
 namespace {
 
 hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
-                     const SamplerSpec &s, const double *q, const double *u, hipStream_t st) {
+                     const SamplerSpec &s, const double *q, const double *u, hipStream_t st, bool q_dev = false) {
     a = SampleArgs{};
     a.rows = rows; a.n = n; a.V = V; a.tokens = tok; a.parent = par;
     a.temperature = s.temperature; a.top_p = s.top_p; a.min_p = s.min_p; a.rp = s.rp; a.top_k = s.top_k;
     a.n_ctx = s.rp != 1.0 ? s.n_ctx : 0;
     a.ctx = m.ctx;
-    a.q = q ? m.q : nullptr;
+    a.q = q ? (q_dev ? q : m.q) : nullptr;   /* q_dev: the caller's device rows, read in place */
     a.u = m.u;
     a.P = m.P; a.skey = m.skey; a.sidx = m.sidx; a.skey2 = m.skey2; a.sidx2 = m.sidx2; a.sort_n = m.sort_n;
     a.seg_begin = m.seg_begin; a.seg_end = m.seg_end; a.bstar = m.bstar;
@@ -1087,7 +1087,8 @@ hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, 
     a.row_rc = m.row_rc; a.path = m.path; a.result = m.result;
     build_tail(V, a.tail);
     hipError_t e = hipSuccess;
-    if (q && (e = hipMemcpyAsync(m.q, q, sizeof(double) * (size_t)n * V, hipMemcpyHostToDevice, st)) != hipSuccess) return e;
+    if (q && !q_dev && (e = hipMemcpyAsync(m.q, q, sizeof(double) * (size_t)n * V, hipMemcpyHostToDevice, st)) != hipSuccess)
+        return e;
     if (u && (e = hipMemcpyAsync(m.u, u, sizeof(double) * 2 * (size_t)n, hipMemcpyHostToDevice, st)) != hipSuccess) return e;
     if (a.n_ctx && (e = hipMemcpyAsync(m.ctx, s.ctx, sizeof(int) * (size_t)a.n_ctx, hipMemcpyHostToDevice, st)) != hipSuccess)
         return e;
@@ -1104,9 +1105,9 @@ hipError_t probs(SampleScratch &, const SampleArgs &a, int n, hipStream_t st) {
 } // namespace
 
 hipError_t accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
-                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st) {
+                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st, bool q_dev) {
     SampleArgs a;
-    hipError_t e = make_args(a, m, rows, n, V, tok, par, s, q, u, st);
+    hipError_t e = make_args(a, m, rows, n, V, tok, par, s, q, u, st, q_dev);
     if (e != hipSuccess || (e = probs(m, a, n, st)) != hipSuccess) return e;
     k_sample_walk<<<1, SP_T, 0, st>>>(a);
     return hipGetLastError();

@@ -141,6 +141,22 @@ HEARTH_API int hearth_verify_sample(hearth_engine *e, const int32_t *tokens, con
                                     const hearth_sampler *s, const double *q, const double *u, int32_t *path_out,
                                     int *n_path, int32_t *final_tok, float *logits);
 
+/* hearth_verify_sample with the draft distributions q_dev [n][V] float64 already in the
+ * engine GPU's memory (hearth_gpu_malloc / hearth_gpu_upload, or a draft model's output
+ * on the same device): read in place, so a step moves no q bytes over the host link.
+ * -1 also when q_dev is not device memory of the engine's GPU. The reference's
+ * hearth_verify_sample (hearth.h) takes q in host memory only. */
+HEARTH_API int hearth_gpu_verify_sample_dq(hearth_engine *e, const int32_t *tokens, const int32_t *parent, int n,
+                                           const hearth_sampler *s, const double *q_dev, const double *u,
+                                           int32_t *path_out, int *n_path, int32_t *final_tok, float *logits);
+
+/* Device memory on the engine's GPU for inputs such as q_dev: NULL on failure; upload
+ * copies host bytes into it after the engine's queued work; free releases it (NULL is
+ * allowed). No counterpart in the reference (its engine has no device). */
+HEARTH_API void *hearth_gpu_malloc(hearth_engine *e, size_t bytes);
+HEARTH_API int hearth_gpu_upload(hearth_engine *e, void *dst, const void *src, size_t bytes);
+HEARTH_API int hearth_gpu_free(hearth_engine *e, void *p);
+
 /* The sampled acceptance alone on caller logits rows [n][V] (no engine); same result as
  * hearth_verify_sample's walk. */
 HEARTH_API int hearth_gpu_accept_sample(const float *rows, int n, int V, const int32_t *tokens, const int32_t *parent,

@@ -178,7 +178,9 @@ def test_tree_4x4x4_sampled_ctx2047(prefilled, model):
         toks[c] = rng.choice(V, p=q[parent[c]])
     u = container.uniforms(91, 2 * n)
     smp = make_sampler(temperature=0.8, top_p=0.95)
-    path, final, lg = eng.verify_sample(toks, parent, smp, q=q, u=u, want_logits=True)
+    qd = eng.device_array(q)   # as the bench hands it over: resident in the GPU's memory
+    path, final, lg = eng.verify_sample(toks, parent, smp, q=qd, u=u, want_logits=True)
+    qd.free()
 
     m = O.Model(model, cap=n0 + n + 8, threads=THREADS)
     m.kv_import(s2, n0)

@@ -201,7 +201,11 @@ def test_verify_sample_matches_oracle_and_commits(eng):
             q = rng.random((n, V)) + 0.01
             q /= q.sum(1, keepdims=True)
         u = rng.random(2 * n)
-        path, fin, lg = eng.verify_sample(tok, par, E.make_sampler(context=prompt, **st), q=q, u=u, want_logits=True)
+        # trials 4 and 5 hand q over in the GPU's memory (hearth_gpu_verify_sample_dq)
+        qa = eng.device_array(q) if trial >= 4 else q
+        path, fin, lg = eng.verify_sample(tok, par, E.make_sampler(context=prompt, **st), q=qa, u=u, want_logits=True)
+        if trial >= 4:
+            qa.free()
         parent = par if par is not None else np.arange(-1, n - 1, dtype=np.int32)
         want = O.accept_tree_s(lg, tok, parent, O.sampler(context=prompt, **st), q=q, u=u)
         assert (0, path, fin) == want, trial
@@ -225,3 +229,27 @@ def test_verify_sample_chain_consumes_reference_uniforms(eng):
     ref.random(used)
     assert rng.random() == ref.random()
     assert eng.pos == 39 + n_acc + 1
+
+
+def test_verify_sample_dq_rejects_host_q(eng):
+    """hearth_gpu_verify_sample_dq returns -1, and commits nothing, for q in host memory."""
+    import ctypes
+    prompt = container.uniform_ints(24, 30, container.TINY.vocab)
+    eng.reset()
+    eng.eval(prompt[:-1])
+    tok = np.array([prompt[-1], 3, 4], dtype=np.int32)
+    q = np.full((3, container.TINY.vocab), 1.0 / container.TINY.vocab)
+    u = np.full(6, 0.5)
+    path, npath, fin = np.zeros(3, dtype=np.int32), ctypes.c_int(0), np.zeros(1, dtype=np.int32)
+    smp = E.make_sampler(temperature=0.8)
+    I32 = ctypes.POINTER(ctypes.c_int32)
+    rc = eng._api.need("gpu_verify_sample_dq")(
+        eng._handle(), tok.ctypes.data_as(I32), None, 3, ctypes.byref(smp), q.ctypes.data,
+        u.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), path.ctypes.data_as(I32), ctypes.byref(npath),
+        fin.ctypes.data_as(I32), None)
+    assert rc == -1 and eng.pos == 29
+    d = eng.device_array(q)
+    with pytest.raises(ValueError):
+        eng.verify_sample(tok[:2], None, smp, q=d, u=u)   # [3][V] rows for a 2-node call
+    d.free()
+    assert d.ptr is None
