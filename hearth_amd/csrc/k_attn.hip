@@ -1173,7 +1173,12 @@ void attention_finish(const AttnArgs &a, hipStream_t st) {
     k_attn_values<<<a.T * qpt * a.Hkv * nd, TV_THREADS, 0, st>>>(a);
 }
 
-bool attention_chunked_ok(int hd, int grp) { return (hd == 64 || hd == 128) && grp >= 1 && grp * hd <= AC_QMAX && grp <= 32 * 4; }
+/* the items of a block (grp / rw per token) must fit the block's waves: k_attn_chunk
+ * processes items wave + k AC_WAVES, k < AC_IPW, only */
+bool attention_chunked_ok(int hd, int grp) {
+    const int rw = grp % 4 == 0 ? 4 : grp % 2 == 0 ? 2 : 1;
+    return (hd == 64 || hd == 128) && grp >= 1 && grp * hd <= AC_QMAX && grp <= 32 * 4 && grp / rw <= AC_WAVES * AC_IPW;
+}
 
 void attention_chunked(const AttnArgs &a, hipStream_t st) {
     const int grp = a.H / a.Hkv, rw = grp % 4 == 0 ? 4 : grp % 2 == 0 ? 2 : 1, ipt = grp / rw;
