@@ -61,6 +61,9 @@ HEARTH_API int hearth_gpu_accept_greedy_noalloc(const float *rows, int n, int V,
                                                 void *stream) {
     if (!rows || n < 1 || V < 1 || !tokens || !path_out || !result) return hx::E_ARG;
     if (n > NOALLOC_ROWS) return hx::E_CAPACITY;
+    /* a HIP error the calling thread has not read yet is the caller's: it is left in place
+     * (not cleared by this call's check below) and nothing is launched */
+    if (hipPeekAtLastError() != hipSuccess) return hx::E_IO;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return hx::E_IO;
     unsigned char *base = (unsigned char *)scratch_on(dev);
@@ -86,7 +89,7 @@ HEARTH_API int hearth_gpu_accept_greedy_noalloc(const float *rows, int n, int V,
     a.path = path_out;
     a.result = result;
     hxl::accept_greedy(a, st);
-    return hipGetLastError() == hipSuccess ? hx::OK : hx::E_IO;
+    return hipGetLastError() == hipSuccess ? hx::OK : hx::E_IO;   /* this call's launches only */
 }
 
 } // extern "C"

@@ -101,7 +101,9 @@ HEARTH_API int hearth_gpu_accept_greedy(const float *rows, int n, int V, const i
  * of HEARTH_GPU_NOALLOC_MAX_ROWS rows (392 KiB) in the library, one per GPU, held until
  * the process ends: the call allocates nothing, and calls that overlap on one GPU race
  * on it. Returns 0, -1 for bad arguments, -3 when n exceeds the limit, -4 for a
- * device error; parent entries are not checked (any values give a bounded walk). */
+ * device error of this call's launches, or -4 without launching when the calling thread
+ * holds a HIP error it has not read yet (that error is left for the caller); parent
+ * entries are not checked (any values give a bounded walk). */
 #define HEARTH_GPU_NOALLOC_MAX_ROWS 1024
 HEARTH_API int hearth_gpu_accept_greedy_noalloc(const float *rows, int n, int V, const int32_t *tokens,
                                                 const int32_t *parent, int32_t *path_out, int32_t *result,

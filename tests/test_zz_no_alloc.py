@@ -122,3 +122,25 @@ def test_noalloc_rejects_rows_past_its_scratch(hip):
     d = hip.put(np.zeros(8, dtype=np.int32))
     assert _noalloc()(d, limit + 1, 4, d, None, d, d, None) == -3
     assert _noalloc()(None, 4, 4, d, None, d, d, None) == -1
+
+
+def test_noalloc_leaves_the_callers_pending_error(hip):
+    """A HIP error the calling thread has not read yet is not cleared or taken for this
+    call's own: the call returns -4 without launching, the error stays pending, and once
+    the caller reads it the call works."""
+    L = hip.L
+    L.hipPeekAtLastError.restype = c_int
+    L.hipGetLastError.restype = c_int
+    rows, tokens = _chain_case(3, 4, 256, 1)
+    d_rows, d_tok = hip.put(rows), hip.put(tokens)
+    d_path, d_res = hip.put(np.zeros(4, dtype=np.int32)), hip.put(np.zeros(3, dtype=np.int32))
+    L.hipGetLastError()
+    assert L.hipSetDevice(c_int(4096)) != 0          # no such device: the thread now holds an error
+    pending = L.hipPeekAtLastError()
+    assert pending != 0
+    assert _noalloc()(d_rows, 4, 256, d_tok, None, d_path, d_res, None) == -4
+    assert L.hipPeekAtLastError() == pending
+    assert L.hipGetLastError() == pending            # the caller reads (and clears) it
+    st, path, fin = _run_noalloc(hip, rows, tokens, None)
+    rc, rpath, rfin = accept_greedy(rows, tokens)
+    assert st == rc == 0 and path == rpath == [0, 1] and fin == rfin
