@@ -141,3 +141,16 @@ def test_sampled_device_loop_equals_host_steps(name, tiny_model, variant_models)
         assert counts[6] == "stop" and counts[7] == first[11]
         for n in (1, 5, 17):
             _same(e, prompt, n, (), "ngram", 6, 3, dict(temperature=1.1, top_p=0.9))
+
+
+@pytest.mark.parametrize("name", ["tiny", "dsv3_gqa"])
+def test_long_drafts_route_through_the_general_bucketing(name, tiny_model, variant_models):
+    """Drafts of 20 tokens: a step's 21 rows are past the small routing (at most 16
+    tokens), so the routing runs k_route_rank (ungrouped) or k_route_tokens (grouped) and
+    k_route_bucket, where the padding rows of short drafts add no expert pairs. The device
+    loop must still equal the host steps."""
+    path = tiny_model if name == "tiny" else variant_models(name)
+    with Engine(path, max_seq=512) as e:
+        prompt = _prompt(e.vocab_size)
+        got = _same(e, prompt, 60, (), "ngram", 20, 3)
+        assert got[1][4] > 0, "no drafts were proposed"
