@@ -622,9 +622,11 @@ def bench_dsv3(a) -> dict:
 
 
 def bench_generate(a) -> dict:
-    """End-to-end greedy generation with n-gram drafts on the Qwen3-30B-A3B shape: the
-    device loop against the host steps, same tokens required."""
+    """End-to-end generation with n-gram drafts on the Qwen3-30B-A3B shape, greedy and
+    sampled (temperature 0.8, top-p 0.95): the device loop against the host steps, the
+    same tokens required. value is the path generate() takes by default."""
     from hearth_amd import container
+    from hearth_amd import generate as G
     from hearth_amd.engine import Engine
     from hearth_amd.generate import Sampler, generate_ids
 
@@ -633,33 +635,44 @@ def bench_generate(a) -> dict:
     rnd = container.uniform_ints(4321, a.ctx // 2, container.QWEN3_30B_A3B.vocab)
     prompt = [int(t) for t in np.concatenate([rnd, rnd])[:a.ctx]]
     eng = Engine(path, max_seq=a.ctx + a.gen + 64, max_batch=512)
+    samplers = {"greedy": lambda: Sampler.greedy(), "sampled": lambda: Sampler(temperature=0.8, top_p=0.95, seed=11)}
     res = {}
-    for spec, k in (("ngram", a.k), ("none", 0)):
-        for loop in (False, True, False, True):   # warm both, then keep the second of each
-            ids, st = generate_ids(eng, prompt, a.gen, Sampler.greedy(), (), spec, k, 3, device_loop=loop)
-            res[spec, loop] = (ids, st)
-            log(f"[bench] {spec} k={k} device_loop={loop}: {st.new_tokens} tokens, {st.forwards} forwards, "
-                f"accepted {st.accepted}/{st.drafted}, decode {st.decode_tok_s:.1f} tok/s")
-        if res[spec, False][0] != res[spec, True][0]:
-            raise RuntimeError(f"{spec}: the device loop and the host steps generated different tokens")
+    for mode, make in samplers.items():
+        for spec, k in (("ngram", a.k), ("none", 0)):
+            for loop in (False, True, False, True):   # warm both, then keep the second of each
+                ids, st = generate_ids(eng, prompt, a.gen, make(), (), spec, k, 3, device_loop=loop)
+                res[mode, spec, loop] = (ids, st)
+                log(f"[bench] {mode} {spec} k={k} device_loop={loop}: {st.new_tokens} tokens, {st.forwards} forwards, "
+                    f"accepted {st.accepted}/{st.drafted}, decode {st.decode_tok_s:.1f} tok/s")
+            if res[mode, spec, False][0] != res[mode, spec, True][0]:
+                raise RuntimeError(f"{mode} {spec}: the device loop and the host steps generated different tokens")
+    default_loop = G._use_device_loop(eng, Sampler.greedy(), frozenset(), None, True, a.k)
     eng.close()
-    if res["ngram", True][0] != res["none", True][0]:
+    if res["greedy", "ngram", True][0] != res["greedy", "none", True][0]:
         raise RuntimeError("speculative and plain greedy generation differ")
-    d_st, h_st = res["ngram", True][1], res["ngram", False][1]
-    p_dev, p_host = res["none", True][1], res["none", False][1]
+    d_st = res["greedy", "ngram", default_loop][1]
+    rate = lambda m, s, l: round(res[m, s, l][1].decode_tok_s, 2)
+    ms = lambda m, s, l: round(res[m, s, l][1].decode_s / max(1, res[m, s, l][1].forwards) * 1e3, 4)
     return {
         "metric": "greedy_generate_decode_tok_s", "value": round(d_st.decode_tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": d_st.forwards, "warmup": 1, "ms_per_step": round(d_st.decode_s / max(1, d_st.forwards) * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": f"Qwen3-30B-A3B-shaped greedy generation of {a.gen} tokens after a {a.ctx}-token "
-                               f"self-repeating prompt, prompt-lookup drafts k={a.k} n<=3, device loop",
+                               f"self-repeating prompt, prompt-lookup drafts k={a.k} n<=3, generate()'s default "
+                               f"path ({'device loop' if default_loop else 'host steps'})",
                    "layers": a.layers, "ctx": a.ctx, "k": a.k, "gen": a.gen,
                    "tokens_per_forward": round(d_st.tokens_per_forward, 3),
                    "acceptance_rate": round(d_st.acceptance_rate, 4),
-                   "host_steps_decode_tok_s": round(h_st.decode_tok_s, 2),
-                   "host_steps_ms_per_forward": round(h_st.decode_s / max(1, h_st.forwards) * 1e3, 4),
-                   "plain_device_loop_decode_tok_s": round(p_dev.decode_tok_s, 2),
-                   "plain_host_steps_decode_tok_s": round(p_host.decode_tok_s, 2)},
+                   "greedy_device_loop_decode_tok_s": rate("greedy", "ngram", True),
+                   "greedy_host_steps_decode_tok_s": rate("greedy", "ngram", False),
+                   "greedy_device_loop_ms_per_forward": ms("greedy", "ngram", True),
+                   "greedy_host_steps_ms_per_forward": ms("greedy", "ngram", False),
+                   "plain_device_loop_decode_tok_s": rate("greedy", "none", True),
+                   "plain_host_steps_decode_tok_s": rate("greedy", "none", False),
+                   "sampled_device_loop_decode_tok_s": rate("sampled", "ngram", True),
+                   "sampled_host_steps_decode_tok_s": rate("sampled", "ngram", False),
+                   "sampled_plain_device_loop_decode_tok_s": rate("sampled", "none", True),
+                   "sampled_plain_host_steps_decode_tok_s": rate("sampled", "none", False)},
     }
 
 
