@@ -17,7 +17,7 @@
  *
  * Top-p does not sort the whole row. A histogram of the probabilities by exponent
  * (and one mantissa bit) picks the highest bins whose approximate mass exceeds top_p;
- * only their entries (tier 0, gathered in index order) take part in the running sum, and
+ * only their entries (tier 0, gathered in any order) take part in the running sum, and
  * they are not sorted whole either: by fine bins of their top bits from the top down,
  * a bin is added in bulk when no entry of it can take the running sum out of its binade,
  * to top_p or onto a rounding tie (then the sum over the bin is order-independent), and
@@ -31,7 +31,7 @@
  * continues -- the result never depends on the histogram.
  *
  * k_sample_probs:  one workgroup per verify row; the distribution up to top-p, then
- *                  the row's top-p candidates (tier 0) in index order;
+ *                  the row's top-p candidates (tier 0);
  * k_sample_top_p:  one workgroup per row; the cumulative-sum chain over tier 0 by fine
  *                  bins, the rest of the row if needed, renormalization, min-p;
  * k_sample_walk:   one workgroup walks the tree from the root with the uniforms.
@@ -96,6 +96,67 @@ __device__ __forceinline__ double lane_value(double x, int t) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
+/* ---------------------------------------------------------------- row passes */
+
+/* A pass over a row of up to SAMPLE_VMAX entries runs on one workgroup, so it is bound by
+ * the latency of its loads unless many are in flight: each thread issues the loads of
+ * SP_U of its indices before it runs their bodies. row_pass visits i = threadIdx.x + k SP_T
+ * (k ascending), range_pass a thread's contiguous [lo, hi) in order: the orders of the
+ * plain loops they replace. */
+constexpr int SP_U = 8;
+
+template <class Load, class Body>
+__device__ __forceinline__ void row_pass(int n, Load load, Body body) {
+    for (int i0 = threadIdx.x; i0 < n; i0 += SP_T * SP_U) {
+        decltype(load(0)) x[SP_U];
+#pragma unroll
+        for (int k = 0; k < SP_U; k++) {
+            const int i = i0 + k * SP_T;
+            if (i < n) x[k] = load(i);
+        }
+#pragma unroll
+        for (int k = 0; k < SP_U; k++) {
+            const int i = i0 + k * SP_T;
+            if (i < n) body(i, x[k]);
+        }
+    }
+}
+
+template <class Load, class Body>
+__device__ __forceinline__ void range_pass(int lo, int hi, Load load, Body body) {
+    for (int i0 = lo; i0 < hi; i0 += SP_U) {
+        decltype(load(0)) x[SP_U];
+#pragma unroll
+        for (int k = 0; k < SP_U; k++)
+            if (i0 + k < hi) x[k] = load(i0 + k);
+#pragma unroll
+        for (int k = 0; k < SP_U; k++)
+            if (i0 + k < hi) body(i0 + k, x[k]);
+    }
+}
+
+/* rounds of SP_T indices covering [0, n), SP_U rounds' loads issued at once, every lane
+ * of the workgroup running every round (index i valid iff i < n), for passes whose
+ * bodies use wave operations */
+template <class Load, class Body>
+__device__ __forceinline__ void row_pass_converged(int n, Load load, Body body) {
+    const int nr = (n + SP_T - 1) / SP_T;
+    for (int r0 = 0; r0 < nr; r0 += SP_U) {
+        decltype(load(0)) x[SP_U];
+#pragma unroll
+        for (int k = 0; k < SP_U; k++) {
+            const int i = (int)threadIdx.x + (r0 + k) * SP_T;
+            x[k] = (r0 + k < nr && i < n) ? load(i) : decltype(load(0))(0);
+        }
+#pragma unroll
+        for (int k = 0; k < SP_U; k++) {
+            if (r0 + k >= nr) break;   /* uniform */
+            const int i = (int)threadIdx.x + (r0 + k) * SP_T;
+            body(i, i < n, x[k]);
+        }
+    }
+}
+
 /* ---------------------------------------------------------------- numpy's sum */
 
 /* numpy's pairwise_sum on one leaf (n <= 128) */
@@ -130,7 +191,12 @@ __device__ double np_sum(const double *a, int V, const PwTail &tail, double *lv,
     const int tl = V - nfull * NP_BUF;
     const int nleaf = nfull * 64 + (tl ? tail.nleaf : 0);
     __syncthreads();                               /* a[] was written by other threads */
-    for (int L = threadIdx.x; L < nleaf; L += SP_T) {
+    /* leaves: eight lanes a leaf, lane k running pw_leaf's accumulator r_k (its loads all
+     * in flight at once for a full leaf), the group combining ((r0 + r1) + (r2 + r3)) +
+     * ((r4 + r5) + (r6 + r7)) by exchanges (the two lanes of a pair hold the same sum) and
+     * lane 0 adding the leaf's last len % 8 entries; leaves below 8 entries go in order */
+    for (int L8 = threadIdx.x; L8 < nleaf * 8; L8 += SP_T) {   /* a leaf's 8 lanes are active together */
+        const int L = L8 >> 3, k = L8 & 7;
         int start, len;
         if (L < nfull * 64) {
             start = (L >> 6) * NP_BUF + (L & 63) * 128;
@@ -140,7 +206,29 @@ __device__ double np_sum(const double *a, int V, const PwTail &tail, double *lv,
             start = nfull * NP_BUF + tail.leaf_start[t];
             len = tail.leaf_len[t];
         }
-        lv[L] = pw_leaf(a + start, len);
+        const double *x = a + start;
+        if (len < 8) {
+            if (k == 0) lv[L] = pw_leaf(x, len);
+            continue;
+        }
+        const int lim = len - (len % 8);
+        double r = x[k];
+        if (lim == 128) {
+            double y[15];
+#pragma unroll
+            for (int u = 0; u < 15; u++) y[u] = x[8 * (u + 1) + k];
+#pragma unroll
+            for (int u = 0; u < 15; u++) r = dadd(r, y[u]);
+        } else {
+            for (int i = 8; i < lim; i += 8) r = dadd(r, x[i + k]);
+        }
+        r = dadd(r, __shfl_xor(r, 1, 64));
+        r = dadd(r, __shfl_xor(r, 2, 64));
+        r = dadd(r, __shfl_xor(r, 4, 64));
+        if (k == 0) {
+            for (int i = lim; i < len; i++) r = dadd(r, x[i]);
+            lv[L] = r;
+        }
     }
     __syncthreads();
     for (int h = 1; h <= 7; h++) {
@@ -188,10 +276,10 @@ __device__ double select_rank(const double *x, int V, int r, uint32_t *hist, int
     for (int shift = 56; shift >= 0; shift -= 8) {
         for (int i = threadIdx.x; i < 256; i += SP_T) hist[i] = 0;
         __syncthreads();
-        for (int i = threadIdx.x; i < V; i += SP_T) {
-            const unsigned long long k = okey(x[i]);
+        row_pass(V, [&](int i) { return x[i]; }, [&](int, double xv) {
+            const unsigned long long k = okey(xv);
             if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255], 1u);
-        }
+        });
         __syncthreads();
         if (threadIdx.x < 64) {
             const int l = threadIdx.x;
@@ -289,22 +377,25 @@ __device__ void bitonic_global(unsigned long long *gkey, int *gidx, int N, unsig
 /* ---------------------------------------------------------------- exact running sums */
 
 /* The float64 running sum c_j = fl(c_{j-1} + x_j), j = 0..m-1, from c_{-1} = 0, of
- * finite x_j >= 0 (np.cumsum's chain), computed SP_T entries at a time by the whole
- * workgroup. While c stays in one binade [2^e, 2^(e+1)) every partial sum is a
- * multiple of u = 2^(e-52) and so is every rounded sum, so fl(c + x) = c + RN_u(x):
- * the integer prefix sums of RN_u(x_j) / u give every c_j of a chunk at once. An entry
- * whose sum would leave the binade, or whose x / u is halfway between two integers
- * (round-half-even then depends on the parity of c / u), is added on its own and the
- * chunk restarts after it. on_entry(j, c_j) is called once per entry by one thread.
- * The chain stops after the chunk in which c_j >= stop_at first holds; *stop_j gets
- * that j (m if never). Returns the last c computed. */
+ * finite x_j >= 0 (np.cumsum's chain), computed CE SP_T entries at a time by the whole
+ * workgroup (thread t takes CE consecutive entries of a chunk; CE 1 where entries added
+ * on their own are frequent, as in the sorted top-p bins near c's binade, since each
+ * restarts the chunk; CE 8 for the draw's chain over the row in index order). While c stays
+ * in one binade [2^e, 2^(e+1)) every partial sum is a multiple of u = 2^(e-52) and so is
+ * every rounded sum, so fl(c + x) = c + RN_u(x): the integer prefix sums of RN_u(x_j) / u
+ * give every c_j of a chunk at once. An entry whose sum would leave the binade, or whose
+ * x / u is halfway between two integers (round-half-even then depends on the parity of
+ * c / u), is added on its own and the chunk restarts after it. on_entry(j, c_j) is
+ * called once per entry by one thread. The chain stops after the chunk in which
+ * c_j >= stop_at first holds; *stop_j gets that j (m if never). Returns the last c
+ * computed. */
 struct ChainShared {
     long long wsum[SP_WAVES];
     double c, cnext;
     int first_bad, stop;
 };
 
-template <class GetX, class OnEntry>
+template <int CE_PER = 1, class GetX, class OnEntry>
 __device__ double chain_exact(GetX get_x, int m, double stop_at, int *stop_j, OnEntry on_entry, ChainShared &cs) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     double c = 0.0;
@@ -321,21 +412,28 @@ __device__ double chain_exact(GetX get_x, int m, double stop_at, int *stop_j, On
         if (e < -1022) e = -1022;
         const double u = ldexp(1.0, e - 52);
         const long long base = (long long)(c / u);   /* exact: c is a multiple of u below 2^53 u */
-        const int j = j0 + tid;
-        const double x = j < m ? get_x(j) : 0.0;
-        long long d = 0;
-        bool bad = false;
-        if (j < m) {
-            const double q = x / u;   /* a power-of-two scaling: exact */
-            if (!(q < 0x1p53)) {
-                bad = true;
-            } else {
-                const double f = floor(q), r = q - f;
-                d = (long long)f + (r > 0.5 ? 1 : 0);
-                bad = r == 0.5;
+        const int jt = j0 + tid * CE_PER;            /* this thread's first entry */
+        long long d[CE_PER];
+        bool bad[CE_PER];
+        long long tsum = 0;
+#pragma unroll
+        for (int k = 0; k < CE_PER; k++) {
+            const int j = jt + k;
+            d[k] = 0;
+            bad[k] = false;
+            if (j < m) {
+                const double q = get_x(j) / u;   /* a power-of-two scaling: exact */
+                if (!(q < 0x1p53)) {
+                    bad[k] = true;
+                } else {
+                    const double f = floor(q), r = q - f;
+                    d[k] = (long long)f + (r > 0.5 ? 1 : 0);
+                    bad[k] = r == 0.5;
+                }
             }
+            tsum += d[k];
         }
-        long long inc = d;
+        long long inc = tsum;
         for (int off = 1; off < 64; off <<= 1) {
             const long long y = __shfl_up(inc, off, 64);
             if (lane >= off) inc += y;
@@ -345,16 +443,35 @@ __device__ double chain_exact(GetX get_x, int m, double stop_at, int *stop_j, On
         __syncthreads();
         long long before = 0;
         for (int i = 0; i < w; i++) before += cs.wsum[i];
-        const long long D = base + before + inc;   /* c_j / u if no entry before j was bad */
-        if (j < m && (bad || D >= (1ll << 53))) atomicMin(&cs.first_bad, j);
+        const long long D0 = base + before + inc - tsum;   /* c / u before entry jt, if no earlier entry was bad */
+        {
+            long long D = D0;
+#pragma unroll
+            for (int k = 0; k < CE_PER; k++) {
+                const int j = jt + k;
+                if (j >= m) break;
+                D += d[k];
+                if (bad[k] || D >= (1ll << 53)) {
+                    atomicMin(&cs.first_bad, j);
+                    break;
+                }
+            }
+        }
         __syncthreads();
-        const int fb = cs.first_bad, jend = j0 + SP_T < m ? j0 + SP_T : m;
+        const int fb = cs.first_bad, jend = j0 + SP_T * CE_PER < m ? j0 + SP_T * CE_PER : m;
         const int last = (fb < jend ? fb : jend) - 1;   /* last entry finished in parallel */
-        if (j <= last) {
-            const double cj = (double)D * u;   /* an integer below 2^53 times a power of two: exact */
-            on_entry(j, cj);
-            if (cj >= stop_at) atomicMin(&cs.stop, j);
-            if (j == last) cs.c = cj;
+        {
+            long long D = D0;
+#pragma unroll
+            for (int k = 0; k < CE_PER; k++) {
+                const int j = jt + k;
+                if (j > last) break;
+                D += d[k];
+                const double cj = (double)D * u;   /* an integer below 2^53 times a power of two: exact */
+                on_entry(j, cj);
+                if (cj >= stop_at) atomicMin(&cs.stop, j);
+                if (j == last) cs.c = cj;
+            }
         }
         __syncthreads();
         if (last >= j0) c = cs.c;
@@ -421,15 +538,14 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
     }
     double best = -INF;
     int bidx = -1, flags = 0;
-    for (int i = tid; i < V; i += SP_T) {
-        const float l = row[i];
+    row_pass(V, [&](int i) { return row[i]; }, [&](int i, float l) {
         if (l != l || l == __builtin_huge_valf()) flags |= 1;
         if (l != -__builtin_huge_valf()) flags |= 2;
         double x = (double)l;
         if (pen && ((bits[i >> 5] >> (i & 31)) & 1u)) x = x > 0.0 ? ddiv(x, a.rp) : dmul(x, a.rp);
         P[i] = x;
         if (bidx < 0 || x > best) { best = x; bidx = i; }
-    }
+    });
     /* max and first argmax over the workgroup, flags */
     for (int off = 32; off >= 1; off >>= 1) {
         const double ob = __shfl_xor(best, off, 64);
@@ -457,19 +573,19 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
         return;
     }
     const double mx = best, T = a.temperature;
-    for (int i = tid; i < V; i += SP_T) P[i] = ddiv(dsub(P[i], mx), T);
     const bool use_k = a.top_k > 0 && a.top_k < V;
     double kth = -INF;
     if (use_k) {
+        row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = ddiv(dsub(x, mx), T); });
         __syncthreads();
         kth = select_rank(P, V, V - a.top_k, (uint32_t *)smem, rs.bi);
-    }
-    for (int i = tid; i < V; i += SP_T) {
-        const double x = P[i];
-        P[i] = (use_k && x < kth) ? 0.0 : exp_port_d(x);
+        row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = x < kth ? 0.0 : exp_port_d(x); });
+    } else {
+        /* the same values as the scaling pass and the exp pass one after the other */
+        row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = exp_port_d(ddiv(dsub(x, mx), T)); });
     }
     double s = np_sum(P, V, a.tail, lv, rs.bd);
-    for (int i = tid; i < V; i += SP_T) P[i] = ddiv(P[i], s);
+    row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = ddiv(x, s); });
 
     if (a.top_p < 1.0) {
         const double top_p = a.top_p;
@@ -477,14 +593,13 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
         double *hmass = (double *)(smem + HBINS * 4);
         for (int i = tid; i < HBINS; i += SP_T) { hcnt[i] = 0; hmass[i] = 0.0; }
         __syncthreads();
-        for (int i = tid; i < V; i += SP_T) {
-            const double p = P[i];
+        row_pass(V, [&](int i) { return P[i]; }, [&](int, double p) {
             if (p > 0.0) {
                 const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
                 atomicAdd(&hcnt[b], 1u);
                 atomicAdd(&hmass[b], p);
             }
-        }
+        });
         __syncthreads();
         /* the highest bin b* whose suffix mass reaches top_p + 1e-9 (approximate sums) */
         if (tid == 0) rs.bi[2] = -1;
@@ -508,27 +623,28 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
         }
         __syncthreads();
         const int bstar = rs.bi[2];
-        /* tier 0 (bins >= b*; all nonzero entries when b* < 0) in index order: thread tid
-         * takes the contiguous indices [tid * per, (tid + 1) * per) */
-        const int blo = bstar < 0 ? 0 : bstar, per = (V + SP_T - 1) / SP_T;
-        const int i0 = tid * per < V ? tid * per : V, i1 = i0 + per < V ? i0 + per : V;
-        int cnt = 0;
-        for (int i = i0; i < i1; i++) {
-            const double p = P[i];
-            cnt += (p > 0.0 && (int)((unsigned long long)__double_as_longlong(p) >> 51) >= blo) ? 1 : 0;
-        }
-        int m;
-        int o = wg_scan_excl(cnt, rs.red_i, &m);
+        /* tier 0 (bins >= b*; all nonzero entries when b* < 0), gathered a wave at a time (in
+         * no particular order: every use of it is by bins, and the bins it sorts are
+         * sorted by (p descending, index ascending), a total order) */
+        const int blo = bstar < 0 ? 0 : bstar;
         unsigned long long *key = a.skey + (size_t)v * a.sort_n;
         int *idx = a.sidx + (size_t)v * a.sort_n;
-        for (int i = i0; i < i1; i++) {
-            const double p = P[i];
-            if (p > 0.0 && (int)((unsigned long long)__double_as_longlong(p) >> 51) >= blo) {
-                key[o] = (unsigned long long)__double_as_longlong(p);
-                idx[o] = i;
-                o++;
+        if (tid == 0) rs.bi[3] = 0;
+        __syncthreads();
+        row_pass_converged(V, [&](int i) { return P[i]; }, [&](int i, bool in, double p) {
+            const bool cand = in && p > 0.0 && (int)((unsigned long long)__double_as_longlong(p) >> 51) >= blo;
+            const unsigned long long bal = __ballot(cand);
+            int base = 0;
+            if (lane == 0 && bal) base = atomicAdd(&rs.bi[3], __popcll(bal));
+            base = __shfl(base, 0, 64);
+            if (cand) {
+                const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+                key[pos] = (unsigned long long)__double_as_longlong(p);
+                idx[pos] = i;
             }
-        }
+        });
+        __syncthreads();
+        const int m = rs.bi[3];
         if (tid == 0) {
             a.seg_end[v] = v * a.sort_n + m;
             a.bstar[v] = bstar;
@@ -538,20 +654,19 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
     if (a.min_p > 0.0) {
         double mp = -INF;
         __syncthreads();
-        for (int i = tid; i < V; i += SP_T) mp = fmax(mp, P[i]);
+        row_pass(V, [&](int i) { return P[i]; }, [&](int, double x) { mp = fmax(mp, x); });
         mp = wg_max(mp, rs.red_d);
         const double thr = dmul(a.min_p, mp);
-        for (int i = tid; i < V; i += SP_T)
-            if (P[i] < thr) P[i] = 0.0;
+        row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { if (x < thr) P[i] = 0.0; });
         s = np_sum(P, V, a.tail, lv, rs.bd);
-        for (int i = tid; i < V; i += SP_T) P[i] = ddiv(P[i], s);
+        row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = ddiv(x, s); });
     }
     if (tid == 0) a.row_rc[v] = 0;
 }
 
 /* ---------------------------------------------------------------- top-p over fine bins */
 
-/* Tier 0 is summed without sorting it whole. The candidates (p bits and index, in index
+/* Tier 0 is summed without sorting it whole. The candidates (p bits and index, in any
  * order) fall into fine bins by their top bits: bin = (bits >> (51 - mb)) - (blo << mb),
  * a larger bin holding larger p, and the descending order is the bins from the top down,
  * each bin in its own order. The running sum c only needs that order inside a bin when
@@ -561,23 +676,27 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
  * between two multiples of u = 2^(e-52) (the tie goes to the even result, which depends
  * on c). Otherwise fl(c + p) = c + u RN(p / u) for each of its entries, whatever their
  * order, and every entry is kept (each c_j < top_p): the bin adds u times the sum of the
- * integers RN(p / u). A round computes those sums for every bin left at the current u
- * (one pass over the candidates), adds the bins above the first bin that meets (b)-(d)
- * in bulk, then gathers that bin, sorts it (p descending, index ascending: the stable
+ * integers RN(p / u). The candidates are first bucketed by bin (a counting sort), so a
+ * bin's entries are contiguous. A round walks the bins down from the current one in
+ * chunks of about TB_CHUNK entries: it computes the chunk's sums at the current u, adds
+ * the bins above the first one that meets (b)-(d) in bulk (or the whole chunk, and goes
+ * on with the next), then sorts that bin (p descending, index ascending: the stable
  * descending argsort) and runs chain_exact over it from c. Rounds continue down the bins
  * until the chain stops (c >= top_p (1 + 2^-48): the rest of the row is dropped) or
  * tier 0 runs out (c carries over to tier 1). Every p left is at most c (the top entry
  * is summed first), so p / u < 2^53; a bin's sum is kept as a high part (>> 20) and a
  * low part so that no 64-bit sum can wrap, and is saturated once it passes 2^53. */
 constexpr int TB_NBIN = 2048;
+constexpr int TB_CHUNK = 8 * SP_T;
 constexpr unsigned long long TB_FLAG = 1ull << 63, TB_SAT = 1ull << 60, TB_LIM = 1ull << 53;
 
 struct TopPBins {
     unsigned long long hi[TB_NBIN], lo[TB_NBIN];
     int cnt[TB_NBIN];
+    int off[TB_NBIN + 1];      /* bucket starts: bin b's entries are [off[b], off[b + 1]) */
     unsigned long long wpre[SP_WAVES];
-    unsigned long long dpre;   /* units before the crossing bin (or all, when none) */
-    int ib[4];                 /* [0] top bin, [1] gather counter, [2] crossing bin */
+    unsigned long long dpre;   /* units before the crossing bin (or after the chunk, when none) */
+    int ib[4];                 /* [0] top bin, [2] crossing bin, [3] chunk's lowest bin */
 };
 
 __device__ __forceinline__ unsigned long long tb_sat_add(unsigned long long a, unsigned long long b) {
@@ -592,6 +711,10 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const unsigned long long *key = a.skey + (size_t)v * a.sort_n;
     const int *idx = a.sidx + (size_t)v * a.sort_n;
+    /* the buckets, in the second candidate arrays; the first ones are free once they are
+     * filled, and hold the sorts too large for LDS */
+    unsigned long long *bkey = a.skey2 + (size_t)v * a.sort_n;
+    int *bidx = a.sidx2 + (size_t)v * a.sort_n;
     int mb = 0;
     while (mb < 7 && ((2048 - blo) << (mb + 1)) <= TB_NBIN) mb++;
     const int nb = (2048 - blo) << mb, sh = 51 - mb, bofs = blo << mb;
@@ -600,13 +723,13 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
     __syncthreads();
     {
         int top = -1;
-        for (int j = tid; j < m; j += SP_T) {
-            const int b = (int)(key[j] >> sh) - bofs;   /* in [0, nb): 0 < p <= 1 in a bin >= blo */
+        row_pass(m, [&](int j) { return key[j]; }, [&](int, unsigned long long k) {
+            const int b = (int)(k >> sh) - bofs;   /* in [0, nb): 0 < p <= 1 in a bin >= blo */
             if (b >= 0 && b < nb) {
                 atomicAdd(&tb.cnt[b], 1);
                 top = b > top ? b : top;
             }
-        }
+        });
         for (int off = 32; off >= 1; off >>= 1) {
             const int o = __shfl_xor(top, off, 64);
             top = o > top ? o : top;
@@ -614,6 +737,27 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
         if (lane == 0 && top >= 0) atomicMax(&tb.ib[0], top);
     }
     __syncthreads();
+    {
+        /* bucket starts (bins ascending), then the scatter with a cursor per bin (the
+         * low sums, not in use yet, hold the cursors) */
+        int *cursor = (int *)tb.lo;
+        const int b0 = 2 * tid, c0 = b0 < nb ? tb.cnt[b0] : 0, c1 = b0 + 1 < nb ? tb.cnt[b0 + 1] : 0;
+        int total;
+        const int o0 = wg_scan_excl(c0 + c1, (int *)tb.wpre, &total);
+        if (b0 < nb) { tb.off[b0] = o0; cursor[b0] = o0; }
+        if (b0 + 1 < nb) { tb.off[b0 + 1] = o0 + c0; cursor[b0 + 1] = o0 + c0; }
+        if (tid == 0) tb.off[nb] = total;
+        __syncthreads();
+        row_pass(m, [&](int j) { return key[j]; }, [&](int j, unsigned long long k) {
+            const int b = (int)(k >> sh) - bofs;
+            if (b >= 0 && b < nb) {
+                const int pos = atomicAdd(&cursor[b], 1);
+                bkey[pos] = k;
+                bidx[pos] = idx[j];
+            }
+        });
+        __syncthreads();
+    }
     int cur = tb.ib[0];
     double c = 0.0;
     stopped = false;
@@ -627,14 +771,29 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
             int e = ilogb(c);
             if (e < -1022) e = -1022;
             const double u = ldexp(1.0, e - 52);
-            const unsigned long long D0 = (unsigned long long)(c / u);   /* exact: c is a multiple of u below 2^53 u */
-            for (int b = tid; b <= cur; b += SP_T) { tb.hi[b] = 0ull; tb.lo[b] = 0ull; }
-            if (tid == 0) tb.ib[2] = -1;
-            __syncthreads();
-            for (int j = tid; j < m; j += SP_T) {
-                const unsigned long long k = key[j];
-                const int b = (int)(k >> sh) - bofs;
-                if (b >= 0 && b <= cur) {
+            unsigned long long D = (unsigned long long)(c / u);   /* exact: c is a multiple of u below 2^53 u */
+            bx = -1;
+            int top_b = cur;
+            while (top_b >= 0) {
+                /* the chunk [lo_b, top_b]: the lowest lo_b with at most TB_CHUNK entries in
+                 * it, and at least the bin top_b (bucket starts ascend with the bin) */
+                if (tid == 0) {
+                    const int want = tb.off[top_b + 1] - TB_CHUNK;
+                    int lo = 0, hi = top_b;   /* the smallest lo in [0, top_b] with off[lo] >= want */
+                    while (lo < hi) {
+                        const int mid = (lo + hi) >> 1;
+                        if (tb.off[mid] >= want) hi = mid; else lo = mid + 1;
+                    }
+                    tb.ib[3] = lo;
+                    tb.ib[2] = -1;
+                }
+                for (int b = tid; b <= top_b; b += SP_T)
+                    if (b >= 0) { tb.hi[b] = 0ull; tb.lo[b] = 0ull; }
+                __syncthreads();
+                const int lo_b = tb.ib[3];
+                const int j0 = tb.off[lo_b], j1 = tb.off[top_b + 1];
+                row_pass(j1 - j0, [&](int j) { return bkey[j0 + j]; }, [&](int, unsigned long long k) {
+                    const int b = (int)(k >> sh) - bofs;
                     const double q = __longlong_as_double((long long)k) / u;   /* a power-of-two scaling: exact */
                     const double f = floor(q), r = q - f;
                     if (r == 0.5) {
@@ -644,48 +803,55 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
                         atomicAdd(&tb.hi[b], d >> 20);
                         atomicAdd(&tb.lo[b], d & 0xFFFFFull);
                     }
+                });
+                __syncthreads();
+                /* descending scan over the chunk: thread t holds bins top_b - 2t (first)
+                 * and top_b - 2t - 1 */
+                const int b1 = top_b - 2 * tid, b2 = b1 - 1;
+                auto sval = [&](int b, bool &flag) -> unsigned long long {
+                    flag = false;
+                    if (b < lo_b) return 0ull;
+                    const unsigned long long h = tb.hi[b];
+                    flag = (h & TB_FLAG) != 0ull;
+                    const unsigned long long hh = h & ~TB_FLAG;
+                    if (hh >= (1ull << 33)) return TB_SAT;
+                    return tb_sat_add(hh << 20, tb.lo[b]);
+                };
+                bool f1, f2;
+                const unsigned long long s1 = sval(b1, f1), s2 = sval(b2, f2), s12 = tb_sat_add(s1, s2);
+                unsigned long long inc = s12;
+                for (int off = 1; off < 64; off <<= 1) {
+                    const unsigned long long y = __shfl_up(inc, off, 64);
+                    if (lane >= off) inc = tb_sat_add(inc, y);
                 }
+                if (lane == 63) tb.wpre[w] = inc;
+                __syncthreads();
+                unsigned long long wb = 0ull;
+                for (int i = 0; i < w; i++) wb = tb_sat_add(wb, tb.wpre[i]);
+                unsigned long long excl = __shfl_up(inc, 1, 64);
+                excl = tb_sat_add(wb, lane ? excl : 0ull);
+                const unsigned long long pre1 = tb_sat_add(D, excl), aft1 = tb_sat_add(pre1, s1), aft2 = tb_sat_add(aft1, s2);
+                auto crosses = [&](unsigned long long after) {
+                    return after >= TB_LIM || (double)after * u >= top_p;
+                };
+                int cand = -1;
+                if (b1 >= lo_b && (f1 || crosses(aft1))) cand = b1;
+                else if (b2 >= lo_b && (f2 || crosses(aft2))) cand = b2;
+                if (cand >= 0) atomicMax(&tb.ib[2], cand);
+                __syncthreads();
+                const int bc = tb.ib[2];
+                if (bc >= 0 && (bc == b1 || bc == b2)) tb.dpre = bc == b1 ? pre1 : aft1;
+                if (bc < 0 && tid == SP_T - 1) tb.dpre = tb_sat_add(D, tb_sat_add(wb, inc));   /* the whole chunk */
+                __syncthreads();
+                D = tb.dpre;
+                __syncthreads();
+                if (bc >= 0) {
+                    bx = bc;
+                    break;
+                }
+                top_b = lo_b - 1;
             }
-            __syncthreads();
-            /* descending scan: thread t holds bins cur - 2t (first) and cur - 2t - 1 */
-            const int b1 = cur - 2 * tid, b2 = b1 - 1;
-            auto sval = [&](int b, bool &flag) -> unsigned long long {
-                flag = false;
-                if (b < 0) return 0ull;
-                const unsigned long long h = tb.hi[b];
-                flag = (h & TB_FLAG) != 0ull;
-                const unsigned long long hh = h & ~TB_FLAG;
-                if (hh >= (1ull << 33)) return TB_SAT;
-                return tb_sat_add(hh << 20, tb.lo[b]);
-            };
-            bool f1, f2;
-            const unsigned long long s1 = sval(b1, f1), s2 = sval(b2, f2), s12 = tb_sat_add(s1, s2);
-            unsigned long long inc = s12;
-            for (int off = 1; off < 64; off <<= 1) {
-                const unsigned long long y = __shfl_up(inc, off, 64);
-                if (lane >= off) inc = tb_sat_add(inc, y);
-            }
-            if (lane == 63) tb.wpre[w] = inc;
-            __syncthreads();
-            unsigned long long wb = 0ull;
-            for (int i = 0; i < w; i++) wb = tb_sat_add(wb, tb.wpre[i]);
-            unsigned long long excl = __shfl_up(inc, 1, 64);
-            excl = tb_sat_add(wb, lane ? excl : 0ull);
-            const unsigned long long pre1 = tb_sat_add(D0, excl), aft1 = tb_sat_add(pre1, s1), aft2 = tb_sat_add(aft1, s2);
-            auto crosses = [&](unsigned long long after) {
-                return after >= TB_LIM || (double)after * u >= top_p;
-            };
-            int cand = -1;
-            if (b1 >= 0 && (f1 || crosses(aft1))) cand = b1;
-            else if (b2 >= 0 && (f2 || crosses(aft2))) cand = b2;
-            if (cand >= 0) atomicMax(&tb.ib[2], cand);
-            __syncthreads();
-            bx = tb.ib[2];
-            if (bx >= 0 && (bx == b1 || bx == b2)) tb.dpre = bx == b1 ? pre1 : aft1;
-            if (bx < 0 && tid == SP_T - 1) tb.dpre = tb_sat_add(D0, tb_sat_add(wb, inc));   /* every bin left */
-            __syncthreads();
-            c = (double)tb.dpre * u;   /* below 2^53 u: exact */
-            __syncthreads();
+            c = (double)D * u;   /* below 2^53 u: exact */
         }
         if (bx < 0) break;   /* every bin left was added in bulk */
         const int n = tb.cnt[bx];
@@ -693,23 +859,12 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
             int N = 1;
             while (N < n) N <<= 1;
             const bool in_lds = N <= SORT_LDS;
-            unsigned long long *sk = in_lds ? (unsigned long long *)smem : a.skey2 + (size_t)v * a.sort_n;
-            int *si = in_lds ? (int *)(smem + SORT_LDS * 8) : a.sidx2 + (size_t)v * a.sort_n;
-            if (tid == 0) tb.ib[1] = 0;
-            __syncthreads();
-            for (int j0 = 0; j0 < m; j0 += SP_T) {
-                const int j = j0 + tid;
-                const unsigned long long k = j < m ? key[j] : 0ull;
-                const bool in = j < m && (int)(k >> sh) - bofs == bx;
-                const unsigned long long bal = __ballot(in);
-                int base = 0;
-                if (lane == 0 && bal) base = atomicAdd(&tb.ib[1], __popcll(bal));
-                base = __shfl(base, 0, 64);
-                if (in) {
-                    const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
-                    sk[pos] = k;
-                    si[pos] = idx[j];
-                }
+            unsigned long long *sk = in_lds ? (unsigned long long *)smem : a.skey + (size_t)v * a.sort_n;
+            int *si = in_lds ? (int *)(smem + SORT_LDS * 8) : a.sidx + (size_t)v * a.sort_n;
+            const int j0 = tb.off[bx];
+            for (int j = tid; j < n; j += SP_T) {
+                sk[j] = bkey[j0 + j];
+                si[j] = bidx[j0 + j];
             }
             for (int j = n + tid; j < N; j += SP_T) { sk[j] = 0ull; si[j] = INT_MAX; }
             __syncthreads();
@@ -739,9 +894,11 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
         }
         cur = bx - 1;
     }
-    if (stopped)
-        for (int j = tid; j < m; j += SP_T)
-            if ((int)(key[j] >> sh) - bofs < stop_bin) P[idx[j]] = 0.0;
+    if (stopped) {
+        /* the bins below the stop's: their entries are the buckets' first off[stop_bin] */
+        const int j1 = tb.off[stop_bin];
+        row_pass(j1, [&](int j) { return bidx[j]; }, [&](int, int i) { P[i] = 0.0; });
+    }
     __syncthreads();
     return c;
 }
@@ -783,22 +940,20 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
                 if (stopped || c >= thr_hi) {
                     done = true;
                     if (blo > 0)
-                        for (int i = tid; i < V; i += SP_T) {
-                            const double p = P[i];
+                        row_pass(V, [&](int i) { return P[i]; }, [&](int i, double p) {
                             const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
                             if (p > 0.0 && b < blo) P[i] = 0.0;
-                        }
+                        });
                 }
                 __syncthreads();
                 continue;
             } else {
             /* count, then gather the tier's entries */
             int cnt = 0;
-            for (int i = tid; i < V; i += SP_T) {
-                const double p = P[i];
+            row_pass(V, [&](int i) { return P[i]; }, [&](int, double p) {
                 const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
                 cnt += (p > 0.0 && b >= blo && b < bhi) ? 1 : 0;
-            }
+            });
             const int off0 = wg_scan_excl(cnt, rs.red_i, &m);
             (void)off0;
             if (m == 0) continue;
@@ -856,27 +1011,25 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
                 done = true;
                 /* every entry below the tier is dropped */
                 if (blo > 0)
-                    for (int i = tid; i < V; i += SP_T) {
-                        const double p = P[i];
+                    row_pass(V, [&](int i) { return P[i]; }, [&](int i, double p) {
                         const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
                         if (p > 0.0 && b < blo) P[i] = 0.0;
-                    }
+                    });
             }
             __syncthreads();
         }
         s = np_sum(P, V, a.tail, lv, rs.bd);
-        for (int i = tid; i < V; i += SP_T) P[i] = ddiv(P[i], s);
+        row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = ddiv(x, s); });
     }
     if (a.min_p > 0.0) {
         double mp = -INF;
         __syncthreads();
-        for (int i = tid; i < V; i += SP_T) mp = fmax(mp, P[i]);
+        row_pass(V, [&](int i) { return P[i]; }, [&](int, double x) { mp = fmax(mp, x); });
         mp = wg_max(mp, rs.red_d);
         const double thr = dmul(a.min_p, mp);
-        for (int i = tid; i < V; i += SP_T)
-            if (P[i] < thr) P[i] = 0.0;
+        row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { if (x < thr) P[i] = 0.0; });
         s = np_sum(P, V, a.tail, lv, rs.bd);
-        for (int i = tid; i < V; i += SP_T) P[i] = ddiv(P[i], s);
+        row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = ddiv(x, s); });
     }
     if (tid == 0) a.row_rc[v] = 0;
 }
@@ -890,20 +1043,27 @@ __device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *
     const int per = (V + SP_T - 1) / SP_T;
     const int lo = tid * per < V ? tid * per : V, hi = lo + per < V ? lo + per : V;
     int cnt = 0;
-    for (int i = lo; i < hi; i++) cnt += w[i] > 0.0 ? 1 : 0;
+    range_pass(lo, hi, [&](int i) { return w[i]; }, [&](int, double x) { cnt += x > 0.0 ? 1 : 0; });
     int nnz;
     int o = wg_scan_excl(cnt, red, &nnz);
-    for (int i = lo; i < hi; i++)
-        if (w[i] > 0.0) { a.cw[o] = w[i]; a.ci[o] = i; o++; }
+    range_pass(lo, hi, [&](int i) { return w[i]; }, [&](int i, double x) {
+        if (x > 0.0) { a.cw[o] = x; a.ci[o] = i; o++; }
+    });
     __syncthreads();
     int stop;
-    const double total = chain_exact([&](int j) { return a.cw[j]; }, nnz, INF, &stop,
+    const double total = chain_exact<8>([&](int j) { return a.cw[j]; }, nnz, INF, &stop,
                                      [&](int j, double cj) { a.cc[j] = cj; }, cs);
     if (tid == 0) sh[0] = INT_MAX;
     __syncthreads();
     const double target = dmul(u, total);
-    for (int j = tid; j < nnz; j += SP_T)
-        if (a.cc[j] > target) { atomicMin(&sh[0], j); break; }
+    {
+        /* a thread's first index above the target is its smallest: the rest of its
+         * indices cannot lower the minimum */
+        bool found = false;
+        row_pass(nnz, [&](int j) { return a.cc[j]; }, [&](int j, double cj) {
+            if (!found && cj > target) { atomicMin(&sh[0], j); found = true; }
+        });
+    }
     __syncthreads();
     const int jb = sh[0];
     const int r = jb < nnz ? a.ci[jb] : (nnz > 0 ? a.ci[nnz - 1] : 0);
@@ -945,12 +1105,12 @@ __global__ __launch_bounds__(SP_T) void k_sample_walk(SampleArgs a) {
             const double ratio = ddiv(px, qv ? qv[x] : 1.0);
             if (a.u[2 * c] < ratio) { next = c; break; }
             double *dst = bufs[cur];
-            for (int i = tid; i < V; i += SP_T) {
-                const double pc = s < 0.0 ? p[i] : ddiv(r[i], s);
-                const double qi = qv ? qv[i] : (i == x ? 1.0 : 0.0);
-                const double d = dsub(pc, qi);
+            row_pass(V, [&](int i) { return make_double2(s < 0.0 ? p[i] : r[i], qv ? qv[i] : (i == x ? 1.0 : 0.0)); },
+                     [&](int i, double2 pq) {
+                const double pc = s < 0.0 ? pq.x : ddiv(pq.x, s);
+                const double d = dsub(pc, pq.y);
                 dst[i] = d > 0.0 ? d : 0.0;
-            }
+            });
             const double ns = np_sum(dst, V, a.tail, lv, shd + 2);
             if (ns <= 0.0) { next = c; break; }
             r = dst;
