@@ -175,6 +175,7 @@ struct hearth_engine {
     };
     std::vector<Captured> graphs;
     bool graph_on = true;    /* HEARTH_GPU_GRAPH=0 turns capture off */
+    bool graph_report = false;   /* HEARTH_GPU_GRAPH_REPORT=1: describe each captured graph on stderr */
     /* attention order of the GQA layers: 0 the reference's canonical order (default), 1
      * chunked (where the shape allows it, attn_chunk_ok); MLA layers are canonical */
     int attn_mode = 0;
@@ -1154,6 +1155,43 @@ int hearth_engine::run_geometry(const int32_t *tok, const int32_t *parent, int n
     return OK;
 }
 
+/* HEARTH_GPU_GRAPH_REPORT: the node census of a captured graph (node types, kernel
+ * nodes' distinct functions, the largest grid, block and LDS request, dependency edges),
+ * for comparing what a tool that walks the graph at launch has to handle. */
+static void report_graph(hipGraph_t g, const char *what, int T) {
+    size_t n = 0;
+    if (hipGraphGetNodes(g, nullptr, &n) != hipSuccess) return;
+    std::vector<hipGraphNode_t> nodes(n);
+    if (n && hipGraphGetNodes(g, nodes.data(), &n) != hipSuccess) return;
+    size_t edges = 0;
+    (void)hipGraphGetEdges(g, nullptr, nullptr, &edges);
+    int counts[16] = {};
+    std::vector<const void *> funcs;
+    unsigned max_grid = 0, max_block = 0, max_lds = 0, null_params = 0;
+    for (hipGraphNode_t nd : nodes) {
+        hipGraphNodeType t{};
+        if (hipGraphNodeGetType(nd, &t) != hipSuccess) continue;
+        counts[(int)t & 15]++;
+        if (t != hipGraphNodeTypeKernel) continue;
+        hipKernelNodeParams kp{};
+        if (hipGraphKernelNodeGetParams(nd, &kp) != hipSuccess) continue;
+        if (std::find(funcs.begin(), funcs.end(), kp.func) == funcs.end()) funcs.push_back(kp.func);
+        max_grid = std::max(max_grid, kp.gridDim.x * kp.gridDim.y * kp.gridDim.z);
+        max_block = std::max(max_block, kp.blockDim.x * kp.blockDim.y * kp.blockDim.z);
+        max_lds = std::max(max_lds, kp.sharedMemBytes);
+        if (!kp.kernelParams && !kp.extra) null_params++;
+    }
+    (void)hipGetLastError();
+    log_msg(LOG_ERROR,
+            "graph report (%s, T=%d): %zu nodes (kernel %d, memcpy %d, memset %d, host %d, graph %d, empty %d, "
+            "wait event %d, record event %d), %zu edges, %zu distinct kernels, largest grid %u workgroups, block %u, "
+            "dynamic LDS %u B, %u kernel nodes without arguments",
+            what, T, n, counts[hipGraphNodeTypeKernel], counts[hipGraphNodeTypeMemcpy], counts[hipGraphNodeTypeMemset],
+            counts[hipGraphNodeTypeHost], counts[hipGraphNodeTypeGraph], counts[hipGraphNodeTypeEmpty],
+            counts[hipGraphNodeTypeWaitEvent], counts[hipGraphNodeTypeEventRecord], edges, funcs.size(), max_grid,
+            max_block, max_lds, null_params);
+}
+
 /* The forward of T tokens whose geometry is uploaded: replayed from a captured graph
  * when the call is one a graph can serve (experts resident, no route replay, no
  * per-launch timing or debug dumps, at most 128 tokens), else launched directly. The
@@ -1201,6 +1239,7 @@ void hearth_engine::run_forward(int T, bool want_logits) {
         }
         rows_bound = 0;
         ck(hipStreamEndCapture(st, &g.graph));
+        if (graph_report) report_graph(g.graph, "forward", T);
         const hipError_t e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
         if (e != hipSuccess) {
             (void)hipGraphDestroy(g.graph);
@@ -1323,6 +1362,7 @@ void hearth_engine::launch_loop_step(int T, int rows) {
             throw;
         }
         ck(hipStreamEndCapture(st, &g.graph));
+        if (graph_report) report_graph(g.graph, "loop step", T);
         const hipError_t e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
         if (e != hipSuccess) {
             (void)hipGraphDestroy(g.graph);
@@ -1503,6 +1543,7 @@ HEARTH_API hearth_engine *hearth_open(const hearth_options *in, char *err, size_
     e->verbose = o.verbose;
     if (const char *dd = getenv("HEARTH_DEBUG_DUMP")) e->dump_dir = dd;
     if (const char *gg = getenv("HEARTH_GPU_GRAPH")) e->graph_on = strcmp(gg, "0") != 0;
+    if (const char *gr = getenv("HEARTH_GPU_GRAPH_REPORT")) e->graph_report = strcmp(gr, "0") != 0;
     if (!e->open_model(err, errlen)) return nullptr;
     const char *am = getenv("HEARTH_GPU_ATTN");
     e->attn_mode = e->attn_chunk_ok && am && strcmp(am, "chunked") == 0 ? 1 : 0;
