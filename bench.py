@@ -537,19 +537,32 @@ def bench_dsv3(a) -> dict:
     """DeepSeek-V3 shape (3 dense + 20 MoE layers), greedy chain verify k=8 at a
     4096-token context with the routed experts streamed from pinned host memory through
     an HBM cache smaller than the expert set (HEARTH_GPU_EXPERT_CACHE_GB, default 56),
-    next-layer prefetch on; the same steps with every expert resident for comparison."""
+    next-layer prefetch on; the same steps with every expert resident for comparison.
+    --routes uniform replays routes drawn uniformly (each token 8 distinct experts of 256 in
+    every MoE layer, hearth_route_replay) instead of the synthetic router's, whose choices
+    concentrate on a subset of each layer: the regime where most demands miss a cache of
+    half the expert set."""
     from hearth_amd import container
     from hearth_amd.engine import Engine
 
     ctx, k = 4096, a.k
-    V = container.DEEPSEEK_V3.vocab
+    sh = container.DEEPSEEK_V3
+    V = sh.vocab
     path = dsv3_model_path(ctx)
     prompt = container.uniform_ints(5678, ctx, V).astype(np.int32)
     need = (a.warmup + a.steps) * (k + 1) + k + 2
     cap = ctx + need + 16
+    trace = None
+    if a.routes == "uniform":
+        n_moe = sh.n_layers - sh.n_dense
+        ids = container.zipf_routes(4242, cap + 64, n_moe, sh.n_experts, sh.top_k, s=0.0)   # s = 0: uniform
+        trace = container.write_route_trace(Path(tempfile.mkdtemp()) / "uniform.hrtr", ids, sh.n_layers,
+                                            sh.n_experts)
     t = time.time()
     eng = Engine(path, max_seq=cap, max_batch=512)
     log(f"[bench] resident open {time.time() - t:.1f}s")
+    if trace is not None:
+        eng.route_replay(trace)
     eng.eval(prompt[:-1])
     base = eng.pos
     snap = eng.kv_export(base)
@@ -577,8 +590,11 @@ def bench_dsv3(a) -> dict:
     os.environ["HEARTH_GPU_EXPERT_CACHE_GB"] = budget
     t = time.time()
     eng = Engine(path, max_seq=cap, max_batch=512, prefetch="shared")
-    log(f"[bench] streamed open {time.time() - t:.1f}s")
+    open_s = time.time() - t
+    log(f"[bench] streamed open {open_s:.1f}s")
     info0 = eng.store_info()
+    if trace is not None:
+        eng.route_replay(trace)
     eng.kv_import(snap, base)
     marks = {}
 
@@ -607,7 +623,9 @@ def bench_dsv3(a) -> dict:
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "DeepSeek-V3-shaped MLA MoE (3 dense + 20 MoE layers, 256 experts top-8 + shared, "
                                "Q4 experts / Q8 dense), greedy chain verify k=8 at context 4096, drafts = greedy "
-                               "continuation with 30% random replacement",
+                               "continuation with 30% random replacement" +
+                               (", routes replayed uniformly at random" if trace is not None else ""),
+                   "routes": a.routes, "streamed_open_s": round(open_s, 2),
                    "expert_cache_gb": float(budget), "cache_slots": info0["slots"], "experts_total": E_all,
                    "slot_bytes": info0["slot_bytes"], "host_tier_bytes": info0["host_tier_bytes"],
                    "tokens_per_step": round(sum(toks) / a.steps, 3),
@@ -691,6 +709,8 @@ def main(argv=None) -> int:
                          "n-gram drafts, device loop against host steps")
     ap.add_argument("--gen", type=int, default=256, help="generate: tokens to generate")
     ap.add_argument("--resident-only", action="store_true", help="dsv3: skip the streamed run")
+    ap.add_argument("--routes", choices=("model", "uniform"), default="model",
+                    help="dsv3: the synthetic router's routes, or uniform random routes replayed")
     ap.add_argument("--cpu-steps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--summarize-trace", metavar="CSV",
