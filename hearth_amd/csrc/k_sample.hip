@@ -400,12 +400,38 @@ __device__ double chain_exact(GetX get_x, int m, double stop_at, int *stop_j, On
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     double c = 0.0;
     int j0 = 0, stop = m;
+    bool in_order = true;   /* the next 64 entries one after the other (from c = 0, or after a round that gained little) */
     while (j0 < m && stop == m) {
-        if (c == 0.0) {   /* fl(0 + x) = x */
-            c = get_x(j0);
-            if (tid == 0) on_entry(j0, c);
-            if (c >= stop_at) stop = j0;
-            j0++;
+        if (in_order) {
+            /* wave 0 loads 64 entries at once and every lane runs the chain through them
+             * (fl(0 + x) = x, so c = 0 needs no case of its own); lane k keeps c after
+             * entry j0 + k. Where entries added on their own are frequent (c small, or
+             * near the entries' own binade), this costs one dependent add an entry
+             * instead of a round of the workgroup. */
+            if (w == 0) {
+                const int n = m - j0 < 64 ? m - j0 : 64;
+                const double x = lane < n ? get_x(j0 + lane) : 0.0;
+                double cc = c, mine = 0.0;
+                for (int k = 0; k < n; k++) {
+                    cc = dadd(cc, lane_value(x, k));
+                    if (lane == k) mine = cc;
+                }
+                if (lane < n) on_entry(j0 + lane, mine);
+                const unsigned long long hit = __ballot(lane < n && mine >= stop_at);
+                if (lane == 0) {
+                    cs.c = cc;
+                    cs.stop = hit ? j0 + __builtin_ctzll(hit) : INT_MAX;
+                }
+            }
+            __syncthreads();
+            c = cs.c;
+            if (cs.stop != INT_MAX) {
+                stop = cs.stop;
+                break;
+            }
+            j0 = j0 + 64 < m ? j0 + 64 : m;
+            in_order = c == 0.0;
+            __syncthreads();
             continue;
         }
         int e = ilogb(c);
@@ -483,6 +509,7 @@ __device__ double chain_exact(GetX get_x, int m, double stop_at, int *stop_j, On
             c = dadd(c, get_x(fb));
             if (tid == 0) on_entry(fb, c);
             if (c >= stop_at) stop = fb;
+            in_order = fb - j0 < 64;   /* the round gained little: go on one entry at a time */
             j0 = fb + 1;
         } else {
             j0 = jend;
@@ -1037,22 +1064,44 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
 /* ---------------------------------------------------------------- the walk */
 
 /* inverse-CDF draw from w[0..V) (unnormalised, nonnegative, not all zero) with
- * uniform u: np.cumsum order, first index whose running sum exceeds u * total */
+ * uniform u: np.cumsum order, first index whose running sum exceeds u * total. The chain
+ * runs over w itself from its first nonzero entry (a zero adds +0.0, which changes no
+ * running sum, so the sums at the nonzero entries are those of the nonzero entries
+ * alone); the first sum above the target is at a nonzero entry, and when none is (u
+ * close to 1) the last nonzero entry is drawn. */
 __device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *red, int *sh, ChainShared &cs) {
-    const int tid = threadIdx.x;
-    const int per = (V + SP_T - 1) / SP_T;
-    const int lo = tid * per < V ? tid * per : V, hi = lo + per < V ? lo + per : V;
-    int cnt = 0;
-    range_pass(lo, hi, [&](int i) { return w[i]; }, [&](int, double x) { cnt += x > 0.0 ? 1 : 0; });
-    int nnz;
-    int o = wg_scan_excl(cnt, red, &nnz);
-    range_pass(lo, hi, [&](int i) { return w[i]; }, [&](int i, double x) {
-        if (x > 0.0) { a.cw[o] = x; a.ci[o] = i; o++; }
-    });
+    const int tid = threadIdx.x, lane = tid & 63;
+    (void)red;
+    if (tid == 0) { sh[1] = INT_MAX; sh[2] = -1; }
     __syncthreads();
+    {
+        int lo = INT_MAX, hi = -1;
+        row_pass(V, [&](int i) { return w[i]; }, [&](int i, double x) {
+            if (x > 0.0) {
+                lo = i < lo ? i : lo;
+                hi = i > hi ? i : hi;
+            }
+        });
+        for (int off = 32; off >= 1; off >>= 1) {
+            const int ol = __shfl_xor(lo, off, 64), oh = __shfl_xor(hi, off, 64);
+            lo = ol < lo ? ol : lo;
+            hi = oh > hi ? oh : hi;
+        }
+        if (lane == 0) {
+            if (lo != INT_MAX) atomicMin(&sh[1], lo);
+            if (hi >= 0) atomicMax(&sh[2], hi);
+        }
+    }
+    __syncthreads();
+    const int j_first = sh[1], j_last = sh[2];
+    if (j_last < 0) {   /* uniform: nothing to draw from */
+        __syncthreads();
+        return 0;
+    }
+    const int m = V - j_first;
     int stop;
-    const double total = chain_exact<8>([&](int j) { return a.cw[j]; }, nnz, INF, &stop,
-                                     [&](int j, double cj) { a.cc[j] = cj; }, cs);
+    const double total = chain_exact<8>([&](int j) { return w[j_first + j]; }, m, INF, &stop,
+                                        [&](int j, double cj) { a.cc[j] = cj; }, cs);
     if (tid == 0) sh[0] = INT_MAX;
     __syncthreads();
     const double target = dmul(u, total);
@@ -1060,13 +1109,13 @@ __device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *
         /* a thread's first index above the target is its smallest: the rest of its
          * indices cannot lower the minimum */
         bool found = false;
-        row_pass(nnz, [&](int j) { return a.cc[j]; }, [&](int j, double cj) {
+        row_pass(m, [&](int j) { return a.cc[j]; }, [&](int j, double cj) {
             if (!found && cj > target) { atomicMin(&sh[0], j); found = true; }
         });
     }
     __syncthreads();
     const int jb = sh[0];
-    const int r = jb < nnz ? a.ci[jb] : (nnz > 0 ? a.ci[nnz - 1] : 0);
+    const int r = jb < m ? j_first + jb : j_last;
     __syncthreads();
     return r;
 }
