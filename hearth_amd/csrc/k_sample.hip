@@ -105,6 +105,11 @@ __device__ __forceinline__ double lane_value(double x, int t) {
  * plain loops they replace. */
 constexpr int SP_U = 8;
 
+struct KeyIdx {   /* a candidate: its p's bits and its index, loaded together */
+    unsigned long long k;
+    int i;
+};
+
 template <class Load, class Body>
 __device__ __forceinline__ void row_pass(int n, Load load, Body body) {
     for (int i0 = threadIdx.x; i0 < n; i0 += SP_T * SP_U) {
@@ -448,7 +453,7 @@ __device__ double chain_exact(GetX get_x, int m, double stop_at, int *stop_j, On
             d[k] = 0;
             bad[k] = false;
             if (j < m) {
-                const double q = get_x(j) / u;   /* a power-of-two scaling: exact */
+                const double q = ldexp(get_x(j), 52 - e);   /* x / u: a power-of-two scaling, exact */
                 if (!(q < 0x1p53)) {
                     bad[k] = true;
                 } else {
@@ -616,24 +621,31 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
 
     if (a.top_p < 1.0) {
         const double top_p = a.top_p;
-        uint32_t *hcnt = (uint32_t *)smem;
-        double *hmass = (double *)(smem + HBINS * 4);
-        for (int i = tid; i < HBINS; i += SP_T) { hcnt[i] = 0; hmass[i] = 0.0; }
+        /* the approximate mass of each bin (exponent and first significand bit): the
+         * significands less their low 12 bits, summed as integers (below 2^41 each, so
+         * that SAMPLE_VMAX of them cannot wrap) in units of 2^(E - 1063) for exponent
+         * field E (2^-1062 for subnormals) */
+        unsigned long long *hsum = (unsigned long long *)smem;
+        for (int i = tid; i < HBINS; i += SP_T) hsum[i] = 0ull;
         __syncthreads();
         row_pass(V, [&](int i) { return P[i]; }, [&](int, double p) {
             if (p > 0.0) {
-                const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
-                atomicAdd(&hcnt[b], 1u);
-                atomicAdd(&hmass[b], p);
+                const unsigned long long bits = (unsigned long long)__double_as_longlong(p);
+                const unsigned long long sig = (bits & 0xFFFFFFFFFFFFFull) | ((bits >> 52) ? (1ull << 52) : 0ull);
+                atomicAdd(&hsum[bits >> 51], sig >> 12);
             }
         });
         __syncthreads();
+        auto hmass = [&](int b) {
+            const int ef = b >> 1;
+            return ldexp((double)hsum[b], (ef ? ef - 1075 : -1074) + 12);
+        };
         /* the highest bin b* whose suffix mass reaches top_p + 1e-9 (approximate sums) */
         if (tid == 0) rs.bi[2] = -1;
         __syncthreads();
         {
             const int b1 = 2 * (SP_T - 1 - tid) + 1, b0 = b1 - 1;   /* thread 0 holds the top bins */
-            const double m1 = hmass[b1], m0 = hmass[b0];
+            const double m1 = hmass(b1), m0 = hmass(b0);
             double inc = dadd(m1, m0);
             for (int off = 1; off < 64; off <<= 1) {
                 const double y = __shfl_up(inc, off, 64);
@@ -705,21 +717,23 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
  * order, and every entry is kept (each c_j < top_p): the bin adds u times the sum of the
  * integers RN(p / u). The candidates are first bucketed by bin (a counting sort), so a
  * bin's entries are contiguous. A round walks the bins down from the current one in
- * chunks of about TB_CHUNK entries: it computes the chunk's sums at the current u, adds
- * the bins above the first one that meets (b)-(d) in bulk (or the whole chunk, and goes
- * on with the next), then sorts that bin (p descending, index ascending: the stable
- * descending argsort) and runs chain_exact over it from c. Rounds continue down the bins
- * until the chain stops (c >= top_p (1 + 2^-48): the rest of the row is dropped) or
- * tier 0 runs out (c carries over to tier 1). Every p left is at most c (the top entry
- * is summed first), so p / u < 2^53; a bin's sum is kept as a high part (>> 20) and a
- * low part so that no 64-bit sum can wrap, and is saturated once it passes 2^53. */
+ * chunks of whole bins of about TB_CHUNK entries: a prefix sum of RN(p / u) over the
+ * chunk's entries in walk order finds the first bin that meets (b)-(d) (the bin of the
+ * first entry whose running units reach top_p or leave the binade, or of a tie: the
+ * units at a bin's last entry are those after the bin, whatever its order), adds the
+ * bins above it in bulk (or the whole chunk, and goes on with the next), then sorts that
+ * bin (p descending, index ascending: the stable descending argsort) and runs
+ * chain_exact over it from c. Rounds continue down the bins until the chain stops
+ * (c >= top_p (1 + 2^-48): the rest of the row is dropped) or tier 0 runs out (c carries
+ * over to tier 1). Every p left is at most c (the top entry is summed first), so
+ * p / u <= 2^53; the unsigned 64-bit prefix sums saturate at 2^60, past every test. */
 constexpr int TB_NBIN = 2048;
-constexpr int TB_CHUNK = 8 * SP_T;
+constexpr int TB_PER = 8, TB_CHUNK = TB_PER * SP_T;
 constexpr unsigned long long TB_FLAG = 1ull << 63, TB_SAT = 1ull << 60, TB_LIM = 1ull << 53;
 
 struct TopPBins {
-    unsigned long long hi[TB_NBIN], lo[TB_NBIN];
     int cnt[TB_NBIN];
+    int cursor[TB_NBIN];       /* the scatter's next free place per bin */
     int off[TB_NBIN + 1];      /* bucket starts: bin b's entries are [off[b], off[b + 1]) */
     unsigned long long wpre[SP_WAVES];
     unsigned long long dpre;   /* units before the crossing bin (or after the chunk, when none) */
@@ -765,9 +779,8 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
     }
     __syncthreads();
     {
-        /* bucket starts (bins ascending), then the scatter with a cursor per bin (the
-         * low sums, not in use yet, hold the cursors) */
-        int *cursor = (int *)tb.lo;
+        /* bucket starts (bins ascending), then the scatter with a cursor per bin */
+        int *cursor = tb.cursor;
         const int b0 = 2 * tid, c0 = b0 < nb ? tb.cnt[b0] : 0, c1 = b0 + 1 < nb ? tb.cnt[b0 + 1] : 0;
         int total;
         const int o0 = wg_scan_excl(c0 + c1, (int *)tb.wpre, &total);
@@ -775,12 +788,12 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
         if (b0 + 1 < nb) { tb.off[b0 + 1] = o0 + c0; cursor[b0 + 1] = o0 + c0; }
         if (tid == 0) tb.off[nb] = total;
         __syncthreads();
-        row_pass(m, [&](int j) { return key[j]; }, [&](int j, unsigned long long k) {
-            const int b = (int)(k >> sh) - bofs;
+        row_pass(m, [&](int j) { return KeyIdx{key[j], idx[j]}; }, [&](int, KeyIdx e) {
+            const int b = (int)(e.k >> sh) - bofs;
             if (b >= 0 && b < nb) {
                 const int pos = atomicAdd(&cursor[b], 1);
-                bkey[pos] = k;
-                bidx[pos] = idx[j];
+                bkey[pos] = e.k;
+                bidx[pos] = e.i;
             }
         });
         __syncthreads();
@@ -814,64 +827,87 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
                     tb.ib[3] = lo;
                     tb.ib[2] = -1;
                 }
-                for (int b = tid; b <= top_b; b += SP_T)
-                    if (b >= 0) { tb.hi[b] = 0ull; tb.lo[b] = 0ull; }
                 __syncthreads();
                 const int lo_b = tb.ib[3];
                 const int j0 = tb.off[lo_b], j1 = tb.off[top_b + 1];
-                row_pass(j1 - j0, [&](int j) { return bkey[j0 + j]; }, [&](int, unsigned long long k) {
-                    const int b = (int)(k >> sh) - bofs;
-                    const double q = __longlong_as_double((long long)k) / u;   /* a power-of-two scaling: exact */
-                    const double f = floor(q), r = q - f;
-                    if (r == 0.5) {
-                        atomicOr(&tb.hi[b], TB_FLAG);
-                    } else {
-                        const unsigned long long d = (unsigned long long)f + (r > 0.5 ? 1ull : 0ull);
-                        atomicAdd(&tb.hi[b], d >> 20);
-                        atomicAdd(&tb.lo[b], d & 0xFFFFFull);
-                    }
-                });
-                __syncthreads();
-                /* descending scan over the chunk: thread t holds bins top_b - 2t (first)
-                 * and top_b - 2t - 1 */
-                const int b1 = top_b - 2 * tid, b2 = b1 - 1;
-                auto sval = [&](int b, bool &flag) -> unsigned long long {
-                    flag = false;
-                    if (b < lo_b) return 0ull;
-                    const unsigned long long h = tb.hi[b];
-                    flag = (h & TB_FLAG) != 0ull;
-                    const unsigned long long hh = h & ~TB_FLAG;
-                    if (hh >= (1ull << 33)) return TB_SAT;
-                    return tb_sat_add(hh << 20, tb.lo[b]);
-                };
-                bool f1, f2;
-                const unsigned long long s1 = sval(b1, f1), s2 = sval(b2, f2), s12 = tb_sat_add(s1, s2);
-                unsigned long long inc = s12;
-                for (int off = 1; off < 64; off <<= 1) {
-                    const unsigned long long y = __shfl_up(inc, off, 64);
-                    if (lane >= off) inc = tb_sat_add(inc, y);
-                }
-                if (lane == 63) tb.wpre[w] = inc;
-                __syncthreads();
-                unsigned long long wb = 0ull;
-                for (int i = 0; i < w; i++) wb = tb_sat_add(wb, tb.wpre[i]);
-                unsigned long long excl = __shfl_up(inc, 1, 64);
-                excl = tb_sat_add(wb, lane ? excl : 0ull);
-                const unsigned long long pre1 = tb_sat_add(D, excl), aft1 = tb_sat_add(pre1, s1), aft2 = tb_sat_add(aft1, s2);
                 auto crosses = [&](unsigned long long after) {
                     return after >= TB_LIM || (double)after * u >= top_p;
                 };
-                int cand = -1;
-                if (b1 >= lo_b && (f1 || crosses(aft1))) cand = b1;
-                else if (b2 >= lo_b && (f2 || crosses(aft2))) cand = b2;
-                if (cand >= 0) atomicMax(&tb.ib[2], cand);
-                __syncthreads();
-                const int bc = tb.ib[2];
-                if (bc >= 0 && (bc == b1 || bc == b2)) tb.dpre = bc == b1 ? pre1 : aft1;
-                if (bc < 0 && tid == SP_T - 1) tb.dpre = tb_sat_add(D, tb_sat_add(wb, inc));   /* the whole chunk */
-                __syncthreads();
-                D = tb.dpre;
-                __syncthreads();
+                /* the chunk's entries in the descending order of bins: walk position q is
+                 * bucket entry j1 - 1 - q; thread t takes positions q0 + TB_PER t .. + TB_PER - 1
+                 * of each block of TB_CHUNK (a chunk of one bin can hold more). The first
+                 * position whose running units cross (or whose p is a tie) names the bin:
+                 * the running units at a bin's last position are those after the bin. */
+                const unsigned long long Dc = D;
+                int bc = -1;
+                for (int q0 = 0; q0 < j1 - j0 && bc < 0; q0 += TB_CHUNK) {
+                    unsigned long long dk[TB_PER];
+                    int bk[TB_PER];
+                    bool tk[TB_PER];
+                    unsigned long long tsum = 0ull;
+#pragma unroll
+                    for (int k = 0; k < TB_PER; k++) {
+                        const int q = q0 + TB_PER * tid + k;
+                        dk[k] = 0ull;
+                        bk[k] = -1;
+                        tk[k] = false;
+                        if (q < j1 - j0) {
+                            const unsigned long long key_q = bkey[j1 - 1 - q];
+                            const double qv = ldexp(__longlong_as_double((long long)key_q), 52 - e);   /* p / u, exact */
+                            const double f = floor(qv), r = qv - f;
+                            bk[k] = (int)(key_q >> sh) - bofs;
+                            tk[k] = r == 0.5;
+                            dk[k] = (unsigned long long)f + (r > 0.5 ? 1ull : 0ull);
+                        }
+                        tsum = tb_sat_add(tsum, dk[k]);
+                    }
+                    unsigned long long inc = tsum;
+                    for (int off = 1; off < 64; off <<= 1) {
+                        const unsigned long long y = __shfl_up(inc, off, 64);
+                        if (lane >= off) inc = tb_sat_add(inc, y);
+                    }
+                    if (lane == 63) tb.wpre[w] = inc;
+                    __syncthreads();
+                    unsigned long long excl = __shfl_up(inc, 1, 64);
+                    excl = lane ? excl : 0ull;
+                    for (int i = 0; i < w; i++) excl = tb_sat_add(excl, tb.wpre[i]);
+                    excl = tb_sat_add(D, excl);   /* units before this thread's first position */
+                    {
+                        unsigned long long run = excl;
+#pragma unroll
+                        for (int k = 0; k < TB_PER; k++) {
+                            if (bk[k] < 0) break;
+                            run = tb_sat_add(run, dk[k]);
+                            if (tk[k] || crosses(run)) {   /* bins descend along k: the first is the highest */
+                                atomicMax(&tb.ib[2], bk[k]);
+                                break;
+                            }
+                        }
+                    }
+                    __syncthreads();
+                    bc = tb.ib[2];
+                    if (bc >= 0) {
+                        /* the units before bin bc's first position */
+                        const int qs = j1 - tb.off[bc + 1] - q0;
+                        if (qs < 0) {   /* a chunk of one bin, found in a later block */
+                            if (tid == 0) tb.dpre = Dc;
+                        } else if (qs >= TB_PER * tid && qs < TB_PER * (tid + 1)) {
+                            unsigned long long run = excl;
+#pragma unroll
+                            for (int k = 0; k < TB_PER; k++)
+                                if (k < qs - TB_PER * tid) run = tb_sat_add(run, dk[k]);
+                            tb.dpre = run;
+                        }
+                    } else if (tid == SP_T - 1) {
+                        unsigned long long run = excl;
+#pragma unroll
+                        for (int k = 0; k < TB_PER; k++) run = tb_sat_add(run, dk[k]);
+                        tb.dpre = run;   /* the whole block */
+                    }
+                    __syncthreads();
+                    D = tb.dpre;
+                    __syncthreads();
+                }
                 if (bc >= 0) {
                     bx = bc;
                     break;
@@ -893,15 +929,44 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
                 sk[j] = bkey[j0 + j];
                 si[j] = bidx[j0 + j];
             }
-            for (int j = n + tid; j < N; j += SP_T) { sk[j] = 0ull; si[j] = INT_MAX; }
-            __syncthreads();
-            if (in_lds) bitonic_block(sk, si, N, 2, N, N, 0);
-            else bitonic_global(sk, si, N, (unsigned long long *)smem, (int *)(smem + SORT_LDS * 8));
+            unsigned long long *ko = sk;   /* the sorted bin */
+            int *io = si;
+            if (n <= SP_T) {
+                /* a small bin: each entry's place is the number of entries before it
+                 * (the order is total: indices differ), counted by G neighbouring lanes
+                 * over a G-th of the bin each, and written after the inputs */
+                __syncthreads();
+                int np2 = 1;
+                while (np2 < n) np2 <<= 1;
+                const int G = SP_T / np2 < 64 ? SP_T / np2 : 64;   /* a power of two */
+                const int j = tid / G, part = tid % G;
+                unsigned long long kj = 0ull;
+                int ij = 0, r = 0;
+                if (j < n) {
+                    kj = sk[j];
+                    ij = si[j];
+#pragma unroll 4
+                    for (int i = part; i < n; i += G) r += before(sk[i], si[i], kj, ij) ? 1 : 0;
+                }
+                for (int off = 1; off < G; off <<= 1) r += __shfl_xor(r, off, 64);
+                if (j < n && part == 0) {
+                    sk[SP_T + r] = kj;
+                    si[SP_T + r] = ij;
+                }
+                ko = sk + SP_T;
+                io = si + SP_T;
+                __syncthreads();
+            } else {
+                for (int j = n + tid; j < N; j += SP_T) { sk[j] = 0ull; si[j] = INT_MAX; }
+                __syncthreads();
+                if (in_lds) bitonic_block(sk, si, N, 2, N, N, 0);
+                else bitonic_global(sk, si, N, (unsigned long long *)smem, (int *)(smem + SORT_LDS * 8));
+            }
             int stop;
             const double c_in = c;
-            auto px = [&](int j) { return __longlong_as_double((long long)sk[j]); };
+            auto px = [&](int j) { return __longlong_as_double((long long)ko[j]); };
             auto drop = [&](int j, double cj) {
-                if (dsub(cj, px(j)) >= top_p) P[si[j]] = 0.0;
+                if (dsub(cj, px(j)) >= top_p) P[io[j]] = 0.0;
             };
             if (c_in == 0.0) {
                 c = chain_exact(px, n, thr_hi, &stop, drop, cs);
@@ -911,7 +976,7 @@ __device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, doubl
                 c = chain_exact(px1, n + 1, thr_hi, &stop, drop1, cs);
                 stop = stop - 1;
             }
-            for (int j = stop + 1 + tid; j < n; j += SP_T) P[si[j]] = 0.0;
+            for (int j = stop + 1 + tid; j < n; j += SP_T) P[io[j]] = 0.0;
             __syncthreads();
             if (stop < n) {
                 stopped = true;
