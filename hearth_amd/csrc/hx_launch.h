@@ -203,6 +203,8 @@ struct PwTail {
 
 constexpr int SAMPLE_VMAX = 262144;  /* vocabulary limit of sampled acceptance */
 constexpr int SAMPLE_NMAX = 4096;    /* verify nodes per call */
+constexpr int SAMPLE_WB = SAMPLE_VMAX / 8192;   /* numpy reduction buffers of a row */
+constexpr int SAMPLE_HBINS = 2048;   /* top-p histogram bins (exponent and first significand bit of p in (0, 1]) */
 
 /* Sampled acceptance of a verify tree (chain: parent[i] = i - 1). */
 struct SampleArgs {
@@ -231,6 +233,9 @@ struct SampleArgs {
     PwTail tail;                      /* pairwise tree of the row's last numpy buffer */
     const int *live;                  /* device [1] or null: rows >= *live are padding (no distribution, never walked) */
     const int *n_ctx_dev;             /* device [1] or null: the penalty context length (else n_ctx) */
+    double *wmax, *wsum;              /* [n][SAMPLE_WB] per reduction buffer of a row: max, then pairwise sum */
+    int *widx, *wflag;                /* [n][SAMPLE_WB] first argmax, flags */
+    unsigned long long *whist;        /* [n][SAMPLE_HBINS] approximate bin masses of a row */
 };
 
 /* Greedy speculative decoding loop on the device (k_loop.hip): fields of the state block. */
@@ -335,6 +340,9 @@ struct SampleScratch {
     unsigned long long *skey = nullptr, *skey2 = nullptr;
     int *sidx = nullptr, *sidx2 = nullptr, *seg_begin = nullptr, *seg_end = nullptr, *bstar = nullptr, *ci = nullptr,
         *row_rc = nullptr, *path = nullptr, *result = nullptr, *ctx = nullptr, *tok = nullptr, *par = nullptr;
+    double *wmax = nullptr, *wsum = nullptr;
+    int *widx = nullptr, *wflag = nullptr;
+    unsigned long long *whist = nullptr;
     hipError_t ensure(int n, int V, bool need_q, int n_ctx);
     void release();
     ~SampleScratch() { release(); }

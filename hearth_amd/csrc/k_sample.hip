@@ -50,7 +50,8 @@ constexpr int SP_WAVES = SP_T / 64;
 constexpr int NP_BUF = 8192;                     /* numpy's reduction buffer (elements) */
 constexpr int LV_MAX = (SAMPLE_VMAX / NP_BUF) * 64 + PW_MAXLEAF;
 constexpr int SORT_LDS = 8192;                   /* candidates sorted in LDS */
-constexpr int HBINS = 2048;                      /* p in (0, 1]: bits >> 51 < 2048 */
+constexpr int HBINS = SAMPLE_HBINS;              /* p in (0, 1]: bits >> 51 < 2048 */
+static_assert(HBINS == 2048 && SAMPLE_WB * NP_BUF == SAMPLE_VMAX, "histogram and buffer counts");
 constexpr int SMEM = SORT_LDS * 12;              /* LDS reused by the stages of a row */
 constexpr double INF = __builtin_huge_val();
 
@@ -535,6 +536,46 @@ struct RowShared {
     int bi[8];
 };
 
+/* the approximate mass of bin b from its integer sum (histogram passes: the significands
+ * less their low 12 bits, summed as integers in units of 2^(E - 1063) for exponent field
+ * E, 2^-1062 for subnormals; below 2^41 each, so that SAMPLE_VMAX of them cannot wrap) */
+__device__ __forceinline__ unsigned long long hist_units(double p) {
+    const unsigned long long bits = (unsigned long long)__double_as_longlong(p);
+    const unsigned long long sig = (bits & 0xFFFFFFFFFFFFFull) | ((bits >> 52) ? (1ull << 52) : 0ull);
+    return sig >> 12;
+}
+__device__ __forceinline__ double hist_mass(unsigned long long units, int b) {
+    const int ef = b >> 1;
+    return ldexp((double)units, (ef ? ef - 1075 : -1074) + 12);
+}
+
+/* b*: the highest histogram bin whose suffix mass reaches top_p + 1e-9 (approximate
+ * sums), -1 if none; hsum[HBINS] are the bins' integer sums */
+__device__ int select_bstar(const unsigned long long *hsum, double top_p, RowShared &rs) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (tid == 0) rs.bi[2] = -1;
+    __syncthreads();
+    const int b1 = 2 * (SP_T - 1 - tid) + 1, b0 = b1 - 1;   /* thread 0 holds the top bins */
+    const double m1 = hist_mass(hsum[b1], b1), m0 = hist_mass(hsum[b0], b0);
+    double inc = dadd(m1, m0);
+    for (int off = 1; off < 64; off <<= 1) {
+        const double y = __shfl_up(inc, off, 64);
+        if (lane >= off) inc = dadd(inc, y);
+    }
+    if (lane == 63) rs.red_d[wv] = inc;
+    __syncthreads();
+    double above = 0.0;
+    for (int i = 0; i < wv; i++) above = dadd(above, rs.red_d[i]);
+    const double excl = dadd(above, dsub(inc, dadd(m1, m0)));
+    const double s1 = dadd(excl, m1), s0 = dadd(s1, m0);
+    const double thr = top_p + 1e-9;
+    if (s0 >= thr) atomicMax(&rs.bi[2], s1 >= thr ? b1 : b0);
+    __syncthreads();
+    const int r = rs.bi[2];
+    __syncthreads();
+    return r;
+}
+
 /* the Sampler.probs pipeline on row v; returns 0 or -1 (bad logits) */
 __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
     __shared__ __align__(16) unsigned char smem[SMEM];
@@ -621,47 +662,15 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
 
     if (a.top_p < 1.0) {
         const double top_p = a.top_p;
-        /* the approximate mass of each bin (exponent and first significand bit): the
-         * significands less their low 12 bits, summed as integers (below 2^41 each, so
-         * that SAMPLE_VMAX of them cannot wrap) in units of 2^(E - 1063) for exponent
-         * field E (2^-1062 for subnormals) */
+        /* the approximate mass of each bin (exponent and first significand bit) */
         unsigned long long *hsum = (unsigned long long *)smem;
         for (int i = tid; i < HBINS; i += SP_T) hsum[i] = 0ull;
         __syncthreads();
         row_pass(V, [&](int i) { return P[i]; }, [&](int, double p) {
-            if (p > 0.0) {
-                const unsigned long long bits = (unsigned long long)__double_as_longlong(p);
-                const unsigned long long sig = (bits & 0xFFFFFFFFFFFFFull) | ((bits >> 52) ? (1ull << 52) : 0ull);
-                atomicAdd(&hsum[bits >> 51], sig >> 12);
-            }
+            if (p > 0.0) atomicAdd(&hsum[(unsigned long long)__double_as_longlong(p) >> 51], hist_units(p));
         });
         __syncthreads();
-        auto hmass = [&](int b) {
-            const int ef = b >> 1;
-            return ldexp((double)hsum[b], (ef ? ef - 1075 : -1074) + 12);
-        };
-        /* the highest bin b* whose suffix mass reaches top_p + 1e-9 (approximate sums) */
-        if (tid == 0) rs.bi[2] = -1;
-        __syncthreads();
-        {
-            const int b1 = 2 * (SP_T - 1 - tid) + 1, b0 = b1 - 1;   /* thread 0 holds the top bins */
-            const double m1 = hmass(b1), m0 = hmass(b0);
-            double inc = dadd(m1, m0);
-            for (int off = 1; off < 64; off <<= 1) {
-                const double y = __shfl_up(inc, off, 64);
-                if (lane >= off) inc = dadd(inc, y);
-            }
-            if (lane == 63) rs.red_d[wv] = inc;
-            __syncthreads();
-            double above = 0.0;
-            for (int i = 0; i < wv; i++) above = dadd(above, rs.red_d[i]);
-            const double excl = dadd(above, dsub(inc, dadd(m1, m0)));
-            const double s1 = dadd(excl, m1), s0 = dadd(s1, m0);
-            const double thr = top_p + 1e-9;
-            if (s0 >= thr) atomicMax(&rs.bi[2], s1 >= thr ? b1 : b0);
-        }
-        __syncthreads();
-        const int bstar = rs.bi[2];
+        const int bstar = select_bstar(hsum, top_p, rs);
         /* tier 0 (bins >= b*; all nonzero entries when b* < 0), gathered a wave at a time (in
          * no particular order: every use of it is by bins, and the bins it sorts are
          * sorted by (p descending, index ascending), a total order) */
@@ -701,6 +710,197 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
         row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = ddiv(x, s); });
     }
     if (tid == 0) a.row_rc[v] = 0;
+}
+
+/* ---------------------------------------------------------------- the distribution, wide */
+
+/* Sampler.probs without top-k, spread over the row: workgroup b of row v takes numpy's
+ * reduction buffer b (entries [8192 b, 8192 b + 8192)), so that a row runs on
+ * ceil(V / 8192) compute units and each buffer's pairwise sum is a workgroup's own.
+ *   k_wide_scan:  the penalty, the logits as float64, the buffer's max and first argmax;
+ *   k_wide_exp:   the row's max and first argmax from the buffers' (a total order:
+ *                 value descending, index ascending), bad rows, temperature 0,
+ *                 exp((x - max) / T), the buffer's pairwise sum;
+ *   k_wide_norm:  numpy's sum (0.0, then the buffers' sums in order), the division, the
+ *                 buffer's bin masses added into the row's histogram (integer sums);
+ *   k_wide_cand:  b* from the row's histogram, the buffer's candidates of tier 0
+ *                 appended to the row's (one global atomic per workgroup; any order).
+ * Every value is computed by the operations of k_sample_probs in the same order, so the
+ * distribution and the candidates (as a set) are the same. row_rc[v] is 1 while the row
+ * goes on, -1 for bad logits, 0 once final. */
+__device__ __forceinline__ void wide_range(int V, int &r0, int &len) {
+    r0 = blockIdx.x * NP_BUF;
+    len = V - r0 < NP_BUF ? V - r0 : NP_BUF;
+}
+
+__global__ __launch_bounds__(SP_T) void k_wide_scan(SampleArgs a) {
+    __shared__ uint32_t bits[NP_BUF / 32];
+    __shared__ RowShared rs;
+    const int v = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (a.live && v >= *a.live) return;   /* padding row (uniform) */
+    const int V = a.V;
+    int r0, len;
+    wide_range(V, r0, len);
+    const float *row = a.rows + (size_t)v * V + r0;
+    double *P = a.P + (size_t)v * V + r0;
+    if (blockIdx.x == 0 && tid == 0) {   /* no candidates unless top-p runs */
+        a.seg_begin[v] = v * a.sort_n;
+        a.seg_end[v] = v * a.sort_n;
+    }
+    for (int i = blockIdx.x * SP_T + tid; i < HBINS; i += gridDim.x * SP_T) a.whist[(size_t)v * HBINS + i] = 0ull;
+    /* Sampler._penalised: the ids of the context and of the path nodes 1..v in this buffer */
+    const bool pen = a.rp != 1.0;
+    if (pen) {
+        for (int i = tid; i < NP_BUF / 32; i += SP_T) bits[i] = 0;
+        __syncthreads();
+        const int n_ctx = a.n_ctx_dev ? *a.n_ctx_dev : a.n_ctx;
+        for (int j = tid; j < n_ctx; j += SP_T) {
+            const int t = a.ctx[j];
+            if (t >= r0 && t < r0 + len) atomicOr(&bits[(t - r0) >> 5], 1u << ((t - r0) & 31));
+        }
+        if (tid == 0)
+            for (int c = v; c > 0; c = a.parent[c]) {
+                const int t = a.tokens[c];
+                if (t >= r0 && t < r0 + len) atomicOr(&bits[(t - r0) >> 5], 1u << ((t - r0) & 31));
+            }
+        __syncthreads();
+    }
+    double best = -INF;
+    int bidx = -1, flags = 0;
+    row_pass(len, [&](int i) { return row[i]; }, [&](int i, float l) {
+        if (l != l || l == __builtin_huge_valf()) flags |= 1;
+        if (l != -__builtin_huge_valf()) flags |= 2;
+        double x = (double)l;
+        if (pen && ((bits[i >> 5] >> (i & 31)) & 1u)) x = x > 0.0 ? ddiv(x, a.rp) : dmul(x, a.rp);
+        P[i] = x;
+        if (bidx < 0 || x > best) { best = x; bidx = r0 + i; }
+    });
+    for (int off = 32; off >= 1; off >>= 1) {
+        const double ob = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(bidx, off, 64);
+        if (oi >= 0 && (bidx < 0 || ob > best || (ob == best && oi < bidx))) { best = ob; bidx = oi; }
+        flags |= __shfl_xor(flags, off, 64);
+    }
+    if (lane == 0) { rs.red_d[wv] = best; rs.red_i[wv] = bidx; rs.red_f[wv] = flags; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < SP_WAVES; i++) {
+            const double ob = rs.red_d[i];
+            const int oi = rs.red_i[i];
+            if (oi >= 0 && (bidx < 0 || ob > best || (ob == best && oi < bidx))) { best = ob; bidx = oi; }
+            flags |= rs.red_f[i];
+        }
+        const size_t o = (size_t)v * SAMPLE_WB + blockIdx.x;
+        a.wmax[o] = best;
+        a.widx[o] = bidx;
+        a.wflag[o] = flags;
+    }
+}
+
+__global__ __launch_bounds__(SP_T) void k_wide_exp(SampleArgs a) {
+    __shared__ double lv[128];
+    __shared__ double bc;
+    const int v = blockIdx.y, tid = threadIdx.x;
+    if (a.live && v >= *a.live) return;
+    const int V = a.V;
+    int r0, len;
+    wide_range(V, r0, len);
+    double *P = a.P + (size_t)v * V + r0;
+    double best = -INF;
+    int bidx = -1, flags = 0;
+    for (int b = 0; b < (int)gridDim.x; b++) {
+        const size_t o = (size_t)v * SAMPLE_WB + b;
+        const double ob = a.wmax[o];
+        const int oi = a.widx[o];
+        if (oi >= 0 && (bidx < 0 || ob > best || (ob == best && oi < bidx))) { best = ob; bidx = oi; }
+        flags |= a.wflag[o];
+    }
+    const bool lead = blockIdx.x == 0 && tid == 0;
+    if ((flags & 1) || !(flags & 2)) {
+        if (lead) a.row_rc[v] = -1;
+        return;
+    }
+    if (a.temperature == 0.0) {
+        for (int i = tid; i < len; i += SP_T) P[i] = r0 + i == bidx ? 1.0 : 0.0;
+        if (lead) a.row_rc[v] = 0;
+        return;
+    }
+    if (lead) a.row_rc[v] = 1;
+    const double mx = best, T = a.temperature;
+    row_pass(len, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = exp_port_d(ddiv(dsub(x, mx), T)); });
+    /* the buffer's pairwise sum: a full buffer, or the row's partial last one */
+    const double s = np_sum(P, len, a.tail, lv, &bc);
+    if (tid == 0) a.wsum[(size_t)v * SAMPLE_WB + blockIdx.x] = s;
+}
+
+__global__ __launch_bounds__(SP_T) void k_wide_norm(SampleArgs a) {
+    __shared__ unsigned long long hs[HBINS];
+    const int v = blockIdx.y, tid = threadIdx.x;
+    if (a.live && v >= *a.live) return;
+    if (a.row_rc[v] != 1) return;   /* final already (uniform) */
+    const int V = a.V;
+    int r0, len;
+    wide_range(V, r0, len);
+    double *P = a.P + (size_t)v * V + r0;
+    double s = 0.0;
+    for (int b = 0; b < (int)gridDim.x; b++) s = dadd(s, a.wsum[(size_t)v * SAMPLE_WB + b]);
+    const bool hist = a.top_p < 1.0;
+    if (hist) {
+        for (int i = tid; i < HBINS; i += SP_T) hs[i] = 0ull;
+        __syncthreads();
+    }
+    row_pass(len, [&](int i) { return P[i]; }, [&](int i, double x) {
+        const double p = ddiv(x, s);
+        P[i] = p;
+        if (hist && p > 0.0) atomicAdd(&hs[(unsigned long long)__double_as_longlong(p) >> 51], hist_units(p));
+    });
+    if (hist) {
+        __syncthreads();
+        unsigned long long *g = a.whist + (size_t)v * HBINS;
+        for (int b = tid; b < HBINS; b += SP_T)
+            if (hs[b]) atomicAdd(&g[b], hs[b]);
+    }
+}
+
+__global__ __launch_bounds__(SP_T) void k_wide_cand(SampleArgs a) {
+    __shared__ __align__(16) unsigned char stage[NP_BUF * 12];
+    __shared__ RowShared rs;
+    const int v = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    if (a.live && v >= *a.live) return;
+    if (a.row_rc[v] != 1) return;   /* (uniform) */
+    const int V = a.V;
+    int r0, len;
+    wide_range(V, r0, len);
+    const double *P = a.P + (size_t)v * V + r0;
+    const int bstar = select_bstar(a.whist + (size_t)v * HBINS, a.top_p, rs);
+    if (blockIdx.x == 0 && tid == 0) a.bstar[v] = bstar;
+    const int blo = bstar < 0 ? 0 : bstar;
+    /* the buffer's tier 0, gathered a wave at a time into LDS, then appended to the row's */
+    unsigned long long *lk = (unsigned long long *)stage;
+    int *li = (int *)(stage + NP_BUF * 8);
+    if (tid == 0) rs.bi[3] = 0;
+    __syncthreads();
+    row_pass_converged(len, [&](int i) { return P[i]; }, [&](int i, bool in, double p) {
+        const bool cand = in && p > 0.0 && (int)((unsigned long long)__double_as_longlong(p) >> 51) >= blo;
+        const unsigned long long bal = __ballot(cand);
+        int base = 0;
+        if (lane == 0 && bal) base = atomicAdd(&rs.bi[3], __popcll(bal));
+        base = __shfl(base, 0, 64);
+        if (cand) {
+            const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+            lk[pos] = (unsigned long long)__double_as_longlong(p);
+            li[pos] = r0 + i;
+        }
+    });
+    __syncthreads();
+    const int cnt = rs.bi[3];
+    if (tid == 0) rs.bi[4] = cnt ? atomicAdd(&a.seg_end[v], cnt) : 0;
+    __syncthreads();
+    const int at = rs.bi[4];   /* the place of the first in skey / sidx */
+    for (int j = tid; j < cnt; j += SP_T) {
+        a.skey[at + j] = lk[j];
+        a.sidx[at + j] = li[j];
+    }
 }
 
 /* ---------------------------------------------------------------- top-p over fine bins */
@@ -1008,7 +1208,10 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
     const int V = a.V;
     double *P = a.P + (size_t)v * V;
     double *lv = (double *)smem;
-    if (a.seg_end[v] == v * a.sort_n) return;   /* uniform */
+    if (a.seg_end[v] == v * a.sort_n) {   /* no top-p candidates: final (uniform) */
+        if (tid == 0 && a.row_rc[v] == 1) a.row_rc[v] = 0;
+        return;
+    }
     double s;
     if (a.top_p < 1.0) {
         const double top_p = a.top_p, thr_hi = dmul(top_p, 1.0 + 0x1p-48);
@@ -1303,10 +1506,12 @@ template <class T> hipError_t grow(T *&p, size_t count) {
 
 void SampleScratch::release() {
     void *ps[] = {P, q, u, wa, wb, cw, cc, skey, skey2, sidx, sidx2, seg_begin, seg_end, bstar, ci, row_rc, path,
-                  result, ctx, tok, par};
+                  result, ctx, tok, par, wmax, wsum, widx, wflag, whist};
     for (void *p : ps)
         if (p) (void)hipFree(p);
-    P = q = u = wa = wb = cw = cc = nullptr;
+    P = q = u = wa = wb = cw = cc = wmax = wsum = nullptr;
+    widx = wflag = nullptr;
+    whist = nullptr;
     skey = skey2 = nullptr;
     sidx = sidx2 = seg_begin = seg_end = bstar = ci = row_rc = path = result = ctx = tok = par = nullptr;
     n_cap = V = ctx_cap = sort_n = 0;
@@ -1328,7 +1533,9 @@ hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
         if ((e = grow(P, rows * V)) || (e = grow(skey, rows * sort_n)) || (e = grow(sidx, rows * sort_n)) ||
             (e = grow(skey2, rows * sort_n)) || (e = grow(sidx2, rows * sort_n)) || (e = grow(seg_begin, rows)) ||
             (e = grow(seg_end, rows)) || (e = grow(bstar, rows)) || (e = grow(u, 2 * rows)) ||
-            (e = grow(row_rc, rows)) || (e = grow(path, rows)) || (e = grow(tok, rows)) || (e = grow(par, rows)))
+            (e = grow(row_rc, rows)) || (e = grow(path, rows)) || (e = grow(tok, rows)) || (e = grow(par, rows)) ||
+            (e = grow(wmax, rows * SAMPLE_WB)) || (e = grow(wsum, rows * SAMPLE_WB)) || (e = grow(widx, rows * SAMPLE_WB)) ||
+            (e = grow(wflag, rows * SAMPLE_WB)) || (e = grow(whist, rows * SAMPLE_HBINS)))
             return e;
         if (has_q && (e = grow(q, rows * V))) return e;
         n_cap = n;
@@ -1359,6 +1566,7 @@ hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, 
     a.seg_begin = m.seg_begin; a.seg_end = m.seg_end; a.bstar = m.bstar;
     a.wa = m.wa; a.wb = m.wb; a.cw = m.cw; a.cc = m.cc; a.ci = m.ci;
     a.row_rc = m.row_rc; a.path = m.path; a.result = m.result;
+    a.wmax = m.wmax; a.wsum = m.wsum; a.widx = m.widx; a.wflag = m.wflag; a.whist = m.whist;
     build_tail(V, a.tail);
     hipError_t e = hipSuccess;
     if (q && !q_dev && (e = hipMemcpyAsync(m.q, q, sizeof(double) * (size_t)n * V, hipMemcpyHostToDevice, st)) != hipSuccess)
@@ -1369,9 +1577,19 @@ hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, 
     return hipSuccess;
 }
 
-/* Sampler.probs of n rows: the distribution and top-p candidates, then the top-p tail */
+/* Sampler.probs of n rows: the distribution and top-p candidates (a workgroup per numpy
+ * buffer of each row; one per row with top-k, or min-p without top-p), then the top-p tail */
 hipError_t probs(SampleScratch &, const SampleArgs &a, int n, hipStream_t st) {
-    k_sample_probs<<<n, SP_T, 0, st>>>(a);
+    const bool wide = !(a.top_k > 0 && a.top_k < a.V) && !(a.top_p >= 1.0 && a.min_p > 0.0);
+    if (wide) {
+        const dim3 g((a.V + NP_BUF - 1) / NP_BUF, n);
+        k_wide_scan<<<g, SP_T, 0, st>>>(a);
+        k_wide_exp<<<g, SP_T, 0, st>>>(a);
+        k_wide_norm<<<g, SP_T, 0, st>>>(a);
+        if (a.top_p < 1.0) k_wide_cand<<<g, SP_T, 0, st>>>(a);
+    } else {
+        k_sample_probs<<<n, SP_T, 0, st>>>(a);
+    }
     k_sample_top_p<<<n, SP_T, 0, st>>>(a);
     return hipGetLastError();
 }

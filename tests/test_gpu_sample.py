@@ -80,7 +80,7 @@ def _check_probs(rows, tokens, st, ctx):
         assert np.array_equal(p[v].view(np.uint64), want.view(np.uint64)), (v, V, st)
 
 
-@pytest.mark.parametrize("V", [7, 300, 4096, 8193, 20000])
+@pytest.mark.parametrize("V", [7, 300, 4096, 8193, 16384, 20000])
 def test_gpu_probs_bit_exact(V):
     rng = np.random.default_rng(V)
     for kind in ["normal1", "normal4", "ties", "neginf", "equal", "flat", "peaked", "wide"]:
