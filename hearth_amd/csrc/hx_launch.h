@@ -236,6 +236,9 @@ struct SampleArgs {
     double *wmax, *wsum;              /* [n][SAMPLE_WB] per reduction buffer of a row: max, then pairwise sum */
     int *widx, *wflag;                /* [n][SAMPLE_WB] first argmax, flags */
     unsigned long long *whist;        /* [n][SAMPLE_HBINS] approximate bin masses of a row */
+    int *bcnt, *brel;                 /* [n][SAMPLE_HBINS] top-p candidates per fine bin; places taken so far */
+    int *tcut;                        /* [n] top-p: every entry of a histogram bin below this one is dropped */
+    int tail_wide;                    /* top-p's renormalization runs a workgroup per numpy buffer */
 };
 
 /* Greedy speculative decoding loop on the device (k_loop.hip): fields of the state block. */
@@ -343,6 +346,7 @@ struct SampleScratch {
     double *wmax = nullptr, *wsum = nullptr;
     int *widx = nullptr, *wflag = nullptr;
     unsigned long long *whist = nullptr;
+    int *bcnt = nullptr, *brel = nullptr, *tcut = nullptr;
     hipError_t ensure(int n, int V, bool need_q, int n_ctx);
     void release();
     ~SampleScratch() { release(); }

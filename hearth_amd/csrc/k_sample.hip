@@ -590,6 +590,10 @@ __global__ __launch_bounds__(SP_T) void k_sample_probs(SampleArgs a) {
         a.seg_begin[v] = v * a.sort_n;
         a.seg_end[v] = v * a.sort_n;
     }
+    for (int i = tid; i < HBINS; i += SP_T) {
+        a.bcnt[(size_t)v * HBINS + i] = 0;
+        a.brel[(size_t)v * HBINS + i] = 0;
+    }
 
     /* Sampler._penalised: the ids of the context and of the path nodes 1..v */
     const bool pen = a.rp != 1.0;
@@ -747,7 +751,11 @@ __global__ __launch_bounds__(SP_T) void k_wide_scan(SampleArgs a) {
         a.seg_begin[v] = v * a.sort_n;
         a.seg_end[v] = v * a.sort_n;
     }
-    for (int i = blockIdx.x * SP_T + tid; i < HBINS; i += gridDim.x * SP_T) a.whist[(size_t)v * HBINS + i] = 0ull;
+    for (int i = blockIdx.x * SP_T + tid; i < HBINS; i += gridDim.x * SP_T) {
+        a.whist[(size_t)v * HBINS + i] = 0ull;
+        a.bcnt[(size_t)v * HBINS + i] = 0;
+        a.brel[(size_t)v * HBINS + i] = 0;
+    }
     /* Sampler._penalised: the ids of the context and of the path nodes 1..v in this buffer */
     const bool pen = a.rp != 1.0;
     if (pen) {
@@ -928,12 +936,12 @@ __global__ __launch_bounds__(SP_T) void k_wide_cand(SampleArgs a) {
  * over to tier 1). Every p left is at most c (the top entry is summed first), so
  * p / u <= 2^53; the unsigned 64-bit prefix sums saturate at 2^60, past every test. */
 constexpr int TB_NBIN = 2048;
+static_assert(TB_NBIN == HBINS, "fine bins share the histogram's arrays");
 constexpr int TB_PER = 8, TB_CHUNK = TB_PER * SP_T;
 constexpr unsigned long long TB_FLAG = 1ull << 63, TB_SAT = 1ull << 60, TB_LIM = 1ull << 53;
 
 struct TopPBins {
     int cnt[TB_NBIN];
-    int cursor[TB_NBIN];       /* the scatter's next free place per bin */
     int off[TB_NBIN + 1];      /* bucket starts: bin b's entries are [off[b], off[b + 1]) */
     unsigned long long wpre[SP_WAVES];
     unsigned long long dpre;   /* units before the crossing bin (or after the chunk, when none) */
@@ -945,57 +953,118 @@ __device__ __forceinline__ unsigned long long tb_sat_add(unsigned long long a, u
     return s > TB_SAT ? TB_SAT : s;
 }
 
-/* returns c after tier 0; stopped: the chain reached its stop (every later entry of the
- * row, below tier 0 included, is to be dropped; those of tier 0 are dropped here) */
-__device__ double top_p_binned(const SampleArgs &a, int v, int m, int blo, double top_p, double thr_hi, double *P,
-                               unsigned char *smem, TopPBins &tb, ChainShared &cs, bool &stopped) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const unsigned long long *key = a.skey + (size_t)v * a.sort_n;
-    const int *idx = a.sidx + (size_t)v * a.sort_n;
-    /* the buckets, in the second candidate arrays; the first ones are free once they are
-     * filled, and hold the sorts too large for LDS */
+/* the fine bins of tier 0 (bins >= blo of the histogram): bin = (bits >> sh) - bofs in
+ * [0, nb), nb = (2048 - blo) 2^mb <= TB_NBIN */
+__device__ __forceinline__ void fine_bins(int blo, int &mb, int &nb, int &sh, int &bofs) {
+    mb = 0;
+    while (mb < 7 && ((2048 - blo) << (mb + 1)) <= TB_NBIN) mb++;
+    nb = (2048 - blo) << mb;
+    sh = 51 - mb;
+    bofs = blo << mb;
+}
+
+/* The candidates of tier 0 bucketed by fine bin (a counting sort), a workgroup per
+ * TB_SLICE of a row's candidates: k_tp_count adds each slice's counts into the row's
+ * bcnt; k_tp_scatter takes, per bin, its places after the bin's start with one global
+ * atomic per slice and bin, and scatters the slice into skey2 / sidx2 (any order within a
+ * bin: every use of a bin sums it or sorts it). */
+constexpr int TB_SLICE = 8192;
+
+__device__ __forceinline__ bool tp_slice(const SampleArgs &a, int v, int &j0, int &j1) {
+    const int m = a.seg_end[v] - v * a.sort_n;
+    j0 = blockIdx.x * TB_SLICE;
+    j1 = m - j0 < TB_SLICE ? m : j0 + TB_SLICE;
+    return j0 < m;
+}
+
+__device__ __forceinline__ void tp_count_slice(const SampleArgs &a, int v, int j0, int j1, int nb, int sh, int bofs,
+                                               int *cnt) {
+    for (int b = threadIdx.x; b < nb; b += SP_T) cnt[b] = 0;
+    __syncthreads();
+    const unsigned long long *key = a.skey + (size_t)v * a.sort_n + j0;
+    row_pass(j1 - j0, [&](int j) { return key[j]; }, [&](int, unsigned long long k) {
+        const int b = (int)(k >> sh) - bofs;   /* in [0, nb): 0 < p <= 1 in a bin >= blo */
+        if (b >= 0 && b < nb) atomicAdd(&cnt[b], 1);
+    });
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(SP_T) void k_tp_count(SampleArgs a) {
+    __shared__ int cnt[TB_NBIN];
+    const int v = blockIdx.y;
+    if (a.live && v >= *a.live) return;   /* padding row (uniform) */
+    int j0, j1;
+    if (!tp_slice(a, v, j0, j1)) return;   /* (uniform) */
+    const int bstar = a.bstar[v], blo = bstar < 0 ? 0 : bstar;
+    int mb, nb, sh, bofs;
+    fine_bins(blo, mb, nb, sh, bofs);
+    tp_count_slice(a, v, j0, j1, nb, sh, bofs, cnt);
+    int *g = a.bcnt + (size_t)v * HBINS;
+    for (int b = threadIdx.x; b < nb; b += SP_T)
+        if (cnt[b]) atomicAdd(&g[b], cnt[b]);
+}
+
+__global__ __launch_bounds__(SP_T) void k_tp_scatter(SampleArgs a) {
+    __shared__ int cnt[TB_NBIN], cur[TB_NBIN];
+    __shared__ int red[SP_WAVES];
+    const int v = blockIdx.y, tid = threadIdx.x;
+    if (a.live && v >= *a.live) return;
+    int j0, j1;
+    if (!tp_slice(a, v, j0, j1)) return;
+    const int bstar = a.bstar[v], blo = bstar < 0 ? 0 : bstar;
+    int mb, nb, sh, bofs;
+    fine_bins(blo, mb, nb, sh, bofs);
+    {
+        /* bucket starts: the exclusive scan of the row's counts, bins ascending */
+        const int *g = a.bcnt + (size_t)v * HBINS;
+        const int b0 = 2 * tid, c0 = b0 < nb ? g[b0] : 0, c1 = b0 + 1 < nb ? g[b0 + 1] : 0;
+        int total;
+        const int o0 = wg_scan_excl(c0 + c1, red, &total);
+        if (b0 < nb) cur[b0] = o0;
+        if (b0 + 1 < nb) cur[b0 + 1] = o0 + c0;
+    }
+    tp_count_slice(a, v, j0, j1, nb, sh, bofs, cnt);
+    int *rel = a.brel + (size_t)v * HBINS;
+    for (int b = tid; b < nb; b += SP_T)
+        if (cnt[b]) cur[b] += atomicAdd(&rel[b], cnt[b]);
+    __syncthreads();
+    const unsigned long long *key = a.skey + (size_t)v * a.sort_n + j0;
+    const int *idx = a.sidx + (size_t)v * a.sort_n + j0;
     unsigned long long *bkey = a.skey2 + (size_t)v * a.sort_n;
     int *bidx = a.sidx2 + (size_t)v * a.sort_n;
-    int mb = 0;
-    while (mb < 7 && ((2048 - blo) << (mb + 1)) <= TB_NBIN) mb++;
-    const int nb = (2048 - blo) << mb, sh = 51 - mb, bofs = blo << mb;
-    for (int b = tid; b < nb; b += SP_T) tb.cnt[b] = 0;
-    if (tid == 0) tb.ib[0] = -1;
-    __syncthreads();
-    {
-        int top = -1;
-        row_pass(m, [&](int j) { return key[j]; }, [&](int, unsigned long long k) {
-            const int b = (int)(k >> sh) - bofs;   /* in [0, nb): 0 < p <= 1 in a bin >= blo */
-            if (b >= 0 && b < nb) {
-                atomicAdd(&tb.cnt[b], 1);
-                top = b > top ? b : top;
-            }
-        });
-        for (int off = 32; off >= 1; off >>= 1) {
-            const int o = __shfl_xor(top, off, 64);
-            top = o > top ? o : top;
+    row_pass(j1 - j0, [&](int j) { return KeyIdx{key[j], idx[j]}; }, [&](int, KeyIdx e) {
+        const int b = (int)(e.k >> sh) - bofs;
+        if (b >= 0 && b < nb) {
+            const int pos = atomicAdd(&cur[b], 1);
+            bkey[pos] = e.k;
+            bidx[pos] = e.i;
         }
-        if (lane == 0 && top >= 0) atomicMax(&tb.ib[0], top);
-    }
-    __syncthreads();
+    });
+}
+
+/* returns c after tier 0; stopped: the chain reached its stop (every later entry of the
+ * row, below tier 0 included, is to be dropped; those of tier 0 are dropped here) */
+__device__ double top_p_binned(const SampleArgs &a, int v, int blo, double top_p, double thr_hi, double *P,
+                               unsigned char *smem, TopPBins &tb, ChainShared &cs, bool &stopped) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    /* the buckets (k_tp_scatter), in the second candidate arrays; the first ones hold the
+     * sorts too large for LDS */
+    const unsigned long long *bkey = a.skey2 + (size_t)v * a.sort_n;
+    const int *bidx = a.sidx2 + (size_t)v * a.sort_n;
+    int mb, nb, sh, bofs;
+    fine_bins(blo, mb, nb, sh, bofs);
+    if (tid == 0) tb.ib[0] = -1;
     {
-        /* bucket starts (bins ascending), then the scatter with a cursor per bin */
-        int *cursor = tb.cursor;
-        const int b0 = 2 * tid, c0 = b0 < nb ? tb.cnt[b0] : 0, c1 = b0 + 1 < nb ? tb.cnt[b0 + 1] : 0;
+        /* the bins' counts, their starts (bins ascending) and the top bin */
+        const int *gcnt = a.bcnt + (size_t)v * HBINS;
+        const int b0 = 2 * tid, c0 = b0 < nb ? gcnt[b0] : 0, c1 = b0 + 1 < nb ? gcnt[b0 + 1] : 0;
         int total;
         const int o0 = wg_scan_excl(c0 + c1, (int *)tb.wpre, &total);
-        if (b0 < nb) { tb.off[b0] = o0; cursor[b0] = o0; }
-        if (b0 + 1 < nb) { tb.off[b0 + 1] = o0 + c0; cursor[b0 + 1] = o0 + c0; }
+        if (b0 < nb) { tb.cnt[b0] = c0; tb.off[b0] = o0; }
+        if (b0 + 1 < nb) { tb.cnt[b0 + 1] = c1; tb.off[b0 + 1] = o0 + c0; }
         if (tid == 0) tb.off[nb] = total;
-        __syncthreads();
-        row_pass(m, [&](int j) { return KeyIdx{key[j], idx[j]}; }, [&](int, KeyIdx e) {
-            const int b = (int)(e.k >> sh) - bofs;
-            if (b >= 0 && b < nb) {
-                const int pos = atomicAdd(&cursor[b], 1);
-                bkey[pos] = e.k;
-                bidx[pos] = e.i;
-            }
-        });
+        if (c1 > 0) atomicMax(&tb.ib[0], b0 + 1);
+        else if (c0 > 0) atomicMax(&tb.ib[0], b0);
         __syncthreads();
     }
     int cur = tb.ib[0];
@@ -1220,6 +1289,7 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
          * tier 1: the rest, sorted here */
         double c = 0.0;
         bool done = false;
+        int cut = 0;   /* entries of histogram bins below cut are dropped */
         for (int tier = 0; tier < 2 && !done; tier++) {
             const int blo = tier == 0 ? (bstar < 0 ? 0 : bstar) : 0;
             const int bhi = tier == 0 ? HBINS : bstar;
@@ -1231,10 +1301,11 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
                 m = a.seg_end[v] - v * a.sort_n;
                 if (m == 0) continue;
                 bool stopped;
-                c = top_p_binned(a, v, m, blo, top_p, thr_hi, P, smem, tb, cs, stopped);
+                c = top_p_binned(a, v, blo, top_p, thr_hi, P, smem, tb, cs, stopped);
                 if (stopped || c >= thr_hi) {
                     done = true;
-                    if (blo > 0)
+                    cut = blo;
+                    if (blo > 0 && !a.tail_wide)
                         row_pass(V, [&](int i) { return P[i]; }, [&](int i, double p) {
                             const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
                             if (p > 0.0 && b < blo) P[i] = 0.0;
@@ -1313,6 +1384,10 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
             }
             __syncthreads();
         }
+        if (a.tail_wide) {   /* the cut and the renormalization: k_wide_tsum, k_wide_tdiv */
+            if (tid == 0) a.tcut[v] = cut;
+            return;
+        }
         s = np_sum(P, V, a.tail, lv, rs.bd);
         row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = ddiv(x, s); });
     }
@@ -1327,6 +1402,43 @@ __global__ __launch_bounds__(SP_T) void k_sample_top_p(SampleArgs a) {
         row_pass(V, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = ddiv(x, s); });
     }
     if (tid == 0) a.row_rc[v] = 0;
+}
+
+/* top-p's renormalization spread like the distribution (rows whose top-p ran, without
+ * min-p): k_wide_tsum drops the entries of histogram bins below the row's cut and takes
+ * each buffer's pairwise sum, k_wide_tdiv divides by numpy's sum of the row */
+__global__ __launch_bounds__(SP_T) void k_wide_tsum(SampleArgs a) {
+    __shared__ double lv[128];
+    __shared__ double bc;
+    const int v = blockIdx.y, tid = threadIdx.x;
+    if (a.live && v >= *a.live) return;
+    if (a.seg_end[v] == v * a.sort_n) return;   /* no top-p candidates (uniform) */
+    const int V = a.V;
+    int r0, len;
+    wide_range(V, r0, len);
+    double *P = a.P + (size_t)v * V + r0;
+    const int cut = a.tcut[v];
+    if (cut > 0)
+        row_pass(len, [&](int i) { return P[i]; }, [&](int i, double p) {
+            const int b = (int)((unsigned long long)__double_as_longlong(p) >> 51);
+            if (p > 0.0 && b < cut) P[i] = 0.0;
+        });
+    const double s = np_sum(P, len, a.tail, lv, &bc);
+    if (tid == 0) a.wsum[(size_t)v * SAMPLE_WB + blockIdx.x] = s;
+}
+
+__global__ __launch_bounds__(SP_T) void k_wide_tdiv(SampleArgs a) {
+    const int v = blockIdx.y;
+    if (a.live && v >= *a.live) return;
+    if (a.seg_end[v] == v * a.sort_n) return;
+    const int V = a.V;
+    int r0, len;
+    wide_range(V, r0, len);
+    double *P = a.P + (size_t)v * V + r0;
+    double s = 0.0;
+    for (int b = 0; b < (int)gridDim.x; b++) s = dadd(s, a.wsum[(size_t)v * SAMPLE_WB + b]);
+    row_pass(len, [&](int i) { return P[i]; }, [&](int i, double x) { P[i] = ddiv(x, s); });
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.row_rc[v] = 0;
 }
 
 /* ---------------------------------------------------------------- the walk */
@@ -1506,11 +1618,11 @@ template <class T> hipError_t grow(T *&p, size_t count) {
 
 void SampleScratch::release() {
     void *ps[] = {P, q, u, wa, wb, cw, cc, skey, skey2, sidx, sidx2, seg_begin, seg_end, bstar, ci, row_rc, path,
-                  result, ctx, tok, par, wmax, wsum, widx, wflag, whist};
+                  result, ctx, tok, par, wmax, wsum, widx, wflag, whist, bcnt, brel, tcut};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     P = q = u = wa = wb = cw = cc = wmax = wsum = nullptr;
-    widx = wflag = nullptr;
+    widx = wflag = bcnt = brel = tcut = nullptr;
     whist = nullptr;
     skey = skey2 = nullptr;
     sidx = sidx2 = seg_begin = seg_end = bstar = ci = row_rc = path = result = ctx = tok = par = nullptr;
@@ -1535,7 +1647,8 @@ hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
             (e = grow(seg_end, rows)) || (e = grow(bstar, rows)) || (e = grow(u, 2 * rows)) ||
             (e = grow(row_rc, rows)) || (e = grow(path, rows)) || (e = grow(tok, rows)) || (e = grow(par, rows)) ||
             (e = grow(wmax, rows * SAMPLE_WB)) || (e = grow(wsum, rows * SAMPLE_WB)) || (e = grow(widx, rows * SAMPLE_WB)) ||
-            (e = grow(wflag, rows * SAMPLE_WB)) || (e = grow(whist, rows * SAMPLE_HBINS)))
+            (e = grow(wflag, rows * SAMPLE_WB)) || (e = grow(whist, rows * SAMPLE_HBINS)) ||
+            (e = grow(bcnt, rows * SAMPLE_HBINS)) || (e = grow(brel, rows * SAMPLE_HBINS)) || (e = grow(tcut, rows)))
             return e;
         if (has_q && (e = grow(q, rows * V))) return e;
         n_cap = n;
@@ -1567,6 +1680,7 @@ hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, 
     a.wa = m.wa; a.wb = m.wb; a.cw = m.cw; a.cc = m.cc; a.ci = m.ci;
     a.row_rc = m.row_rc; a.path = m.path; a.result = m.result;
     a.wmax = m.wmax; a.wsum = m.wsum; a.widx = m.widx; a.wflag = m.wflag; a.whist = m.whist;
+    a.bcnt = m.bcnt; a.brel = m.brel; a.tcut = m.tcut;
     build_tail(V, a.tail);
     hipError_t e = hipSuccess;
     if (q && !q_dev && (e = hipMemcpyAsync(m.q, q, sizeof(double) * (size_t)n * V, hipMemcpyHostToDevice, st)) != hipSuccess)
@@ -1579,10 +1693,12 @@ hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, 
 
 /* Sampler.probs of n rows: the distribution and top-p candidates (a workgroup per numpy
  * buffer of each row; one per row with top-k, or min-p without top-p), then the top-p tail */
-hipError_t probs(SampleScratch &, const SampleArgs &a, int n, hipStream_t st) {
+hipError_t probs(SampleScratch &, const SampleArgs &a0, int n, hipStream_t st) {
+    SampleArgs a = a0;
     const bool wide = !(a.top_k > 0 && a.top_k < a.V) && !(a.top_p >= 1.0 && a.min_p > 0.0);
+    a.tail_wide = wide && a.top_p < 1.0 && a.min_p == 0.0;
+    const dim3 g((a.V + NP_BUF - 1) / NP_BUF, n), gs((a.V + TB_SLICE - 1) / TB_SLICE, n);
     if (wide) {
-        const dim3 g((a.V + NP_BUF - 1) / NP_BUF, n);
         k_wide_scan<<<g, SP_T, 0, st>>>(a);
         k_wide_exp<<<g, SP_T, 0, st>>>(a);
         k_wide_norm<<<g, SP_T, 0, st>>>(a);
@@ -1590,7 +1706,15 @@ hipError_t probs(SampleScratch &, const SampleArgs &a, int n, hipStream_t st) {
     } else {
         k_sample_probs<<<n, SP_T, 0, st>>>(a);
     }
+    if (a.top_p < 1.0) {
+        k_tp_count<<<gs, SP_T, 0, st>>>(a);
+        k_tp_scatter<<<gs, SP_T, 0, st>>>(a);
+    }
     k_sample_top_p<<<n, SP_T, 0, st>>>(a);
+    if (a.tail_wide) {
+        k_wide_tsum<<<g, SP_T, 0, st>>>(a);
+        k_wide_tdiv<<<g, SP_T, 0, st>>>(a);
+    }
     return hipGetLastError();
 }
 
