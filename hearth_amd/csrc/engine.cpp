@@ -179,6 +179,7 @@ struct hearth_engine {
     /* attention order of the GQA layers: 0 the reference's canonical order (default), 1
      * chunked (where the shape allows it, attn_chunk_ok); MLA layers are canonical */
     int attn_mode = 0;
+    int read_ahead = 0;      /* extra workgroups of the value kernel that read the next weights ahead */
     bool attn_chunk_ok = false;
     float *apo = nullptr, *apm = nullptr, *apl = nullptr;   /* chunked partials (alias S) */
     int anc_ld = 0;                                         /* chunks per partial row */
@@ -925,6 +926,25 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos = d_pos; at.g.nr_max = nr_max(T); at.g.chain = geom_chain;
             at.g.live = route_live;
             at.qo = aatt; at.qo_on = w.o.quant && hd % 64 == 0;
+            if (read_ahead > 0) {
+                /* the value kernel reads ahead this layer's output projection and router and
+                 * the next layer's QKV weights */
+                int r = 0;
+                auto add = [&](const DMat &m) {
+                    if (!m.quant || r + 2 > hxd::AF_NR) return;
+                    at.pf_p[r] = m.q.w;
+                    at.pf_n[r++] = (size_t)(m.q.rows_pad / 16) * m.q.nbp * 1024 / (m.q.dtype == HEARTH_Q4 ? 2 : 1);
+                    at.pf_p[r] = (const uint8_t *)m.q.d;
+                    at.pf_n[r++] = sizeof(uint16_t) * (size_t)m.q.nbp * m.q.rows_pad;
+                };
+                add(w.o);
+                if (w.moe && w.router) {
+                    at.pf_p[r] = (const uint8_t *)w.router;
+                    at.pf_n[r++] = sizeof(float) * (size_t)E * D;
+                }
+                if (l + 1 < L) { add(layers[l + 1].q); add(layers[l + 1].k); add(layers[l + 1].v); }
+                at.pf_wgs = read_ahead;
+            }
             if (attn_mode == 1) {
                 at.po = apo; at.pm = apm; at.pl = apl; at.nc_ld = anc_ld;
                 hxl::attention_chunked(at, st);
@@ -1547,6 +1567,7 @@ HEARTH_API hearth_engine *hearth_open(const hearth_options *in, char *err, size_
     if (!e->open_model(err, errlen)) return nullptr;
     const char *am = getenv("HEARTH_GPU_ATTN");
     e->attn_mode = e->attn_chunk_ok && am && strcmp(am, "chunked") == 0 ? 1 : 0;
+    e->read_ahead = std::max(0, std::min(256, env_int("HEARTH_GPU_READ_AHEAD", 64)));
     log_msg(LOG_INFO, "%s: %s, %d layers (%d MoE), d_model %d, vocab %d, KV %d positions, device %d", o.model_path,
             e->c.arch.c_str(), e->L, e->c.n_moe, e->D, e->V, e->cap, e->dev);
     return e.release();

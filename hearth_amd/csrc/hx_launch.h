@@ -94,6 +94,8 @@ struct TokGeom {
     const int *live;
 };
 
+constexpr int AF_NR = 10;     /* read-ahead ranges of the value kernel */
+
 struct AttnArgs {
     const float *q;           /* [T][H][hd] after qk-norm and RoPE */
     const float *kc, *vc;     /* layer caches [Hkv][cap][hd] */
@@ -108,6 +110,9 @@ struct AttnArgs {
     int qo_hm;                /* 1: qo rows are (head, token) = h * T + t with hd / 64 blocks each */
     float *po, *pm, *pl;      /* chunked attention partials: [T * H][nc_ld][hd], [T * H][nc_ld] twice */
     int nc_ld;                /* chunks per partial row: at least ceil(nr_max / 64) */
+    const uint8_t *pf_p[AF_NR];   /* k_attn_values: byte ranges its pf_wgs extra workgroups read */
+    unsigned long long pf_n[AF_NR];
+    int pf_wgs;
 };
 
 struct QkvArgs {
@@ -225,8 +230,7 @@ struct SampleArgs {
     int *seg_begin, *seg_end;         /* [n] row v's candidates: [seg_begin, seg_end) = v * sort_n + [0, m) */
     int *bstar;                       /* [n] first histogram bin of tier 0 (-1: every nonzero entry) */
     int sort_n;                       /* power of two >= V */
-    double *wa, *wb, *cw, *cc;        /* [V] residuals and draw scratch */
-    int *ci;                          /* [V] */
+    double *wa, *wb, *cc;             /* [V] residuals; the draw's running sums */
     int *row_rc;                      /* [n] 0 ok, -1 bad logits */
     int *path;                        /* [n] accepted nodes from the root */
     int *result;                      /* [0] path length, [1] final token, [2] status */
@@ -339,9 +343,9 @@ struct SamplerSpec {
 struct SampleScratch {
     int n_cap = 0, V = 0, ctx_cap = 0, sort_n = 0;
     bool has_q = false;
-    double *P = nullptr, *q = nullptr, *u = nullptr, *wa = nullptr, *wb = nullptr, *cw = nullptr, *cc = nullptr;
+    double *P = nullptr, *q = nullptr, *u = nullptr, *wa = nullptr, *wb = nullptr, *cc = nullptr;
     unsigned long long *skey = nullptr, *skey2 = nullptr;
-    int *sidx = nullptr, *sidx2 = nullptr, *seg_begin = nullptr, *seg_end = nullptr, *bstar = nullptr, *ci = nullptr,
+    int *sidx = nullptr, *sidx2 = nullptr, *seg_begin = nullptr, *seg_end = nullptr, *bstar = nullptr,
         *row_rc = nullptr, *path = nullptr, *result = nullptr, *ctx = nullptr, *tok = nullptr, *par = nullptr;
     double *wmax = nullptr, *wsum = nullptr;
     int *widx = nullptr, *wflag = nullptr;

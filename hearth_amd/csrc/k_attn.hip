@@ -484,12 +484,36 @@ __device__ __forceinline__ void tv_sum16(float &acc, float P, const float4 (&V)[
     acc = fadd(acc, q12); acc = fadd(acc, q13); acc = fadd(acc, q14); acc = fadd(acc, q15);
 }
 
+/* The extra workgroups of k_attn_values: one byte of every 128-byte line of the ranges
+ * pf_p[r][0, pf_n[r]) is read (the weights of the products after the attention, so that
+ * they find them in the memory-side cache instead of HBM). The value kernel is a chain of
+ * latencies on a part of the compute units; these reads run beside it on the others. The
+ * empty asm keeps each load. */
+__device__ void values_read_ahead(const AttnArgs &a, int wg) {
+    const size_t stride = (size_t)a.pf_wgs * TV_THREADS * 128;
+    const size_t first = ((size_t)wg * TV_THREADS + threadIdx.x) * 128;
+    for (int r = 0; r < AF_NR; r++) {
+        const uint8_t *p = a.pf_p[r];
+        if (!p) continue;
+        const size_t n = a.pf_n[r];
+        for (size_t o = first; o < n; o += stride) {
+            const unsigned x = p[o];
+            asm volatile("" ::"v"(x));
+        }
+    }
+}
+
 __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float vt[2][(TV_ROWS / 4) * TV_BQ];
     __shared__ __attribute__((aligned(16))) float pt[TV_PS][4][TV_ROWS];
     __shared__ int anc_s[MAX_ANC];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
     const int nd = (hd + 63) / 64, qpt = (grp + TV_SUM - 1) / TV_SUM;
+    const int nmain = a.T * qpt * Hkv * nd;
+    if ((int)blockIdx.x >= nmain) {   /* a read-ahead workgroup (uniform) */
+        values_read_ahead(a, blockIdx.x - nmain);
+        return;
+    }
     int b = blockIdx.x;
     const int dc = b % nd;
     b /= nd;
@@ -1170,7 +1194,7 @@ void attention_finish(const AttnArgs &a, hipStream_t st) {
     if (wide && grp >= 8) HX_TV(4, 4, 2, 64)
 #undef HX_TV
     const int qpt = (grp + TV_SUM - 1) / TV_SUM;
-    k_attn_values<<<a.T * qpt * a.Hkv * nd, TV_THREADS, 0, st>>>(a);
+    k_attn_values<<<a.T * qpt * a.Hkv * nd + a.pf_wgs, TV_THREADS, 0, st>>>(a);
 }
 
 /* the items of a block (grp / rw per token) must fit the block's waves: k_attn_chunk

@@ -30,10 +30,16 @@
  * (bitonic, in LDS up to 8192 entries, else in the row's global scratch) and the chain
  * continues -- the result never depends on the histogram.
  *
- * k_sample_probs:  one workgroup per verify row; the distribution up to top-p, then
- *                  the row's top-p candidates (tier 0);
+ * k_wide_scan, k_wide_exp, k_wide_norm, k_wide_cand: a workgroup per numpy reduction
+ *                  buffer (8192 entries) of each verify row; the distribution up to top-p,
+ *                  then the row's top-p candidates (tier 0);
+ * k_sample_probs:  the same with one workgroup per row, for top-k (an exact k-th value
+ *                  over the row) and for min-p without top-p;
+ * k_tp_count, k_tp_scatter: a workgroup per 8192 candidates; tier 0 bucketed by fine bin;
  * k_sample_top_p:  one workgroup per row; the cumulative-sum chain over tier 0 by fine
- *                  bins, the rest of the row if needed, renormalization, min-p;
+ *                  bins, the rest of the row if needed (and, with min-p, the
+ *                  renormalization and min-p);
+ * k_wide_tsum, k_wide_tdiv: a workgroup per buffer; top-p's cut and renormalization;
  * k_sample_walk:   one workgroup walks the tree from the root with the uniforms.
  */
 #include <climits>
@@ -1617,15 +1623,15 @@ template <class T> hipError_t grow(T *&p, size_t count) {
 } // namespace
 
 void SampleScratch::release() {
-    void *ps[] = {P, q, u, wa, wb, cw, cc, skey, skey2, sidx, sidx2, seg_begin, seg_end, bstar, ci, row_rc, path,
+    void *ps[] = {P, q, u, wa, wb, cc, skey, skey2, sidx, sidx2, seg_begin, seg_end, bstar, row_rc, path,
                   result, ctx, tok, par, wmax, wsum, widx, wflag, whist, bcnt, brel, tcut};
     for (void *p : ps)
         if (p) (void)hipFree(p);
-    P = q = u = wa = wb = cw = cc = wmax = wsum = nullptr;
+    P = q = u = wa = wb = cc = wmax = wsum = nullptr;
     widx = wflag = bcnt = brel = tcut = nullptr;
     whist = nullptr;
     skey = skey2 = nullptr;
-    sidx = sidx2 = seg_begin = seg_end = bstar = ci = row_rc = path = result = ctx = tok = par = nullptr;
+    sidx = sidx2 = seg_begin = seg_end = bstar = row_rc = path = result = ctx = tok = par = nullptr;
     n_cap = V = ctx_cap = sort_n = 0;
     has_q = false;
 }
@@ -1636,7 +1642,7 @@ hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
         release();
         V = V_;
         sort_n = sort_len(V);
-        if ((e = grow(wa, V)) || (e = grow(wb, V)) || (e = grow(cw, V)) || (e = grow(cc, V)) || (e = grow(ci, V)) ||
+        if ((e = grow(wa, V)) || (e = grow(wb, V)) || (e = grow(cc, V)) ||
             (e = grow(result, 4)))
             return e;
     }
@@ -1677,7 +1683,7 @@ hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, 
     a.u = m.u;
     a.P = m.P; a.skey = m.skey; a.sidx = m.sidx; a.skey2 = m.skey2; a.sidx2 = m.sidx2; a.sort_n = m.sort_n;
     a.seg_begin = m.seg_begin; a.seg_end = m.seg_end; a.bstar = m.bstar;
-    a.wa = m.wa; a.wb = m.wb; a.cw = m.cw; a.cc = m.cc; a.ci = m.ci;
+    a.wa = m.wa; a.wb = m.wb; a.cc = m.cc;
     a.row_rc = m.row_rc; a.path = m.path; a.result = m.result;
     a.wmax = m.wmax; a.wsum = m.wsum; a.widx = m.widx; a.wflag = m.wflag; a.whist = m.whist;
     a.bcnt = m.bcnt; a.brel = m.brel; a.tcut = m.tcut;
