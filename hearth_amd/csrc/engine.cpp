@@ -933,9 +933,9 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 auto add = [&](const DMat &m) {
                     if (!m.quant || r + 2 > hxd::AF_NR) return;
                     at.pf_p[r] = m.q.w;
-                    at.pf_n[r++] = (size_t)(m.q.rows_pad / 16) * m.q.nbp * 1024 / (m.q.dtype == HEARTH_Q4 ? 2 : 1);
+                    at.pf_n[r++] = hxd::qmat_w_bytes(m.q);
                     at.pf_p[r] = (const uint8_t *)m.q.d;
-                    at.pf_n[r++] = sizeof(uint16_t) * (size_t)m.q.nbp * m.q.rows_pad;
+                    at.pf_n[r++] = hxd::qmat_d_bytes(m.q);
                 };
                 add(w.o);
                 if (w.moe && w.router) {

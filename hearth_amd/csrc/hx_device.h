@@ -52,6 +52,33 @@ struct Act {
     int nbp;
 };
 
+/* ---- read-ahead (device) ---- */
+
+/* One byte of every 128-byte line of p[0, n) that falls to this thread: lines
+ * part * blockDim.x + threadIdx.x + k * nparts * blockDim.x. Extra workgroups of a
+ * latency-bound kernel use it to bring the weights of a later product into the
+ * memory-side cache; the empty asm keeps each load, four of them in flight at once. */
+__device__ __forceinline__ void read_lines_ahead(const uint8_t *p, size_t n, int part, int nparts) {
+    const size_t step = (size_t)nparts * blockDim.x * 128;
+    size_t o = ((size_t)part * blockDim.x + threadIdx.x) * 128;
+    for (; o + 3 * step < n; o += 4 * step) {
+        const unsigned x0 = p[o], x1 = p[o + step], x2 = p[o + 2 * step], x3 = p[o + 3 * step];
+        asm volatile("" ::"v"(x0), "v"(x1), "v"(x2), "v"(x3));
+    }
+    for (; o < n; o += step) {
+        const unsigned x = p[o];
+        asm volatile("" ::"v"(x));
+    }
+}
+
+/* bytes of a tile-repacked matrix: its weights and its scale rows */
+__device__ __host__ __forceinline__ size_t qmat_w_bytes(const QMat &m) {
+    return (size_t)(m.rows_pad / 16) * m.nbp * 1024 / (m.dtype == 4 ? 2 : 1);
+}
+__device__ __host__ __forceinline__ size_t qmat_d_bytes(const QMat &m) {
+    return sizeof(uint16_t) * (size_t)m.nbp * m.rows_pad;
+}
+
 /* ---- canonical scalar helpers (device) ---- */
 
 __device__ __forceinline__ float fadd(float a, float b) { return __fadd_rn(a, b); }

@@ -484,23 +484,13 @@ __device__ __forceinline__ void tv_sum16(float &acc, float P, const float4 (&V)[
     acc = fadd(acc, q12); acc = fadd(acc, q13); acc = fadd(acc, q14); acc = fadd(acc, q15);
 }
 
-/* The extra workgroups of k_attn_values: one byte of every 128-byte line of the ranges
- * pf_p[r][0, pf_n[r]) is read (the weights of the products after the attention, so that
- * they find them in the memory-side cache instead of HBM). The value kernel is a chain of
- * latencies on a part of the compute units; these reads run beside it on the others. The
- * empty asm keeps each load. */
+/* The extra workgroups of k_attn_values read the ranges pf_p[r][0, pf_n[r]) (the weights
+ * of the products after the attention, so that those find them in the memory-side cache
+ * instead of HBM). The value kernel is a chain of latencies on a part of the compute
+ * units; these reads run beside it on the others. */
 __device__ void values_read_ahead(const AttnArgs &a, int wg) {
-    const size_t stride = (size_t)a.pf_wgs * TV_THREADS * 128;
-    const size_t first = ((size_t)wg * TV_THREADS + threadIdx.x) * 128;
-    for (int r = 0; r < AF_NR; r++) {
-        const uint8_t *p = a.pf_p[r];
-        if (!p) continue;
-        const size_t n = a.pf_n[r];
-        for (size_t o = first; o < n; o += stride) {
-            const unsigned x = p[o];
-            asm volatile("" ::"v"(x));
-        }
-    }
+    for (int r = 0; r < AF_NR; r++)
+        if (a.pf_p[r]) read_lines_ahead(a.pf_p[r], a.pf_n[r], wg, a.pf_wgs);
 }
 
 __global__ __launch_bounds__(TV_THREADS) void k_attn_values(AttnArgs a) {
