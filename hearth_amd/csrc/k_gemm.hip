@@ -78,7 +78,47 @@ __device__ __forceinline__ void unpack_q4(v4i raw, v4i &a0, v4i &a1) {
 /* Folds blocks [0, nb) of row tile rt of m against NT*16 tokens starting at token
  * index t0 (token t's activation row is row_of(t); tokens >= n read row_of(n - 1) and
  * their results are discarded). acc[tt][i] holds (row rt*16 + 4*(lane/16) + i,
- * token t0 + tt*16 + lane%16). */
+ * token t0 + tt*16 + lane%16).
+ *
+ * A wave walks K one block pair at a time; the loads of pair gp + 1 (weights, scales,
+ * the tokens' activation blocks and their scales) are issued before pair gp is folded,
+ * so each pair's loads wait behind the previous pair's MFMAs and folds instead of
+ * stalling the wave. */
+template <int NT>
+struct FoldStage {
+    v4i w0, w1;          /* Q8: the two blocks; Q4: w0 the packed pair */
+    uint2 s0, s1;        /* the blocks' f16 scales of this lane's 4 rows */
+    v4i b[2][NT];        /* activation blocks (16 bytes of each token's block) */
+    float dx[2][NT];
+    int sx[2][NT];       /* Q4: the activation block sums */
+};
+
+template <int NT>
+__device__ __forceinline__ void fold_load(FoldStage<NT> &f, const QMat &m, int rt, const Act &a, int gp,
+                                          const int (&arow)[NT], const uint16_t *dcol) {
+    const int lane = threadIdx.x & 63, kg = lane >> 4, npair = m.nbp >> 1;
+    if (m.dtype == 4) {
+        f.w0 = load16(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
+    } else {
+        const uint8_t *base = m.w + ((size_t)rt * m.nbp + 2 * gp) * 1024 + lane * 16;
+        f.w0 = load16(base);
+        f.w1 = load16(base + 1024);
+    }
+    f.s0 = *(const uint2 *)(dcol + (size_t)(2 * gp) * m.rows_pad);
+    f.s1 = *(const uint2 *)(dcol + (size_t)(2 * gp + 1) * m.rows_pad);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int g = 2 * gp + j < m.nb ? 2 * gp + j : m.nb - 1;   /* a pad block is never folded */
+#pragma unroll
+        for (int tt = 0; tt < NT; tt++) {
+            const size_t ab = (size_t)arow[tt] * a.nbp + g;
+            f.b[j][tt] = load16((const uint8_t *)(a.q + ab * 64 + kg * 16));
+            f.dx[j][tt] = a.d[ab];
+            if (m.dtype == 4) f.sx[j][tt] = a.s[ab];
+        }
+    }
+}
+
 template <int NT, typename RowOf>
 __device__ __forceinline__ void fold_tile(const QMat &m, int rt, const Act &a, int t0, int n, RowOf row_of,
                                           float (&acc)[NT][4]) {
@@ -95,23 +135,17 @@ __device__ __forceinline__ void fold_tile(const QMat &m, int rt, const Act &a, i
     const v4i zero = {0, 0, 0, 0};
     const int npair = m.nbp >> 1;
     const uint16_t *dcol = m.d + rt * 16 + 4 * kg;
+    FoldStage<NT> cur, nxt;
+    fold_load<NT>(cur, m, rt, a, 0, arow, dcol);
     for (int gp = 0; gp < npair; gp++) {
-        v4i w0, w1;
-        if (m.dtype == 4) {
-            const v4i raw = load16(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
-            unpack_q4(raw, w0, w1);
-        } else {
-            const uint8_t *base = m.w + ((size_t)rt * m.nbp + 2 * gp) * 1024 + lane * 16;
-            w0 = load16(base);
-            w1 = load16(base + 1024);
-        }
-        const uint2 s0 = *(const uint2 *)(dcol + (size_t)(2 * gp) * m.rows_pad);
-        const uint2 s1 = *(const uint2 *)(dcol + (size_t)(2 * gp + 1) * m.rows_pad);
+        if (gp + 1 < npair) fold_load<NT>(nxt, m, rt, a, gp + 1, arow, dcol);
+        v4i w0 = cur.w0, w1 = cur.w1;
+        if (m.dtype == 4) unpack_q4(cur.w0, w0, w1);
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int g = 2 * gp + j;
             if (g >= m.nb) break;
-            const uint2 sw = j ? s1 : s0;
+            const uint2 sw = j ? cur.s1 : cur.s0;
             float dw[4];
             dw[0] = h2f((uint16_t)(sw.x & 0xffff));
             dw[1] = h2f((uint16_t)(sw.x >> 16));
@@ -120,12 +154,10 @@ __device__ __forceinline__ void fold_tile(const QMat &m, int rt, const Act &a, i
             const v4i wa = j ? w1 : w0;
 #pragma unroll
             for (int tt = 0; tt < NT; tt++) {
-                const size_t ab = (size_t)arow[tt] * a.nbp + g;
-                const v4i b = load16((const uint8_t *)(a.q + ab * 64 + kg * 16));
-                v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, b, zero, 0, 0, 0);
-                const float dx = a.d[ab];
+                v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, cur.b[j][tt], zero, 0, 0, 0);
+                const float dx = cur.dx[j][tt];
                 if (m.dtype == 4) {
-                    const int off = 8 * a.s[ab];   /* sum(nib * q) - 8 sum(q) = sum((nib - 8) q) */
+                    const int off = 8 * cur.sx[j][tt];   /* sum(nib * q) - 8 sum(q) = sum((nib - 8) q) */
                     c.x -= off; c.y -= off; c.z -= off; c.w -= off;
                 }
                 acc[tt][0] = fadd(acc[tt][0], fmul((float)c.x, fmul(dw[0], dx)));
@@ -134,6 +166,7 @@ __device__ __forceinline__ void fold_tile(const QMat &m, int rt, const Act &a, i
                 acc[tt][3] = fadd(acc[tt][3], fmul((float)c.w, fmul(dw[3], dx)));
             }
         }
+        cur = nxt;
     }
 }
 
@@ -327,6 +360,124 @@ __global__ __launch_bounds__(512) void k_gemm_sk(GemmArgs args, int ntok) {
             const int c = f >> 4, row = rt * 16 + (f & 15), t = t0 + c;
             const float acc = fold_terms(P, sg.m.nb, ntok, f);
             if (t < args.T && row < sg.m.rows) {
+                float y = canon(acc);
+                if (sg.scale_on) y = canon(fmul(sg.scale, y));
+                sg.Y[(size_t)t * sg.ldy + row] = y;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+/* Dense product of more tokens than one tile (a tree's, a prefill chunk's) with each
+ * weight byte read once: one workgroup per 16-row tile of a segment, as k_gemm_sk; each
+ * wave keeps the weights and scales of its block pairs (at most SK_MAXP) in registers
+ * and runs every token tile through them: the MFMAs, the terms into LDS, the next
+ * tile's activation loads (in flight during the barrier and the fold), one thread per
+ * (row, token) folding the terms in block order. The same terms and fold as k_gemm_sk,
+ * so the same bits as every other product kernel. */
+template <int DT>
+__global__ __launch_bounds__(512) void k_gemm_skm(GemmArgs args, int ntok, int nwg, int nsplit) {
+    extern __shared__ float P[];
+    /* workgroup b takes row tile b % nwg and token tiles b / nwg, b / nwg + nsplit, ... */
+    const int bid = (int)blockIdx.x % nwg, split = (int)blockIdx.x / nwg;
+    int s = 0;
+    while (s + 1 < args.nseg && bid >= args.seg[s + 1].wg0) s++;
+    const GemmSeg &sg = args.seg[s];
+    const QMat &m = sg.m;
+    const int rt = bid - sg.wg0;
+    const int tfirst = args.t0 + split * ntok, tstep = nsplit * ntok;
+    const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    const int lane = tid & 63, kg = lane >> 4, lr = lane & 15;
+    const int npair = m.nbp >> 1, nb = m.nb;
+    int p0, p1;
+    wave_pairs(npair, W, wave, p0, p1);
+    const bool has = p0 < p1;   /* uniform per wave */
+    v4i raw[SK_MAXP][DT == 4 ? 1 : 2];
+    uint2 sc[SK_MAXP][2];
+    v4i xq[SK_MAXP][2];
+    float dx[SK_MAXP][2];
+    int sx[SK_MAXP][2];
+    auto load_x = [&](int t0) {
+        int t = t0 + lr;
+        t = t < args.T ? t : args.T - 1;
+#pragma unroll
+        for (int k = 0; k < SK_MAXP; k++) {
+            const int gp = p0 + k < p1 ? p0 + k : p1 - 1;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const size_t ab = (size_t)t * args.a.nbp + 2 * gp + j;
+                xq[k][j] = load16((const uint8_t *)(args.a.q + ab * 64 + kg * 16));
+                dx[k][j] = args.a.d[ab];
+                sx[k][j] = DT == 4 ? args.a.s[ab] : 0;
+            }
+        }
+    };
+    if (has) {
+#pragma unroll
+        for (int k = 0; k < SK_MAXP; k++) {
+            const int gp = p0 + k < p1 ? p0 + k : p1 - 1;
+            if (DT == 4) {
+                raw[k][0] = load16(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
+            } else {
+                const uint8_t *base = m.w + ((size_t)rt * m.nbp + 2 * gp) * 1024 + lane * 16;
+                raw[k][0] = load16(base);
+                raw[k][DT == 4 ? 0 : 1] = load16(base + 1024);
+            }
+            const uint16_t *dcol = m.d + rt * 16 + 4 * kg;
+            sc[k][0] = *(const uint2 *)(dcol + (size_t)(2 * gp) * m.rows_pad);
+            sc[k][1] = *(const uint2 *)(dcol + (size_t)(2 * gp + 1) * m.rows_pad);
+        }
+        if (tfirst < args.T) load_x(tfirst);
+    }
+    const v4i zero = {0, 0, 0, 0};
+    float *dmy = P + (size_t)nb * ntok * 16 + lane * 4;   /* padding token columns store here */
+    for (int t0 = tfirst; t0 < args.T; t0 += tstep) {
+        if (has) {
+            v4i cc[SK_MAXP][2];
+#pragma unroll
+            for (int k = 0; k < SK_MAXP; k++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    v4i wa;
+                    if (DT == 4) {
+                        v4i w0, w1;
+                        unpack_q4(raw[k][0], w0, w1);
+                        wa = j ? w1 : w0;
+                    } else {
+                        wa = raw[k][DT == 4 ? 0 : j];
+                    }
+                    cc[k][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, xq[k][j], zero, 0, 0, 0);
+                }
+#pragma unroll
+            for (int k = 0; k < SK_MAXP; k++) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int g = 2 * (p0 + k) + j;
+                    if (p0 + k >= p1 || g >= nb) continue;   /* uniform */
+                    v4i c = cc[k][j];
+                    if (DT == 4) {
+                        const int off = 8 * sx[k][j];   /* sum(nib * q) - 8 sum(q) = sum((nib - 8) q) */
+                        c.x -= off; c.y -= off; c.z -= off; c.w -= off;
+                    }
+                    const uint2 sw = sc[k][j];
+                    const float d = dx[k][j];
+                    float4 v;
+                    v.x = fmul((float)c.x, fmul(h2f((uint16_t)(sw.x & 0xffff)), d));
+                    v.y = fmul((float)c.y, fmul(h2f((uint16_t)(sw.x >> 16)), d));
+                    v.z = fmul((float)c.z, fmul(h2f((uint16_t)(sw.y & 0xffff)), d));
+                    v.w = fmul((float)c.w, fmul(h2f((uint16_t)(sw.y >> 16)), d));
+                    float *dst = lr < ntok ? P + ((size_t)g * ntok + lr) * 16 + 4 * kg : dmy;
+                    *(float4 *)dst = v;
+                }
+            }
+            if (t0 + tstep < args.T) load_x(t0 + tstep);
+        }
+        __syncthreads();
+        for (int f = tid; f < ntok * 16; f += blockDim.x) {
+            const int c = f >> 4, row = rt * 16 + (f & 15), t = t0 + c;
+            const float acc = fold_terms(P, nb, ntok, f);
+            if (t < args.T && row < m.rows) {
                 float y = canon(acc);
                 if (sg.scale_on) y = canon(fmul(sg.scale, y));
                 sg.Y[(size_t)t * sg.ldy + row] = y;
@@ -1011,8 +1162,21 @@ static int sk_ntok(int T, int NM, int nb) {
     return n < 1 ? 1 : n;
 }
 
-/* few-token dense product: one launch per run of consecutive segments of one dtype */
-static void gemm_sk(const GemmArgs &in, hipStream_t st) {
+/* k_gemm_skm applies: every segment's block pairs fit its waves' registers (at most 8
+ * waves of SK_MAXP pairs) and its terms the LDS */
+static bool skm_ok(const GemmArgs &in) {
+    static const bool on = [] { const char *e = getenv("HX_SKM"); return !(e && e[0] == '0'); }();
+    if (!on) return false;
+    for (int s = 0; s < in.nseg; s++) {
+        const QMat &m = in.seg[s].m;
+        if ((m.nbp >> 1) > 8 * SK_MAXP || (size_t)m.nb * 64 > (size_t)SK_LDS) return false;
+    }
+    return true;
+}
+
+/* dense product through the split-K kernels (k_gemm_sk, or k_gemm_skm when resident):
+ * one launch per run of consecutive segments of one dtype */
+static void gemm_sk(const GemmArgs &in, hipStream_t st, bool resident = false) {
     for (int s0 = 0; s0 < in.nseg;) {
         int s1 = s0 + 1;
         while (s1 < in.nseg && in.seg[s1].m.dtype == in.seg[s0].m.dtype && in.seg[s1].m.nb == in.seg[s0].m.nb) s1++;
@@ -1028,7 +1192,14 @@ static void gemm_sk(const GemmArgs &in, hipStream_t st) {
         const int ntok = sk_ntok(in.T, 1, m.nb);
         const int threads = 64 * sk_waves(m.nbp / 2);
         const size_t lds = (size_t)m.nb * ntok * 64 + SK_DUMMY;
-        if (wg) {
+        if (wg && resident) {
+            /* token tiles split over workgroups until the row tiles fill the CUs */
+            const int ntile = (in.T + ntok - 1) / ntok;
+            int nsplit = 1;
+            while (nsplit < ntile && wg * (nsplit + 1) <= cu_count()) nsplit++;
+            if (m.dtype == 4) k_gemm_skm<4><<<wg * nsplit, threads, lds, st>>>(g, ntok, wg, nsplit);
+            else k_gemm_skm<3><<<wg * nsplit, threads, lds, st>>>(g, ntok, wg, nsplit);
+        } else if (wg) {
             if (m.dtype == 4) k_gemm_sk<4><<<wg, threads, lds, st>>>(g, ntok);
             else k_gemm_sk<3><<<wg, threads, lds, st>>>(g, ntok);
         }
@@ -1042,6 +1213,7 @@ void gemm(const GemmArgs &in, hipStream_t st) {
         for (int s = 0; s < in.nseg; s++) ok = ok && (size_t)in.seg[s].m.nb * 64 <= (size_t)SK_LDS;
         if (ok) { gemm_sk(in, st); return; }
     }
+    if (in.t0 == 0 && skm_ok(in)) { gemm_sk(in, st, true); return; }
     GemmArgs g = in;
     int wg = 0, tiles = 0;
     for (int s = 0; s < g.nseg; s++) {
