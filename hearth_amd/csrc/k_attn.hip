@@ -427,6 +427,63 @@ __global__ __launch_bounds__(SM_T) void k_attn_softmax(AttnArgs a) {
     }
 }
 
+/* The same softmax with one wave per (token, head) row, for many rows of at most
+ * SMW_PER * 64 scores (a tree's or a prefill's): the row's scores and exps stay in the
+ * lane's registers, the exps also go to the wave's own LDS slice for the 16 sequential
+ * partial sums, and nothing waits on the workgroup: the same operations in the same
+ * order as k_attn_softmax, so the same bits. */
+constexpr int SMW_WAVES = 4;
+constexpr int SMW_PER = 48;
+constexpr int SMW_MAX = SMW_PER * 64;
+constexpr int SMW_ROWS = 1024;   /* rows from which a wave per row beats a workgroup per row */
+
+__global__ __launch_bounds__(64 * SMW_WAVES) void k_attn_softmax_w(AttnArgs a) {
+    __shared__ float es_all[SMW_WAVES][SMW_MAX];
+    __shared__ unsigned long long etab[32];
+    exp_table_to_lds(etab);
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = blockIdx.x * SMW_WAVES + wave;
+    if (row >= a.T * a.H) return;   /* uniform per wave; no barrier follows */
+    const int t = row / a.H, h = row % a.H;
+    if (a.g.live && t >= *a.g.live) return;   /* padding token */
+    const int pos0 = *a.g.pos, nr = pos0 + a.g.depth[t] + 1;
+    float *s = a.S + ((size_t)t * a.H + h) * a.ldS;
+    float *es = es_all[wave];
+    float x[SMW_PER];
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int u = 0; u < SMW_PER; u++) {
+        const int i = lane + 64 * u;
+        x[u] = i < nr ? s[i] : -__builtin_huge_valf();
+    }
+#pragma unroll
+    for (int u = 0; u < SMW_PER; u++)
+        if (x[u] == x[u]) m = fmaxf(m, x[u]);
+    m = wave_max_f32(m);   /* a maximum: any reduction order gives the same value */
+    const float s0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x[0])));
+    if (s0 != s0) m = s0;
+#pragma unroll
+    for (int u = 0; u < SMW_PER; u++) {
+        if (64 * u < nr) {   /* uniform */
+            const int i = lane + 64 * u;
+            const float e = exp_glibc_f(fadd(x[u], -m), etab);
+            x[u] = e;
+            if (i < nr) es[i] = e;
+        }
+    }
+    wave_sync();
+    float L = 0.0f;   /* lane < 16: partial of the elements i = lane (mod 16) */
+    if (lane < 16) L = sum16_lds(es, nr, lane, L);
+    L = tree16(L);
+    const float sum = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L)));
+#pragma unroll
+    for (int u = 0; u < SMW_PER; u++) {
+        const int i = lane + 64 * u;
+        if (64 * u < nr && i < nr) s[i] = fdiv(x[u], sum);
+    }
+}
+
 /* o[t][h][d] = sum_v p_v * V_v[d], v in order. A workgroup sums up to four heads of
  * one token t in one KV group g, for one 64-wide d chunk: one summing wave per head
  * (lane = column d, one dependent add chain per lane), and eight loader waves.
@@ -1172,7 +1229,10 @@ void attention_scores(const AttnArgs &a, hipStream_t st) {
 
 void attention_finish(const AttnArgs &a, hipStream_t st) {
     const int grp = a.H / a.Hkv, nd = (a.hd + 63) / 64;
-    k_attn_softmax<<<a.T * a.H, SM_T, 0, st>>>(a);
+    if (a.g.nr_max <= SMW_MAX && a.T * a.H >= SMW_ROWS)
+        k_attn_softmax_w<<<(a.T * a.H + SMW_WAVES - 1) / SMW_WAVES, 64 * SMW_WAVES, 0, st>>>(a);
+    else
+        k_attn_softmax<<<a.T * a.H, SM_T, 0, st>>>(a);
     const bool wide = (long long)a.T * a.H * nd >= TV_WIDE;
 #define HX_TV(NS_, NL_, R_, ROWS_)                                                                     \
     {                                                                                                  \
