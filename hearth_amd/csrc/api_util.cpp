@@ -174,7 +174,9 @@ HEARTH_API int hearth_gpu_accept_sample(const float *rows, int n, int V, const i
         return E_IO;
     const hxl::SamplerSpec sp{smp->temperature, smp->top_p, smp->min_p, smp->repetition_penalty, smp->top_k,
                               smp->context, n_ctx};
-    if (hxl::accept_sample(m, dr, n, V, m.tok, m.par, sp, q, u, s.st) != hipSuccess) return E_IO;
+    if (hxl::accept_sample(m, dr, n, V, m.tok, m.par, sp, q, u, s.st, false, hxl::max_siblings(hp.data(), n)) !=
+        hipSuccess)
+        return E_IO;
     std::vector<int> res(3), path(n);
     if (hipMemcpyAsync(res.data(), m.result, sizeof(int) * 3, hipMemcpyDeviceToHost, s.st) != hipSuccess ||
         hipMemcpyAsync(path.data(), m.path, sizeof(int) * n, hipMemcpyDeviceToHost, s.st) != hipSuccess ||

@@ -2118,7 +2118,8 @@ HEARTH_API int hearth_verify_sample(hearth_engine *e, const int32_t *tokens, con
         const int n_ctx = s->repetition_penalty != 1.0 ? s->n_context : 0;
         ck(e->samp.ensure(n, e->V, q != nullptr, n_ctx));
         hxl::SamplerSpec sp{s->temperature, s->top_p, s->min_p, s->repetition_penalty, s->top_k, s->context, n_ctx};
-        ck(hxl::accept_sample(e->samp, e->logits, n, e->V, e->tokens, d_par, sp, q, u, e->st));
+        ck(hxl::accept_sample(e->samp, e->logits, n, e->V, e->tokens, d_par, sp, q, u, e->st, false,
+                              hxl::max_siblings(parent, n)));
         d_path = e->samp.path;
         d_res = e->samp.result;
     });
@@ -2140,7 +2141,8 @@ HEARTH_API int hearth_gpu_verify_sample_dq(hearth_engine *e, const int32_t *toke
         const int n_ctx = s->repetition_penalty != 1.0 ? s->n_context : 0;
         ck(e->samp.ensure(n, e->V, false, n_ctx));
         hxl::SamplerSpec sp{s->temperature, s->top_p, s->min_p, s->repetition_penalty, s->top_k, s->context, n_ctx};
-        ck(hxl::accept_sample(e->samp, e->logits, n, e->V, e->tokens, d_par, sp, q_dev, u, e->st, true));
+        ck(hxl::accept_sample(e->samp, e->logits, n, e->V, e->tokens, d_par, sp, q_dev, u, e->st, true,
+                              hxl::max_siblings(parent, n)));
         d_path = e->samp.path;
         d_res = e->samp.result;
     });

@@ -7,6 +7,8 @@
 
 #include "hx_device.h"
 
+#include <vector>
+
 namespace hxd {
 
 struct GemmSeg {
@@ -230,7 +232,7 @@ struct SampleArgs {
     int *seg_begin, *seg_end;         /* [n] row v's candidates: [seg_begin, seg_end) = v * sort_n + [0, m) */
     int *bstar;                       /* [n] first histogram bin of tier 0 (-1: every nonzero entry) */
     int sort_n;                       /* power of two >= V */
-    double *wa, *wb, *cc;             /* [V] residuals; the draw's running sums */
+    double *cc;                       /* [V] the draw's running sums */
     int *row_rc;                      /* [n] 0 ok, -1 bad logits */
     int *path;                        /* [n] accepted nodes from the root */
     int *result;                      /* [0] path length, [1] final token, [2] status */
@@ -243,6 +245,9 @@ struct SampleArgs {
     int *bcnt, *brel;                 /* [n][SAMPLE_HBINS] top-p candidates per fine bin; places taken so far */
     int *tcut;                        /* [n] top-p: every entry of a histogram bin below this one is dropped */
     int tail_wide;                    /* top-p's renormalization runs a workgroup per numpy buffer */
+    double *R;                        /* [n][V] residual after node c is rejected (unnormalized) */
+    double *rsum;                     /* [n][SAMPLE_WB] its numpy buffers' pairwise sums */
+    int *sib_prev, *sib_rank;         /* [n] the sibling before c in index order (-1: none), c's place among them */
 };
 
 /* Greedy speculative decoding loop on the device (k_loop.hip): fields of the state block. */
@@ -343,7 +348,7 @@ struct SamplerSpec {
 struct SampleScratch {
     int n_cap = 0, V = 0, ctx_cap = 0, sort_n = 0;
     bool has_q = false;
-    double *P = nullptr, *q = nullptr, *u = nullptr, *wa = nullptr, *wb = nullptr, *cc = nullptr;
+    double *P = nullptr, *q = nullptr, *u = nullptr, *cc = nullptr;
     unsigned long long *skey = nullptr, *skey2 = nullptr;
     int *sidx = nullptr, *sidx2 = nullptr, *seg_begin = nullptr, *seg_end = nullptr, *bstar = nullptr,
         *row_rc = nullptr, *path = nullptr, *result = nullptr, *ctx = nullptr, *tok = nullptr, *par = nullptr;
@@ -351,6 +356,8 @@ struct SampleScratch {
     int *widx = nullptr, *wflag = nullptr;
     unsigned long long *whist = nullptr;
     int *bcnt = nullptr, *brel = nullptr, *tcut = nullptr;
+    double *R = nullptr, *rsum = nullptr;
+    int *sib_prev = nullptr, *sib_rank = nullptr;
     hipError_t ensure(int n, int V, bool need_q, int n_ctx);
     void release();
     ~SampleScratch() { release(); }
@@ -361,7 +368,19 @@ struct SampleScratch {
  * with device tokens/parent. The accepted path is left in m.path, and n_path, final
  * token and status (0, or -1 for bad logits) in m.result[0..2]. */
 hipError_t accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
-                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st, bool q_dev = false);
+                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st, bool q_dev = false,
+                         int max_sib = -1);
+/* the most children of one node of a verify tree (host parent[], or null for a chain);
+ * the residual steps of accept_sample run that many launches (-1 there: n - 1) */
+inline int max_siblings(const int *parent, int n) {
+    if (n <= 1) return 0;
+    if (!parent) return 1;
+    std::vector<int> kids(n, 0);
+    int mx = 0;
+    for (int c = 1; c < n; c++)
+        if (parent[c] >= 0 && parent[c] < n && ++kids[parent[c]] > mx) mx = kids[parent[c]];
+    return mx;
+}
 /* The distribution kernel alone: m.P[v] = the final distribution of row v (the penalty
  * context of row v includes the path tokens of nodes 1..v), m.row_rc[v] its status. */
 hipError_t sample_probs(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,

@@ -40,7 +40,10 @@
  *                  bins, the rest of the row if needed (and, with min-p, the
  *                  renormalization and min-p);
  * k_wide_tsum, k_wide_tdiv: a workgroup per buffer; top-p's cut and renormalization;
- * k_sample_walk:   one workgroup walks the tree from the root with the uniforms.
+ * k_sib, k_resid:  every child's rejection residual and its buffers' sums, a launch per
+ *                  sibling rank, a workgroup per buffer of each child;
+ * k_sample_walk:   one workgroup walks the tree from the root with the uniforms (reading
+ *                  single entries of the residuals) and draws the final token.
  */
 #include <climits>
 #include <functional>
@@ -54,7 +57,6 @@ namespace {
 constexpr int SP_T = 1024;
 constexpr int SP_WAVES = SP_T / 64;
 constexpr int NP_BUF = 8192;                     /* numpy's reduction buffer (elements) */
-constexpr int LV_MAX = (SAMPLE_VMAX / NP_BUF) * 64 + PW_MAXLEAF;
 constexpr int SORT_LDS = 8192;                   /* candidates sorted in LDS */
 constexpr int HBINS = SAMPLE_HBINS;              /* p in (0, 1]: bits >> 51 < 2048 */
 static_assert(HBINS == 2048 && SAMPLE_WB * NP_BUF == SAMPLE_VMAX, "histogram and buffer counts");
@@ -1455,6 +1457,67 @@ __global__ __launch_bounds__(SP_T) void k_wide_tdiv(SampleArgs a) {
  * running sum, so the sums at the nonzero entries are those of the nonzero entries
  * alone); the first sum above the target is at a nonzero entry, and when none is (u
  * close to 1) the last nonzero entry is drawn. */
+/* ---------------------------------------------------------------- residuals, ahead of the walk */
+
+/* The walk rejects the children of a node in index order; after child c of v is
+ * rejected the next sibling is tried against r_c = max(d_prev - q_v, 0), d_prev being p_v
+ * (first child) or the previous sibling's residual divided by its numpy sum, q_v the
+ * point mass at c's token or v's draft distribution (generate.py:113-147 applied
+ * recursively). None of this depends on the uniforms, so every child's residual is
+ * computed before the walk, a launch per sibling rank (the ranks depend on each other
+ * through the previous sibling's sum) and a workgroup per numpy buffer of each child:
+ * the walk then reads one entry of a residual where it used to compute the whole row. */
+__global__ void k_sib(SampleArgs a, int n) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n) return;
+    int prev = -1, rank = 0;
+    if (c > 0) {
+        const int v = a.parent[c];
+        for (int j = 1; j < c; j++)
+            if (a.parent[j] == v) { prev = j; rank++; }
+    }
+    a.sib_prev[c] = prev;
+    a.sib_rank[c] = c > 0 ? rank : -1;
+}
+
+__global__ __launch_bounds__(SP_T) void k_resid(SampleArgs a, int rank) {
+    __shared__ double lv[128];
+    __shared__ double bc;
+    const int c = blockIdx.y, tid = threadIdx.x;
+    const int n = a.live ? *a.live : a.n;
+    if (c >= n || a.sib_rank[c] != rank) return;   /* (uniform) */
+    const int v = a.parent[c], prev = a.sib_prev[c];
+    if (a.row_rc[v] != 0) return;   /* the walk stops at a bad row */
+    const int V = a.V;
+    int r0, len;
+    wide_range(V, r0, len);
+    double s = -1.0;   /* < 0: p_v itself */
+    if (prev >= 0) {
+        s = 0.0;
+        for (int b = 0; b < (int)gridDim.x; b++) s = dadd(s, a.rsum[(size_t)prev * SAMPLE_WB + b]);
+        if (s <= 0.0) return;   /* the walk accepts prev: c is never tried */
+    }
+    const double *src = (prev >= 0 ? a.R + (size_t)prev * V : a.P + (size_t)v * V) + r0;
+    const double *qv = a.q ? a.q + (size_t)v * V + r0 : nullptr;
+    const int x = a.tokens[c] - r0;
+    double *dst = a.R + (size_t)c * V + r0;
+    row_pass(len, [&](int i) { return make_double2(src[i], qv ? qv[i] : (i == x ? 1.0 : 0.0)); }, [&](int i, double2 pq) {
+        const double pc = s < 0.0 ? pq.x : ddiv(pq.x, s);
+        const double d = dsub(pc, pq.y);
+        dst[i] = d > 0.0 ? d : 0.0;
+    });
+    const double bs = np_sum(dst, len, a.tail, lv, &bc);
+    if (tid == 0) a.rsum[(size_t)c * SAMPLE_WB + blockIdx.x] = bs;
+}
+
+/* numpy's sum of residual c from its buffers' sums (0.0, then each in order) */
+__device__ double resid_sum(const SampleArgs &a, int c) {
+    const int nb = (a.V + NP_BUF - 1) / NP_BUF;
+    double s = 0.0;
+    for (int b = 0; b < nb; b++) s = dadd(s, a.rsum[(size_t)c * SAMPLE_WB + b]);
+    return s;
+}
+
 __device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *red, int *sh, ChainShared &cs) {
     const int tid = threadIdx.x, lane = tid & 63;
     (void)red;
@@ -1507,11 +1570,9 @@ __device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *
 }
 
 __global__ __launch_bounds__(SP_T) void k_sample_walk(SampleArgs a) {
-    __shared__ double lv[LV_MAX];
     __shared__ int head[SAMPLE_NMAX], nxt[SAMPLE_NMAX];
     __shared__ int red[SP_WAVES];
     __shared__ int sh[4];
-    __shared__ double shd[4];
     __shared__ ChainShared cs;
     const int V = a.V, tid = threadIdx.x;
     const int n = a.live ? *a.live : a.n;   /* padding rows are not in the tree */
@@ -1532,25 +1593,17 @@ __global__ __launch_bounds__(SP_T) void k_sample_walk(SampleArgs a) {
         const double *qv = a.q ? a.q + (size_t)v * V : nullptr;
         const double *r = nullptr;
         double s = -1.0;                       /* < 0: p itself is the current distribution */
-        double *bufs[2] = {a.wa, a.wb};
-        int cur = 0, next = -1;
+        int next = -1;
         for (int c = head[v]; c >= 0; c = nxt[c]) {
             const int x = a.tokens[c];
             const double px = s < 0.0 ? p[x] : ddiv(r[x], s);
             const double ratio = ddiv(px, qv ? qv[x] : 1.0);
             if (a.u[2 * c] < ratio) { next = c; break; }
-            double *dst = bufs[cur];
-            row_pass(V, [&](int i) { return make_double2(s < 0.0 ? p[i] : r[i], qv ? qv[i] : (i == x ? 1.0 : 0.0)); },
-                     [&](int i, double2 pq) {
-                const double pc = s < 0.0 ? pq.x : ddiv(pq.x, s);
-                const double d = dsub(pc, pq.y);
-                dst[i] = d > 0.0 ? d : 0.0;
-            });
-            const double ns = np_sum(dst, V, a.tail, lv, shd + 2);
+            /* the residual after c (k_resid) and its numpy sum */
+            const double ns = resid_sum(a, c);
             if (ns <= 0.0) { next = c; break; }
-            r = dst;
+            r = a.R + (size_t)c * V;
             s = ns;
-            cur ^= 1;
         }
         if (next < 0) {
             fin = draw(s < 0.0 ? p : r, V, a.u[2 * v + 1], a, red, sh, cs);
@@ -1623,12 +1676,12 @@ template <class T> hipError_t grow(T *&p, size_t count) {
 } // namespace
 
 void SampleScratch::release() {
-    void *ps[] = {P, q, u, wa, wb, cc, skey, skey2, sidx, sidx2, seg_begin, seg_end, bstar, row_rc, path,
-                  result, ctx, tok, par, wmax, wsum, widx, wflag, whist, bcnt, brel, tcut};
+    void *ps[] = {P, q, u, cc, skey, skey2, sidx, sidx2, seg_begin, seg_end, bstar, row_rc, path,
+                  result, ctx, tok, par, wmax, wsum, widx, wflag, whist, bcnt, brel, tcut, R, rsum, sib_prev, sib_rank};
     for (void *p : ps)
         if (p) (void)hipFree(p);
-    P = q = u = wa = wb = cc = wmax = wsum = nullptr;
-    widx = wflag = bcnt = brel = tcut = nullptr;
+    P = q = u = cc = wmax = wsum = R = rsum = nullptr;
+    widx = wflag = bcnt = brel = tcut = sib_prev = sib_rank = nullptr;
     whist = nullptr;
     skey = skey2 = nullptr;
     sidx = sidx2 = seg_begin = seg_end = bstar = row_rc = path = result = ctx = tok = par = nullptr;
@@ -1642,7 +1695,7 @@ hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
         release();
         V = V_;
         sort_n = sort_len(V);
-        if ((e = grow(wa, V)) || (e = grow(wb, V)) || (e = grow(cc, V)) ||
+        if ((e = grow(cc, V)) ||
             (e = grow(result, 4)))
             return e;
     }
@@ -1654,7 +1707,9 @@ hipError_t SampleScratch::ensure(int n, int V_, bool need_q, int n_ctx) {
             (e = grow(row_rc, rows)) || (e = grow(path, rows)) || (e = grow(tok, rows)) || (e = grow(par, rows)) ||
             (e = grow(wmax, rows * SAMPLE_WB)) || (e = grow(wsum, rows * SAMPLE_WB)) || (e = grow(widx, rows * SAMPLE_WB)) ||
             (e = grow(wflag, rows * SAMPLE_WB)) || (e = grow(whist, rows * SAMPLE_HBINS)) ||
-            (e = grow(bcnt, rows * SAMPLE_HBINS)) || (e = grow(brel, rows * SAMPLE_HBINS)) || (e = grow(tcut, rows)))
+            (e = grow(bcnt, rows * SAMPLE_HBINS)) || (e = grow(brel, rows * SAMPLE_HBINS)) || (e = grow(tcut, rows)) ||
+            (e = grow(R, rows * V)) || (e = grow(rsum, rows * SAMPLE_WB)) || (e = grow(sib_prev, rows)) ||
+            (e = grow(sib_rank, rows)))
             return e;
         if (has_q && (e = grow(q, rows * V))) return e;
         n_cap = n;
@@ -1683,10 +1738,11 @@ hipError_t make_args(SampleArgs &a, SampleScratch &m, const float *rows, int n, 
     a.u = m.u;
     a.P = m.P; a.skey = m.skey; a.sidx = m.sidx; a.skey2 = m.skey2; a.sidx2 = m.sidx2; a.sort_n = m.sort_n;
     a.seg_begin = m.seg_begin; a.seg_end = m.seg_end; a.bstar = m.bstar;
-    a.wa = m.wa; a.wb = m.wb; a.cc = m.cc;
+    a.cc = m.cc;
     a.row_rc = m.row_rc; a.path = m.path; a.result = m.result;
     a.wmax = m.wmax; a.wsum = m.wsum; a.widx = m.widx; a.wflag = m.wflag; a.whist = m.whist;
     a.bcnt = m.bcnt; a.brel = m.brel; a.tcut = m.tcut;
+    a.R = m.R; a.rsum = m.rsum; a.sib_prev = m.sib_prev; a.sib_rank = m.sib_rank;
     build_tail(V, a.tail);
     hipError_t e = hipSuccess;
     if (q && !q_dev && (e = hipMemcpyAsync(m.q, q, sizeof(double) * (size_t)n * V, hipMemcpyHostToDevice, st)) != hipSuccess)
@@ -1726,11 +1782,22 @@ hipError_t probs(SampleScratch &, const SampleArgs &a0, int n, hipStream_t st) {
 
 } // namespace
 
+/* the residuals of every child, ahead of the walk */
+void residuals(const SampleArgs &a, int n, int max_sib, hipStream_t st) {
+    if (n <= 1) return;
+    if (max_sib < 0 || max_sib > n - 1) max_sib = n - 1;
+    k_sib<<<(n + 255) / 256, 256, 0, st>>>(a, n);
+    const dim3 g((a.V + NP_BUF - 1) / NP_BUF, n);
+    for (int k = 0; k < max_sib; k++) k_resid<<<g, SP_T, 0, st>>>(a, k);
+}
+
 hipError_t accept_sample(SampleScratch &m, const float *rows, int n, int V, const int *tok, const int *par,
-                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st, bool q_dev) {
+                         const SamplerSpec &s, const double *q, const double *u, hipStream_t st, bool q_dev,
+                         int max_sib) {
     SampleArgs a;
     hipError_t e = make_args(a, m, rows, n, V, tok, par, s, q, u, st, q_dev);
     if (e != hipSuccess || (e = probs(m, a, n, st)) != hipSuccess) return e;
+    residuals(a, n, max_sib, st);
     k_sample_walk<<<1, SP_T, 0, st>>>(a);
     return hipGetLastError();
 }
@@ -1749,6 +1816,7 @@ hipError_t accept_sample_dev(SampleScratch &m, const float *rows, int n, int V, 
     }
     a.live = live;
     if ((e = probs(m, a, n, st)) != hipSuccess) return e;
+    residuals(a, n, 1, st);   /* the loop verifies a chain */
     k_sample_walk<<<1, SP_T, 0, st>>>(a);
     return hipGetLastError();
 }
