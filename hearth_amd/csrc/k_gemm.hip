@@ -342,6 +342,109 @@ __device__ __forceinline__ void wave_pairs(int npair, int W, int w, int &p0, int
     p1 = p0 + ppw < npair ? p0 + ppw : npair;
 }
 
+/* Resident split-K: a wave's weights and scales of NM matrices for its block pairs
+ * [p0, p1) (at most SK_MAXP) stay in registers while token tiles pass through them;
+ * skm_load_x loads one tile's activation blocks (row arow of a for this lane's token),
+ * skm_terms writes the tile's terms as tile_terms_chunk does. */
+template <int DT, int NM>
+struct SkmRegs {
+    v4i raw[NM][SK_MAXP][DT == 4 ? 1 : 2];
+    uint2 sc[NM][SK_MAXP][2];
+    v4i xq[SK_MAXP][2];
+    float dx[SK_MAXP][2];
+    int sx[SK_MAXP][2];
+};
+
+template <int DT, int NM>
+__device__ __forceinline__ void skm_load_w(SkmRegs<DT, NM> &r, const QMat *ms, int rt, int p0, int p1) {
+    const int lane = threadIdx.x & 63, kg = lane >> 4;
+    const int npair = ms[0].nbp >> 1;
+#pragma unroll
+    for (int k = 0; k < SK_MAXP; k++) {
+        const int gp = p0 + k < p1 ? p0 + k : p1 - 1;
+#pragma unroll
+        for (int mi = 0; mi < NM; mi++) {
+            const QMat &m = ms[mi];
+            if (DT == 4) {
+                r.raw[mi][k][0] = load16(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
+            } else {
+                const uint8_t *base = m.w + ((size_t)rt * m.nbp + 2 * gp) * 1024 + lane * 16;
+                r.raw[mi][k][0] = load16(base);
+                r.raw[mi][k][DT == 4 ? 0 : 1] = load16(base + 1024);
+            }
+            const uint16_t *dcol = m.d + rt * 16 + 4 * kg;
+            r.sc[mi][k][0] = *(const uint2 *)(dcol + (size_t)(2 * gp) * m.rows_pad);
+            r.sc[mi][k][1] = *(const uint2 *)(dcol + (size_t)(2 * gp + 1) * m.rows_pad);
+        }
+    }
+}
+
+template <int DT, int NM>
+__device__ __forceinline__ void skm_load_x(SkmRegs<DT, NM> &r, const Act &a, int arow, int p0, int p1) {
+    const int kg = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int k = 0; k < SK_MAXP; k++) {
+        const int gp = p0 + k < p1 ? p0 + k : p1 - 1;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const size_t ab = (size_t)arow * a.nbp + 2 * gp + j;
+            r.xq[k][j] = load16((const uint8_t *)(a.q + ab * 64 + kg * 16));
+            r.dx[k][j] = a.d[ab];
+            r.sx[k][j] = DT == 4 ? a.s[ab] : 0;
+        }
+    }
+}
+
+template <int DT, int NM>
+__device__ __forceinline__ void skm_terms(const SkmRegs<DT, NM> &r, int nb, int ntok, int p0, int p1, float *P,
+                                          int pstride) {
+    const int lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
+    const v4i zero = {0, 0, 0, 0};
+    v4i cc[NM][SK_MAXP][2];
+#pragma unroll
+    for (int k = 0; k < SK_MAXP; k++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int mi = 0; mi < NM; mi++) {
+                v4i wa;
+                if (DT == 4) {
+                    v4i w0, w1;
+                    unpack_q4(r.raw[mi][k][0], w0, w1);
+                    wa = j ? w1 : w0;
+                } else {
+                    wa = r.raw[mi][k][DT == 4 ? 0 : j];
+                }
+                cc[mi][k][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, r.xq[k][j], zero, 0, 0, 0);
+            }
+    float *dmy = P + (size_t)NM * nb * ntok * 16 + lane * 4;   /* after the NM matrices' terms */
+#pragma unroll
+    for (int k = 0; k < SK_MAXP; k++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int g = 2 * (p0 + k) + j;
+            if (p0 + k >= p1 || g >= nb) continue;   /* uniform */
+#pragma unroll
+            for (int mi = 0; mi < NM; mi++) {
+                v4i c = cc[mi][k][j];
+                if (DT == 4) {
+                    const int off = 8 * r.sx[k][j];   /* sum(nib * q) - 8 sum(q) = sum((nib - 8) q) */
+                    c.x -= off; c.y -= off; c.z -= off; c.w -= off;
+                }
+                const uint2 sw = r.sc[mi][k][j];
+                const float d = r.dx[k][j];
+                float4 v;
+                v.x = fmul((float)c.x, fmul(h2f((uint16_t)(sw.x & 0xffff)), d));
+                v.y = fmul((float)c.y, fmul(h2f((uint16_t)(sw.x >> 16)), d));
+                v.z = fmul((float)c.z, fmul(h2f((uint16_t)(sw.y & 0xffff)), d));
+                v.w = fmul((float)c.w, fmul(h2f((uint16_t)(sw.y >> 16)), d));
+                float *dst = lr < ntok ? P + (size_t)mi * pstride + ((size_t)g * ntok + lr) * 16 + 4 * kg : dmy;
+                *(float4 *)dst = v;
+            }
+        }
+    }
+}
+
 /* dense product of few tokens: one workgroup per 16-row tile of a segment. */
 template <int DT>
 __global__ __launch_bounds__(512) void k_gemm_sk(GemmArgs args, int ntok) {
@@ -387,96 +490,25 @@ __global__ __launch_bounds__(512) void k_gemm_skm(GemmArgs args, int ntok, int n
     const QMat &m = sg.m;
     const int rt = bid - sg.wg0;
     const int tfirst = args.t0 + split * ntok, tstep = nsplit * ntok;
-    const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
-    const int lane = tid & 63, kg = lane >> 4, lr = lane & 15;
-    const int npair = m.nbp >> 1, nb = m.nb;
+    const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x, lr = tid & 15;
     int p0, p1;
-    wave_pairs(npair, W, wave, p0, p1);
+    wave_pairs(m.nbp >> 1, W, wave, p0, p1);
     const bool has = p0 < p1;   /* uniform per wave */
-    v4i raw[SK_MAXP][DT == 4 ? 1 : 2];
-    uint2 sc[SK_MAXP][2];
-    v4i xq[SK_MAXP][2];
-    float dx[SK_MAXP][2];
-    int sx[SK_MAXP][2];
-    auto load_x = [&](int t0) {
-        int t = t0 + lr;
-        t = t < args.T ? t : args.T - 1;
-#pragma unroll
-        for (int k = 0; k < SK_MAXP; k++) {
-            const int gp = p0 + k < p1 ? p0 + k : p1 - 1;
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const size_t ab = (size_t)t * args.a.nbp + 2 * gp + j;
-                xq[k][j] = load16((const uint8_t *)(args.a.q + ab * 64 + kg * 16));
-                dx[k][j] = args.a.d[ab];
-                sx[k][j] = DT == 4 ? args.a.s[ab] : 0;
-            }
-        }
-    };
+    auto arow = [&](int t0) { const int t = t0 + lr; return t < args.T ? t : args.T - 1; };
+    SkmRegs<DT, 1> r;
     if (has) {
-#pragma unroll
-        for (int k = 0; k < SK_MAXP; k++) {
-            const int gp = p0 + k < p1 ? p0 + k : p1 - 1;
-            if (DT == 4) {
-                raw[k][0] = load16(m.w + ((size_t)rt * npair + gp) * 1024 + lane * 16);
-            } else {
-                const uint8_t *base = m.w + ((size_t)rt * m.nbp + 2 * gp) * 1024 + lane * 16;
-                raw[k][0] = load16(base);
-                raw[k][DT == 4 ? 0 : 1] = load16(base + 1024);
-            }
-            const uint16_t *dcol = m.d + rt * 16 + 4 * kg;
-            sc[k][0] = *(const uint2 *)(dcol + (size_t)(2 * gp) * m.rows_pad);
-            sc[k][1] = *(const uint2 *)(dcol + (size_t)(2 * gp + 1) * m.rows_pad);
-        }
-        if (tfirst < args.T) load_x(tfirst);
+        skm_load_w<DT, 1>(r, &m, rt, p0, p1);
+        if (tfirst < args.T) skm_load_x<DT, 1>(r, args.a, arow(tfirst), p0, p1);
     }
-    const v4i zero = {0, 0, 0, 0};
-    float *dmy = P + (size_t)nb * ntok * 16 + lane * 4;   /* padding token columns store here */
     for (int t0 = tfirst; t0 < args.T; t0 += tstep) {
         if (has) {
-            v4i cc[SK_MAXP][2];
-#pragma unroll
-            for (int k = 0; k < SK_MAXP; k++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    v4i wa;
-                    if (DT == 4) {
-                        v4i w0, w1;
-                        unpack_q4(raw[k][0], w0, w1);
-                        wa = j ? w1 : w0;
-                    } else {
-                        wa = raw[k][DT == 4 ? 0 : j];
-                    }
-                    cc[k][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, xq[k][j], zero, 0, 0, 0);
-                }
-#pragma unroll
-            for (int k = 0; k < SK_MAXP; k++) {
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const int g = 2 * (p0 + k) + j;
-                    if (p0 + k >= p1 || g >= nb) continue;   /* uniform */
-                    v4i c = cc[k][j];
-                    if (DT == 4) {
-                        const int off = 8 * sx[k][j];   /* sum(nib * q) - 8 sum(q) = sum((nib - 8) q) */
-                        c.x -= off; c.y -= off; c.z -= off; c.w -= off;
-                    }
-                    const uint2 sw = sc[k][j];
-                    const float d = dx[k][j];
-                    float4 v;
-                    v.x = fmul((float)c.x, fmul(h2f((uint16_t)(sw.x & 0xffff)), d));
-                    v.y = fmul((float)c.y, fmul(h2f((uint16_t)(sw.x >> 16)), d));
-                    v.z = fmul((float)c.z, fmul(h2f((uint16_t)(sw.y & 0xffff)), d));
-                    v.w = fmul((float)c.w, fmul(h2f((uint16_t)(sw.y >> 16)), d));
-                    float *dst = lr < ntok ? P + ((size_t)g * ntok + lr) * 16 + 4 * kg : dmy;
-                    *(float4 *)dst = v;
-                }
-            }
-            if (t0 + tstep < args.T) load_x(t0 + tstep);
+            skm_terms<DT, 1>(r, m.nb, ntok, p0, p1, P, 0);
+            if (t0 + tstep < args.T) skm_load_x<DT, 1>(r, args.a, arow(t0 + tstep), p0, p1);
         }
         __syncthreads();
         for (int f = tid; f < ntok * 16; f += blockDim.x) {
             const int c = f >> 4, row = rt * 16 + (f & 15), t = t0 + c;
-            const float acc = fold_terms(P, nb, ntok, f);
+            const float acc = fold_terms(P, m.nb, ntok, f);
             if (t < args.T && row < m.rows) {
                 float y = canon(acc);
                 if (sg.scale_on) y = canon(fmul(sg.scale, y));
@@ -1165,8 +1197,6 @@ static int sk_ntok(int T, int NM, int nb) {
 /* k_gemm_skm applies: every segment's block pairs fit its waves' registers (at most 8
  * waves of SK_MAXP pairs) and its terms the LDS */
 static bool skm_ok(const GemmArgs &in) {
-    static const bool on = [] { const char *e = getenv("HX_SKM"); return !(e && e[0] == '0'); }();
-    if (!on) return false;
     for (int s = 0; s < in.nseg; s++) {
         const QMat &m = in.seg[s].m;
         if ((m.nbp >> 1) > 8 * SK_MAXP || (size_t)m.nb * 64 > (size_t)SK_LDS) return false;
