@@ -232,7 +232,7 @@ struct SampleArgs {
     int *seg_begin, *seg_end;         /* [n] row v's candidates: [seg_begin, seg_end) = v * sort_n + [0, m) */
     int *bstar;                       /* [n] first histogram bin of tier 0 (-1: every nonzero entry) */
     int sort_n;                       /* power of two >= V */
-    double *cc;                       /* [V] the draw's running sums */
+    double *cc;                       /* [V / 8] the draw's running sum at the end of each group of 8 entries */
     int *row_rc;                      /* [n] 0 ok, -1 bad logits */
     int *path;                        /* [n] accepted nodes from the root */
     int *result;                      /* [0] path length, [1] final token, [2] status */

@@ -405,6 +405,9 @@ __device__ void bitonic_global(unsigned long long *gkey, int *gidx, int N, unsig
  * computed. */
 struct ChainShared {
     long long wsum[SP_WAVES];
+    int wtie[SP_WAVES], wdel[SP_WAVES];   /* per wave: a of its last tie (-1: none), its ties' adjustments */
+    long long dfb[SP_T];                  /* per thread: the units before its first entry that leaves the binade */
+    long long dend;                       /* the units after the block's last entry */
     double c, cnext;
     int first_bad, stop;
 };
@@ -448,86 +451,168 @@ __device__ double chain_exact(GetX get_x, int m, double stop_at, int *stop_j, On
             __syncthreads();
             continue;
         }
-        int e = ilogb(c);
-        if (e < -1022) e = -1022;
-        const double u = ldexp(1.0, e - 52);
-        const long long base = (long long)(c / u);   /* exact: c is a multiple of u below 2^53 u */
-        const int jt = j0 + tid * CE_PER;            /* this thread's first entry */
-        long long d[CE_PER];
-        bool bad[CE_PER];
-        long long tsum = 0;
+        /* a block of SP_T CE_PER entries is loaded once; sub-rounds run the chain through
+         * it from js, each in the binade of the current c, until it is used up */
+        const int jb = j0, jend = j0 + SP_T * CE_PER < m ? j0 + SP_T * CE_PER : m;
+        const int jt = jb + tid * CE_PER;   /* this thread's first entry */
+        double xv[CE_PER];
 #pragma unroll
-        for (int k = 0; k < CE_PER; k++) {
-            const int j = jt + k;
-            d[k] = 0;
-            bad[k] = false;
-            if (j < m) {
-                const double q = ldexp(get_x(j), 52 - e);   /* x / u: a power-of-two scaling, exact */
-                if (!(q < 0x1p53)) {
-                    bad[k] = true;
-                } else {
-                    const double f = floor(q), r = q - f;
-                    d[k] = (long long)f + (r > 0.5 ? 1 : 0);
-                    bad[k] = r == 0.5;
-                }
-            }
-            tsum += d[k];
-        }
-        long long inc = tsum;
-        for (int off = 1; off < 64; off <<= 1) {
-            const long long y = __shfl_up(inc, off, 64);
-            if (lane >= off) inc += y;
-        }
-        if (lane == 63) cs.wsum[w] = inc;
-        if (tid == 0) { cs.first_bad = INT_MAX; cs.stop = INT_MAX; }
-        __syncthreads();
-        long long before = 0;
-        for (int i = 0; i < w; i++) before += cs.wsum[i];
-        const long long D0 = base + before + inc - tsum;   /* c / u before entry jt, if no earlier entry was bad */
-        {
-            long long D = D0;
+        for (int k = 0; k < CE_PER; k++) xv[k] = jt + k < jend ? get_x(jt + k) : 0.0;
+        int js = j0;
+        while (js < jend && stop == m) {
+            int e = ilogb(c);
+            if (e < -1022) e = -1022;
+            const double u = ldexp(1.0, e - 52);
+            const long long base = (long long)(c / u);   /* exact: c is a multiple of u below 2^53 u */
+            long long d[CE_PER];
+            bool tie[CE_PER], huge[CE_PER];
+            long long tsum = 0;
+            bool has_tie = false;
 #pragma unroll
             for (int k = 0; k < CE_PER; k++) {
                 const int j = jt + k;
-                if (j >= m) break;
-                D += d[k];
-                if (bad[k] || D >= (1ll << 53)) {
-                    atomicMin(&cs.first_bad, j);
+                d[k] = 0;
+                tie[k] = huge[k] = false;
+                if (j >= js && j < jend) {
+                    const double q = ldexp(xv[k], 52 - e);   /* x / u: a power-of-two scaling, exact */
+                    if (!(q < 0x1p53)) {
+                        huge[k] = true;
+                    } else {
+                        const double f = floor(q), r = q - f;
+                        d[k] = (long long)f + (r > 0.5 ? 1 : 0);
+                        tie[k] = r == 0.5;   /* its d is the floor until its parity is known */
+                        has_tie |= tie[k];
+                    }
+                }
+                tsum += d[k];
+            }
+            long long inc = tsum;
+            for (int off = 1; off < 64; off <<= 1) {
+                const long long y = __shfl_up(inc, off, 64);
+                if (lane >= off) inc += y;
+            }
+            if (lane == 63) cs.wsum[w] = inc;
+            if (tid == 0) { cs.first_bad = INT_MAX; cs.stop = INT_MAX; }
+            const bool any_tie = __syncthreads_or(has_tie);
+            long long before = 0;
+            for (int i = 0; i < w; i++) before += cs.wsum[i];
+            const long long D0 = base + before + inc - tsum;   /* units before entry jt (ties at their floor) */
+            /* A tie i rounds to even: with P_i the units before it at the floor of every
+             * earlier tie and a_i = (P_i + floor_i) mod 2, it adds floor_i + (a_i xor
+             * a_(i-1)) (a of the previous tie of the round, 0 for the first): the parity of
+             * the adjustments so far is always a of the last tie. */
+            int dl[CE_PER];
+            long long Dx = 0;   /* adjustments before this thread's first entry */
+#pragma unroll
+            for (int k = 0; k < CE_PER; k++) dl[k] = 0;
+            if (any_tie) {
+                int a_last = 0;
+                long long P = D0;
+#pragma unroll
+                for (int k = 0; k < CE_PER; k++) {
+                    if (tie[k]) { dl[k] = (int)((P + d[k]) & 1); a_last = dl[k]; }   /* a_k for now */
+                    P += d[k];
+                }
+                /* a of the last tie before this thread: in the wave, then the earlier waves */
+                const unsigned long long tb = __ballot(has_tie);
+                const unsigned long long before_me = tb & ((1ull << lane) - 1ull);
+                const int src = before_me ? 63 - __builtin_clzll(before_me) : 0;
+                const int got = __shfl(a_last, src, 64);
+                int a_prev = before_me ? got : 0;
+                const int wl = tb ? 63 - __builtin_clzll(tb) : 0;
+                const int wa = __shfl(a_last, wl, 64);
+                if (lane == 0) cs.wtie[w] = tb ? wa : -1;
+                __syncthreads();
+                if (!before_me)
+                    for (int i = w - 1; i >= 0; i--)
+                        if (cs.wtie[i] >= 0) { a_prev = cs.wtie[i]; break; }
+                int dsum = 0;
+#pragma unroll
+                for (int k = 0; k < CE_PER; k++)
+                    if (tie[k]) {
+                        const int ak = dl[k];
+                        dl[k] = ak ^ a_prev;
+                        a_prev = ak;
+                        dsum += dl[k];
+                    }
+                int di = dsum;
+                for (int off = 1; off < 64; off <<= 1) {
+                    const int y = __shfl_up(di, off, 64);
+                    if (lane >= off) di += y;
+                }
+                if (lane == 63) cs.wdel[w] = di;
+                __syncthreads();
+                long long db = 0;
+                for (int i = 0; i < w; i++) db += cs.wdel[i];
+                Dx = db + di - dsum;
+            }
+            /* the sums of this thread's entries up to its first entry that leaves the binade
+             * (or is huge), which it reports with the units before it; the sub-round ends at
+             * the first such entry of the block */
+            double cjv[CE_PER];
+            {
+                long long D = D0 + Dx;
+                int myfb = INT_MAX;
+#pragma unroll
+                for (int k = 0; k < CE_PER; k++) {
+                    cjv[k] = 0.0;
+                    const int j = jt + k;
+                    if (j < js || j >= jend || myfb != INT_MAX) continue;
+                    if (huge[k] || D + d[k] + dl[k] >= (1ll << 53)) {
+                        myfb = j;
+                        continue;
+                    }
+                    D += d[k] + dl[k];
+                    cjv[k] = (double)D * u;   /* an integer below 2^53 times a power of two: exact */
+                    if (cjv[k] >= stop_at) atomicMin(&cs.stop, j);
+                }
+                if (myfb != INT_MAX) {
+                    atomicMin(&cs.first_bad, myfb);
+                    cs.dfb[tid] = D;
+                } else if (jend - 1 >= jt && jend - 1 < jt + CE_PER) {
+                    cs.dend = D;   /* the block's last entry is this thread's */
+                }
+            }
+            __syncthreads();
+            const int fb = cs.first_bad, fend = fb < jend ? fb : jend;
+            if (fend > js) c = (double)(fb < jend ? cs.dfb[(fb - jb) / CE_PER] : cs.dend) * u;
+#pragma unroll
+            for (int k = 0; k < CE_PER; k++) {
+                const int j = jt + k;
+                if (j >= js && j < fend) on_entry(j, cjv[k]);
+            }
+            if (cs.stop < fend) {   /* a stop past fb came from sums that do not hold */
+                stop = cs.stop;
+                break;
+            }
+            if (fb < jend) {   /* entry fb on its own, from the value its thread holds */
+                if (fb >= jt && fb < jt + CE_PER) {
+                    double xf = 0.0;
+#pragma unroll
+                    for (int k = 0; k < CE_PER; k++)
+                        if (jt + k == fb) xf = xv[k];
+                    const double cf = dadd(c, xf);
+                    cs.cnext = cf;
+                    on_entry(fb, cf);
+                }
+                __syncthreads();
+                c = cs.cnext;
+                if (c >= stop_at) stop = fb;
+                const bool little = fb - js < 64;
+                js = fb + 1;
+                if (little) {   /* entries added on their own are frequent here: go on in order */
+                    in_order = true;
                     break;
                 }
+            } else {
+                js = jend;
             }
+            /* no barrier before the next sub-round (there is one after fb's entry, and the
+             * loop ends otherwise): every thread read cs.first_bad, cs.stop, cs.wsum, cs.dfb
+             * and cs.dend before that barrier, and cs.cnext is written again only after two
+             * more */
         }
-        __syncthreads();
-        const int fb = cs.first_bad, jend = j0 + SP_T * CE_PER < m ? j0 + SP_T * CE_PER : m;
-        const int last = (fb < jend ? fb : jend) - 1;   /* last entry finished in parallel */
-        {
-            long long D = D0;
-#pragma unroll
-            for (int k = 0; k < CE_PER; k++) {
-                const int j = jt + k;
-                if (j > last) break;
-                D += d[k];
-                const double cj = (double)D * u;   /* an integer below 2^53 times a power of two: exact */
-                on_entry(j, cj);
-                if (cj >= stop_at) atomicMin(&cs.stop, j);
-                if (j == last) cs.c = cj;
-            }
-        }
-        __syncthreads();
-        if (last >= j0) c = cs.c;
-        if (cs.stop != INT_MAX) {
-            stop = cs.stop;
-            break;
-        }
-        if (fb < jend) {   /* entry fb on its own */
-            c = dadd(c, get_x(fb));
-            if (tid == 0) on_entry(fb, c);
-            if (c >= stop_at) stop = fb;
-            in_order = fb - j0 < 64;   /* the round gained little: go on one entry at a time */
-            j0 = fb + 1;
-        } else {
-            j0 = jend;
-        }
+        j0 = js;
         __syncthreads();
     }
     *stop_j = stop;
@@ -1547,23 +1632,43 @@ __device__ int draw(const double *w, int V, double u, const SampleArgs &a, int *
         __syncthreads();
         return 0;
     }
-    const int m = V - j_first;
+    const int m = V - j_first, ng = (m + 7) / 8;
     int stop;
+    /* the running sums are kept at the end of each group of 8 entries only (cc[g]): the
+     * search finds the group, then runs the chain through it again */
     const double total = chain_exact<8>([&](int j) { return w[j_first + j]; }, m, INF, &stop,
-                                        [&](int j, double cj) { a.cc[j] = cj; }, cs);
+                                        [&](int j, double cj) {
+                                            if ((j & 7) == 7 || j == m - 1) a.cc[j >> 3] = cj;
+                                        }, cs);
     if (tid == 0) sh[0] = INT_MAX;
     __syncthreads();
     const double target = dmul(u, total);
     {
-        /* a thread's first index above the target is its smallest: the rest of its
-         * indices cannot lower the minimum */
+        /* the first group whose last sum passes the target (the sums rise along the row);
+         * a thread's first such group is its smallest */
         bool found = false;
-        row_pass(m, [&](int j) { return a.cc[j]; }, [&](int j, double cj) {
-            if (!found && cj > target) { atomicMin(&sh[0], j); found = true; }
+        row_pass(ng, [&](int g) { return a.cc[g]; }, [&](int g, double cg) {
+            if (!found && cg > target) { atomicMin(&sh[0], g); found = true; }
         });
     }
     __syncthreads();
-    const int jb = sh[0];
+    const int gb = sh[0];
+    int jb = m;
+    if (gb < ng) {   /* uniform */
+        if (tid == 0) {
+            /* the same adds from the sum before the group give the same sums */
+            double c = gb > 0 ? a.cc[gb - 1] : 0.0;
+            const int je = 8 * gb + 8 < m ? 8 * gb + 8 : m;
+            int hit = je - 1;
+            for (int j = 8 * gb; j < je; j++) {
+                c = dadd(c, w[j_first + j]);
+                if (c > target) { hit = j; break; }
+            }
+            sh[3] = hit;
+        }
+        __syncthreads();
+        jb = sh[3];
+    }
     const int r = jb < m ? j_first + jb : j_last;
     __syncthreads();
     return r;
