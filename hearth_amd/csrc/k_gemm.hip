@@ -400,13 +400,16 @@ __device__ __forceinline__ void skm_terms(const SkmRegs<DT, NM> &r, int nb, int 
                                           int pstride) {
     const int lane = threadIdx.x & 63, kg = lane >> 4, lr = lane & 15;
     const v4i zero = {0, 0, 0, 0};
-    v4i cc[NM][SK_MAXP][2];
+    float *dmy = P + (size_t)NM * nb * ntok * 16 + lane * 4;   /* after the NM matrices' terms */
+    /* one matrix at a time: its MFMAs first (each into its own registers), then its f32
+     * terms, so no term waits on the MFMA just issued */
 #pragma unroll
-    for (int k = 0; k < SK_MAXP; k++)
+    for (int mi = 0; mi < NM; mi++) {
+        v4i cc[SK_MAXP][2];
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int k = 0; k < SK_MAXP; k++)
 #pragma unroll
-            for (int mi = 0; mi < NM; mi++) {
+            for (int j = 0; j < 2; j++) {
                 v4i wa;
                 if (DT == 4) {
                     v4i w0, w1;
@@ -415,18 +418,15 @@ __device__ __forceinline__ void skm_terms(const SkmRegs<DT, NM> &r, int nb, int 
                 } else {
                     wa = r.raw[mi][k][DT == 4 ? 0 : j];
                 }
-                cc[mi][k][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, r.xq[k][j], zero, 0, 0, 0);
+                cc[k][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, r.xq[k][j], zero, 0, 0, 0);
             }
-    float *dmy = P + (size_t)NM * nb * ntok * 16 + lane * 4;   /* after the NM matrices' terms */
 #pragma unroll
-    for (int k = 0; k < SK_MAXP; k++) {
+        for (int k = 0; k < SK_MAXP; k++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int g = 2 * (p0 + k) + j;
-            if (p0 + k >= p1 || g >= nb) continue;   /* uniform */
-#pragma unroll
-            for (int mi = 0; mi < NM; mi++) {
-                v4i c = cc[mi][k][j];
+            for (int j = 0; j < 2; j++) {
+                const int g = 2 * (p0 + k) + j;
+                if (p0 + k >= p1 || g >= nb) continue;   /* uniform */
+                v4i c = cc[k][j];
                 if (DT == 4) {
                     const int off = 8 * r.sx[k][j];   /* sum(nib * q) - 8 sum(q) = sum((nib - 8) q) */
                     c.x -= off; c.y -= off; c.z -= off; c.w -= off;
@@ -513,6 +513,52 @@ __global__ __launch_bounds__(512) void k_gemm_skm(GemmArgs args, int ntok, int n
                 float y = canon(acc);
                 if (sg.scale_on) y = canon(fmul(sg.scale, y));
                 sg.Y[(size_t)t * sg.ldy + row] = y;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+/* gate/up with resident weights: a slot's gate and up weights are read once and every
+ * token tile of the slot runs through them (as k_gemm_skm); for waves of at most SK_MAXP
+ * block pairs and 4 waves a workgroup, held to 256 VGPRs (two waves per SIMD: with
+ * 272 the kernel ran one and was slower than reloading the weights per tile) */
+template <int DT>
+__global__ __launch_bounds__(256, 2) void k_expert_gateup_skm(MoeArgs a, int ntok) {
+    extern __shared__ float P[];
+    const int ntile = a.F / 16;
+    const int u = (int)blockIdx.x / ntile, rt = (int)blockIdx.x % ntile;
+    const SlotDesc &sd = a.desc[u];
+    const int n = sd.n, p0 = sd.p0;
+    if (n == 0) return;
+    const ExpertW ew = sd.w;
+    if (ew.gate.dtype != DT) return;   /* the launcher runs one instantiation per dtype */
+    const QMat ms[2] = {ew.gate, ew.up};
+    const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x, lr = tid & 15;
+    int q0, q1;
+    wave_pairs(ew.gate.nbp >> 1, W, wave, q0, q1);
+    const bool has = q0 < q1;
+    const int nb = ew.gate.nb, pstride = nb * ntok * 16;
+    const int *ptok = a.pair_tok + p0;
+    auto arow = [&](int t0) { const int t = t0 + lr; return ptok[t < n ? t : n - 1]; };
+    SkmRegs<DT, 2> r;
+    if (has) {
+        skm_load_w<DT, 2>(r, ms, rt, q0, q1);
+        skm_load_x<DT, 2>(r, a.x, arow(0), q0, q1);
+    }
+    for (int t0 = 0; t0 < n; t0 += ntok) {
+        if (has) {
+            skm_terms<DT, 2>(r, nb, ntok, q0, q1, P, pstride);
+            if (t0 + ntok < n) skm_load_x<DT, 2>(r, a.x, arow(t0 + ntok), q0, q1);
+        }
+        __syncthreads();
+        for (int f = tid; f < ntok * 16; f += blockDim.x) {
+            const int c = f >> 4, row = rt * 16 + (f & 15);
+            const float gv = canon(fold_terms(P, nb, ntok, f));
+            const float uv = canon(fold_terms(P + pstride, nb, ntok, f));
+            if (t0 + c < n) {
+                const float sg = fdiv(gv, fadd(1.0f, exp_glibc_f(-gv)));
+                a.midf[(size_t)(p0 + t0 + c) * a.F + row] = fmul(sg, uv);
             }
         }
         __syncthreads();
@@ -1289,6 +1335,13 @@ bool expert_gateup(const MoeArgs &a, int n_slots, hipStream_t st, hipEvent_t ev0
         const int pgrid = grid < 2 * ncu ? grid : 2 * ncu;
         if (q4) hipExtLaunchKernelGGL(k_expert_gateup_pp<4>, dim3(pgrid), dim3(threads), (uint32_t)lds, st, ev0, ev1, 0u, a, ntok);
         else hipExtLaunchKernelGGL(k_expert_gateup_pp<3>, dim3(pgrid), dim3(threads), (uint32_t)lds, st, ev0, ev1, 0u, a, ntok);
+        return false;
+    }
+    if ((npair + W - 1) / W <= SK_MAXP && threads <= 256) {   /* the wave's pairs fit its registers */
+        if (q4) hipExtLaunchKernelGGL(k_expert_gateup_skm<4>, dim3(grid), dim3(threads), (uint32_t)lds, st, ev0,
+                                      q8 ? nullptr : ev1, 0u, a, ntok);
+        if (q8) hipExtLaunchKernelGGL(k_expert_gateup_skm<3>, dim3(grid), dim3(threads), (uint32_t)lds, st,
+                                      q4 ? nullptr : ev0, ev1, 0u, a, ntok);
         return false;
     }
     if (q4) hipExtLaunchKernelGGL(k_expert_gateup_sk<4>, dim3(grid), dim3(threads), (uint32_t)lds, st, ev0,
