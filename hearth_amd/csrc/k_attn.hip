@@ -1241,7 +1241,10 @@ void attention_finish(const AttnArgs &a, hipStream_t st) {
         return;                                                                                        \
     }
     if (wide && grp >= 16) HX_TV(8, 4, 2, 64)
-    if (wide && grp >= 8) HX_TV(4, 4, 2, 64)
+    /* groups of 8 heads: one head per summing wave, 8 of them (measured on the tree's 85
+     * tokens: 16.91 ms per step against 17.04 with two heads per wave on 4 waves, 17.97
+     * with 8 loader waves and 128-row tiles, 19.91 with four heads per wave) */
+    if (wide && grp >= 8) HX_TV(8, 4, 1, 64)
 #undef HX_TV
     const int qpt = (grp + TV_SUM - 1) / TV_SUM;
     k_attn_values<<<a.T * qpt * a.Hkv * nd + a.pf_wgs, TV_THREADS, 0, st>>>(a);
