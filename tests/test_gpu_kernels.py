@@ -4,7 +4,9 @@
   (engine/tests/test_quant.c:923-931) for F32/F16/BF16/Q8/Q4, libm-free inputs;
 - the int8-MFMA Q8/Q4 GEMM: T tokens in one call equal T single-token calls and the
   oracle bit for bit, across shapes with pad rows, odd block counts and the input kinds
-  of the reference's tests (zero blocks, outliers, .5 ties, tiny values, NaN);
+  of the reference's tests (zero blocks, outliers, .5 ties, tiny values, NaN); T > 16
+  takes the resident-weight kernel, with token tiles split over workgroups where the
+  row tiles are few (T = 17, 23, 40, 85; K up to 4096);
 - the greedy acceptance kernel equals the oracle's walk on tie-heavy random logits,
   chains and trees.
 """
@@ -48,7 +50,8 @@ def _kind(rng, kind, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", [3, 4])
-@pytest.mark.parametrize("rows,cols,T", [(16, 64, 1), (37, 192, 5), (250, 2048, 9), (96, 128, 40), (300, 768, 17)])
+@pytest.mark.parametrize("rows,cols,T", [(16, 64, 1), (37, 192, 5), (250, 2048, 9), (96, 128, 40), (300, 768, 17),
+                                         (48, 4096, 85), (33, 2112, 23)])
 @pytest.mark.parametrize("kind", ["gauss", "zero_blocks", "outlier", "ties", "tiny", "nan"])
 def test_gpu_gemm_equals_oracle_and_single_tokens(dtype, rows, cols, T, kind):
     rng = np.random.default_rng(rows * 31 + cols + T)
