@@ -1240,10 +1240,10 @@ void attention_finish(const AttnArgs &a, hipStream_t st) {
         k_attn_values_w<NS_, NL_, R_, ROWS_><<<a.T * qpt * a.Hkv * nd, 64 * (NS_ + NL_), 0, st>>>(a);  \
         return;                                                                                        \
     }
-    if (wide && grp >= 16) HX_TV(8, 4, 2, 64)
-    /* groups of 8 heads: one head per summing wave, 8 of them (measured on the tree's 85
+    /* groups of 8 or more heads: one head per summing wave, 8 of them (the tree's 85
      * tokens: 16.91 ms per step against 17.04 with two heads per wave on 4 waves, 17.97
-     * with 8 loader waves and 128-row tiles, 19.91 with four heads per wave) */
+     * with 8 loader waves and 128-row tiles, 19.91 with four heads per wave; MLA's 128
+     * heads: 27.08 against 27.50 with two heads per wave on 8 waves, 28.4 with 12) */
     if (wide && grp >= 8) HX_TV(8, 4, 1, 64)
 #undef HX_TV
     const int qpt = (grp + TV_SUM - 1) / TV_SUM;
