@@ -220,15 +220,16 @@ __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
  * latent, 512), where every token reads row v from slot v: one workgroup per 64 rows and
  * block of up to ST_HB heads, for every token. Thread (row, j) loads its row's K elements
  * j + 16 i once and runs through all (token, 8-head) blocks of q, staged transposed in
- * LDS two at a time (one barrier per block), so the K rows are read once per layer
- * instead of once per token. Each score is the same sequence of operations as in
+ * LDS two at a time (one barrier per block), so the K rows are read once per block of
+ * heads instead of once per token (more, smaller head blocks keep more workgroups in
+ * flight: the K rows come from L2 after the first). Each score is the same sequence of operations as in
  * k_attn_scores16. (At head_dim 128 the per-token kernel is faster: it has nine times
  * the workgroups to hide its latencies with; measured 16.8 against 24.6 µs.) */
-constexpr int ST_HB = 32;
+constexpr int ST_HB = 8;   /* 8 heads a workgroup: 24.99 ms per DeepSeek-V3 step against 25.84 with 16 and 27.02 with 32 */
 constexpr int ST_TMAX = 64;
 
 template <int HI>
-__global__ __launch_bounds__(1024) void k_attn_scores16t(AttnArgs a, int nhb) {
+__global__ __launch_bounds__(1024) void k_attn_scores16t(AttnArgs a, int nhb, int hbsz) {
     constexpr int QS = HI / 4 + 1;
     __shared__ float4 qT[2][8][16][QS];
     __shared__ int nr_s[ST_TMAX];
@@ -248,7 +249,7 @@ __global__ __launch_bounds__(1024) void k_attn_scores16t(AttnArgs a, int nhb) {
 #pragma unroll
         for (int i = 0; i < HI; i++) kv[i] = kr[16 * i];
     }
-    const int h_lo = hb * ST_HB, h_hi = min(grp, h_lo + ST_HB), nh8 = (h_hi - h_lo + 7) / 8, nblk = T * nh8;
+    const int h_lo = hb * hbsz, h_hi = min(grp, h_lo + hbsz), nh8 = (h_hi - h_lo + 7) / 8, nblk = T * nh8;
     auto stage = [&](int blk, int buf) {
         const int t = blk / nh8, h0 = h_lo + (blk % nh8) * 8;
         const float *qb = a.q + ((size_t)t * a.H + (size_t)g * grp + h0) * hd;
@@ -1196,7 +1197,7 @@ void attention_scores(const AttnArgs &a, hipStream_t st) {
     if (a.g.chain && a.T <= ST_TMAX && a.hd == 512) {
         const int nhb = (a.H / a.Hkv + ST_HB - 1) / ST_HB, grid = ((max_nr + 63) / 64) * a.Hkv * nhb;
         if (grid >= 128) {
-            k_attn_scores16t<32><<<grid, 1024, 0, st>>>(a, nhb);
+            k_attn_scores16t<32><<<grid, 1024, 0, st>>>(a, nhb, ST_HB);
             return;
         }
     }
