@@ -208,11 +208,11 @@ struct hearth_engine {
     /* the greedy speculative loop on the device (hearth_gpu_spec_greedy), allocated on
      * first use: state block, committed sequence, stop ids, handled tokens, per-step
      * records, the acceptance's draft ids and chain parents, its path, and the RoPE
-     * table of every position (rows [0, lp_rtab_rows) filled so far) */
+     * table indexed by position (rows [lp_rtab_lo, lp_rtab_hi) filled) */
     int *lp_state = nullptr, *lp_hist = nullptr, *lp_stops = nullptr, *lp_out = nullptr, *lp_rec = nullptr,
         *lp_cmp = nullptr, *lp_par = nullptr, *lp_path = nullptr;
     float *lp_rtab = nullptr;
-    int lp_rtab_rows = 0;
+    int lp_rtab_lo = 0, lp_rtab_hi = 0;
     int *h_lp = nullptr;                 /* pinned: (LS_NEW, LS_DONE) of the steps in flight, then the state */
     hipEvent_t lp_ev[2] = {nullptr, nullptr};
     /* sampled runs (hearth_gpu_spec_sample): the acceptance scratch of the loop (its own,
@@ -225,7 +225,7 @@ struct hearth_engine {
     uint64_t lp_skey = 0;
     const int *route_live = nullptr;     /* RouteArgs.live of the forwards being launched */
     void loop_prepare();
-    void loop_rope_table(int rows);
+    void loop_rope_table(int lo, int hi);
     hxd::LoopArgs loop_args(int T);
     void loop_step(int T);
     void launch_loop_step(int T, int rows);
@@ -812,6 +812,7 @@ void hearth_engine::matmul(const DMat &m, const Act &a, const float *xf, int ldx
         g.seg[0].scale = scale;
         g.a = a;
         g.T = T;
+        g.live = route_live;
         hxl::gemm(g, st);
     } else {
         hxl::fgemv(m.dtype, m.f, m.rows, m.cols, xf, ldx, T, Yp, ldy, st);
@@ -836,6 +837,7 @@ void hearth_engine::attn_mla(const Layer &w, int l, int T) {
         g.seg[1].m = w.kv_a.q; g.seg[1].Y = kva; g.seg[1].ldy = kvd;
         g.a = ax;
         g.T = T;
+        g.live = route_live;
         hxl::gemm(g, st);
     } else {
         matmul(qin, ax, x, D, T, qdst, qld, false, 1.0f);
@@ -888,6 +890,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
         hxd::NormArgs n{};
         n.mode = 0; n.h = h; n.tokens = tokens; n.emb = emb; n.emb_dtype = emb_dtype; n.emb_rb = emb_rb;
         n.es = c.emb_scale; n.norm_w = layers[0].attn_norm; n.eps = c.eps; n.x = x; n.a = ax; n.T = T; n.D = D;
+        n.live = route_live;
         hxl::norm(n, st);
     });
     for (int l = 0; l < L; l++) {
@@ -905,6 +908,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 for (int s = 0; s < 3; s++) { g.seg[s].m = ms[s]->q; g.seg[s].Y = ys[s]; g.seg[s].ldy = ld[s]; }
                 g.a = ax;
                 g.T = T;
+                g.live = route_live;
                 hxl::gemm(g, st);
             } else {
                 matmul(w.q, ax, x, D, T, qb, q_dim, false, 1.0f);
@@ -918,6 +922,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             qa.qout = qr; qa.kc = kv + (size_t)l * kv_layer; qa.vc = qa.kc + (size_t)Hkv * cap * hd;
             qa.rope = rope; qa.rfull = rfull; qa.T = T; qa.H = H; qa.Hkv = Hkv; qa.hd = hd; qa.cap = cap;
             qa.qk_norm = c.qk_norm; qa.rope_dim = rope_dim; qa.rope_style = c.rope_style; qa.eps = c.eps; qa.pos = d_pos;
+            qa.live = route_live;
             hxl::qkv_post(qa, st);
             dump("q", l, qr, T, q_dim);
             hxd::AttnArgs at{};
@@ -959,7 +964,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
         timed(&ks.norm_s, [&] {
             hxd::NormArgs n{};
             n.mode = 1; n.h = h; n.add = ao; n.rs = rs; n.norm_w = w.ffn_norm; n.eps = c.eps; n.x = x; n.a = ax;
-            n.T = T; n.D = D;
+            n.T = T; n.D = D; n.live = route_live;
             hxl::norm(n, st);
         });
         dump("h_mid", l, h, T, D);
@@ -1028,7 +1033,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
                 hxd::NormArgs n{};
                 n.mode = 2; n.h = h; n.Y = Y; n.wts = wts; n.pair_of = pair_of; n.K = K; n.rs = rs;
                 n.add = Fs ? shb : nullptr; n.add_gate = w.sh_gate_inp ? shg : nullptr;
-                n.norm_w = next_norm; n.eps = c.eps; n.x = x; n.a = ax; n.T = T; n.D = D;
+                n.norm_w = next_norm; n.eps = c.eps; n.x = x; n.a = ax; n.T = T; n.D = D; n.live = route_live;
                 hxl::norm(n, st);
             });
             /* the layer's work is queued: the prediction's loads overlap it */
@@ -1044,7 +1049,7 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             timed(&ks.norm_s, [&] {
                 hxd::NormArgs n{};
                 n.mode = 1; n.h = h; n.add = ao; n.rs = rs; n.norm_w = next_norm; n.eps = c.eps; n.x = x; n.a = ax;
-                n.T = T; n.D = D;
+                n.T = T; n.D = D; n.live = route_live;
                 hxl::norm(n, st);
             });
         }
@@ -1290,23 +1295,27 @@ void hearth_engine::loop_prepare() {
     lp_state = dnew<int>(hxd::LS_FIELDS);   /* last: a failure above retries everything */
 }
 
-/* RoPE rows of positions [lp_rtab_rows, rows): the same host cosf/sinf values that
- * run_geometry uploads per call (rope_tables, model.c:386-397) */
-void hearth_engine::loop_rope_table(int rows) {
-    if (!rope_dim || rows <= lp_rtab_rows) return;
-    const int half = rope_dim / 2;
-    std::vector<float> tab((size_t)(rows - lp_rtab_rows) * rope_dim);
-    for (int p = lp_rtab_rows; p < rows; p++) {
-        float *r = tab.data() + (size_t)(p - lp_rtab_rows) * rope_dim;
+/* RoPE rows of positions [lo, hi) in the table: the same host cosf/sinf values that
+ * run_geometry uploads per call (rope_tables, model.c:386-397). Only rows not filled
+ * yet are computed: a run's batches extend the filled range, and a batch that starts
+ * outside it (after a rewind) starts a new range, so a run after a long prompt pays for
+ * its own positions, not every position before them. */
+void hearth_engine::loop_rope_table(int lo, int hi) {
+    if (!rope_dim) return;
+    if (lo < lp_rtab_lo || lo > lp_rtab_hi) lp_rtab_lo = lp_rtab_hi = lo;
+    if (hi <= lp_rtab_hi) return;
+    const int half = rope_dim / 2, r0 = lp_rtab_hi;
+    std::vector<float> tab((size_t)(hi - r0) * rope_dim);
+    for (int p = r0; p < hi; p++) {
+        float *r = tab.data() + (size_t)(p - r0) * rope_dim;
         for (int j = 0; j < half; j++) {
             const float th = (float)p * inv_freq[j];
             r[2 * j] = host_cosf(th) * c.rope_factor;
             r[2 * j + 1] = host_sinf(th) * c.rope_factor;
         }
     }
-    ck(hipMemcpy(lp_rtab + (size_t)lp_rtab_rows * rope_dim, tab.data(), sizeof(float) * tab.size(),
-                 hipMemcpyHostToDevice));
-    lp_rtab_rows = rows;
+    ck(hipMemcpy(lp_rtab + (size_t)r0 * rope_dim, tab.data(), sizeof(float) * tab.size(), hipMemcpyHostToDevice));
+    lp_rtab_hi = hi;
 }
 
 hxd::LoopArgs hearth_engine::loop_args(int T) {
@@ -2002,7 +2011,7 @@ static int spec_run(hearth_engine *e, const int32_t *seq, int n_seq, int new_tok
     try {
         ck(hipStreamSynchronize(e->st));
         e->loop_prepare();
-        e->loop_rope_table(std::min(e->cap, pos0 + S * T));
+        e->loop_rope_table(pos0, std::min(e->cap, pos0 + S * T));
         e->lp_skey = 0;
         if (smp) {
             /* a captured step bakes the sampler settings into its kernel arguments: they

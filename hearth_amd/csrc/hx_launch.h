@@ -25,6 +25,9 @@ struct GemmArgs {
     int nseg;
     Act a;             /* activations of tokens [0, T) */
     int T, t0;
+    /* device [1] or null: tokens t >= *live are padding, whose output rows the split-K
+     * product leaves unwritten (nothing reads them) */
+    const int *live;
 };
 
 struct ExpertW { QMat gate, up, down; };
@@ -127,6 +130,7 @@ struct QkvArgs {
     int T, H, Hkv, hd, cap, qk_norm, rope_dim, rope_style;
     float eps;
     const int *pos;           /* device [1]: pos0; token t's K/V go to slot pos0 + t */
+    const int *live;          /* device [1] or null: tokens t >= *live are padding (skipped) */
 };
 
 /* Residual update + RMSNorm + activation quantization, one workgroup per token:
@@ -155,6 +159,7 @@ struct NormArgs {
     float *x;                 /* [T][D] or null */
     Act a;
     int T, D;
+    const int *live;          /* device [1] or null: tokens t >= *live are padding (skipped) */
 };
 
 constexpr int ACCEPT_PARTS = 32;   /* slices per logits row in the argmax */

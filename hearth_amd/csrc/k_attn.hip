@@ -149,11 +149,22 @@ __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
     constexpr int S16_NP = s16_np<HI>(), S16_RB = 16 * S16_NP, QS = HI / 4 + 1;
     __shared__ float4 qT[8][16][QS];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
-    int b = blockIdx.x;
-    const int g = b % Hkv;
-    b /= Hkv;
-    const int t = b % a.T, c = b / a.T;
-    if (a.g.live && t >= *a.g.live) return;   /* padding token (uniform) */
+    int b = blockIdx.x, g, t, c;
+    if (a.g.live) {
+        /* with padding tokens the token is the slowest index: the live tokens' workgroups
+         * dispatch first and the padding ones (which exit at once) after them */
+        const int per_t = (int)gridDim.x / a.T;
+        t = b / per_t;
+        b -= t * per_t;
+        g = b % Hkv;
+        c = b / Hkv;
+        if (t >= *a.g.live) return;   /* padding token (uniform) */
+    } else {
+        g = b % Hkv;
+        b /= Hkv;
+        t = b % a.T;
+        c = b / a.T;
+    }
     const int pos0 = *a.g.pos, nr = pos0 + a.g.depth[t] + 1;
     const int v0 = c * S16_RB;
     if (v0 >= nr) return;   /* uniform */

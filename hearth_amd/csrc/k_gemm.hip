@@ -456,13 +456,19 @@ __global__ __launch_bounds__(512) void k_gemm_sk(GemmArgs args, int ntok) {
     const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
     int p0, p1;
     wave_pairs(sg.m.nbp >> 1, W, wave, p0, p1);
-    for (int t0 = args.t0; t0 < args.T; t0 += ntok) {
-        tile_terms<DT, 1>(&sg.m, rt, args.a, t0, args.T, ntok, [](int t) { return t; }, p0, p1, P, 0);
+    int T = args.T;
+    if (args.live) {   /* padding tokens: no columns of their own, no folds, no rows written */
+        const int lv = *args.live;
+        T = lv < T ? lv : T;
+    }
+    for (int t0 = args.t0; t0 < T; t0 += ntok) {
+        tile_terms<DT, 1>(&sg.m, rt, args.a, t0, T, ntok, [](int t) { return t; }, p0, p1, P, 0);
         __syncthreads();
-        for (int f = tid; f < ntok * 16; f += blockDim.x) {
+        const int nc = T - t0 < ntok ? T - t0 : ntok;
+        for (int f = tid; f < nc * 16; f += blockDim.x) {
             const int c = f >> 4, row = rt * 16 + (f & 15), t = t0 + c;
             const float acc = fold_terms(P, sg.m.nb, ntok, f);
-            if (t < args.T && row < sg.m.rows) {
+            if (row < sg.m.rows) {
                 float y = canon(acc);
                 if (sg.scale_on) y = canon(fmul(sg.scale, y));
                 sg.Y[(size_t)t * sg.ldy + row] = y;

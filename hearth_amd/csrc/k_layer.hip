@@ -91,6 +91,7 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
     extern __shared__ float sq[];
     __shared__ float r_sh;
     const int t = blockIdx.x, D = a.D, tid = threadIdx.x, nth = blockDim.x, K = a.K;
+    if (a.live && t >= *a.live) return;   /* padding token (uniform) */
     const int kp = norm_kp(D), sqs = norm_sq_stride(D), nsq = 16 * kp;
     const int nu = (norm_cover(D, a.a.nbp) + nth - 1) / nth;   /* <= EPT, uniform */
     float *h = a.h + (size_t)t * D;
@@ -250,6 +251,7 @@ __global__ __launch_bounds__(1024) void k_norm_wide(NormArgs a) {
     __shared__ int pk[64];
     __shared__ float r_sh;
     const int t = blockIdx.x, D = a.D, tid = threadIdx.x, nth = blockDim.x, K = a.K;
+    if (a.live && t >= *a.live) return;   /* padding token (uniform) */
     float *h = a.h + (size_t)t * D;
     if (a.mode == 2) {
         if (tid < K) {
@@ -665,11 +667,12 @@ static_assert(__builtin_offsetof(SlotDesc, p0) == sizeof(ExpertW) && __builtin_o
               "slot descriptor fields after the matrices: p0, n, e, pad");
 
 /* routing of token t by one wave (lane e % 64 holds expert e, NU experts per lane):
- * scores into sc, then the K experts, their weights, and the token's bits in tmask */
+ * scores into sc, then the K experts, their weights (also into wk), and the token's
+ * bits in tmask */
 template <int NU>
 __device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, const float (&lgv)[RS_EMAX / 64],
                                                   const float (&bv)[RS_EMAX / 64], int live, float *sc, int *pid,
-                                                  uint32_t *tmask) {
+                                                  uint32_t *tmask, float *wk) {
     const int lane = threadIdx.x & 63, E = a.E, K = a.K;
     float x[NU];
     bool ok[NU];
@@ -755,6 +758,7 @@ __device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, con
         a.ids[(size_t)t * K + lane] = my_id;
         a.wts[(size_t)t * K + lane] = w;
         pid[t * K + lane] = my_id;
+        wk[t * K + lane] = w;
         if (t < live) atomicOr(&tmask[my_id], 1u << t);   /* padding tokens add no pair */
         if (a.route_out) a.route_out[((size_t)t * a.n_moe + a.moe_ord) * K + lane] = my_id;
     }
@@ -765,6 +769,7 @@ __device__ __forceinline__ void route_token_small(const RouteArgs &a, int t, con
 struct RouteSmem {
     float score[RS_TMAX][RS_EMAX];
     int pid[RS_TMAX * 64];
+    float wk[RS_TMAX * 64];
     uint32_t tmask[RS_EMAX];
     int base[RS_EMAX], slot_e[RS_EMAX];
     uint32_t tab[RS_EMAX * RS_TW];
@@ -792,17 +797,16 @@ __device__ __forceinline__ void route_small_stage(const RouteArgs &a, RouteSmem 
     for (int e = tid; e < a.E; e += nth) rs.tmask[e] = 0u;
 }
 
-/* logits of token t and of token 0 (the row of padding tokens), and the selection bias,
- * expert lane + 64 u, into registers: every load issued at once */
+/* logits of token t and the selection bias, expert lane + 64 u, into registers: every
+ * load issued at once */
 __device__ __forceinline__ void route_small_logits(const RouteArgs &a, const float *logits, int t, float (&lgv)[RS_EMAX / 64],
-                                                   float (&lg0)[RS_EMAX / 64], float (&bv)[RS_EMAX / 64]) {
+                                                   float (&bv)[RS_EMAX / 64]) {
     const int lane = threadIdx.x & 63;
     const float *lg = logits + (size_t)t * a.E;
 #pragma unroll
     for (int u = 0; u < RS_EMAX / 64; u++) {
         const int e = lane + 64 * u;
         lgv[u] = e < a.E ? lg[e] : 0.0f;
-        lg0[u] = e < a.E && a.live ? logits[e] : 0.0f;
         bv[u] = e < a.E && a.bias ? a.bias[e] : 0.0f;
     }
 }
@@ -811,10 +815,10 @@ __device__ __forceinline__ void route_small_logits(const RouteArgs &a, const flo
 __device__ __forceinline__ void route_small_token(const RouteArgs &a, RouteSmem &rs, int t, const float (&lgv)[RS_EMAX / 64],
                                                   const float (&bv)[RS_EMAX / 64], int live) {
     switch ((a.E + 63) / 64) {
-    case 1: route_token_small<1>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask); break;
-    case 2: route_token_small<2>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask); break;
-    case 3: route_token_small<3>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask); break;
-    default: route_token_small<4>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask); break;
+    case 1: route_token_small<1>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask, rs.wk); break;
+    case 2: route_token_small<2>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask, rs.wk); break;
+    case 3: route_token_small<3>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask, rs.wk); break;
+    default: route_token_small<4>(a, t, lgv, bv, live, rs.score[t], rs.pid, rs.tmask, rs.wk); break;
     }
 }
 
@@ -823,6 +827,15 @@ __device__ __forceinline__ void route_small_token(const RouteArgs &a, RouteSmem 
 __device__ __forceinline__ void route_small_bucket(const RouteArgs &a, RouteSmem &rs, int tid, int nth, int live) {
     const int E = a.E, K = a.K, P = a.T * K, wave = tid >> 6, lane = tid & 63;
     __syncthreads();
+    /* padding tokens take token 0's experts and weights, rank by rank (no pairs of their
+     * own: their bits are not in the token masks) */
+    for (int p = live * K + tid; p < P; p += nth) {
+        const int tt = p / K, r = p - tt * K, e = rs.pid[r];
+        rs.pid[p] = e;
+        a.ids[p] = e;
+        a.wts[p] = rs.wk[r];
+        if (a.route_out) a.route_out[((size_t)tt * a.n_moe + a.moe_ord) * K + r] = e;
+    }
     if (wave == 0) {
         /* exclusive scan of the pair counts over experts, 64 experts per round */
         int run = 0, nu_run = 0;
@@ -864,41 +877,32 @@ __device__ __forceinline__ void route_small_bucket(const RouteArgs &a, RouteSmem
         a.pair_tok[pos] = tt;
         a.pair_of[p] = pos;
     }
-    /* slot descriptors, one word per thread: the active slots in full, n = 0 in the rest */
+    /* slot descriptors: the active slots in full, one word per thread, then n = 0 in the
+     * rest, one slot per thread */
     uint32_t *dw = (uint32_t *)a.desc;
-    for (int w = tid; w < a.n_slots * RS_DW; w += nth) {
-        const int slot = w / RS_DW, k = w % RS_DW;
-        if (slot < nu) {
-            const int e = rs.slot_e[slot];
-            uint32_t v = 0u;
-            if (k < RS_TW) v = rs.tab[e * RS_TW + k];
-            else if (k == RS_TW) v = (uint32_t)rs.base[e];
-            else if (k == RS_TW + 1) v = (uint32_t)__popc(rs.tmask[e]);
-            else if (k == RS_TW + 2) v = (uint32_t)e;
-            dw[w] = v;
-        } else if (k == RS_TW + 1) {
-            dw[w] = 0u;
-        }
+    for (int w = tid; w < nu * RS_DW; w += nth) {
+        const int slot = w / RS_DW, k = w % RS_DW, e = rs.slot_e[slot];
+        uint32_t v = 0u;
+        if (k < RS_TW) v = rs.tab[e * RS_TW + k];
+        else if (k == RS_TW) v = (uint32_t)rs.base[e];
+        else if (k == RS_TW + 1) v = (uint32_t)__popc(rs.tmask[e]);
+        else if (k == RS_TW + 2) v = (uint32_t)e;
+        dw[w] = v;
     }
+    for (int slot = nu + tid; slot < a.n_slots; slot += nth) dw[(size_t)slot * RS_DW + RS_TW + 1] = 0u;
 }
 
 __global__ __launch_bounds__(1024) void k_route_small(RouteArgs a) {
     __shared__ RouteSmem rs;
     const int tid = threadIdx.x, nth = blockDim.x, t = tid >> 6;
     /* the padding bound is read with the logits (route_row would make the logit loads
-     * wait for it): padding tokens take token 0's logits */
+     * wait for it): padding tokens route nothing and take token 0's experts and weights */
     const int live = a.live ? *a.live : a.T;
-    float lgv[RS_EMAX / 64], lg0[RS_EMAX / 64], bv[RS_EMAX / 64];
-    if (t < a.T) route_small_logits(a, a.logits, t, lgv, lg0, bv);
+    float lgv[RS_EMAX / 64], bv[RS_EMAX / 64];
+    if (t < a.T) route_small_logits(a, a.logits, t, lgv, bv);
     route_small_stage(a, rs, tid, nth);
     __syncthreads();
-    if (t < a.T) {
-        if (t >= live) {
-#pragma unroll
-            for (int u = 0; u < RS_EMAX / 64; u++) lgv[u] = lg0[u];
-        }
-        route_small_token(a, rs, t, lgv, bv, live);
-    }
+    if (t < live) route_small_token(a, rs, t, lgv, bv, live);   /* padding tokens: after the barrier in the bucketing */
     route_small_bucket(a, rs, tid, nth, live);
 }
 
@@ -914,6 +918,7 @@ __global__ __launch_bounds__(256) void k_qkv_post(QkvArgs a, const float *__rest
     const int item = blockIdx.x * 4 + wave;
     if (item >= a.T * nslot) return;
     const int t = item / nslot, j = item % nslot;
+    if (a.live && t >= *a.live) return;   /* padding token: its K/V slot is never read */
     const bool isq = j < a.H;
     const int g = isq ? j : j - a.H;
     const int qd = a.H * hd, kd = a.Hkv * hd;

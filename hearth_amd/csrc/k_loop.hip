@@ -44,6 +44,15 @@ __global__ __launch_bounds__(1024) void k_loop_draft(LoopArgs a) {
         const int left = s[LS_MAXNEW] - s[LS_NEW] - 1;
         nmax = a.T - 1 < left ? a.T - 1 : left;
     }
+    /* RoPE rows of positions pos0 + i from the table (the engine checks that every step
+     * of a run stays below the capacity; the clamp only keeps the read in the table);
+     * first, so their loads overlap the lookup's */
+    const int p = *a.pos;
+    for (int idx = tid; idx < a.T * a.rope_dim; idx += blockDim.x) {
+        const int i = idx / a.rope_dim, d = idx - i * a.rope_dim;
+        const int r = p + i < a.cap ? p + i : a.cap - 1;
+        a.rope[idx] = a.rtab[(size_t)r * a.rope_dim + d];
+    }
     if (tid == 0) best_sh = 0ull;
     __syncthreads();
     if (nmax > 0 && ng > 0) {
@@ -89,14 +98,6 @@ __global__ __launch_bounds__(1024) void k_loop_draft(LoopArgs a) {
             }
             a.u[i] = v;
         }
-    }
-    /* RoPE rows of positions pos0 + i from the table (the engine checks that every step
-     * of a run stays below the capacity; the clamp only keeps the read in the table) */
-    const int p = *a.pos;
-    for (int idx = tid; idx < a.T * a.rope_dim; idx += blockDim.x) {
-        const int i = idx / a.rope_dim, d = idx - i * a.rope_dim;
-        const int r = p + i < a.cap ? p + i : a.cap - 1;
-        a.rope[idx] = a.rtab[(size_t)r * a.rope_dim + d];
     }
 }
 
