@@ -923,10 +923,24 @@ void hearth_engine::forward(int T, bool want_logits, int /*logit_rows_from*/) {
             qa.rope = rope; qa.rfull = rfull; qa.T = T; qa.H = H; qa.Hkv = Hkv; qa.hd = hd; qa.cap = cap;
             qa.qk_norm = c.qk_norm; qa.rope_dim = rope_dim; qa.rope_style = c.rope_style; qa.eps = c.eps; qa.pos = d_pos;
             qa.live = route_live;
-            hxl::qkv_post(qa, st);
-            dump("q", l, qr, T, q_dim);
+            /* the canonical score kernel does the post-step itself (one launch fewer) for
+             * per-head or no qk-norm and NEOX RoPE over the whole head, at most 16 tokens
+             * (every score workgroup redoes its token's q: with a tree's 85 tokens that cost
+             * more than the launch it saves, 17.01 -> 17.41 ms per step; the chain of 9
+             * gained 6.545 -> 6.507 ms) */
+            const bool fuse_post = T <= 16 && attn_mode != 1 && dump_dir.empty() && hd % 64 == 0 && hd <= 256 &&
+                                   (c.qk_norm == 0 || c.qk_norm == 1) && c.rope_style == 0 && rope_dim == hd;
+            if (!fuse_post) {
+                hxl::qkv_post(qa, st);
+                dump("q", l, qr, T, q_dim);
+            }
             hxd::AttnArgs at{};
-            at.q = qr; at.kc = qa.kc; at.vc = qa.vc; at.S = S; at.ldS = ldS; at.out = att; at.T = T; at.H = H;
+            at.q = fuse_post ? qb : qr;
+            if (fuse_post) {
+                at.post = 1; at.qk_norm = c.qk_norm; at.rk = kb; at.rv = vb; at.bq = w.bq; at.bk = w.bk; at.bv = w.bv;
+                at.qn = w.qn; at.kn = w.kn; at.rope = rope; at.qout = qr; at.eps = c.eps;
+            }
+            at.kc = qa.kc; at.vc = qa.vc; at.S = S; at.ldS = ldS; at.out = att; at.T = T; at.H = H;
             at.Hkv = Hkv; at.hd = hd; at.cap = cap; at.scale = c.attn_scale;
             at.g.depth = depth; at.g.anc = anc; at.g.anc_ld = B; at.g.pos = d_pos; at.g.nr_max = nr_max(T); at.g.chain = geom_chain;
             at.g.live = route_live;

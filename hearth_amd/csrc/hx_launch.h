@@ -118,6 +118,15 @@ struct AttnArgs {
     const uint8_t *pf_p[AF_NR];   /* k_attn_values: byte ranges its pf_wgs extra workgroups read */
     unsigned long long pf_n[AF_NR];
     int pf_wgs;
+    /* post = 1: the score kernel does the QKV post-step itself. q is then the raw query
+     * projection and rk, rv the raw key and value projections ([T][Hkv*hd]); bias,
+     * qk-norm (qk_norm 0 or 1) and RoPE (NEOX halves over the whole head) are applied to
+     * q as it is staged and to the step's new K rows as they are loaded, token t's K and
+     * V rows of group g go to slot pos0 + t, and the processed q to qout */
+    int post, qk_norm;
+    const float *rk, *rv, *bq, *bk, *bv, *qn, *kn, *rope;
+    float *qout;
+    float eps;
 };
 
 struct QkvArgs {

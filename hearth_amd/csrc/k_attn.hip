@@ -144,8 +144,39 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a) {
  * NP * HI = 32 K values in registers per thread. */
 template <int HI> constexpr int s16_np() { return HI <= 8 ? 4 : HI <= 16 ? 2 : 1; }
 
+/* bias, qk-norm and RoPE of one K or q head held by the 16 lanes of a row, lane j
+ * holding elements j + 16 i (k_qkv_post's operations in its order): the squares summed
+ * per lane in i order, the 8/4/2/1 tree across the row (DPP, lane j adds lane j + s),
+ * r = 1 / sqrt(sum / hd + eps), x * r * w; NEOX RoPE pairs (p, p + hd / 2) sit in
+ * registers i and i + HI / 2 of the same lane. Every lane of the wave calls it. */
 template <int HI>
-__global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
+__device__ __forceinline__ void post_row(float (&x)[HI], const float *bias, const float *w, const float *cs, int qk_norm,
+                                         float eps, int j) {
+    if (bias) {
+#pragma unroll
+        for (int i = 0; i < HI; i++) x[i] = fadd(x[i], bias[j + 16 * i]);
+    }
+    if (qk_norm == 1) {
+        float L = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HI; i++) L = fadd(L, fmul(x[i], x[i]));
+        L = tree16(L);
+        L = __shfl(L, 0, 16);
+        const float r = fdiv(1.0f, sqrt_rn(fadd(fdiv(L, (float)(16 * HI)), eps)));
+#pragma unroll
+        for (int i = 0; i < HI; i++) x[i] = fmul(fmul(x[i], r), w[j + 16 * i]);
+    }
+#pragma unroll
+    for (int i = 0; i < HI / 2; i++) {
+        const int pp = j + 16 * i;
+        const float av = x[i], bv = x[i + HI / 2], c = cs[2 * pp], sn = cs[2 * pp + 1];
+        x[i] = fadd(fmul(av, c), -fmul(bv, sn));
+        x[i + HI / 2] = fadd(fmul(bv, c), fmul(av, sn));
+    }
+}
+
+template <int HI, bool POST>
+__global__ __launch_bounds__(256, (HI <= 8 ? 5 : 1)) void k_attn_scores16(AttnArgs a) {
     constexpr int S16_NP = s16_np<HI>(), S16_RB = 16 * S16_NP, QS = HI / 4 + 1;
     __shared__ float4 qT[8][16][QS];
     const int Hkv = a.Hkv, grp = a.H / Hkv, hd = a.hd;
@@ -169,21 +200,79 @@ __global__ __launch_bounds__(256) void k_attn_scores16(AttnArgs a) {
     const int v0 = c * S16_RB;
     if (v0 >= nr) return;   /* uniform */
     const int tid = threadIdx.x, j = tid & 15, rl = tid >> 4;
+    const size_t kvd = (size_t)Hkv * hd;
+    if (POST && c == 0 && tid < 64) {
+        /* token t's K row of group g (processed) and V row (+ bias) into slot pos0 + t */
+        float x[HI];
+        const float *kr = a.rk + (size_t)t * kvd + (size_t)g * hd + j;
+#pragma unroll
+        for (int i = 0; i < HI; i++) x[i] = kr[16 * i];
+        post_row<HI>(x, a.bk ? a.bk + (size_t)g * hd : nullptr, a.kn, a.rope + (size_t)t * hd, a.qk_norm, a.eps, j);
+        const size_t slot = (size_t)g * a.cap + pos0 + t;
+        if (tid < 16) {
+#pragma unroll
+            for (int i = 0; i < HI; i++) ((float *)a.kc)[slot * hd + j + 16 * i] = x[i];
+        }
+        const float *vs = a.rv + (size_t)t * kvd + (size_t)g * hd;
+        for (int e = tid; e < hd; e += 64)
+            ((float *)a.vc)[slot * hd + e] = a.bv ? fadd(vs[e], a.bv[(size_t)g * hd + e]) : vs[e];
+    }
     float kv[S16_NP][HI];
     int vrow[S16_NP];
+    bool isnew[S16_NP];
 #pragma unroll
     for (int pass = 0; pass < S16_NP; pass++) {
         const int v = v0 + pass * 16 + rl;
         vrow[pass] = v;
-        const float *kr = a.kc + ((size_t)g * a.cap + row_slot(a.g, pos0, t, v < nr ? v : nr - 1)) * hd + j;
+        const int slot = row_slot(a.g, pos0, t, v < nr ? v : nr - 1);
+        /* with the post-step, rows of this step's tokens come from the raw projection */
+        isnew[pass] = POST && slot >= pos0;
+        const float *kr = isnew[pass] ? a.rk + (size_t)(slot - pos0) * kvd + (size_t)g * hd + j
+                                      : a.kc + ((size_t)g * a.cap + slot) * hd + j;
 #pragma unroll
         for (int i = 0; i < HI; i++) kv[pass][i] = kr[16 * i];
     }
+    if (POST) {
+#pragma unroll
+        for (int pass = 0; pass < S16_NP; pass++) {
+            if (__ballot(isnew[pass]) == 0ull) continue;   /* uniform */
+            const int slot = row_slot(a.g, pos0, t, vrow[pass] < nr ? vrow[pass] : nr - 1);
+            const int tok = isnew[pass] ? slot - pos0 : 0;
+            float x[HI];
+#pragma unroll
+            for (int i = 0; i < HI; i++) x[i] = kv[pass][i];
+            post_row<HI>(x, a.bk ? a.bk + (size_t)g * hd : nullptr, a.kn, a.rope + (size_t)tok * hd, a.qk_norm, a.eps, j);
+            if (isnew[pass]) {
+#pragma unroll
+                for (int i = 0; i < HI; i++) kv[pass][i] = x[i];
+            }
+        }
+    }
     for (int h0 = 0; h0 < grp; h0 += 8) {
         __syncthreads();
-        {
-            const float *qb = a.q + ((size_t)t * a.H + (size_t)g * grp + h0) * hd;
-            float *qf = (float *)qT;
+        const float *qb = a.q + ((size_t)t * a.H + (size_t)g * grp + h0) * hd;
+        float *qf = (float *)qT;
+        if (POST) {
+            /* a head per 16 lanes of the first two waves: raw q (+ bias), qk-norm and
+             * RoPE in registers, then into the transposed stage */
+            if (tid < 128) {
+                const int hh = tid >> 4;
+                const bool in = h0 + hh < grp;
+                const int hq = in ? hh : 0;
+                float x[HI];
+#pragma unroll
+                for (int i = 0; i < HI; i++) x[i] = qb[(size_t)hq * hd + j + 16 * i];
+                post_row<HI>(x, a.bq ? a.bq + ((size_t)g * grp + h0 + hq) * hd : nullptr, a.qn, a.rope + (size_t)t * hd,
+                             a.qk_norm, a.eps, j);
+#pragma unroll
+                for (int i = 0; i < HI; i++) qf[(hh * 16 + j) * (4 * QS) + i] = in ? x[i] : 0.0f;
+                if (c == 0 && in && a.qout) {
+                    float *qo = a.qout + ((size_t)t * a.H + (size_t)g * grp + h0 + hh) * hd + j;
+#pragma unroll
+                    for (int i = 0; i < HI; i++) qo[16 * i] = x[i];
+                }
+            }
+        } else {
             for (int x = tid; x < 8 * hd; x += 256) {
                 const int hh = x / hd, e = x % hd;
                 qf[(hh * 16 + (e & 15)) * (4 * QS) + (e >> 4)] = h0 + hh < grp ? qb[(size_t)hh * hd + e] : 0.0f;
@@ -1203,6 +1292,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
 
 namespace hxl {
 
+/* a.post (the fused QKV post-step) is set only for head_dim a multiple of 64 up to 256,
+ * which takes the k_attn_scores16 launch below */
 void attention_scores(const AttnArgs &a, hipStream_t st) {
     const int max_nr = a.g.nr_max;
     if (a.g.chain && a.T <= ST_TMAX && a.hd == 512) {
@@ -1216,7 +1307,9 @@ void attention_scores(const AttnArgs &a, hipStream_t st) {
 #define HX_S16(HI_)                                                                         \
         {                                                                                   \
             constexpr int rb = 16 * s16_np<HI_>();                                          \
-            k_attn_scores16<HI_><<<((max_nr + rb - 1) / rb) * a.T * a.Hkv, 256, 0, st>>>(a); \
+            const int grid = ((max_nr + rb - 1) / rb) * a.T * a.Hkv;                       \
+            if (a.post) k_attn_scores16<HI_, (HI_ <= 16)><<<grid, 256, 0, st>>>(a);         \
+            else k_attn_scores16<HI_, false><<<grid, 256, 0, st>>>(a);                      \
             return;                                                                         \
         }
         switch (a.hd / 16) {
