@@ -1087,12 +1087,20 @@ __device__ int row_argmax(const AcceptArgs &a, int v) {
     return ((fl & 1) || !(fl & 2)) ? -1 : bi;
 }
 
-__global__ void k_accept_walk(AcceptArgs a) {
+/* rows whose argmax the walk's workgroup merges from the slices up front, in parallel
+ * (the walk then reads them from LDS); rows past it are merged when the walk reaches them */
+constexpr int AW_ROWS = 1024;
+
+__global__ __launch_bounds__(256) void k_accept_walk(AcceptArgs a) {
+    __shared__ int am_s[AW_ROWS];
+    const int nw = a.n < AW_ROWS ? a.n : AW_ROWS;
+    for (int v = threadIdx.x; v < nw; v += blockDim.x) am_s[v] = row_argmax(a, v);
+    __syncthreads();
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     int v = 0, np = 0, status = 0, fin = -1;
     a.path[np++] = 0;
     for (;;) {
-        const int t = row_argmax(a, v);
+        const int t = v < nw ? am_s[v] : row_argmax(a, v);
         a.amax[v] = t;
         if (t < 0) { status = -1; break; }
         int next = -1;
@@ -1180,7 +1188,7 @@ void desc_refresh(SlotDesc *desc, const ExpertW *table, const int *ulist, const 
 
 void accept_greedy(const AcceptArgs &a, hipStream_t st) {
     k_argmax_part<<<a.n * ACCEPT_PARTS, 256, 0, st>>>(a);
-    k_accept_walk<<<1, 64, 0, st>>>(a);
+    k_accept_walk<<<1, 256, 0, st>>>(a);
 }
 
 } // namespace hxl
