@@ -213,7 +213,8 @@ struct hearth_engine {
         *lp_cmp = nullptr, *lp_par = nullptr, *lp_path = nullptr;
     float *lp_rtab = nullptr;
     int lp_rtab_lo = 0, lp_rtab_hi = 0;
-    int *h_lp = nullptr;                 /* pinned: (LS_NEW, LS_DONE) of the steps in flight, then the state */
+    int *h_lp = nullptr;                 /* pinned: the state block after a batch */
+    int *h_lpf = nullptr, *d_lpf = nullptr;   /* pinned, coherent [4]: the commits' (LS_NEW, LS_DONE) flags */
     hipEvent_t lp_ev[2] = {nullptr, nullptr};
     /* sampled runs (hearth_gpu_spec_sample): the acceptance scratch of the loop (its own,
      * so that growing the call-by-call scratch never moves what a captured step reads),
@@ -317,6 +318,7 @@ struct hearth_engine {
         if (h_meta) (void)hipHostFree(h_meta);
         if (h_plog) (void)hipHostFree(h_plog);
         if (h_lp) (void)hipHostFree(h_lp);
+        if (h_lpf) (void)hipHostFree(h_lpf);
         for (hipEvent_t &ev : lp_ev)
             if (ev) (void)hipEventDestroy(ev);
         if (replay_dev) (void)hipFree(replay_dev);
@@ -1304,6 +1306,11 @@ void hearth_engine::loop_prepare() {
     if (rope_dim) lp_rtab = dnew<float>((size_t)cap * rope_dim);
     lp_ustream = dnew<double>((size_t)HEARTH_GPU_SPEC_MAX_STEPS * 128);
     if (!h_lp) ck(hipHostMalloc((void **)&h_lp, sizeof(int) * hxd::LS_FIELDS, hipHostMallocDefault));
+    if (!h_lpf) {
+        /* fine-grained host memory the commit kernel writes directly */
+        ck(hipHostMalloc((void **)&h_lpf, 4 * sizeof(int), hipHostMallocCoherent | hipHostMallocMapped));
+        ck(hipHostGetDevicePointer((void **)&d_lpf, h_lpf, 0));
+    }
     for (hipEvent_t &ev : lp_ev)
         if (!ev) ck(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     lp_state = dnew<int>(hxd::LS_FIELDS);   /* last: a failure above retries everything */
@@ -1337,7 +1344,7 @@ hxd::LoopArgs hearth_engine::loop_args(int T) {
     a.state = lp_state; a.hist = lp_hist; a.hist_cap = cap + B + 2; a.stops = lp_stops;
     a.out = lp_out; a.out_cap = HEARTH_GPU_SPEC_MAX_STEPS * B; a.rec = lp_rec; a.rec_cap = HEARTH_GPU_SPEC_MAX_STEPS;
     a.tokens = tokens; a.cmp = lp_cmp; a.rope = rope; a.rtab = lp_rtab; a.rope_dim = rope_dim; a.cap = cap;
-    a.pos = d_pos; a.result = lp_skey ? lp_samp.result : acc_i + 2 * B; a.T = T;
+    a.pos = d_pos; a.result = lp_skey ? lp_samp.result : acc_i + 2 * B; a.T = T; a.hflag = d_lpf;
     if (lp_skey) {
         /* temperature 0 (a penalised argmax) draws nothing: zero uniforms, as the host
          * steps pass */
@@ -1368,8 +1375,7 @@ void hearth_engine::loop_step(int T) {
     a.part_v = (float *)acc_part; a.part_i = acc_part + (size_t)T * hxd::ACCEPT_PARTS;
     a.part_f = acc_part + 2 * (size_t)T * hxd::ACCEPT_PARTS;
     a.path = lp_path; a.result = acc_i + 2 * B;
-    hxl::accept_greedy(a, st);
-    hxl::loop_commit(la, st);
+    hxl::accept_greedy_commit(a, la, st);
 }
 
 /* A step of T rows whose positions stay below rows: replayed from a captured graph
@@ -2072,22 +2078,22 @@ static int spec_run(hearth_engine *e, const int32_t *seq, int n_seq, int new_tok
         /* two steps in flight: before step i is queued, step i - 2 has finished, and step
          * i - 1 too when it could spend the token budget (a step yields at most T tokens),
          * so a run that ends on its budget queues no step after the last; a stop token or
-         * bad logits can leave two more, which commit nothing. Each step copies its
-         * (LS_NEW, LS_DONE) pair to h_lp + 2 (i & 1). */
-        static_assert(hxd::LS_DONE == hxd::LS_NEW + 1, "the step copy reads LS_NEW and LS_DONE together");
+         * bad logits can leave two more, which commit nothing. Step i's commit writes its
+         * (LS_NEW, LS_DONE) pair to h_lpf + 2 (i & 1) (LS_BSTEP counts the batch's
+         * commits from 0); step i + 2, which reuses the pair, is queued only after it is
+         * read. */
         int seen = new_tokens;   /* tokens yielded as of the last step read */
         auto finished = [&](int j) {
             ck(hipEventSynchronize(e->lp_ev[j & 1]));
-            seen = e->h_lp[2 * (j & 1)];
-            return e->h_lp[2 * (j & 1) + 1] != hxd::LOOP_RUNNING;
+            const volatile int *f = e->h_lpf + 2 * (j & 1);
+            seen = f[0];
+            return f[1] != hxd::LOOP_RUNNING;
         };
         for (int i = 0; i < S; i++) {
             if (i >= 2 && finished(i - 2)) break;
             if (i >= 1 && seen + T >= max_new && finished(i - 1)) break;
             e->launch_loop_step(T, rows);
             launched++;
-            ck(hipMemcpyAsync(e->h_lp + 2 * (i & 1), e->lp_state + hxd::LS_NEW, 2 * sizeof(int),
-                              hipMemcpyDeviceToHost, e->st));
             ck(hipEventRecord(e->lp_ev[i & 1], e->st));
         }
         ck(hipMemcpyAsync(e->h_lp, e->lp_state, sizeof(int) * hxd::LS_FIELDS, hipMemcpyDeviceToHost, e->st));

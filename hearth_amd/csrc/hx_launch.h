@@ -279,6 +279,7 @@ enum LoopField {
     LS_NSTOP,     /* stop ids */
     LS_KVPOS,     /* the engine position after the last committed step */
     LS_UOFF,      /* sampled runs: uniforms of the run's stream consumed so far */
+    LS_BSTEP,     /* commits of the current batch (the host-visible flag slot) */
     LS_FIELDS = 16
 };
 enum LoopDone { LOOP_RUNNING = 0, LOOP_STOP = 1, LOOP_LENGTH = 2, LOOP_BAD = 3 };
@@ -308,6 +309,10 @@ struct LoopArgs {
     int ustream_n;
     double *u;
     int sampled;
+    /* host-visible memory [4] or null: every commit of the batch (committing or not)
+     * writes (LS_NEW, LS_DONE) after it to [2 (s & 1)], s = LS_BSTEP before it, so the
+     * host sees a step's outcome without a copy */
+    int *hflag;
 };
 
 } // namespace hxd
@@ -350,6 +355,8 @@ void kv_move_rows(float *cache, size_t layer_stride, int L, size_t off, int widt
 void desc_refresh(SlotDesc *desc, const ExpertW *table, const int *ulist, const int *n_active, int n_slots,
                   hipStream_t st);
 void accept_greedy(const AcceptArgs &a, hipStream_t st);
+/* the same, and the device loop's commit of the step in the walk's thread */
+void accept_greedy_commit(const AcceptArgs &a, const LoopArgs &la, hipStream_t st);
 /* Sampler settings of one sampled acceptance (the reference's Sampler fields). */
 struct SamplerSpec {
     double temperature, top_p, min_p, rp;

@@ -9,6 +9,7 @@
  */
 #include "hx_device.h"
 #include "hx_launch.h"
+#include "hx_loop.h"
 
 using namespace hxd;
 
@@ -1091,12 +1092,13 @@ __device__ int row_argmax(const AcceptArgs &a, int v) {
  * (the walk then reads them from LDS); rows past it are merged when the walk reaches them */
 constexpr int AW_ROWS = 1024;
 
-__global__ __launch_bounds__(256) void k_accept_walk(AcceptArgs a) {
+/* the walk by thread 0, every row's argmax merged first by the whole workgroup */
+__device__ void accept_walk(const AcceptArgs &a) {
     __shared__ int am_s[AW_ROWS];
     const int nw = a.n < AW_ROWS ? a.n : AW_ROWS;
     for (int v = threadIdx.x; v < nw; v += blockDim.x) am_s[v] = row_argmax(a, v);
     __syncthreads();
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    if (threadIdx.x != 0) return;
     int v = 0, np = 0, status = 0, fin = -1;
     a.path[np++] = 0;
     for (;;) {
@@ -1113,6 +1115,15 @@ __global__ __launch_bounds__(256) void k_accept_walk(AcceptArgs a) {
     a.result[0] = np;
     a.result[1] = fin;
     a.result[2] = status;
+}
+
+__global__ __launch_bounds__(256) void k_accept_walk(AcceptArgs a) { accept_walk(a); }
+
+/* the device loop's greedy step: the walk, then the commit in the same thread (one
+ * launch instead of two; the commit reads the result the walk just wrote) */
+__global__ __launch_bounds__(256) void k_accept_walk_commit(AcceptArgs a, LoopArgs la) {
+    accept_walk(a);
+    if (threadIdx.x == 0) loop_commit_thread(la);
 }
 
 } // namespace
@@ -1189,6 +1200,11 @@ void desc_refresh(SlotDesc *desc, const ExpertW *table, const int *ulist, const 
 void accept_greedy(const AcceptArgs &a, hipStream_t st) {
     k_argmax_part<<<a.n * ACCEPT_PARTS, 256, 0, st>>>(a);
     k_accept_walk<<<1, 256, 0, st>>>(a);
+}
+
+void accept_greedy_commit(const AcceptArgs &a, const LoopArgs &la, hipStream_t st) {
+    k_argmax_part<<<a.n * ACCEPT_PARTS, 256, 0, st>>>(a);
+    k_accept_walk_commit<<<1, 256, 0, st>>>(a, la);
 }
 
 } // namespace hxl
