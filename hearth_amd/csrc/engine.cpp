@@ -1356,18 +1356,17 @@ hxd::LoopArgs hearth_engine::loop_args(int T) {
     return a;
 }
 
-/* One step: drafts and geometry rows, the forward of T rows with the head, the greedy
- * acceptance of the live rows, the commit. */
+/* One step (its draft already made): the forward of T rows with the head, the greedy or
+ * sampled acceptance of the live rows, the commit and the next step's draft. */
 void hearth_engine::loop_step(int T) {
     const hxd::LoopArgs la = loop_args(T);
-    hxl::loop_draft(la, st);
     forward(T, true, 0);
     if (lp_skey) {
         /* the sampled walk over the live rows (the chain parents of lp_par), penalty context
          * = the committed sequence (it ends with the step's first token) */
         ck(hxl::accept_sample_dev(lp_samp, logits, T, V, tokens, lp_par, lp_spec, lp_hist, lp_state + hxd::LS_LEN,
                                   lp_state + hxd::LS_LIVE, st));
-        hxl::loop_commit(la, st);
+        hxl::loop_commit_draft(la, st);
         return;
     }
     hxd::AcceptArgs a{};
@@ -2082,6 +2081,8 @@ static int spec_run(hearth_engine *e, const int32_t *seq, int n_seq, int new_tok
          * (LS_NEW, LS_DONE) pair to h_lpf + 2 (i & 1) (LS_BSTEP counts the batch's
          * commits from 0); step i + 2, which reuses the pair, is queued only after it is
          * read. */
+        /* the first step's draft; every step then drafts the next after its commit */
+        hxl::loop_draft(e->loop_args(T), e->st);
         int seen = new_tokens;   /* tokens yielded as of the last step read */
         auto finished = [&](int j) {
             ck(hipEventSynchronize(e->lp_ev[j & 1]));

@@ -355,7 +355,7 @@ void kv_move_rows(float *cache, size_t layer_stride, int L, size_t off, int widt
 void desc_refresh(SlotDesc *desc, const ExpertW *table, const int *ulist, const int *n_active, int n_slots,
                   hipStream_t st);
 void accept_greedy(const AcceptArgs &a, hipStream_t st);
-/* the same, and the device loop's commit of the step in the walk's thread */
+/* the same, then the device loop's commit of the step and the next step's draft */
 void accept_greedy_commit(const AcceptArgs &a, const LoopArgs &la, hipStream_t st);
 /* Sampler settings of one sampled acceptance (the reference's Sampler fields). */
 struct SamplerSpec {
@@ -415,5 +415,5 @@ hipError_t accept_sample_dev(SampleScratch &m, const float *rows, int n, int V, 
 /* One step of the greedy loop: the drafts, token ids and RoPE rows of the next forward
  * (loop_draft), and the commit of the acceptance that followed it (loop_commit). */
 void loop_draft(const LoopArgs &a, hipStream_t st);
-void loop_commit(const LoopArgs &a, hipStream_t st);
+void loop_commit_draft(const LoopArgs &a, hipStream_t st);
 } // namespace hxl

@@ -1119,11 +1119,14 @@ __device__ void accept_walk(const AcceptArgs &a) {
 
 __global__ __launch_bounds__(256) void k_accept_walk(AcceptArgs a) { accept_walk(a); }
 
-/* the device loop's greedy step: the walk, then the commit in the same thread (one
- * launch instead of two; the commit reads the result the walk just wrote) */
-__global__ __launch_bounds__(256) void k_accept_walk_commit(AcceptArgs a, LoopArgs la) {
+/* the device loop's greedy step: the walk, the commit in the same thread (it reads the
+ * result the walk just wrote), then the next step's draft by the whole workgroup: one
+ * launch instead of three */
+__global__ __launch_bounds__(1024) void k_accept_walk_commit(AcceptArgs a, LoopArgs la) {
     accept_walk(a);
     if (threadIdx.x == 0) loop_commit_thread(la);
+    __syncthreads();
+    draft_body(la);
 }
 
 } // namespace
@@ -1204,7 +1207,7 @@ void accept_greedy(const AcceptArgs &a, hipStream_t st) {
 
 void accept_greedy_commit(const AcceptArgs &a, const LoopArgs &la, hipStream_t st) {
     k_argmax_part<<<a.n * ACCEPT_PARTS, 256, 0, st>>>(a);
-    k_accept_walk_commit<<<1, 256, 0, st>>>(a, la);
+    k_accept_walk_commit<<<1, 1024, 0, st>>>(a, la);
 }
 
 } // namespace hxl
