@@ -456,13 +456,12 @@ __global__ __launch_bounds__(512) void k_gemm_sk(GemmArgs args, int ntok) {
     const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
     int p0, p1;
     wave_pairs(sg.m.nbp >> 1, W, wave, p0, p1);
-    int T = args.T;
-    if (args.live) {   /* padding tokens: no columns of their own, no folds, no rows written */
-        const int lv = *args.live;
-        T = lv < T ? lv : T;
-    }
+    /* padding tokens (t >= *live) get no folds and no rows written; their terms are
+     * computed with the rest, so the weight loads do not wait for the bound */
+    const int lv = args.live ? *args.live : args.T;
+    const int T = lv < args.T ? lv : args.T;
     for (int t0 = args.t0; t0 < T; t0 += ntok) {
-        tile_terms<DT, 1>(&sg.m, rt, args.a, t0, T, ntok, [](int t) { return t; }, p0, p1, P, 0);
+        tile_terms<DT, 1>(&sg.m, rt, args.a, t0, args.T, ntok, [](int t) { return t; }, p0, p1, P, 0);
         __syncthreads();
         const int nc = T - t0 < ntok ? T - t0 : ntok;
         for (int f = tid; f < nc * 16; f += blockDim.x) {

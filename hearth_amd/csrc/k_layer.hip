@@ -92,7 +92,6 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
     extern __shared__ float sq[];
     __shared__ float r_sh;
     const int t = blockIdx.x, D = a.D, tid = threadIdx.x, nth = blockDim.x, K = a.K;
-    if (a.live && t >= *a.live) return;   /* padding token (uniform) */
     const int kp = norm_kp(D), sqs = norm_sq_stride(D), nsq = 16 * kp;
     const int nu = (norm_cover(D, a.a.nbp) + nth - 1) / nth;   /* <= EPT, uniform */
     float *h = a.h + (size_t)t * D;
@@ -107,6 +106,7 @@ __global__ __launch_bounds__(1024) void k_norm(NormArgs a) {
             if (MODE == 1 || ((MODE == 2 || MODE == 4) && ad)) av[u] = ad[ic];
         }
     }
+    if (a.live && t >= *a.live) return;   /* padding token (uniform), after the row's loads are issued */
     float gs = 1.0f;   /* sigmoid of the shared expert's gate logit (modes 2, 4) */
     if ((MODE == 2 || MODE == 4) && a.add_gate) gs = fdiv(1.0f, fadd(1.0f, exp_glibc_f(-a.add_gate[t])));
     if (MODE == 0) {
