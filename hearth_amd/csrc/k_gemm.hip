@@ -456,12 +456,14 @@ __global__ __launch_bounds__(512) void k_gemm_sk(GemmArgs args, int ntok) {
     const int W = blockDim.x >> 6, wave = threadIdx.x >> 6, tid = threadIdx.x;
     int p0, p1;
     wave_pairs(sg.m.nbp >> 1, W, wave, p0, p1);
-    /* padding tokens (t >= *live) get no folds and no rows written; their terms are
-     * computed with the rest, so the weight loads do not wait for the bound */
+    /* padding tokens (t >= *live): no columns of their own (their activation loads repeat
+     * the last live row's), no folds, no rows written. Bounding the columns only after
+     * the loads (every padding row's activations loaded) cost 0.96 us a launch in a loop
+     * with short drafts. */
     const int lv = args.live ? *args.live : args.T;
     const int T = lv < args.T ? lv : args.T;
     for (int t0 = args.t0; t0 < T; t0 += ntok) {
-        tile_terms<DT, 1>(&sg.m, rt, args.a, t0, args.T, ntok, [](int t) { return t; }, p0, p1, P, 0);
+        tile_terms<DT, 1>(&sg.m, rt, args.a, t0, T, ntok, [](int t) { return t; }, p0, p1, P, 0);
         __syncthreads();
         const int nc = T - t0 < ntok ? T - t0 : ntok;
         for (int f = tid; f < nc * 16; f += blockDim.x) {
