@@ -16,7 +16,7 @@ no logits block crosses PCIe. Greedy runs without a repetition penalty can go fu
 the engine's device loop (Engine.spec_greedy) drafts from the sequence it keeps in HBM
 and applies the stop and length rules itself, so a batch of steps runs with no host
 round trip between them, and only the committed tokens and per-step counts come back
-(`device_loop`: by default for runs without drafts).
+(`device_loop`: by default whenever the engine can run it).
 `generate()` applies the stop and length rules to the tokens each forward commits (for a
 device batch, the same cut the device made).
 
@@ -414,12 +414,10 @@ class _Run:
 
 def _use_device_loop(engine, sampler: Sampler, stops: frozenset, device_loop: bool | None, drafts: bool,
                      draft_len: int = 0) -> bool:
-    """None picks the device loop for runs without drafts only: with drafts, every device
-    step evaluates draft_len + 1 rows however short its draft, which at low acceptance
-    costs about what the saved host round trip gains."""
+    """None picks the device loop whenever the engine can run it, with or without drafts
+    (its padding rows past a short draft cost no work in the forward, and the tokens are
+    the host steps' tokens); False forces host steps, True the loop."""
     able = len(stops) <= _eng.SPEC_STOPS_MAX and draft_len + 1 <= _eng.SPEC_ROWS_MAX
-    if device_loop is None and drafts:
-        return False
     if device_loop is False or not able:
         if device_loop:
             raise ValueError(f"the device loop runs at most {_eng.SPEC_STOPS_MAX} stop ids and drafts of at most "
